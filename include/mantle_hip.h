@@ -1,0 +1,210 @@
+/*
+ * mantle_hip.h -- C ABI of libmantle_hip.so: Mantle's elementwise / broadcast / reduction
+ * op layer as hand-written HIP kernels for gfx950 (MI355X).
+ *
+ * This is the drop-in boundary for Mantle's op structs. Each entry point replaces the body
+ * of one reference function (paths relative to the Mantle checkout, cited per entry):
+ * mantle/core/tensorutils.mojo primitives and the op structs of
+ * mantle/autograd/ops/basics.mojo and mantle/autograd/ops/mlops.mojo, reached through
+ * forward_op / backward_op in mantle/autograd/ops/ops.mojo.
+ *
+ * Conventions
+ *   - Plain C types only; no exceptions cross the ABI. Every int-returning call returns
+ *     MH_OK (0) or a negative mh_status; mh_last_error() gives a thread-local message.
+ *   - Tensors are fp32, row-major contiguous, rank 1..8 (mantle/core/tensor.mojo:20-155),
+ *     described by mh_shape. Tensor pointers are device pointers from mh_malloc (or any
+ *     device allocation on the initialised device). The library never frees caller memory.
+ *   - Shapes are validated before any device work: a pair that does not broadcast (which
+ *     the reference only prints about, tensorutils.mojo:116-122), rank outside 1..8, a
+ *     negative dim or a null tensor pointer returns an error and launches nothing.
+ *   - One context per process, one HIP stream (default priority). Calls are complete when
+ *     they return unless mh_init was given MH_INIT_ASYNC; then mh_sync() waits.
+ *   - Backward entry points ACCUMULATE into grad (grad = grad + op gradient), fusing the
+ *     op struct's backward with accumulate_grad exactly as backward_op does
+ *     (ops.mojo:355-463). Pass a zeroed grad to get the plain gradient.
+ *   - Not re-entrant across host threads (the reference calls ops from one thread).
+ */
+#ifndef MANTLE_HIP_H
+#define MANTLE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MH_MAX_RANK 8 /* mantle/core/tensor.mojo:20 MAX_RANK */
+
+/* TensorShape (mantle/core/tensor.mojo:28-229): rank and row-major dims. */
+typedef struct {
+    int32_t rank;
+    int64_t dims[MH_MAX_RANK];
+} mh_shape;
+
+/* Op ids: the same numbers as Mantle's OP registry (mantle/autograd/ops/ops.mojo:57-83). */
+enum mh_op {
+    MH_ADD = 0, MH_SUB = 1, MH_MUL = 2, MH_DIV = 3, MH_EXP = 4, MH_LOG = 5, MH_POW = 6,
+    MH_SUM = 8, MH_MEAN = 9, MH_MAX = 10, MH_SIGMOID = 13, MH_RELU = 14, MH_TANH = 15
+};
+
+enum mh_status {
+    MH_OK = 0,
+    MH_ERR_INVALID = -1,   /* bad argument (tensor_id, axis, flag ...) */
+    MH_ERR_SHAPE = -2,     /* shapes do not broadcast / do not match the op */
+    MH_ERR_RANK = -3,      /* rank outside 1..8 or a negative dim */
+    MH_ERR_NULL = -4,      /* null pointer for a non-empty tensor */
+    MH_ERR_OP = -5,        /* op id not supported by this entry point */
+    MH_ERR_NOT_INIT = -6,  /* mh_init has not succeeded */
+    MH_ERR_HIP = -7,       /* a HIP runtime call failed (message in mh_last_error) */
+    MH_ERR_NO_DEVICE = -8, /* no usable gfx950 device */
+    MH_ERR_OVERFLOW = -9   /* element count or byte size overflow */
+};
+
+#define MH_INIT_ASYNC 1u /* do not synchronise at the end of each call */
+
+/* ---- context and memory (the device-resident side of Tensor / Collection) ---- */
+int mh_init(int device, uint64_t flags);
+int mh_shutdown(void);
+int mh_sync(void);
+const char* mh_last_error(void);
+const char* mh_status_string(int status);
+int mh_device_count(int* count);
+
+/* Tensor storage: Tensor[f32] allocation and zero-init (tensor.mojo:250-302). */
+int mh_malloc(void** dptr, size_t bytes);
+int mh_free(void* dptr);
+int mh_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int mh_memcpy_d2h(void* dst, const void* src, size_t bytes);
+/* Tensor.copy (tensor.mojo:345-361): device-to-device deep copy. */
+int mh_memcpy_d2d(void* dst, const void* src, size_t bytes);
+/* Tensor.zero / Collection.set_zero (collection.mojo:221-224); a fill kernel, not a memset. */
+int mh_zero(float* t, int64_t n);
+
+/* fill, tensorutils.mojo:29-44: t[i] = v. */
+int mh_fill(float* t, float v, int64_t n);
+
+/* ---- forward ---- */
+
+/* ADD/SUB/MUL/DIV forward: the elwise_op dispatcher, tensorutils.mojo:242-357
+ * (same shape :277-290, tensor-scalar :293-304, scalar-tensor :307-318,
+ * broadcast_elwise_op :321-357) as called by ADD/SUB/MUL/DIV.forward
+ * (basics.mojo:36-43, 66-73, 102-109, 140-147). sres must equal broadcast(sa, sb). */
+int mh_binary_fwd(int op, float* res, mh_shape sres, const float* a, mh_shape sa,
+                  const float* b, mh_shape sb);
+
+/* EXP/LOG/SIGMOID/RELU/TANH forward: elwise_transform, tensorutils.mojo:181-200, with the
+ * functions of EXP.forward (basics.mojo:266-270), LOG.forward (:294-298),
+ * SIGMOID.sigmoid (mlops.mojo:35-42), RELU.relu (:85-90), TANH.tanh (:195-201). */
+int mh_unary_fwd(int op, float* res, const float* x, int64_t n);
+
+/* POW.forward, basics.mojo:320-327 -> elwise_pow, tensorutils.mojo:226-239:
+ * res = powi(x, Int(exponent[0])), the exponent truncated toward zero. `exponent` is the
+ * device pointer of the shape-(1) graph scalar t2. */
+int mh_pow_fwd(float* res, const float* x, int64_t n, const float* exponent);
+
+/* SUM/MEAN/MAX forward: SUM.forward (basics.mojo:393-406), MEAN.forward (:440-452),
+ * MAX.forward (:521-534) -> reduce all (tensorutils.mojo:564-598, tsum/tmean/tmax
+ * :694-720, :850-862) or reduce axis (:622-684, :746-772, :865-876). axis = -1 reduces all
+ * elements into res[0]; otherwise res has get_reduce_shape(sx, axis) (:601-619). */
+int mh_reduce_fwd(int op, float* res, const float* x, mh_shape sx, int32_t axis);
+
+/* ---- backward (accumulating) ---- */
+
+/* backward_op for ADD/SUB/MUL/DIV (ops.mojo:408-463): the struct backward of operand
+ * tensor_id (ADD :46-55, SUB :82-91, MUL :118-129, DIV :155-219 of basics.mojo) followed
+ * by accumulate_grad[grad_shape = s_k, res_grad_shape = broadcast(s1, s2)]
+ * (tensorutils.mojo:454-487), i.e. un-broadcast by summation when the operand was
+ * broadcast. sug must equal broadcast(s1, s2); sgrad must equal s1 (id 0) or s2 (id 1). */
+int mh_binary_bwd_accum(int op, int tensor_id, float* grad, mh_shape sgrad,
+                        const float* ug, mh_shape sug, const float* t1, mh_shape s1,
+                        const float* t2, mh_shape s2);
+
+/* Both operand gradients of a same-shape ADD/SUB/MUL/DIV in one pass (the two
+ * backward_op calls that Model.backward makes when both operands are trainable,
+ * model.mojo:233-270). Requires s1 == s2 == sug; either grad pointer may be NULL to skip
+ * that operand. */
+int mh_binary_bwd_accum2(int op, float* grad1, float* grad2, const float* ug,
+                         const float* t1, const float* t2, mh_shape s);
+
+/* backward_op for EXP/LOG/SIGMOID/RELU/TANH (ops.mojo:355-405): EXP.backward
+ * (basics.mojo:272-285), LOG.backward (:300-309), SIGMOID.backward (mlops.mojo:50-76),
+ * RELU.backward (:99-125), TANH.backward (:209-235), then the same-shape
+ * accumulate_grad (tensorutils.mojo:442-451): grad = grad + f'(x) * ug. */
+int mh_unary_bwd_accum(int op, float* grad, const float* x, const float* ug, int64_t n);
+
+/* backward_op for POW (ops.mojo:408-463 with POW.backward, basics.mojo:329-378).
+ * tensor_id 0: grad = grad + (a * powf(x + 1e-12, a - 1)) * ug, a = exponent[0].
+ * tensor_id 1: grad[0] = grad[0] + sum(powf(x, a) * (isinf(log x) ? 0 : log x) * ug).
+ * n is the element count of x and ug. */
+int mh_pow_bwd_accum(int tensor_id, float* grad, const float* x, const float* exponent,
+                     const float* ug, int64_t n);
+
+/* backward_op for SUM/MEAN/MAX (ops.mojo:355-405): SUM.backward (basics.mojo:408-425),
+ * MEAN.backward (:454-506), MAX.backward (:536-615, ties split as fl(1/count) * ug),
+ * then the same-shape accumulate_grad. ug has the reduced shape (axis >= 0) or (1). */
+int mh_reduce_bwd_accum(int op, float* grad, const float* x, mh_shape sx, const float* ug,
+                        int32_t axis);
+
+/* accumulate_grad, tensorutils.mojo:442-487: grad += rg for equal shapes, grad += rg[0]
+ * for rg of shape (1), otherwise grad += un-broadcast(rg) (sum over the broadcast axes).
+ * Pairs that are not numpy-broadcastable (which the reference indexes out of bounds with,
+ * tensorutils.mojo:149-175 and :482-484) return MH_ERR_SHAPE. */
+int mh_accumulate_grad(float* grad, mh_shape sgrad, const float* rg, mh_shape srg);
+
+/* ---- fused graph-level entry points (no single reference counterpart) ---- */
+
+/* Linear-layer / NCHW bias + RELU forward: y = ADD(x, bias) (broadcast) and
+ * r = RELU(y) in one pass, the two forward_op calls of a graph ADD -> RELU
+ * (ADD.forward basics.mojo:36-43, RELU.forward mlops.mojo:92-97). Writes both y (needed
+ * by RELU's backward) and r. sbias must broadcast to sx. */
+int mh_bias_relu_fwd(float* y, float* r, const float* x, mh_shape sx, const float* bias,
+                     mh_shape sbias);
+
+/* Backward of the same graph: g_y = g_y + relu'(y) * ug (RELU backward_op), then both
+ * ADD backward_op calls: grad_x += g_y and grad_bias += un-broadcast(g_y). g_y may be NULL
+ * when the graph's grad of y starts at zero and is not needed afterwards; then the sum
+ * uses relu'(y) * ug directly. grad_x or grad_bias may be NULL to skip that operand. */
+int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const float* y,
+                           const float* ug, mh_shape sx, mh_shape sbias);
+
+/* Seeded synthetic fill (the device counterpart of rand_uniform / rand_normal,
+ * mantle/core/rand_utils.mojo:23-63): element i of stream `seed` comes from a counter-based
+ * SplitMix64, so the result does not depend on the launch shape. U(lo, hi) and N(mean, std). */
+int mh_rand_uniform(float* t, int64_t n, uint64_t seed, float lo, float hi);
+int mh_rand_normal(float* t, int64_t n, uint64_t seed, float mean, float std);
+
+/* ---- timing (events on the library's stream) ---- */
+int mh_event_create(void** ev);
+int mh_event_destroy(void* ev);
+int mh_event_record(void* ev);
+int mh_event_elapsed_ms(float* ms, void* start, void* stop);
+
+/* ---- diagnostics ---- */
+
+/* How mh_binary_fwd would execute (sres, sa, sb): after dropping size-1 dims and merging
+ * dims that are contiguous for every operand. kind: 0 same-shape, 1 b is one element,
+ * 2 a is one element, 3 strided broadcast. Host-only, needs no device. */
+typedef struct {
+    int32_t kind;
+    int32_t rank;
+    int64_t dims[MH_MAX_RANK];
+    int64_t stride_a[MH_MAX_RANK];
+    int64_t stride_b[MH_MAX_RANK];
+} mh_plan_info;
+int mh_plan_binary(mh_shape sres, mh_shape sa, mh_shape sb, mh_plan_info* out);
+
+/* The chain of single-axis reductions that un-broadcasting rg into grad runs: the number
+ * of steps and, per step, the [A, B, C] view reduced over B. Host-only. */
+typedef struct {
+    int32_t nsteps; /* 0: same shape (no reduction) */
+    int64_t a[MH_MAX_RANK];
+    int64_t b[MH_MAX_RANK];
+    int64_t c[MH_MAX_RANK];
+} mh_reduce_plan_info;
+int mh_plan_unbroadcast(mh_shape sgrad, mh_shape srg, mh_reduce_plan_info* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,20 @@
+"""mantle_amd: Mantle's elementwise / broadcast / reduction op layer on MI355X (gfx950).
+
+The compute path is libmantle_hip.so (hand-written HIP kernels behind the C ABI in
+include/mantle_hip.h); this package is its Python host side: a device-resident Tensor and
+a mirror of Mantle's op structs and forward_op / backward_op. Nothing here falls back to
+the CPU: if the library is missing or the device is absent, calls raise.
+"""
+from ._lib import MantleHipError, lib  # noqa: F401
+from .tensor import Tensor, TensorShape, init, sync  # noqa: F401
+from .ops import (  # noqa: F401
+    OP, ADD, SUB, MUL, DIV, EXP, LOG, POW, SUM, MEAN, MAX, SIGMOID, RELU, TANH,
+    forward_op, backward_op, backward_op_both, broadcast_shapes, get_reduce_shape, fill,
+    elwise_transform, elwise_op, accumulate_grad, tsum, tmean, tmax, static_result_shape,
+)
+
+__all__ = [
+    "MantleHipError", "Tensor", "TensorShape", "init", "sync", "OP", "forward_op", "backward_op",
+    "backward_op_both", "broadcast_shapes", "get_reduce_shape", "fill", "elwise_transform",
+    "elwise_op", "accumulate_grad", "tsum", "tmean", "tmax", "static_result_shape",
+]

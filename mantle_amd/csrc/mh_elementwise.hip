@@ -1,0 +1,740 @@
+// mh_elementwise.hip -- forward and accumulating-backward elementwise kernels.
+//
+// One engine serves every elementwise entry point: an output stream (written, or
+// read-modify-written for "grad = grad + rg") and up to four input streams, each FULL (same
+// shape as the output), SCALAR (one element, loaded once per thread) or BCAST (strided in the
+// collapsed output space). Same-shape work takes the float4 path: 256-thread blocks, each
+// thread issuing all of its 128-bit loads before any arithmetic. Broadcast work decodes the
+// output coordinate of each quad with precomputed fast divisors; an inner dimension divisible
+// by 4 keeps 128-bit accesses for every operand whose inner stride is 0 or 1.
+#include "mh_internal.h"
+#include "mh_math.h"
+
+namespace mh {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;  // quads per thread per block
+
+struct DevScal {
+    const float* p[4];
+};
+
+template <int N>
+struct InPtrs {
+    const float* p[N > 0 ? N : 1];
+};
+
+// ---------------------------------------------------------------------------------------
+// functors: operator()(v) with v[k] the k-th input value; setup() reads device scalars.
+// ---------------------------------------------------------------------------------------
+template <int OP>
+struct FBin {  // add/sub/mul/div, math_util.mojo:37-126
+    __device__ void setup(const DevScal&) {}
+    __device__ float operator()(const float* v) const {
+        if constexpr (OP == MH_ADD) return v[0] + v[1];
+        else if constexpr (OP == MH_SUB) return v[0] - v[1];
+        else if constexpr (OP == MH_MUL) return v[0] * v[1];
+        else return v[0] / v[1];
+    }
+};
+
+template <int OP>
+struct FUn {  // elwise_transform bodies
+    __device__ void setup(const DevScal&) {}
+    __device__ float operator()(const float* v) const {
+        if constexpr (OP == MH_EXP) return mexp(v[0]);
+        else if constexpr (OP == MH_LOG) return mlog(v[0]);
+        else if constexpr (OP == MH_SIGMOID) return msigmoid(v[0]);
+        else if constexpr (OP == MH_RELU) return mrelu(v[0]);
+        else return mtanh(v[0]);
+    }
+};
+
+struct FPowi {  // POW.forward: powi(x, Int(t2[0])), basics.mojo:320-327
+    int64_t n;
+    __device__ void setup(const DevScal& s) {
+        float e = s.p[0][0];
+        n = (e != e) ? 0 : (int64_t)__builtin_truncf(e);
+    }
+    __device__ float operator()(const float* v) const { return mpowi(v[0], n); }
+};
+
+template <int OP>
+struct FUnBwd {  // v[0] = x, v[1] = ug: the rg of each unary struct backward
+    __device__ void setup(const DevScal&) {}
+    __device__ float operator()(const float* v) const {
+        const float x = v[0], ug = v[1];
+        if constexpr (OP == MH_EXP) return mexp(x) * ug;  // basics.mojo:281-284
+        else if constexpr (OP == MH_LOG) return ug / x;   // basics.mojo:305-309
+        else if constexpr (OP == MH_SIGMOID) {            // mlops.mojo:50-76
+            float s = msigmoid(x);
+            return (s * (1.0f - s)) * ug;
+        } else if constexpr (OP == MH_RELU) {             // mlops.mojo:99-125
+            return (x > 0.0f ? 1.0f : 0.0f) * ug;
+        } else {                                          // mlops.mojo:209-235
+            float t = mtanh(x);
+            return (1.0f - t * t) * ug;
+        }
+    }
+};
+
+struct FPowBwdX {  // basics.mojo:345-357: (a * (x + 1e-12) ** (a - 1)) * ug
+    float a, am1;
+    __device__ void setup(const DevScal& s) {
+        a = s.p[0][0];
+        am1 = a - 1.0f;
+    }
+    __device__ float operator()(const float* v) const { return (a * mpowf(v[0] + 1e-12f, am1)) * v[1]; }
+};
+
+// Binary struct backward of one operand (basics.mojo:28-219). Inputs: v[0] = ug, then
+//   ADD, SUB id0: -            -> ug
+//   SUB id1:      -            -> ug * -1
+//   MUL id0:      v[1] = t2    -> ug * t2        MUL id1: v[1] = t1 -> ug * t1
+//   DIV id0:      v[1] = t2    -> ug / t2
+//   DIV id1:      v[1] = t1, v[2] = t2 -> ((-t1) / (t2 * t2)) * ug
+//   DIV id1 with t2 of shape (1) (DIVS): v[1] = t1, f = -1 / (s * s) -> (f * t1) * ug
+template <int OP, int ID, bool DIVS>
+struct FBinRg {
+    float f;
+    __device__ void setup(const DevScal& s) {
+        if constexpr (DIVS) {
+            const float t = s.p[0][0];
+            f = -1.0f / (t * t);
+        }
+    }
+    __device__ float operator()(const float* v) const {
+        const float ug = v[0];
+        if constexpr (OP == MH_ADD) return ug;
+        else if constexpr (OP == MH_SUB) return ID == 0 ? ug : ug * -1.0f;
+        else if constexpr (OP == MH_MUL) return ug * v[1];
+        else if constexpr (ID == 0) return ug / v[1];
+        else if constexpr (DIVS) return (f * v[1]) * ug;
+        else return ((-v[1]) / (v[2] * v[2])) * ug;
+    }
+};
+
+// SUM/MEAN axis backward (basics.mojo:416-425, 489-506): fill(c) then accumulate_op[mul]
+// with the broadcast ug: rg = c * ug; TWICE (rg = (c * ug) * ug) when the reduced shape
+// equals the input shape (accumulate_op applies func twice then, tensorutils.mojo:380-393).
+template <bool TWICE>
+struct FScaleBcast {
+    float c;
+    __device__ void setup(const DevScal&) {}
+    __device__ float operator()(const float* v) const {
+        if constexpr (TWICE) return (c * v[0]) * v[0];
+        else return c * v[0];
+    }
+};
+
+// MEAN all-element backward (basics.mojo:470-487): g = f32(1/N) * ug[0], filled.
+struct FMeanAll {
+    float c, g;
+    __device__ void setup(const DevScal& s) { g = c * s.p[0][0]; }
+    __device__ float operator()(const float*) const { return g; }
+};
+
+// MAX backward routing (basics.mojo:567-577, 597-613): v[0] = x, v[1] = line max,
+// v[2] = fl(1/count) of the line, v[3] = ug of the line.
+struct FMaxRoute {
+    __device__ void setup(const DevScal&) {}
+    __device__ float operator()(const float* v) const { return v[0] == v[1] ? v[2] * v[3] : 0.0f; }
+};
+
+// ---------------------------------------------------------------------------------------
+// kernels
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float comp(const float4& q, int j) {
+    return j == 0 ? q.x : (j == 1 ? q.y : (j == 2 ? q.z : q.w));
+}
+
+// Same-shape engine: all inputs FULL or SCALAR (bit k of smask).
+template <class F, int NIN, bool ACCUM>
+__global__ void __launch_bounds__(kThreads)
+    k_same4(float* __restrict__ out, InPtrs<NIN> in, int smask, int64_t n, DevScal ds, F f) {
+    f.setup(ds);
+    float sv[NIN > 0 ? NIN : 1];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) sv[k] = ((smask >> k) & 1) ? in.p[k][0] : 0.0f;
+    const int64_t nq = n >> 2;
+    const int64_t q0 = (int64_t)blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
+    float4 iv[kUnroll][NIN > 0 ? NIN : 1];
+    float4 ov[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t q = q0 + (int64_t)u * kThreads;
+        if (q < nq) {
+#pragma unroll
+            for (int k = 0; k < NIN; ++k)
+                if (!((smask >> k) & 1)) iv[u][k] = reinterpret_cast<const float4*>(in.p[k])[q];
+            if (ACCUM) ov[u] = reinterpret_cast<const float4*>(out)[q];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t q = q0 + (int64_t)u * kThreads;
+        if (q < nq) {
+            float r[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float v[NIN > 0 ? NIN : 1];
+#pragma unroll
+                for (int k = 0; k < NIN; ++k) v[k] = ((smask >> k) & 1) ? sv[k] : comp(iv[u][k], j);
+                r[j] = f(v);
+                if (ACCUM) r[j] = comp(ov[u], j) + r[j];
+            }
+            reinterpret_cast<float4*>(out)[q] = make_float4(r[0], r[1], r[2], r[3]);
+        }
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        for (int64_t i = nq << 2; i < n; ++i) {
+            float v[NIN > 0 ? NIN : 1];
+#pragma unroll
+            for (int k = 0; k < NIN; ++k) v[k] = ((smask >> k) & 1) ? sv[k] : in.p[k][i];
+            float r = f(v);
+            out[i] = ACCUM ? out[i] + r : r;
+        }
+    }
+}
+
+// Same-shape engine, scalar accesses (some pointer not 16-byte aligned).
+template <class F, int NIN, bool ACCUM>
+__global__ void __launch_bounds__(kThreads)
+    k_same1(float* __restrict__ out, InPtrs<NIN> in, int smask, int64_t n, DevScal ds, F f) {
+    f.setup(ds);
+    float sv[NIN > 0 ? NIN : 1];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) sv[k] = ((smask >> k) & 1) ? in.p[k][0] : 0.0f;
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+        float v[NIN > 0 ? NIN : 1];
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) v[k] = ((smask >> k) & 1) ? sv[k] : in.p[k][i];
+        float r = f(v);
+        out[i] = ACCUM ? out[i] + r : r;
+    }
+}
+
+// Broadcast engine over an ElwPlan. VEC = 4: each work item is a quad of the inner dim
+// (requires plan.vec_ok and aligned pointers); VEC = 1: single elements. BIG: 64-bit
+// coordinate decode (n >= 2^31).
+template <class F, int NIN, bool ACCUM, int VEC, bool BIG>
+__global__ void __launch_bounds__(kThreads)
+    k_bcast(float* __restrict__ out, InPtrs<NIN> in, ElwPlan pl, DevScal ds, F f) {
+    constexpr int NA = NIN > 0 ? NIN : 1;
+    f.setup(ds);
+    float sv[NA];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) sv[k] = pl.kind[k] == IN_SCALAR ? in.p[k][0] : 0.0f;
+    const int64_t nitems = VEC == 4 ? (pl.n >> 2) : pl.n;
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    const int inner = pl.rank - 1;
+    for (int64_t it = (int64_t)blockIdx.x * kThreads + threadIdx.x; it < nitems; it += stride) {
+        const int64_t idx = it * VEC;
+        int64_t off[NA];
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) off[k] = 0;
+        if (pl.any_bcast) {
+            int64_t rem = idx;
+#pragma unroll
+            for (int d = MH_MAX_RANK - 1; d >= 0; --d) {
+                if (d > inner) continue;
+                int64_t q, c;
+                if (BIG) {
+                    q = rem / pl.dims[d];
+                    c = rem - q * pl.dims[d];
+                } else {
+                    uint32_t r32 = (uint32_t)rem;
+                    uint32_t q32 = fdiv(r32, pl.fd[d]);
+                    q = q32;
+                    c = (int64_t)(r32 - q32 * pl.fd[d].d);
+                }
+#pragma unroll
+                for (int k = 0; k < NIN; ++k)
+                    if (pl.kind[k] == IN_BCAST) off[k] += c * pl.st[k][d];
+                rem = q;
+            }
+        }
+        float v[VEC][NA];
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) {
+            if (pl.kind[k] == IN_SCALAR) {
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) v[j][k] = sv[k];
+            } else if (pl.kind[k] == IN_FULL) {
+                if constexpr (VEC == 4) {
+                    float4 q = reinterpret_cast<const float4*>(in.p[k])[it];
+                    v[0][k] = q.x; v[1][k] = q.y; v[2][k] = q.z; v[3][k] = q.w;
+                } else {
+                    v[0][k] = in.p[k][idx];
+                }
+            } else {
+                if constexpr (VEC == 4) {
+                    if (pl.st[k][inner] == 1) {
+                        float4 q = *reinterpret_cast<const float4*>(in.p[k] + off[k]);
+                        v[0][k] = q.x; v[1][k] = q.y; v[2][k] = q.z; v[3][k] = q.w;
+                    } else {
+                        float s = in.p[k][off[k]];
+#pragma unroll
+                        for (int j = 0; j < VEC; ++j) v[j][k] = s;
+                    }
+                } else {
+                    v[0][k] = in.p[k][off[k]];
+                }
+            }
+        }
+        if constexpr (VEC == 4) {
+            float4 o = ACCUM ? reinterpret_cast<const float4*>(out)[it] : make_float4(0.f, 0.f, 0.f, 0.f);
+            float r[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                r[j] = f(v[j]);
+                if (ACCUM) r[j] = comp(o, j) + r[j];
+            }
+            reinterpret_cast<float4*>(out)[it] = make_float4(r[0], r[1], r[2], r[3]);
+        } else {
+            float r = f(v[0]);
+            out[idx] = ACCUM ? out[idx] + r : r;
+        }
+    }
+}
+
+// Fused two-operand backward of a same-shape binary op (both backward_op calls of
+// ops.mojo:408-463 with equal shapes): g1 = g1 + rg0, g2 = g2 + rg1.
+template <int OP>
+__global__ void __launch_bounds__(kThreads)
+    k_bwd2_same4(float* __restrict__ g1, float* __restrict__ g2, const float* __restrict__ ug,
+                 const float* __restrict__ a, const float* __restrict__ b, int64_t n) {
+    constexpr bool NEED_AB = (OP == MH_MUL || OP == MH_DIV);
+    const int64_t nq = n >> 2;
+    const int64_t q0 = (int64_t)blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
+    float4 vu[kUnroll], va[kUnroll], vb[kUnroll], v1[kUnroll], v2[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t q = q0 + (int64_t)u * kThreads;
+        if (q < nq) {
+            vu[u] = reinterpret_cast<const float4*>(ug)[q];
+            if (NEED_AB) {
+                va[u] = reinterpret_cast<const float4*>(a)[q];
+                vb[u] = reinterpret_cast<const float4*>(b)[q];
+            }
+            v1[u] = reinterpret_cast<const float4*>(g1)[q];
+            v2[u] = reinterpret_cast<const float4*>(g2)[q];
+        }
+    }
+    FBinRg<OP, 0, false> f0;
+    FBinRg<OP, 1, false> f1;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t q = q0 + (int64_t)u * kThreads;
+        if (q < nq) {
+            float r1[4], r2[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float uu = comp(vu[u], j);
+                const float aa = NEED_AB ? comp(va[u], j) : 0.0f;
+                const float bb = NEED_AB ? comp(vb[u], j) : 0.0f;
+                float x0[3] = {uu, bb, 0.0f};      // id0 reads t2
+                float x1[3] = {uu, aa, bb};        // id1 reads t1 (and t2 for DIV)
+                r1[j] = comp(v1[u], j) + f0(x0);
+                r2[j] = comp(v2[u], j) + f1(x1);
+            }
+            reinterpret_cast<float4*>(g1)[q] = make_float4(r1[0], r1[1], r1[2], r1[3]);
+            reinterpret_cast<float4*>(g2)[q] = make_float4(r2[0], r2[1], r2[2], r2[3]);
+        }
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        for (int64_t i = nq << 2; i < n; ++i) {
+            const float aa = NEED_AB ? a[i] : 0.0f, bb = NEED_AB ? b[i] : 0.0f;
+            float x0[3] = {ug[i], bb, 0.0f};
+            float x1[3] = {ug[i], aa, bb};
+            g1[i] = g1[i] + f0(x0);
+            g2[i] = g2[i] + f1(x1);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------------------
+static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+static inline unsigned grid_for(int64_t items, int64_t per_block) {
+    int64_t b = (items + per_block - 1) / per_block;
+    if (b < 1) b = 1;
+    if (b > 0x7fffffff) b = 0x7fffffff;
+    return (unsigned)b;
+}
+
+// Runs F over the plan: out (shape = plan output) = F(inputs), or out += F(inputs).
+template <class F, int NIN, bool ACCUM>
+static int run_map(float* out, const ElwPlan& pl, const float* const* ptrs, const DevScal& ds, F f) {
+    if (pl.n == 0) return MH_OK;
+    InPtrs<NIN> in;
+    for (int k = 0; k < NIN; ++k) in.p[k] = ptrs[k];
+    hipStream_t st = ctx().stream;
+    bool al = aligned16(out);
+    for (int k = 0; k < NIN; ++k)
+        if (pl.kind[k] != IN_SCALAR) al = al && aligned16(ptrs[k]);
+    if (!pl.any_bcast) {
+        int smask = 0;
+        for (int k = 0; k < NIN; ++k)
+            if (pl.kind[k] == IN_SCALAR) smask |= 1 << k;
+        if (al) {
+            hipLaunchKernelGGL((k_same4<F, NIN, ACCUM>), dim3(grid_for(pl.n >> 2, kThreads * kUnroll)),
+                               dim3(kThreads), 0, st, out, in, smask, pl.n, ds, f);
+        } else {
+            int64_t b = (pl.n + kThreads - 1) / kThreads;
+            if (b > 65536) b = 65536;
+            hipLaunchKernelGGL((k_same1<F, NIN, ACCUM>), dim3((unsigned)b), dim3(kThreads), 0, st, out,
+                               in, smask, pl.n, ds, f);
+        }
+        return MH_OK;
+    }
+    const bool big = pl.n >= ((int64_t)1 << 31);
+    const bool vec = pl.vec_ok && al;
+    const int64_t items = vec ? (pl.n >> 2) : pl.n;
+    int64_t blocks = (items + kThreads - 1) / kThreads;
+    if (blocks > 262144) blocks = 262144;
+    if (blocks < 1) blocks = 1;
+    dim3 g((unsigned)blocks), b(kThreads);
+    if (vec) {
+        if (big) hipLaunchKernelGGL((k_bcast<F, NIN, ACCUM, 4, true>), g, b, 0, st, out, in, pl, ds, f);
+        else hipLaunchKernelGGL((k_bcast<F, NIN, ACCUM, 4, false>), g, b, 0, st, out, in, pl, ds, f);
+    } else {
+        if (big) hipLaunchKernelGGL((k_bcast<F, NIN, ACCUM, 1, true>), g, b, 0, st, out, in, pl, ds, f);
+        else hipLaunchKernelGGL((k_bcast<F, NIN, ACCUM, 1, false>), g, b, 0, st, out, in, pl, ds, f);
+    }
+    return MH_OK;
+}
+
+static DevScal no_scal() {
+    DevScal d;
+    for (int i = 0; i < 4; ++i) d.p[i] = nullptr;
+    return d;
+}
+static DevScal scal1(const float* p) {
+    DevScal d = no_scal();
+    d.p[0] = p;
+    return d;
+}
+
+static int check_op_binary(int op) {
+    if (op < MH_ADD || op > MH_DIV) return fail(MH_ERR_OP, "op %d is not ADD/SUB/MUL/DIV", op);
+    return MH_OK;
+}
+static int check_op_unary(int op) {
+    if (op != MH_EXP && op != MH_LOG && op != MH_SIGMOID && op != MH_RELU && op != MH_TANH)
+        return fail(MH_ERR_OP, "op %d is not EXP/LOG/SIGMOID/RELU/TANH", op);
+    return MH_OK;
+}
+
+template <int OP>
+static int binary_fwd_t(float* res, const ElwPlan& pl, const float* a, const float* b) {
+    const float* p[2] = {a, b};
+    return run_map<FBin<OP>, 2, false>(res, pl, p, no_scal(), FBin<OP>{});
+}
+
+template <int OP>
+static int unary_fwd_t(float* res, const ElwPlan& pl, const float* x) {
+    const float* p[1] = {x};
+    return run_map<FUn<OP>, 1, false>(res, pl, p, no_scal(), FUn<OP>{});
+}
+
+template <int OP>
+static int unary_bwd_t(float* grad, const ElwPlan& pl, const float* x, const float* ug) {
+    const float* p[2] = {x, ug};
+    return run_map<FUnBwd<OP>, 2, true>(grad, pl, p, no_scal(), FUnBwd<OP>{});
+}
+
+// rg of one binary operand, written (ACCUM = false) or accumulated (ACCUM = true) over the
+// ug-shaped plan whose inputs are ordered as FBinRg expects.
+template <int OP, int ID, bool DIVS, bool ACCUM>
+static int binary_rg_t(float* out, const mh_shape& sug, const float* ug, const float* t1,
+                       const mh_shape& s1, const float* t2, const mh_shape& s2) {
+    using F = FBinRg<OP, ID, DIVS>;
+    ElwPlan pl;
+    if constexpr (OP == MH_ADD || OP == MH_SUB) {
+        mh_shape in[1] = {sug};
+        MH_TRY(build_elw_plan(sug, 1, in, &pl));
+        const float* p[1] = {ug};
+        return run_map<F, 1, ACCUM>(out, pl, p, no_scal(), F{});
+    } else if constexpr ((OP == MH_MUL && ID == 0) || (OP == MH_DIV && ID == 0)) {
+        mh_shape in[2] = {sug, s2};
+        MH_TRY(build_elw_plan(sug, 2, in, &pl));
+        const float* p[2] = {ug, t2};
+        return run_map<F, 2, ACCUM>(out, pl, p, no_scal(), F{});
+    } else if constexpr (OP == MH_MUL || DIVS) {
+        mh_shape in[2] = {sug, s1};
+        MH_TRY(build_elw_plan(sug, 2, in, &pl));
+        const float* p[2] = {ug, t1};
+        return run_map<F, 2, ACCUM>(out, pl, p, DIVS ? scal1(t2) : no_scal(), F{});
+    } else {
+        mh_shape in[3] = {sug, s1, s2};
+        MH_TRY(build_elw_plan(sug, 3, in, &pl));
+        const float* p[3] = {ug, t1, t2};
+        return run_map<F, 3, ACCUM>(out, pl, p, no_scal(), F{});
+    }
+}
+
+template <bool ACCUM>
+static int binary_rg(int op, int id, bool divs, float* out, const mh_shape& sug, const float* ug,
+                     const float* t1, const mh_shape& s1, const float* t2, const mh_shape& s2) {
+#define MH_RG(OPV, IDV, DV) return binary_rg_t<OPV, IDV, DV, ACCUM>(out, sug, ug, t1, s1, t2, s2)
+    switch (op) {
+        case MH_ADD: MH_RG(MH_ADD, 0, false);
+        case MH_SUB: if (id == 0) MH_RG(MH_SUB, 0, false); else MH_RG(MH_SUB, 1, false);
+        case MH_MUL: if (id == 0) MH_RG(MH_MUL, 0, false); else MH_RG(MH_MUL, 1, false);
+        default:
+            if (id == 0) MH_RG(MH_DIV, 0, false);
+            if (divs) MH_RG(MH_DIV, 1, true);
+            MH_RG(MH_DIV, 1, false);
+    }
+#undef MH_RG
+}
+
+// Exported to mh_reduce.hip / mh_fused.hip.
+int map_max_route(float* grad, const mh_shape& sx, const float* x, const mh_shape& sline,
+                  const float* m, const float* f, const float* ug) {
+    mh_shape in[4] = {sx, sline, sline, sline};
+    ElwPlan pl;
+    MH_TRY(build_elw_plan(sx, 4, in, &pl));
+    const float* p[4] = {x, m, f, ug};
+    return run_map<FMaxRoute, 4, true>(grad, pl, p, no_scal(), FMaxRoute{});
+}
+
+int map_scale_bcast(float* grad, const mh_shape& sx, const float* ug, const mh_shape& sug, float c,
+                    bool twice) {
+    mh_shape in[1] = {sug};
+    ElwPlan pl;
+    MH_TRY(build_elw_plan(sx, 1, in, &pl));
+    const float* p[1] = {ug};
+    if (twice) {
+        FScaleBcast<true> f;
+        f.c = c;
+        return run_map<FScaleBcast<true>, 1, true>(grad, pl, p, no_scal(), f);
+    }
+    FScaleBcast<false> f;
+    f.c = c;
+    return run_map<FScaleBcast<false>, 1, true>(grad, pl, p, no_scal(), f);
+}
+
+int map_mean_all(float* grad, int64_t n, const float* ug, float c) {
+    mh_shape s = flat_shape(n);
+    ElwPlan pl;
+    MH_TRY(build_elw_plan(s, 0, nullptr, &pl));
+    FMeanAll f;
+    f.c = c;
+    return run_map<FMeanAll, 0, true>(grad, pl, nullptr, scal1(ug), f);
+}
+
+int map_binary_rg_store(int op, int id, bool divs, float* rg, const mh_shape& sug, const float* ug,
+                        const float* t1, const mh_shape& s1, const float* t2, const mh_shape& s2) {
+    return binary_rg<false>(op, id, divs, rg, sug, ug, t1, s1, t2, s2);
+}
+
+int map_accum_same(float* grad, const float* rg, int64_t n, bool scalar_rg) {
+    mh_shape so = flat_shape(n);
+    mh_shape si = flat_shape(scalar_rg ? 1 : n);
+    ElwPlan pl;
+    MH_TRY(build_elw_plan(so, 1, &si, &pl));
+    const float* p[1] = {rg};
+    return run_map<FBinRg<MH_ADD, 0, false>, 1, true>(grad, pl, p, no_scal(), FBinRg<MH_ADD, 0, false>{});
+}
+
+int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* rg,
+                              const mh_shape& srg, bool negate, float* tmp);
+size_t unbroadcast_scratch_floats(const mh_shape& sgrad, const mh_shape& srg);
+
+}  // namespace mh
+
+using namespace mh;
+
+extern "C" {
+
+int mh_binary_fwd(int op, float* res, mh_shape sres, const float* a, mh_shape sa, const float* b,
+                  mh_shape sb) {
+    MH_TRY(check_op_binary(op));
+    MH_TRY(check_shape(sres, "res"));
+    MH_TRY(check_shape(sa, "a"));
+    MH_TRY(check_shape(sb, "b"));
+    mh_shape bs;
+    MH_TRY(broadcast_shapes(sa, sb, &bs));
+    if (!shape_eq(bs, sres)) return fail(MH_ERR_SHAPE, "mh_binary_fwd: res shape is not broadcast(a, b)");
+    if (numel(sres) == 0) return MH_OK;
+    if (!res || !a || !b) return fail(MH_ERR_NULL, "mh_binary_fwd: null tensor");
+    MH_TRY(require_init());
+    mh_shape in[2] = {sa, sb};
+    ElwPlan pl;
+    MH_TRY(build_elw_plan(sres, 2, in, &pl));
+    switch (op) {
+        case MH_ADD: MH_TRY(binary_fwd_t<MH_ADD>(res, pl, a, b)); break;
+        case MH_SUB: MH_TRY(binary_fwd_t<MH_SUB>(res, pl, a, b)); break;
+        case MH_MUL: MH_TRY(binary_fwd_t<MH_MUL>(res, pl, a, b)); break;
+        default: MH_TRY(binary_fwd_t<MH_DIV>(res, pl, a, b)); break;
+    }
+    return finish("mh_binary_fwd");
+}
+
+int mh_unary_fwd(int op, float* res, const float* x, int64_t n) {
+    MH_TRY(check_op_unary(op));
+    if (n < 0) return fail(MH_ERR_INVALID, "mh_unary_fwd: negative count");
+    if (n == 0) return MH_OK;
+    if (!res || !x) return fail(MH_ERR_NULL, "mh_unary_fwd: null tensor");
+    MH_TRY(require_init());
+    mh_shape s = flat_shape(n);
+    ElwPlan pl;
+    MH_TRY(build_elw_plan(s, 1, &s, &pl));
+    switch (op) {
+        case MH_EXP: MH_TRY(unary_fwd_t<MH_EXP>(res, pl, x)); break;
+        case MH_LOG: MH_TRY(unary_fwd_t<MH_LOG>(res, pl, x)); break;
+        case MH_SIGMOID: MH_TRY(unary_fwd_t<MH_SIGMOID>(res, pl, x)); break;
+        case MH_RELU: MH_TRY(unary_fwd_t<MH_RELU>(res, pl, x)); break;
+        default: MH_TRY(unary_fwd_t<MH_TANH>(res, pl, x)); break;
+    }
+    return finish("mh_unary_fwd");
+}
+
+int mh_pow_fwd(float* res, const float* x, int64_t n, const float* exponent) {
+    if (n < 0) return fail(MH_ERR_INVALID, "mh_pow_fwd: negative count");
+    if (n == 0) return MH_OK;
+    if (!res || !x || !exponent) return fail(MH_ERR_NULL, "mh_pow_fwd: null tensor");
+    MH_TRY(require_init());
+    mh_shape s = flat_shape(n);
+    ElwPlan pl;
+    MH_TRY(build_elw_plan(s, 1, &s, &pl));
+    const float* p[1] = {x};
+    MH_TRY((run_map<FPowi, 1, false>(res, pl, p, scal1(exponent), FPowi{})));
+    return finish("mh_pow_fwd");
+}
+
+int mh_unary_bwd_accum(int op, float* grad, const float* x, const float* ug, int64_t n) {
+    MH_TRY(check_op_unary(op));
+    if (n < 0) return fail(MH_ERR_INVALID, "mh_unary_bwd_accum: negative count");
+    if (n == 0) return MH_OK;
+    if (!grad || !x || !ug) return fail(MH_ERR_NULL, "mh_unary_bwd_accum: null tensor");
+    MH_TRY(require_init());
+    mh_shape s = flat_shape(n);
+    mh_shape in[2] = {s, s};
+    ElwPlan pl;
+    MH_TRY(build_elw_plan(s, 2, in, &pl));
+    switch (op) {
+        case MH_EXP: MH_TRY(unary_bwd_t<MH_EXP>(grad, pl, x, ug)); break;
+        case MH_LOG: MH_TRY(unary_bwd_t<MH_LOG>(grad, pl, x, ug)); break;
+        case MH_SIGMOID: MH_TRY(unary_bwd_t<MH_SIGMOID>(grad, pl, x, ug)); break;
+        case MH_RELU: MH_TRY(unary_bwd_t<MH_RELU>(grad, pl, x, ug)); break;
+        default: MH_TRY(unary_bwd_t<MH_TANH>(grad, pl, x, ug)); break;
+    }
+    return finish("mh_unary_bwd_accum");
+}
+
+int mh_pow_bwd_accum(int tensor_id, float* grad, const float* x, const float* exponent,
+                     const float* ug, int64_t n) {
+    if (tensor_id != 0 && tensor_id != 1) return fail(MH_ERR_INVALID, "mh_pow_bwd_accum: tensor_id %d", tensor_id);
+    if (n < 0) return fail(MH_ERR_INVALID, "mh_pow_bwd_accum: negative count");
+    if (n == 0) return MH_OK;
+    if (!grad || !x || !ug || !exponent) return fail(MH_ERR_NULL, "mh_pow_bwd_accum: null tensor");
+    MH_TRY(require_init());
+    if (tensor_id == 1) {
+        MH_TRY(pow_exponent_grad(grad, x, exponent, ug, n));
+        return finish("mh_pow_bwd_accum");
+    }
+    mh_shape s = flat_shape(n);
+    mh_shape in[2] = {s, s};
+    ElwPlan pl;
+    MH_TRY(build_elw_plan(s, 2, in, &pl));
+    const float* p[2] = {x, ug};
+    MH_TRY((run_map<FPowBwdX, 2, true>(grad, pl, p, scal1(exponent), FPowBwdX{})));
+    return finish("mh_pow_bwd_accum");
+}
+
+int mh_binary_bwd_accum(int op, int tensor_id, float* grad, mh_shape sgrad, const float* ug,
+                        mh_shape sug, const float* t1, mh_shape s1, const float* t2, mh_shape s2) {
+    MH_TRY(check_op_binary(op));
+    if (tensor_id != 0 && tensor_id != 1) return fail(MH_ERR_INVALID, "mh_binary_bwd_accum: tensor_id %d", tensor_id);
+    MH_TRY(check_shape(sgrad, "grad"));
+    MH_TRY(check_shape(sug, "ug"));
+    MH_TRY(check_shape(s1, "t1"));
+    MH_TRY(check_shape(s2, "t2"));
+    mh_shape bs;
+    MH_TRY(broadcast_shapes(s1, s2, &bs));
+    if (!shape_eq(bs, sug)) return fail(MH_ERR_SHAPE, "mh_binary_bwd_accum: ug shape is not broadcast(t1, t2)");
+    if (!shape_eq(sgrad, tensor_id == 0 ? s1 : s2))
+        return fail(MH_ERR_SHAPE, "mh_binary_bwd_accum: grad shape differs from operand %d", tensor_id);
+    if (numel(sug) == 0) return MH_OK;
+    const bool need_t1 = (op == MH_MUL && tensor_id == 1) || (op == MH_DIV && tensor_id == 1);
+    const bool need_t2 = (op == MH_MUL || op == MH_DIV);
+    if (!grad || !ug || (need_t1 && !t1) || (need_t2 && !t2))
+        return fail(MH_ERR_NULL, "mh_binary_bwd_accum: null tensor");
+    MH_TRY(require_init());
+    const bool divs = op == MH_DIV && tensor_id == 1 && is_scalar_shape(s2);
+    if (shape_eq(sgrad, sug)) {
+        MH_TRY(binary_rg<true>(op, tensor_id, divs, grad, sug, ug, t1, s1, t2, s2));
+        return finish("mh_binary_bwd_accum");
+    }
+    // operand was broadcast: accumulate_grad sums rg over the broadcast axes
+    const size_t red_floats = unbroadcast_scratch_floats(sgrad, sug);
+    if (op == MH_ADD || op == MH_SUB) {
+        float* tmp = nullptr;
+        MH_TRY(scratch(red_floats * sizeof(float), reinterpret_cast<void**>(&tmp)));
+        MH_TRY(unbroadcast_accum_scratch(grad, sgrad, ug, sug, op == MH_SUB && tensor_id == 1, tmp));
+        return finish("mh_binary_bwd_accum");
+    }
+    const size_t n = (size_t)numel(sug);
+    const size_t rg_floats = (n + 63) & ~(size_t)63;
+    float* base = nullptr;
+    MH_TRY(scratch((rg_floats + red_floats) * sizeof(float), reinterpret_cast<void**>(&base)));
+    float* rg = base;
+    MH_TRY(binary_rg<false>(op, tensor_id, divs, rg, sug, ug, t1, s1, t2, s2));
+    MH_TRY(unbroadcast_accum_scratch(grad, sgrad, rg, sug, false, base + rg_floats));
+    return finish("mh_binary_bwd_accum");
+}
+
+int mh_binary_bwd_accum2(int op, float* grad1, float* grad2, const float* ug, const float* t1,
+                         const float* t2, mh_shape s) {
+    MH_TRY(check_op_binary(op));
+    MH_TRY(check_shape(s, "shape"));
+    if (!grad1 && !grad2) return MH_OK;
+    if (!grad1 || !grad2 || is_scalar_shape(s) || numel(s) == 0 ||
+        !(aligned16(grad1) && aligned16(grad2) && aligned16(ug) && aligned16(t1) && aligned16(t2))) {
+        // one operand, a graph scalar (DIV's scalar rule), empty or unaligned: per operand
+        if (grad1) MH_TRY(mh_binary_bwd_accum(op, 0, grad1, s, ug, s, t1, s, t2, s));
+        if (grad2) MH_TRY(mh_binary_bwd_accum(op, 1, grad2, s, ug, s, t1, s, t2, s));
+        return MH_OK;
+    }
+    const bool need_ab = op == MH_MUL || op == MH_DIV;
+    if (!ug || (need_ab && (!t1 || !t2))) return fail(MH_ERR_NULL, "mh_binary_bwd_accum2: null tensor");
+    MH_TRY(require_init());
+    const int64_t n = numel(s);
+    dim3 g(grid_for(n >> 2, kThreads * kUnroll)), b(kThreads);
+    hipStream_t st = ctx().stream;
+    switch (op) {
+        case MH_ADD: hipLaunchKernelGGL(k_bwd2_same4<MH_ADD>, g, b, 0, st, grad1, grad2, ug, t1, t2, n); break;
+        case MH_SUB: hipLaunchKernelGGL(k_bwd2_same4<MH_SUB>, g, b, 0, st, grad1, grad2, ug, t1, t2, n); break;
+        case MH_MUL: hipLaunchKernelGGL(k_bwd2_same4<MH_MUL>, g, b, 0, st, grad1, grad2, ug, t1, t2, n); break;
+        default: hipLaunchKernelGGL(k_bwd2_same4<MH_DIV>, g, b, 0, st, grad1, grad2, ug, t1, t2, n); break;
+    }
+    return finish("mh_binary_bwd_accum2");
+}
+
+int mh_accumulate_grad(float* grad, mh_shape sgrad, const float* rg, mh_shape srg) {
+    MH_TRY(check_shape(sgrad, "grad"));
+    MH_TRY(check_shape(srg, "rg"));
+    const bool same = shape_eq(sgrad, srg);
+    const bool scal = !same && is_scalar_shape(srg);
+    if (!same && !scal && !broadcasts_to(sgrad, srg))
+        return fail(MH_ERR_SHAPE, "mh_accumulate_grad: grad shape does not broadcast to rg shape");
+    if (numel(sgrad) == 0 || numel(srg) == 0) return MH_OK;
+    if (!grad || !rg) return fail(MH_ERR_NULL, "mh_accumulate_grad: null tensor");
+    MH_TRY(require_init());
+    if (same || scal) {
+        MH_TRY(map_accum_same(grad, rg, numel(sgrad), scal));
+        return finish("mh_accumulate_grad");
+    }
+    float* tmp = nullptr;
+    MH_TRY(scratch(unbroadcast_scratch_floats(sgrad, srg) * sizeof(float), reinterpret_cast<void**>(&tmp)));
+    MH_TRY(unbroadcast_accum_scratch(grad, sgrad, rg, srg, false, tmp));
+    return finish("mh_accumulate_grad");
+}
+
+}  // extern "C"

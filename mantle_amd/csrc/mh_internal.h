@@ -1,0 +1,145 @@
+// mh_internal.h -- host-side internals of libmantle_hip.so: context, error reporting,
+// shape validation and the collapsed launch plans shared by the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+
+#include "../../include/mantle_hip.h"
+
+namespace mh {
+
+// ---------------------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------------------
+struct Context {
+    bool initialized = false;
+    int device = -1;
+    uint64_t flags = 0;
+    hipStream_t stream = nullptr;
+    void* scratch = nullptr;  // library-owned, grown on demand (two-pass reductions)
+    size_t scratch_bytes = 0;
+    void* stage = nullptr;  // library-owned staging for materialised intermediates
+    size_t stage_bytes = 0;
+    int num_cus = 256;
+};
+Context& ctx();
+
+// Error reporting: records a thread-local message and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Wraps every HIP runtime call. MANTLE_HIP_FAIL_AT=<n> makes the n-th wrapped call fail
+// (failure-path tests without a GPU fault).
+int hip_check(hipError_t e, const char* what);
+#define MH_HIP(call)                                      \
+    do {                                                  \
+        int rc__ = ::mh::hip_check((call), #call);        \
+        if (rc__ != MH_OK) return rc__;                   \
+    } while (0)
+#define MH_TRY(expr)                    \
+    do {                                \
+        int rc__ = (expr);              \
+        if (rc__ != MH_OK) return rc__; \
+    } while (0)
+
+int require_init();
+// End of an entry point: checks the launch and synchronises unless MH_INIT_ASYNC.
+int finish(const char* what);
+// Library scratch of at least `bytes` (synchronises before growing).
+int scratch(size_t bytes, void** out);
+// A second library buffer for intermediates that live across calls using scratch().
+int stage(size_t bytes, void** out);
+
+// ---------------------------------------------------------------------------------------
+// shapes
+// ---------------------------------------------------------------------------------------
+int check_shape(const mh_shape& s, const char* name);
+int64_t numel(const mh_shape& s);
+bool shape_eq(const mh_shape& a, const mh_shape& b);
+bool is_scalar_shape(const mh_shape& s);  // TensorShape(1)
+int broadcast_shapes(const mh_shape& s1, const mh_shape& s2, mh_shape* out);
+bool broadcasts_to(const mh_shape& small, const mh_shape& big);
+void broadcast_strides(int size, const mh_shape& shape, int64_t* strides);
+mh_shape reduced_shape(const mh_shape& s, int axis);  // get_reduce_shape; axis<0 -> (1)
+mh_shape flat_shape(int64_t n);
+
+// ---------------------------------------------------------------------------------------
+// fast unsigned division by an invariant (Granlund & Montgomery, "Division by invariant
+// integers using multiplication", PLDI 1994): q = (umulhi(n, mul) + n) >> shr, exact for
+// all 32-bit n and 1 <= d < 2^31.
+// ---------------------------------------------------------------------------------------
+struct FastDiv {
+    uint32_t d, mul, shr;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+    FastDiv f;
+    f.d = d;
+    uint32_t s = 0;
+    while ((1ull << s) < d) ++s;
+    f.shr = s;
+    f.mul = (uint32_t)(((1ull << 32) * ((1ull << s) - d)) / d + 1);
+    return f;
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+    uint32_t t = __umulhi(n, f.mul);
+    return (uint32_t)(((uint64_t)t + n) >> f.shr);
+}
+
+// ---------------------------------------------------------------------------------------
+// elementwise launch plan: output shape collapsed (size-1 dims dropped, dims merged where
+// every input is contiguous across the pair), one stride row per input.
+// ---------------------------------------------------------------------------------------
+constexpr int kMaxIn = 4;
+enum InKind : int32_t { IN_FULL = 0, IN_SCALAR = 1, IN_BCAST = 2 };
+
+struct ElwPlan {
+    int64_t n = 0;   // output element count
+    int32_t rank = 0;
+    int32_t nin = 0;
+    int32_t kind[kMaxIn] = {0, 0, 0, 0};
+    int64_t dims[MH_MAX_RANK] = {};
+    int64_t st[kMaxIn][MH_MAX_RANK] = {};
+    FastDiv fd[MH_MAX_RANK] = {};
+    int32_t vec_ok = 0;  // inner dim % 4 == 0 and each strided input has inner stride 0/1
+    int32_t any_bcast = 0;
+};
+// Builds the plan for an output of shape `out` and inputs of the given shapes (each must
+// broadcast to `out`).
+int build_elw_plan(const mh_shape& out, int nin, const mh_shape* in, ElwPlan* plan);
+
+// ---------------------------------------------------------------------------------------
+// kernels (defined in mh_elementwise.hip / mh_reduce.hip)
+// ---------------------------------------------------------------------------------------
+// Reduction operator and epilogue ids shared by the reduce launchers.
+enum RedOp : int { RED_SUM = 0, RED_MAX = 1, RED_MAXCNT = 2 };
+enum Epi : int {
+    EPI_STORE = 0,     // out = v
+    EPI_MEAN = 1,      // out = v / (float)len
+    EPI_ACCUM = 2,     // out = out + v
+    EPI_ACCUM_NEG = 3  // out = out + (-v)
+};
+// Reduce x viewed as [A, B, C] over B into out[A*C] (out2: fl(1/count) for RED_MAXCNT).
+// `div` is the float divisor of EPI_MEAN; `tmp` holds split partials
+// (reduce_abc_tmp_floats(op, A, B, C) floats, may be null when that is 0).
+size_t reduce_abc_tmp_floats(int op, int64_t A, int64_t B, int64_t C);
+int reduce_abc(int op, int epi, const float* x, int64_t A, int64_t B, int64_t C, float* out,
+               float* out2, float div, float* tmp);
+// Sum over all n elements of the POW exponent-gradient term, accumulated into grad[0].
+int pow_exponent_grad(float* grad, const float* x, const float* exponent, const float* ug,
+                      int64_t n);
+// grad += un-broadcast(rg) (or += -un-broadcast(rg)): the chain of single-axis reductions.
+size_t unbroadcast_scratch_floats(const mh_shape& sgrad, const mh_shape& srg);
+int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* rg,
+                              const mh_shape& srg, bool negate, float* tmp);
+int plan_unbroadcast(const mh_shape& sgrad, const mh_shape& srg, mh_reduce_plan_info* info);
+
+// Elementwise helpers used by the reduction and fused entry points.
+int map_max_route(float* grad, const mh_shape& sx, const float* x, const mh_shape& sline,
+                  const float* m, const float* f, const float* ug);
+int map_scale_bcast(float* grad, const mh_shape& sx, const float* ug, const mh_shape& sug,
+                    float c, bool twice);
+int map_mean_all(float* grad, int64_t n, const float* ug, float c);
+int map_accum_same(float* grad, const float* rg, int64_t n, bool scalar_rg);
+
+}  // namespace mh

@@ -1,0 +1,116 @@
+// mh_math.h -- fp32 device math of Mantle's ops, evaluated in the reference's exact
+// expression order. Compiled with -ffp-contract=off: an fma appears only where written.
+//
+// exp and log follow the algorithms Mantle's CPU path gets from the Mojo stdlib
+// (std.math.exp / std.math.log as called at mantle/core/math_util.mojo:149-196 and
+// mantle/autograd/ops/mlops.mojo:13,39,201):
+//   exp: clamp to [-88.3762626647949, 88.3762626647950], k = floor(fma(x, 1/ln2, 0.5)),
+//        r = fma(k, -ln2, x), degree-7 Taylor polynomial of e^r (fma Horner), times 2^k;
+//   log: the Cephes logf method (S. L. Moshier, Cephes Math Library): frexp, fold below
+//        sqrt(1/2), degree-8 minimax polynomial, exponent added in two parts of ln 2.
+// Float pow is the stdlib's scalar rule: integral exponent -> binary exponentiation,
+// negative base with fractional exponent -> NaN, otherwise exp(y * log(x)).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace mh {
+
+__device__ __forceinline__ float pow2i(int e) {  // 2^e, e in [-126, 127]
+    return __uint_as_float((uint32_t)(e + 127) << 23);
+}
+
+// p * 2^k in two exact power-of-two steps (one rounding only for subnormal results).
+__device__ __forceinline__ float scale2(float p, int k) {
+    int k1 = k >> 1;
+    int k2 = k - k1;
+    return (p * pow2i(k1)) * pow2i(k2);
+}
+
+__device__ __forceinline__ float mexp(float x) {
+    if (x != x) return x;
+    const float lo = -88.3762626647949f, hi = 88.3762626647950f;
+    float xc = x < lo ? lo : (x > hi ? hi : x);
+    float k = __builtin_floorf(__builtin_fmaf(xc, 1.442695040888963407359924681001892137426646f, 0.5f));
+    float r = __builtin_fmaf(k, -0.69314718055966295651160180568695068359375f, xc);
+    float p = 1.98412698412698412698e-4f;
+    p = __builtin_fmaf(p, r, 1.38888888888888888889e-3f);
+    p = __builtin_fmaf(p, r, 8.33333333333333333333e-3f);
+    p = __builtin_fmaf(p, r, 4.16666666666666666667e-2f);
+    p = __builtin_fmaf(p, r, 1.66666666666666666667e-1f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return scale2(p, (int)k);
+}
+
+__device__ __forceinline__ float mlog(float x) {
+    if (x != x) return x;
+    if (x < 0.0f) return __builtin_nanf("");
+    if (x == 0.0f) return -__builtin_inff();
+    if (x == __builtin_inff()) return x;
+    int eadj = 0;
+    if (x < 1.17549435e-38f) {  // FLT_MIN: scale subnormals by 2^25 (exact)
+        x = x * 33554432.0f;
+        eadj = -25;
+    }
+    uint32_t u = __float_as_uint(x);
+    int e = (int)((u >> 23) & 0xffu) - 126 + eadj;
+    float m = __uint_as_float((u & 0x807fffffu) | 0x3f000000u);
+    if (m < 0.707106781186547524f) {
+        e -= 1;
+        m = m + m - 1.0f;
+    } else {
+        m = m - 1.0f;
+    }
+    float z = m * m;
+    float y = 7.0376836292e-2f;
+    y = y * m - 1.1514610310e-1f;
+    y = y * m + 1.1676998740e-1f;
+    y = y * m - 1.2420140846e-1f;
+    y = y * m + 1.4249322787e-1f;
+    y = y * m - 1.6668057665e-1f;
+    y = y * m + 2.0000714765e-1f;
+    y = y * m - 2.4999993993e-1f;
+    y = y * m + 3.3333331174e-1f;
+    y = y * m * z;
+    float fe = (float)e;
+    y = y + -2.12194440e-4f * fe;
+    y = y + -0.5f * z;
+    float r = m + y;
+    r = r + 0.693359375f * fe;
+    return r;
+}
+
+// pow(SIMD, Int): result seeded at 1, square-and-multiply, 1/res for negative n.
+__device__ __forceinline__ float mpowi(float x, int64_t n) {
+    uint64_t b = n < 0 ? (uint64_t)(-(n + 1)) + 1u : (uint64_t)n;
+    float a = x, res = 1.0f;
+    while (b > 0) {
+        if (b & 1u) res = res * a;
+        a = a * a;
+        b >>= 1;
+    }
+    return n < 0 ? 1.0f / res : res;
+}
+
+__device__ __forceinline__ float mpowf(float x, float y) {
+    if (y != y) return y;
+    float yi = __builtin_truncf(y);
+    if (yi == y && __builtin_fabsf(y) < 2147483648.0f) return mpowi(x, (int64_t)yi);
+    if (x < 0.0f) return __builtin_nanf("");
+    return mexp(y * mlog(x));
+}
+
+__device__ __forceinline__ float msigmoid(float x) { return 1.0f / (1.0f + mexp(-x)); }
+
+__device__ __forceinline__ float mtanh(float x) {
+    float ep = mexp(x), em = mexp(-x);
+    return (ep - em) / (ep + em);
+}
+
+__device__ __forceinline__ float mrelu(float x) { return x > 0.0f ? x : 0.0f; }
+
+}  // namespace mh

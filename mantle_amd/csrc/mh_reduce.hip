@@ -1,0 +1,576 @@
+// mh_reduce.hip -- axis / all-element reductions, un-broadcast gradient accumulation, MAX
+// backward tie routing and the POW exponent gradient.
+//
+// Every reduction is expressed on a view [A, B, C] reduced over B:
+//   C == 1, B <= 64 : one thread per output row;
+//   C == 1          : one wavefront (64 lanes) per row, 128-bit loads, butterfly shuffle;
+//                     few long rows are cut into chunks whose partials a second pass combines;
+//   C  > 1          : one thread per output column (a quad of columns when C % 4 == 0), the
+//                     B rows split across blocks when that is needed to fill the chip, the
+//                     split partials combined by a second pass in fixed split order.
+// No atomics: each output's summation order is fixed by the launch shape, so a call repeated
+// on the same input returns the same bits.
+#include <cfloat>
+
+#include "mh_internal.h"
+#include "mh_math.h"
+
+namespace mh {
+
+constexpr int kRThreads = 256;
+
+// ---------------------------------------------------------------------------------------
+// reduction policies
+// ---------------------------------------------------------------------------------------
+struct RSum {
+    using T = float;
+    __device__ static T init() { return 0.0f; }
+    __device__ static T lift(float x) { return x; }
+    __device__ static T comb(T a, T b) { return a + b; }
+    __device__ static T shfl(T v, int m) { return __shfl_xor(v, m); }
+};
+struct RMax {  // max_simd (math_util.mojo:224-244): a > b ? a : b, start -FLT_MAX
+    using T = float;
+    __device__ static T init() { return -FLT_MAX; }
+    __device__ static T lift(float x) { return x; }
+    __device__ static T comb(T a, T b) { return a > b ? a : b; }
+    __device__ static T shfl(T v, int m) { return __shfl_xor(v, m); }
+};
+struct MC {
+    float m;
+    uint32_t c;
+};
+struct RMaxCnt {  // (line max, number of elements equal to it)
+    using T = MC;
+    __device__ static T init() { return MC{-FLT_MAX, 0u}; }
+    __device__ static T lift(float x) { return MC{x, 1u}; }
+    __device__ static T comb(T a, T b) {
+        if (a.m > b.m) return a;
+        if (b.m > a.m) return b;
+        return MC{a.m, a.c + b.c};
+    }
+    __device__ static T shfl(T v, int m) {
+        return MC{__shfl_xor(v.m, m), (uint32_t)__shfl_xor((int)v.c, m)};
+    }
+};
+
+// ---------------------------------------------------------------------------------------
+// loaders: get(i) -> R::T at element i; get4 for 16-byte aligned quads
+// ---------------------------------------------------------------------------------------
+template <class R>
+struct LdPlain {
+    const float* x;
+    __device__ void setup() {}
+    __device__ typename R::T get(int64_t i) const { return R::lift(x[i]); }
+    __device__ void get4(int64_t i, typename R::T* o) const {
+        float4 q = *reinterpret_cast<const float4*>(x + i);
+        o[0] = R::lift(q.x); o[1] = R::lift(q.y); o[2] = R::lift(q.z); o[3] = R::lift(q.w);
+    }
+};
+
+struct LdPairs {  // split partials of RMaxCnt
+    const float* m;
+    const uint32_t* c;
+    __device__ void setup() {}
+    __device__ MC get(int64_t i) const { return MC{m[i], c[i]}; }
+    __device__ void get4(int64_t i, MC* o) const {
+        for (int j = 0; j < 4; ++j) o[j] = get(i + j);
+    }
+};
+
+// POW exponent gradient term (basics.mojo:359-376): powf(x, a) * (isinf(log x) ? 0 : log x) * ug.
+struct LdPowGrad {
+    const float* x;
+    const float* ug;
+    const float* ap;
+    float a;
+    __device__ void setup() { a = ap[0]; }
+    __device__ float term(float xv, float u) const {
+        float lg = mlog(xv);
+        if (__builtin_isinf(lg)) lg = 0.0f;
+        return (mpowf(xv, a) * lg) * u;
+    }
+    __device__ float get(int64_t i) const { return term(x[i], ug[i]); }
+    __device__ void get4(int64_t i, float* o) const {
+        float4 q = *reinterpret_cast<const float4*>(x + i);
+        float4 u = *reinterpret_cast<const float4*>(ug + i);
+        o[0] = term(q.x, u.x); o[1] = term(q.y, u.y); o[2] = term(q.z, u.z); o[3] = term(q.w, u.w);
+    }
+};
+
+// ---------------------------------------------------------------------------------------
+// epilogues
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ void epi_store(float* out, float*, int64_t o, float v, int epi, float div) {
+    switch (epi) {
+        case EPI_STORE: out[o] = v; break;
+        case EPI_MEAN: out[o] = v / div; break;
+        case EPI_ACCUM: out[o] = out[o] + v; break;
+        default: out[o] = out[o] + (-v); break;
+    }
+}
+__device__ __forceinline__ void epi_store(float* out, float* out2, int64_t o, MC v, int, float) {
+    out[o] = v.m;
+    out2[o] = 1.0f / (float)v.c;  // MAX.backward: factor = 1 / count, basics.mojo:573, 609
+}
+// MC partials keep the counts in a second array right after the maxima.
+__device__ __forceinline__ void part_store2(float* pm, int64_t npart, int64_t o, float v) { pm[o] = v; (void)npart; }
+__device__ __forceinline__ void part_store2(float* pm, int64_t npart, int64_t o, MC v) {
+    pm[o] = v.m;
+    reinterpret_cast<uint32_t*>(pm + npart)[o] = v.c;
+}
+
+template <class R>
+__device__ __forceinline__ typename R::T wave_reduce(typename R::T v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = R::comb(v, R::shfl(v, m));
+    return v;
+}
+
+// ---------------------------------------------------------------------------------------
+// kernels
+// ---------------------------------------------------------------------------------------
+// One thread per row of length B (B small or zero).
+template <class R, class LD>
+__global__ void __launch_bounds__(kRThreads)
+    k_rows_thread(LD ld, int64_t nrows, int64_t B, float* out, float* out2, int epi, float div) {
+    ld.setup();
+    const int64_t stride = (int64_t)gridDim.x * kRThreads;
+    for (int64_t r = (int64_t)blockIdx.x * kRThreads + threadIdx.x; r < nrows; r += stride) {
+        typename R::T acc = R::init();
+        const int64_t base = r * B;
+        for (int64_t j = 0; j < B; ++j) acc = R::comb(acc, ld.get(base + j));
+        epi_store(out, out2, r, acc, epi, div);
+    }
+}
+
+// One wavefront per (row, chunk): virtual row vr = r * S + s covers elements
+// [r*B + s*L, r*B + min((s+1)*L, B)). S == 1 writes the epilogue, S > 1 writes partials.
+template <class R, class LD, bool VEC>
+__global__ void __launch_bounds__(kRThreads)
+    k_rows_wave(LD ld, int64_t nvrows, int64_t S, int64_t B, int64_t L, float* out, float* out2,
+                int epi, float div, float* part) {
+    ld.setup();
+    using T = typename R::T;
+    const int lane = threadIdx.x & 63;
+    const int64_t vr = (int64_t)blockIdx.x * (kRThreads / 64) + (threadIdx.x >> 6);
+    if (vr >= nvrows) return;  // uniform per wavefront; no block-level barrier follows
+    const int64_t r = vr / S, s = vr - r * S;
+    const int64_t start = r * B + s * L;
+    const int64_t rem = B - s * L;
+    const int64_t len = rem < L ? rem : L;
+    T acc = R::init();
+    if (VEC) {
+        const int64_t nq = len >> 2;
+        T a4[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a4[u][j] = R::init();
+        int64_t q = lane;
+        for (; q + 192 < nq; q += 256) {
+            T v[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) ld.get4(start + (q + 64 * u) * 4, v[u]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a4[u][j] = R::comb(a4[u][j], v[u][j]);
+        }
+        for (; q < nq; q += 64) {
+            T v[4];
+            ld.get4(start + q * 4, v);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a4[0][j] = R::comb(a4[0][j], v[j]);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = R::comb(acc, a4[u][j]);
+    } else {
+        for (int64_t j = lane; j < len; j += 64) acc = R::comb(acc, ld.get(start + j));
+    }
+    acc = wave_reduce<R>(acc);
+    if (lane == 0) {
+        if (S == 1) epi_store(out, out2, r, acc, epi, div);
+        else part_store2(part, nvrows, vr, acc);
+    }
+}
+
+// Column reduction: item = a quad (VEC) or one element of the flattened [A, C] output; the
+// rows [b0, b1) of split blockIdx.y. S == 1 writes the epilogue, S > 1 writes partials at
+// s * (A * C) + o.
+template <class R, class LD, bool VEC>
+__global__ void __launch_bounds__(kRThreads)
+    k_cols(LD ld, int64_t A, int64_t B, int64_t C, int64_t rps, int64_t S, float* out, float* out2,
+           int epi, float div, float* part) {
+    ld.setup();
+    using T = typename R::T;
+    constexpr int W = VEC ? 4 : 1;
+    const int64_t AC = A * C;
+    const int64_t item = (int64_t)blockIdx.x * kRThreads + threadIdx.x;
+    const int64_t o = item * W;
+    if (o >= AC) return;
+    const int64_t a = o / C, c = o - a * C;
+    const int64_t s = blockIdx.y;
+    const int64_t b0 = s * rps;
+    const int64_t b1 = (b0 + rps < B) ? b0 + rps : B;
+    const int64_t base = a * B * C + c;
+    T acc[W];
+#pragma unroll
+    for (int j = 0; j < W; ++j) acc[j] = R::init();
+    int64_t b = b0;
+    for (; b + 3 < b1; b += 4) {
+        T v[4][W];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (VEC) ld.get4(base + (b + u) * C, v[u]);
+            else v[u][0] = ld.get(base + (b + u) * C);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < W; ++j) acc[j] = R::comb(acc[j], v[u][j]);
+    }
+    for (; b < b1; ++b) {
+        T v[W];
+        if (VEC) ld.get4(base + b * C, v);
+        else v[0] = ld.get(base + b * C);
+#pragma unroll
+        for (int j = 0; j < W; ++j) acc[j] = R::comb(acc[j], v[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+        if (S == 1) epi_store(out, out2, o + j, acc[j], epi, div);
+        else part_store2(part, S * AC, s * AC + o + j, acc[j]);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// launch planning
+// ---------------------------------------------------------------------------------------
+static inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+struct RowSplit {
+    int64_t S, L;
+};
+static RowSplit row_split(int64_t A, int64_t B) {
+    RowSplit rs{1, B};
+    const int64_t target = 8 * (int64_t)ctx().num_cus;  // wavefronts wanted in flight
+    if (A < target && B >= 8192) {
+        int64_t S = (target + A - 1) / A;
+        int64_t L = (B + S - 1) / S;
+        L = (L + 1023) & ~(int64_t)1023;
+        rs.S = (B + L - 1) / L;
+        rs.L = L;
+    }
+    return rs;
+}
+
+struct ColSplit {
+    int64_t S, rps;
+    bool vec;
+};
+static ColSplit col_split(int64_t A, int64_t B, int64_t C, bool vec) {
+    ColSplit cs;
+    cs.vec = vec;
+    const int64_t items = A * C / (vec ? 4 : 1);
+    const int64_t bx = (items + kRThreads - 1) / kRThreads;
+    const int64_t target = 8 * (int64_t)ctx().num_cus;  // blocks wanted
+    int64_t S = 1;
+    if (bx < target) {
+        S = (target + bx - 1) / bx;
+        int64_t maxS = B / 16;
+        if (maxS < 1) maxS = 1;
+        if (S > maxS) S = maxS;
+        if (S > 65535) S = 65535;
+    }
+    cs.rps = (B + S - 1) / S;
+    if (cs.rps < 1) cs.rps = 1;
+    cs.S = (B + cs.rps - 1) / cs.rps;
+    if (cs.S < 1) cs.S = 1;
+    return cs;
+}
+
+template <class R>
+static constexpr int part_words() {
+    return sizeof(typename R::T) == 4 ? 1 : 2;
+}
+
+// Scratch floats a reduction of [A, B, C] needs for its partials.
+template <class R>
+static size_t tmp_floats_t(int64_t A, int64_t B, int64_t C, bool vec_ok) {
+    if (A * C == 0) return 0;
+    if (C == 1) {
+        if (B <= 64) return 0;
+        RowSplit rs = row_split(A, B);
+        return rs.S > 1 ? (size_t)(A * rs.S) * part_words<R>() : 0;
+    }
+    ColSplit cs = col_split(A, B, C, vec_ok && C % 4 == 0);
+    return cs.S > 1 ? (size_t)(cs.S * A * C) * part_words<R>() : 0;
+}
+
+size_t reduce_abc_tmp_floats(int op, int64_t A, int64_t B, int64_t C) {
+    if (op == RED_MAXCNT) return tmp_floats_t<RMaxCnt>(A, B, C, true);
+    return tmp_floats_t<RSum>(A, B, C, true);
+}
+
+template <class R>
+struct PartLoader {
+    using type = LdPlain<R>;
+    static type make(float* p, int64_t) { return type{p}; }
+};
+template <>
+struct PartLoader<RMaxCnt> {
+    using type = LdPairs;
+    static type make(float* p, int64_t n) { return LdPairs{p, reinterpret_cast<const uint32_t*>(p + n)}; }
+};
+
+// nosplit: a combine stage over split partials runs as a single pass (tmp unused).
+template <class R, class LD>
+static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C, float* out,
+                    float* out2, float div, float* tmp, bool nosplit = false) {
+    if (A * C == 0) return MH_OK;
+    hipStream_t st = ctx().stream;
+    if (C == 1) {
+        if (B <= 64) {
+            int64_t blocks = (A + kRThreads - 1) / kRThreads;
+            if (blocks > 65536) blocks = 65536;
+            hipLaunchKernelGGL((k_rows_thread<R, LD>), dim3((unsigned)blocks), dim3(kRThreads), 0, st, ld, A,
+                               B, out, out2, epi, div);
+            return MH_OK;
+        }
+        RowSplit rs = nosplit ? RowSplit{1, B} : row_split(A, B);
+        const bool vec = vec_ok && B % 4 == 0 && rs.L % 4 == 0;
+        const int64_t nv = A * rs.S;
+        dim3 g((unsigned)((nv + 3) / 4)), b(kRThreads);
+        if (vec) hipLaunchKernelGGL((k_rows_wave<R, LD, true>), g, b, 0, st, ld, nv, rs.S, B, rs.L, out, out2, epi, div, tmp);
+        else hipLaunchKernelGGL((k_rows_wave<R, LD, false>), g, b, 0, st, ld, nv, rs.S, B, rs.L, out, out2, epi, div, tmp);
+        if (rs.S > 1) {
+            using PL = PartLoader<R>;
+            return reduce_t<R, typename PL::type>(PL::make(tmp, nv), true, epi, A, rs.S, 1, out, out2, div,
+                                                  nullptr, true);
+        }
+        return MH_OK;
+    }
+    ColSplit cs = col_split(A, B, C, vec_ok && C % 4 == 0);
+    if (nosplit) {
+        cs.S = 1;
+        cs.rps = B;
+    }
+    const int64_t items = A * C / (cs.vec ? 4 : 1);
+    dim3 g((unsigned)((items + kRThreads - 1) / kRThreads), (unsigned)cs.S), b(kRThreads);
+    if (cs.vec) hipLaunchKernelGGL((k_cols<R, LD, true>), g, b, 0, st, ld, A, B, C, cs.rps, cs.S, out, out2, epi, div, tmp);
+    else hipLaunchKernelGGL((k_cols<R, LD, false>), g, b, 0, st, ld, A, B, C, cs.rps, cs.S, out, out2, epi, div, tmp);
+    if (cs.S > 1) {
+        using PL = PartLoader<R>;
+        const int64_t np = cs.S * A * C;
+        return reduce_t<R, typename PL::type>(PL::make(tmp, np), sizeof(typename R::T) == 4, epi, 1, cs.S,
+                                              A * C, out, out2, div, nullptr, true);
+    }
+    return MH_OK;
+}
+
+int reduce_abc(int op, int epi, const float* x, int64_t A, int64_t B, int64_t C, float* out, float* out2,
+               float div, float* tmp) {
+    const bool al = al16(x);
+    switch (op) {
+        case RED_SUM: return reduce_t<RSum, LdPlain<RSum>>(LdPlain<RSum>{x}, al, epi, A, B, C, out, out2, div, tmp);
+        case RED_MAX: return reduce_t<RMax, LdPlain<RMax>>(LdPlain<RMax>{x}, al, epi, A, B, C, out, out2, div, tmp);
+        default:
+            return reduce_t<RMaxCnt, LdPlain<RMaxCnt>>(LdPlain<RMaxCnt>{x}, al, epi, A, B, C, out, out2, div, tmp);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// un-broadcast chain: accumulate_grad with grad broadcast to rg (tensorutils.mojo:473-487)
+// ---------------------------------------------------------------------------------------
+int plan_unbroadcast(const mh_shape& sgrad, const mh_shape& srg, mh_reduce_plan_info* info) {
+    if (!broadcasts_to(sgrad, srg))
+        return fail(MH_ERR_SHAPE, "grad shape does not broadcast to the gradient's shape");
+    int64_t gst[MH_MAX_RANK];
+    broadcast_strides(srg.rank, sgrad, gst);
+    // groups of adjacent non-unit dims with the same class (reduced: grad stride 0)
+    int64_t size[MH_MAX_RANK];
+    bool red[MH_MAX_RANK];
+    int ng = 0;
+    for (int d = 0; d < srg.rank; ++d) {
+        if (srg.dims[d] == 1) continue;
+        const bool r = gst[d] == 0;
+        if (ng > 0 && red[ng - 1] == r) {
+            size[ng - 1] *= srg.dims[d];
+        } else {
+            size[ng] = srg.dims[d];
+            red[ng] = r;
+            ++ng;
+        }
+    }
+    memset(info, 0, sizeof *info);
+    int steps = 0;
+    for (;;) {
+        int j = -1;
+        for (int g = ng - 1; g >= 0; --g)
+            if (red[g]) {
+                j = g;
+                break;
+            }
+        if (j < 0) break;
+        int64_t A = 1, C = 1;
+        for (int g = 0; g < j; ++g) A *= size[g];
+        for (int g = j + 1; g < ng; ++g) C *= size[g];
+        info->a[steps] = A;
+        info->b[steps] = size[j];
+        info->c[steps] = C;
+        ++steps;
+        // remove group j; merge the kept neighbours that become adjacent
+        for (int g = j; g + 1 < ng; ++g) {
+            size[g] = size[g + 1];
+            red[g] = red[g + 1];
+        }
+        --ng;
+        if (j > 0 && j < ng && !red[j - 1] && !red[j]) {
+            size[j - 1] *= size[j];
+            for (int g = j; g + 1 < ng; ++g) {
+                size[g] = size[g + 1];
+                red[g] = red[g + 1];
+            }
+            --ng;
+        }
+    }
+    info->nsteps = steps;
+    return MH_OK;
+}
+
+size_t unbroadcast_scratch_floats(const mh_shape& sgrad, const mh_shape& srg) {
+    mh_reduce_plan_info p;
+    if (plan_unbroadcast(sgrad, srg, &p) != MH_OK) return 0;
+    size_t tmax = 0, bmax = 0;
+    for (int i = 0; i < p.nsteps; ++i) {
+        size_t t = reduce_abc_tmp_floats(RED_SUM, p.a[i], p.b[i], p.c[i]);
+        if (t > tmax) tmax = t;
+        size_t o = (size_t)(p.a[i] * p.c[i]);
+        if (o > bmax) bmax = o;
+    }
+    auto pad = [](size_t v) { return (v + 63) & ~(size_t)63; };
+    return pad(tmax) + 2 * pad(bmax) + 64;
+}
+
+int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* rg, const mh_shape& srg,
+                              bool negate, float* tmp) {
+    mh_reduce_plan_info p;
+    MH_TRY(plan_unbroadcast(sgrad, srg, &p));
+    const int final_epi = negate ? EPI_ACCUM_NEG : EPI_ACCUM;
+    if (p.nsteps == 0)  // only size-1 dims differ: same element order
+        return reduce_abc(RED_SUM, final_epi, rg, numel(srg), 1, 1, grad, nullptr, 0.0f, nullptr);
+    size_t tmax = 0, bmax = 0;
+    for (int i = 0; i < p.nsteps; ++i) {
+        size_t t = reduce_abc_tmp_floats(RED_SUM, p.a[i], p.b[i], p.c[i]);
+        if (t > tmax) tmax = t;
+        size_t o = (size_t)(p.a[i] * p.c[i]);
+        if (o > bmax) bmax = o;
+    }
+    auto pad = [](size_t v) { return (v + 63) & ~(size_t)63; };
+    float* part = tmp;
+    float* buf[2] = {tmp + pad(tmax), tmp + pad(tmax) + pad(bmax)};
+    const float* src = rg;
+    for (int i = 0; i < p.nsteps; ++i) {
+        const bool last = i == p.nsteps - 1;
+        float* dst = last ? grad : buf[i & 1];
+        MH_TRY(reduce_abc(RED_SUM, last ? final_epi : EPI_STORE, src, p.a[i], p.b[i], p.c[i], dst, nullptr,
+                          0.0f, part));
+        src = dst;
+    }
+    return MH_OK;
+}
+
+int pow_exponent_grad(float* grad, const float* x, const float* exponent, const float* ug, int64_t n) {
+    LdPowGrad ld{x, ug, exponent, 0.0f};
+    const size_t t = tmp_floats_t<RSum>(1, n, 1, true);
+    float* tmp = nullptr;
+    MH_TRY(scratch((t + 64) * sizeof(float), reinterpret_cast<void**>(&tmp)));
+    return reduce_t<RSum, LdPowGrad>(ld, al16(x) && al16(ug), EPI_ACCUM, 1, n, 1, grad, nullptr, 0.0f, tmp);
+}
+
+// elementwise helpers (mh_elementwise.hip)
+int map_max_route(float* grad, const mh_shape& sx, const float* x, const mh_shape& sline, const float* m,
+                  const float* f, const float* ug);
+int map_scale_bcast(float* grad, const mh_shape& sx, const float* ug, const mh_shape& sug, float c, bool twice);
+int map_mean_all(float* grad, int64_t n, const float* ug, float c);
+
+static void abc_of(const mh_shape& s, int axis, int64_t* A, int64_t* B, int64_t* C) {
+    if (axis < 0) {
+        *A = 1;
+        *B = numel(s);
+        *C = 1;
+        return;
+    }
+    int64_t a = 1, c = 1;
+    for (int i = 0; i < axis; ++i) a *= s.dims[i];
+    for (int i = axis + 1; i < s.rank; ++i) c *= s.dims[i];
+    *A = a;
+    *B = s.dims[axis];
+    *C = c;
+}
+
+static int check_reduce_args(int op, const mh_shape& sx, int32_t axis) {
+    if (op != MH_SUM && op != MH_MEAN && op != MH_MAX) return fail(MH_ERR_OP, "op %d is not SUM/MEAN/MAX", op);
+    MH_TRY(check_shape(sx, "x"));
+    if (axis < -1 || axis >= sx.rank) return fail(MH_ERR_INVALID, "axis %d outside [-1, %d)", axis, sx.rank);
+    return MH_OK;
+}
+
+}  // namespace mh
+
+using namespace mh;
+
+extern "C" {
+
+int mh_reduce_fwd(int op, float* res, const float* x, mh_shape sx, int32_t axis) {
+    MH_TRY(check_reduce_args(op, sx, axis));
+    int64_t A, B, C;
+    abc_of(sx, axis, &A, &B, &C);
+    if (A * C == 0) return MH_OK;
+    if (!res || (!x && B > 0)) return fail(MH_ERR_NULL, "mh_reduce_fwd: null tensor");
+    MH_TRY(require_init());
+    const int epi = op == MH_MEAN ? EPI_MEAN : EPI_STORE;
+    const float div = op == MH_MEAN ? (float)B : 0.0f;  // tmean: / Scalar[f32](count)
+    const int rop = op == MH_MAX ? RED_MAX : RED_SUM;
+    float* tmp = nullptr;
+    const size_t t = reduce_abc_tmp_floats(rop, A, B, C);
+    if (t) MH_TRY(scratch(t * sizeof(float), reinterpret_cast<void**>(&tmp)));
+    MH_TRY(reduce_abc(rop, epi, x, A, B, C, res, nullptr, div, tmp));
+    return finish("mh_reduce_fwd");
+}
+
+int mh_reduce_bwd_accum(int op, float* grad, const float* x, mh_shape sx, const float* ug, int32_t axis) {
+    MH_TRY(check_reduce_args(op, sx, axis));
+    const int64_t n = numel(sx);
+    if (n == 0) return MH_OK;
+    if (!grad || !ug || (op == MH_MAX && !x)) return fail(MH_ERR_NULL, "mh_reduce_bwd_accum: null tensor");
+    MH_TRY(require_init());
+    const mh_shape sug = reduced_shape(sx, axis);
+    int64_t A, B, C;
+    abc_of(sx, axis, &A, &B, &C);
+    if (op == MH_SUM) {  // basics.mojo:416-425
+        MH_TRY(map_scale_bcast(grad, sx, ug, sug, 1.0f, shape_eq(sx, sug)));
+    } else if (op == MH_MEAN) {
+        if (axis < 0) {  // basics.mojo:470-487
+            MH_TRY(map_mean_all(grad, n, ug, (float)(1.0 / (double)n)));
+        } else {  // basics.mojo:489-506
+            MH_TRY(map_scale_bcast(grad, sx, ug, sug, (float)(1.0 / (double)B), shape_eq(sx, sug)));
+        }
+    } else {  // MAX, basics.mojo:536-615: line max and fl(1/count), then routing
+        const int64_t nl = A * C;
+        const size_t pad_nl = ((size_t)nl + 63) & ~(size_t)63;
+        const size_t t = reduce_abc_tmp_floats(RED_MAXCNT, A, B, C);
+        float* base = nullptr;
+        MH_TRY(scratch((2 * pad_nl + t + 64) * sizeof(float), reinterpret_cast<void**>(&base)));
+        float* m = base;
+        float* f = base + pad_nl;
+        MH_TRY(reduce_abc(RED_MAXCNT, EPI_STORE, x, A, B, C, m, f, 0.0f, base + 2 * pad_nl));
+        MH_TRY(map_max_route(grad, sx, x, sug, m, f, ug));
+    }
+    return finish("mh_reduce_bwd_accum");
+}
+
+}  // extern "C"

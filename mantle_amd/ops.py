@@ -1,0 +1,283 @@
+"""Mantle's op layer for the elementwise / broadcast / reduction path, on the HIP library.
+
+Mirrors the reference interface so that its callers read the same:
+  * ``OP`` ids and ``forward_op`` / ``backward_op`` (mantle/autograd/ops/ops.mojo:52-101,
+    243-311, 355-463);
+  * the op structs ``ADD SUB MUL DIV EXP LOG POW SUM MEAN MAX SIGMOID RELU TANH`` with
+    ``result_shape`` and ``forward`` (mantle/autograd/ops/basics.mojo, mlops.mojo);
+  * the tensorutils primitives ``fill``, ``elwise_transform``, ``elwise_pow``, ``elwise_op``,
+    ``broadcast_shapes``, ``get_reduce_shape``, ``accumulate_grad``, ``tsum``, ``tmean``,
+    ``tmax`` (mantle/core/tensorutils.mojo).
+
+Every call runs the gfx950 kernels of libmantle_hip.so on device-resident ``Tensor``s.
+Errors the reference only prints (non-broadcastable shapes, unknown ops) raise
+``MantleHipError`` here. Backward calls accumulate into ``grad`` as backward_op does.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+from . import _lib
+from .tensor import Tensor, TensorShape, as_shape
+
+
+class OP:
+    """Operator ids (ops.mojo:57-83); only the ids this layer implements."""
+    ADD, SUB, MUL, DIV, EXP, LOG, POW = 0, 1, 2, 3, 4, 5, 6
+    SUM, MEAN, MAX = 8, 9, 10
+    SIGMOID, RELU, TANH = 13, 14, 15
+
+    NAMES = {0: "ADD", 1: "SUB", 2: "MUL", 3: "DIV", 4: "EXP", 5: "LOG", 6: "POW", 8: "SUM",
+             9: "MEAN", 10: "MAX", 13: "SIGMOID", 14: "RELU", 15: "TANH"}
+
+
+BINARY = (OP.ADD, OP.SUB, OP.MUL, OP.DIV)
+UNARY = (OP.EXP, OP.LOG, OP.SIGMOID, OP.RELU, OP.TANH)
+REDUCE = (OP.SUM, OP.MEAN, OP.MAX)
+
+
+def _axis(attributes) -> int:
+    if attributes is None:
+        return -1
+    ax = attributes.get("axis") if isinstance(attributes, dict) else attributes
+    return -1 if ax is None else int(ax)
+
+
+# ---------------------------------------------------------------------------------------
+# tensorutils
+# ---------------------------------------------------------------------------------------
+def broadcast_shapes(s1, s2) -> TensorShape:
+    """broadcast_shapes, tensorutils.mojo:88-127 (raises on a mismatch)."""
+    a, b = as_shape(s1).dims, as_shape(s2).dims
+    big, small = (a, b) if len(a) > len(b) else (b, a)
+    diff = len(big) - len(small)
+    res = list(big)
+    for i in range(len(big) - 1, diff - 1, -1):
+        x, y = big[i], small[i - diff]
+        if x == y:
+            res[i] = x
+        elif x == 1 or y == 1:
+            res[i] = x * y
+        else:
+            raise _lib.MantleHipError(_lib.ERR_SHAPE, f"Shapes {a} and {b} cannot be broadcasted together.")
+    return TensorShape(res)
+
+
+def get_reduce_shape(t, axis: int) -> TensorShape:
+    """get_reduce_shape, tensorutils.mojo:601-619."""
+    d = list(as_shape(t).dims)
+    d[axis] = 1
+    return TensorShape(d)
+
+
+def fill(t: Tensor, val: float) -> None:
+    _lib.call("mh_fill", t.ptr, float(val), t.num_elements())
+
+
+def elwise_transform(op: int, res: Tensor, t: Tensor) -> None:
+    """elwise_transform, tensorutils.mojo:181-200, with op in EXP/LOG/SIGMOID/RELU/TANH."""
+    _lib.call("mh_unary_fwd", int(op), res.ptr, t.ptr, t.num_elements())
+
+
+def elwise_op(op: int, res: Tensor, t1: Tensor, t2: Tensor) -> None:
+    """elwise_op dispatcher, tensorutils.mojo:242-357."""
+    _lib.call("mh_binary_fwd", int(op), res.ptr, res.shape().c(), t1.ptr, t1.shape().c(), t2.ptr,
+              t2.shape().c())
+
+
+def accumulate_grad(grad: Tensor, res_grad: Tensor) -> None:
+    """accumulate_grad, tensorutils.mojo:442-487 (same shape, scalar or un-broadcast)."""
+    _lib.call("mh_accumulate_grad", grad.ptr, grad.shape().c(), res_grad.ptr, res_grad.shape().c())
+
+
+def _reduce(op: int, t: Tensor, axis: int, res: Optional[Tensor]) -> Tensor:
+    if res is None:
+        res = Tensor(TensorShape(1) if axis < 0 else get_reduce_shape(t.shape(), axis))
+    _lib.call("mh_reduce_fwd", int(op), res.ptr, t.ptr, t.shape().c(), int(axis))
+    return res
+
+
+def tsum(t: Tensor, axis: int = -1, res: Optional[Tensor] = None) -> Tensor:
+    return _reduce(OP.SUM, t, axis, res)
+
+
+def tmean(t: Tensor, axis: int = -1, res: Optional[Tensor] = None) -> Tensor:
+    return _reduce(OP.MEAN, t, axis, res)
+
+
+def tmax(t: Tensor, axis: int = -1, res: Optional[Tensor] = None) -> Tensor:
+    return _reduce(OP.MAX, t, axis, res)
+
+
+# ---------------------------------------------------------------------------------------
+# op structs (result_shape + forward); backward goes through backward_op
+# ---------------------------------------------------------------------------------------
+class _Binary:
+    op = -1
+
+    @staticmethod
+    def result_shape(t1_shape, t2_shape) -> TensorShape:
+        return broadcast_shapes(t1_shape, t2_shape)
+
+    @classmethod
+    def forward(cls, res: Tensor, t1: Tensor, t2: Tensor) -> None:
+        elwise_op(cls.op, res, t1, t2)
+
+
+class ADD(_Binary):
+    op = OP.ADD
+
+
+class SUB(_Binary):
+    op = OP.SUB
+
+
+class MUL(_Binary):
+    op = OP.MUL
+
+
+class DIV(_Binary):
+    op = OP.DIV
+
+
+class _Unary:
+    op = -1
+
+    @staticmethod
+    def result_shape(t1_shape) -> TensorShape:
+        return as_shape(t1_shape)
+
+    @classmethod
+    def forward(cls, res: Tensor, t1: Tensor) -> None:
+        elwise_transform(cls.op, res, t1)
+
+
+class EXP(_Unary):
+    op = OP.EXP
+
+
+class LOG(_Unary):
+    op = OP.LOG
+
+
+class SIGMOID(_Unary):
+    op = OP.SIGMOID
+
+
+class RELU(_Unary):
+    op = OP.RELU
+
+
+class TANH(_Unary):
+    op = OP.TANH
+
+
+class POW:
+    """POW with a shape-(1) graph-scalar exponent (basics.mojo:312-378)."""
+    op = OP.POW
+
+    @staticmethod
+    def result_shape(t1_shape, t2_shape) -> TensorShape:
+        return as_shape(t1_shape)
+
+    @staticmethod
+    def forward(res: Tensor, t1: Tensor, t2: Tensor) -> None:
+        _lib.call("mh_pow_fwd", res.ptr, t1.ptr, t1.num_elements(), t2.ptr)
+
+
+class _Reduce:
+    op = -1
+
+    @staticmethod
+    def result_shape(t_shape, attributes=None) -> TensorShape:
+        ax = _axis(attributes)
+        return TensorShape(1) if ax < 0 else get_reduce_shape(t_shape, ax)
+
+    @classmethod
+    def forward(cls, res: Tensor, t: Tensor, attributes=None) -> None:
+        _reduce(cls.op, t, _axis(attributes), res)
+
+
+class SUM(_Reduce):
+    op = OP.SUM
+
+
+class MEAN(_Reduce):
+    op = OP.MEAN
+
+
+class MAX(_Reduce):
+    op = OP.MAX
+
+
+STRUCTS = {OP.ADD: ADD, OP.SUB: SUB, OP.MUL: MUL, OP.DIV: DIV, OP.EXP: EXP, OP.LOG: LOG,
+           OP.POW: POW, OP.SUM: SUM, OP.MEAN: MEAN, OP.MAX: MAX, OP.SIGMOID: SIGMOID,
+           OP.RELU: RELU, OP.TANH: TANH}
+
+
+def static_result_shape(op: int, *shapes, attributes=None) -> TensorShape:
+    """static_result_shape, ops.mojo:104-218 (the subset of ops implemented here)."""
+    s = STRUCTS.get(op)
+    if s is None:
+        raise _lib.MantleHipError(_lib.ERR_OP, f"Operator {op} not found.")
+    if op in REDUCE:
+        return s.result_shape(shapes[0], attributes)
+    return s.result_shape(*shapes)
+
+
+# ---------------------------------------------------------------------------------------
+# dispatch
+# ---------------------------------------------------------------------------------------
+def forward_op(op: int, res: Tensor, t1: Tensor, t2: Optional[Tensor] = None, attributes=None) -> None:
+    """forward_op, ops.mojo:243-311: writes op(t1[, t2]) into the preallocated res."""
+    if op in BINARY or op == OP.POW:
+        if t2 is None:
+            raise _lib.MantleHipError(_lib.ERR_INVALID, f"{OP.NAMES[op]} needs two operands")
+        STRUCTS[op].forward(res, t1, t2)
+    elif op in UNARY:
+        STRUCTS[op].forward(res, t1)
+    elif op in REDUCE:
+        STRUCTS[op].forward(res, t1, attributes)
+    else:
+        raise _lib.MantleHipError(_lib.ERR_OP, f"Operator {op} not found.")
+
+
+def backward_op(tensor_id: int, op: int, ug: Tensor, t1: Tensor, t2: Optional[Tensor] = None,
+                grad: Optional[Tensor] = None, attributes=None) -> None:
+    """backward_op, ops.mojo:355-463: grad += the gradient of operand ``tensor_id``.
+
+    Signature order follows the reference's binary form (ug, t1, t2, grad); for unary and
+    reduce ops pass ``t2=None`` and ``grad`` by keyword or positionally."""
+    if grad is None:
+        raise _lib.MantleHipError(_lib.ERR_NULL, "backward_op needs the grad tensor")
+    if op in BINARY:
+        _lib.call("mh_binary_bwd_accum", int(op), int(tensor_id), grad.ptr, grad.shape().c(), ug.ptr,
+                  ug.shape().c(), t1.ptr, t1.shape().c(), t2.ptr, t2.shape().c())
+    elif op == OP.POW:
+        if t2.num_elements() != 1 or t2.shape() != TensorShape(1):
+            raise _lib.MantleHipError(_lib.ERR_SHAPE, "POW exponent must be a shape-(1) graph scalar")
+        _lib.call("mh_pow_bwd_accum", int(tensor_id), grad.ptr, t1.ptr, t2.ptr, ug.ptr, t1.num_elements())
+    elif op in UNARY:
+        if ug.shape() != t1.shape():
+            raise _lib.MantleHipError(_lib.ERR_SHAPE, "ug shape differs from the operand shape")
+        _lib.call("mh_unary_bwd_accum", int(op), grad.ptr, t1.ptr, ug.ptr, t1.num_elements())
+    elif op in REDUCE:
+        ax = _axis(attributes)
+        if ug.shape() != _Reduce.result_shape(t1.shape(), attributes):
+            raise _lib.MantleHipError(_lib.ERR_SHAPE, "ug shape is not the reduced shape")
+        _lib.call("mh_reduce_bwd_accum", int(op), grad.ptr, t1.ptr, t1.shape().c(), ug.ptr, ax)
+    else:
+        raise _lib.MantleHipError(_lib.ERR_OP, f"Operator {op} not found.")
+
+
+def backward_op_both(op: int, ug: Tensor, t1: Tensor, t2: Tensor, grad1: Optional[Tensor],
+                     grad2: Optional[Tensor]) -> None:
+    """Both backward_op calls of a same-shape binary op in one fused pass."""
+    if t1.shape() != t2.shape() or ug.shape() != t1.shape():
+        if grad1 is not None:
+            backward_op(0, op, ug, t1, t2, grad1)
+        if grad2 is not None:
+            backward_op(1, op, ug, t1, t2, grad2)
+        return
+    _lib.call("mh_binary_bwd_accum2", int(op), grad1.ptr if grad1 is not None else None,
+              grad2.ptr if grad2 is not None else None, ug.ptr, t1.ptr, t2.ptr, t1.shape().c())

@@ -1,0 +1,89 @@
+/*
+ * mantle_oracle.h -- CPU restatement of Mantle's elementwise / broadcast / reduction path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the parity checker for the HIP path in
+ * mantle_amd/: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load it, and only to check or to time the reference semantics. The product path never
+ * links, loads or calls it.
+ *
+ * Every function restates one piece of the reference (paths relative to the Mantle
+ * checkout): mantle/core/tensorutils.mojo, mantle/core/math_util.mojo,
+ * mantle/autograd/ops/{basics,mlops,ops}.mojo. The fp32 expression order of each op is
+ * kept exactly (built with -ffp-contract=off; fmaf only where the restated algorithm uses
+ * a fused multiply-add).
+ *
+ * Pinning status (what checks each function; see tests/test_oracle_*.py):
+ *   - closed-form single-IEEE-op functions (add/sub/mul/div, relu, max, broadcast index
+ *     math, accumulate, tie routing): reference fixtures from the tests/mojo test files plus
+ *     brute-force checks against numpy on small inputs;
+ *   - or_exp / or_log / or_powf: reference special points plus an fp64 bound (<= 2 ulp
+ *     over the config domains). Bit-level agreement with Mojo's stdlib exp/log/pow
+ *     (mojo 1.0.0b3.dev2026061606, not installable here) is PARITY UNPINNED.
+ *   - lane-ordered sums (or_reduce_*): exact-integer fixtures plus an fp64 bound; the
+ *     reduce_add lane-combine shape is PARITY UNPINNED at the bit level (rtol class).
+ */
+#ifndef MANTLE_ORACLE_H
+#define MANTLE_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OR_MAX_RANK 8 /* mantle/core/tensor.mojo:20 MAX_RANK */
+
+/* Same layout as mh_shape in include/mantle_hip.h: rank, then row-major dims. */
+typedef struct {
+    int32_t rank;
+    int64_t dims[OR_MAX_RANK];
+} or_shape;
+
+/* Mantle OP ids (mantle/autograd/ops/ops.mojo:57-83). */
+enum {
+    OR_ADD = 0, OR_SUB = 1, OR_MUL = 2, OR_DIV = 3, OR_EXP = 4, OR_LOG = 5, OR_POW = 6,
+    OR_SUM = 8, OR_MEAN = 9, OR_MAX = 10, OR_SIGMOID = 13, OR_RELU = 14, OR_TANH = 15
+};
+
+/* Return codes. */
+enum { OR_OK = 0, OR_ERR_SHAPE = -2, OR_ERR_RANK = -3, OR_ERR_OP = -4 };
+
+/* nelts = 2 * simd_width_of[f32]() (mantle/__init__.mojo:21): the lane count that fixes
+ * the CPU summation order. 32 on an AVX-512 host (the default here). */
+void or_set_nelts(int nelts);
+int or_get_nelts(void);
+
+/* ---- scalar math (mantle/core/math_util.mojo:149-196, mlops.mojo:27-235) ---- */
+float or_exp(float x);
+float or_log(float x);
+float or_powi(float x, int64_t n);
+float or_powf(float x, float y);
+float or_sigmoid(float x);
+float or_tanh(float x);
+float or_relu(float x);
+
+/* ---- tensorutils primitives ---- */
+void or_fill(float* t, int64_t n, float v);
+int or_broadcast_shapes(const or_shape* s1, const or_shape* s2, or_shape* out);
+void or_broadcast_calculate_strides(int size, const or_shape* shape, int64_t* strides);
+int64_t or_get_real_index(int size, const int64_t* strides, const or_shape* bshape, int64_t i);
+int or_elwise_transform(int op, float* res, const float* t, int64_t n);
+void or_elwise_pow(float* res, const float* t, int64_t n, int64_t x);
+int or_elwise_op(int op, float* res, const float* t1, const or_shape* s1,
+                 const float* t2, const or_shape* s2);
+int or_accumulate_grad(float* grad, const or_shape* sg, const float* rg, const or_shape* srg);
+float or_reduce_all(int op, const float* t, int64_t n);
+int or_reduce_axis(int op, float* res, const float* t, const or_shape* s, int axis);
+
+/* ---- op-level dispatch (mantle/autograd/ops/ops.mojo:243-311, 355-463) ----
+ * axis < 0 means "no axis attribute" (reduce over all elements). */
+int or_forward_op(int op, float* res, const float* t1, const or_shape* s1,
+                  const float* t2, const or_shape* s2, int axis);
+int or_backward_op(int tensor_id, int op, const float* ug, const or_shape* sug,
+                   const float* t1, const or_shape* s1, const float* t2, const or_shape* s2,
+                   int axis, float* grad);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,317 @@
+"""GPU parity: the HIP path (libmantle_hip.so through the C ABI) against the CPU oracle on the
+same seeded inputs, at sizes the oracle finishes in seconds, plus the reference fixtures.
+
+Bars (written per assertion): bit-exact for add/sub/mul/div, relu, max, broadcast gathers and
+every backward that is a single expression per element; <= 2 ulp for exp/log/sigmoid/tanh/pow
+(the kernels use the same algorithm as the oracle, so these are expected bit-exact too); the
+rtol 1e-5 class with the condition-aware comparator for sums whose order differs."""
+import numpy as np
+import pytest
+
+from mantle_amd import synth
+from util import (O, OPS, GpuEngine, Graph, OracleEngine, assert_bitexact, assert_sum_close, assert_ulp,
+                  check_fixture, load_fixtures)
+
+pytestmark = pytest.mark.gpu
+
+ORC = OracleEngine()
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    print("\n[gpu] init device 0", flush=True)
+    return GpuEngine()
+
+
+# ---------------------------------------------------------------------------------------
+# reference fixtures
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("case", [c for c in load_fixtures() if c["kind"] != "accumulate"], ids=lambda c: c["id"])
+def test_reference_fixture_on_gpu(gpu, case):
+    check_fixture(gpu, case)
+
+
+def test_accumulate_fixture_on_gpu(gpu):
+    m = gpu.m
+    g = m.Tensor(m.TensorShape(2, 1, 1))
+    rg = gpu.T(np.full((2, 3, 4), 3.0, np.float32))
+    m.accumulate_grad(g, rg)
+    np.testing.assert_array_equal(g.to_numpy(), np.full((2, 1, 1), 36.0, np.float32))
+    with pytest.raises(m.MantleHipError):
+        m.accumulate_grad(m.Tensor(m.TensorShape(2, 1)), rg)
+
+
+# ---------------------------------------------------------------------------------------
+# binary ops: forward bit-exact, backward per operand
+# ---------------------------------------------------------------------------------------
+BIN_SHAPES = [((37, 63, 107), (37, 63, 107)), ((37, 63, 107), (37, 63, 1)), ((37, 63, 1), (37, 63, 107)),
+              ((2, 3, 4), (5, 2, 1, 4)), ((1001,), (1,)), ((1,), (1001,)), ((32, 32), (1, 32)),
+              ((4, 32, 7, 7), (1, 32, 1, 1)), ((4099, 10), (4099, 1)), ((8, 1, 5), (1, 6, 1)),
+              ((3,), (3,)), ((1,), (1,)), ((7, 5), (5,)), ((2, 1, 3, 1, 5), (1, 4, 3, 6, 1))]
+
+
+def _binary_inputs(sa, sb, seed):
+    a = synth.uniform(sa, -1, 1, seed)
+    b = synth.uniform(sb, 0.5, 2, seed + 1)
+    return a, b
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3], ids=["ADD", "SUB", "MUL", "DIV"])
+@pytest.mark.parametrize("sa,sb", BIN_SHAPES, ids=[f"{a}x{b}" for a, b in BIN_SHAPES])
+def test_binary_fwd_bwd_parity(gpu, op, sa, sb):
+    a, b = _binary_inputs(sa, sb, 100 + op)
+    assert_bitexact(gpu.forward(op, a, b), ORC.forward(op, a, b), f"fwd op{op}")
+    out_shape = np.broadcast_shapes(sa, sb)
+    ug = synth.normal(out_shape, 0, 1, 200 + op)
+    for k, shape in ((0, sa), (1, sb)):
+        g0 = synth.normal(shape, 0, 1, 300 + k)  # accumulate into a non-zero grad
+        got = gpu.backward(k, op, ug, a, b, grad=g0)
+        ref = ORC.backward(k, op, ug, a, b, grad=g0)
+        if tuple(shape) == tuple(out_shape):
+            assert_bitexact(got, ref, f"bwd op{op} id{k}")
+        else:  # un-broadcast: a sum over the broadcast axes in a different order
+            A, B, U = (v.astype(np.float64) for v in (a, b, ug))
+            rg = {0: U, 1: (U if k == 0 else -U), 2: (U * B if k == 0 else U * A),
+                  3: (U / B if k == 0 else -A / (B * B) * U)}[op]
+            red = tuple(i for i in range(len(out_shape)) if i >= len(out_shape) - len(shape) and
+                        shape[i - (len(out_shape) - len(shape))] == 1 and out_shape[i] != 1) + \
+                tuple(range(len(out_shape) - len(shape)))
+            ex = (rg.sum(axis=red, keepdims=True).reshape(shape) + g0.astype(np.float64))
+            mag = np.abs(rg).sum(axis=red, keepdims=True).reshape(shape) + np.abs(g0)
+            assert_sum_close(got, ref, ex, f"bwd op{op} id{k}", terms_abs=mag)
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3], ids=["ADD", "SUB", "MUL", "DIV"])
+def test_binary_bwd_both_operands_fused(gpu, op):
+    m = gpu.m
+    n = (1 << 20) + 3
+    a, b = _binary_inputs((n,), (n,), 400 + op)
+    ug = synth.normal((n,), 0, 1, 401)
+    g1, g2 = synth.normal((n,), 0, 1, 402), synth.normal((n,), 0, 1, 403)
+    ta, tb, tu, tg1, tg2 = (gpu.T(v) for v in (a, b, ug, g1, g2))
+    m.backward_op_both(op, tu, ta, tb, tg1, tg2)
+    assert_bitexact(tg1.to_numpy(), ORC.backward(0, op, ug, a, b, grad=g1), "fused id0")
+    assert_bitexact(tg2.to_numpy(), ORC.backward(1, op, ug, a, b, grad=g2), "fused id1")
+
+
+# ---------------------------------------------------------------------------------------
+# unary ops and POW on the config-2 distributions
+# ---------------------------------------------------------------------------------------
+UNARY_DIST = {"EXP": ("u", -10, 10), "LOG": ("u", 1e-3, 10), "TANH": ("n", 0, 3), "SIGMOID": ("n", 0, 3),
+              "RELU": ("n", 0, 3)}
+
+
+def _dist(name, n, seed):
+    kind, p, q = UNARY_DIST[name]
+    return synth.uniform((n,), p, q, seed) if kind == "u" else synth.normal((n,), p, q, seed)
+
+
+@pytest.mark.parametrize("name", list(UNARY_DIST))
+def test_unary_fwd_bwd_parity(gpu, name):
+    op = OPS[name]
+    n = (1 << 20) + 5
+    x = _dist(name, n, 500 + op)
+    ug = synth.normal((n,), 0, 1, 501)
+    g0 = synth.normal((n,), 0, 1, 502)
+    fwd = gpu.forward(op, x)
+    ref = ORC.forward(op, x)
+    if name == "RELU":
+        assert_bitexact(fwd, ref, "relu fwd")
+        assert_bitexact(gpu.backward(0, op, ug, x, grad=g0), ORC.backward(0, op, ug, x, grad=g0), "relu bwd")
+        return
+    assert_ulp(fwd, ref, 2, f"{name} fwd")
+    exact = np.mean(fwd.view(np.uint32) == ref.view(np.uint32))
+    print(f"[gpu] {name} fwd bit-exact fraction {exact:.6f}", flush=True)
+    bwd = gpu.backward(0, op, ug, x, grad=g0)
+    assert_ulp(bwd, ORC.backward(0, op, ug, x, grad=g0), 2, f"{name} bwd")
+
+
+@pytest.mark.parametrize("e", [2.37, 0.61, 1.0, 2.0, -1.5, 3.9])
+def test_pow_parity(gpu, e):
+    n = (1 << 18) + 7
+    x = synth.uniform((n,), 0.1, 4, 600)
+    t2 = np.array([e], np.float32)
+    ug = synth.normal((n,), 0, 1, 601)
+    assert_bitexact(gpu.forward(OPS["POW"], x, t2), ORC.forward(OPS["POW"], x, t2), f"pow fwd {e}")
+    g0 = synth.normal((n,), 0, 1, 602)
+    assert_ulp(gpu.backward(0, OPS["POW"], ug, x, t2, grad=g0), ORC.backward(0, OPS["POW"], ug, x, t2, grad=g0), 2,
+               f"pow bwd x {e}")
+    got = gpu.backward(1, OPS["POW"], ug, x, t2)
+    ref = ORC.backward(1, OPS["POW"], ug, x, t2)
+    X, U = x.astype(np.float64), ug.astype(np.float64)
+    terms = X ** np.float64(t2[0]) * np.log(X) * U
+    assert_sum_close(got, ref, np.array([terms.sum()]), f"pow bwd exponent {e}", terms_abs=np.array([np.abs(terms).sum()]))
+
+
+# ---------------------------------------------------------------------------------------
+# reductions
+# ---------------------------------------------------------------------------------------
+RED_CASES = [((87, 73, 107), 0), ((87, 73, 107), 1), ((87, 73, 107), 2), ((87, 73, 107), None),
+             ((1024, 1024), 0), ((1024, 1024), 1), ((64, 512, 1024), 2), ((4099, 10), 1), ((3, 1, 5), 1),
+             ((1,), None), ((5,), 0), ((2, 70000), 1), ((70000, 3), 0), ((1 << 22,), None), ((6, 33, 2), 1)]
+
+
+@pytest.mark.parametrize("shape,axis", RED_CASES, ids=[f"{s}-ax{a}" for s, a in RED_CASES])
+def test_reduce_fwd_bwd_parity(gpu, shape, axis):
+    x = synth.normal(shape, 0, 1, 700)
+    if axis is not None and shape[axis] > 1:
+        synth.inject_ties(x, axis, 701)
+    elif x.size > 1:
+        x.reshape(-1)[x.size // 2] = x.max()
+    red_shape = (1,) if axis is None else tuple(1 if i == axis else d for i, d in enumerate(shape))
+    kd = dict(axis=axis, keepdims=True) if axis is not None else {}
+    ex = x.astype(np.float64).sum(**kd).reshape(red_shape)
+    mag = np.abs(x.astype(np.float64)).sum(**kd).reshape(red_shape)
+    d = x.size if axis is None else shape[axis]
+    s = gpu.forward(OPS["SUM"], x, axis=axis)
+    assert_sum_close(s, ORC.forward(OPS["SUM"], x, axis=axis), ex, "sum", terms_abs=mag)
+    mn = gpu.forward(OPS["MEAN"], x, axis=axis)
+    assert_sum_close(mn, ORC.forward(OPS["MEAN"], x, axis=axis), ex / d, "mean", terms_abs=mag / d)
+    assert_bitexact(gpu.forward(OPS["MAX"], x, axis=axis), ORC.forward(OPS["MAX"], x, axis=axis), "max")
+    ug = synth.normal(red_shape, 0, 1, 702)
+    g0 = synth.normal(shape, 0, 1, 703)
+    for name in ("SUM", "MEAN", "MAX"):
+        got = gpu.backward(0, OPS[name], ug, x, axis=axis, grad=g0)
+        assert_bitexact(got, ORC.backward(0, OPS[name], ug, x, axis=axis, grad=g0), f"{name} bwd")
+
+
+def test_reductions_are_deterministic(gpu):
+    m = gpu.m
+    x = gpu.T(synth.normal((4096, 4096), 0, 1, 710))
+    for ax in (0, 1, -1):
+        r1 = m.tsum(x, ax).to_numpy()
+        r2 = m.tsum(x, ax).to_numpy()
+        assert_bitexact(r1, r2, f"sum twice axis {ax}")
+
+
+# ---------------------------------------------------------------------------------------
+# ragged, tiny and unaligned inputs
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 63, 65, 1023, 4097])
+def test_ragged_sizes(gpu, n):
+    a, b = _binary_inputs((n,), (n,), 800)
+    for op in (0, 3):
+        assert_bitexact(gpu.forward(op, a, b), ORC.forward(op, a, b), f"op{op} n={n}")
+    x = _dist("EXP", n, 801)
+    assert_ulp(gpu.forward(OPS["EXP"], x), ORC.forward(OPS["EXP"], x), 2, f"exp n={n}")
+    assert_bitexact(gpu.forward(OPS["MAX"], x), ORC.forward(OPS["MAX"], x), f"max n={n}")
+
+
+def test_unaligned_device_pointers(gpu):
+    m = gpu.m
+    n = 10007
+    a, b = _binary_inputs((n,), (n,), 810)
+    base_a, base_b, base_r = gpu.T(np.concatenate([[0], a])), gpu.T(np.concatenate([[0], b])), m.Tensor(n + 1)
+    va = m.Tensor(m.TensorShape(n), _ptr=base_a.ptr + 4, _owner=base_a)
+    vb = m.Tensor(m.TensorShape(n), _ptr=base_b.ptr + 4, _owner=base_b)
+    vr = m.Tensor(m.TensorShape(n), _ptr=base_r.ptr + 4, _owner=base_r)
+    m.forward_op(m.OP.MUL, vr, va, vb)
+    assert_bitexact(vr.to_numpy(), a * b, "unaligned mul")
+    # broadcast path with an unaligned operand
+    x = synth.normal((101, 40), 0, 1, 811)
+    bias = synth.normal((1, 40), 0, 0.1, 812)
+    bx = gpu.T(np.concatenate([[0], x.reshape(-1)]))
+    vx = m.Tensor(m.TensorShape(101, 40), _ptr=bx.ptr + 4, _owner=bx)
+    r = m.Tensor(m.TensorShape(101, 40))
+    m.forward_op(m.OP.ADD, r, vx, gpu.T(bias))
+    assert_bitexact(r.to_numpy(), x + bias, "unaligned bcast add")
+
+
+def test_empty_tensors_are_noops(gpu):
+    m = gpu.m
+    lib = m.lib()
+    S = m._lib.make_shape
+    assert lib.mh_binary_fwd(0, None, S((0, 4)), None, S((0, 4)), None, S((1, 4))) == 0
+    assert lib.mh_reduce_fwd(8, None, None, S((0, 4)), 1) == 0
+
+
+# ---------------------------------------------------------------------------------------
+# graphs: config 1 (bias + RELU), config 3 (NCHW bias + RELU) and config 5 (classifier head)
+# ---------------------------------------------------------------------------------------
+def _graph_parity(gpu, nodes, inputs, trainable, seed=None, exact=()):
+    g = Graph(nodes, trainable)
+    vg = g.forward(gpu, inputs)
+    vo = g.forward(ORC, inputs)
+    gg = g.backward(gpu, vg, seed)
+    go = g.backward(ORC, vo, seed)
+    return vg, vo, gg, go
+
+
+def test_config1_mlp_bias_relu_chain(gpu):
+    x = synth.normal((32, 32), 0, 1, 1)
+    bias = synth.normal((1, 32), 0, 0.1, 2)
+    ug = synth.normal((32, 32), 0, 1, 3)
+    nodes = [(OPS["ADD"], ["x", "b"], None, "y"), (OPS["RELU"], ["y"], None, "r")]
+    vg, vo, gg, go = _graph_parity(gpu, nodes, {"x": x, "b": bias}, ["x", "b"], seed=ug)
+    assert_bitexact(vg["r"], vo["r"], "r")
+    assert_bitexact(gg["x"], go["x"], "grad x")
+    assert_bitexact(gg["y"], go["y"], "grad y")
+    ex = np.where(vo["y"] > 0, ug, 0).astype(np.float64).sum(axis=0, keepdims=True)
+    assert_sum_close(gg["b"], go["b"], ex, "grad bias", terms_abs=np.abs(ug).sum(axis=0, keepdims=True))
+
+
+def test_config3_nchw_bias_relu_small(gpu):
+    x = synth.normal((8, 32, 28, 28), 0, 1, 11)
+    bias = synth.normal((1, 32, 1, 1), 0, 0.1, 12)
+    ug = synth.normal((8, 32, 28, 28), 0, 1, 13)
+    nodes = [(OPS["ADD"], ["x", "b"], None, "y"), (OPS["RELU"], ["y"], None, "r")]
+    vg, vo, gg, go = _graph_parity(gpu, nodes, {"x": x, "b": bias}, ["x", "b"], seed=ug)
+    assert_bitexact(vg["r"], vo["r"], "r")
+    assert_bitexact(gg["x"], go["x"], "grad x")
+    gy = np.where(vo["y"] > 0, ug, 0).astype(np.float64)
+    assert_sum_close(gg["b"], go["b"], gy.sum(axis=(0, 2, 3), keepdims=True), "grad bias",
+                     terms_abs=np.abs(gy).sum(axis=(0, 2, 3), keepdims=True))
+
+
+def test_fused_bias_relu_matches_op_by_op(gpu):
+    m = gpu.m
+    x = synth.normal((8, 32, 28, 28), 0, 1, 21)
+    bias = synth.normal((1, 32, 1, 1), 0, 0.1, 22)
+    ug = synth.normal((8, 32, 28, 28), 0, 1, 23)
+    tx, tb, tu = gpu.T(x), gpu.T(bias), gpu.T(ug)
+    y, r = m.Tensor(tx.shape()), m.Tensor(tx.shape())
+    S = m._lib
+    S.call("mh_bias_relu_fwd", y.ptr, r.ptr, tx.ptr, tx.shape().c(), tb.ptr, tb.shape().c())
+    y_ref = ORC.forward(OPS["ADD"], x, bias)
+    assert_bitexact(y.to_numpy(), y_ref, "y")
+    assert_bitexact(r.to_numpy(), ORC.forward(OPS["RELU"], y_ref), "r")
+    gx, gb = m.Tensor(tx.shape()), m.Tensor(tb.shape())
+    S.call("mh_bias_relu_bwd_accum", None, gx.ptr, gb.ptr, y.ptr, tu.ptr, tx.shape().c(), tb.shape().c())
+    gy = ORC.backward(0, OPS["RELU"], ug, y_ref)
+    assert_bitexact(gx.to_numpy(), ORC.backward(0, OPS["ADD"], gy, x, bias), "fused grad x")
+    gyd = gy.astype(np.float64)
+    assert_sum_close(gb.to_numpy(), ORC.backward(1, OPS["ADD"], gy, x, bias), gyd.sum(axis=(0, 2, 3), keepdims=True),
+                     "fused grad bias", terms_abs=np.abs(gyd).sum(axis=(0, 2, 3), keepdims=True))
+
+
+def config5_nodes():
+    # MAX(ax1) -> SUB -> EXP -> SUM(ax1) -> DIV -> LOG -> MUL(onehot) -> MEAN
+    from util import softmax_nodes
+    return softmax_nodes("logits", 1) + [(OPS["LOG"], ["sm"], None, "lp"), (OPS["MUL"], ["lp", "onehot"], None, "t"),
+                                         (OPS["MEAN"], ["t"], None, "loss")]
+
+
+def config5_inputs(n, seed=0):
+    logits = synth.normal((n, 10), 0, 2, 31 + seed)
+    cls = synth.integers((n,), 0, 10, 32 + seed)
+    onehot = np.zeros((n, 10), np.float32)
+    onehot[np.arange(n), cls] = 1.0
+    return logits, onehot
+
+
+def test_config5_classifier_chain_small(gpu):
+    logits, onehot = config5_inputs(4099)
+    vg, vo, gg, go = _graph_parity(gpu, config5_nodes(), {"logits": logits, "onehot": onehot}, ["logits"])
+    assert_bitexact(vg["max"], vo["max"], "max")
+    assert_bitexact(vg["xm"], vo["xm"], "xm")
+    assert_ulp(vg["e"], vo["e"], 2, "exp")
+    # 10-term row sums run sequentially on both sides: same order, same bits
+    assert_bitexact(vg["s"], vo["s"], "row sums")
+    for k in ("sm", "lp", "t"):
+        assert_ulp(vg[k], vo[k], 2, k)
+    t64 = vo["t"].astype(np.float64)
+    assert_sum_close(vg["loss"], vo["loss"], np.array([t64.mean()]), "loss",
+                     terms_abs=np.array([np.abs(t64).mean()]))
+    # the loss grad is seeded with 1.0, so no backward value depends on the loss sum
+    for k in ("logits", "max", "xm", "e", "s", "sm", "lp", "t"):
+        assert_ulp(gg[k], go[k], 2, f"grad {k}")

@@ -1,0 +1,144 @@
+"""Host-side checks that need no GPU: the C-ABI library loads and exports every symbol the
+header declares, argument validation rejects bad calls before any device work, and the
+launch planning (dim collapsing, un-broadcast reduction chains) is right."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from util import ROOT
+
+import mantle_amd
+from mantle_amd import _lib
+
+HEADER = os.path.join(ROOT, "include", "mantle_hip.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(mh_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = header_functions()
+    assert len(names) >= 30
+    L = _lib.lib()
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    # the ctypes binding covers the whole header
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_status_strings():
+    L = _lib.lib()
+    for code in range(-9, 1):
+        assert L.mh_status_string(code)
+    assert L.mh_status_string(-2) == b"shape mismatch"
+
+
+S = _lib.make_shape
+
+
+def test_shape_errors_before_device_work():
+    L = _lib.lib()
+    # non-broadcastable (the reference only prints, tensorutils.mojo:116-122)
+    assert L.mh_binary_fwd(0, None, S((3,)), None, S((4,)), None, S((3,))) == _lib.ERR_SHAPE
+    assert b"broadcast" in L.mh_last_error()
+    # result shape must be broadcast(a, b)
+    assert L.mh_binary_fwd(0, None, S((2, 3)), None, S((3,)), None, S((3,))) == _lib.ERR_SHAPE
+    # rank outside 1..8 and negative dims
+    bad = _lib.mh_shape()
+    bad.rank = 0
+    assert L.mh_binary_fwd(0, None, bad, None, S((1,)), None, S((1,))) == _lib.ERR_RANK
+    bad.rank = 9
+    assert L.mh_binary_fwd(0, None, bad, None, S((1,)), None, S((1,))) == _lib.ERR_RANK
+    assert L.mh_binary_fwd(0, None, S((2, -1)), None, S((2, -1)), None, S((2, -1))) == _lib.ERR_RANK
+    # op ids outside the entry point
+    assert L.mh_binary_fwd(4, None, S((1,)), None, S((1,)), None, S((1,))) == _lib.ERR_OP
+    assert L.mh_unary_fwd(0, None, None, 4) == _lib.ERR_OP
+    assert L.mh_reduce_fwd(0, None, None, S((2, 3)), -1) == _lib.ERR_OP
+    # axis outside [-1, rank)
+    assert L.mh_reduce_fwd(8, None, None, S((2, 3)), 2) == _lib.ERR_INVALID
+    # tensor_id
+    assert L.mh_binary_bwd_accum(0, 2, None, S((1,)), None, S((1,)), None, S((1,)), None, S((1,))) == _lib.ERR_INVALID
+    # grad shape must be the operand's
+    assert L.mh_binary_bwd_accum(0, 0, None, S((3,)), None, S((2, 3)), None, S((2, 3)), None, S((3,))) == _lib.ERR_SHAPE
+    # the reference's non-numpy accumulate pair (test_tensorutils.mojo:409-414) is rejected
+    assert L.mh_accumulate_grad(None, S((2, 1)), None, S((2, 3, 4))) == _lib.ERR_SHAPE
+    # null tensors on non-empty work
+    assert L.mh_binary_fwd(0, None, S((3,)), None, S((3,)), None, S((3,))) == _lib.ERR_NULL
+    assert L.mh_unary_fwd(4, None, None, 5) == _lib.ERR_NULL
+    # empty work is a no-op
+    assert L.mh_binary_fwd(0, None, S((0, 3)), None, S((0, 3)), None, S((1,))) == _lib.OK
+    assert L.mh_unary_fwd(4, None, None, 0) == _lib.OK
+
+
+def test_requires_init_or_reports_no_device():
+    L = _lib.lib()
+    n = ctypes.c_int(-1)
+    assert L.mh_device_count(ctypes.byref(n)) == _lib.OK
+    if n.value == 0:
+        assert L.mh_init(0, 0) == _lib.ERR_NO_DEVICE
+        p = ctypes.c_void_p(16)
+        assert L.mh_unary_fwd(4, p, p, 4) == _lib.ERR_NOT_INIT
+        assert L.mh_malloc(ctypes.byref(ctypes.c_void_p()), 16) == _lib.ERR_NOT_INIT
+        with pytest.raises(mantle_amd.MantleHipError):
+            mantle_amd.init(0)
+
+
+def plan(sres, sa, sb):
+    info = _lib.mh_plan_info()
+    _lib.check(_lib.lib().mh_plan_binary(S(sres), S(sa), S(sb), ctypes.byref(info)))
+    r = info.rank
+    return info.kind, list(info.dims)[:r], list(info.stride_a)[:r], list(info.stride_b)[:r]
+
+
+def test_plan_binary_collapses_dims():
+    # config 1: Linear bias [32,32] + [1,32]
+    assert plan((32, 32), (32, 32), (1, 32)) == (3, [32, 32], [32, 1], [0, 1])
+    # config 3: NCHW bias: [256,32,28,28] + [1,32,1,1] -> [256, 32, 784]
+    assert plan((256, 32, 28, 28), (256, 32, 28, 28), (1, 32, 1, 1)) == \
+        (3, [256, 32, 784], [25088, 784, 1], [0, 1, 0])
+    # config 5: [N,10] - [N,1]
+    assert plan((1048576, 10), (1048576, 10), (1048576, 1)) == (3, [1048576, 10], [10, 1], [1, 0])
+    # same shape collapses to one dim; graph scalars on either side
+    assert plan((4, 5, 6), (4, 5, 6), (4, 5, 6)) == (0, [120], [1], [1])
+    assert plan((4, 5, 6), (4, 5, 6), (1,)) == (1, [120], [1], [0])
+    assert plan((4, 5, 6), (1,), (4, 5, 6)) == (2, [120], [0], [1])
+    # the reference's broadcast fixture [2,3,4] + [5,2,1,4] (test_tensorutils.mojo:161-181)
+    k, dims, sa, sb = plan((5, 2, 3, 4), (2, 3, 4), (5, 2, 1, 4))
+    assert k == 3 and dims == [5, 2, 3, 4] and sa == [0, 12, 4, 1] and sb == [8, 4, 0, 1]
+
+
+def unb(sg, srg):
+    info = _lib.mh_reduce_plan_info()
+    _lib.check(_lib.lib().mh_plan_unbroadcast(S(sg), S(srg), ctypes.byref(info)))
+    return [(info.a[i], info.b[i], info.c[i]) for i in range(info.nsteps)]
+
+
+def test_plan_unbroadcast_chains():
+    assert unb((1, 32), (32, 32)) == [(1, 32, 32)]                       # config 1 bias grad
+    assert unb((1, 32, 1, 1), (256, 32, 28, 28)) == [(8192, 784, 1), (1, 256, 32)]  # config 3
+    assert unb((1048576, 1), (1048576, 10)) == [(1048576, 10, 1)]        # config 5 row sums
+    assert unb((1,), (6, 7)) == [(1, 42, 1)]                              # everything
+    assert unb((32,), (1, 32)) == []                                      # only unit dims differ
+    assert unb((3, 1, 5, 1), (3, 4, 5, 6)) == [(60, 6, 1), (3, 4, 5)]     # K R K R
+    with pytest.raises(_lib.MantleHipError):
+        unb((2, 1), (2, 3, 4))
+
+
+def test_python_mirror_broadcast_and_result_shapes():
+    from mantle_amd.ops import broadcast_shapes, static_result_shape, OP
+    rng = np.random.default_rng(3)
+    for _ in range(300):
+        r = int(rng.integers(1, 5))
+        a = tuple(int(x) for x in rng.integers(1, 4, r))
+        b = tuple(d if rng.random() < 0.5 else 1 for d in a)[int(rng.integers(0, r)):] or (1,)
+        assert broadcast_shapes(a, b).dims == np.broadcast_shapes(a, b)
+    assert static_result_shape(OP.SUM, (4, 5, 6), attributes={"axis": 1}).dims == (4, 1, 6)
+    assert static_result_shape(OP.MAX, (4, 5, 6)).dims == (1,)
+    assert static_result_shape(OP.POW, (4, 5), (1,)).dims == (4, 5)
+    with pytest.raises(mantle_amd.MantleHipError):
+        broadcast_shapes((3,), (4,))

@@ -1,0 +1,331 @@
+"""Pins the CPU oracle (oracle/liboracle.so) before it is trusted as the parity checker:
+against the closed-form cases of Mantle's own tests, and against what the mathematics fixes
+(fp64 results, exact small-integer sums, brute force on tiny inputs, symmetries)."""
+import math
+
+import numpy as np
+import pytest
+
+from util import (O, OPS, OracleEngine, assert_bitexact, assert_sum_close, check_fixture,
+                  load_fixtures, spec_to_array, ulp_dist)
+
+FIXTURES = load_fixtures()
+ENG = OracleEngine()
+
+
+@pytest.fixture(autouse=True)
+def _nelts():
+    O.set_nelts(32)
+    yield
+    O.set_nelts(32)
+
+
+@pytest.mark.parametrize("case", [c for c in FIXTURES if c["kind"] != "accumulate"], ids=lambda c: c["id"])
+def test_reference_fixture(case):
+    check_fixture(ENG, case)
+
+
+def test_accumulate_fixtures():
+    ok = [c for c in FIXTURES if c["kind"] == "accumulate" and "reject" not in c]
+    for c in ok:
+        g = O.accumulate_grad(np.zeros(c["grad_shape"], np.float32), spec_to_array(c["rg"]))
+        np.testing.assert_array_equal(g, spec_to_array(c["expected"]))
+    # (2,1) <- (2,3,4) is accepted by the reference only by indexing out of bounds
+    bad = [c for c in FIXTURES if "reject" in c]
+    assert bad
+    for c in bad:
+        assert O.accumulate_grad_rc(tuple(c["grad_shape"]), spec_to_array(c["rg"])) == -2
+
+
+# ---------------------------------------------------------------------------------------
+# shapes and broadcasting (tests/python/test_broadcast_shapes.mojo checks numpy agreement)
+# ---------------------------------------------------------------------------------------
+def _rand_shapes(rng, n):
+    out = []
+    for _ in range(n):
+        r = int(rng.integers(1, 6))
+        base = [int(rng.integers(1, 5)) for _ in range(r)]
+        other = [d if rng.random() < 0.6 else (1 if rng.random() < 0.8 else int(rng.integers(1, 5))) for d in base]
+        cut = int(rng.integers(0, r))
+        out.append((tuple(base), tuple(other[cut:]) or (1,)))
+    return out
+
+
+def test_broadcast_shapes_vs_numpy():
+    rng = np.random.default_rng(1)
+    for a, b in _rand_shapes(rng, 400):
+        try:
+            ref = np.broadcast_shapes(a, b)
+        except ValueError:
+            ref = None
+        assert O.broadcast_shapes(a, b) == ref, (a, b)
+        assert O.broadcast_shapes(b, a) == ref, (b, a)
+
+
+def test_get_real_index_matches_numpy_broadcast_view():
+    # index of the compact operand element feeding each output element
+    for small, big in [((1, 32), (32, 32)), ((1, 32, 1, 1), (4, 32, 3, 3)), ((5, 2, 1, 4), (5, 2, 3, 4)),
+                       ((2, 3, 4), (5, 2, 3, 4)), ((7, 1), (7, 10)), ((1,), (3, 4))]:
+        ids = np.arange(int(np.prod(small)), dtype=np.int64).reshape(small)
+        expect = np.broadcast_to(ids, big).reshape(-1)
+        st = O.broadcast_calculate_strides(len(big), small)
+        got = [O.get_real_index(st, big, i) for i in range(int(np.prod(big)))]
+        np.testing.assert_array_equal(got, expect)
+
+
+# ---------------------------------------------------------------------------------------
+# elementwise forward: single IEEE ops, bit-exact against numpy's float32 arithmetic
+# ---------------------------------------------------------------------------------------
+BIN_NP = {0: np.add, 1: np.subtract, 2: np.multiply, 3: np.divide}
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3])
+@pytest.mark.parametrize("sa,sb", [((37, 63, 107), (37, 63, 107)), ((37, 63, 107), (37, 63, 1)),
+                                   ((37, 63, 1), (37, 63, 107)), ((2, 3, 4), (5, 2, 1, 4)),
+                                   ((33,), (1,)), ((1,), (33,)), ((8, 1, 5), (1, 6, 1))])
+def test_binary_forward_bitexact(op, sa, sb):
+    rng = np.random.default_rng(op)
+    a = rng.uniform(-1, 1, sa).astype(np.float32)
+    b = rng.uniform(0.5, 2, sb).astype(np.float32)
+    with np.errstate(all="ignore"):
+        ref = BIN_NP[op](a, b)
+    assert_bitexact(ENG.forward(op, a, b), ref, f"op {op} {sa} {sb}")
+
+
+def test_relu_signed_zero_and_nan():
+    x = np.array([-0.0, 0.0, -1.0, 2.0, np.nan, -np.inf, np.inf], np.float32)
+    r = O.elwise_transform(O.RELU, x)
+    np.testing.assert_array_equal(r.view(np.uint32), np.array([0, 0, 0, 2.0, 0, 0, np.inf], np.float32).view(np.uint32))
+    # backward into a zero grad: 0 * (negative ug) = -0.0, then 0 + -0.0 = +0.0 (ops.mojo:405)
+    g = O.backward_op(0, O.RELU, np.full(7, -3.0, np.float32), x)
+    assert not np.signbit(g[[0, 1, 2, 4, 5]]).any()
+
+
+# ---------------------------------------------------------------------------------------
+# transcendental functions: bounds against fp64
+# ---------------------------------------------------------------------------------------
+def _ulps_vs64(got32, ref64):
+    ref32 = ref64.astype(np.float32)
+    return np.abs(got32.astype(np.float64) - ref64) / np.spacing(np.abs(ref32)).astype(np.float64)
+
+
+def test_exp_within_2ulp_of_fp64_on_config_domains():
+    rng = np.random.default_rng(7)
+    for lo, hi, bound in [(-10, 10, 2.0), (-30, 30, 2.0), (-88, 88, 6.0)]:
+        x = rng.uniform(lo, hi, 200_000).astype(np.float32)
+        e = _ulps_vs64(O.elwise_transform(O.EXP, x), np.exp(x.astype(np.float64)))
+        assert e.max() <= bound, (lo, hi, e.max())
+    sp = O.elwise_transform(O.EXP, np.array([0.0, -0.0, np.nan], np.float32))
+    assert sp[0] == 1.0 and sp[1] == 1.0 and np.isnan(sp[2])
+
+
+def test_log_within_2ulp_of_fp64_and_special_values():
+    rng = np.random.default_rng(8)
+    x = np.concatenate([rng.uniform(1e-3, 10, 200_000), np.exp(rng.uniform(-87, 88, 100_000)),
+                        rng.uniform(1e-44, 1e-38, 1000)]).astype(np.float32)
+    x = x[x > 0]
+    e = _ulps_vs64(O.elwise_transform(O.LOG, x), np.log(x.astype(np.float64)))
+    assert e.max() <= 2.0, e.max()
+    sp = O.elwise_transform(O.LOG, np.array([1.0, 0.0, -1.0, np.inf, np.nan], np.float32))
+    assert sp[0] == 0.0 and sp[1] == -np.inf and np.isnan(sp[2]) and sp[3] == np.inf and np.isnan(sp[4])
+
+
+def test_sigmoid_bound_and_special_points():
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal(200_000) * 3).astype(np.float32)
+    ref = 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
+    assert _ulps_vs64(O.elwise_transform(O.SIGMOID, x), ref).max() <= 3.0
+    assert O.lib().or_sigmoid(0.0) == 0.5
+
+
+def test_tanh_formula_bound_and_symmetry():
+    # (e^x - e^-x)/(e^x + e^-x) cancels near 0: bounded in absolute terms, exactly odd
+    rng = np.random.default_rng(10)
+    x = (rng.standard_normal(200_000) * 3).astype(np.float32)
+    t = O.elwise_transform(O.TANH, x)
+    assert np.abs(t.astype(np.float64) - np.tanh(x.astype(np.float64))).max() <= 4e-7
+    assert_bitexact(O.elwise_transform(O.TANH, -x), -t, "tanh odd")
+    assert O.lib().or_tanh(0.0) == 0.0
+    # the sign is right and |t| <= 1
+    assert (np.sign(t) == np.sign(x)).all() and (np.abs(t) <= 1).all()
+
+
+def test_powi_is_square_and_multiply():
+    rng = np.random.default_rng(11)
+    x = rng.uniform(0.1, 4, 1000).astype(np.float32)
+    assert_bitexact(O.elwise_pow(x, 0), np.ones_like(x), "x^0")
+    assert_bitexact(O.elwise_pow(x, 1), x, "x^1")
+    assert_bitexact(O.elwise_pow(x, 2), x * x, "x^2")
+    assert_bitexact(O.elwise_pow(x, 3), x * (x * x), "x^3")
+    assert_bitexact(O.elwise_pow(x, 5), x * ((x * x) * (x * x)), "x^5")
+    assert_bitexact(O.elwise_pow(x, -2), np.float32(1) / (x * x), "x^-2")
+    # POW.forward truncates the float exponent toward zero (basics.mojo:327)
+    for e, n in [(2.9, 2), (0.7, 0), (-1.5, -1), (1.0, 1)]:
+        got = O.forward_op(O.POW, x, np.array([e], np.float32))
+        assert_bitexact(got, O.elwise_pow(x, n), f"trunc {e}")
+
+
+def test_powf_bound_and_rules():
+    rng = np.random.default_rng(12)
+    x = rng.uniform(0.1, 4, 20_000).astype(np.float32)
+    for y in (0.5, 1.37, 2.71, -0.5):
+        got = np.array([O.powf_scalar(v, y) for v in x], np.float32)
+        ref = x.astype(np.float64) ** np.float64(np.float32(y))
+        # exp(y*log x) carries |y log x| * 2^-24 relative error from the product rounding
+        assert _ulps_vs64(got, ref).max() <= 8.0, y
+    assert O.powf_scalar(0.0, 0.0) == 1.0  # integral exponent: _powi (0^0 = 1)
+    assert O.powf_scalar(3.0, 2.0) == 9.0
+    assert math.isnan(O.powf_scalar(-2.0, 0.5))
+    assert O.powf_scalar(-2.0, 3.0) == -8.0
+
+
+# ---------------------------------------------------------------------------------------
+# reductions
+# ---------------------------------------------------------------------------------------
+def test_reduce_all_nelts1_is_sequential():
+    rng = np.random.default_rng(13)
+    x = rng.standard_normal(1001).astype(np.float32)
+    O.set_nelts(1)
+    acc = np.float32(0)
+    for v in x:
+        acc = np.float32(acc + v)
+    assert O.reduce_all(O.SUM, x) == acc
+
+
+@pytest.mark.parametrize("nelts", [1, 8, 32])
+def test_small_integer_sums_are_exact_in_any_order(nelts):
+    O.set_nelts(nelts)
+    rng = np.random.default_rng(14)
+    x = rng.integers(-50, 50, (13, 37, 11)).astype(np.float32)
+    for ax in (None, 0, 1, 2):
+        got = ENG.forward(OPS["SUM"], x, axis=ax)
+        ref = x.sum(axis=ax, keepdims=True).astype(np.float32) if ax is not None else np.array([x.sum()], np.float32)
+        np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("shape,axis", [((87, 73, 107), 0), ((87, 73, 107), 1), ((87, 73, 107), 2),
+                                        ((87, 73, 107), None), ((4096, 3), 0)])
+def test_sum_mean_max_vs_fp64(shape, axis):
+    rng = np.random.default_rng(15)
+    x = rng.uniform(-1, 1, shape).astype(np.float32)
+    kd = dict(axis=axis, keepdims=True) if axis is not None else {}
+    ex = x.astype(np.float64).sum(**kd).reshape(-1)
+    s = ENG.forward(OPS["SUM"], x, axis=axis).reshape(-1)
+    assert_sum_close(s, ex.astype(np.float32), ex, "sum", terms_abs=np.abs(x.astype(np.float64)).sum(**kd).reshape(-1))
+    d = x.shape[axis] if axis is not None else x.size
+    m = ENG.forward(OPS["MEAN"], x, axis=axis).reshape(-1)
+    np.testing.assert_array_equal(m, (s / np.float32(d)).astype(np.float32))
+    mx = ENG.forward(OPS["MAX"], x, axis=axis).reshape(-1)
+    np.testing.assert_array_equal(mx, x.max(**kd).reshape(-1) if axis is not None else [x.max()])
+
+
+def test_max_of_all_neg_inf_is_min_finite():
+    x = np.full((3, 4), -np.inf, np.float32)
+    assert ENG.forward(OPS["MAX"], x)[0] == -np.finfo(np.float32).max
+
+
+# ---------------------------------------------------------------------------------------
+# backward
+# ---------------------------------------------------------------------------------------
+def test_binary_backward_matches_derivatives():
+    rng = np.random.default_rng(16)
+    a = rng.uniform(-1, 1, (5, 7, 9)).astype(np.float32)
+    b = rng.uniform(0.5, 2, (5, 7, 9)).astype(np.float32)
+    ug = rng.standard_normal((5, 7, 9)).astype(np.float32)
+    A, B, U = (v.astype(np.float64) for v in (a, b, ug))
+    d = {(0, 0): U, (0, 1): U, (1, 0): U, (1, 1): -U, (2, 0): U * B, (2, 1): U * A,
+         (3, 0): U / B, (3, 1): -A / (B * B) * U}
+    for (op, k), ref in d.items():
+        g = ENG.backward(k, op, ug, a, b)
+        assert ulp_dist(g, ref.astype(np.float32)).max() <= 3, (op, k)
+    # exact ones: pure copies and single products
+    assert_bitexact(ENG.backward(0, 0, ug, a, b), ug + np.float32(0), "add")
+    assert_bitexact(ENG.backward(1, 1, ug, a, b), np.float32(0) + ug * np.float32(-1), "sub id1")
+    assert_bitexact(ENG.backward(0, 2, ug, a, b), np.float32(0) + ug * b, "mul id0")
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3])
+def test_unbroadcast_backward_sums_over_broadcast_axes(op):
+    rng = np.random.default_rng(17 + op)
+    a = rng.uniform(-1, 1, (6, 5, 4)).astype(np.float32)
+    b = rng.uniform(0.5, 2, (1, 5, 1)).astype(np.float32)
+    ug = rng.standard_normal((6, 5, 4)).astype(np.float32)
+    A, B, U = (v.astype(np.float64) for v in (a, b, ug))
+    rg = {0: U, 1: -U, 2: U * A, 3: -A / (B * B) * U}[op]
+    ex = rg.sum(axis=(0, 2), keepdims=True)
+    g = ENG.backward(1, op, ug, a, b)
+    assert_sum_close(g.reshape(-1), ex.reshape(-1).astype(np.float32), ex.reshape(-1), f"op {op}",
+                     terms_abs=np.abs(rg).sum(axis=(0, 2)).reshape(-1))
+
+
+def test_div_backward_scalar_rule():
+    # t2 of shape (1): factor = -1 / (s*s), rg = (factor * t1) * ug (basics.mojo:168-180)
+    rng = np.random.default_rng(18)
+    a = rng.uniform(-1, 1, 64).astype(np.float32)
+    s = np.array([1.7], np.float32)
+    ug = rng.standard_normal(64).astype(np.float32)
+    g = ENG.backward(1, 3, ug, a, s)
+    ref = (-a.astype(np.float64) / (1.7 ** 2) * ug).sum()
+    assert abs(g[0] - ref) <= 1e-5 * np.abs(a.astype(np.float64) / 1.7 ** 2 * ug).sum()
+    g0 = ENG.backward(0, 3, ug, a, s)
+    assert_bitexact(g0, np.float32(0) + ug / s[0], "div id0 scalar")
+
+
+def test_unary_backward_matches_derivatives():
+    rng = np.random.default_rng(19)
+    x = rng.uniform(0.2, 3, 5000).astype(np.float32)
+    ug = rng.standard_normal(5000).astype(np.float32)
+    X, U = x.astype(np.float64), ug.astype(np.float64)
+    sig = 1 / (1 + np.exp(-X))
+    refs = {OPS["EXP"]: np.exp(X) * U, OPS["LOG"]: U / X, OPS["SIGMOID"]: sig * (1 - sig) * U,
+            OPS["TANH"]: (1 - np.tanh(X) ** 2) * U, OPS["RELU"]: U}
+    for op, ref in refs.items():
+        g = ENG.backward(0, op, ug, x)
+        # 1 - t*t cancels as t -> 1: TANH is bounded in absolute terms (ulp(1) * |ug| scale)
+        slack = 4e-7 * np.abs(U) if op == OPS["TANH"] else 0.0
+        assert (np.abs(g - ref) <= 1e-5 * np.abs(ref) + slack + 1e-30).all(), op
+
+
+def test_pow_backward_derivatives():
+    rng = np.random.default_rng(20)
+    x = rng.uniform(0.1, 4, 3000).astype(np.float32)
+    ug = rng.standard_normal(3000).astype(np.float32)
+    a = np.array([1.7], np.float32)
+    X, U, Af = x.astype(np.float64), ug.astype(np.float64), np.float64(a[0])
+    g0 = ENG.backward(0, O.POW, ug, x, a)
+    ref0 = Af * X ** (Af - 1) * U
+    assert (np.abs(g0 - ref0) <= 1e-5 * np.abs(ref0) + 1e-30).all()
+    g1 = ENG.backward(1, O.POW, ug, x, a)
+    terms = X ** Af * np.log(X) * U
+    assert abs(g1[0] - terms.sum()) <= 1e-5 * np.abs(terms).sum()
+
+
+def test_max_backward_tie_rule_bruteforce():
+    rng = np.random.default_rng(21)
+    x = rng.integers(0, 4, (6, 5, 7)).astype(np.float32)  # many exact ties
+    for ax in (0, 1, 2, None):
+        ug_shape = (1,) if ax is None else tuple(1 if i == ax else d for i, d in enumerate(x.shape))
+        ug = rng.standard_normal(ug_shape).astype(np.float32)
+        g = ENG.backward(0, O.MAX, ug, x, axis=ax)
+        m = x.max() if ax is None else x.max(axis=ax, keepdims=True)
+        eq = x == m
+        cnt = eq.sum() if ax is None else eq.sum(axis=ax, keepdims=True)
+        f = (np.float32(1) / cnt.astype(np.float32)).astype(np.float32)
+        ref = np.where(eq, (f * (ug[0] if ax is None else ug)).astype(np.float32), np.float32(0))
+        assert_bitexact(g, np.float32(0) + ref, f"max axis {ax}")
+
+
+def test_sum_backward_size1_axis_applies_mul_twice():
+    # accumulate_op with res_shape == t1_shape applies func twice (tensorutils.mojo:380-393)
+    x = np.ones((4, 1, 3), np.float32)
+    ug = np.arange(12, dtype=np.float32).reshape(4, 1, 3) - 5
+    assert_bitexact(ENG.backward(0, O.SUM, ug, x, axis=1), np.float32(0) + ug * ug, "sum size-1 axis")
+    c = np.float32(1.0 / 1.0)
+    assert_bitexact(ENG.backward(0, O.MEAN, ug, x, axis=1), np.float32(0) + (c * ug) * ug, "mean size-1 axis")
+
+
+def test_mean_backward_all_uses_f32_of_f64_reciprocal():
+    x = np.ones((3, 7), np.float32)
+    ug = np.array([2.5], np.float32)
+    g = ENG.backward(0, O.MEAN, ug, x)
+    assert_bitexact(g, np.full((3, 7), np.float32(1.0 / 21.0) * np.float32(2.5), np.float32), "mean all")

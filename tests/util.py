@@ -1,0 +1,268 @@
+"""Shared test helpers: fixture specs, comparators, the two engines (CPU oracle and the HIP
+library) behind one interface, and a small graph executor that drives forward_op /
+backward_op in the node order and trainable gating of Mantle's Model
+(mantle/nn/model.mojo:113-330)."""
+from __future__ import annotations
+
+import json
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+from oracle import oracle as O  # noqa: E402  (test infrastructure: the checker)
+
+OPS = {"ADD": 0, "SUB": 1, "MUL": 2, "DIV": 3, "EXP": 4, "LOG": 5, "POW": 6, "SUM": 8, "MEAN": 9,
+       "MAX": 10, "SIGMOID": 13, "RELU": 14, "TANH": 15}
+BINARY = (0, 1, 2, 3)
+UNARY = (4, 5, 13, 14, 15)
+REDUCE = (8, 9, 10)
+
+
+# ---------------------------------------------------------------------------------------
+# fixtures
+# ---------------------------------------------------------------------------------------
+def load_fixtures():
+    with open(os.path.join(ROOT, "tests", "golden", "reference_fixtures.json")) as f:
+        return json.load(f)["cases"]
+
+
+def spec_to_array(spec):
+    if spec is None:
+        return None
+    shape = tuple(spec["shape"])
+    n = int(np.prod(shape))
+    if "fill" in spec:
+        a = np.full(n, spec["fill"], dtype=np.float32)
+    elif spec.get("arange1"):
+        a = np.arange(1, n + 1, dtype=np.float32)
+    else:
+        a = np.asarray(spec["data"], dtype=np.float32).reshape(-1)
+    for k, v in spec.get("set", {}).items():
+        a[int(k)] = v
+    return a.reshape(shape)
+
+
+# ---------------------------------------------------------------------------------------
+# comparators
+# ---------------------------------------------------------------------------------------
+def ordered(a: np.ndarray) -> np.ndarray:
+    """float32 -> int64 with the same order (for ulp distances)."""
+    i = np.asarray(a, dtype=np.float32).view(np.int32).astype(np.int64)
+    return np.where(i < 0, -(i & 0x7FFFFFFF), i)
+
+
+def ulp_dist(a, b) -> np.ndarray:
+    return np.abs(ordered(a) - ordered(b))
+
+
+def assert_bitexact(got, ref, what=""):
+    got = np.asarray(got, dtype=np.float32)
+    ref = np.asarray(ref, dtype=np.float32)
+    assert got.shape == ref.shape, f"{what}: shape {got.shape} vs {ref.shape}"
+    same = (got.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(got) & np.isnan(ref))
+    if not same.all():
+        bad = np.flatnonzero(~same.reshape(-1))
+        i = bad[0]
+        raise AssertionError(f"{what}: {bad.size} of {got.size} differ; first at {i}: "
+                             f"{got.reshape(-1)[i]!r} vs {ref.reshape(-1)[i]!r}")
+
+
+def assert_ulp(got, ref, max_ulp, what=""):
+    got = np.asarray(got, dtype=np.float32)
+    ref = np.asarray(ref, dtype=np.float32)
+    assert got.shape == ref.shape, f"{what}: shape {got.shape} vs {ref.shape}"
+    both_nan = np.isnan(got) & np.isnan(ref)
+    d = np.where(both_nan, 0, ulp_dist(got, ref))
+    if d.max(initial=0) > max_ulp:
+        i = int(np.argmax(d.reshape(-1)))
+        raise AssertionError(f"{what}: max {d.max()} ulp > {max_ulp} at {i}: "
+                             f"{got.reshape(-1)[i]!r} vs {ref.reshape(-1)[i]!r}")
+
+
+def assert_sum_close(got, ref, exact64, what="", rtol=1e-5, terms_abs=None):
+    """The rtol-1e-5 class for sums whose order differs: pass where |got - ref| <= rtol*|ref|,
+    or where got is no farther from the fp64 sum than the reference is, or (if given) where
+    |got - exact| <= rtol * sum|terms| (the conditioning bound for cancelling sums)."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    ex = np.asarray(exact64, dtype=np.float64)
+    ok = np.abs(got - ref) <= rtol * np.abs(ref)
+    ok |= np.abs(got - ex) <= np.abs(ref - ex)
+    if terms_abs is not None:
+        ok |= np.abs(got - ex) <= rtol * np.asarray(terms_abs, dtype=np.float64)
+    ok |= (got == ref)
+    if not ok.all():
+        i = int(np.flatnonzero(~ok.reshape(-1))[0])
+        raise AssertionError(f"{what}: {int((~ok).sum())} sums out of tolerance; first at {i}: "
+                             f"got {got.reshape(-1)[i]!r} ref {ref.reshape(-1)[i]!r} "
+                             f"fp64 {ex.reshape(-1)[i]!r}")
+
+
+def assert_almost(got, ref, what="", rtol=1e-5, atol=1e-5):
+    """testing_utils.mojo:16-27 'almost': rtol = atol = 1e-5 per element."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert got.shape == ref.shape, f"{what}: shape {got.shape} vs {ref.shape}"
+    ok = np.abs(got - ref) <= atol + rtol * np.abs(ref)
+    if not ok.all():
+        i = int(np.flatnonzero(~ok.reshape(-1))[0])
+        raise AssertionError(f"{what}: {got.reshape(-1)[i]!r} vs {ref.reshape(-1)[i]!r} at {i}")
+
+
+# ---------------------------------------------------------------------------------------
+# engines
+# ---------------------------------------------------------------------------------------
+class OracleEngine:
+    name = "oracle"
+
+    def forward(self, op, t1, t2=None, axis=None):
+        return O.forward_op(op, t1, t2, axis)
+
+    def backward(self, tensor_id, op, ug, t1, t2=None, axis=None, grad=None):
+        return O.backward_op(tensor_id, op, ug, t1, t2, grad=grad, axis=axis)
+
+
+class GpuEngine:
+    """Runs each op through mantle_amd (libmantle_hip.so) with host round trips (tests only)."""
+    name = "gpu"
+
+    def __init__(self):
+        import mantle_amd
+        self.m = mantle_amd
+        mantle_amd.init(0)
+
+    def T(self, a):
+        return self.m.Tensor.from_numpy(np.asarray(a, dtype=np.float32))
+
+    def forward(self, op, t1, t2=None, axis=None):
+        m = self.m
+        a = self.T(t1)
+        b = self.T(t2) if t2 is not None else None
+        shapes = [a.shape()] + ([b.shape()] if b is not None else [])
+        attrs = None if axis is None else {"axis": axis}
+        res = m.Tensor(m.static_result_shape(op, *shapes, attributes=attrs))
+        m.forward_op(op, res, a, b, attributes=attrs)
+        return res.to_numpy()
+
+    def backward(self, tensor_id, op, ug, t1, t2=None, axis=None, grad=None):
+        m = self.m
+        a = self.T(t1)
+        b = self.T(t2) if t2 is not None else None
+        u = self.T(ug)
+        gshape = np.asarray(t1 if tensor_id == 0 or t2 is None else t2).shape or (1,)
+        g = self.T(np.zeros(gshape, np.float32) if grad is None else grad)
+        attrs = None if axis is None else {"axis": axis}
+        m.backward_op(tensor_id, op, u, a, b, g, attributes=attrs)
+        return g.to_numpy()
+
+
+# ---------------------------------------------------------------------------------------
+# graph executor (Model semantics on numpy arrays, one engine call per node)
+# ---------------------------------------------------------------------------------------
+class Graph:
+    """nodes: (op, [input names], axis, output name). Symbols not produced by a node are
+    inputs; `trainable` names those with a grad. Node outputs are trainable when any operand
+    is (graph.mojo:212-217)."""
+
+    def __init__(self, nodes, trainable=()):
+        self.nodes = nodes
+        self.trainable = set(trainable)
+        for op, ins, ax, out in nodes:
+            if any(i in self.trainable for i in ins):
+                self.trainable.add(out)
+
+    def forward(self, eng, values):
+        vals = dict(values)
+        for op, ins, ax, out in self.nodes:
+            t1 = vals[ins[0]]
+            t2 = vals[ins[1]] if len(ins) > 1 else None
+            vals[out] = eng.forward(op, t1, t2, ax)
+        return vals
+
+    def backward(self, eng, vals, seed=None):
+        """Model.backward (model.mojo:173-330): seed the last node's grad (1.0 for a loss, else
+        `seed`), then reverse node order, operands gated on trainable."""
+        grads = {k: np.zeros(np.asarray(v).shape, np.float32) for k, v in vals.items() if k in self.trainable}
+        last = self.nodes[-1][3]
+        grads[last] = np.ones(np.asarray(vals[last]).shape, np.float32) if seed is None else \
+            np.asarray(seed, np.float32).copy()
+        for op, ins, ax, out in reversed(self.nodes):
+            t1 = vals[ins[0]]
+            t2 = vals[ins[1]] if len(ins) > 1 else None
+            for k, name in enumerate(ins):
+                if name in self.trainable:
+                    grads[name] = eng.backward(k, op, grads[out], t1, t2, ax, grad=grads[name])
+        return grads
+
+
+def softmax_nodes(x, axis, prefix=""):
+    """Softmax graph, mantle/nn/activations.mojo:74-87."""
+    p = prefix
+    return [(OPS["MAX"], [x], axis, p + "max"), (OPS["SUB"], [x, p + "max"], None, p + "xm"),
+            (OPS["EXP"], [p + "xm"], None, p + "e"), (OPS["SUM"], [p + "e"], axis, p + "s"),
+            (OPS["DIV"], [p + "e", p + "s"], None, p + "sm")]
+
+
+def logsoftmax_nodes(x, axis, prefix=""):
+    """LogSoftmax graph, mantle/nn/activations.mojo:94-108."""
+    p = prefix
+    return [(OPS["MAX"], [x], axis, p + "max"), (OPS["SUB"], [x, p + "max"], None, p + "xm"),
+            (OPS["EXP"], [p + "xm"], None, p + "e"), (OPS["SUM"], [p + "e"], axis, p + "s"),
+            (OPS["LOG"], [p + "s"], None, p + "ls"), (OPS["SUB"], [p + "xm", p + "ls"], None, p + "lsm")]
+
+
+def run_fixture_graph(eng, case):
+    kind = case["graph"]
+    t1 = spec_to_array(case["t1"])
+    if kind in ("softmax", "logsoftmax"):
+        nodes = (softmax_nodes if kind == "softmax" else logsoftmax_nodes)("x", case["axis"])
+        vals = Graph(nodes).forward(eng, {"x": t1})
+        return vals[nodes[-1][3]]
+    t2 = spec_to_array(case["t2"])
+    if kind == "mse":  # mantle/nn/loss.mojo:25-38: SUB(y_true, y_pred) -> POW 2 -> MEAN
+        two = np.array([2.0], np.float32)
+        nodes = [(OPS["SUB"], ["yt", "yp"], None, "d"), (OPS["POW"], ["d", "two"], None, "p"),
+                 (OPS["MEAN"], ["p"], None, "loss")]
+        return Graph(nodes).forward(eng, {"yp": t1, "yt": t2, "two": two})["loss"]
+    # crossentropy, mantle/nn/loss.mojo:45-61: -1/N * SUM(y_true * logsoftmax(y_pred, 1))
+    negn = np.array([np.float32(-1.0 / float(t1.shape[0]))], np.float32)
+    nodes = logsoftmax_nodes("yp", 1) + [(OPS["MUL"], ["yt", "lsm"], None, "tl"),
+                                         (OPS["SUM"], ["tl"], None, "s2"),
+                                         (OPS["MUL"], ["s2", "negn"], None, "loss")]
+    return Graph(nodes).forward(eng, {"yp": t1, "yt": t2, "negn": negn})["loss"]
+
+
+def check_fixture(eng, case):
+    """Runs one reference fixture on `eng` and checks it against its expected values."""
+    tol = case["tol"]
+
+    def cmp(got, exp, what):
+        if tol == "exact":
+            np.testing.assert_array_equal(np.asarray(got, np.float32), exp, err_msg=what)
+        elif tol == "almost6":
+            assert_almost(got, exp, what, rtol=1e-5, atol=1e-8)
+        else:
+            assert_almost(got, exp, what)
+
+    kind = case["kind"]
+    if kind == "forward":
+        op = OPS[case["op"]]
+        got = eng.forward(op, spec_to_array(case["t1"]), spec_to_array(case["t2"]), case["axis"])
+        cmp(got, spec_to_array(case["expected"]), case["id"])
+    elif kind == "backward":
+        op = OPS[case["op"]]
+        t1, t2, ug = spec_to_array(case["t1"]), spec_to_array(case["t2"]), spec_to_array(case["ug"])
+        g1 = eng.backward(0, op, ug, t1, t2, case["axis"])
+        cmp(g1, spec_to_array(case["grad1"]), case["id"] + " grad1")
+        if case.get("grad2") is not None:
+            g2 = eng.backward(1, op, ug, t1, t2, case["axis"])
+            cmp(g2, spec_to_array(case["grad2"]), case["id"] + " grad2")
+    elif kind == "graph":
+        cmp(run_fixture_graph(eng, case), spec_to_array(case["expected"]), case["id"])
+    else:
+        raise AssertionError(f"unknown fixture kind {kind}")
