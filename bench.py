@@ -1,22 +1,38 @@
-"""Benchmark: Mantle's elementwise op layer on one MI355X.
+"""Benchmark: Mantle's elementwise / broadcast / reduction op layer on one MI355X.
 
-A step is one forward + backward pass of every config-2 op over 2^28-element fp32 tensors
-already resident in HBM:
+The headline line is config 2 of BASELINE.json. A step is one forward + backward pass of
+every config-2 op over 2^28-element fp32 tensors already resident in HBM:
   ADD/SUB/MUL/DIV   fwd (a ~ U(-1,1), b ~ U(0.5,2)) and the backward of both operands,
   EXP (x ~ U(-10,10)), LOG (x ~ U(1e-3,10)), TANH/SIGMOID/RELU (x ~ N(0,3))  fwd and bwd,
   POW (base ~ U(0.1,4), one seeded scalar exponent ~ U(0.5,3))  fwd, bwd of x, bwd of the exponent.
-Throughput is algorithmic bytes per step / step time (inputs read once, outputs written once,
-accumulated gradients read and written). Per-op times come from HIP events recorded on the
-library's stream between the ops of each timed step.
+Throughput is algorithmic bytes per step / step time (each input read once, each output
+written once, each accumulated gradient read and written). Per-op times come from HIP events
+recorded on the library's stream around each call.
+
+The other configs are measured after the headline step and reported under "workloads"
+(per op: ms, GB/s of algorithmic bytes, fraction of 8 TB/s):
+  c3  NCHW bias + RELU, [256,32,28,28] + [1,32,1,1]: fused and op-by-op, fwd and bwd;
+  c4  SUM/MEAN/MAX over axis 0, axis 1 and all of [8192,8192] (ties injected in half the
+      lines) and over the last axis of [64,512,1024], fwd and bwd;
+  c5  classifier head on logits [1048576,10]: MAX -> SUB -> EXP -> SUM -> DIV -> LOG ->
+      MUL(onehot) -> MEAN, forward and backward op by op (the drop-in path);
+  copy  a plain 1 GiB device copy (the library's copy kernel): the practical streaming rate.
+Tensors smaller than the 256 MB Infinity Cache are timed with the cache flushed before each
+op (a 1 GiB read sweep between ops, outside the timed events).
+
+`roofline.traffic` is filled from profiles/traffic.json when that summary of the rocprofv3
+FETCH_SIZE / WRITE_SIZE runs is present (see `--pmc-summary`), else null.
 
 Prints one JSON line. `--gpus N` with N > 1 exits: this build runs on one GPU.
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import ctypes
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -28,17 +44,17 @@ sys.path.insert(0, ROOT)
 METRIC = "elementwise/broadcast/reduce fwd+bwd: achieved HBM GB/s and % of MI355X peak"
 PEAK_GBS = 8000.0
 SEED = 42
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")
 
-# (name, algorithmic bytes per element)
 BINARY = ["ADD", "SUB", "MUL", "DIV"]
 UNARY = ["EXP", "LOG", "TANH", "SIGMOID", "RELU"]
-OP_ID = {"ADD": 0, "SUB": 1, "MUL": 2, "DIV": 3, "EXP": 4, "LOG": 5, "POW": 6, "SIGMOID": 13,
-         "RELU": 14, "TANH": 15}
+OP_ID = {"ADD": 0, "SUB": 1, "MUL": 2, "DIV": 3, "EXP": 4, "LOG": 5, "POW": 6, "SUM": 8, "MEAN": 9, "MAX": 10,
+         "SIGMOID": 13, "RELU": 14, "TANH": 15}
 BWD2_BYTES = {"ADD": 20, "SUB": 20, "MUL": 28, "DIV": 28}  # ug (+a, b), both grads read+written
 
 
 def step_plan():
-    """[(label, bytes per element)] in execution order."""
+    """Config 2: [(label, algorithmic bytes per element)] in execution order."""
     plan = []
     for op in BINARY:
         plan += [(f"{op}.fwd", 12), (f"{op}.bwd", BWD2_BYTES[op])]
@@ -48,55 +64,128 @@ def step_plan():
     return plan
 
 
-class Dev:
-    """Owns the device tensors of the workload (raw mh_malloc pointers)."""
-
-    def __init__(self, L, n):
-        self.L, self.n, self.ptrs = L, n, {}
-
-    def alloc(self, name, n=None):
-        p = ctypes.c_void_p()
-        n = self.n if n is None else n
-        rc = self.L.mh_malloc(ctypes.byref(p), n * 4)
-        if rc:
-            raise RuntimeError(f"mh_malloc({name}): {self.L.mh_last_error().decode()}")
-        self.ptrs[name] = p.value
-        return p.value
-
-    def free(self):
-        for p in self.ptrs.values():
-            self.L.mh_free(p)
-
-
 def chk(L, rc, what):
     if rc != 0:
         raise RuntimeError(f"{what}: [{rc}] {L.mh_last_error().decode()}")
 
 
-def setup_gpu(L, n):
-    d = Dev(L, n)
-    P = d.alloc
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Dev:
+    """Device buffers (raw mh_malloc pointers), events and the cache flush of one run."""
+
+    def __init__(self, L):
+        self.L, self.ptrs, self.evs = L, {}, []
+        self._flush = None
+
+    def alloc(self, name, n):
+        p = ctypes.c_void_p()
+        chk(self.L, self.L.mh_malloc(ctypes.byref(p), max(int(n), 1) * 4), f"mh_malloc({name})")
+        self.ptrs[name] = p.value
+        return p.value
+
+    def upload(self, name, arr):
+        arr = np.ascontiguousarray(arr, np.float32)
+        p = self.alloc(name, arr.size)
+        chk(self.L, self.L.mh_memcpy_h2d(p, arr.ctypes.data, arr.size * 4), f"h2d {name}")
+        return p
+
+    def zeros(self, name, n):
+        p = self.alloc(name, n)
+        chk(self.L, self.L.mh_zero(p, n), f"zero {name}")
+        return p
+
+    def event(self):
+        e = ctypes.c_void_p()
+        chk(self.L, self.L.mh_event_create(ctypes.byref(e)), "event")
+        self.evs.append(e.value)
+        return e.value
+
+    def flush(self):
+        """Reads 1 GiB (a SUM over a buffer 4x the 256 MB Infinity Cache) so that no operand
+        of the next op is cached. A read sweep leaves clean lines: a write sweep would leave
+        dirty ones whose write-back the next op would pay for."""
+        from mantle_amd._lib import make_shape
+        if self._flush is None:
+            self._flush = self.zeros("_flush", 1 << 28)
+            self._flush_out = self.zeros("_flush_out", 1)
+            self._flush_shape = make_shape((1 << 28,))
+        chk(self.L, self.L.mh_reduce_fwd(8, self._flush_out, self._flush, self._flush_shape, -1), "flush")
+
+    def free(self):
+        for p in self.ptrs.values():
+            self.L.mh_free(p)
+        for e in self.evs:
+            self.L.mh_event_destroy(e)
+        self.ptrs, self.evs, self._flush = {}, [], None
+
+
+def time_ops(d, ops, reps, flush=True, setup=None):
+    """ops: [(label, fn, bytes)]. Each op timed alone between two events; with `flush`,
+    the caches are flushed before it. `setup()` runs (untimed) before every repetition.
+    Returns {label: median ms} and the summed medians."""
+    L = d.L
+    evs = [(d.event(), d.event()) for _ in ops]
+    times = {label: [] for label, _, _ in ops}
+    ms = ctypes.c_float()
+    for _ in range(reps + 1):  # the first repetition is a warm-up
+        if setup:
+            setup()
+        for (label, fn, _), (e0, e1) in zip(ops, evs):
+            if flush:
+                d.flush()
+            chk(L, L.mh_event_record(e0), "record")
+            chk(L, fn(), label)
+            chk(L, L.mh_event_record(e1), "record")
+        chk(L, L.mh_sync(), "sync")
+        for (label, _, _), (e0, e1) in zip(ops, evs):
+            chk(L, L.mh_event_elapsed_ms(ctypes.byref(ms), e0, e1), "elapsed")
+            times[label].append(ms.value)
+    return {k: statistics.median(v[1:]) for k, v in times.items()}
+
+
+def op_report(ops, med):
+    out = {}
+    for label, _, nbytes in ops:
+        t = med[label]
+        gbs = nbytes / (t * 1e-3) / 1e9
+        out[label] = {"ms": round(t, 4), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+    return out
+
+
+def total_report(ops, med):
+    tot_b = sum(b for _, _, b in ops)
+    tot_t = sum(med[label] for label, _, _ in ops)
+    gbs = tot_b / (tot_t * 1e-3) / 1e9
+    return {"bytes": tot_b, "ms": round(tot_t, 4), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+
+
+# ---------------------------------------------------------------------------------------
+# config 2 (headline)
+# ---------------------------------------------------------------------------------------
+def setup_c2(d, n):
+    L = d.L
     gens = [("a", "u", -1, 1), ("b", "u", 0.5, 2), ("ug", "n", 0, 1), ("x_exp", "u", -10, 10),
             ("x_log", "u", 1e-3, 10), ("x_act", "n", 0, 3), ("x_pow", "u", 0.1, 4)]
     for i, (name, kind, p, q) in enumerate(gens):
-        ptr = P(name)
+        ptr = d.alloc(name, n)
         fn = L.mh_rand_uniform if kind == "u" else L.mh_rand_normal
         chk(L, fn(ptr, n, SEED * 1000 + i, p, q), f"rand {name}")
     for name in ("res", "ga", "gb", "gx"):
-        chk(L, L.mh_zero(P(name), n), f"zero {name}")
-    e = P("exp", 1)
-    ge = P("gexp", 1)
+        d.zeros(name, n)
     expo = np.array([np.float32(0.5 + 2.5 * np.random.default_rng(SEED).random())], np.float32)
-    chk(L, L.mh_memcpy_h2d(e, expo.ctypes.data, 4), "exponent")
-    chk(L, L.mh_zero(ge, 1), "zero gexp")
+    d.upload("exp", expo)
+    d.zeros("gexp", 1)
     chk(L, L.mh_sync(), "sync")
-    return d, float(expo[0])
+    return float(expo[0])
 
 
-def make_step(L, d, n):
+def make_c2_calls(d, n):
     from mantle_amd._lib import make_shape
+    L, p = d.L, d.ptrs
     s = make_shape((n,))
-    p = d.ptrs
     x_of = {"EXP": "x_exp", "LOG": "x_log", "TANH": "x_act", "SIGMOID": "x_act", "RELU": "x_act"}
     calls = []
     for op in BINARY:
@@ -113,6 +202,231 @@ def make_step(L, d, n):
     return calls
 
 
+def run_c2(L, n, steps, warmup):
+    """The headline step: every config-2 op back to back, events between the ops."""
+    d = Dev(L)
+    expo = setup_c2(d, n)
+    calls = make_c2_calls(d, n)
+    plan = dict(step_plan())
+    evs = [d.event() for _ in range(len(calls) + 1)]
+
+    def run_step(timed):
+        if timed:
+            chk(L, L.mh_event_record(evs[0]), "record")
+        for i, (label, fn) in enumerate(calls):
+            chk(L, fn(), label)
+            if timed:
+                chk(L, L.mh_event_record(evs[i + 1]), "record")
+
+    for _ in range(warmup):
+        run_step(False)
+    chk(L, L.mh_sync(), "sync")
+    log(f"c2 warmup done ({warmup} steps)")
+    op_ms = {label: 0.0 for label, _ in calls}
+    ms = ctypes.c_float()
+    t0 = time.perf_counter()
+    step_ms_sum = 0.0
+    for _ in range(steps):
+        run_step(True)
+        chk(L, L.mh_sync(), "sync")
+        for i, (label, _) in enumerate(calls):
+            chk(L, L.mh_event_elapsed_ms(ctypes.byref(ms), evs[i], evs[i + 1]), "elapsed")
+            op_ms[label] += ms.value
+        chk(L, L.mh_event_elapsed_ms(ctypes.byref(ms), evs[0], evs[-1]), "elapsed")
+        step_ms_sum += ms.value
+    wall = time.perf_counter() - t0
+    d.free()
+    avg = {k: v / steps for k, v in op_ms.items()}
+    return {"ms_per_step": step_ms_sum / steps, "op_ms": avg, "wall": wall, "expo": expo,
+            "bytes_per_step": sum(plan.values()) * n, "plan": plan}
+
+
+# ---------------------------------------------------------------------------------------
+# config 3: NCHW bias + RELU
+# ---------------------------------------------------------------------------------------
+def run_c3(L, reps):
+    from mantle_amd import synth
+    from mantle_amd._lib import make_shape
+    shape, bshape = (256, 32, 28, 28), (1, 32, 1, 1)
+    n, nb = int(np.prod(shape)), 32
+    d = Dev(L)
+    p = d.ptrs
+    d.upload("x", synth.normal(shape, 0, 1, 11))
+    d.upload("bias", synth.normal(bshape, 0, 0.1, 12))
+    d.upload("ug", synth.normal(shape, 0, 1, 13))
+    for k in ("y", "r", "gy", "gx"):
+        d.zeros(k, n)
+    d.zeros("gb", nb)
+    sx, sb = make_shape(shape), make_shape(bshape)
+    chk(L, L.mh_sync(), "sync")
+    B = 4 * n
+    fused = [("bias_relu.fwd", lambda: L.mh_bias_relu_fwd(p["y"], p["r"], p["x"], sx, p["bias"], sb), 3 * B + 128),
+             ("bias_relu.bwd", lambda: L.mh_bias_relu_bwd_accum(None, p["gx"], p["gb"], p["y"], p["ug"], sx, sb),
+              4 * B + 256)]
+    opbyop = [("ADD.fwd", lambda: L.mh_binary_fwd(0, p["y"], sx, p["x"], sx, p["bias"], sb), 2 * B + 128),
+              ("RELU.fwd", lambda: L.mh_unary_fwd(14, p["r"], p["y"], n), 2 * B),
+              ("RELU.bwd", lambda: L.mh_unary_bwd_accum(14, p["gy"], p["y"], p["ug"], n), 4 * B),
+              ("ADD.bwd_x", lambda: L.mh_binary_bwd_accum(0, 0, p["gx"], sx, p["gy"], sx, p["x"], sx, p["bias"], sb),
+               3 * B),
+              ("ADD.bwd_bias", lambda: L.mh_binary_bwd_accum(0, 1, p["gb"], sb, p["gy"], sx, p["x"], sx, p["bias"], sb),
+               B + 256)]
+    mf = time_ops(d, fused, reps)
+    mo = time_ops(d, opbyop, reps)
+    d.free()
+    return {"shape": [list(shape), list(bshape)], "elements": n,
+            "fused": op_report(fused, mf), "fused_total": total_report(fused, mf),
+            "op_by_op": op_report(opbyop, mo), "op_by_op_total": total_report(opbyop, mo)}
+
+
+# ---------------------------------------------------------------------------------------
+# config 4: axis reductions
+# ---------------------------------------------------------------------------------------
+def run_c4(L, reps):
+    from mantle_amd import synth
+    from mantle_amd._lib import make_shape
+    d = Dev(L)
+    p = d.ptrs
+    ops = []
+    cases = [("8192x8192", (8192, 8192), 0, "n"), ("8192x8192", (8192, 8192), 1, "n"),
+             ("8192x8192", (8192, 8192), -1, "n"), ("64x512x1024", (64, 512, 1024), 2, "u")]
+    for tag, shape, axis, dist in cases:
+        n = int(np.prod(shape))
+        x = synth.normal(shape, 0, 1, 40) if dist == "n" else synth.uniform(shape, -1, 1, 41)
+        if axis >= 0:
+            synth.inject_ties(x, axis, 42)
+        else:
+            x.reshape(-1)[n // 2] = x.max()
+        name = f"x_{tag}_{axis}"
+        d.upload(name, x)
+        del x
+        red = (1,) if axis < 0 else tuple(1 if i == axis else s for i, s in enumerate(shape))
+        m = int(np.prod(red))
+        d.upload(f"ug_{name}", synth.normal(red, 0, 1, 43))
+        d.zeros(f"res_{name}", m)
+        d.zeros(f"g_{name}", n)
+        s = make_shape(shape)
+        ax = "all" if axis < 0 else f"ax{axis}"
+        for op in ("SUM", "MEAN", "MAX"):
+            o = OP_ID[op]
+            ops.append((f"{tag}.{ax}.{op}.fwd",
+                        lambda o=o, name=name, s=s, axis=axis: L.mh_reduce_fwd(o, p[f"res_{name}"], p[name], s, axis),
+                        4 * n + 4 * m))
+        for op in ("SUM", "MEAN", "MAX"):
+            o = OP_ID[op]
+            nb = (12 * n + 8 * m) if op == "MAX" else (8 * n + 4 * m)
+            ops.append((f"{tag}.{ax}.{op}.bwd",
+                        lambda o=o, name=name, s=s, axis=axis: L.mh_reduce_bwd_accum(o, p[f"g_{name}"], p[name], s,
+                                                                                     p[f"ug_{name}"], axis), nb))
+    chk(L, L.mh_sync(), "sync")
+    med = time_ops(d, ops, reps)
+    d.free()
+    fwd = [o for o in ops if o[0].endswith(".fwd")]
+    bwd = [o for o in ops if o[0].endswith(".bwd")]
+    return {"ops": op_report(ops, med), "fwd_total": total_report(fwd, med), "bwd_total": total_report(bwd, med)}
+
+
+# ---------------------------------------------------------------------------------------
+# config 5: classifier head, op by op
+# ---------------------------------------------------------------------------------------
+def run_c5(L, reps, rows=1 << 20, classes=10):
+    from mantle_amd import synth
+    from mantle_amd._lib import make_shape
+    d = Dev(L)
+    p = d.ptrs
+    E, N = rows * classes, rows
+    logits = synth.normal((rows, classes), 0, 2, 31)
+    cls = synth.integers((rows,), 0, classes, 32)
+    onehot = np.zeros((rows, classes), np.float32)
+    onehot[np.arange(rows), cls] = 1.0
+    d.upload("logits", logits)
+    d.upload("onehot", onehot)
+    for k in ("xm", "e", "sm", "lp", "t"):
+        d.zeros(k, E)
+    for k in ("max", "s"):
+        d.zeros(k, N)
+    d.zeros("loss", 1)
+    grads_full = ("g_logits", "g_xm", "g_e", "g_sm", "g_lp", "g_t")
+    grads_row = ("g_max", "g_s")
+    for k in grads_full:
+        d.zeros(k, E)
+    for k in grads_row:
+        d.zeros(k, N)
+    d.zeros("g_loss", 1)
+    SE, SN, S1 = make_shape((rows, classes)), make_shape((rows, 1)), make_shape((1,))
+    F, R = 4 * E, 4 * N
+    fwd = [
+        ("MAX.fwd", lambda: L.mh_reduce_fwd(10, p["max"], p["logits"], SE, 1), F + R),
+        ("SUB.fwd", lambda: L.mh_binary_fwd(1, p["xm"], SE, p["logits"], SE, p["max"], SN), 2 * F + R),
+        ("EXP.fwd", lambda: L.mh_unary_fwd(4, p["e"], p["xm"], E), 2 * F),
+        ("SUM.fwd", lambda: L.mh_reduce_fwd(8, p["s"], p["e"], SE, 1), F + R),
+        ("DIV.fwd", lambda: L.mh_binary_fwd(3, p["sm"], SE, p["e"], SE, p["s"], SN), 2 * F + R),
+        ("LOG.fwd", lambda: L.mh_unary_fwd(5, p["lp"], p["sm"], E), 2 * F),
+        ("MUL.fwd", lambda: L.mh_binary_fwd(2, p["t"], SE, p["lp"], SE, p["onehot"], SE), 3 * F),
+        ("MEAN.fwd", lambda: L.mh_reduce_fwd(9, p["loss"], p["t"], SE, -1), F + 4),
+    ]
+    bwd = [
+        ("MEAN.bwd", lambda: L.mh_reduce_bwd_accum(9, p["g_t"], p["t"], SE, p["g_loss"], -1), 2 * F + 4),
+        ("MUL.bwd0", lambda: L.mh_binary_bwd_accum(2, 0, p["g_lp"], SE, p["g_t"], SE, p["lp"], SE, p["onehot"], SE),
+         4 * F),
+        ("LOG.bwd", lambda: L.mh_unary_bwd_accum(5, p["g_sm"], p["sm"], p["g_lp"], E), 4 * F),
+        ("DIV.bwd0", lambda: L.mh_binary_bwd_accum(3, 0, p["g_e"], SE, p["g_sm"], SE, p["e"], SE, p["s"], SN),
+         3 * F + R),
+        ("DIV.bwd1", lambda: L.mh_binary_bwd_accum(3, 1, p["g_s"], SN, p["g_sm"], SE, p["e"], SE, p["s"], SN),
+         2 * F + 3 * R),
+        ("SUM.bwd", lambda: L.mh_reduce_bwd_accum(8, p["g_e"], p["e"], SE, p["g_s"], 1), 2 * F + R),
+        ("EXP.bwd", lambda: L.mh_unary_bwd_accum(4, p["g_xm"], p["xm"], p["g_e"], E), 4 * F),
+        ("SUB.bwd0", lambda: L.mh_binary_bwd_accum(1, 0, p["g_logits"], SE, p["g_xm"], SE, p["logits"], SE,
+                                                   p["max"], SN), 3 * F),
+        ("SUB.bwd1", lambda: L.mh_binary_bwd_accum(1, 1, p["g_max"], SN, p["g_xm"], SE, p["logits"], SE,
+                                                   p["max"], SN), F + 2 * R),
+        ("MAX.bwd", lambda: L.mh_reduce_bwd_accum(10, p["g_logits"], p["logits"], SE, p["g_max"], 1), 3 * F + 2 * R),
+    ]
+
+    def zero_grads():  # optim.zero_grad + the loss-grad seed (model.mojo:178-180)
+        for k in grads_full:
+            chk(L, L.mh_zero(p[k], E), "zero")
+        for k in grads_row:
+            chk(L, L.mh_zero(p[k], N), "zero")
+        chk(L, L.mh_fill(p["g_loss"], 1.0, 1), "seed")
+
+    chk(L, L.mh_sync(), "sync")
+    med = time_ops(d, fwd + bwd, reps, flush=False, setup=zero_grads)
+    # the whole chain between two events (includes host launch gaps), caches flushed first
+    e0, e1 = d.event(), d.event()
+    ms = ctypes.c_float()
+    chain = []
+    for _ in range(reps + 1):
+        zero_grads()
+        d.flush()
+        chk(L, L.mh_event_record(e0), "record")
+        for label, fn, _ in fwd + bwd:
+            chk(L, fn(), label)
+        chk(L, L.mh_event_record(e1), "record")
+        chk(L, L.mh_sync(), "sync")
+        chk(L, L.mh_event_elapsed_ms(ctypes.byref(ms), e0, e1), "elapsed")
+        chain.append(ms.value)
+    chain_ms = statistics.median(chain[1:])
+    d.free()
+    return {"shape": [rows, classes], "elements": E,
+            "fwd": op_report(fwd, med), "bwd": op_report(bwd, med),
+            "fwd_total": total_report(fwd, med), "bwd_total": total_report(bwd, med),
+            "chain_ms": round(chain_ms, 4), "chain_rows_per_s": round(rows / (chain_ms * 1e-3), 1),
+            "fused_min_bytes": 24 * E}
+
+
+def run_copy(L, reps):
+    d = Dev(L)
+    n = 1 << 28
+    src, dst = d.zeros("src", n), d.zeros("dst", n)
+    ops = [("copy_1GiB", lambda: L.mh_memcpy_d2d(dst, src, 4 * n), 8 * n)]
+    med = time_ops(d, ops, reps, flush=False)
+    d.free()
+    return op_report(ops, med)
+
+
+# ---------------------------------------------------------------------------------------
+# CPU baseline
+# ---------------------------------------------------------------------------------------
 def cpu_baseline(n_sample: int, reps: int, expo: float):
     """The CPU restatement (oracle/, single thread, like the reference's elementwise paths)
     on the same op sequence over a bounded sample; GB/s with the same byte accounting."""
@@ -150,16 +464,83 @@ def cpu_baseline(n_sample: int, reps: int, expo: float):
                       f"(oracle/mantle_oracle.c, -O3)"}
 
 
+# ---------------------------------------------------------------------------------------
+# rocprofv3 summaries
+# ---------------------------------------------------------------------------------------
+def _read_pmc_csv(path, counter):
+    """{kernel name: [counter value per dispatch]} from a rocprofv3 --pmc counter_collection.csv."""
+    out = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") != counter:
+                continue
+            out.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+    return out
+
+
+def pmc_summary(fetch_csv, write_csv, copy_bytes=8 << 28):
+    """Writes profiles/traffic.json: HBM bytes per dispatch of each kernel, from FETCH_SIZE
+    and WRITE_SIZE (KiB per dispatch), each scaled by the factor that makes the library's
+    copy kernel (k_copy, `copy_bytes / 2` read and written) read exactly its size."""
+    fetch, write = _read_pmc_csv(fetch_csv, "FETCH_SIZE"), _read_pmc_csv(write_csv, "WRITE_SIZE")
+    copy_k = [k for k in fetch if "k_copy" in k]
+    if not copy_k:
+        raise SystemExit("no k_copy dispatch in the FETCH_SIZE run: run the 'copy' workload under rocprofv3")
+    half = copy_bytes / 2
+    f_scale = half / (statistics.median(fetch[copy_k[0]]) * 1024)
+    w_scale = half / (statistics.median(write[copy_k[0]]) * 1024)
+    kernels = {}
+    for k in sorted(set(fetch) | set(write)):
+        fv = statistics.median(fetch[k]) * 1024 * f_scale if k in fetch else None
+        wv = statistics.median(write[k]) * 1024 * w_scale if k in write else None
+        kernels[k] = {"fetch_bytes": fv, "write_bytes": wv,
+                      "hbm_bytes": (fv or 0) + (wv or 0), "dispatches": len(fetch.get(k, []))}
+    summary = {"fetch_scale": f_scale, "write_scale": w_scale, "copy_kernel": copy_k[0], "kernels": kernels}
+    os.makedirs(os.path.dirname(TRAFFIC_JSON), exist_ok=True)
+    with open(TRAFFIC_JSON, "w") as f:
+        json.dump(summary, f, indent=1, sort_keys=True)
+    return summary
+
+
+# label of a config-2 op -> substring of its kernel's name
+C2_KERNEL = {"ADD.bwd": "k_bwd2_same4<0>", "SUB.bwd": "k_bwd2_same4<1>", "MUL.bwd": "k_bwd2_same4<2>",
+             "DIV.bwd": "k_bwd2_same4<3>", "ADD.fwd": "FBin<0>", "SUB.fwd": "FBin<1>", "MUL.fwd": "FBin<2>",
+             "DIV.fwd": "FBin<3>", "EXP.fwd": "FUn<4>", "LOG.fwd": "FUn<5>", "SIGMOID.fwd": "FUn<13>",
+             "RELU.fwd": "FUn<14>", "TANH.fwd": "FUn<15>", "EXP.bwd": "FUnBwd<4>", "LOG.bwd": "FUnBwd<5>",
+             "SIGMOID.bwd": "FUnBwd<13>", "RELU.bwd": "FUnBwd<14>", "TANH.bwd": "FUnBwd<15>",
+             "POW.fwd": "FPowi", "POW.bwd_x": "FPowBwdX", "POW.bwd_exp": "LdPowGrad"}
+
+
+def traffic_for(label):
+    if not os.path.exists(TRAFFIC_JSON):
+        return None
+    with open(TRAFFIC_JSON) as f:
+        kernels = json.load(f)["kernels"]
+    key = C2_KERNEL.get(label)
+    hits = [v for k, v in kernels.items() if key and key in k]
+    return round(hits[0]["hbm_bytes"]) if len(hits) == 1 else None
+
+
+# ---------------------------------------------------------------------------------------
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--log2n", type=int, default=28)
+    ap.add_argument("--workloads", default="c3,c4,c5,copy",
+                    help="extra workloads after the headline step (comma list of c3,c4,c5,copy; 'none')")
+    ap.add_argument("--reps", type=int, default=10, help="repetitions per op of the extra workloads")
     ap.add_argument("--cpu-log2n", type=int, default=24)
     ap.add_argument("--cpu-reps", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write profiles/traffic.json from two rocprofv3 --pmc runs and exit")
     args = ap.parse_args()
+    if args.pmc_summary:
+        s = pmc_summary(*args.pmc_summary)
+        print(json.dumps({"fetch_scale": s["fetch_scale"], "write_scale": s["write_scale"]}))
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
         print(f"bench.py: this build runs the op layer on one GPU; --gpus {args.gpus} "
@@ -171,74 +552,47 @@ def main():
     from mantle_amd._lib import lib
     L = lib()
     n = 1 << args.log2n
-    print(f"[bench] init, n = 2^{args.log2n}", file=sys.stderr, flush=True)
+    log(f"init, n = 2^{args.log2n}")
     chk(L, L.mh_init(0, 1), "mh_init")  # MH_INIT_ASYNC: no host sync per call
-    d, expo = setup_gpu(L, n)
-    calls = make_step(L, d, n)
-    plan = dict(step_plan())
-    evs = []
-    for _ in range(len(calls) + 1):
-        e = ctypes.c_void_p()
-        chk(L, L.mh_event_create(ctypes.byref(e)), "event")
-        evs.append(e.value)
-
-    def run_step(timed):
-        if timed:
-            chk(L, L.mh_event_record(evs[0]), "record")
-        for i, (label, fn) in enumerate(calls):
-            chk(L, fn(), label)
-            if timed:
-                chk(L, L.mh_event_record(evs[i + 1]), "record")
-
-    for _ in range(args.warmup):
-        run_step(False)
-    chk(L, L.mh_sync(), "sync")
-    print(f"[bench] warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
-
-    op_ms = {label: 0.0 for label, _ in calls}
-    ms = ctypes.c_float()
-    t0 = time.perf_counter()
-    step_ms_sum = 0.0
-    for _ in range(args.steps):
-        run_step(True)
-        chk(L, L.mh_sync(), "sync")
-        for i, (label, _) in enumerate(calls):
-            chk(L, L.mh_event_elapsed_ms(ctypes.byref(ms), evs[i], evs[i + 1]), "elapsed")
-            op_ms[label] += ms.value
-        chk(L, L.mh_event_elapsed_ms(ctypes.byref(ms), evs[0], evs[-1]), "elapsed")
-        step_ms_sum += ms.value
-    wall = time.perf_counter() - t0
-    K = args.steps
-    ms_per_step = step_ms_sum / K
-    bytes_per_step = sum(plan.values()) * n
-    value = bytes_per_step / (ms_per_step * 1e-3) / 1e9
-    ops = {}
-    for label, tot in op_ms.items():
-        avg = tot / K
-        ops[label] = {"ms": round(avg, 4), "GB/s": round(plan[label] * n / (avg * 1e-3) / 1e9, 1),
-                      "frac": round(plan[label] * n / (avg * 1e-3) / 1e9 / PEAK_GBS, 4)}
-    dom = max(op_ms, key=op_ms.get)
-    dom_avg_ms = op_ms[dom] / K
-    dom_bytes = plan[dom] * n
-    achieved = dom_bytes / (dom_avg_ms * 1e-3) / 1e9
-    roof = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "bytes_per_launch": dom_bytes,
-            "avg_launch_ms": round(dom_avg_ms, 4)}
-    out = {"metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K,
-           "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+    r = run_c2(L, n, args.steps, args.warmup) if args.steps > 0 else None
+    out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-           "data": "synthetic (seeded device SplitMix64: U/N as in config 2)",
-           "config": {"workload": "config2: fp32 2^28-element elementwise fwd+bwd "
-                                  "(ADD/SUB/MUL/DIV/EXP/LOG/TANH/SIGMOID/RELU/POW)",
-                      "elements": n, "bytes_per_step": bytes_per_step, "pow_exponent": expo,
-                      "frac_of_peak": round(value / PEAK_GBS, 4), "wall_s": round(wall, 3)},
-           "roofline": roof, "ops": ops}
-    d.free()
-    for e in evs:
-        L.mh_event_destroy(e)
-    if rank == 0 and not args.no_cpu_baseline:
-        print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(1 << args.cpu_log2n, args.cpu_reps, expo)
+           "data": "synthetic (seeded: device SplitMix64 for config 2, numpy SFC64 for configs 3-5)"}
+    if r is not None:
+        K = args.steps
+        value = r["bytes_per_step"] / (r["ms_per_step"] * 1e-3) / 1e9
+        plan = r["plan"]
+        ops = {}
+        for label, avg in r["op_ms"].items():
+            gbs = plan[label] * n / (avg * 1e-3) / 1e9
+            ops[label] = {"ms": round(avg, 4), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+        dom = max(r["op_ms"], key=r["op_ms"].get)
+        dom_ms = r["op_ms"][dom]
+        dom_bytes = plan[dom] * n
+        achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+        out.update({
+            "value": round(value, 1), "unit": "GB/s", "ms_per_step": round(r["ms_per_step"], 4),
+            "config": {"workload": "config2: fp32 2^28-element elementwise fwd+bwd "
+                                   "(ADD/SUB/MUL/DIV/EXP/LOG/TANH/SIGMOID/RELU/POW)",
+                       "elements": n, "bytes_per_step": r["bytes_per_step"], "pow_exponent": r["expo"],
+                       "frac_of_peak": round(value / PEAK_GBS, 4), "elements_per_s": round(n / (r["ms_per_step"] * 1e-3)),
+                       "wall_s": round(r["wall"], 3)},
+            "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS,
+                         "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic_for(dom),
+                         "bytes_per_launch": dom_bytes, "avg_launch_ms": round(dom_ms, 4)},
+            "ops": ops})
+        log(f"c2: {value:.1f} GB/s, {r['ms_per_step']:.3f} ms/step")
+    wl = [w for w in args.workloads.split(",") if w and w != "none"]
+    runners = {"c3": lambda: run_c3(L, args.reps), "c4": lambda: run_c4(L, args.reps),
+               "c5": lambda: run_c5(L, args.reps), "copy": lambda: run_copy(L, args.reps)}
+    if wl:
+        out["workloads"] = {}
+    for w in wl:
+        log(f"workload {w}")
+        out["workloads"][w] = runners[w]()
+    if rank == 0 and not args.no_cpu_baseline and r is not None:
+        log("cpu baseline")
+        out["cpu_baseline"] = cpu_baseline(1 << args.cpu_log2n, args.cpu_reps, r["expo"])
     elif rank == 0:
         out["cpu_baseline"] = None
     if rank == 0:

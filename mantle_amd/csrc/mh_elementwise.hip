@@ -3,17 +3,17 @@
 // One engine serves every elementwise entry point: an output stream (written, or
 // read-modify-written for "grad = grad + rg") and up to four input streams, each FULL (same
 // shape as the output), SCALAR (one element, loaded once per thread) or BCAST (strided in the
-// collapsed output space). Same-shape work takes the float4 path: 256-thread blocks, each
-// thread issuing all of its 128-bit loads before any arithmetic. Broadcast work decodes the
-// output coordinate of each quad with precomputed fast divisors; an inner dimension divisible
-// by 4 keeps 128-bit accesses for every operand whose inner stride is 0 or 1.
+// collapsed output space). Same-shape work takes the float4 path: 256-thread blocks, one
+// 128-bit access per stream per thread, all loads issued before any arithmetic. Broadcast work
+// decodes the output coordinate of each quad with precomputed fast divisors; an inner
+// dimension divisible by 4 keeps 128-bit accesses for every operand whose inner stride is 0
+// or 1.
 #include "mh_internal.h"
 #include "mh_math.h"
 
 namespace mh {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;  // quads per thread per block
 
 struct DevScal {
     const float* p[4];
@@ -148,7 +148,10 @@ __device__ __forceinline__ float comp(const float4& q, int j) {
     return j == 0 ? q.x : (j == 1 ? q.y : (j == 2 ? q.z : q.w));
 }
 
-// Same-shape engine: all inputs FULL or SCALAR (bit k of smask).
+// Same-shape engine: all inputs FULL or SCALAR (bit k of smask). One quad (16 B per
+// stream) per thread per iteration: on gfx950 this streams faster than several quads per
+// thread (fewer bytes in flight per wave, more waves resident). The launch covers every quad
+// in one iteration up to 2^31 blocks; the stride loop only matters beyond that.
 template <class F, int NIN, bool ACCUM>
 __global__ void __launch_bounds__(kThreads)
     k_same4(float* __restrict__ out, InPtrs<NIN> in, int smask, int64_t n, DevScal ds, F f) {
@@ -157,34 +160,24 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int k = 0; k < NIN; ++k) sv[k] = ((smask >> k) & 1) ? in.p[k][0] : 0.0f;
     const int64_t nq = n >> 2;
-    const int64_t q0 = (int64_t)blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
-    float4 iv[kUnroll][NIN > 0 ? NIN : 1];
-    float4 ov[kUnroll];
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
+        float4 iv[NIN > 0 ? NIN : 1];
+        float4 ov;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-        const int64_t q = q0 + (int64_t)u * kThreads;
-        if (q < nq) {
+        for (int k = 0; k < NIN; ++k)
+            if (!((smask >> k) & 1)) iv[k] = reinterpret_cast<const float4*>(in.p[k])[q];
+        if (ACCUM) ov = reinterpret_cast<const float4*>(out)[q];
+        float r[4];
 #pragma unroll
-            for (int k = 0; k < NIN; ++k)
-                if (!((smask >> k) & 1)) iv[u][k] = reinterpret_cast<const float4*>(in.p[k])[q];
-            if (ACCUM) ov[u] = reinterpret_cast<const float4*>(out)[q];
+        for (int j = 0; j < 4; ++j) {
+            float v[NIN > 0 ? NIN : 1];
+#pragma unroll
+            for (int k = 0; k < NIN; ++k) v[k] = ((smask >> k) & 1) ? sv[k] : comp(iv[k], j);
+            r[j] = f(v);
+            if (ACCUM) r[j] = comp(ov, j) + r[j];
         }
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-        const int64_t q = q0 + (int64_t)u * kThreads;
-        if (q < nq) {
-            float r[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float v[NIN > 0 ? NIN : 1];
-#pragma unroll
-                for (int k = 0; k < NIN; ++k) v[k] = ((smask >> k) & 1) ? sv[k] : comp(iv[u][k], j);
-                r[j] = f(v);
-                if (ACCUM) r[j] = comp(ov[u], j) + r[j];
-            }
-            reinterpret_cast<float4*>(out)[q] = make_float4(r[0], r[1], r[2], r[3]);
-        }
+        reinterpret_cast<float4*>(out)[q] = make_float4(r[0], r[1], r[2], r[3]);
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         for (int64_t i = nq << 2; i < n; ++i) {
@@ -215,133 +208,172 @@ __global__ void __launch_bounds__(kThreads)
     }
 }
 
-// Broadcast engine over an ElwPlan. VEC = 4: each work item is a quad of the inner dim
-// (requires plan.vec_ok and aligned pointers); VEC = 1: single elements. BIG: 64-bit
-// coordinate decode (n >= 2^31).
-template <class F, int NIN, bool ACCUM, int VEC, bool BIG>
+// Offsets of the broadcast (IN_BCAST) operands at output element idx, and the element's
+// coordinate along the innermost collapsed dim. BIG: 64-bit division (n >= 2^31).
+template <int NIN, bool BIG>
+__device__ __forceinline__ void bcast_decode(const ElwPlan& pl, int64_t idx, int64_t* off, int64_t* cin) {
+    const int inner = pl.rank - 1;
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) off[k] = 0;
+    int64_t rem = idx;
+#pragma unroll
+    for (int d = MH_MAX_RANK - 1; d >= 0; --d) {
+        if (d > inner) continue;
+        int64_t q, c;
+        if (BIG) {
+            q = rem / pl.dims[d];
+            c = rem - q * pl.dims[d];
+        } else {
+            const uint32_t r32 = (uint32_t)rem;
+            const uint32_t q32 = fdiv(r32, pl.fd[d]);
+            q = q32;
+            c = (int64_t)(r32 - q32 * pl.fd[d].d);
+        }
+        if (d == inner) *cin = c;
+#pragma unroll
+        for (int k = 0; k < NIN; ++k)
+            if (pl.kind[k] == IN_BCAST) off[k] += c * pl.st[k][d];
+        rem = q;
+    }
+}
+
+// Broadcast engine, 128-bit path: the output and every FULL operand stream as flat float4
+// quads whatever the shape (all must be 16-byte aligned); only the broadcast operands are
+// gathered. The quad's first element is decoded; the next three step along the inner dim
+// unless they cross into the next row, where they are decoded afresh. INNER4 (inner dim a
+// multiple of 4, broadcast operands 16-byte aligned): a quad never crosses a row, and an
+// operand contiguous along the inner dim is read as one float4.
+template <class F, int NIN, bool ACCUM, bool INNER4, bool BIG>
 __global__ void __launch_bounds__(kThreads)
-    k_bcast(float* __restrict__ out, InPtrs<NIN> in, ElwPlan pl, DevScal ds, F f) {
+    k_bcast4(float* __restrict__ out, InPtrs<NIN> in, ElwPlan pl, DevScal ds, F f) {
     constexpr int NA = NIN > 0 ? NIN : 1;
     f.setup(ds);
     float sv[NA];
 #pragma unroll
     for (int k = 0; k < NIN; ++k) sv[k] = pl.kind[k] == IN_SCALAR ? in.p[k][0] : 0.0f;
-    const int64_t nitems = VEC == 4 ? (pl.n >> 2) : pl.n;
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
     const int inner = pl.rank - 1;
-    for (int64_t it = (int64_t)blockIdx.x * kThreads + threadIdx.x; it < nitems; it += stride) {
-        const int64_t idx = it * VEC;
-        int64_t off[NA];
+    const int64_t dinner = pl.dims[inner];
+    const int64_t nq = pl.n >> 2;
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
+        const int64_t idx = q * 4;
+        int64_t off[4][NA];
+        int64_t cin = 0;
+        bcast_decode<NIN, BIG>(pl, idx, off[0], &cin);
+        if (!INNER4) {
 #pragma unroll
-        for (int k = 0; k < NIN; ++k) off[k] = 0;
-        if (pl.any_bcast) {
-            int64_t rem = idx;
+            for (int j = 1; j < 4; ++j) {
+                if (cin + j < dinner) {
 #pragma unroll
-            for (int d = MH_MAX_RANK - 1; d >= 0; --d) {
-                if (d > inner) continue;
-                int64_t q, c;
-                if (BIG) {
-                    q = rem / pl.dims[d];
-                    c = rem - q * pl.dims[d];
+                    for (int k = 0; k < NIN; ++k) off[j][k] = off[0][k] + j * pl.st[k][inner];
                 } else {
-                    uint32_t r32 = (uint32_t)rem;
-                    uint32_t q32 = fdiv(r32, pl.fd[d]);
-                    q = q32;
-                    c = (int64_t)(r32 - q32 * pl.fd[d].d);
+                    int64_t c2;
+                    bcast_decode<NIN, BIG>(pl, idx + j, off[j], &c2);
                 }
-#pragma unroll
-                for (int k = 0; k < NIN; ++k)
-                    if (pl.kind[k] == IN_BCAST) off[k] += c * pl.st[k][d];
-                rem = q;
             }
         }
-        float v[VEC][NA];
+        float v[4][NA];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
             if (pl.kind[k] == IN_SCALAR) {
 #pragma unroll
-                for (int j = 0; j < VEC; ++j) v[j][k] = sv[k];
+                for (int j = 0; j < 4; ++j) v[j][k] = sv[k];
             } else if (pl.kind[k] == IN_FULL) {
-                if constexpr (VEC == 4) {
-                    float4 q = reinterpret_cast<const float4*>(in.p[k])[it];
-                    v[0][k] = q.x; v[1][k] = q.y; v[2][k] = q.z; v[3][k] = q.w;
+                const float4 t = reinterpret_cast<const float4*>(in.p[k])[q];
+                v[0][k] = t.x; v[1][k] = t.y; v[2][k] = t.z; v[3][k] = t.w;
+            } else if (INNER4) {
+                if (pl.st[k][inner] == 1) {
+                    const float4 t = *reinterpret_cast<const float4*>(in.p[k] + off[0][k]);
+                    v[0][k] = t.x; v[1][k] = t.y; v[2][k] = t.z; v[3][k] = t.w;
                 } else {
-                    v[0][k] = in.p[k][idx];
+                    const float t = in.p[k][off[0][k]];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) v[j][k] = t;
                 }
             } else {
-                if constexpr (VEC == 4) {
-                    if (pl.st[k][inner] == 1) {
-                        float4 q = *reinterpret_cast<const float4*>(in.p[k] + off[k]);
-                        v[0][k] = q.x; v[1][k] = q.y; v[2][k] = q.z; v[3][k] = q.w;
-                    } else {
-                        float s = in.p[k][off[k]];
 #pragma unroll
-                        for (int j = 0; j < VEC; ++j) v[j][k] = s;
-                    }
-                } else {
-                    v[0][k] = in.p[k][off[k]];
-                }
+                for (int j = 0; j < 4; ++j) v[j][k] = in.p[k][off[j][k]];
             }
         }
-        if constexpr (VEC == 4) {
-            float4 o = ACCUM ? reinterpret_cast<const float4*>(out)[it] : make_float4(0.f, 0.f, 0.f, 0.f);
-            float r[4];
+        const float4 o = ACCUM ? reinterpret_cast<const float4*>(out)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        float r[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                r[j] = f(v[j]);
-                if (ACCUM) r[j] = comp(o, j) + r[j];
-            }
-            reinterpret_cast<float4*>(out)[it] = make_float4(r[0], r[1], r[2], r[3]);
-        } else {
-            float r = f(v[0]);
-            out[idx] = ACCUM ? out[idx] + r : r;
+        for (int j = 0; j < 4; ++j) {
+            r[j] = f(v[j]);
+            if (ACCUM) r[j] = comp(o, j) + r[j];
+        }
+        reinterpret_cast<float4*>(out)[q] = make_float4(r[0], r[1], r[2], r[3]);
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        for (int64_t i = nq << 2; i < pl.n; ++i) {
+            int64_t off1[NA], c;
+            bcast_decode<NIN, BIG>(pl, i, off1, &c);
+            float v1[NA];
+#pragma unroll
+            for (int k = 0; k < NIN; ++k)
+                v1[k] = pl.kind[k] == IN_SCALAR ? sv[k] : (pl.kind[k] == IN_FULL ? in.p[k][i] : in.p[k][off1[k]]);
+            const float r1 = f(v1);
+            out[i] = ACCUM ? out[i] + r1 : r1;
         }
     }
 }
 
+// Broadcast engine, scalar path (the output or a FULL operand is not 16-byte aligned).
+template <class F, int NIN, bool ACCUM, bool BIG>
+__global__ void __launch_bounds__(kThreads)
+    k_bcast1(float* __restrict__ out, InPtrs<NIN> in, ElwPlan pl, DevScal ds, F f) {
+    constexpr int NA = NIN > 0 ? NIN : 1;
+    f.setup(ds);
+    float sv[NA];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) sv[k] = pl.kind[k] == IN_SCALAR ? in.p[k][0] : 0.0f;
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < pl.n; i += stride) {
+        int64_t off[NA], c;
+        bcast_decode<NIN, BIG>(pl, i, off, &c);
+        float v[NA];
+#pragma unroll
+        for (int k = 0; k < NIN; ++k)
+            v[k] = pl.kind[k] == IN_SCALAR ? sv[k] : (pl.kind[k] == IN_FULL ? in.p[k][i] : in.p[k][off[k]]);
+        const float r = f(v);
+        out[i] = ACCUM ? out[i] + r : r;
+    }
+}
+
 // Fused two-operand backward of a same-shape binary op (both backward_op calls of
-// ops.mojo:408-463 with equal shapes): g1 = g1 + rg0, g2 = g2 + rg1.
+// ops.mojo:408-463 with equal shapes): g1 = g1 + rg0, g2 = g2 + rg1. One quad per thread per
+// iteration, as k_same4.
 template <int OP>
 __global__ void __launch_bounds__(kThreads)
     k_bwd2_same4(float* __restrict__ g1, float* __restrict__ g2, const float* __restrict__ ug,
                  const float* __restrict__ a, const float* __restrict__ b, int64_t n) {
     constexpr bool NEED_AB = (OP == MH_MUL || OP == MH_DIV);
     const int64_t nq = n >> 2;
-    const int64_t q0 = (int64_t)blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
-    float4 vu[kUnroll], va[kUnroll], vb[kUnroll], v1[kUnroll], v2[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-        const int64_t q = q0 + (int64_t)u * kThreads;
-        if (q < nq) {
-            vu[u] = reinterpret_cast<const float4*>(ug)[q];
-            if (NEED_AB) {
-                va[u] = reinterpret_cast<const float4*>(a)[q];
-                vb[u] = reinterpret_cast<const float4*>(b)[q];
-            }
-            v1[u] = reinterpret_cast<const float4*>(g1)[q];
-            v2[u] = reinterpret_cast<const float4*>(g2)[q];
-        }
-    }
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
     FBinRg<OP, 0, false> f0;
     FBinRg<OP, 1, false> f1;
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-        const int64_t q = q0 + (int64_t)u * kThreads;
-        if (q < nq) {
-            float r1[4], r2[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float uu = comp(vu[u], j);
-                const float aa = NEED_AB ? comp(va[u], j) : 0.0f;
-                const float bb = NEED_AB ? comp(vb[u], j) : 0.0f;
-                float x0[3] = {uu, bb, 0.0f};      // id0 reads t2
-                float x1[3] = {uu, aa, bb};        // id1 reads t1 (and t2 for DIV)
-                r1[j] = comp(v1[u], j) + f0(x0);
-                r2[j] = comp(v2[u], j) + f1(x1);
-            }
-            reinterpret_cast<float4*>(g1)[q] = make_float4(r1[0], r1[1], r1[2], r1[3]);
-            reinterpret_cast<float4*>(g2)[q] = make_float4(r2[0], r2[1], r2[2], r2[3]);
+    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
+        const float4 vu = reinterpret_cast<const float4*>(ug)[q];
+        float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vb = va;
+        if (NEED_AB) {
+            va = reinterpret_cast<const float4*>(a)[q];
+            vb = reinterpret_cast<const float4*>(b)[q];
         }
+        const float4 v1 = reinterpret_cast<const float4*>(g1)[q];
+        const float4 v2 = reinterpret_cast<const float4*>(g2)[q];
+        float r1[4], r2[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float uu = comp(vu, j);
+            const float aa = comp(va, j);
+            const float bb = comp(vb, j);
+            float x0[3] = {uu, bb, 0.0f};  // id0 reads t2
+            float x1[3] = {uu, aa, bb};    // id1 reads t1 (and t2 for DIV)
+            r1[j] = comp(v1, j) + f0(x0);
+            r2[j] = comp(v2, j) + f1(x1);
+        }
+        reinterpret_cast<float4*>(g1)[q] = make_float4(r1[0], r1[1], r1[2], r1[3]);
+        reinterpret_cast<float4*>(g2)[q] = make_float4(r2[0], r2[1], r2[2], r2[3]);
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         for (int64_t i = nq << 2; i < n; ++i) {
@@ -373,15 +405,15 @@ static int run_map(float* out, const ElwPlan& pl, const float* const* ptrs, cons
     InPtrs<NIN> in;
     for (int k = 0; k < NIN; ++k) in.p[k] = ptrs[k];
     hipStream_t st = ctx().stream;
-    bool al = aligned16(out);
+    bool al = aligned16(out);  // the output and every FULL operand are 16-byte aligned
     for (int k = 0; k < NIN; ++k)
-        if (pl.kind[k] != IN_SCALAR) al = al && aligned16(ptrs[k]);
+        if (pl.kind[k] == IN_FULL) al = al && aligned16(ptrs[k]);
     if (!pl.any_bcast) {
         int smask = 0;
         for (int k = 0; k < NIN; ++k)
             if (pl.kind[k] == IN_SCALAR) smask |= 1 << k;
         if (al) {
-            hipLaunchKernelGGL((k_same4<F, NIN, ACCUM>), dim3(grid_for(pl.n >> 2, kThreads * kUnroll)),
+            hipLaunchKernelGGL((k_same4<F, NIN, ACCUM>), dim3(grid_for(pl.n >> 2, kThreads)),
                                dim3(kThreads), 0, st, out, in, smask, pl.n, ds, f);
         } else {
             int64_t b = (pl.n + kThreads - 1) / kThreads;
@@ -392,19 +424,26 @@ static int run_map(float* out, const ElwPlan& pl, const float* const* ptrs, cons
         return MH_OK;
     }
     const bool big = pl.n >= ((int64_t)1 << 31);
-    const bool vec = pl.vec_ok && al;
-    const int64_t items = vec ? (pl.n >> 2) : pl.n;
-    int64_t blocks = (items + kThreads - 1) / kThreads;
+    bool al_b = true;  // broadcast operands 16-byte aligned (float4 gathers when INNER4)
+    for (int k = 0; k < NIN; ++k)
+        if (pl.kind[k] == IN_BCAST) al_b = al_b && aligned16(ptrs[k]);
+    if (al) {
+        dim3 g(grid_for(pl.n >> 2, kThreads)), b(kThreads);
+        if (pl.vec_ok && al_b) {
+            if (big) hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, true, true>), g, b, 0, st, out, in, pl, ds, f);
+            else hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, true, false>), g, b, 0, st, out, in, pl, ds, f);
+        } else {
+            if (big) hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, false, true>), g, b, 0, st, out, in, pl, ds, f);
+            else hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, false, false>), g, b, 0, st, out, in, pl, ds, f);
+        }
+        return MH_OK;
+    }
+    int64_t blocks = (pl.n + kThreads - 1) / kThreads;
     if (blocks > 262144) blocks = 262144;
     if (blocks < 1) blocks = 1;
     dim3 g((unsigned)blocks), b(kThreads);
-    if (vec) {
-        if (big) hipLaunchKernelGGL((k_bcast<F, NIN, ACCUM, 4, true>), g, b, 0, st, out, in, pl, ds, f);
-        else hipLaunchKernelGGL((k_bcast<F, NIN, ACCUM, 4, false>), g, b, 0, st, out, in, pl, ds, f);
-    } else {
-        if (big) hipLaunchKernelGGL((k_bcast<F, NIN, ACCUM, 1, true>), g, b, 0, st, out, in, pl, ds, f);
-        else hipLaunchKernelGGL((k_bcast<F, NIN, ACCUM, 1, false>), g, b, 0, st, out, in, pl, ds, f);
-    }
+    if (big) hipLaunchKernelGGL((k_bcast1<F, NIN, ACCUM, true>), g, b, 0, st, out, in, pl, ds, f);
+    else hipLaunchKernelGGL((k_bcast1<F, NIN, ACCUM, false>), g, b, 0, st, out, in, pl, ds, f);
     return MH_OK;
 }
 
@@ -706,7 +745,7 @@ int mh_binary_bwd_accum2(int op, float* grad1, float* grad2, const float* ug, co
     if (!ug || (need_ab && (!t1 || !t2))) return fail(MH_ERR_NULL, "mh_binary_bwd_accum2: null tensor");
     MH_TRY(require_init());
     const int64_t n = numel(s);
-    dim3 g(grid_for(n >> 2, kThreads * kUnroll)), b(kThreads);
+    dim3 g(grid_for(n >> 2, kThreads)), b(kThreads);
     hipStream_t st = ctx().stream;
     switch (op) {
         case MH_ADD: hipLaunchKernelGGL(k_bwd2_same4<MH_ADD>, g, b, 0, st, grad1, grad2, ug, t1, t2, n); break;

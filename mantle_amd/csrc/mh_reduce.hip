@@ -2,7 +2,8 @@
 // backward tie routing and the POW exponent gradient.
 //
 // Every reduction is expressed on a view [A, B, C] reduced over B:
-//   C == 1, B <= 64 : one thread per output row;
+//   C == 1, B <= 32 : 256 rows staged in LDS by coalesced float4 loads, one thread per
+//                     row (unaligned x: one thread per row straight from memory);
 //   C == 1          : one wavefront (64 lanes) per row, 128-bit loads, butterfly shuffle;
 //                     few long rows are cut into chunks whose partials a second pass combines;
 //   C  > 1          : one thread per output column (a quad of columns when C % 4 == 0), the
@@ -11,6 +12,7 @@
 // No atomics: each output's summation order is fixed by the launch shape, so a call repeated
 // on the same input returns the same bits.
 #include <cfloat>
+#include <type_traits>
 
 #include "mh_internal.h"
 #include "mh_math.h"
@@ -144,6 +146,87 @@ __global__ void __launch_bounds__(kRThreads)
     }
 }
 
+// Short rows (C == 1, B <= BMAX): the block stages rows [r0, r0 + 256) -- one contiguous,
+// 16-byte aligned run of floats -- in LDS with float4 loads, then thread t reduces row r0 + t
+// in element order (the order of the reference's scalar tail loop for rows shorter than
+// its SIMD width).
+template <int BMAX>
+__device__ __forceinline__ int64_t stage_rows(float* tile, const float* __restrict__ x, int64_t nrows, int B,
+                                              int64_t* rows_out) {
+    const int64_t r0 = (int64_t)blockIdx.x * kRThreads;
+    const int64_t rows = (nrows - r0) < kRThreads ? (nrows - r0) : kRThreads;
+    const int64_t base = r0 * B;
+    const int cnt = (int)(rows * B);
+    const int nq = cnt >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(x + base);
+    for (int i = threadIdx.x; i < nq; i += kRThreads) reinterpret_cast<float4*>(tile)[i] = x4[i];
+    for (int i = (nq << 2) + threadIdx.x; i < cnt; i += kRThreads) tile[i] = x[base + i];
+    *rows_out = rows;
+    return base;
+}
+
+template <class R, int BMAX>
+__global__ void __launch_bounds__(kRThreads)
+    k_rows_lds(const float* __restrict__ x, int64_t nrows, int B, float* out, float* out2, int epi, float div) {
+    __shared__ float4 tile4[kRThreads * BMAX / 4];
+    float* tile = reinterpret_cast<float*>(tile4);
+    int64_t rows;
+    stage_rows<BMAX>(tile, x, nrows, B, &rows);
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < rows) {
+        typename R::T acc = R::init();
+        for (int j = 0; j < B; ++j) acc = R::comb(acc, R::lift(tile[t * B + j]));
+        epi_store(out, out2, (int64_t)blockIdx.x * kRThreads + t, acc, epi, div);
+    }
+}
+
+// MAX backward over short rows in one pass (basics.mojo:581-615 for a last-axis reduce):
+// the row max m and count c from the LDS tile, then grad[i] = grad[i] + (x[i] == m ?
+// fl(1/c) * ug[row] : 0), x read once from HBM.
+template <int BMAX>
+__global__ void __launch_bounds__(kRThreads)
+    k_max_bwd_rows(float* __restrict__ grad, const float* __restrict__ x, const float* __restrict__ ug,
+                   int64_t nrows, int B, FastDiv fdB) {
+    __shared__ float4 tile4[kRThreads * BMAX / 4];
+    __shared__ float sm[kRThreads], sg[kRThreads];
+    float* tile = reinterpret_cast<float*>(tile4);
+    int64_t rows;
+    const int64_t base = stage_rows<BMAX>(tile, x, nrows, B, &rows);
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < rows) {
+        MC acc = RMaxCnt::init();
+        for (int j = 0; j < B; ++j) acc = RMaxCnt::comb(acc, RMaxCnt::lift(tile[t * B + j]));
+        const float f = 1.0f / (float)acc.c;  // basics.mojo:609
+        sm[t] = acc.m;
+        sg[t] = f * ug[(int64_t)blockIdx.x * kRThreads + t];
+    }
+    __syncthreads();
+    const int cnt = (int)(rows * B);
+    const int nq = cnt >> 2;
+    float4* g4 = reinterpret_cast<float4*>(grad + base);
+    for (int i = t; i < nq; i += kRThreads) {
+        float4 g = g4[i];
+        float r[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = 4 * i + j;
+            const int row = (int)fdiv((uint32_t)e, fdB);
+            r[j] = tile[e] == sm[row] ? sg[row] : 0.0f;
+        }
+        g.x = g.x + r[0];
+        g.y = g.y + r[1];
+        g.z = g.z + r[2];
+        g.w = g.w + r[3];
+        g4[i] = g;
+    }
+    for (int e = (nq << 2) + t; e < cnt; e += kRThreads) {
+        const int row = (int)fdiv((uint32_t)e, fdB);
+        grad[base + e] = grad[base + e] + (tile[e] == sm[row] ? sg[row] : 0.0f);
+    }
+}
+
 // One wavefront per (row, chunk): virtual row vr = r * S + s covers elements
 // [r*B + s*L, r*B + min((s+1)*L, B)). S == 1 writes the epilogue, S > 1 writes partials.
 template <class R, class LD, bool VEC>
@@ -256,7 +339,7 @@ struct RowSplit {
 };
 static RowSplit row_split(int64_t A, int64_t B) {
     RowSplit rs{1, B};
-    const int64_t target = 8 * (int64_t)ctx().num_cus;  // wavefronts wanted in flight
+    const int64_t target = 32 * (int64_t)ctx().num_cus;  // wavefronts wanted in flight
     if (A < target && B >= 8192) {
         int64_t S = (target + A - 1) / A;
         int64_t L = (B + S - 1) / S;
@@ -334,6 +417,18 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
     hipStream_t st = ctx().stream;
     if (C == 1) {
         if (B <= 64) {
+            if constexpr (std::is_same<LD, LdPlain<R>>::value) {
+                if (B <= 32 && vec_ok && A <= ((int64_t)1 << 40)) {
+                    const unsigned blocks = (unsigned)((A + kRThreads - 1) / kRThreads);
+                    if (B <= 16)
+                        hipLaunchKernelGGL((k_rows_lds<R, 16>), dim3(blocks), dim3(kRThreads), 0, st, ld.x, A,
+                                           (int)B, out, out2, epi, div);
+                    else
+                        hipLaunchKernelGGL((k_rows_lds<R, 32>), dim3(blocks), dim3(kRThreads), 0, st, ld.x, A,
+                                           (int)B, out, out2, epi, div);
+                    return MH_OK;
+                }
+            }
             int64_t blocks = (A + kRThreads - 1) / kRThreads;
             if (blocks > 65536) blocks = 65536;
             hipLaunchKernelGGL((k_rows_thread<R, LD>), dim3((unsigned)blocks), dim3(kRThreads), 0, st, ld, A,
@@ -559,6 +654,16 @@ int mh_reduce_bwd_accum(int op, float* grad, const float* x, mh_shape sx, const 
         } else {  // basics.mojo:489-506
             MH_TRY(map_scale_bcast(grad, sx, ug, sug, (float)(1.0 / (double)B), shape_eq(sx, sug)));
         }
+    } else if (C == 1 && B >= 1 && B <= 32 && A <= ((int64_t)1 << 40) && al16(x) && al16(grad)) {
+        // MAX over short last-axis rows: one pass (max, count and routing per LDS tile)
+        const unsigned blocks = (unsigned)((A + kRThreads - 1) / kRThreads);
+        const FastDiv fdB = make_fastdiv((uint32_t)B);
+        if (B <= 16)
+            hipLaunchKernelGGL(k_max_bwd_rows<16>, dim3(blocks), dim3(kRThreads), 0, ctx().stream, grad, x, ug, A,
+                               (int)B, fdB);
+        else
+            hipLaunchKernelGGL(k_max_bwd_rows<32>, dim3(blocks), dim3(kRThreads), 0, ctx().stream, grad, x, ug, A,
+                               (int)B, fdB);
     } else {  // MAX, basics.mojo:536-615: line max and fl(1/count), then routing
         const int64_t nl = A * C;
         const size_t pad_nl = ((size_t)nl + 63) & ~(size_t)63;

@@ -423,8 +423,8 @@ int mh_memcpy_d2d(void* dst, const void* src, size_t bytes) {
     MH_TRY(require_init());
     if (((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) | bytes) & 15) == 0) {
         int64_t nq = (int64_t)(bytes >> 4);
-        int64_t blocks = (nq + 255) / 256;
-        if (blocks > 65536) blocks = 65536;
+        int64_t blocks = (nq + 255) / 256;  // one quad per thread (the stride loop covers > 2^31 blocks)
+        if (blocks > 0x7fffffff) blocks = 0x7fffffff;
         hipLaunchKernelGGL(k_copy, dim3((unsigned)blocks), dim3(256), 0, ctx().stream,
                            reinterpret_cast<float4*>(dst), reinterpret_cast<const float4*>(src), nq);
     } else {

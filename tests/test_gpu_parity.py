@@ -47,7 +47,9 @@ def test_accumulate_fixture_on_gpu(gpu):
 BIN_SHAPES = [((37, 63, 107), (37, 63, 107)), ((37, 63, 107), (37, 63, 1)), ((37, 63, 1), (37, 63, 107)),
               ((2, 3, 4), (5, 2, 1, 4)), ((1001,), (1,)), ((1,), (1001,)), ((32, 32), (1, 32)),
               ((4, 32, 7, 7), (1, 32, 1, 1)), ((4099, 10), (4099, 1)), ((8, 1, 5), (1, 6, 1)),
-              ((3,), (3,)), ((1,), (1,)), ((7, 5), (5,)), ((2, 1, 3, 1, 5), (1, 4, 3, 6, 1))]
+              ((3,), (3,)), ((1,), (1,)), ((7, 5), (5,)), ((2, 1, 3, 1, 5), (1, 4, 3, 6, 1)),
+              ((5, 3), (5, 1)), ((7, 2), (1, 2)), ((9, 1, 3), (9, 4, 1)), ((1023, 6), (1023, 1)),
+              ((65, 4), (65, 1))]
 
 
 def _binary_inputs(sa, sb, seed):
@@ -148,7 +150,9 @@ def test_pow_parity(gpu, e):
 # ---------------------------------------------------------------------------------------
 RED_CASES = [((87, 73, 107), 0), ((87, 73, 107), 1), ((87, 73, 107), 2), ((87, 73, 107), None),
              ((1024, 1024), 0), ((1024, 1024), 1), ((64, 512, 1024), 2), ((4099, 10), 1), ((3, 1, 5), 1),
-             ((1,), None), ((5,), 0), ((2, 70000), 1), ((70000, 3), 0), ((1 << 22,), None), ((6, 33, 2), 1)]
+             ((1,), None), ((5,), 0), ((2, 70000), 1), ((70000, 3), 0), ((1 << 22,), None), ((6, 33, 2), 1),
+             ((1000, 20), 1), ((513, 32), 1), ((1001, 3), 1), ((300, 1), 1), ((257, 16), 1), ((40, 33), 1),
+             ((30,), None), ((2, 3, 17), 2)]
 
 
 @pytest.mark.parametrize("shape,axis", RED_CASES, ids=[f"{s}-ax{a}" for s, a in RED_CASES])
