@@ -468,47 +468,64 @@ def cpu_baseline(n_sample: int, reps: int, expo: float):
 # rocprofv3 summaries
 # ---------------------------------------------------------------------------------------
 def _read_pmc_csv(path, counter):
-    """{kernel name: [counter value per dispatch]} from a rocprofv3 --pmc counter_collection.csv."""
+    """{kernel name: {grid size: [counter value per dispatch]}} from a rocprofv3 --pmc
+    counter_collection.csv."""
     out = {}
     with open(path, newline="") as f:
         for row in csv.DictReader(f):
             if row.get("Counter_Name") != counter:
                 continue
-            out.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+            out.setdefault(row["Kernel_Name"], {}).setdefault(int(row["Grid_Size"]), []).append(
+                float(row["Counter_Value"]))
     return out
 
 
 def pmc_summary(fetch_csv, write_csv, copy_bytes=8 << 28):
     """Writes profiles/traffic.json: HBM bytes per dispatch of each kernel, from FETCH_SIZE
     and WRITE_SIZE (KiB per dispatch), each scaled by the factor that makes the library's
-    copy kernel (k_copy, `copy_bytes / 2` read and written) read exactly its size."""
+    copy kernel (k_copy over `copy_bytes / 2` read and as many written) count exactly its
+    bytes. Per kernel, dispatches are grouped by grid size (median per group); `hbm_bytes`
+    is the largest launch, which for the config-2 kernels is the 2^28-element one."""
     fetch, write = _read_pmc_csv(fetch_csv, "FETCH_SIZE"), _read_pmc_csv(write_csv, "WRITE_SIZE")
     copy_k = [k for k in fetch if "k_copy" in k]
     if not copy_k:
         raise SystemExit("no k_copy dispatch in the FETCH_SIZE run: run the 'copy' workload under rocprofv3")
     half = copy_bytes / 2
-    f_scale = half / (statistics.median(fetch[copy_k[0]]) * 1024)
-    w_scale = half / (statistics.median(write[copy_k[0]]) * 1024)
+    cf, cw = fetch[copy_k[0]], write[copy_k[0]]
+    f_scale = half / (statistics.median(cf[max(cf)]) * 1024)
+    w_scale = half / (statistics.median(cw[max(cw)]) * 1024)
     kernels = {}
     for k in sorted(set(fetch) | set(write)):
-        fv = statistics.median(fetch[k]) * 1024 * f_scale if k in fetch else None
-        wv = statistics.median(write[k]) * 1024 * w_scale if k in write else None
-        kernels[k] = {"fetch_bytes": fv, "write_bytes": wv,
-                      "hbm_bytes": (fv or 0) + (wv or 0), "dispatches": len(fetch.get(k, []))}
+        grids = sorted(set(fetch.get(k, {})) | set(write.get(k, {})))
+        by_grid = {}
+        for g in grids:
+            fv = statistics.median(fetch[k][g]) * 1024 * f_scale if g in fetch.get(k, {}) else None
+            wv = statistics.median(write[k][g]) * 1024 * w_scale if g in write.get(k, {}) else None
+            by_grid[str(g)] = {"fetch_bytes": None if fv is None else round(fv),
+                               "write_bytes": None if wv is None else round(wv),
+                               "hbm_bytes": round((fv or 0) + (wv or 0))}
+        top = by_grid[str(grids[-1])]
+        kernels[k] = {"largest_grid": grids[-1], "fetch_bytes": top["fetch_bytes"], "write_bytes": top["write_bytes"],
+                      "hbm_bytes": top["hbm_bytes"], "by_grid": by_grid}
     summary = {"fetch_scale": f_scale, "write_scale": w_scale, "copy_kernel": copy_k[0], "kernels": kernels}
     os.makedirs(os.path.dirname(TRAFFIC_JSON), exist_ok=True)
     with open(TRAFFIC_JSON, "w") as f:
-        json.dump(summary, f, indent=1, sort_keys=True)
+        json.dump(summary, f, indent=0, sort_keys=True)
     return summary
 
 
-# label of a config-2 op -> substring of its kernel's name
-C2_KERNEL = {"ADD.bwd": "k_bwd2_same4<0>", "SUB.bwd": "k_bwd2_same4<1>", "MUL.bwd": "k_bwd2_same4<2>",
-             "DIV.bwd": "k_bwd2_same4<3>", "ADD.fwd": "FBin<0>", "SUB.fwd": "FBin<1>", "MUL.fwd": "FBin<2>",
-             "DIV.fwd": "FBin<3>", "EXP.fwd": "FUn<4>", "LOG.fwd": "FUn<5>", "SIGMOID.fwd": "FUn<13>",
-             "RELU.fwd": "FUn<14>", "TANH.fwd": "FUn<15>", "EXP.bwd": "FUnBwd<4>", "LOG.bwd": "FUnBwd<5>",
-             "SIGMOID.bwd": "FUnBwd<13>", "RELU.bwd": "FUnBwd<14>", "TANH.bwd": "FUnBwd<15>",
-             "POW.fwd": "FPowi", "POW.bwd_x": "FPowBwdX", "POW.bwd_exp": "LdPowGrad"}
+# label of a config-2 op -> prefix of its kernel's name (the 2^28-element launch)
+C2_KERNEL = {"ADD.bwd": "void mh::k_bwd2_same4<0>", "SUB.bwd": "void mh::k_bwd2_same4<1>",
+             "MUL.bwd": "void mh::k_bwd2_same4<2>", "DIV.bwd": "void mh::k_bwd2_same4<3>",
+             "ADD.fwd": "void mh::k_same4<mh::FBin<0>,", "SUB.fwd": "void mh::k_same4<mh::FBin<1>,",
+             "MUL.fwd": "void mh::k_same4<mh::FBin<2>,", "DIV.fwd": "void mh::k_same4<mh::FBin<3>,",
+             "EXP.fwd": "void mh::k_same4<mh::FUn<4>,", "LOG.fwd": "void mh::k_same4<mh::FUn<5>,",
+             "SIGMOID.fwd": "void mh::k_same4<mh::FUn<13>,", "RELU.fwd": "void mh::k_same4<mh::FUn<14>,",
+             "TANH.fwd": "void mh::k_same4<mh::FUn<15>,", "EXP.bwd": "void mh::k_same4<mh::FUnBwd<4>,",
+             "LOG.bwd": "void mh::k_same4<mh::FUnBwd<5>,", "SIGMOID.bwd": "void mh::k_same4<mh::FUnBwd<13>,",
+             "RELU.bwd": "void mh::k_same4<mh::FUnBwd<14>,", "TANH.bwd": "void mh::k_same4<mh::FUnBwd<15>,",
+             "POW.fwd": "void mh::k_same4<mh::FPowi,", "POW.bwd_x": "void mh::k_same4<mh::FPowBwdX,",
+             "POW.bwd_exp": "void mh::k_rows_wave<mh::RSum, mh::LdPowGrad,"}
 
 
 def traffic_for(label):
@@ -517,7 +534,7 @@ def traffic_for(label):
     with open(TRAFFIC_JSON) as f:
         kernels = json.load(f)["kernels"]
     key = C2_KERNEL.get(label)
-    hits = [v for k, v in kernels.items() if key and key in k]
+    hits = [v for k, v in kernels.items() if key and k.startswith(key)]
     return round(hits[0]["hbm_bytes"]) if len(hits) == 1 else None
 
 

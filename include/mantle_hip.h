@@ -12,8 +12,10 @@
  *   - Plain C types only; no exceptions cross the ABI. Every int-returning call returns
  *     MH_OK (0) or a negative mh_status; mh_last_error() gives a thread-local message.
  *   - Tensors are fp32, row-major contiguous, rank 1..8 (mantle/core/tensor.mojo:20-155),
- *     described by mh_shape. Tensor pointers are device pointers from mh_malloc (or any
- *     device allocation on the initialised device). The library never frees caller memory.
+ *     described by an mh_shape passed by pointer (const mh_shape*, read during the call
+ *     only), so that any FFI can pass it without struct-by-value rules. Tensor pointers
+ *     are device pointers from mh_malloc (or any device allocation on the initialised
+ *     device). The library never frees caller memory.
  *   - Shapes are validated before any device work: a pair that does not broadcast (which
  *     the reference only prints about, tensorutils.mojo:116-122), rank outside 1..8, a
  *     negative dim or a null tensor pointer returns an error and launches nothing.
@@ -90,8 +92,8 @@ int mh_fill(float* t, float v, int64_t n);
  * (same shape :277-290, tensor-scalar :293-304, scalar-tensor :307-318,
  * broadcast_elwise_op :321-357) as called by ADD/SUB/MUL/DIV.forward
  * (basics.mojo:36-43, 66-73, 102-109, 140-147). sres must equal broadcast(sa, sb). */
-int mh_binary_fwd(int op, float* res, mh_shape sres, const float* a, mh_shape sa,
-                  const float* b, mh_shape sb);
+int mh_binary_fwd(int op, float* res, const mh_shape* sres, const float* a, const mh_shape* sa,
+                  const float* b, const mh_shape* sb);
 
 /* EXP/LOG/SIGMOID/RELU/TANH forward: elwise_transform, tensorutils.mojo:181-200, with the
  * functions of EXP.forward (basics.mojo:266-270), LOG.forward (:294-298),
@@ -107,7 +109,7 @@ int mh_pow_fwd(float* res, const float* x, int64_t n, const float* exponent);
  * MAX.forward (:521-534) -> reduce all (tensorutils.mojo:564-598, tsum/tmean/tmax
  * :694-720, :850-862) or reduce axis (:622-684, :746-772, :865-876). axis = -1 reduces all
  * elements into res[0]; otherwise res has get_reduce_shape(sx, axis) (:601-619). */
-int mh_reduce_fwd(int op, float* res, const float* x, mh_shape sx, int32_t axis);
+int mh_reduce_fwd(int op, float* res, const float* x, const mh_shape* sx, int32_t axis);
 
 /* ---- backward (accumulating) ---- */
 
@@ -116,16 +118,16 @@ int mh_reduce_fwd(int op, float* res, const float* x, mh_shape sx, int32_t axis)
  * by accumulate_grad[grad_shape = s_k, res_grad_shape = broadcast(s1, s2)]
  * (tensorutils.mojo:454-487), i.e. un-broadcast by summation when the operand was
  * broadcast. sug must equal broadcast(s1, s2); sgrad must equal s1 (id 0) or s2 (id 1). */
-int mh_binary_bwd_accum(int op, int tensor_id, float* grad, mh_shape sgrad,
-                        const float* ug, mh_shape sug, const float* t1, mh_shape s1,
-                        const float* t2, mh_shape s2);
+int mh_binary_bwd_accum(int op, int tensor_id, float* grad, const mh_shape* sgrad,
+                        const float* ug, const mh_shape* sug, const float* t1, const mh_shape* s1,
+                        const float* t2, const mh_shape* s2);
 
 /* Both operand gradients of a same-shape ADD/SUB/MUL/DIV in one pass (the two
  * backward_op calls that Model.backward makes when both operands are trainable,
  * model.mojo:233-270). Requires s1 == s2 == sug; either grad pointer may be NULL to skip
  * that operand. */
 int mh_binary_bwd_accum2(int op, float* grad1, float* grad2, const float* ug,
-                         const float* t1, const float* t2, mh_shape s);
+                         const float* t1, const float* t2, const mh_shape* s);
 
 /* backward_op for EXP/LOG/SIGMOID/RELU/TANH (ops.mojo:355-405): EXP.backward
  * (basics.mojo:272-285), LOG.backward (:300-309), SIGMOID.backward (mlops.mojo:50-76),
@@ -143,14 +145,14 @@ int mh_pow_bwd_accum(int tensor_id, float* grad, const float* x, const float* ex
 /* backward_op for SUM/MEAN/MAX (ops.mojo:355-405): SUM.backward (basics.mojo:408-425),
  * MEAN.backward (:454-506), MAX.backward (:536-615, ties split as fl(1/count) * ug),
  * then the same-shape accumulate_grad. ug has the reduced shape (axis >= 0) or (1). */
-int mh_reduce_bwd_accum(int op, float* grad, const float* x, mh_shape sx, const float* ug,
+int mh_reduce_bwd_accum(int op, float* grad, const float* x, const mh_shape* sx, const float* ug,
                         int32_t axis);
 
 /* accumulate_grad, tensorutils.mojo:442-487: grad += rg for equal shapes, grad += rg[0]
  * for rg of shape (1), otherwise grad += un-broadcast(rg) (sum over the broadcast axes).
  * Pairs that are not numpy-broadcastable (which the reference indexes out of bounds with,
  * tensorutils.mojo:149-175 and :482-484) return MH_ERR_SHAPE. */
-int mh_accumulate_grad(float* grad, mh_shape sgrad, const float* rg, mh_shape srg);
+int mh_accumulate_grad(float* grad, const mh_shape* sgrad, const float* rg, const mh_shape* srg);
 
 /* ---- fused graph-level entry points (no single reference counterpart) ---- */
 
@@ -158,15 +160,15 @@ int mh_accumulate_grad(float* grad, mh_shape sgrad, const float* rg, mh_shape sr
  * r = RELU(y) in one pass, the two forward_op calls of a graph ADD -> RELU
  * (ADD.forward basics.mojo:36-43, RELU.forward mlops.mojo:92-97). Writes both y (needed
  * by RELU's backward) and r. sbias must broadcast to sx. */
-int mh_bias_relu_fwd(float* y, float* r, const float* x, mh_shape sx, const float* bias,
-                     mh_shape sbias);
+int mh_bias_relu_fwd(float* y, float* r, const float* x, const mh_shape* sx, const float* bias,
+                     const mh_shape* sbias);
 
 /* Backward of the same graph: g_y = g_y + relu'(y) * ug (RELU backward_op), then both
  * ADD backward_op calls: grad_x += g_y and grad_bias += un-broadcast(g_y). g_y may be NULL
  * when the graph's grad of y starts at zero and is not needed afterwards; then the sum
  * uses relu'(y) * ug directly. grad_x or grad_bias may be NULL to skip that operand. */
 int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const float* y,
-                           const float* ug, mh_shape sx, mh_shape sbias);
+                           const float* ug, const mh_shape* sx, const mh_shape* sbias);
 
 /* Seeded synthetic fill (the device counterpart of rand_uniform / rand_normal,
  * mantle/core/rand_utils.mojo:23-63): element i of stream `seed` comes from a counter-based
@@ -192,7 +194,7 @@ typedef struct {
     int64_t stride_a[MH_MAX_RANK];
     int64_t stride_b[MH_MAX_RANK];
 } mh_plan_info;
-int mh_plan_binary(mh_shape sres, mh_shape sa, mh_shape sb, mh_plan_info* out);
+int mh_plan_binary(const mh_shape* sres, const mh_shape* sa, const mh_shape* sb, mh_plan_info* out);
 
 /* The chain of single-axis reductions that un-broadcasting rg into grad runs: the number
  * of steps and, per step, the [A, B, C] view reduced over B. Host-only. */
@@ -202,7 +204,7 @@ typedef struct {
     int64_t b[MH_MAX_RANK];
     int64_t c[MH_MAX_RANK];
 } mh_reduce_plan_info;
-int mh_plan_unbroadcast(mh_shape sgrad, mh_shape srg, mh_reduce_plan_info* out);
+int mh_plan_unbroadcast(const mh_shape* sgrad, const mh_shape* srg, mh_reduce_plan_info* out);
 
 #ifdef __cplusplus
 }

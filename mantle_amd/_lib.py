@@ -60,7 +60,7 @@ _VP = ctypes.c_void_p
 _I = ctypes.c_int
 _I64 = ctypes.c_int64
 _F = ctypes.c_float
-_S = mh_shape
+_S = ctypes.POINTER(mh_shape)  # shapes cross the ABI by pointer (ctypes passes an mh_shape byref)
 
 # name -> argtypes (all return int unless listed in _RESTYPE)
 SIGNATURES = {

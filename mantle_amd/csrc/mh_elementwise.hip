@@ -591,8 +591,11 @@ using namespace mh;
 
 extern "C" {
 
-int mh_binary_fwd(int op, float* res, mh_shape sres, const float* a, mh_shape sa, const float* b,
-                  mh_shape sb) {
+int mh_binary_fwd(int op, float* res, const mh_shape* psres, const float* a, const mh_shape* psa,
+                  const float* b, const mh_shape* psb) {
+    MH_SHAPE_ARG(sres);
+    MH_SHAPE_ARG(sa);
+    MH_SHAPE_ARG(sb);
     MH_TRY(check_op_binary(op));
     MH_TRY(check_shape(sres, "res"));
     MH_TRY(check_shape(sa, "a"));
@@ -687,8 +690,13 @@ int mh_pow_bwd_accum(int tensor_id, float* grad, const float* x, const float* ex
     return finish("mh_pow_bwd_accum");
 }
 
-int mh_binary_bwd_accum(int op, int tensor_id, float* grad, mh_shape sgrad, const float* ug,
-                        mh_shape sug, const float* t1, mh_shape s1, const float* t2, mh_shape s2) {
+int mh_binary_bwd_accum(int op, int tensor_id, float* grad, const mh_shape* psgrad, const float* ug,
+                        const mh_shape* psug, const float* t1, const mh_shape* ps1, const float* t2,
+                        const mh_shape* ps2) {
+    MH_SHAPE_ARG(sgrad);
+    MH_SHAPE_ARG(sug);
+    MH_SHAPE_ARG(s1);
+    MH_SHAPE_ARG(s2);
     MH_TRY(check_op_binary(op));
     if (tensor_id != 0 && tensor_id != 1) return fail(MH_ERR_INVALID, "mh_binary_bwd_accum: tensor_id %d", tensor_id);
     MH_TRY(check_shape(sgrad, "grad"));
@@ -730,15 +738,16 @@ int mh_binary_bwd_accum(int op, int tensor_id, float* grad, mh_shape sgrad, cons
 }
 
 int mh_binary_bwd_accum2(int op, float* grad1, float* grad2, const float* ug, const float* t1,
-                         const float* t2, mh_shape s) {
+                         const float* t2, const mh_shape* ps) {
+    MH_SHAPE_ARG(s);
     MH_TRY(check_op_binary(op));
     MH_TRY(check_shape(s, "shape"));
     if (!grad1 && !grad2) return MH_OK;
     if (!grad1 || !grad2 || is_scalar_shape(s) || numel(s) == 0 ||
         !(aligned16(grad1) && aligned16(grad2) && aligned16(ug) && aligned16(t1) && aligned16(t2))) {
         // one operand, a graph scalar (DIV's scalar rule), empty or unaligned: per operand
-        if (grad1) MH_TRY(mh_binary_bwd_accum(op, 0, grad1, s, ug, s, t1, s, t2, s));
-        if (grad2) MH_TRY(mh_binary_bwd_accum(op, 1, grad2, s, ug, s, t1, s, t2, s));
+        if (grad1) MH_TRY(mh_binary_bwd_accum(op, 0, grad1, &s, ug, &s, t1, &s, t2, &s));
+        if (grad2) MH_TRY(mh_binary_bwd_accum(op, 1, grad2, &s, ug, &s, t1, &s, t2, &s));
         return MH_OK;
     }
     const bool need_ab = op == MH_MUL || op == MH_DIV;
@@ -756,7 +765,9 @@ int mh_binary_bwd_accum2(int op, float* grad1, float* grad2, const float* ug, co
     return finish("mh_binary_bwd_accum2");
 }
 
-int mh_accumulate_grad(float* grad, mh_shape sgrad, const float* rg, mh_shape srg) {
+int mh_accumulate_grad(float* grad, const mh_shape* psgrad, const float* rg, const mh_shape* psrg) {
+    MH_SHAPE_ARG(sgrad);
+    MH_SHAPE_ARG(srg);
     MH_TRY(check_shape(sgrad, "grad"));
     MH_TRY(check_shape(srg, "rg"));
     const bool same = shape_eq(sgrad, srg);

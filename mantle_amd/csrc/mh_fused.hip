@@ -7,7 +7,10 @@ using namespace mh;
 
 extern "C" {
 
-int mh_bias_relu_fwd(float* y, float* r, const float* x, mh_shape sx, const float* bias, mh_shape sbias) {
+int mh_bias_relu_fwd(float* y, float* r, const float* x, const mh_shape* psx, const float* bias,
+                     const mh_shape* psbias) {
+    MH_SHAPE_ARG(sx);
+    MH_SHAPE_ARG(sbias);
     MH_TRY(check_shape(sx, "x"));
     MH_TRY(check_shape(sbias, "bias"));
     mh_shape bs;
@@ -16,12 +19,14 @@ int mh_bias_relu_fwd(float* y, float* r, const float* x, mh_shape sx, const floa
     const int64_t n = numel(sx);
     if (n == 0) return MH_OK;
     if (!y || !r || !x || !bias) return fail(MH_ERR_NULL, "mh_bias_relu_fwd: null tensor");
-    MH_TRY(mh_binary_fwd(MH_ADD, y, sx, x, sx, bias, sbias));  // ADD.forward
+    MH_TRY(mh_binary_fwd(MH_ADD, y, &sx, x, &sx, bias, &sbias));  // ADD.forward
     return mh_unary_fwd(MH_RELU, r, y, n);                     // RELU.forward
 }
 
 int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const float* y, const float* ug,
-                           mh_shape sx, mh_shape sbias) {
+                           const mh_shape* psx, const mh_shape* psbias) {
+    MH_SHAPE_ARG(sx);
+    MH_SHAPE_ARG(sbias);
     MH_TRY(check_shape(sx, "x"));
     MH_TRY(check_shape(sbias, "bias"));
     mh_shape bs;
@@ -37,8 +42,8 @@ int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const fl
         MH_TRY(mh_zero(gy, n));
     }
     MH_TRY(mh_unary_bwd_accum(MH_RELU, gy, y, ug, n));  // RELU backward_op
-    if (grad_x) MH_TRY(mh_binary_bwd_accum(MH_ADD, 0, grad_x, sx, gy, sx, y, sx, y, sbias));
-    if (grad_bias) MH_TRY(mh_binary_bwd_accum(MH_ADD, 1, grad_bias, sbias, gy, sx, y, sx, y, sbias));
+    if (grad_x) MH_TRY(mh_binary_bwd_accum(MH_ADD, 0, grad_x, &sx, gy, &sx, y, &sx, y, &sbias));
+    if (grad_bias) MH_TRY(mh_binary_bwd_accum(MH_ADD, 1, grad_bias, &sbias, gy, &sx, y, &sx, y, &sbias));
     return MH_OK;
 }
 

@@ -43,6 +43,12 @@ int hip_check(hipError_t e, const char* what);
         if (rc__ != MH_OK) return rc__; \
     } while (0)
 
+// Copies the shape argument `p<name>` (a const mh_shape* of the C ABI) into a local
+// `name`, rejecting a null pointer.
+#define MH_SHAPE_ARG(name)                                                                  \
+    if (!p##name) return ::mh::fail(MH_ERR_NULL, "%s: null shape argument " #name, __func__); \
+    const mh_shape name = *p##name
+
 int require_init();
 // End of an entry point: checks the launch and synchronises unless MH_INIT_ASYNC.
 int finish(const char* what);

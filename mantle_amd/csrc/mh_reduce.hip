@@ -620,7 +620,8 @@ using namespace mh;
 
 extern "C" {
 
-int mh_reduce_fwd(int op, float* res, const float* x, mh_shape sx, int32_t axis) {
+int mh_reduce_fwd(int op, float* res, const float* x, const mh_shape* psx, int32_t axis) {
+    MH_SHAPE_ARG(sx);
     MH_TRY(check_reduce_args(op, sx, axis));
     int64_t A, B, C;
     abc_of(sx, axis, &A, &B, &C);
@@ -637,7 +638,9 @@ int mh_reduce_fwd(int op, float* res, const float* x, mh_shape sx, int32_t axis)
     return finish("mh_reduce_fwd");
 }
 
-int mh_reduce_bwd_accum(int op, float* grad, const float* x, mh_shape sx, const float* ug, int32_t axis) {
+int mh_reduce_bwd_accum(int op, float* grad, const float* x, const mh_shape* psx, const float* ug,
+                        int32_t axis) {
+    MH_SHAPE_ARG(sx);
     MH_TRY(check_reduce_args(op, sx, axis));
     const int64_t n = numel(sx);
     if (n == 0) return MH_OK;

@@ -490,7 +490,10 @@ int mh_event_elapsed_ms(float* ms, void* start, void* stop) {
     return MH_OK;
 }
 
-int mh_plan_binary(mh_shape sres, mh_shape sa, mh_shape sb, mh_plan_info* out) {
+int mh_plan_binary(const mh_shape* psres, const mh_shape* psa, const mh_shape* psb, mh_plan_info* out) {
+    MH_SHAPE_ARG(sres);
+    MH_SHAPE_ARG(sa);
+    MH_SHAPE_ARG(sb);
     if (!out) return fail(MH_ERR_NULL, "mh_plan_binary: null");
     MH_TRY(check_shape(sres, "res"));
     MH_TRY(check_shape(sa, "a"));
@@ -515,7 +518,9 @@ int mh_plan_binary(mh_shape sres, mh_shape sa, mh_shape sb, mh_plan_info* out) {
     return MH_OK;
 }
 
-int mh_plan_unbroadcast(mh_shape sgrad, mh_shape srg, mh_reduce_plan_info* out) {
+int mh_plan_unbroadcast(const mh_shape* psgrad, const mh_shape* psrg, mh_reduce_plan_info* out) {
+    MH_SHAPE_ARG(sgrad);
+    MH_SHAPE_ARG(srg);
     if (!out) return fail(MH_ERR_NULL, "mh_plan_unbroadcast: null");
     MH_TRY(check_shape(sgrad, "grad"));
     MH_TRY(check_shape(srg, "rg"));

@@ -12,7 +12,7 @@
  * kept exactly (built with -ffp-contract=off; fmaf only where the restated algorithm uses
  * a fused multiply-add).
  *
- * Pinning status (what checks each function; see tests/test_oracle_*.py):
+ * Pinning status (what checks each function; see tests/test_oracle.py):
  *   - closed-form single-IEEE-op functions (add/sub/mul/div, relu, max, broadcast index
  *     math, accumulate, tie routing): reference fixtures from the tests/mojo test files plus
  *     brute-force checks against numpy on small inputs;

@@ -70,6 +70,11 @@ def test_shape_errors_before_device_work():
     # null tensors on non-empty work
     assert L.mh_binary_fwd(0, None, S((3,)), None, S((3,)), None, S((3,))) == _lib.ERR_NULL
     assert L.mh_unary_fwd(4, None, None, 5) == _lib.ERR_NULL
+    # shapes cross the ABI by pointer: a null shape pointer is an error, not a crash
+    assert L.mh_binary_fwd(0, None, None, None, S((3,)), None, S((3,))) == _lib.ERR_NULL
+    assert b"null shape" in L.mh_last_error()
+    assert L.mh_reduce_fwd(8, None, None, None, -1) == _lib.ERR_NULL
+    assert L.mh_accumulate_grad(None, S((3,)), None, None) == _lib.ERR_NULL
     # empty work is a no-op
     assert L.mh_binary_fwd(0, None, S((0, 3)), None, S((0, 3)), None, S((1,))) == _lib.OK
     assert L.mh_unary_fwd(4, None, None, 0) == _lib.OK
