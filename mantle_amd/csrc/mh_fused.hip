@@ -1,7 +1,164 @@
 // mh_fused.hip -- graph-level entry points that cover several forward_op / backward_op
 // calls of one graph pattern: bias ADD followed by RELU (a Linear layer's bias + activation,
 // or an NCHW per-channel bias).
+//
+// Forward: one pass reads x (and the small bias) and writes y = x + bias and r = relu(y):
+// 12 B per element instead of the 16 B of two separate ops.
+// Backward: with x viewed as [N, C, S] and the bias indexed by C alone (NCHW bias
+// [1, C, 1, 1], or any bias that is constant over a contiguous inner run S), one block per
+// (plane, chunk) computes gy = g_y + relu'(y) * ug, accumulates it into grad_x (and g_y when
+// the caller keeps it), and writes the chunk's sum of gy; a second pass adds those partials
+// into grad_bias in a fixed order. Shapes outside that form run the op-by-op kernels.
 #include "mh_internal.h"
+#include "mh_math.h"
+
+namespace mh {
+
+constexpr int kFThreads = 256;
+
+static inline bool al16f(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// y = x + bias (ADD.forward, basics.mojo:36-43), r = relu(y) (RELU.forward, mlops.mojo:92-97).
+// Plan inputs: 0 = x (FULL), 1 = bias (BCAST, SCALAR or FULL). y, r, x 16-byte aligned.
+template <bool INNER4, bool BIG>
+__global__ void __launch_bounds__(kFThreads)
+    k_bias_relu_fwd4(float* __restrict__ y, float* __restrict__ r, const float* __restrict__ x,
+                     const float* __restrict__ bias, ElwPlan pl) {
+    const int inner = pl.rank - 1;
+    const int64_t dinner = pl.dims[inner];
+    const int kb = pl.kind[1];
+    const float sb = kb == IN_SCALAR ? bias[0] : 0.0f;
+    const int64_t nq = pl.n >> 2;
+    const int64_t stride = (int64_t)gridDim.x * kFThreads;
+    for (int64_t q = (int64_t)blockIdx.x * kFThreads + threadIdx.x; q < nq; q += stride) {
+        const int64_t idx = q * 4;
+        float bv[4];
+        if (kb == IN_SCALAR) {
+            bv[0] = bv[1] = bv[2] = bv[3] = sb;
+        } else if (kb == IN_FULL) {
+            const float4 t = reinterpret_cast<const float4*>(bias)[q];
+            bv[0] = t.x; bv[1] = t.y; bv[2] = t.z; bv[3] = t.w;
+        } else {
+            int64_t off[4][2];
+            int64_t cin = 0;
+            bcast_decode<2, BIG>(pl, idx, off[0], &cin);
+            if (INNER4) {
+                if (pl.st[1][inner] == 1) {
+                    const float4 t = *reinterpret_cast<const float4*>(bias + off[0][1]);
+                    bv[0] = t.x; bv[1] = t.y; bv[2] = t.z; bv[3] = t.w;
+                } else {
+                    bv[0] = bv[1] = bv[2] = bv[3] = bias[off[0][1]];
+                }
+            } else {
+                bv[0] = bias[off[0][1]];
+#pragma unroll
+                for (int j = 1; j < 4; ++j) {
+                    if (cin + j < dinner) {
+                        bv[j] = bias[off[0][1] + j * pl.st[1][inner]];
+                    } else {
+                        int64_t c2;
+                        bcast_decode<2, BIG>(pl, idx + j, off[j], &c2);
+                        bv[j] = bias[off[j][1]];
+                    }
+                }
+            }
+        }
+        const float4 xv = reinterpret_cast<const float4*>(x)[q];
+        float yv[4], rv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            yv[j] = comp(xv, j) + bv[j];
+            rv[j] = mrelu(yv[j]);
+        }
+        reinterpret_cast<float4*>(y)[q] = make_float4(yv[0], yv[1], yv[2], yv[3]);
+        reinterpret_cast<float4*>(r)[q] = make_float4(rv[0], rv[1], rv[2], rv[3]);
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        for (int64_t i = nq << 2; i < pl.n; ++i) {
+            int64_t off1[2], c;
+            bcast_decode<2, BIG>(pl, i, off1, &c);
+            const float b = kb == IN_SCALAR ? sb : (kb == IN_FULL ? bias[i] : bias[off1[1]]);
+            const float yy = x[i] + b;
+            y[i] = yy;
+            r[i] = mrelu(yy);
+        }
+    }
+}
+
+__device__ __forceinline__ float block_sum256(float v, float* ws) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) ws[wave] = v;
+    __syncthreads();
+    return ((ws[0] + ws[1]) + ws[2]) + ws[3];
+}
+
+// Backward over [N, C, S] planes, S % 4 == 0; block b covers chunk k = b % K of plane
+// p = b / K (p = n * C + c): quads [k * QC, min((k + 1) * QC, Sq)) of the plane.
+//   rg = (y > 0 ? 1 : 0) * ug            RELU.backward (mlops.mojo:118-123)
+//   g  = g_y + rg  (0 + rg without g_y)  accumulate_grad into the grad of y (ops.mojo:405)
+//   grad_x = grad_x + g                  ADD backward_op, operand 0 (ops.mojo:457-461)
+//   part[(n * K + k) * C + c] = sum of g over the chunk (for ADD's operand-1 un-broadcast)
+template <bool HAS_GY, bool HAS_GX, bool HAS_PART>
+__global__ void __launch_bounds__(kFThreads)
+    k_bias_relu_bwd_planes(float* __restrict__ gy, float* __restrict__ gx, const float* __restrict__ y,
+                           const float* __restrict__ ug, int64_t C, int64_t Sq, int64_t QC, int64_t K,
+                           float* __restrict__ part) {
+    __shared__ float ws[4];
+    const int64_t b = blockIdx.x;
+    const int64_t p = b / K, k = b - p * K;
+    const int64_t q0 = p * Sq + k * QC;
+    const int64_t rem = Sq - k * QC;
+    const int64_t cnt = rem < QC ? rem : QC;
+    float acc = 0.0f;
+    for (int64_t i = threadIdx.x; i < cnt; i += kFThreads) {
+        const int64_t q = q0 + i;
+        const float4 yv = reinterpret_cast<const float4*>(y)[q];
+        const float4 uv = reinterpret_cast<const float4*>(ug)[q];
+        float4 gv = make_float4(0.f, 0.f, 0.f, 0.f), xv = gv;
+        if (HAS_GY) gv = reinterpret_cast<const float4*>(gy)[q];
+        if (HAS_GX) xv = reinterpret_cast<const float4*>(gx)[q];
+        float g[4], o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float rg = (comp(yv, j) > 0.0f ? 1.0f : 0.0f) * comp(uv, j);
+            g[j] = comp(gv, j) + rg;
+            o[j] = comp(xv, j) + g[j];
+        }
+        if (HAS_GY) reinterpret_cast<float4*>(gy)[q] = make_float4(g[0], g[1], g[2], g[3]);
+        if (HAS_GX) reinterpret_cast<float4*>(gx)[q] = make_float4(o[0], o[1], o[2], o[3]);
+        if (HAS_PART) acc = (((acc + g[0]) + g[1]) + g[2]) + g[3];
+    }
+    if (HAS_PART) {
+        const float s = block_sum256(acc, ws);
+        if (threadIdx.x == 0) {
+            const int64_t n = p / C, c = p - n * C;
+            part[(n * K + k) * C + c] = s;
+        }
+    }
+}
+
+// [N, C, S] form of x with the bias indexed by C alone, from the collapsed plan of
+// (x, bias); false when the shapes have another form.
+static bool plane_form(const ElwPlan& pl, int64_t* N, int64_t* C, int64_t* S) {
+    if (pl.kind[1] == IN_SCALAR) {
+        *N = 1; *C = 1; *S = pl.n;
+        return true;
+    }
+    if (pl.kind[1] != IN_BCAST) return false;
+    if (pl.rank == 3 && pl.st[1][0] == 0 && pl.st[1][1] == 1 && pl.st[1][2] == 0) {
+        *N = pl.dims[0]; *C = pl.dims[1]; *S = pl.dims[2];
+        return true;
+    }
+    if (pl.rank == 2 && pl.st[1][0] == 1 && pl.st[1][1] == 0) {
+        *N = 1; *C = pl.dims[0]; *S = pl.dims[1];
+        return true;
+    }
+    return false;
+}
+
+}  // namespace mh
 
 using namespace mh;
 
@@ -19,8 +176,30 @@ int mh_bias_relu_fwd(float* y, float* r, const float* x, const mh_shape* psx, co
     const int64_t n = numel(sx);
     if (n == 0) return MH_OK;
     if (!y || !r || !x || !bias) return fail(MH_ERR_NULL, "mh_bias_relu_fwd: null tensor");
-    MH_TRY(mh_binary_fwd(MH_ADD, y, &sx, x, &sx, bias, &sbias));  // ADD.forward
-    return mh_unary_fwd(MH_RELU, r, y, n);                     // RELU.forward
+    MH_TRY(require_init());
+    mh_shape in[2] = {sx, sbias};
+    ElwPlan pl;
+    MH_TRY(build_elw_plan(sx, 2, in, &pl));
+    const bool al = al16f(y) && al16f(r) && al16f(x) && (pl.kind[1] != IN_FULL || al16f(bias));
+    if (!al) {  // unaligned views: the two forward_op calls
+        MH_TRY(mh_binary_fwd(MH_ADD, y, &sx, x, &sx, bias, &sbias));  // ADD.forward
+        return mh_unary_fwd(MH_RELU, r, y, n);                       // RELU.forward
+    }
+    const bool big = n >= ((int64_t)1 << 31);
+    const bool inner4 = pl.vec_ok && al16f(bias);
+    int64_t blocks = ((n >> 2) + kFThreads - 1) / kFThreads;
+    if (blocks < 1) blocks = 1;
+    if (blocks > 0x7fffffff) blocks = 0x7fffffff;
+    dim3 g((unsigned)blocks), b(kFThreads);
+    hipStream_t st = ctx().stream;
+    if (inner4) {
+        if (big) hipLaunchKernelGGL((k_bias_relu_fwd4<true, true>), g, b, 0, st, y, r, x, bias, pl);
+        else hipLaunchKernelGGL((k_bias_relu_fwd4<true, false>), g, b, 0, st, y, r, x, bias, pl);
+    } else {
+        if (big) hipLaunchKernelGGL((k_bias_relu_fwd4<false, true>), g, b, 0, st, y, r, x, bias, pl);
+        else hipLaunchKernelGGL((k_bias_relu_fwd4<false, false>), g, b, 0, st, y, r, x, bias, pl);
+    }
+    return finish("mh_bias_relu_fwd");
 }
 
 int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const float* y, const float* ug,
@@ -36,6 +215,48 @@ int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const fl
     if (n == 0) return MH_OK;
     if (!y || !ug) return fail(MH_ERR_NULL, "mh_bias_relu_bwd_accum: null tensor");
     MH_TRY(require_init());
+    mh_shape in[2] = {sx, sbias};
+    ElwPlan pl;
+    MH_TRY(build_elw_plan(sx, 2, in, &pl));
+    int64_t N = 0, C = 0, S = 0;
+    const bool al = al16f(y) && al16f(ug) && (!g_y || al16f(g_y)) && (!grad_x || al16f(grad_x));
+    // planes of at least 64 elements (16 quads), so that a block has work for its waves
+    const bool planes = al && plane_form(pl, &N, &C, &S) && S % 4 == 0 && S >= 64;
+    const int64_t Sq = S / 4;
+    const int64_t QC = Sq < 4096 ? Sq : 4096;  // quads per block
+    const int64_t K = planes ? (Sq + QC - 1) / QC : 0;
+    const int64_t nblocks = N * C * K;
+    if (planes && nblocks <= 0x7fffffff) {
+        float* part = nullptr;
+        float* tmp = nullptr;
+        const bool has_part = grad_bias != nullptr;
+        if (has_part) {
+            const size_t np = ((size_t)(N * K * C) + 63) & ~(size_t)63;
+            const size_t t = reduce_abc_tmp_floats(RED_SUM, 1, N * K, C);
+            MH_TRY(scratch((np + t + 64) * sizeof(float), reinterpret_cast<void**>(&part)));
+            tmp = part + np;
+        }
+        hipStream_t st = ctx().stream;
+        dim3 g((unsigned)nblocks), b(kFThreads);
+#define MH_BRB(GY, GX, PT)                                                                                  \
+    hipLaunchKernelGGL((k_bias_relu_bwd_planes<GY, GX, PT>), g, b, 0, st, g_y, grad_x, y, ug, C, Sq, QC, K, part)
+        const int sel = (g_y ? 4 : 0) | (grad_x ? 2 : 0) | (has_part ? 1 : 0);
+        switch (sel) {
+            case 0: return MH_OK;  // nothing to produce
+            case 1: MH_BRB(false, false, true); break;
+            case 2: MH_BRB(false, true, false); break;
+            case 3: MH_BRB(false, true, true); break;
+            case 4: MH_BRB(true, false, false); break;
+            case 5: MH_BRB(true, false, true); break;
+            case 6: MH_BRB(true, true, false); break;
+            default: MH_BRB(true, true, true); break;
+        }
+#undef MH_BRB
+        if (has_part)  // grad_bias[c] += sum over (n, k) of part[(n * K + k) * C + c]
+            MH_TRY(reduce_abc(RED_SUM, EPI_ACCUM, part, 1, N * K, C, grad_bias, nullptr, 0.0f, tmp));
+        return finish("mh_bias_relu_bwd_accum");
+    }
+    // other shapes (a Linear layer's [rows, features] bias, unaligned views): op by op
     float* gy = g_y;
     if (!gy) {  // the grad of y starts at zero: stage it
         MH_TRY(stage((size_t)n * sizeof(float), reinterpret_cast<void**>(&gy)));

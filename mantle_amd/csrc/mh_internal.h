@@ -114,6 +114,41 @@ struct ElwPlan {
 // broadcast to `out`).
 int build_elw_plan(const mh_shape& out, int nin, const mh_shape* in, ElwPlan* plan);
 
+// Component j of a float4.
+__device__ __forceinline__ float comp(const float4& q, int j) {
+    return j == 0 ? q.x : (j == 1 ? q.y : (j == 2 ? q.z : q.w));
+}
+
+// Offsets of the broadcast (IN_BCAST) operands at output element idx, and the element's
+// coordinate along the innermost collapsed dim. BIG: 64-bit division (n >= 2^31).
+template <int NIN, bool BIG>
+__device__ __forceinline__ void bcast_decode(const ElwPlan& pl, int64_t idx, int64_t* off, int64_t* cin) {
+    const int inner = pl.rank - 1;
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) off[k] = 0;
+    int64_t rem = idx;
+#pragma unroll
+    for (int d = MH_MAX_RANK - 1; d >= 0; --d) {
+        if (d > inner) continue;
+        int64_t q, c;
+        if (BIG) {
+            q = rem / pl.dims[d];
+            c = rem - q * pl.dims[d];
+        } else {
+            const uint32_t r32 = (uint32_t)rem;
+            const uint32_t q32 = fdiv(r32, pl.fd[d]);
+            q = q32;
+            c = (int64_t)(r32 - q32 * pl.fd[d].d);
+        }
+        if (d == inner) *cin = c;
+#pragma unroll
+        for (int k = 0; k < NIN; ++k)
+            if (pl.kind[k] == IN_BCAST) off[k] += c * pl.st[k][d];
+        rem = q;
+    }
+}
+
+
 // ---------------------------------------------------------------------------------------
 // kernels (defined in mh_elementwise.hip / mh_reduce.hip)
 // ---------------------------------------------------------------------------------------

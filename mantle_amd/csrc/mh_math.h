@@ -104,6 +104,16 @@ __device__ __forceinline__ float mpowf(float x, float y) {
     return mexp(y * mlog(x));
 }
 
+// mpowf(x, y) for a caller that already holds lgx = mlog(x): the same branches and the same
+// bits, without evaluating the log a second time.
+__device__ __forceinline__ float mpowf_lg(float x, float y, float lgx) {
+    if (y != y) return y;
+    float yi = __builtin_truncf(y);
+    if (yi == y && __builtin_fabsf(y) < 2147483648.0f) return mpowi(x, (int64_t)yi);
+    if (x < 0.0f) return __builtin_nanf("");
+    return mexp(y * lgx);
+}
+
 __device__ __forceinline__ float msigmoid(float x) { return 1.0f / (1.0f + mexp(-x)); }
 
 __device__ __forceinline__ float mtanh(float x) {

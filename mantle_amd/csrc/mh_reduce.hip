@@ -88,9 +88,9 @@ struct LdPowGrad {
     float a;
     __device__ void setup() { a = ap[0]; }
     __device__ float term(float xv, float u) const {
-        float lg = mlog(xv);
-        if (__builtin_isinf(lg)) lg = 0.0f;
-        return (mpowf(xv, a) * lg) * u;
+        const float lx = mlog(xv);  // one log serves both the power and the log factor
+        const float lg = __builtin_isinf(lx) ? 0.0f : lx;
+        return (mpowf_lg(xv, a, lx) * lg) * u;
     }
     __device__ float get(int64_t i) const { return term(x[i], ug[i]); }
     __device__ void get4(int64_t i, float* o) const {

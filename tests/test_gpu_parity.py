@@ -288,6 +288,42 @@ def test_fused_bias_relu_matches_op_by_op(gpu):
                      "fused grad bias", terms_abs=np.abs(gyd).sum(axis=(0, 2, 3), keepdims=True))
 
 
+FUSED_SHAPES = [((8, 32, 28, 28), (1, 32, 1, 1)), ((2, 3, 64), (3, 1)), ((5, 300), (5, 1)), ((4, 6, 96), (1,)),
+                ((3, 7, 10), (1, 7, 1)), ((64, 40), (1, 40)), ((2, 3, 4, 80), (1, 3, 4, 1)), ((3, 2, 20000), (1, 2, 1))]
+
+
+@pytest.mark.parametrize("sx,sb", FUSED_SHAPES, ids=[f"{a}+{b}" for a, b in FUSED_SHAPES])
+@pytest.mark.parametrize("keep_gy", [False, True], ids=["no_gy", "gy"])
+def test_fused_bias_relu_shapes(gpu, sx, sb, keep_gy):
+    """mh_bias_relu_fwd / _bwd_accum against the op-by-op oracle, accumulating into non-zero
+    grads (plane-form shapes take the fused kernels, the others the op-by-op path)."""
+    m = gpu.m
+    x = synth.normal(sx, 0, 1, 31)
+    bias = synth.normal(sb, 0, 0.1, 32)
+    ug = synth.normal(sx, 0, 1, 33)
+    gy0, gx0, gb0 = synth.normal(sx, 0, 1, 34), synth.normal(sx, 0, 1, 35), synth.normal(sb, 0, 1, 36)
+    tx, tb, tu = gpu.T(x), gpu.T(bias), gpu.T(ug)
+    y, r = m.Tensor(tx.shape()), m.Tensor(tx.shape())
+    S = m._lib
+    S.call("mh_bias_relu_fwd", y.ptr, r.ptr, tx.ptr, tx.shape().c(), tb.ptr, tb.shape().c())
+    y_ref = ORC.forward(OPS["ADD"], x, bias)
+    assert_bitexact(y.to_numpy(), y_ref, "y")
+    assert_bitexact(r.to_numpy(), ORC.forward(OPS["RELU"], y_ref), "r")
+    tgy, tgx, tgb = gpu.T(gy0), gpu.T(gx0), gpu.T(gb0)
+    S.call("mh_bias_relu_bwd_accum", tgy.ptr if keep_gy else None, tgx.ptr, tgb.ptr, y.ptr, tu.ptr, tx.shape().c(),
+           tb.shape().c())
+    gy = ORC.backward(0, OPS["RELU"], ug, y_ref, grad=gy0 if keep_gy else np.zeros(sx, np.float32))
+    if keep_gy:
+        assert_bitexact(tgy.to_numpy(), gy, "fused grad y")
+    assert_bitexact(tgx.to_numpy(), ORC.backward(0, OPS["ADD"], gy, x, bias, grad=gx0), "fused grad x")
+    red = tuple(i for i in range(len(sx)) if i < len(sx) - len(sb) or sb[i - (len(sx) - len(sb))] == 1)
+    gyd = gy.astype(np.float64)
+    ex = gyd.sum(axis=red).reshape(sb) + gb0.astype(np.float64)
+    mag = np.abs(gyd).sum(axis=red).reshape(sb) + np.abs(gb0)
+    assert_sum_close(tgb.to_numpy(), ORC.backward(1, OPS["ADD"], gy, x, bias, grad=gb0), ex, "fused grad bias",
+                     terms_abs=mag)
+
+
 def config5_nodes():
     # MAX(ax1) -> SUB -> EXP -> SUM(ax1) -> DIV -> LOG -> MUL(onehot) -> MEAN
     from util import softmax_nodes
