@@ -5,10 +5,13 @@
 //   C == 1, B <= 32 : 256 rows staged in LDS by coalesced float4 loads, one thread per
 //                     row (unaligned x: one thread per row straight from memory);
 //   C == 1          : one wavefront (64 lanes) per row, 128-bit loads, butterfly shuffle;
-//                     few long rows are cut into chunks whose partials a second pass combines;
-//   C  > 1          : one thread per output column (a quad of columns when C % 4 == 0), the
-//                     B rows split across blocks when that is needed to fill the chip, the
-//                     split partials combined by a second pass in fixed split order.
+//                     few long rows are cut into chunks of one 4-wave block each, whose
+//                     partials a second pass combines;
+//   C  > 1, C % 4 == 0 and >= 128 columns: a block per (strip of 64 column quads, chunk of
+//                     rows), its four waves interleaving the rows, combined through LDS;
+//   C  > 1 otherwise  : one thread per output column (a quad of columns when C % 4 == 0);
+//   in both column forms the rows split across blocks when that is needed to fill the chip,
+//   and a second pass combines the split partials in fixed split order.
 // No atomics: each output's summation order is fixed by the launch shape, so a call repeated
 // on the same input returns the same bits.
 #include <cfloat>
@@ -329,6 +332,172 @@ __global__ void __launch_bounds__(kRThreads)
     }
 }
 
+// One block (4 waves) per (row, chunk) of a split row: block vr = r * S + s covers elements
+// [r*B + s*L, r*B + min((s+1)*L, B)); the threads stride over its quads, the four wave
+// results combine in wave order, and the chunk's value goes to part[vr].
+template <class R, class LD, bool VEC>
+__global__ void __launch_bounds__(kRThreads)
+    k_rows_block(LD ld, int64_t S, int64_t B, int64_t L, float* part, int64_t npart) {
+    using T = typename R::T;
+    __shared__ T ws[4];
+    ld.setup();
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int64_t vr = blockIdx.x;
+    const int64_t r = vr / S, s = vr - r * S;
+    const int64_t start = r * B + s * L;
+    const int64_t rem = B - s * L;
+    const int64_t len = rem < L ? rem : L;
+    T acc = R::init();
+    if (VEC) {
+        const int64_t nq = len >> 2;
+        T a4[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a4[u][j] = R::init();
+        int64_t q = t;
+        for (; q + 3 * kRThreads < nq; q += 4 * kRThreads) {
+            T v[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) ld.get4(start + (q + (int64_t)u * kRThreads) * 4, v[u]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a4[u][j] = R::comb(a4[u][j], v[u][j]);
+        }
+        for (; q < nq; q += kRThreads) {
+            T v[4];
+            ld.get4(start + q * 4, v);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a4[0][j] = R::comb(a4[0][j], v[j]);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = R::comb(acc, a4[u][j]);
+    } else {
+        for (int64_t j = t; j < len; j += kRThreads) acc = R::comb(acc, ld.get(start + j));
+    }
+    acc = wave_reduce<R>(acc);
+    if (lane == 0) ws[w] = acc;
+    __syncthreads();
+    if (t == 0) part_store2(part, npart, vr, R::comb(R::comb(R::comb(ws[0], ws[1]), ws[2]), ws[3]));
+}
+
+// Strided-axis reduction over [A, B, C] with C % 4 == 0: block (a * nstrips + strip, s) owns
+// the 64 column quads [strip * 64, strip * 64 + 64) of slab a (lane = quad) and the rows
+// [s * rps, min((s + 1) * rps, B)), which its four waves interleave (wave w: rows b0 + w,
+// b0 + w + 4, ...). Every wave reads 1 KiB contiguous per row; the wave results combine in
+// wave order through LDS. S == 1 writes the epilogue, S > 1 partials at s * (A * C) + o.
+template <class R, class LD>
+__global__ void __launch_bounds__(kRThreads)
+    k_cols_strip(LD ld, int64_t A, int64_t B, int64_t C, int64_t nstrips, int64_t rps, int64_t S,
+                 float* out, float* out2, int epi, float div, float* part) {
+    using T = typename R::T;
+    __shared__ T lds[3][64][4];
+    ld.setup();
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t bx = blockIdx.x;
+    const int64_t a = bx / nstrips, strip = bx - a * nstrips;
+    const int64_t cq = strip * 64 + lane;
+    const bool active = cq < (C >> 2);
+    const int64_t s = blockIdx.y;
+    const int64_t b0 = s * rps;
+    const int64_t b1 = (b0 + rps < B) ? b0 + rps : B;
+    T acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = R::init();
+    if (active) {
+        const int64_t base = a * B * C + cq * 4;
+        int64_t b = b0 + w;
+        for (; b + 12 < b1; b += 16) {
+            T v[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) ld.get4(base + (b + 4 * u) * C, v[u]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[j] = R::comb(acc[j], v[u][j]);
+        }
+        for (; b < b1; b += 4) {
+            T v[4];
+            ld.get4(base + b * C, v);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = R::comb(acc[j], v[j]);
+        }
+    }
+    if (w > 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lds[w - 1][lane][j] = acc[j];
+    }
+    __syncthreads();
+    if (w == 0 && active) {
+#pragma unroll
+        for (int ww = 0; ww < 3; ++ww)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = R::comb(acc[j], lds[ww][lane][j]);
+        const int64_t o = a * C + cq * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (S == 1) epi_store(out, out2, o + j, acc[j], epi, div);
+            else part_store2(part, S * A * C, s * A * C + o + j, acc[j]);
+        }
+    }
+}
+
+// MAX backward over rows of B <= 16384 elements (B % 4 == 0), one pass: the row is held in
+// registers (NQ quads per thread, WPR waves per row), its max and count reduced across the
+// row's threads, then grad[i] = grad[i] + (x[i] == m ? fl(1/c) * ug[row] : 0) from the same
+// registers (basics.mojo:581-615 for a last-axis reduce): x is read once.
+template <int WPR, int NQ>
+__global__ void __launch_bounds__(kRThreads)
+    k_max_bwd_rowreg(float* __restrict__ grad, const float* __restrict__ x, const float* __restrict__ ug,
+                     int64_t nrows, int64_t B) {
+    __shared__ MC ws[4];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t row = WPR == 1 ? (int64_t)blockIdx.x * 4 + w : (int64_t)blockIdx.x;
+    if (row >= nrows) return;  // WPR == 1: uniform per wave, and that path has no barrier
+    const int tr = WPR == 1 ? lane : (int)threadIdx.x;
+    constexpr int NT = 64 * WPR;
+    const int64_t Bq = B >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(x + row * B);
+    float4 v[NQ];
+    MC acc = RMaxCnt::init();
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const int64_t qi = tr + (int64_t)k * NT;
+        if (qi < Bq) {
+            v[k] = x4[qi];
+            acc = RMaxCnt::comb(acc, RMaxCnt::lift(v[k].x));
+            acc = RMaxCnt::comb(acc, RMaxCnt::lift(v[k].y));
+            acc = RMaxCnt::comb(acc, RMaxCnt::lift(v[k].z));
+            acc = RMaxCnt::comb(acc, RMaxCnt::lift(v[k].w));
+        }
+    }
+    acc = wave_reduce<RMaxCnt>(acc);
+    if (WPR == 4) {
+        if (lane == 0) ws[w] = acc;
+        __syncthreads();
+        acc = RMaxCnt::comb(RMaxCnt::comb(RMaxCnt::comb(ws[0], ws[1]), ws[2]), ws[3]);
+    }
+    const float f = 1.0f / (float)acc.c;  // basics.mojo:609
+    const float g = f * ug[row];
+    const float m = acc.m;
+    float4* g4 = reinterpret_cast<float4*>(grad + row * B);
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const int64_t qi = tr + (int64_t)k * NT;
+        if (qi < Bq) {
+            float4 o = g4[qi];
+            o.x = o.x + (v[k].x == m ? g : 0.0f);
+            o.y = o.y + (v[k].y == m ? g : 0.0f);
+            o.z = o.z + (v[k].z == m ? g : 0.0f);
+            o.w = o.w + (v[k].w == m ? g : 0.0f);
+            g4[qi] = o;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------------------
 // launch planning
 // ---------------------------------------------------------------------------------------
@@ -337,9 +506,11 @@ static inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) 
 struct RowSplit {
     int64_t S, L;
 };
+// Few long rows are cut into chunks of L elements, one 4-wave block each (k_rows_block),
+// so that about 8 blocks per CU are in flight.
 static RowSplit row_split(int64_t A, int64_t B) {
     RowSplit rs{1, B};
-    const int64_t target = 32 * (int64_t)ctx().num_cus;  // wavefronts wanted in flight
+    const int64_t target = 8 * (int64_t)ctx().num_cus;  // blocks wanted in flight
     if (A < target && B >= 8192) {
         int64_t S = (target + A - 1) / A;
         int64_t L = (B + S - 1) / S;
@@ -375,6 +546,30 @@ static ColSplit col_split(int64_t A, int64_t B, int64_t C, bool vec) {
     return cs;
 }
 
+// The strip kernel (C % 4 == 0, at least 32 column quads): blocks = A * nstrips * S, with S
+// raising the block count to about 8 per CU while each wave keeps >= 8 rows.
+static bool use_strip(int64_t C, bool vec) { return vec && C % 4 == 0 && (C >> 2) >= 32; }
+static ColSplit strip_split(int64_t A, int64_t B, int64_t C, int64_t* nstrips) {
+    ColSplit cs;
+    cs.vec = true;
+    *nstrips = ((C >> 2) + 63) / 64;
+    const int64_t bx = A * *nstrips;
+    const int64_t target = 8 * (int64_t)ctx().num_cus;
+    int64_t S = 1;
+    if (bx < target) {
+        S = (target + bx - 1) / bx;
+        int64_t maxS = B / 32;
+        if (maxS < 1) maxS = 1;
+        if (S > maxS) S = maxS;
+        if (S > 65535) S = 65535;
+    }
+    cs.rps = (B + S - 1) / S;
+    if (cs.rps < 1) cs.rps = 1;
+    cs.S = (B + cs.rps - 1) / cs.rps;
+    if (cs.S < 1) cs.S = 1;
+    return cs;
+}
+
 template <class R>
 static constexpr int part_words() {
     return sizeof(typename R::T) == 4 ? 1 : 2;
@@ -389,8 +584,17 @@ static size_t tmp_floats_t(int64_t A, int64_t B, int64_t C, bool vec_ok) {
         RowSplit rs = row_split(A, B);
         return rs.S > 1 ? (size_t)(A * rs.S) * part_words<R>() : 0;
     }
-    ColSplit cs = col_split(A, B, C, vec_ok && C % 4 == 0);
-    return cs.S > 1 ? (size_t)(cs.S * A * C) * part_words<R>() : 0;
+    // the largest split any column launcher may pick (the choice depends on alignment)
+    int64_t S = 1;
+    if (use_strip(C, vec_ok)) {
+        int64_t ns;
+        ColSplit cs = strip_split(A, B, C, &ns);
+        S = cs.S > S ? cs.S : S;
+    }
+    ColSplit c4 = col_split(A, B, C, vec_ok && C % 4 == 0), c1 = col_split(A, B, C, false);
+    S = c4.S > S ? c4.S : S;
+    S = c1.S > S ? c1.S : S;
+    return S > 1 ? (size_t)(S * A * C) * part_words<R>() : 0;
 }
 
 size_t reduce_abc_tmp_floats(int op, int64_t A, int64_t B, int64_t C) {
@@ -438,12 +642,35 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
         RowSplit rs = nosplit ? RowSplit{1, B} : row_split(A, B);
         const bool vec = vec_ok && B % 4 == 0 && rs.L % 4 == 0;
         const int64_t nv = A * rs.S;
-        dim3 g((unsigned)((nv + 3) / 4)), b(kRThreads);
-        if (vec) hipLaunchKernelGGL((k_rows_wave<R, LD, true>), g, b, 0, st, ld, nv, rs.S, B, rs.L, out, out2, epi, div, tmp);
-        else hipLaunchKernelGGL((k_rows_wave<R, LD, false>), g, b, 0, st, ld, nv, rs.S, B, rs.L, out, out2, epi, div, tmp);
+        if (rs.S == 1) {  // one wavefront per row
+            dim3 g((unsigned)((nv + 3) / 4)), b(kRThreads);
+            if (vec) hipLaunchKernelGGL((k_rows_wave<R, LD, true>), g, b, 0, st, ld, nv, rs.S, B, rs.L, out, out2, epi, div, tmp);
+            else hipLaunchKernelGGL((k_rows_wave<R, LD, false>), g, b, 0, st, ld, nv, rs.S, B, rs.L, out, out2, epi, div, tmp);
+        } else {  // one block per row chunk, partials combined below
+            dim3 g((unsigned)nv), b(kRThreads);
+            if (vec) hipLaunchKernelGGL((k_rows_block<R, LD, true>), g, b, 0, st, ld, rs.S, B, rs.L, tmp, nv);
+            else hipLaunchKernelGGL((k_rows_block<R, LD, false>), g, b, 0, st, ld, rs.S, B, rs.L, tmp, nv);
+        }
         if (rs.S > 1) {
             using PL = PartLoader<R>;
             return reduce_t<R, typename PL::type>(PL::make(tmp, nv), true, epi, A, rs.S, 1, out, out2, div,
+                                                  nullptr, true);
+        }
+        return MH_OK;
+    }
+    if (use_strip(C, vec_ok)) {
+        int64_t ns;
+        ColSplit cs = strip_split(A, B, C, &ns);
+        if (nosplit) {
+            cs.S = 1;
+            cs.rps = B;
+        }
+        dim3 g((unsigned)(A * ns), (unsigned)cs.S), b(kRThreads);
+        hipLaunchKernelGGL((k_cols_strip<R, LD>), g, b, 0, st, ld, A, B, C, ns, cs.rps, cs.S, out, out2, epi, div, tmp);
+        if (cs.S > 1) {
+            using PL = PartLoader<R>;
+            const int64_t np = cs.S * A * C;
+            return reduce_t<R, typename PL::type>(PL::make(tmp, np), true, epi, 1, cs.S, A * C, out, out2, div,
                                                   nullptr, true);
         }
         return MH_OK;
@@ -667,6 +894,34 @@ int mh_reduce_bwd_accum(int op, float* grad, const float* x, const mh_shape* psx
         else
             hipLaunchKernelGGL(k_max_bwd_rows<32>, dim3(blocks), dim3(kRThreads), 0, ctx().stream, grad, x, ug, A,
                                (int)B, fdB);
+    } else if (C == 1 && B % 4 == 0 && B <= 16384 && al16(x) && al16(grad) && A < ((int64_t)1 << 31)) {
+        // MAX over rows held in registers: one pass
+        const int64_t Bq = B / 4;
+        hipStream_t st = ctx().stream;
+        if (Bq <= 64 * 16) {  // one wave per row, four rows per block
+            const int nq = Bq <= 64 ? 1 : Bq <= 128 ? 2 : Bq <= 256 ? 4 : Bq <= 512 ? 8 : 16;
+            dim3 g((unsigned)((A + 3) / 4)), b(kRThreads);
+#define MH_MBR(NQ) hipLaunchKernelGGL((k_max_bwd_rowreg<1, NQ>), g, b, 0, st, grad, x, ug, A, B)
+            switch (nq) {
+                case 1: MH_MBR(1); break;
+                case 2: MH_MBR(2); break;
+                case 4: MH_MBR(4); break;
+                case 8: MH_MBR(8); break;
+                default: MH_MBR(16); break;
+            }
+#undef MH_MBR
+        } else {  // one block per row
+            const int nq = Bq <= 512 ? 2 : Bq <= 1024 ? 4 : Bq <= 2048 ? 8 : 16;
+            dim3 g((unsigned)A), b(kRThreads);
+#define MH_MBR(NQ) hipLaunchKernelGGL((k_max_bwd_rowreg<4, NQ>), g, b, 0, st, grad, x, ug, A, B)
+            switch (nq) {
+                case 2: MH_MBR(2); break;
+                case 4: MH_MBR(4); break;
+                case 8: MH_MBR(8); break;
+                default: MH_MBR(16); break;
+            }
+#undef MH_MBR
+        }
     } else {  // MAX, basics.mojo:536-615: line max and fl(1/count), then routing
         const int64_t nl = A * C;
         const size_t pad_nl = ((size_t)nl + 63) & ~(size_t)63;

@@ -152,7 +152,9 @@ RED_CASES = [((87, 73, 107), 0), ((87, 73, 107), 1), ((87, 73, 107), 2), ((87, 7
              ((1024, 1024), 0), ((1024, 1024), 1), ((64, 512, 1024), 2), ((4099, 10), 1), ((3, 1, 5), 1),
              ((1,), None), ((5,), 0), ((2, 70000), 1), ((70000, 3), 0), ((1 << 22,), None), ((6, 33, 2), 1),
              ((1000, 20), 1), ((513, 32), 1), ((1001, 3), 1), ((300, 1), 1), ((257, 16), 1), ((40, 33), 1),
-             ((30,), None), ((2, 3, 17), 2)]
+             ((30,), None), ((2, 3, 17), 2), ((5, 16384), 1), ((3, 4100), 1), ((7, 2052), 1), ((16, 36), 1),
+             ((300, 256), 0), ((33, 512, 128), 1), ((4, 8, 1024), 0), ((2, 5000, 132), 1), ((9000, 64), 0),
+             ((3, 12000), None)]
 
 
 @pytest.mark.parametrize("shape,axis", RED_CASES, ids=[f"{s}-ax{a}" for s, a in RED_CASES])
@@ -219,6 +221,29 @@ def test_unaligned_device_pointers(gpu):
     r = m.Tensor(m.TensorShape(101, 40))
     m.forward_op(m.OP.ADD, r, vx, gpu.T(bias))
     assert_bitexact(r.to_numpy(), x + bias, "unaligned bcast add")
+
+
+@pytest.mark.parametrize("shape,axis", [((1000, 256), 0), ((256, 1000), 1), ((70001,), None), ((40, 1000), 1)])
+def test_unaligned_reduction_input(gpu, shape, axis):
+    """x starting 4 bytes into its allocation: the scalar launchers, whose split partials
+    must still fit the library scratch."""
+    m = gpu.m
+    x = synth.normal(shape, 0, 1, 820)
+    base = gpu.T(np.concatenate([[0], x.reshape(-1)]).astype(np.float32))
+    vx = m.Tensor(m.TensorShape(*shape), _ptr=base.ptr + 4, _owner=base)
+    ax = -1 if axis is None else axis
+    kd = dict(axis=axis, keepdims=True) if axis is not None else {}
+    red = (1,) if axis is None else tuple(1 if i == axis else d for i, d in enumerate(shape))
+    ex = x.astype(np.float64).sum(**kd).reshape(red)
+    mag = np.abs(x.astype(np.float64)).sum(**kd).reshape(red)
+    assert_sum_close(m.tsum(vx, ax).to_numpy(), ORC.forward(OPS["SUM"], x, axis=axis), ex, "unaligned sum",
+                     terms_abs=mag)
+    assert_bitexact(m.tmax(vx, ax).to_numpy(), ORC.forward(OPS["MAX"], x, axis=axis), "unaligned max")
+    g = m.Tensor(m.TensorShape(*shape))
+    ug = synth.normal(red, 0, 1, 821)
+    m.backward_op(0, m.OP.MAX, gpu.T(ug), vx, None, g, attributes=None if axis is None else {"axis": axis})
+    assert_bitexact(g.to_numpy(), ORC.backward(0, OPS["MAX"], ug, x, axis=axis, grad=np.zeros(shape, np.float32)),
+                    "unaligned max bwd")
 
 
 def test_empty_tensors_are_noops(gpu):
