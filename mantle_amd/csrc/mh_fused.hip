@@ -5,10 +5,10 @@
 // Forward: one pass reads x (and the small bias) and writes y = x + bias and r = relu(y):
 // 12 B per element instead of the 16 B of two separate ops.
 // Backward: with x viewed as [N, C, S] and the bias indexed by C alone (NCHW bias
-// [1, C, 1, 1], or any bias that is constant over a contiguous inner run S), one block per
-// (plane, chunk) computes gy = g_y + relu'(y) * ug, accumulates it into grad_x (and g_y when
-// the caller keeps it), and writes the chunk's sum of gy; a second pass adds those partials
-// into grad_bias in a fixed order. Shapes outside that form run the op-by-op kernels.
+// [1, C, 1, 1], or any bias that is constant over a contiguous inner run S), one wavefront
+// per (plane, chunk) computes gy = g_y + relu'(y) * ug, accumulates it into grad_x (and g_y
+// when the caller keeps it), and writes the chunk's sum of gy; a second pass adds those
+// partials into grad_bias in a fixed order. Shapes outside that form run the op-by-op kernels.
 #include "mh_internal.h"
 #include "mh_math.h"
 
@@ -85,34 +85,28 @@ __global__ void __launch_bounds__(kFThreads)
     }
 }
 
-__device__ __forceinline__ float block_sum256(float v, float* ws) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) ws[wave] = v;
-    __syncthreads();
-    return ((ws[0] + ws[1]) + ws[2]) + ws[3];
-}
-
-// Backward over [N, C, S] planes, S % 4 == 0; block b covers chunk k = b % K of plane
-// p = b / K (p = n * C + c): quads [k * QC, min((k + 1) * QC, Sq)) of the plane.
+// Backward over [N, C, S] planes, S % 4 == 0. One wavefront per (plane, chunk): wave
+// v = blockIdx.x * 4 + wave covers chunk k = v % K of plane p = v / K (p = n * C + c), i.e.
+// quads [k * QC, min((k + 1) * QC, Sq)) of the plane, QC <= 1024 (<= 16 quads per lane).
 //   rg = (y > 0 ? 1 : 0) * ug            RELU.backward (mlops.mojo:118-123)
 //   g  = g_y + rg  (0 + rg without g_y)  accumulate_grad into the grad of y (ops.mojo:405)
 //   grad_x = grad_x + g                  ADD backward_op, operand 0 (ops.mojo:457-461)
-//   part[(n * K + k) * C + c] = sum of g over the chunk (for ADD's operand-1 un-broadcast)
+//   part[(n * K + k) * C + c] = sum of g over the chunk (for ADD's operand-1 un-broadcast):
+//   each lane sums its quads in order, then a butterfly across the wave.
 template <bool HAS_GY, bool HAS_GX, bool HAS_PART>
 __global__ void __launch_bounds__(kFThreads)
     k_bias_relu_bwd_planes(float* __restrict__ gy, float* __restrict__ gx, const float* __restrict__ y,
                            const float* __restrict__ ug, int64_t C, int64_t Sq, int64_t QC, int64_t K,
-                           float* __restrict__ part) {
-    __shared__ float ws[4];
-    const int64_t b = blockIdx.x;
-    const int64_t p = b / K, k = b - p * K;
+                           int64_t nwaves, float* __restrict__ part) {
+    const int lane = threadIdx.x & 63;
+    const int64_t v = (int64_t)blockIdx.x * (kFThreads / 64) + (threadIdx.x >> 6);
+    if (v >= nwaves) return;  // uniform per wavefront; no barrier follows
+    const int64_t p = v / K, k = v - p * K;
     const int64_t q0 = p * Sq + k * QC;
     const int64_t rem = Sq - k * QC;
     const int64_t cnt = rem < QC ? rem : QC;
     float acc = 0.0f;
-    for (int64_t i = threadIdx.x; i < cnt; i += kFThreads) {
+    for (int64_t i = lane; i < cnt; i += 64) {
         const int64_t q = q0 + i;
         const float4 yv = reinterpret_cast<const float4*>(y)[q];
         const float4 uv = reinterpret_cast<const float4*>(ug)[q];
@@ -131,10 +125,11 @@ __global__ void __launch_bounds__(kFThreads)
         if (HAS_PART) acc = (((acc + g[0]) + g[1]) + g[2]) + g[3];
     }
     if (HAS_PART) {
-        const float s = block_sum256(acc, ws);
-        if (threadIdx.x == 0) {
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
+        if (lane == 0) {
             const int64_t n = p / C, c = p - n * C;
-            part[(n * K + k) * C + c] = s;
+            part[(n * K + k) * C + c] = acc;
         }
     }
 }
@@ -223,9 +218,10 @@ int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const fl
     // planes of at least 64 elements (16 quads), so that a block has work for its waves
     const bool planes = al && plane_form(pl, &N, &C, &S) && S % 4 == 0 && S >= 64;
     const int64_t Sq = S / 4;
-    const int64_t QC = Sq < 4096 ? Sq : 4096;  // quads per block
+    const int64_t QC = Sq < 1024 ? Sq : 1024;  // quads per wavefront
     const int64_t K = planes ? (Sq + QC - 1) / QC : 0;
-    const int64_t nblocks = N * C * K;
+    const int64_t nwaves = N * C * K;
+    const int64_t nblocks = (nwaves + 3) / 4;
     if (planes && nblocks <= 0x7fffffff) {
         float* part = nullptr;
         float* tmp = nullptr;
@@ -239,7 +235,8 @@ int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const fl
         hipStream_t st = ctx().stream;
         dim3 g((unsigned)nblocks), b(kFThreads);
 #define MH_BRB(GY, GX, PT)                                                                                  \
-    hipLaunchKernelGGL((k_bias_relu_bwd_planes<GY, GX, PT>), g, b, 0, st, g_y, grad_x, y, ug, C, Sq, QC, K, part)
+    hipLaunchKernelGGL((k_bias_relu_bwd_planes<GY, GX, PT>), g, b, 0, st, g_y, grad_x, y, ug, C, Sq, QC, K, nwaves, \
+               part)
         const int sel = (g_y ? 4 : 0) | (grad_x ? 2 : 0) | (has_part ? 1 : 0);
         switch (sel) {
             case 0: return MH_OK;  // nothing to produce

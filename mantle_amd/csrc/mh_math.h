@@ -8,6 +8,9 @@
 //        r = fma(k, -ln2, x), degree-7 Taylor polynomial of e^r (fma Horner), times 2^k;
 //   log: the Cephes logf method (S. L. Moshier, Cephes Math Library): frexp, fold below
 //        sqrt(1/2), degree-8 minimax polynomial, exponent added in two parts of ln 2.
+// Arguments that need special handling (exp: NaN or out of range; log: anything but a
+// positive normal finite value) leave the straight-line path through one range test, so
+// that the common case runs without per-element selects.
 // Float pow is the stdlib's scalar rule: integral exponent -> binary exponentiation,
 // negative base with fractional exponent -> NaN, otherwise exp(y * log(x)).
 #pragma once
@@ -18,21 +21,11 @@
 
 namespace mh {
 
-__device__ __forceinline__ float pow2i(int e) {  // 2^e, e in [-126, 127]
-    return __uint_as_float((uint32_t)(e + 127) << 23);
-}
-
-// p * 2^k in two exact power-of-two steps (one rounding only for subnormal results).
-__device__ __forceinline__ float scale2(float p, int k) {
-    int k1 = k >> 1;
-    int k2 = k - k1;
-    return (p * pow2i(k1)) * pow2i(k2);
-}
-
-__device__ __forceinline__ float mexp(float x) {
-    if (x != x) return x;
-    const float lo = -88.3762626647949f, hi = 88.3762626647950f;
-    float xc = x < lo ? lo : (x > hi ? hi : x);
+// exp on the clamped argument: k = floor(fma(x, 1/ln2, 0.5)), r = fma(k, -ln2, x), degree-7
+// Taylor polynomial of e^r in fma-Horner form, times 2^k. ldexp rounds p * 2^k once, the
+// same value as multiplying by two normal powers of two in turn (exact unless the result is
+// subnormal, where both round the exact product once).
+__device__ __forceinline__ float mexp_core(float xc) {
     float k = __builtin_floorf(__builtin_fmaf(xc, 1.442695040888963407359924681001892137426646f, 0.5f));
     float r = __builtin_fmaf(k, -0.69314718055966295651160180568695068359375f, xc);
     float p = 1.98412698412698412698e-4f;
@@ -43,19 +36,21 @@ __device__ __forceinline__ float mexp(float x) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return scale2(p, (int)k);
+    return __builtin_ldexpf(p, (int)k);
 }
 
-__device__ __forceinline__ float mlog(float x) {
-    if (x != x) return x;
-    if (x < 0.0f) return __builtin_nanf("");
-    if (x == 0.0f) return -__builtin_inff();
-    if (x == __builtin_inff()) return x;
-    int eadj = 0;
-    if (x < 1.17549435e-38f) {  // FLT_MIN: scale subnormals by 2^25 (exact)
-        x = x * 33554432.0f;
-        eadj = -25;
-    }
+__device__ __forceinline__ float mexp(float x) {
+    const float lo = -88.3762626647949f, hi = 88.3762626647950f;
+    float xc = x;
+    if (__builtin_expect(!(x >= lo && x <= hi), 0)) xc = x < lo ? lo : hi;  // clamp (NaN: see below)
+    const float e = mexp_core(xc);
+    return x != x ? x : e;
+}
+
+// log of a positive normal finite x (Cephes logf): frexp, fold below sqrt(1/2), degree-8
+// polynomial, exponent added in two parts of ln 2. eadj corrects the exponent of a
+// pre-scaled subnormal.
+__device__ __forceinline__ float mlog_core(float x, int eadj) {
     uint32_t u = __float_as_uint(x);
     int e = (int)((u >> 23) & 0xffu) - 126 + eadj;
     float m = __uint_as_float((u & 0x807fffffu) | 0x3f000000u);
@@ -82,6 +77,20 @@ __device__ __forceinline__ float mlog(float x) {
     float r = m + y;
     r = r + 0.693359375f * fe;
     return r;
+}
+
+// NaN, negative, zero, subnormal and infinite arguments, off the hot path.
+__device__ __attribute__((noinline)) float mlog_special(float x) {
+    if (x != x) return x;
+    if (x < 0.0f) return __builtin_nanf("");
+    if (x == 0.0f) return -__builtin_inff();
+    if (x == __builtin_inff()) return x;
+    return mlog_core(x * 33554432.0f, -25);  // subnormal: scale by 2^25 (exact)
+}
+
+__device__ __forceinline__ float mlog(float x) {
+    if (__builtin_expect(!(x >= 1.17549435e-38f && x < __builtin_inff()), 0)) return mlog_special(x);
+    return mlog_core(x, 0);
 }
 
 // pow(SIMD, Int): result seeded at 1, square-and-multiply, 1/res for negative n.

@@ -128,6 +128,40 @@ def test_unary_fwd_bwd_parity(gpu, name):
     assert_ulp(bwd, ORC.backward(0, op, ug, x, grad=g0), 2, f"{name} bwd")
 
 
+def _special_inputs(seed):
+    """Arguments around every branch of the device exp/log: NaN, +-inf, +-0, the exp clamp
+    bounds and just beyond, results that underflow to subnormal, subnormal and tiny log
+    arguments, negative log arguments, and a dense sweep of ordinary values."""
+    f32 = np.float32
+    lo, hi = f32(-88.3762626647949), f32(88.3762626647950)
+    pts = [np.nan, np.inf, -np.inf, 0.0, -0.0, 1.0, -1.0, 2.0, 0.5, 1e-45, 1e-40, 1.17549435e-38, 3e-38,
+           float(lo), float(hi), float(np.nextafter(lo, f32(-1e9))), float(np.nextafter(hi, f32(1e9))), -100.0, 100.0,
+           -87.0, -87.5, -88.0, 88.0, 3.4e38, -3.4e38, 0.7071067, 0.70710677, 0.7071068]
+    sweep = synth.uniform((20000,), -104, 90, seed)
+    tiny = (synth.uniform((4000,), 0, 1, seed + 1) * f32(1.2e-38)).astype(f32)
+    return np.concatenate([np.array(pts, f32), sweep, tiny, -tiny]).astype(f32)
+
+
+@pytest.mark.parametrize("name", ["EXP", "LOG", "SIGMOID", "TANH"])
+def test_device_math_matches_oracle_bitwise(gpu, name):
+    """The device exp/log and the oracle's restatement are the same algorithm: the GPU must
+    reproduce the oracle's bits on every branch (the north-star bar against Mantle itself is
+    2 ulp; this is the stricter internal check)."""
+    x = _special_inputs(900 + OPS[name])
+    assert_bitexact(gpu.forward(OPS[name], x), ORC.forward(OPS[name], x), f"{name} special inputs")
+
+
+def test_device_pow_matches_oracle_bitwise(gpu):
+    x = np.abs(_special_inputs(950))
+    ug = synth.normal(x.shape, 0, 1, 951)
+    for e in (2.37, 0.5, -0.75, 3.0, 0.0, -2.0):
+        t2 = np.array([e], np.float32)
+        assert_bitexact(gpu.forward(OPS["POW"], x, t2), ORC.forward(OPS["POW"], x, t2), f"pow fwd {e}")
+        g0 = np.zeros_like(x)
+        assert_bitexact(gpu.backward(0, OPS["POW"], ug, x, t2, grad=g0), ORC.backward(0, OPS["POW"], ug, x, t2, grad=g0),
+                        f"pow bwd x {e}")
+
+
 @pytest.mark.parametrize("e", [2.37, 0.61, 1.0, 2.0, -1.5, 3.9])
 def test_pow_parity(gpu, e):
     n = (1 << 18) + 7
