@@ -207,40 +207,46 @@ __global__ void __launch_bounds__(kThreads)
 
 // Broadcast engine, 128-bit path: the output and every FULL operand stream as flat float4
 // quads whatever the shape (all must be 16-byte aligned); only the broadcast operands are
-// gathered. The quad's first element is decoded; the next three step along the inner dim
-// unless they cross into the next row, where they are decoded afresh. INNER4 (inner dim a
-// multiple of 4, broadcast operands 16-byte aligned): a quad never crosses a row, and an
-// operand contiguous along the inner dim is read as one float4.
-template <class F, int NIN, bool ACCUM, bool INNER4, bool BIG>
+// gathered, with 32-bit offsets below 2^31 elements and a decode loop bounded by MAXR.
+// The quad's first element is decoded. INNER4 (inner dim a multiple of 4, broadcast
+// operands 16-byte aligned): a quad never crosses a row, and an operand contiguous along
+// the inner dim is read as one float4. Otherwise elements past the end of the row are in
+// the next one, whose offsets follow by addition while the next-outer coordinate does not
+// wrap (a full decode per element only for rows shorter than 4 or at such a wrap); an
+// operand constant along the inner dim is read once per row touched.
+template <class F, int NIN, bool ACCUM, bool INNER4, bool BIG, int MAXR>
 __global__ void __launch_bounds__(kThreads)
     k_bcast4(float* __restrict__ out, InPtrs<NIN> in, ElwPlan pl, DevScal ds, F f) {
     constexpr int NA = NIN > 0 ? NIN : 1;
+    using OT = off_type<BIG>;
     f.setup(ds);
     float sv[NA];
 #pragma unroll
     for (int k = 0; k < NIN; ++k) sv[k] = pl.kind[k] == IN_SCALAR ? in.p[k][0] : 0.0f;
     const int inner = pl.rank - 1;
     const int64_t dinner = pl.dims[inner];
+    const int64_t douter = inner > 0 ? pl.dims[inner - 1] : 1;
     const int64_t nq = pl.n >> 2;
     const int64_t stride = (int64_t)gridDim.x * kThreads;
     for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
         const int64_t idx = q * 4;
-        int64_t off[4][NA];
-        int64_t cin = 0;
-        bcast_decode<NIN, BIG>(pl, idx, off[0], &cin);
-        if (!INNER4) {
+        OT off0[NA];
+        int64_t cin = 0, cprev = -1;
+        bcast_decode<NIN, BIG, MAXR>(pl, idx, off0, &cin, &cprev);
+        float v[4][NA];
+        int jc = 4;         // first element of the quad in the next row (4: none)
+        bool slow = false;  // per-element decode (row shorter than 4, or the next-outer coordinate wraps)
+        OT offc[NA];        // offsets of element jc
+        if (!INNER4 && cin + 3 >= dinner) {
+            jc = (int)(dinner - cin);
+            if (dinner >= 4 && inner > 0 && cprev + 1 < douter) {
 #pragma unroll
-            for (int j = 1; j < 4; ++j) {
-                if (cin + j < dinner) {
-#pragma unroll
-                    for (int k = 0; k < NIN; ++k) off[j][k] = off[0][k] + j * pl.st[k][inner];
-                } else {
-                    int64_t c2;
-                    bcast_decode<NIN, BIG>(pl, idx + j, off[j], &c2);
-                }
+                for (int k = 0; k < NIN; ++k)
+                    offc[k] = off0[k] + (OT)pl.st[k][inner - 1] - (OT)cin * (OT)pl.st[k][inner];
+            } else {
+                slow = true;
             }
         }
-        float v[4][NA];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
             if (pl.kind[k] == IN_SCALAR) {
@@ -251,16 +257,41 @@ __global__ void __launch_bounds__(kThreads)
                 v[0][k] = t.x; v[1][k] = t.y; v[2][k] = t.z; v[3][k] = t.w;
             } else if (INNER4) {
                 if (pl.st[k][inner] == 1) {
-                    const float4 t = *reinterpret_cast<const float4*>(in.p[k] + off[0][k]);
+                    const float4 t = *reinterpret_cast<const float4*>(in.p[k] + off0[k]);
                     v[0][k] = t.x; v[1][k] = t.y; v[2][k] = t.z; v[3][k] = t.w;
                 } else {
-                    const float t = in.p[k][off[0][k]];
+                    const float t = in.p[k][off0[k]];
 #pragma unroll
                     for (int j = 0; j < 4; ++j) v[j][k] = t;
                 }
-            } else {
+            } else if (!slow) {
+                const OT si = (OT)pl.st[k][inner];
+                if (si == 0) {
+                    const float a = in.p[k][off0[k]];
+                    const float b = jc < 4 ? in.p[k][offc[k]] : a;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) v[j][k] = in.p[k][off[j][k]];
+                    for (int j = 0; j < 4; ++j) v[j][k] = j < jc ? a : b;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        v[j][k] = in.p[k][j < jc ? off0[k] + (OT)j * si : offc[k] + (OT)(j - jc) * si];
+                }
+            }
+        }
+        if (slow) {  // broadcast operands element by element
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                OT oj[NA];
+                int64_t c1, c2;
+                if (j < jc) {
+#pragma unroll
+                    for (int k = 0; k < NIN; ++k) oj[k] = off0[k] + (OT)j * (OT)pl.st[k][inner];
+                } else {
+                    bcast_decode<NIN, BIG, MAXR>(pl, idx + j, oj, &c1, &c2);
+                }
+#pragma unroll
+                for (int k = 0; k < NIN; ++k)
+                    if (pl.kind[k] == IN_BCAST) v[j][k] = in.p[k][oj[k]];
             }
         }
         const float4 o = ACCUM ? reinterpret_cast<const float4*>(out)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -274,8 +305,9 @@ __global__ void __launch_bounds__(kThreads)
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         for (int64_t i = nq << 2; i < pl.n; ++i) {
-            int64_t off1[NA], c;
-            bcast_decode<NIN, BIG>(pl, i, off1, &c);
+            OT off1[NA];
+            int64_t c, c2;
+            bcast_decode<NIN, BIG, MAXR>(pl, i, off1, &c, &c2);
             float v1[NA];
 #pragma unroll
             for (int k = 0; k < NIN; ++k)
@@ -291,14 +323,16 @@ template <class F, int NIN, bool ACCUM, bool BIG>
 __global__ void __launch_bounds__(kThreads)
     k_bcast1(float* __restrict__ out, InPtrs<NIN> in, ElwPlan pl, DevScal ds, F f) {
     constexpr int NA = NIN > 0 ? NIN : 1;
+    using OT = off_type<BIG>;
     f.setup(ds);
     float sv[NA];
 #pragma unroll
     for (int k = 0; k < NIN; ++k) sv[k] = pl.kind[k] == IN_SCALAR ? in.p[k][0] : 0.0f;
     const int64_t stride = (int64_t)gridDim.x * kThreads;
     for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < pl.n; i += stride) {
-        int64_t off[NA], c;
-        bcast_decode<NIN, BIG>(pl, i, off, &c);
+        OT off[NA];
+        int64_t c, c2;
+        bcast_decode<NIN, BIG, MH_MAX_RANK>(pl, i, off, &c, &c2);
         float v[NA];
 #pragma unroll
         for (int k = 0; k < NIN; ++k)
@@ -397,12 +431,16 @@ static int run_map(float* out, const ElwPlan& pl, const float* const* ptrs, cons
         if (pl.kind[k] == IN_BCAST) al_b = al_b && aligned16(ptrs[k]);
     if (al) {
         dim3 g(grid_for(pl.n >> 2, kThreads)), b(kThreads);
-        if (pl.vec_ok && al_b) {
-            if (big) hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, true, true>), g, b, 0, st, out, in, pl, ds, f);
-            else hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, true, false>), g, b, 0, st, out, in, pl, ds, f);
+        const bool inner4 = pl.vec_ok && al_b;
+        if (big) {  // 64-bit offsets, any rank
+            if (inner4) hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, true, true, MH_MAX_RANK>), g, b, 0, st, out, in, pl, ds, f);
+            else hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, false, true, MH_MAX_RANK>), g, b, 0, st, out, in, pl, ds, f);
+        } else if (pl.rank <= 3) {
+            if (inner4) hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, true, false, 3>), g, b, 0, st, out, in, pl, ds, f);
+            else hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, false, false, 3>), g, b, 0, st, out, in, pl, ds, f);
         } else {
-            if (big) hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, false, true>), g, b, 0, st, out, in, pl, ds, f);
-            else hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, false, false>), g, b, 0, st, out, in, pl, ds, f);
+            if (inner4) hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, true, false, MH_MAX_RANK>), g, b, 0, st, out, in, pl, ds, f);
+            else hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, false, false, MH_MAX_RANK>), g, b, 0, st, out, in, pl, ds, f);
         }
         return MH_OK;
     }

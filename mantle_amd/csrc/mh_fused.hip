@@ -39,9 +39,9 @@ __global__ void __launch_bounds__(kFThreads)
             const float4 t = reinterpret_cast<const float4*>(bias)[q];
             bv[0] = t.x; bv[1] = t.y; bv[2] = t.z; bv[3] = t.w;
         } else {
-            int64_t off[4][2];
-            int64_t cin = 0;
-            bcast_decode<2, BIG>(pl, idx, off[0], &cin);
+            off_type<BIG> off[4][2];
+            int64_t cin = 0, cp;
+            bcast_decode<2, BIG, MH_MAX_RANK>(pl, idx, off[0], &cin, &cp);
             if (INNER4) {
                 if (pl.st[1][inner] == 1) {
                     const float4 t = *reinterpret_cast<const float4*>(bias + off[0][1]);
@@ -56,8 +56,8 @@ __global__ void __launch_bounds__(kFThreads)
                     if (cin + j < dinner) {
                         bv[j] = bias[off[0][1] + j * pl.st[1][inner]];
                     } else {
-                        int64_t c2;
-                        bcast_decode<2, BIG>(pl, idx + j, off[j], &c2);
+                        int64_t c2, c3;
+                        bcast_decode<2, BIG, MH_MAX_RANK>(pl, idx + j, off[j], &c2, &c3);
                         bv[j] = bias[off[j][1]];
                     }
                 }
@@ -75,8 +75,9 @@ __global__ void __launch_bounds__(kFThreads)
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         for (int64_t i = nq << 2; i < pl.n; ++i) {
-            int64_t off1[2], c;
-            bcast_decode<2, BIG>(pl, i, off1, &c);
+            off_type<BIG> off1[2];
+            int64_t c, c2;
+            bcast_decode<2, BIG, MH_MAX_RANK>(pl, i, off1, &c, &c2);
             const float b = kb == IN_SCALAR ? sb : (kb == IN_FULL ? bias[i] : bias[off1[1]]);
             const float yy = x[i] + b;
             y[i] = yy;

@@ -6,6 +6,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <type_traits>
 
 #include "../../include/mantle_hip.h"
 
@@ -119,35 +120,45 @@ __device__ __forceinline__ float comp(const float4& q, int j) {
     return j == 0 ? q.x : (j == 1 ? q.y : (j == 2 ? q.z : q.w));
 }
 
-// Offsets of the broadcast (IN_BCAST) operands at output element idx, and the element's
-// coordinate along the innermost collapsed dim. BIG: 64-bit division (n >= 2^31).
-template <int NIN, bool BIG>
-__device__ __forceinline__ void bcast_decode(const ElwPlan& pl, int64_t idx, int64_t* off, int64_t* cin) {
+// Offset type of the broadcast engine: 32-bit below 2^31 output elements (every operand is
+// no larger than the output, so its offsets fit too).
+template <bool BIG>
+using off_type = typename std::conditional<BIG, int64_t, int32_t>::type;
+
+// Offsets of the broadcast (IN_BCAST) operands at output element idx, the element's
+// coordinate along the innermost collapsed dim (cin) and along the next outer dim (cprev, -1
+// for a rank-1 plan). MAXR bounds the collapsed rank the loop covers (the caller guarantees
+// pl.rank <= MAXR). BIG: 64-bit division (n >= 2^31).
+template <int NIN, bool BIG, int MAXR>
+__device__ __forceinline__ void bcast_decode(const ElwPlan& pl, int64_t idx, off_type<BIG>* off, int64_t* cin,
+                                             int64_t* cprev) {
+    using OT = off_type<BIG>;
     const int inner = pl.rank - 1;
 #pragma unroll
     for (int k = 0; k < NIN; ++k) off[k] = 0;
+    *cprev = -1;
     int64_t rem = idx;
+    uint32_t rem32 = (uint32_t)idx;
 #pragma unroll
-    for (int d = MH_MAX_RANK - 1; d >= 0; --d) {
+    for (int d = MAXR - 1; d >= 0; --d) {
         if (d > inner) continue;
-        int64_t q, c;
+        int64_t c;
         if (BIG) {
-            q = rem / pl.dims[d];
+            const int64_t q = rem / pl.dims[d];
             c = rem - q * pl.dims[d];
+            rem = q;
         } else {
-            const uint32_t r32 = (uint32_t)rem;
-            const uint32_t q32 = fdiv(r32, pl.fd[d]);
-            q = q32;
-            c = (int64_t)(r32 - q32 * pl.fd[d].d);
+            const uint32_t q32 = fdiv(rem32, pl.fd[d]);
+            c = (int64_t)(rem32 - q32 * pl.fd[d].d);
+            rem32 = q32;
         }
         if (d == inner) *cin = c;
+        if (d == inner - 1) *cprev = c;
 #pragma unroll
         for (int k = 0; k < NIN; ++k)
-            if (pl.kind[k] == IN_BCAST) off[k] += c * pl.st[k][d];
-        rem = q;
+            if (pl.kind[k] == IN_BCAST) off[k] += (OT)c * (OT)pl.st[k][d];
     }
 }
-
 
 // ---------------------------------------------------------------------------------------
 // kernels (defined in mh_elementwise.hip / mh_reduce.hip)

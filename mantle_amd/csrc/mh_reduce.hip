@@ -4,9 +4,9 @@
 // Every reduction is expressed on a view [A, B, C] reduced over B:
 //   C == 1, B <= 32 : 256 rows staged in LDS by coalesced float4 loads, one thread per
 //                     row (unaligned x: one thread per row straight from memory);
-//   C == 1          : one wavefront (64 lanes) per row, 128-bit loads, butterfly shuffle;
-//                     few long rows are cut into chunks of one 4-wave block each, whose
-//                     partials a second pass combines;
+//   C == 1, B < 2048: one wavefront (64 lanes) per row, 128-bit loads, butterfly shuffle;
+//   C == 1, B >= 2048: 2048-element chunks, one 4-wave block each (two quads per thread),
+//                     whose partials reduce again along the row the same way;
 //   C  > 1, C % 4 == 0 and >= 128 columns: a block per (strip of 64 column quads, chunk of
 //                     rows), its four waves interleaving the rows, combined through LDS;
 //   C  > 1 otherwise  : one thread per output column (a quad of columns when C % 4 == 0);
@@ -332,12 +332,15 @@ __global__ void __launch_bounds__(kRThreads)
     }
 }
 
-// One block (4 waves) per (row, chunk) of a split row: block vr = r * S + s covers elements
-// [r*B + s*L, r*B + min((s+1)*L, B)); the threads stride over its quads, the four wave
-// results combine in wave order, and the chunk's value goes to part[vr].
+// Rows of >= 2048 elements: one block (4 waves) per (row, chunk) of L = 2048 elements, two
+// quads per thread in flight (small one-shot blocks stream best on gfx950). Block
+// vr = r * S + s covers elements [r*B + s*L, r*B + min((s+1)*L, B)); the four wave results
+// combine in wave order. S == 1 writes the row's epilogue, S > 1 the partial part[vr].
+constexpr int64_t kRowChunk = 2048;
 template <class R, class LD, bool VEC>
 __global__ void __launch_bounds__(kRThreads)
-    k_rows_block(LD ld, int64_t S, int64_t B, int64_t L, float* part, int64_t npart) {
+    k_rows_block(LD ld, int64_t S, int64_t B, int64_t L, float* out, float* out2, int epi, float div,
+                 float* part, int64_t npart) {
     using T = typename R::T;
     __shared__ T ws[4];
     ld.setup();
@@ -350,38 +353,42 @@ __global__ void __launch_bounds__(kRThreads)
     T acc = R::init();
     if (VEC) {
         const int64_t nq = len >> 2;
-        T a4[4][4];
+        T a2[2][4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) a4[u][j] = R::init();
+            for (int j = 0; j < 4; ++j) a2[u][j] = R::init();
         int64_t q = t;
-        for (; q + 3 * kRThreads < nq; q += 4 * kRThreads) {
-            T v[4][4];
+        for (; q + kRThreads < nq; q += 2 * kRThreads) {
+            T v[2][4];
+            ld.get4(start + q * 4, v[0]);
+            ld.get4(start + (q + kRThreads) * 4, v[1]);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) ld.get4(start + (q + (int64_t)u * kRThreads) * 4, v[u]);
+            for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) a4[u][j] = R::comb(a4[u][j], v[u][j]);
+                for (int j = 0; j < 4; ++j) a2[u][j] = R::comb(a2[u][j], v[u][j]);
         }
-        for (; q < nq; q += kRThreads) {
+        if (q < nq) {
             T v[4];
             ld.get4(start + q * 4, v);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) a4[0][j] = R::comb(a4[0][j], v[j]);
+            for (int j = 0; j < 4; ++j) a2[0][j] = R::comb(a2[0][j], v[j]);
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc = R::comb(acc, a4[u][j]);
+            for (int j = 0; j < 4; ++j) acc = R::comb(acc, a2[u][j]);
     } else {
         for (int64_t j = t; j < len; j += kRThreads) acc = R::comb(acc, ld.get(start + j));
     }
     acc = wave_reduce<R>(acc);
     if (lane == 0) ws[w] = acc;
     __syncthreads();
-    if (t == 0) part_store2(part, npart, vr, R::comb(R::comb(R::comb(ws[0], ws[1]), ws[2]), ws[3]));
+    if (t == 0) {
+        const T tot = R::comb(R::comb(R::comb(ws[0], ws[1]), ws[2]), ws[3]);
+        if (S == 1) epi_store(out, out2, r, tot, epi, div);
+        else part_store2(part, npart, vr, tot);
+    }
 }
 
 // Strided-axis reduction over [A, B, C] with C % 4 == 0: block (a * nstrips + strip, s) owns
@@ -503,24 +510,6 @@ __global__ void __launch_bounds__(kRThreads)
 // ---------------------------------------------------------------------------------------
 static inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-struct RowSplit {
-    int64_t S, L;
-};
-// Few long rows are cut into chunks of L elements, one 4-wave block each (k_rows_block),
-// so that about 8 blocks per CU are in flight.
-static RowSplit row_split(int64_t A, int64_t B) {
-    RowSplit rs{1, B};
-    const int64_t target = 8 * (int64_t)ctx().num_cus;  // blocks wanted in flight
-    if (A < target && B >= 8192) {
-        int64_t S = (target + A - 1) / A;
-        int64_t L = (B + S - 1) / S;
-        L = (L + 1023) & ~(int64_t)1023;
-        rs.S = (B + L - 1) / L;
-        rs.L = L;
-    }
-    return rs;
-}
-
 struct ColSplit {
     int64_t S, rps;
     bool vec;
@@ -575,15 +564,27 @@ static constexpr int part_words() {
     return sizeof(typename R::T) == 4 ? 1 : 2;
 }
 
+static inline size_t pad64(size_t v) { return (v + 63) & ~(size_t)63; }
+
+// Rows (C == 1): B <= 64 one thread (or an LDS tile) per row, B < 2048 one wavefront per
+// row, longer rows kRowChunk-element block chunks whose partials reduce again the same way.
+static inline bool rows_chunked(int64_t B) { return B >= 2048; }
+static inline int64_t row_chunks(int64_t B) { return (B + kRowChunk - 1) / kRowChunk; }
+
+// Scratch floats of the row path: every level's partials, one after another.
+template <class R>
+static size_t row_tmp_floats(int64_t A, int64_t B) {
+    if (!rows_chunked(B)) return 0;
+    const int64_t S = row_chunks(B);
+    if (S == 1) return 0;
+    return pad64((size_t)(A * S) * part_words<R>()) + row_tmp_floats<R>(A, S);
+}
+
 // Scratch floats a reduction of [A, B, C] needs for its partials.
 template <class R>
 static size_t tmp_floats_t(int64_t A, int64_t B, int64_t C, bool vec_ok) {
     if (A * C == 0) return 0;
-    if (C == 1) {
-        if (B <= 64) return 0;
-        RowSplit rs = row_split(A, B);
-        return rs.S > 1 ? (size_t)(A * rs.S) * part_words<R>() : 0;
-    }
+    if (C == 1) return row_tmp_floats<R>(A, B);
     // the largest split any column launcher may pick (the choice depends on alignment)
     int64_t S = 1;
     if (use_strip(C, vec_ok)) {
@@ -613,7 +614,7 @@ struct PartLoader<RMaxCnt> {
     static type make(float* p, int64_t n) { return LdPairs{p, reinterpret_cast<const uint32_t*>(p + n)}; }
 };
 
-// nosplit: a combine stage over split partials runs as a single pass (tmp unused).
+// nosplit: the combine stage over column-split partials runs as a single pass (tmp unused).
 template <class R, class LD>
 static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C, float* out,
                     float* out2, float div, float* tmp, bool nosplit = false) {
@@ -639,22 +640,22 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
                                B, out, out2, epi, div);
             return MH_OK;
         }
-        RowSplit rs = nosplit ? RowSplit{1, B} : row_split(A, B);
-        const bool vec = vec_ok && B % 4 == 0 && rs.L % 4 == 0;
-        const int64_t nv = A * rs.S;
-        if (rs.S == 1) {  // one wavefront per row
-            dim3 g((unsigned)((nv + 3) / 4)), b(kRThreads);
-            if (vec) hipLaunchKernelGGL((k_rows_wave<R, LD, true>), g, b, 0, st, ld, nv, rs.S, B, rs.L, out, out2, epi, div, tmp);
-            else hipLaunchKernelGGL((k_rows_wave<R, LD, false>), g, b, 0, st, ld, nv, rs.S, B, rs.L, out, out2, epi, div, tmp);
-        } else {  // one block per row chunk, partials combined below
-            dim3 g((unsigned)nv), b(kRThreads);
-            if (vec) hipLaunchKernelGGL((k_rows_block<R, LD, true>), g, b, 0, st, ld, rs.S, B, rs.L, tmp, nv);
-            else hipLaunchKernelGGL((k_rows_block<R, LD, false>), g, b, 0, st, ld, rs.S, B, rs.L, tmp, nv);
+        const bool vec = vec_ok && B % 4 == 0;
+        if (!rows_chunked(B)) {  // one wavefront per row
+            dim3 g((unsigned)((A + 3) / 4)), b(kRThreads);
+            if (vec) hipLaunchKernelGGL((k_rows_wave<R, LD, true>), g, b, 0, st, ld, A, (int64_t)1, B, B, out, out2, epi, div, tmp);
+            else hipLaunchKernelGGL((k_rows_wave<R, LD, false>), g, b, 0, st, ld, A, (int64_t)1, B, B, out, out2, epi, div, tmp);
+            return MH_OK;
         }
-        if (rs.S > 1) {
+        const int64_t S = row_chunks(B);
+        const int64_t nv = A * S;
+        dim3 g((unsigned)nv), b(kRThreads);
+        if (vec) hipLaunchKernelGGL((k_rows_block<R, LD, true>), g, b, 0, st, ld, S, B, kRowChunk, out, out2, epi, div, tmp, nv);
+        else hipLaunchKernelGGL((k_rows_block<R, LD, false>), g, b, 0, st, ld, S, B, kRowChunk, out, out2, epi, div, tmp, nv);
+        if (S > 1) {  // the chunk partials [A, S] reduce again along their rows
             using PL = PartLoader<R>;
-            return reduce_t<R, typename PL::type>(PL::make(tmp, nv), true, epi, A, rs.S, 1, out, out2, div,
-                                                  nullptr, true);
+            return reduce_t<R, typename PL::type>(PL::make(tmp, nv), true, epi, A, S, 1, out, out2, div,
+                                                  tmp + pad64((size_t)nv * part_words<R>()));
         }
         return MH_OK;
     }
