@@ -15,7 +15,8 @@ The other configs are measured after the headline step and reported under "workl
   c4  SUM/MEAN/MAX over axis 0, axis 1 and all of [8192,8192] (ties injected in half the
       lines) and over the last axis of [64,512,1024], fwd and bwd;
   c5  classifier head on logits [1048576,10]: MAX -> SUB -> EXP -> SUM -> DIV -> LOG ->
-      MUL(onehot) -> MEAN, forward and backward op by op (the drop-in path);
+      MUL(onehot) -> MEAN, forward and backward op by op (the drop-in path), and the same graph
+      row-fused (one kernel each way, caches flushed before each);
   copy  a plain 1 GiB device copy (the library's copy kernel): the practical streaming rate.
 Tensors smaller than the 256 MB Infinity Cache are timed with the cache flushed before each
 op (a 1 GiB read sweep between ops, outside the timed events).
@@ -133,6 +134,7 @@ def time_ops(d, ops, reps, flush=True, setup=None):
     for _ in range(reps + 1):  # the first repetition is a warm-up
         if setup:
             setup()
+            d.flush()  # the first op does not pay for the write-back of the setup's stores
         for (label, fn, _), (e0, e1) in zip(ops, evs):
             if flush:
                 d.flush()
@@ -406,8 +408,15 @@ def run_c5(L, reps, rows=1 << 20, classes=10):
         chk(L, L.mh_event_elapsed_ms(ctypes.byref(ms), e0, e1), "elapsed")
         chain.append(ms.value)
     chain_ms = statistics.median(chain[1:])
+    # the same graph row-fused: 8 B/elem forward (logits, onehot), 16 B/elem backward
+    fused = [("fused.fwd", lambda: L.mh_softmax_log_mul_mean_fwd(p["loss"], p["logits"], p["onehot"], rows, classes),
+              2 * F + 4),
+             ("fused.bwd", lambda: L.mh_softmax_log_mul_mean_bwd_accum(p["g_logits"], p["logits"], p["onehot"],
+                                                                       p["g_loss"], rows, classes), 4 * F + 4)]
+    mf = time_ops(d, fused, reps)
     d.free()
     return {"shape": [rows, classes], "elements": E,
+            "fused": op_report(fused, mf), "fused_total": total_report(fused, mf),
             "fwd": op_report(fwd, med), "bwd": op_report(bwd, med),
             "fwd_total": total_report(fwd, med), "bwd_total": total_report(bwd, med),
             "chain_ms": round(chain_ms, 4), "chain_rows_per_s": round(rows / (chain_ms * 1e-3), 1),

@@ -170,6 +170,22 @@ int mh_bias_relu_fwd(float* y, float* r, const float* x, const mh_shape* sx, con
 int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const float* y,
                            const float* ug, const mh_shape* sx, const mh_shape* sbias);
 
+/* Row-fused forward of the classifier-head graph over x [rows, classes] (classes <= 32):
+ *   MAX(x, axis 1) -> SUB -> EXP -> SUM(axis 1) -> DIV -> LOG -> MUL(target) -> MEAN
+ * i.e. Softmax (mantle/nn/activations.mojo:74-87) followed by LOG, MUL and MEAN
+ * (basics.mojo:288-309, 94-129, 428-506): loss[0] = mean(log(softmax(x)) * target), with no
+ * sign change. Per element the same values as the eight forward_op calls; the final mean
+ * sums in another order (rtol class). Reads x and target once. */
+int mh_softmax_log_mul_mean_fwd(float* loss, const float* x, const float* target, int64_t rows,
+                                int64_t classes);
+
+/* Backward of the same graph from ug = the grad of the loss (a device scalar), accumulated:
+ * grad_x = grad_x + d(loss)/dx, bit-identical to the ten backward_op calls Model.backward
+ * makes for the graph (model.mojo:194-330) from zeroed intermediate grads. Reads x and
+ * target, updates grad_x, in one pass. */
+int mh_softmax_log_mul_mean_bwd_accum(float* grad_x, const float* x, const float* target,
+                                      const float* ug, int64_t rows, int64_t classes);
+
 /* Seeded synthetic fill (the device counterpart of rand_uniform / rand_normal,
  * mantle/core/rand_utils.mojo:23-63): element i of stream `seed` comes from a counter-based
  * SplitMix64, so the result does not depend on the launch shape. U(lo, hi) and N(mean, std). */

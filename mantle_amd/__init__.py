@@ -11,10 +11,12 @@ from .ops import (  # noqa: F401
     OP, ADD, SUB, MUL, DIV, EXP, LOG, POW, SUM, MEAN, MAX, SIGMOID, RELU, TANH,
     forward_op, backward_op, backward_op_both, broadcast_shapes, get_reduce_shape, fill,
     elwise_transform, elwise_op, accumulate_grad, tsum, tmean, tmax, static_result_shape,
+    bias_relu_forward, bias_relu_backward, softmax_log_mul_mean_forward, softmax_log_mul_mean_backward,
 )
 
 __all__ = [
     "MantleHipError", "Tensor", "TensorShape", "init", "sync", "OP", "forward_op", "backward_op",
     "backward_op_both", "broadcast_shapes", "get_reduce_shape", "fill", "elwise_transform",
-    "elwise_op", "accumulate_grad", "tsum", "tmean", "tmax", "static_result_shape",
+    "elwise_op", "accumulate_grad", "tsum", "tmean", "tmax", "static_result_shape", "bias_relu_forward",
+    "bias_relu_backward", "softmax_log_mul_mean_forward", "softmax_log_mul_mean_backward",
 ]

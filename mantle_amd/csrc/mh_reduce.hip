@@ -568,16 +568,22 @@ static inline size_t pad64(size_t v) { return (v + 63) & ~(size_t)63; }
 
 // Rows (C == 1): B <= 64 one thread (or an LDS tile) per row, B < 2048 one wavefront per
 // row, longer rows kRowChunk-element block chunks whose partials reduce again the same way.
+// A pass over partials (`combine`) takes rows of up to kCombineMax elements in one block
+// each (one launch for the combine instead of a chain).
+constexpr int64_t kCombineMax = 16384;
 static inline bool rows_chunked(int64_t B) { return B >= 2048; }
-static inline int64_t row_chunks(int64_t B) { return (B + kRowChunk - 1) / kRowChunk; }
+static inline int64_t row_chunks(int64_t B, bool combine) {
+    if (combine && B <= kCombineMax) return 1;
+    return (B + kRowChunk - 1) / kRowChunk;
+}
 
 // Scratch floats of the row path: every level's partials, one after another.
 template <class R>
-static size_t row_tmp_floats(int64_t A, int64_t B) {
+static size_t row_tmp_floats(int64_t A, int64_t B, bool combine = false) {
     if (!rows_chunked(B)) return 0;
-    const int64_t S = row_chunks(B);
+    const int64_t S = row_chunks(B, combine);
     if (S == 1) return 0;
-    return pad64((size_t)(A * S) * part_words<R>()) + row_tmp_floats<R>(A, S);
+    return pad64((size_t)(A * S) * part_words<R>()) + row_tmp_floats<R>(A, S, true);
 }
 
 // Scratch floats a reduction of [A, B, C] needs for its partials.
@@ -617,7 +623,7 @@ struct PartLoader<RMaxCnt> {
 // nosplit: the combine stage over column-split partials runs as a single pass (tmp unused).
 template <class R, class LD>
 static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C, float* out,
-                    float* out2, float div, float* tmp, bool nosplit = false) {
+                    float* out2, float div, float* tmp, bool nosplit = false, bool combine = false) {
     if (A * C == 0) return MH_OK;
     hipStream_t st = ctx().stream;
     if (C == 1) {
@@ -647,15 +653,16 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
             else hipLaunchKernelGGL((k_rows_wave<R, LD, false>), g, b, 0, st, ld, A, (int64_t)1, B, B, out, out2, epi, div, tmp);
             return MH_OK;
         }
-        const int64_t S = row_chunks(B);
+        const int64_t S = row_chunks(B, combine);
+        const int64_t L = S == 1 ? B : kRowChunk;
         const int64_t nv = A * S;
         dim3 g((unsigned)nv), b(kRThreads);
-        if (vec) hipLaunchKernelGGL((k_rows_block<R, LD, true>), g, b, 0, st, ld, S, B, kRowChunk, out, out2, epi, div, tmp, nv);
-        else hipLaunchKernelGGL((k_rows_block<R, LD, false>), g, b, 0, st, ld, S, B, kRowChunk, out, out2, epi, div, tmp, nv);
+        if (vec) hipLaunchKernelGGL((k_rows_block<R, LD, true>), g, b, 0, st, ld, S, B, L, out, out2, epi, div, tmp, nv);
+        else hipLaunchKernelGGL((k_rows_block<R, LD, false>), g, b, 0, st, ld, S, B, L, out, out2, epi, div, tmp, nv);
         if (S > 1) {  // the chunk partials [A, S] reduce again along their rows
             using PL = PartLoader<R>;
             return reduce_t<R, typename PL::type>(PL::make(tmp, nv), true, epi, A, S, 1, out, out2, div,
-                                                  tmp + pad64((size_t)nv * part_words<R>()));
+                                                  tmp + pad64((size_t)nv * part_words<R>()), false, true);
         }
         return MH_OK;
     }

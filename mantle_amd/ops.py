@@ -281,3 +281,38 @@ def backward_op_both(op: int, ug: Tensor, t1: Tensor, t2: Tensor, grad1: Optiona
         return
     _lib.call("mh_binary_bwd_accum2", int(op), grad1.ptr if grad1 is not None else None,
               grad2.ptr if grad2 is not None else None, ug.ptr, t1.ptr, t2.ptr, t1.shape().c())
+
+
+# ---------------------------------------------------------------------------------------
+# fused graph patterns (no single reference counterpart)
+# ---------------------------------------------------------------------------------------
+def bias_relu_forward(y: Tensor, r: Tensor, x: Tensor, bias: Tensor) -> None:
+    """The graph ADD(x, bias) -> RELU in one pass: y = x + bias (broadcast), r = relu(y)."""
+    _lib.call("mh_bias_relu_fwd", y.ptr, r.ptr, x.ptr, x.shape().c(), bias.ptr, bias.shape().c())
+
+
+def bias_relu_backward(ug: Tensor, y: Tensor, bias_shape, grad_x: Optional[Tensor], grad_bias: Optional[Tensor],
+                       grad_y: Optional[Tensor] = None) -> None:
+    """Backward of ADD(x, bias) -> RELU from the grad ug of r: grad_y (if kept) += relu'(y) * ug,
+    then grad_x += grad_y and grad_bias += its sum over the broadcast axes of bias_shape."""
+    _lib.call("mh_bias_relu_bwd_accum", grad_y.ptr if grad_y is not None else None,
+              grad_x.ptr if grad_x is not None else None, grad_bias.ptr if grad_bias is not None else None,
+              y.ptr, ug.ptr, y.shape().c(), as_shape(bias_shape).c())
+
+
+def softmax_log_mul_mean_forward(loss: Tensor, x: Tensor, target: Tensor) -> None:
+    """The graph MAX -> SUB -> EXP -> SUM -> DIV -> LOG -> MUL(target) -> MEAN over the rows of
+    x [rows, classes] in one pass (Softmax, mantle/nn/activations.mojo:74-87, then LOG, MUL,
+    MEAN): loss[0] = mean(log(softmax(x)) * target)."""
+    rows, classes = x.shape().dims
+    if target.shape() != x.shape() or loss.num_elements() != 1:
+        raise _lib.MantleHipError(_lib.ERR_SHAPE, "target must match x and loss must hold one element")
+    _lib.call("mh_softmax_log_mul_mean_fwd", loss.ptr, x.ptr, target.ptr, rows, classes)
+
+
+def softmax_log_mul_mean_backward(grad_x: Tensor, x: Tensor, target: Tensor, ug: Tensor) -> None:
+    """Backward of the same graph from the loss grad ug (shape (1)): grad_x += d loss / dx."""
+    rows, classes = x.shape().dims
+    if target.shape() != x.shape() or grad_x.shape() != x.shape() or ug.num_elements() != 1:
+        raise _lib.MantleHipError(_lib.ERR_SHAPE, "grad_x and target must match x; ug holds one element")
+    _lib.call("mh_softmax_log_mul_mean_bwd_accum", grad_x.ptr, x.ptr, target.ptr, ug.ptr, rows, classes)

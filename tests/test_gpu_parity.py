@@ -414,3 +414,57 @@ def test_config5_classifier_chain_small(gpu):
     # the loss grad is seeded with 1.0, so no backward value depends on the loss sum
     for k in ("logits", "max", "xm", "e", "s", "sm", "lp", "t"):
         assert_ulp(gg[k], go[k], 2, f"grad {k}")
+
+
+SMLM_CASES = [(4099, 10), (1, 1), (3, 2), (257, 3), (1000, 16), (513, 17), (300, 32), (64, 1), (7, 5), (2048, 10)]
+
+
+@pytest.mark.parametrize("rows,classes", SMLM_CASES, ids=[f"{r}x{c}" for r, c in SMLM_CASES])
+@pytest.mark.parametrize("ugv", [1.0, -0.37])
+def test_fused_softmax_log_mul_mean(gpu, rows, classes, ugv):
+    """mh_softmax_log_mul_mean_fwd / _bwd_accum against the op-by-op graph: the loss in the sum
+    class, the gradient bit-exact -- including its accumulation into a non-zero grad_x, which
+    the graph does as grad_x + g_xm (SUB) and then + the MAX routing. Rows shorter than the
+    oracle's 32 SIMD lanes sum in element order on every path, so the oracle is the
+    reference; at 32 classes its row sums follow the lane order, so the bit-exact reference
+    is the GPU op-by-op chain and the oracle is met within the sum class."""
+    m = gpu.m
+    logits = synth.normal((rows, classes), 0, 2, 61)
+    if classes > 1:
+        synth.inject_ties(logits, 1, 62)
+    cls = synth.integers((rows,), 0, classes, 63)
+    onehot = np.zeros((rows, classes), np.float32)
+    onehot[np.arange(rows), cls] = 1.0
+    g = Graph(config5_nodes(), ["logits"])
+    seed = np.array([ugv], np.float32)
+    vo = g.forward(ORC, {"logits": logits, "onehot": onehot})
+    go = g.backward(ORC, vo, seed)
+    ref_eng, vr, gr = ORC, vo, go
+    if classes >= 32:
+        ref_eng = gpu
+        vr = g.forward(gpu, {"logits": logits, "onehot": onehot})
+        gr = g.backward(gpu, vr, seed)
+        np.testing.assert_allclose(gr["logits"], go["logits"], rtol=1e-4,
+                                   atol=1e-4 * float(np.abs(go["logits"]).max()))
+    tl, to = gpu.T(logits), gpu.T(onehot)
+    loss = m.Tensor(m.TensorShape(1))
+    m.softmax_log_mul_mean_forward(loss, tl, to)
+    t64 = vo["t"].astype(np.float64)
+    assert_sum_close(loss.to_numpy(), vo["loss"], np.array([t64.mean()]), "fused loss",
+                     terms_abs=np.array([np.abs(t64).mean()]))
+    g0 = synth.normal((rows, classes), 0, 1, 64)
+    tg = gpu.T(g0)
+    m.softmax_log_mul_mean_backward(tg, tl, to, gpu.T(seed))
+    exp = ref_eng.backward(0, OPS["SUB"], gr["xm"], logits, vr["max"], grad=g0)
+    exp = ref_eng.backward(0, OPS["MAX"], gr["max"], logits, axis=1, grad=exp)
+    assert_bitexact(tg.to_numpy(), exp, "fused grad, accumulated")
+    tz = m.Tensor(m.TensorShape(rows, classes))
+    m.softmax_log_mul_mean_backward(tz, tl, to, gpu.T(seed))
+    assert_bitexact(tz.to_numpy(), gr["logits"], "fused grad from zero")
+
+
+def test_fused_softmax_rejects_wide_rows(gpu):
+    m = gpu.m
+    x = gpu.T(np.zeros((4, 33), np.float32))
+    with pytest.raises(m.MantleHipError):
+        m.softmax_log_mul_mean_forward(m.Tensor(m.TensorShape(1)), x, x)
