@@ -14,9 +14,9 @@
 // tail loop and the op-by-op GPU path do for rows this short). Only the final MEAN over all
 // elements sums in another order (the rtol class).
 //
-// One thread owns one row; a block of 256 threads stages RB rows (256, or 128 when 32-wide
-// rows would exceed 64 KB of LDS) of each operand in LDS with coalesced loads (rows of up to
-// 32 classes).
+// One thread owns one row, held in registers (loops unrolled to 8, 16 or 32 classes); a block
+// of 256 threads stages RB rows (256, fewer when wide rows would exceed 64 KB of LDS) of each
+// operand in LDS with coalesced loads (rows of up to 32 classes).
 #include <cfloat>
 
 #include "mh_internal.h"
@@ -58,7 +58,9 @@ __device__ __forceinline__ float block_sum_rows(float v, float* ws) {
 }
 
 // Forward: part[block] = sum over the block's rows of sum_j log(softmax(x)_j) * target_j.
-// LDS: x tile (overwritten by e), target tile.
+// The row lives in registers (KM >= K: loops unrolled, elements j >= K skipped); LDS only
+// stages the coalesced loads.
+template <int KM>
 __global__ void __launch_bounds__(kSThreads)
     k_smlm_fwd(const float* __restrict__ x, const float* __restrict__ tg, int64_t rows, int K, int rb, bool al,
                float* __restrict__ part) {
@@ -75,20 +77,28 @@ __global__ void __launch_bounds__(kSThreads)
     float rowsum = 0.0f;
     const int t = threadIdx.x;
     if (t < nr) {
-        float* xr = xs + t * K;
-        const float* tr = ts + t * K;
+        float xr[KM], e[KM];
+#pragma unroll
+        for (int j = 0; j < KM; ++j) xr[j] = j < K ? xs[t * K + j] : 0.0f;
         float m = -FLT_MAX;  // MAX.forward: reduce with max_simd from min_finite
-        for (int j = 0; j < K; ++j) m = m > xr[j] ? m : xr[j];
-        float s = 0.0f;  // SUM.forward over the row
-        for (int j = 0; j < K; ++j) {
-            const float e = mexp(xr[j] - m);  // SUB.forward, EXP.forward
-            xr[j] = e;
-            s = s + e;
+#pragma unroll
+        for (int j = 0; j < KM; ++j)
+            if (j < K) m = m > xr[j] ? m : xr[j];
+        float s = 0.0f;  // SUM.forward over the row, in element order
+#pragma unroll
+        for (int j = 0; j < KM; ++j) {
+            if (j < K) {
+                e[j] = mexp(xr[j] - m);  // SUB.forward, EXP.forward
+                s = s + e[j];
+            }
         }
-        for (int j = 0; j < K; ++j) {
-            const float sm = xr[j] / s;    // DIV.forward
-            const float lp = mlog(sm);     // LOG.forward
-            rowsum = rowsum + lp * tr[j];  // MUL.forward, then the MEAN's sum
+#pragma unroll
+        for (int j = 0; j < KM; ++j) {
+            if (j < K) {
+                const float sm = e[j] / s;                 // DIV.forward
+                const float lp = mlog(sm);                 // LOG.forward
+                rowsum = rowsum + lp * ts[t * K + j];      // MUL.forward, then the MEAN's sum
+            }
         }
     }
     const float tot = block_sum_rows(rowsum, ws);
@@ -106,7 +116,8 @@ __global__ void __launch_bounds__(kSThreads)
 //   SUB 0 : grad_x = grad_x + g_xm
 //   SUB 1 : g_max = 0 + (-sum_j g_xm_j)
 //   MAX   : grad_x = grad_x + (x == m ? fl(1/count) * g_max : 0)
-// LDS: x tile, target tile (overwritten by g_e), grad tile, work tile (e, then g_xm).
+// Registers hold the row (KM >= K); LDS stages x, target and grad_x (written back in place).
+template <int KM>
 __global__ void __launch_bounds__(kSThreads)
     k_smlm_bwd(float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ tg,
                const float* __restrict__ ug, int64_t rows, int K, int rb, bool al, float cmean) {
@@ -114,7 +125,6 @@ __global__ void __launch_bounds__(kSThreads)
     float* xs = reinterpret_cast<float*>(smem4);
     float* ts = xs + rb * K;
     float* gs = ts + rb * K;
-    float* ws = gs + rb * K;
     const int64_t r0 = (int64_t)blockIdx.x * rb;
     const int nr = (int)((rows - r0) < rb ? (rows - r0) : rb);
     const int64_t base = r0 * K;
@@ -125,43 +135,49 @@ __global__ void __launch_bounds__(kSThreads)
     __syncthreads();
     const int t = threadIdx.x;
     if (t < nr) {
-        const float* xr = xs + t * K;
-        float* tr = ts + t * K;
-        float* gr = gs + t * K;
-        float* wr = ws + t * K;
+        float xr[KM], e[KM], w[KM];
+#pragma unroll
+        for (int j = 0; j < KM; ++j) xr[j] = j < K ? xs[t * K + j] : 0.0f;
         // forward values: the row max as MAX.forward takes it (max_simd from min_finite),
         // e = exp(x - m), s = sum e; and, as MAX.backward recomputes it, the max with its
         // count (an element that is neither above nor below the running max -- equal, or
         // NaN -- adds to the count)
         float m = -FLT_MAX, mb = -FLT_MAX;
         uint32_t c = 0;
-        for (int j = 0; j < K; ++j) {
-            const float v = xr[j];
-            m = m > v ? m : v;
-            if (mb > v) {
-            } else if (v > mb) {
-                mb = v;
-                c = 1;
-            } else {
-                c += 1;
+#pragma unroll
+        for (int j = 0; j < KM; ++j) {
+            if (j < K) {
+                const float v = xr[j];
+                m = m > v ? m : v;
+                if (mb > v) {
+                } else if (v > mb) {
+                    mb = v;
+                    c = 1;
+                } else {
+                    c += 1;
+                }
             }
         }
         float s = 0.0f;
-        for (int j = 0; j < K; ++j) {
-            const float e = mexp(xr[j] - m);
-            wr[j] = e;
-            s = s + e;
+#pragma unroll
+        for (int j = 0; j < KM; ++j) {
+            if (j < K) {
+                e[j] = mexp(xr[j] - m);
+                s = s + e[j];
+            }
         }
         const float gt = 0.0f + cmean * ug[0];  // MEAN backward (all elements)
         const float s2 = s * s;
         float acc = 0.0f;
-        for (int j = 0; j < K; ++j) {
-            const float e = wr[j];
-            const float sm = e / s;
-            const float glp = 0.0f + gt * tr[j];  // MUL backward, operand 0
-            const float gsm = 0.0f + glp / sm;    // LOG backward
-            tr[j] = 0.0f + gsm / s;               // DIV backward, operand 0: g_e
-            acc = acc + ((-e) / s2) * gsm;        // DIV backward, operand 1 (row sum)
+#pragma unroll
+        for (int j = 0; j < KM; ++j) {
+            if (j < K) {
+                const float sm = e[j] / s;
+                const float glp = 0.0f + gt * ts[t * K + j];  // MUL backward, operand 0
+                const float gsm = 0.0f + glp / sm;            // LOG backward
+                w[j] = 0.0f + gsm / s;                        // DIV backward, operand 0: g_e
+                acc = acc + ((-e[j]) / s2) * gsm;             // DIV backward, operand 1
+            }
         }
         const float gS = 0.0f + acc;
         // SUM backward: rg = 1 * g_s, except over a size-1 axis (K == 1), where the reduced
@@ -169,17 +185,22 @@ __global__ void __launch_bounds__(kSThreads)
         // (tensorutils.mojo:380-393): rg = (1 * g_s) * g_s
         const float rgs = K == 1 ? (1.0f * gS) * gS : 1.0f * gS;
         float acc2 = 0.0f;
-        for (int j = 0; j < K; ++j) {
-            const float ge = tr[j] + rgs;  // SUM backward
-            const float gxm = 0.0f + wr[j] * ge;  // EXP backward (wr = exp(xm))
-            wr[j] = gxm;
-            acc2 = acc2 + gxm;
+#pragma unroll
+        for (int j = 0; j < KM; ++j) {
+            if (j < K) {
+                const float ge = w[j] + rgs;  // SUM backward
+                w[j] = 0.0f + e[j] * ge;      // EXP backward: g_xm
+                acc2 = acc2 + w[j];
+            }
         }
-        const float gmax = 0.0f + (-acc2);           // SUB backward, operand 1
-        const float sg = (1.0f / (float)c) * gmax;   // MAX backward factor
-        for (int j = 0; j < K; ++j) {
-            const float a = gr[j] + wr[j];               // SUB backward, operand 0
-            gr[j] = a + (xr[j] == mb ? sg : 0.0f);       // MAX backward
+        const float gmax = 0.0f + (-acc2);          // SUB backward, operand 1
+        const float sg = (1.0f / (float)c) * gmax;  // MAX backward factor
+#pragma unroll
+        for (int j = 0; j < KM; ++j) {
+            if (j < K) {
+                const float a = gs[t * K + j] + w[j];           // SUB backward, operand 0
+                gs[t * K + j] = a + (xr[j] == mb ? sg : 0.0f);  // MAX backward
+            }
         }
     }
     __syncthreads();
@@ -227,8 +248,11 @@ int mh_softmax_log_mul_mean_fwd(float* loss, const float* x, const float* target
     MH_TRY(scratch((np + t + 64) * sizeof(float), reinterpret_cast<void**>(&part)));
     const bool al = al16s(x) && al16s(target);
     const size_t lds = 2 * (size_t)rb * (size_t)classes * sizeof(float);
-    hipLaunchKernelGGL(k_smlm_fwd, dim3((unsigned)nblocks), dim3(kSThreads), lds, ctx().stream, x, target, rows,
-                       (int)classes, rb, al, part);
+    dim3 g((unsigned)nblocks), b(kSThreads);
+    hipStream_t st = ctx().stream;
+    if (classes <= 8) hipLaunchKernelGGL(k_smlm_fwd<8>, g, b, lds, st, x, target, rows, (int)classes, rb, al, part);
+    else if (classes <= 16) hipLaunchKernelGGL(k_smlm_fwd<16>, g, b, lds, st, x, target, rows, (int)classes, rb, al, part);
+    else hipLaunchKernelGGL(k_smlm_fwd<32>, g, b, lds, st, x, target, rows, (int)classes, rb, al, part);
     // MEAN.forward: the sum of every element divided by f32(N)
     MH_TRY(reduce_abc(RED_SUM, EPI_MEAN, part, 1, nblocks, 1, loss, nullptr, (float)n, part + np));
     return finish("mh_softmax_log_mul_mean_fwd");
@@ -241,14 +265,20 @@ int mh_softmax_log_mul_mean_bwd_accum(float* grad_x, const float* x, const float
     if (n == 0) return MH_OK;
     if (!grad_x || !ug) return fail(MH_ERR_NULL, "mh_softmax_log_mul_mean_bwd_accum: null tensor");
     MH_TRY(require_init());
-    const int rb = rows_per_block(4, classes);
+    const int rb = rows_per_block(3, classes);
     const int64_t nblocks = (rows + rb - 1) / rb;
     if (nblocks > 0x7fffffff) return fail(MH_ERR_OVERFLOW, "mh_softmax_log_mul_mean_bwd_accum: too many rows");
     const bool al = al16s(x) && al16s(target) && al16s(grad_x);
-    const size_t lds = 4 * (size_t)rb * (size_t)classes * sizeof(float);
+    const size_t lds = 3 * (size_t)rb * (size_t)classes * sizeof(float);
     const float cmean = (float)(1.0 / (double)n);  // MEAN.backward, basics.mojo:470-487
-    hipLaunchKernelGGL(k_smlm_bwd, dim3((unsigned)nblocks), dim3(kSThreads), lds, ctx().stream, grad_x, x, target,
-                       ug, rows, (int)classes, rb, al, cmean);
+    dim3 g((unsigned)nblocks), b(kSThreads);
+    hipStream_t st = ctx().stream;
+    if (classes <= 8)
+        hipLaunchKernelGGL(k_smlm_bwd<8>, g, b, lds, st, grad_x, x, target, ug, rows, (int)classes, rb, al, cmean);
+    else if (classes <= 16)
+        hipLaunchKernelGGL(k_smlm_bwd<16>, g, b, lds, st, grad_x, x, target, ug, rows, (int)classes, rb, al, cmean);
+    else
+        hipLaunchKernelGGL(k_smlm_bwd<32>, g, b, lds, st, grad_x, x, target, ug, rows, (int)classes, rb, al, cmean);
     return finish("mh_softmax_log_mul_mean_bwd_accum");
 }
 
