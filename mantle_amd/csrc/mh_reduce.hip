@@ -7,8 +7,10 @@
 //   C == 1, B < 2048: one wavefront (64 lanes) per row, 128-bit loads, butterfly shuffle;
 //   C == 1, B >= 2048: 2048-element chunks, one 4-wave block each (two quads per thread),
 //                     whose partials reduce again along the row the same way;
+//   C  > 1, C % 4 == 0 and >= 1024 columns: one thread per column quad, 128-row chunks;
 //   C  > 1, C % 4 == 0 and >= 128 columns: a block per (strip of 64 column quads, chunk of
-//                     rows), its four waves interleaving the rows, combined through LDS;
+//                     rows), its four waves interleaving the rows, combined through LDS (also
+//                     the combine pass of the wide form);
 //   C  > 1 otherwise  : one thread per output column (a quad of columns when C % 4 == 0);
 //   in both column forms the rows split across blocks when that is needed to fill the chip,
 //   and a second pass combines the split partials in fixed split order.
@@ -559,6 +561,27 @@ static ColSplit strip_split(int64_t A, int64_t B, int64_t C, int64_t* nstrips) {
     return cs;
 }
 
+// Wide strided reductions (C % 4 == 0, at least 256 column quads): one thread per column
+// quad (k_cols, 4 rows in flight), 128 rows per block when the chip is full anyway: about 2
+// blocks per CU, each thread with a long run of rows, streamed best in a sweep of layouts
+// on gfx950 (blocks of few rows, or a strip of 64 quads per block, were 5-10 % slower).
+static bool use_wide_cols(int64_t C, bool vec) { return vec && C % 4 == 0 && (C >> 2) >= 256; }
+static ColSplit wide_split(int64_t A, int64_t B, int64_t C) {
+    ColSplit cs;
+    cs.vec = true;
+    const int64_t bx = (A * (C >> 2) + kRThreads - 1) / kRThreads;
+    const int64_t target = 2 * (int64_t)ctx().num_cus;
+    int64_t S = (target + bx - 1) / bx;
+    int64_t maxS = B / 32;
+    if (maxS < 1) maxS = 1;
+    if (S > maxS) S = maxS;
+    if (S > 65535) S = 65535;
+    if (S < 1) S = 1;
+    cs.rps = (B + S - 1) / S;
+    cs.S = (B + cs.rps - 1) / cs.rps;
+    return cs;
+}
+
 template <class R>
 static constexpr int part_words() {
     return sizeof(typename R::T) == 4 ? 1 : 2;
@@ -593,6 +616,10 @@ static size_t tmp_floats_t(int64_t A, int64_t B, int64_t C, bool vec_ok) {
     if (C == 1) return row_tmp_floats<R>(A, B);
     // the largest split any column launcher may pick (the choice depends on alignment)
     int64_t S = 1;
+    if (use_wide_cols(C, vec_ok)) {
+        ColSplit cw = wide_split(A, B, C);
+        S = cw.S > S ? cw.S : S;
+    }
     if (use_strip(C, vec_ok)) {
         int64_t ns;
         ColSplit cs = strip_split(A, B, C, &ns);
@@ -663,6 +690,19 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
             using PL = PartLoader<R>;
             return reduce_t<R, typename PL::type>(PL::make(tmp, nv), true, epi, A, S, 1, out, out2, div,
                                                   tmp + pad64((size_t)nv * part_words<R>()), false, true);
+        }
+        return MH_OK;
+    }
+    if (!nosplit && use_wide_cols(C, vec_ok)) {
+        ColSplit cs = wide_split(A, B, C);
+        const int64_t items = A * C / 4;
+        dim3 g((unsigned)((items + kRThreads - 1) / kRThreads), (unsigned)cs.S), b(kRThreads);
+        hipLaunchKernelGGL((k_cols<R, LD, true>), g, b, 0, st, ld, A, B, C, cs.rps, cs.S, out, out2, epi, div, tmp);
+        if (cs.S > 1) {  // combine the split partials with the strip kernel (4 waves per quad)
+            using PL = PartLoader<R>;
+            const int64_t np = cs.S * A * C;
+            return reduce_t<R, typename PL::type>(PL::make(tmp, np), true, epi, 1, cs.S, A * C, out, out2, div,
+                                                  nullptr, true);
         }
         return MH_OK;
     }
