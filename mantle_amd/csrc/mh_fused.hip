@@ -7,14 +7,16 @@
 // Backward: with x viewed as [N, C, S] and the bias indexed by C alone (NCHW bias
 // [1, C, 1, 1], or any bias that is constant over a contiguous inner run S), one wavefront
 // per (plane, chunk) computes gy = g_y + relu'(y) * ug, accumulates it into grad_x (and g_y
-// when the caller keeps it), and writes the chunk's sum of gy; a second pass adds those
-// partials into grad_bias in a fixed order. Shapes outside that form run the op-by-op kernels.
+// when the caller keeps it), and writes the chunk's sum of gy; the last wave of each channel
+// adds that channel's partials into grad_bias in a fixed order, in the same launch. Shapes
+// outside that form run the op-by-op kernels.
 #include "mh_internal.h"
 #include "mh_math.h"
 
 namespace mh {
 
 constexpr int kFThreads = 256;
+constexpr int64_t kTicketStride = 32;  // one 128-byte line per channel counter
 
 static inline bool al16f(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -92,13 +94,18 @@ __global__ void __launch_bounds__(kFThreads)
 //   rg = (y > 0 ? 1 : 0) * ug            RELU.backward (mlops.mojo:118-123)
 //   g  = g_y + rg  (0 + rg without g_y)  accumulate_grad into the grad of y (ops.mojo:405)
 //   grad_x = grad_x + g                  ADD backward_op, operand 0 (ops.mojo:457-461)
-//   part[(n * K + k) * C + c] = sum of g over the chunk (for ADD's operand-1 un-broadcast):
-//   each lane sums its quads in order, then a butterfly across the wave.
+//   part[(n * K + k) * C + c] = sum of g over the chunk: each lane sums its quads in order,
+//   then a butterfly across the wave.
+// The bias gradient (ADD's operand-1 un-broadcast) completes in the same launch: every wave
+// publishes its partial with an agent-scope store, waits for that store to complete, then
+// takes a ticket on its channel; the wave that takes the channel's last ticket reads the
+// channel's N * K partials with agent-scope loads, adds them in a fixed order into
+// grad_bias[c] and resets the ticket. No wave waits for another.
 template <bool HAS_GY, bool HAS_GX, bool HAS_PART>
 __global__ void __launch_bounds__(kFThreads)
     k_bias_relu_bwd_planes(float* __restrict__ gy, float* __restrict__ gx, const float* __restrict__ y,
                            const float* __restrict__ ug, int64_t C, int64_t Sq, int64_t QC, int64_t K,
-                           int64_t nwaves, float* __restrict__ part) {
+                           int64_t nwaves, float* part, uint32_t* tickets, float* grad_bias) {
     const int lane = threadIdx.x & 63;
     const int64_t v = (int64_t)blockIdx.x * (kFThreads / 64) + (threadIdx.x >> 6);
     if (v >= nwaves) return;  // uniform per wavefront; no barrier follows
@@ -128,9 +135,28 @@ __global__ void __launch_bounds__(kFThreads)
     if (HAS_PART) {
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
+        const int64_t n = p / C, c = p - n * C;
+        const int64_t nper = nwaves / C;  // partials per channel: N * K
+        uint32_t ticket = 0;
         if (lane == 0) {
-            const int64_t n = p / C, c = p - n * C;
-            part[(n * K + k) * C + c] = acc;
+            // The partial is an agent-scope store (coherent across XCDs by itself), so the
+            // ticket needs only to follow its completion, not a release of every earlier
+            // store (which would write back this XCD's whole L2 once per wave).
+            __hip_atomic_store(&part[(n * K + k) * C + c], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);
+            ticket = __hip_atomic_fetch_add(&tickets[c * kTicketStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        ticket = __shfl(ticket, 0);
+        if (ticket == (uint32_t)(nper - 1)) {  // the channel's last partial: sum them all
+            float s = 0.0f;
+            for (int64_t i = lane; i < nper; i += 64)
+                s = s + __hip_atomic_load(&part[i * C + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) s = s + __shfl_xor(s, m);
+            if (lane == 0) {
+                grad_bias[c] = grad_bias[c] + s;
+                __hip_atomic_store(&tickets[c * kTicketStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
 }
@@ -225,19 +251,17 @@ int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const fl
     const int64_t nblocks = (nwaves + 3) / 4;
     if (planes && nblocks <= 0x7fffffff) {
         float* part = nullptr;
-        float* tmp = nullptr;
+        uint32_t* tk = nullptr;
         const bool has_part = grad_bias != nullptr;
         if (has_part) {
-            const size_t np = ((size_t)(N * K * C) + 63) & ~(size_t)63;
-            const size_t t = reduce_abc_tmp_floats(RED_SUM, 1, N * K, C);
-            MH_TRY(scratch((np + t + 64) * sizeof(float), reinterpret_cast<void**>(&part)));
-            tmp = part + np;
+            MH_TRY(scratch(((size_t)(N * K * C) + 64) * sizeof(float), reinterpret_cast<void**>(&part)));
+            MH_TRY(tickets(C * kTicketStride, &tk));
         }
         hipStream_t st = ctx().stream;
         dim3 g((unsigned)nblocks), b(kFThreads);
 #define MH_BRB(GY, GX, PT)                                                                                  \
     hipLaunchKernelGGL((k_bias_relu_bwd_planes<GY, GX, PT>), g, b, 0, st, g_y, grad_x, y, ug, C, Sq, QC, K, nwaves, \
-               part)
+                       part, tk, grad_bias)
         const int sel = (g_y ? 4 : 0) | (grad_x ? 2 : 0) | (has_part ? 1 : 0);
         switch (sel) {
             case 0: return MH_OK;  // nothing to produce
@@ -250,8 +274,6 @@ int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const fl
             default: MH_BRB(true, true, true); break;
         }
 #undef MH_BRB
-        if (has_part)  // grad_bias[c] += sum over (n, k) of part[(n * K + k) * C + c]
-            MH_TRY(reduce_abc(RED_SUM, EPI_ACCUM, part, 1, N * K, C, grad_bias, nullptr, 0.0f, tmp));
         return finish("mh_bias_relu_bwd_accum");
     }
     // other shapes (a Linear layer's [rows, features] bias, unaligned views): op by op

@@ -24,6 +24,8 @@ struct Context {
     size_t scratch_bytes = 0;
     void* stage = nullptr;  // library-owned staging for materialised intermediates
     size_t stage_bytes = 0;
+    uint32_t* tickets = nullptr;  // zeroed arrival counters of single-launch reductions
+    int64_t ntickets = 0;
     int num_cus = 256;
 };
 Context& ctx();
@@ -57,6 +59,9 @@ int finish(const char* what);
 int scratch(size_t bytes, void** out);
 // A second library buffer for intermediates that live across calls using scratch().
 int stage(size_t bytes, void** out);
+// At least n zeroed arrival counters. A kernel that takes tickets leaves every one it
+// touched at zero again when it ends (the last arrival resets it).
+int tickets(int64_t n, uint32_t** out);
 
 // ---------------------------------------------------------------------------------------
 // shapes

@@ -72,6 +72,31 @@ static int grow(void** buf, size_t* have, size_t bytes, void** out) {
 int scratch(size_t bytes, void** out) { return grow(&ctx().scratch, &ctx().scratch_bytes, bytes, out); }
 int stage(size_t bytes, void** out) { return grow(&ctx().stage, &ctx().stage_bytes, bytes, out); }
 
+static int launch_fill(float* t, float v, int64_t n);
+
+int tickets(int64_t n, uint32_t** out) {
+    Context& c = ctx();
+    if (n > c.ntickets) {
+        int64_t want = n < 65536 ? 65536 : n;
+        if (c.tickets) {
+            MH_HIP(hipStreamSynchronize(c.stream));
+            MH_HIP(hipFree(c.tickets));
+            c.tickets = nullptr;
+            c.ntickets = 0;
+        }
+        MH_HIP(hipMalloc(reinterpret_cast<void**>(&c.tickets), (size_t)want * sizeof(uint32_t)));
+        c.ntickets = want;
+        // all-zero bits: a fill kernel of 0.0f (no memset node if a caller captures a graph)
+        const uint64_t saved = c.flags;
+        c.flags |= MH_INIT_ASYNC;
+        const int rc = launch_fill(reinterpret_cast<float*>(c.tickets), 0.0f, want);
+        c.flags = saved;
+        MH_TRY(rc);
+    }
+    *out = c.tickets;
+    return MH_OK;
+}
+
 // ---------------------------------------------------------------------------------------
 // shapes
 // ---------------------------------------------------------------------------------------
@@ -369,6 +394,9 @@ int mh_shutdown(void) {
     if (c.stage) MH_HIP(hipFree(c.stage));
     c.stage = nullptr;
     c.stage_bytes = 0;
+    if (c.tickets) MH_HIP(hipFree(c.tickets));
+    c.tickets = nullptr;
+    c.ntickets = 0;
     MH_HIP(hipStreamDestroy(c.stream));
     c.stream = nullptr;
     c.initialized = false;
