@@ -537,6 +537,59 @@ C2_KERNEL = {"ADD.bwd": "void mh::k_bwd2_same4<0>", "SUB.bwd": "void mh::k_bwd2_
              "POW.bwd_exp": "void mh::k_rows_wave<mh::RSum, mh::LdPowGrad,"}
 
 
+def stats_summary(stats_csv, command, bench_json=None):
+    """Writes profiles/bench_kernel_stats.md from a rocprofv3 --kernel-trace --stats
+    kernel_stats.csv (durations in microseconds), with the command that made it."""
+    rows = list(csv.DictReader(open(stats_csv, newline="")))
+    lines = ["# rocprofv3 kernel statistics: bench.py (config 2 headline step + configs 3, 4, 5 and the copy reference)",
+             "", "Command (run from the repository root on one MI355X):", "", "```", command, "```", "",
+             "Durations in microseconds, as rocprofv3 `--stats` reports them (`*_kernel_stats.csv`). Counts include the",
+             "bench's warm-up launches, the Infinity Cache flush before each small op (`k_rows_block<RSum, LdPlain>` over",
+             "a 1 GiB buffer and its combine passes), gradient zeroing (`k_fill`) and input generation (`k_rand`).", "",
+             "| Kernel | Calls | Avg us | Min us | Max us | % time |", "|---|---:|---:|---:|---:|---:|"]
+    for r in rows:
+        name = r["Name"].replace("|", "\\|")
+        if len(name) > 120:
+            name = name[:117] + "..."
+        lines.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                     f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
+    if bench_json:
+        rf = json.load(open(bench_json))["roofline"]
+        lines += ["", "## Dominant config-2 kernel", "",
+                  f"In the bench run of the same tree, `bench.py` (HIP events on the library stream) timed `{rf['kernel']}` "
+                  f"at {rf['avg_launch_ms'] * 1e3:.1f} us per launch: {rf['achieved']} GB/s of algorithmic bytes "
+                  f"({rf['bytes_per_launch']} B per launch), {rf['frac']:.3f} of 8 TB/s."]
+    os.makedirs(os.path.dirname(TRAFFIC_JSON), exist_ok=True)
+    with open(os.path.join(os.path.dirname(TRAFFIC_JSON), "bench_kernel_stats.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
+def traffic_summary_md(commands):
+    """Writes profiles/traffic.md from profiles/traffic.json: the config-2 kernels' HBM bytes
+    against their algorithmic bytes."""
+    t = json.load(open(TRAFFIC_JSON))
+    alg = dict(step_plan())
+    lines = ["# HBM traffic per dispatch (rocprofv3 FETCH_SIZE / WRITE_SIZE)", "",
+             "Commands (run from the repository root on one MI355X; one counter per run):", "", "```", *commands, "```", "",
+             f"Calibration: the library's copy kernel `k_copy` over a 1 GiB buffer (reads 1 GiB, writes 1 GiB) counts "
+             f"FETCH_SIZE = {1 / t['fetch_scale']:.4f} x and WRITE_SIZE = {1 / t['write_scale']:.4f} x its bytes, so "
+             f"FETCH_SIZE is scaled by {t['fetch_scale']:.4f} and WRITE_SIZE by {t['write_scale']:.4f}. Values are medians "
+             "over the dispatches of each kernel's largest launch (for config 2, the 2^28-element one); "
+             "`profiles/traffic.json` holds every kernel and launch size, and `bench.py` reads it for `roofline.traffic`.",
+             "", "Config-2 kernels (2^28 fp32 elements per tensor):", "",
+             "| Op | Kernel | Fetch GB | Write GB | HBM GB | Algorithmic GB |", "|---|---|---:|---:|---:|---:|"]
+    for label, key in C2_KERNEL.items():
+        hits = [(k, v) for k, v in t["kernels"].items() if k.startswith(key)]
+        if len(hits) != 1:
+            continue
+        k, v = hits[0]
+        short = k.split("(")[0].replace("void ", "")
+        lines.append(f"| {label} | `{short}` | {(v['fetch_bytes'] or 0) / 1e9:.3f} | {(v['write_bytes'] or 0) / 1e9:.3f} | "
+                     f"{v['hbm_bytes'] / 1e9:.3f} | {alg[label] * 2 ** 28 / 1e9:.3f} |")
+    with open(os.path.join(os.path.dirname(TRAFFIC_JSON), "traffic.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
 def traffic_for(label):
     if not os.path.exists(TRAFFIC_JSON):
         return None
@@ -561,11 +614,20 @@ def main():
     ap.add_argument("--cpu-reps", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
-                    help="write profiles/traffic.json from two rocprofv3 --pmc runs and exit")
+                    help="write profiles/traffic.json and traffic.md from two rocprofv3 --pmc runs and exit")
+    ap.add_argument("--stats-summary", metavar="KERNEL_STATS_CSV",
+                    help="write profiles/bench_kernel_stats.md from a rocprofv3 --stats run and exit")
+    ap.add_argument("--command", default="", help="the rocprofv3 command(s) a summary records (';'-separated)")
+    ap.add_argument("--bench-json", default=None, help="a bench JSON line of the same tree (for --stats-summary)")
     args = ap.parse_args()
     if args.pmc_summary:
         s = pmc_summary(*args.pmc_summary)
+        traffic_summary_md([c.strip() for c in args.command.split(";") if c.strip()] +
+                           [f"python bench.py --pmc-summary {args.pmc_summary[0]} {args.pmc_summary[1]}"])
         print(json.dumps({"fetch_scale": s["fetch_scale"], "write_scale": s["write_scale"]}))
+        return
+    if args.stats_summary:
+        stats_summary(args.stats_summary, args.command, args.bench_json)
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
