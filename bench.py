@@ -17,6 +17,8 @@ The other configs are measured after the headline step and reported under "workl
   c5  classifier head on logits [1048576,10]: MAX -> SUB -> EXP -> SUM -> DIV -> LOG ->
       MUL(onehot) -> MEAN, forward and backward op by op (the drop-in path), and the same graph
       row-fused (one kernel each way, caches flushed before each);
+  adam  Adam.step (mantle/nn/optim.mojo:94-140) on one 2^28-element parameter and on 400
+        tensors through the multi-tensor entry point, 28 B/elem;
   copy  a plain 1 GiB device copy (the library's copy kernel): the practical streaming rate.
 Tensors smaller than the 256 MB Infinity Cache are timed with the cache flushed before each
 op (a 1 GiB read sweep between ops, outside the timed events).
@@ -423,6 +425,42 @@ def run_c5(L, reps, rows=1 << 20, classes=10):
             "fused_min_bytes": 24 * E}
 
 
+def run_adam(L, reps):
+    """Adam.step on one 2^28-element parameter (28 B/elem) and on 400 tensors of 1..2^18
+    elements (about 2^26 in all) through the multi-tensor entry point."""
+    d = Dev(L)
+    n = 1 << 28
+    for k in ("p", "g", "m", "v"):
+        d.zeros(k, n)
+    chk(L, L.mh_rand_normal(d.ptrs["p"], n, 7, 0.0, 1.0), "rand")
+    chk(L, L.mh_rand_normal(d.ptrs["g"], n, 8, 0.0, 0.1), "rand")
+    p = d.ptrs
+    sizes = [int(x) for x in np.random.default_rng(SEED).integers(1, 1 << 18, size=400)]
+    slot = [(n + 63) & ~63 for n in sizes]  # arena slots on 256-byte boundaries, as mh_malloc places tensors
+    tot = sum(sizes)
+    for k in ("P", "G", "M", "V"):
+        d.zeros(k, sum(slot))
+    chk(L, L.mh_rand_normal(d.ptrs["G"], sum(slot), 9, 0.0, 0.1), "rand")
+    off = np.concatenate([[0], np.cumsum(slot)[:-1]])
+    VP = ctypes.c_void_p * len(sizes)
+    tabs = {k: VP(*[p[k] + 4 * int(o) for o in off]) for k in ("P", "G", "M", "V")}
+    csz = (ctypes.c_int64 * len(sizes))(*sizes)
+    it = [0]
+
+    def single():
+        it[0] += 1
+        return L.mh_adam_step(p["p"], p["g"], p["m"], p["v"], n, 1e-3, 0.9, 0.999, 1e-8, it[0])
+
+    def multi():
+        return L.mh_adam_step_multi(len(sizes), tabs["P"], tabs["G"], tabs["M"], tabs["V"], csz, 1e-3, 0.9, 0.999,
+                                    1e-8, 1)
+    chk(L, L.mh_sync(), "sync")
+    ops = [("adam.single_2^28", single, 28 * n), ("adam.multi_400", multi, 28 * tot)]
+    med = time_ops(d, ops, reps, flush=False)
+    d.free()
+    return {"elements_single": n, "elements_multi": tot, "tensors_multi": len(sizes), **op_report(ops, med)}
+
+
 def run_copy(L, reps):
     d = Dev(L)
     n = 1 << 28
@@ -607,8 +645,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--log2n", type=int, default=28)
-    ap.add_argument("--workloads", default="c3,c4,c5,copy",
-                    help="extra workloads after the headline step (comma list of c3,c4,c5,copy; 'none')")
+    ap.add_argument("--workloads", default="c3,c4,c5,adam,copy",
+                    help="extra workloads after the headline step (comma list of c3,c4,c5,adam,copy; 'none')")
     ap.add_argument("--reps", type=int, default=10, help="repetitions per op of the extra workloads")
     ap.add_argument("--cpu-log2n", type=int, default=24)
     ap.add_argument("--cpu-reps", type=int, default=2)
@@ -672,7 +710,8 @@ def main():
         log(f"c2: {value:.1f} GB/s, {r['ms_per_step']:.3f} ms/step")
     wl = [w for w in args.workloads.split(",") if w and w != "none"]
     runners = {"c3": lambda: run_c3(L, args.reps), "c4": lambda: run_c4(L, args.reps),
-               "c5": lambda: run_c5(L, args.reps), "copy": lambda: run_copy(L, args.reps)}
+               "c5": lambda: run_c5(L, args.reps), "adam": lambda: run_adam(L, args.reps),
+               "copy": lambda: run_copy(L, args.reps)}
     if wl:
         out["workloads"] = {}
     for w in wl:

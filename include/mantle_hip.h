@@ -186,6 +186,22 @@ int mh_softmax_log_mul_mean_fwd(float* loss, const float* x, const float* target
 int mh_softmax_log_mul_mean_bwd_accum(float* grad_x, const float* x, const float* target,
                                       const float* ug, int64_t rows, int64_t classes);
 
+/* ---- optimizer ---- */
+
+/* Adam.step for one parameter tensor (mantle/nn/optim.mojo:94-140, per-element body :101-132):
+ * m = b1*m + (1-b1)*g; v = b2*v + ((1-b2)*g)*g; p = p - lr*((m/(1-b1**iter)) /
+ * (sqrt(v/(1-b2**iter)) + eps)), in that order, with iter >= 1 the already-incremented step
+ * count. Updates param, m and v in place (28 bytes per element). */
+int mh_adam_step(float* param, const float* grad, float* m, float* v, int64_t n, float lr, float beta1,
+                 float beta2, float eps, int64_t iter);
+
+/* Adam.step over every trainable parameter of a model (the parallelize over parameters,
+ * optim.mojo:140): arrays of ntensors device pointers and sizes, one launch per 64 tensors.
+ * Same arithmetic as mh_adam_step. */
+int mh_adam_step_multi(int64_t ntensors, float* const* params, const float* const* grads, float* const* m,
+                       float* const* v, const int64_t* sizes, float lr, float beta1, float beta2, float eps,
+                       int64_t iter);
+
 /* Seeded synthetic fill (the device counterpart of rand_uniform / rand_normal,
  * mantle/core/rand_utils.mojo:23-63): element i of stream `seed` comes from a counter-based
  * SplitMix64, so the result does not depend on the launch shape. U(lo, hi) and N(mean, std). */

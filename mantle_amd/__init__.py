@@ -7,6 +7,7 @@ the CPU: if the library is missing or the device is absent, calls raise.
 """
 from ._lib import MantleHipError, lib  # noqa: F401
 from .tensor import Tensor, TensorShape, init, sync  # noqa: F401
+from .optim import Adam  # noqa: F401
 from .ops import (  # noqa: F401
     OP, ADD, SUB, MUL, DIV, EXP, LOG, POW, SUM, MEAN, MAX, SIGMOID, RELU, TANH,
     forward_op, backward_op, backward_op_both, broadcast_shapes, get_reduce_shape, fill,
@@ -15,7 +16,7 @@ from .ops import (  # noqa: F401
 )
 
 __all__ = [
-    "MantleHipError", "Tensor", "TensorShape", "init", "sync", "OP", "forward_op", "backward_op",
+    "Adam", "MantleHipError", "Tensor", "TensorShape", "init", "sync", "OP", "forward_op", "backward_op",
     "backward_op_both", "broadcast_shapes", "get_reduce_shape", "fill", "elwise_transform",
     "elwise_op", "accumulate_grad", "tsum", "tmean", "tmax", "static_result_shape", "bias_relu_forward",
     "bias_relu_backward", "softmax_log_mul_mean_forward", "softmax_log_mul_mean_backward",

@@ -91,6 +91,9 @@ SIGNATURES = {
     "mh_bias_relu_bwd_accum": [_VP, _VP, _VP, _VP, _VP, _S, _S],
     "mh_softmax_log_mul_mean_fwd": [_VP, _VP, _VP, _I64, _I64],
     "mh_softmax_log_mul_mean_bwd_accum": [_VP, _VP, _VP, _VP, _I64, _I64],
+    "mh_adam_step": [_VP, _VP, _VP, _VP, _I64, _F, _F, _F, _F, _I64],
+    "mh_adam_step_multi": [_I64, ctypes.POINTER(_VP), ctypes.POINTER(_VP), ctypes.POINTER(_VP), ctypes.POINTER(_VP),
+                           ctypes.POINTER(_I64), _F, _F, _F, _F, _I64],
     "mh_rand_uniform": [_VP, _I64, ctypes.c_uint64, _F, _F],
     "mh_rand_normal": [_VP, _I64, ctypes.c_uint64, _F, _F],
     "mh_event_create": [ctypes.POINTER(_VP)],

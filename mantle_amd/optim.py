@@ -1,0 +1,47 @@
+"""Adam over device-resident parameters: a mirror of mantle/nn/optim.mojo:51-149.
+
+``Adam(params, lr, beta1, beta2, epsilon)`` takes the trainable parameters as (param, grad)
+``Tensor`` pairs (the reference takes them from the graph's Parameters collection) and keeps
+the momentum and rms tensors, zero-initialised, beside them. ``step()`` increments ``iter``
+and updates every parameter with one ``mh_adam_step_multi`` launch per 64 tensors;
+``zero_grad()`` zeroes the gradients (``Collection.set_zero``, collection.mojo:221-224).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Sequence, Tuple
+
+from . import _lib
+from .tensor import Tensor
+
+
+class Adam:
+    def __init__(self, params: Sequence[Tuple[Tensor, Tensor]], lr: float = 0.001, beta1: float = 0.9,
+                 beta2: float = 0.999, epsilon: float = 1e-8):
+        self.params: List[Tuple[Tensor, Tensor]] = list(params)
+        for p, g in self.params:
+            if p.shape() != g.shape():
+                raise _lib.MantleHipError(_lib.ERR_SHAPE, "a parameter and its gradient differ in shape")
+        self.lr, self.beta1, self.beta2, self.epsilon = float(lr), float(beta1), float(beta2), float(epsilon)
+        self.iter = 0
+        # allocate_rms_and_momentum (optim.mojo:142-149): zero-initialised, one per parameter
+        self.momentum_grads = [Tensor(p.shape()) for p, _ in self.params]
+        self.rms_grads = [Tensor(p.shape()) for p, _ in self.params]
+
+    def zero_grad(self) -> None:
+        for _, g in self.params:
+            g.zero()
+
+    def step(self) -> None:
+        self.iter += 1
+        n = len(self.params)
+        if n == 0:
+            return
+        VP = ctypes.c_void_p * n
+        ps = VP(*[p.ptr for p, _ in self.params])
+        gs = VP(*[g.ptr for _, g in self.params])
+        ms = VP(*[t.ptr for t in self.momentum_grads])
+        vs = VP(*[t.ptr for t in self.rms_grads])
+        sizes = (ctypes.c_int64 * n)(*[p.num_elements() for p, _ in self.params])
+        _lib.call("mh_adam_step_multi", n, ps, gs, ms, vs, sizes, self.lr, self.beta1, self.beta2, self.epsilon,
+                  self.iter)

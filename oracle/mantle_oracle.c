@@ -655,3 +655,26 @@ int or_backward_op(int tensor_id, int op, const float* ug, const or_shape* sug,
     }
     return OR_ERR_OP;
 }
+
+/* ------------------------------------------------------------------------------------ */
+/* Adam.step, mantle/nn/optim.mojo:94-140 (the per-element body v_step, :101-132)        */
+/* ------------------------------------------------------------------------------------ */
+void or_adam_step(float* param, const float* grad, float* m, float* v, int64_t n, float lr,
+                  float beta1, float beta2, float eps, int64_t iter) {
+    /* Scalar[f32] arithmetic on the hyper-parameters: 1 - beta, and beta ** iter as Mojo's
+     * SIMD ** Int (square-and-multiply, or_powi) */
+    const float c1 = 1.0f - beta1;
+    const float c2 = 1.0f - beta2;
+    const float bc1 = 1.0f - or_powi(beta1, iter);
+    const float bc2 = 1.0f - or_powi(beta2, iter);
+    for (int64_t j = 0; j < n; ++j) {
+        const float g = grad[j];
+        float mj = beta1 * m[j] + c1 * g;          /* :109-111 */
+        m[j] = mj;
+        mj = mj / bc1;                             /* :116 */
+        float vj = beta2 * v[j] + c2 * g * g;      /* :120-122, (c2 * g) * g */
+        v[j] = vj;
+        vj = vj / bc2;                             /* :127 */
+        param[j] = param[j] - lr * (mj / (sqrtf(vj) + eps)); /* :130-132 */
+    }
+}

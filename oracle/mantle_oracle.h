@@ -83,6 +83,14 @@ int or_backward_op(int tensor_id, int op, const float* ug, const or_shape* sug,
                    const float* t1, const or_shape* s1, const float* t2, const or_shape* s2,
                    int axis, float* grad);
 
+/* ---- optimizer (mantle/nn/optim.mojo:94-140) ----
+ * One Adam.step for one parameter tensor of n elements at iteration `iter` (already
+ * incremented, as step() does before the update). Updates param, m (momentum) and v (rms)
+ * in place. Pinned by: fp64 Adam within a small bound, the exact g = 0 invariant, and the
+ * first-step closed form lr * g / (|g| + eps) (tests/test_oracle.py). */
+void or_adam_step(float* param, const float* grad, float* m, float* v, int64_t n, float lr,
+                  float beta1, float beta2, float eps, int64_t iter);
+
 #ifdef __cplusplus
 }
 #endif

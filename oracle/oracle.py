@@ -77,6 +77,8 @@ def lib():
              [ctypes.c_int, f32p, f32p, shp, f32p, shp, ctypes.c_int]),
             ("or_backward_op", ctypes.c_int,
              [ctypes.c_int, ctypes.c_int, f32p, shp, f32p, shp, f32p, shp, ctypes.c_int, f32p]),
+            ("or_adam_step", None, [f32p, f32p, f32p, f32p, i64, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                    ctypes.c_float, i64]),
         ]:
             fn = getattr(L, name)
             fn.restype = res
@@ -251,3 +253,12 @@ def backward_op_rc(tensor_id: int, op: int, ug, t1, t2=None, axis=None) -> int:
         return 0
     except OracleError as e:
         return int(str(e).rsplit(" ", 1)[-1])
+
+
+def adam_step(param, grad, m, v, iter_: int, lr=0.001, beta1=0.9, beta2=0.999, eps=1e-8):
+    """Adam.step (mantle/nn/optim.mojo:94-140) on one parameter tensor at iteration iter_;
+    returns new (param, m, v) arrays."""
+    p, g, mm, vv = (_f32(a).copy() for a in (param, grad, m, v))
+    lib().or_adam_step(_ptr(p), _ptr(g), _ptr(mm), _ptr(vv), p.size, float(lr), float(beta1), float(beta2),
+                       float(eps), int(iter_))
+    return p, mm, vv

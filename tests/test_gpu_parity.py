@@ -468,3 +468,94 @@ def test_fused_softmax_rejects_wide_rows(gpu):
     x = gpu.T(np.zeros((4, 33), np.float32))
     with pytest.raises(m.MantleHipError):
         m.softmax_log_mul_mean_forward(m.Tensor(m.TensorShape(1)), x, x)
+
+
+# ---------------------------------------------------------------------------------------
+# Adam.step (mantle/nn/optim.mojo:94-140)
+# ---------------------------------------------------------------------------------------
+ADAM_HP = dict(lr=0.01, beta1=0.9, beta2=0.999, eps=1e-8)
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 1023, 65537])
+def test_adam_step_single(gpu, n):
+    m = gpu.m
+    p = synth.normal((n,), 0, 1, 70)
+    mo, vo = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    tp, tm, tv = gpu.T(p), m.Tensor(m.TensorShape(n)), m.Tensor(m.TensorShape(n))
+    L = m.lib()
+    for it in range(1, 5):
+        g = synth.normal((n,), 0, 0.1, 71 + it)
+        tg = gpu.T(g)
+        m._lib.check(L.mh_adam_step(tp.ptr, tg.ptr, tm.ptr, tv.ptr, n, ADAM_HP["lr"], ADAM_HP["beta1"],
+                                    ADAM_HP["beta2"], ADAM_HP["eps"], it))
+        p, mo, vo = O.adam_step(p, g, mo, vo, it, ADAM_HP["lr"], ADAM_HP["beta1"], ADAM_HP["beta2"], ADAM_HP["eps"])
+        assert_bitexact(tm.to_numpy(), mo, f"m it {it}")
+        assert_bitexact(tv.to_numpy(), vo, f"v it {it}")
+        assert_bitexact(tp.to_numpy(), p, f"param it {it}")
+    assert L.mh_adam_step(tp.ptr, tp.ptr, tm.ptr, tv.ptr, n, 0.01, 0.9, 0.999, 1e-8, 0) == m._lib.ERR_INVALID
+
+
+def test_adam_step_multi_and_optimizer(gpu):
+    """70 tensors (two launches of the 64-tensor table), sizes 0..5000 with ragged tails and one
+    unaligned view, through mantle_amd.Adam (step counts iter, zero_grad clears)."""
+    m = gpu.m
+    sizes = [0, 1, 2, 3, 4, 5, 7, 8, 33, 64, 100, 257, 1000, 4099, 5000] + [int(s) for s in synth.integers((55,), 1, 3000, 75)]
+    params, grads, ps, owners = [], [], [], []
+    for i, n in enumerate(sizes):
+        p = synth.normal((max(n, 1),), 0, 1, 100 + i)[:n] if n else np.zeros(0, np.float32)
+        ps.append(p.copy())
+        if i == 20 and n > 0:  # an unaligned view
+            base = gpu.T(np.concatenate([[0], p]).astype(np.float32))
+            owners.append(base)
+            tp = m.Tensor(m.TensorShape(n), _ptr=base.ptr + 4, _owner=base)
+        else:
+            tp = gpu.T(p) if n else m.Tensor(m.TensorShape(0))
+        params.append(tp)
+        grads.append(m.Tensor(m.TensorShape(n)))
+    opt = m.Adam(list(zip(params, grads)), lr=ADAM_HP["lr"])
+    mos = [np.zeros(n, np.float32) for n in sizes]
+    vos = [np.zeros(n, np.float32) for n in sizes]
+    for it in range(1, 4):
+        gs = []
+        for i, n in enumerate(sizes):
+            g = synth.normal((max(n, 1),), 0, 0.1, 300 + 10 * i + it)[:n]
+            gs.append(g)
+            if n:
+                m._lib.call("mh_memcpy_h2d", grads[i].ptr, np.ascontiguousarray(g).ctypes.data, n * 4)
+        opt.step()
+        assert opt.iter == it
+        for i, n in enumerate(sizes):
+            ps[i], mos[i], vos[i] = O.adam_step(ps[i], gs[i], mos[i], vos[i], it, ADAM_HP["lr"])
+            if n:
+                assert_bitexact(params[i].to_numpy(), ps[i], f"param {i} it {it}")
+                assert_bitexact(opt.momentum_grads[i].to_numpy(), mos[i], f"m {i} it {it}")
+                assert_bitexact(opt.rms_grads[i].to_numpy(), vos[i], f"v {i} it {it}")
+    opt.zero_grad()
+    assert all(not g.to_numpy().any() for g in grads)
+
+
+@pytest.mark.parametrize("off", [(1, 1, 1, 1), (2, 2, 2, 2), (3, 3, 3, 3), (1, 0, 2, 3)])
+@pytest.mark.parametrize("n", [1, 2, 5, 1001])
+def test_adam_step_misaligned_views(gpu, off, n):
+    """Views at element offsets into aligned buffers: a shared offset takes the head-then-quads
+    path, mixed offsets the scalar one."""
+    m = gpu.m
+    L = m.lib()
+    p = synth.normal((n,), 0, 1, 80)
+    mo, vo = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    views, owners = [], []
+    for j, init in enumerate([p, None, mo, vo]):
+        base = gpu.T(np.zeros(n + off[j], np.float32) if init is None else np.concatenate([np.zeros(off[j], np.float32), init]))
+        owners.append(base)
+        views.append(base.ptr + 4 * off[j])
+    for it in range(1, 4):
+        g = synth.normal((n,), 0, 0.1, 81 + it)
+        m._lib.call("mh_memcpy_h2d", views[1], np.ascontiguousarray(g).ctypes.data, n * 4)
+        m._lib.check(L.mh_adam_step(views[0], views[1], views[2], views[3], n, 0.01, 0.9, 0.999, 1e-8, it))
+        p, mo, vo = O.adam_step(p, g, mo, vo, it, 0.01, 0.9, 0.999, 1e-8)
+        got = [owners[j].to_numpy()[off[j]:] for j in (0, 2, 3)]
+        assert_bitexact(got[0], p, f"param it {it}")
+        assert_bitexact(got[1], mo, f"m it {it}")
+        assert_bitexact(got[2], vo, f"v it {it}")
+        for j in (0, 2, 3):  # nothing written before the view
+            assert not owners[j].to_numpy()[:off[j]].any()

@@ -329,3 +329,71 @@ def test_mean_backward_all_uses_f32_of_f64_reciprocal():
     ug = np.array([2.5], np.float32)
     g = ENG.backward(0, O.MEAN, ug, x)
     assert_bitexact(g, np.full((3, 7), np.float32(1.0 / 21.0) * np.float32(2.5), np.float32), "mean all")
+
+
+# ---------------------------------------------------------------------------------------
+# Adam.step (mantle/nn/optim.mojo:94-140)
+# ---------------------------------------------------------------------------------------
+def _adam64(p, g, m, v, it, lr, b1, b2, eps):
+    m = b1 * m + (1 - b1) * g
+    v = b2 * v + (1 - b2) * g * g
+    mh = m / (1 - b1 ** it)
+    vh = v / (1 - b2 ** it)
+    return p - lr * mh / (np.sqrt(vh) + eps), m, v
+
+
+def test_adam_matches_fp64_over_steps():
+    rng = np.random.default_rng(5)
+    n = 4096
+    p = rng.standard_normal(n).astype(np.float32)
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    P, M, V = (a.astype(np.float64) for a in (p, m, v))
+    lr, b1, b2, eps = 0.01, 0.9, 0.999, 1e-8
+    for it in range(1, 8):
+        g = rng.standard_normal(n).astype(np.float32) * np.float32(0.1)
+        p, m, v = O.adam_step(p, g, m, v, it, lr, b1, b2, eps)
+        # fp64 on the same f32 hyper-parameters
+        P, M, V = _adam64(P, g.astype(np.float64), M, V, it, float(np.float32(lr)), float(np.float32(b1)),
+                          float(np.float32(b2)), float(np.float32(eps)))
+        # m can cancel towards 0: the bound is relative to the gradient's scale there
+        np.testing.assert_allclose(m, M, rtol=2e-6, atol=1e-7 * float(np.abs(g).max()))
+        np.testing.assert_allclose(v, V, rtol=2e-6, atol=1e-12)
+        # the update is lr-sized: its error stays a tiny fraction of lr
+        assert np.abs(p.astype(np.float64) - P).max() <= 1e-6 * np.abs(P).max() + 1e-4 * lr
+
+
+def test_adam_zero_gradient_leaves_state_unchanged():
+    p = np.linspace(-3, 3, 1001).astype(np.float32)
+    z = np.zeros_like(p)
+    for it in (1, 2, 10):
+        p2, m2, v2 = O.adam_step(p, z, z, z, it, 0.1)
+        assert np.array_equal(p2, p) and not m2.any() and not v2.any()
+
+
+def test_adam_first_step_moves_by_lr_times_sign():
+    """From m = v = 0 the first step is p - lr * g / (|g| + eps) up to rounding."""
+    g = np.array([0.5, -0.25, 3.0, -1e-3, 1e-6], np.float32)
+    p = np.ones_like(g)
+    z = np.zeros_like(g)
+    lr, eps = 0.01, 1e-8
+    p2, m2, v2 = O.adam_step(p, g, z, z, 1, lr, 0.9, 0.999, eps)
+    exp = 1.0 - lr * g.astype(np.float64) / (np.abs(g.astype(np.float64)) + eps)
+    np.testing.assert_allclose(p2, exp, rtol=1e-6)
+    c1 = np.float32(np.float32(1.0) - np.float32(0.9))
+    np.testing.assert_array_equal(m2, c1 * g)  # beta1 * 0 + (1 - beta1) * g, in f32
+
+
+def test_adam_bias_correction_uses_square_and_multiply_power():
+    """beta ** iter is Mojo's SIMD ** Int: 1 - powi(beta, iter) in f32, with powi pinned as
+    square-and-multiply above; at iter = 3 the correction is 1 - beta * (beta * beta)."""
+    b1 = np.float32(0.9)
+    g = np.array([1.0], np.float32)
+    z = np.zeros(1, np.float32)
+    m3 = np.array([0.3], np.float32)
+    p2, m2, _ = O.adam_step(np.zeros(1, np.float32), g, m3, np.ones(1, np.float32), 3, 1.0, 0.9, 0.999, 0.0)
+    mj = np.float32(b1 * m3[0]) + np.float32(np.float32(1) - b1) * g[0]
+    assert m2[0] == np.float32(mj)
+    bc = np.float32(1) - np.float32(b1 * np.float32(b1 * b1))
+    assert O.lib().or_powi(b1, 3) == np.float32(b1 * np.float32(b1 * b1))
+    del p2, bc, z
