@@ -19,6 +19,8 @@ The other configs are measured after the headline step and reported under "workl
       row-fused (one kernel each way, caches flushed before each);
   adam  Adam.step (mantle/nn/optim.mojo:94-140) on one 2^28-element parameter and on 400
         tensors through the multi-tensor entry point, 28 B/elem;
+  adj   FMA / LEAKYRELU / CLIP forward and backward over 2^28 elements, and tstd over
+        [8192, 8192] (axis 0, axis 1, all);
   copy  a plain 1 GiB device copy (the library's copy kernel): the practical streaming rate.
 Tensors smaller than the 256 MB Infinity Cache are timed with the cache flushed before each
 op (a 1 GiB read sweep between ops, outside the timed events).
@@ -461,6 +463,37 @@ def run_adam(L, reps):
     return {"elements_single": n, "elements_multi": tot, "tensors_multi": len(sizes), **op_report(ops, med)}
 
 
+def run_adj(L, reps):
+    """FMA, LEAKYRELU and CLIP forward / backward over 2^28 elements, and tstd over
+    [8192, 8192] (axis 0, axis 1, all elements; x read twice: the mean, then the squared
+    deviations, 4 B/elem algorithmic)."""
+    from mantle_amd._lib import make_shape
+    d = Dev(L)
+    n = 1 << 28
+    for k in ("a", "b", "c", "r", "g"):
+        d.zeros(k, n)
+    p = d.ptrs
+    chk(L, L.mh_rand_normal(p["a"], n, 11, 0.0, 3.0), "rand")
+    chk(L, L.mh_rand_normal(p["b"], n, 12, 0.0, 1.0), "rand")
+    chk(L, L.mh_rand_normal(p["c"], n, 13, 0.0, 1.0), "rand")
+    ops = [("FMA.fwd", lambda: L.mh_fma_fwd(p["r"], p["a"], p["b"], p["c"], n), 16 * n),
+           ("FMA.bwd0", lambda: L.mh_fma_bwd_accum(0, p["g"], p["c"], p["a"], p["b"], n), 16 * n),
+           ("FMA.bwd2", lambda: L.mh_fma_bwd_accum(2, p["g"], p["c"], p["a"], p["b"], n), 12 * n),
+           ("LEAKYRELU.fwd", lambda: L.mh_leakyrelu_fwd(p["r"], p["a"], n, 0.1), 8 * n),
+           ("LEAKYRELU.bwd", lambda: L.mh_leakyrelu_bwd_accum(p["g"], p["a"], p["b"], n, 0.1), 16 * n),
+           ("CLIP.fwd", lambda: L.mh_clip_fwd(p["r"], p["a"], n, -1.1, 1.1), 8 * n),
+           ("CLIP.bwd", lambda: L.mh_clip_bwd_accum(p["g"], p["a"], p["b"], n, -1.1, 1.1), 16 * n)]
+    m = 8192 * 8192
+    s = make_shape((8192, 8192))
+    for axis, nout in ((0, 8192), (1, 8192), (-1, 1)):
+        ax = "all" if axis < 0 else f"ax{axis}"
+        ops.append((f"tstd.8192x8192.{ax}", lambda axis=axis: L.mh_tstd(p["r"], p["a"], s, axis), 4 * m + 4 * nout))
+    chk(L, L.mh_sync(), "sync")
+    med = time_ops(d, ops, reps)  # flushed: tstd's 256 MB input would otherwise sit in the MALL
+    d.free()
+    return {"elements": n, **op_report(ops, med)}
+
+
 def run_copy(L, reps):
     d = Dev(L)
     n = 1 << 28
@@ -645,8 +678,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--log2n", type=int, default=28)
-    ap.add_argument("--workloads", default="c3,c4,c5,adam,copy",
-                    help="extra workloads after the headline step (comma list of c3,c4,c5,adam,copy; 'none')")
+    ap.add_argument("--workloads", default="c3,c4,c5,adam,adj,copy",
+                    help="extra workloads after the headline step (comma list of c3,c4,c5,adam,adj,copy; 'none')")
     ap.add_argument("--reps", type=int, default=10, help="repetitions per op of the extra workloads")
     ap.add_argument("--cpu-log2n", type=int, default=24)
     ap.add_argument("--cpu-reps", type=int, default=2)
@@ -711,6 +744,7 @@ def main():
     wl = [w for w in args.workloads.split(",") if w and w != "none"]
     runners = {"c3": lambda: run_c3(L, args.reps), "c4": lambda: run_c4(L, args.reps),
                "c5": lambda: run_c5(L, args.reps), "adam": lambda: run_adam(L, args.reps),
+               "adj": lambda: run_adj(L, args.reps),
                "copy": lambda: run_copy(L, args.reps)}
     if wl:
         out["workloads"] = {}

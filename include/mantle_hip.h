@@ -154,6 +154,35 @@ int mh_reduce_bwd_accum(int op, float* grad, const float* x, const mh_shape* sx,
  * tensorutils.mojo:149-175 and :482-484) return MH_ERR_SHAPE. */
 int mh_accumulate_grad(float* grad, const mh_shape* sgrad, const float* rg, const mh_shape* srg);
 
+/* ---- adjacent ops (same-shape, flat element count) ---- */
+
+/* FMA.forward (mantle/autograd/ops/basics.mojo:768-788): res = fma(t1, t2, t3), one rounding.
+ * FMA.result_shape (:759-766) assumes all three shapes equal; so does this entry point. */
+int mh_fma_fwd(float* res, const float* t1, const float* t2, const float* t3, int64_t n);
+
+/* FMA.backward (basics.mojo:790-817) accumulated as the ternary backward_op does
+ * (ops.mojo:466-497): tensor_id 0 grad += ug * t2; 1 grad += ug * t1; 2 grad += ug. */
+int mh_fma_bwd_accum(int tensor_id, float* grad, const float* ug, const float* t1, const float* t2, int64_t n);
+
+/* LEAKYRELU (mantle/autograd/ops/mlops.mojo:128-186), attribute negative_slope:
+ * fwd res = x > 0 ? x : x * slope; bwd grad += (x > 0 ? 1 : slope) * ug. */
+int mh_leakyrelu_fwd(float* res, const float* x, int64_t n, float negative_slope);
+int mh_leakyrelu_bwd_accum(float* grad, const float* x, const float* ug, int64_t n, float negative_slope);
+
+/* CLIP (mlops.mojo:238-299), attributes min / max (absent: pass -FLT_MAX / FLT_MAX, the
+ * reference's min_finite / max_finite): fwd res = max(min(x, max_val), min_val) with
+ * minnum / maxnum semantics (a NaN input gives max_val); bwd grad += (x >= min_val &&
+ * x <= max_val) ? ug : 0. */
+int mh_clip_fwd(float* res, const float* x, int64_t n, float min_val, float max_val);
+int mh_clip_bwd_accum(float* grad, const float* x, const float* ug, int64_t n, float min_val, float max_val);
+
+/* tstd (mantle/core/tensorutils.mojo:724-741 all elements, :776-840 one axis): population
+ * standard deviation, sqrt(sum((x - mean)^2) / count), with the mean of tmean. axis -1 = all
+ * elements (res has one element), else res has get_reduce_shape(sx, axis). Each output line
+ * is the line tmean reads; the reference's axis form reads other lines for most shapes (its
+ * index arithmetic takes i % shape[k] without dividing), which is not reproduced. */
+int mh_tstd(float* res, const float* x, const mh_shape* sx, int32_t axis);
+
 /* ---- fused graph-level entry points (no single reference counterpart) ---- */
 
 /* Linear-layer / NCHW bias + RELU forward: y = ADD(x, bias) (broadcast) and

@@ -91,6 +91,13 @@ SIGNATURES = {
     "mh_bias_relu_bwd_accum": [_VP, _VP, _VP, _VP, _VP, _S, _S],
     "mh_softmax_log_mul_mean_fwd": [_VP, _VP, _VP, _I64, _I64],
     "mh_softmax_log_mul_mean_bwd_accum": [_VP, _VP, _VP, _VP, _I64, _I64],
+    "mh_fma_fwd": [_VP, _VP, _VP, _VP, _I64],
+    "mh_fma_bwd_accum": [_I, _VP, _VP, _VP, _VP, _I64],
+    "mh_leakyrelu_fwd": [_VP, _VP, _I64, _F],
+    "mh_leakyrelu_bwd_accum": [_VP, _VP, _VP, _I64, _F],
+    "mh_clip_fwd": [_VP, _VP, _I64, _F, _F],
+    "mh_clip_bwd_accum": [_VP, _VP, _VP, _I64, _F, _F],
+    "mh_tstd": [_VP, _VP, _S, ctypes.c_int32],
     "mh_adam_step": [_VP, _VP, _VP, _VP, _I64, _F, _F, _F, _F, _I64],
     "mh_adam_step_multi": [_I64, ctypes.POINTER(_VP), ctypes.POINTER(_VP), ctypes.POINTER(_VP), ctypes.POINTER(_VP),
                            ctypes.POINTER(_I64), _F, _F, _F, _F, _I64],

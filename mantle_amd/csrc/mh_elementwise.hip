@@ -141,6 +141,49 @@ struct FMaxRoute {
     __device__ float operator()(const float* v) const { return v[0] == v[1] ? v[2] * v[3] : 0.0f; }
 };
 
+struct FFma {  // FMA.forward, basics.mojo:782-786: t1.fma(t2, t3), a single rounding
+    __device__ void setup(const DevScal&) {}
+    __device__ float operator()(const float* v) const { return __builtin_fmaf(v[0], v[1], v[2]); }
+};
+
+struct FLeaky {  // LEAKYRELU.forward, mlops.mojo:141-154
+    float slope;
+    __device__ void setup(const DevScal&) {}
+    __device__ float operator()(const float* v) const { return v[0] > 0.0f ? v[0] : v[0] * slope; }
+};
+
+struct FLeakyBwd {  // v[0] = x, v[1] = ug: LEAKYRELU.backward, mlops.mojo:164-184
+    float slope;
+    __device__ void setup(const DevScal&) {}
+    __device__ float operator()(const float* v) const { return (v[0] > 0.0f ? 1.0f : slope) * v[1]; }
+};
+
+// min / max as LLVM minnum / maxnum: a NaN operand yields the other one, equal operands the
+// first, so a NaN input clips to hi.
+__device__ __forceinline__ float minnum_f(float a, float b) { return (b < a || a != a) ? b : a; }
+__device__ __forceinline__ float maxnum_f(float a, float b) { return (b > a || a != a) ? b : a; }
+
+struct FClip {  // CLIP.forward, mlops.mojo:243-266: max(min(x, hi), lo)
+    float lo, hi;
+    __device__ void setup(const DevScal&) {}
+    __device__ float operator()(const float* v) const { return maxnum_f(minnum_f(v[0], hi), lo); }
+};
+
+struct FClipBwd {  // v[0] = x, v[1] = ug: CLIP.backward, mlops.mojo:281-297
+    float lo, hi;
+    __device__ void setup(const DevScal&) {}
+    __device__ float operator()(const float* v) const { return (v[0] >= lo && v[0] <= hi) ? v[1] : 0.0f; }
+};
+
+template <int ID>
+struct FFmaRg {  // FMA.backward, basics.mojo:804-817: id 0 ug * t2, id 1 ug * t1, id 2 ug
+    __device__ void setup(const DevScal&) {}
+    __device__ float operator()(const float* v) const {
+        if constexpr (ID == 2) return v[0];
+        else return v[0] * v[1];
+    }
+};
+
 // ---------------------------------------------------------------------------------------
 // kernels
 // ---------------------------------------------------------------------------------------
@@ -791,6 +834,80 @@ int mh_accumulate_grad(float* grad, const mh_shape* psgrad, const float* rg, con
     MH_TRY(scratch(unbroadcast_scratch_floats(sgrad, srg) * sizeof(float), reinterpret_cast<void**>(&tmp)));
     MH_TRY(unbroadcast_accum_scratch(grad, sgrad, rg, srg, false, tmp));
     return finish("mh_accumulate_grad");
+}
+
+}  // extern "C"
+
+namespace mh {
+
+// ---------------------------------------------------------------------------------------
+// FMA (basics.mojo:759-817), LEAKYRELU (mlops.mojo:128-186), CLIP (mlops.mojo:238-299):
+// same-shape maps over a flat element count
+// ---------------------------------------------------------------------------------------
+static int flat_check(const char* what, int64_t n, bool ptrs_ok) {
+    if (n < 0) return fail(MH_ERR_INVALID, "%s: negative count", what);
+    if (n > 0 && !ptrs_ok) return fail(MH_ERR_NULL, "%s: null tensor", what);
+    return MH_OK;
+}
+
+template <class F, int NIN, bool ACCUM>
+static int flat_map(const char* what, float* out, const float* const* ptrs, int64_t n, F f) {
+    MH_TRY(require_init());
+    mh_shape s = flat_shape(n);
+    mh_shape in[kMaxIn] = {s, s, s, s};
+    ElwPlan pl;
+    MH_TRY(build_elw_plan(s, NIN, in, &pl));
+    MH_TRY((run_map<F, NIN, ACCUM>(out, pl, ptrs, no_scal(), f)));
+    return finish(what);
+}
+
+}  // namespace mh
+
+extern "C" {
+
+int mh_fma_fwd(float* res, const float* t1, const float* t2, const float* t3, int64_t n) {
+    MH_TRY(flat_check("mh_fma_fwd", n, res && t1 && t2 && t3));
+    if (n == 0) return MH_OK;
+    const float* p[3] = {t1, t2, t3};
+    return flat_map<FFma, 3, false>("mh_fma_fwd", res, p, n, FFma{});
+}
+
+int mh_fma_bwd_accum(int tensor_id, float* grad, const float* ug, const float* t1, const float* t2, int64_t n) {
+    if (tensor_id < 0 || tensor_id > 2) return fail(MH_ERR_INVALID, "mh_fma_bwd_accum: tensor_id %d", tensor_id);
+    const float* other = tensor_id == 0 ? t2 : t1;
+    MH_TRY(flat_check("mh_fma_bwd_accum", n, grad && ug && (tensor_id == 2 || other)));
+    if (n == 0) return MH_OK;
+    const float* p[2] = {ug, other};
+    if (tensor_id == 2) return flat_map<FFmaRg<2>, 1, true>("mh_fma_bwd_accum", grad, p, n, FFmaRg<2>{});
+    return flat_map<FFmaRg<0>, 2, true>("mh_fma_bwd_accum", grad, p, n, FFmaRg<0>{});
+}
+
+int mh_leakyrelu_fwd(float* res, const float* x, int64_t n, float negative_slope) {
+    MH_TRY(flat_check("mh_leakyrelu_fwd", n, res && x));
+    if (n == 0) return MH_OK;
+    const float* p[1] = {x};
+    return flat_map<FLeaky, 1, false>("mh_leakyrelu_fwd", res, p, n, FLeaky{negative_slope});
+}
+
+int mh_leakyrelu_bwd_accum(float* grad, const float* x, const float* ug, int64_t n, float negative_slope) {
+    MH_TRY(flat_check("mh_leakyrelu_bwd_accum", n, grad && x && ug));
+    if (n == 0) return MH_OK;
+    const float* p[2] = {x, ug};
+    return flat_map<FLeakyBwd, 2, true>("mh_leakyrelu_bwd_accum", grad, p, n, FLeakyBwd{negative_slope});
+}
+
+int mh_clip_fwd(float* res, const float* x, int64_t n, float min_val, float max_val) {
+    MH_TRY(flat_check("mh_clip_fwd", n, res && x));
+    if (n == 0) return MH_OK;
+    const float* p[1] = {x};
+    return flat_map<FClip, 1, false>("mh_clip_fwd", res, p, n, FClip{min_val, max_val});
+}
+
+int mh_clip_bwd_accum(float* grad, const float* x, const float* ug, int64_t n, float min_val, float max_val) {
+    MH_TRY(flat_check("mh_clip_bwd_accum", n, grad && x && ug));
+    if (n == 0) return MH_OK;
+    const float* p[2] = {x, ug};
+    return flat_map<FClipBwd, 2, true>("mh_clip_bwd_accum", grad, p, n, FClipBwd{min_val, max_val});
 }
 
 }  // extern "C"

@@ -105,6 +105,46 @@ struct LdPowGrad {
     }
 };
 
+// tstd's second pass (tensorutils.mojo:724-741, 776-840): (x - mu) * (x - mu) with mu the
+// mean of the element's line. Element i of [A, B, C] (reduced over B) is on line
+// (i / (B*C)) * C + i % C; BIG = false divides with 32-bit fast divisors.
+template <bool BIG>
+struct LdSqDev {
+    const float* x;
+    const float* mu;
+    int64_t BC, C;
+    FastDiv fbc, fc;
+    __device__ void setup() {}
+    __device__ int64_t line(int64_t i) const {
+        if constexpr (BIG) {
+            return (i / BC) * C + i % C;
+        } else {
+            const uint32_t u = (uint32_t)i;
+            const uint32_t c = u - fdiv(u, fc) * (uint32_t)C;
+            return (int64_t)fdiv(u, fbc) * C + c;
+        }
+    }
+    __device__ float term(int64_t i, float xv) const {
+        const float d = xv - mu[line(i)];
+        return d * d;
+    }
+    __device__ float get(int64_t i) const { return term(i, x[i]); }
+    // A vector quad lies in one row (C == 1: one line) or across four columns (C % 4 == 0:
+    // four consecutive lines, a 16-byte aligned run of mu), so its lines take one division.
+    __device__ void get4(int64_t i, float* o) const {
+        const float4 q = *reinterpret_cast<const float4*>(x + i);
+        const int64_t l = line(i);
+        float4 m;
+        if (C == 1) m = make_float4(mu[l], mu[l], mu[l], mu[l]);
+        else m = *reinterpret_cast<const float4*>(mu + l);
+        float d;
+        d = q.x - m.x; o[0] = d * d;
+        d = q.y - m.y; o[1] = d * d;
+        d = q.z - m.z; o[2] = d * d;
+        d = q.w - m.w; o[3] = d * d;
+    }
+};
+
 // ---------------------------------------------------------------------------------------
 // epilogues
 // ---------------------------------------------------------------------------------------
@@ -113,6 +153,7 @@ __device__ __forceinline__ void epi_store(float* out, float*, int64_t o, float v
         case EPI_STORE: out[o] = v; break;
         case EPI_MEAN: out[o] = v / div; break;
         case EPI_ACCUM: out[o] = out[o] + v; break;
+        case EPI_STD: out[o] = __builtin_sqrtf(v / div); break;
         default: out[o] = out[o] + (-v); break;
     }
 }
@@ -505,6 +546,62 @@ __global__ void __launch_bounds__(kRThreads)
             g4[qi] = o;
         }
     }
+}
+
+// tstd over rows held in registers (B % 4 == 0, B <= 16384): the row is read once, its
+// mean and then its squared deviations come from registers. WPR waves per row.
+template <int WPR, int NQ>
+__global__ void __launch_bounds__(kRThreads)
+    k_tstd_rowreg(float* __restrict__ res, const float* __restrict__ x, int64_t nrows, int64_t B) {
+    __shared__ float ws[4];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t row = WPR == 1 ? (int64_t)blockIdx.x * 4 + w : (int64_t)blockIdx.x;
+    if (row >= nrows) return;  // WPR == 1: uniform per wave, and that path has no barrier
+    const int tr = WPR == 1 ? lane : (int)threadIdx.x;
+    constexpr int NT = 64 * WPR;
+    const int64_t Bq = B >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(x + row * B);
+    float4 v[NQ];
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const int64_t qi = tr + (int64_t)k * NT;
+        if (qi < Bq) {
+            v[k] = x4[qi];
+            acc = acc + v[k].x;
+            acc = acc + v[k].y;
+            acc = acc + v[k].z;
+            acc = acc + v[k].w;
+        }
+    }
+    acc = wave_reduce<RSum>(acc);
+    if (WPR == 4) {
+        if (lane == 0) ws[w] = acc;
+        __syncthreads();
+        acc = ((ws[0] + ws[1]) + ws[2]) + ws[3];
+        __syncthreads();  // ws is reused below
+    }
+    const float fb = (float)B;
+    const float mu = acc / fb;  // tmean: sum / Scalar[f32](count)
+    float sq = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const int64_t qi = tr + (int64_t)k * NT;
+        if (qi < Bq) {
+            float d;
+            d = v[k].x - mu; sq = sq + d * d;
+            d = v[k].y - mu; sq = sq + d * d;
+            d = v[k].z - mu; sq = sq + d * d;
+            d = v[k].w - mu; sq = sq + d * d;
+        }
+    }
+    sq = wave_reduce<RSum>(sq);
+    if (WPR == 4) {
+        if (lane == 0) ws[w] = sq;
+        __syncthreads();
+        sq = ((ws[0] + ws[1]) + ws[2]) + ws[3];
+    }
+    if (tr == 0) res[row] = __builtin_sqrtf(sq / fb);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -911,6 +1008,61 @@ int mh_reduce_fwd(int op, float* res, const float* x, const mh_shape* psx, int32
     if (t) MH_TRY(scratch(t * sizeof(float), reinterpret_cast<void**>(&tmp)));
     MH_TRY(reduce_abc(rop, epi, x, A, B, C, res, nullptr, div, tmp));
     return finish("mh_reduce_fwd");
+}
+
+int mh_tstd(float* res, const float* x, const mh_shape* psx, int32_t axis) {
+    MH_SHAPE_ARG(sx);
+    MH_TRY(check_shape(sx, "x"));
+    if (axis < -1 || axis >= sx.rank) return fail(MH_ERR_INVALID, "mh_tstd: axis %d outside [-1, %d)", axis, sx.rank);
+    int64_t A, B, C;
+    abc_of(sx, axis, &A, &B, &C);
+    if (A * C == 0) return MH_OK;
+    if (!res || (!x && B > 0)) return fail(MH_ERR_NULL, "mh_tstd: null tensor");
+    MH_TRY(require_init());
+    if (C == 1 && B >= 4 && B % 4 == 0 && B <= 16384 && al16(x) && A < ((int64_t)1 << 31)) {
+        // rows held in registers: one pass over x
+        const int64_t Bq = B / 4;
+        hipStream_t st = ctx().stream;
+        if (Bq <= 64 * 16) {  // one wave per row, four rows per block
+            const int nq = Bq <= 64 ? 1 : Bq <= 128 ? 2 : Bq <= 256 ? 4 : Bq <= 512 ? 8 : 16;
+            dim3 g((unsigned)((A + 3) / 4)), b(kRThreads);
+#define MH_TSR(NQ) hipLaunchKernelGGL((k_tstd_rowreg<1, NQ>), g, b, 0, st, res, x, A, B)
+            switch (nq) {
+                case 1: MH_TSR(1); break;
+                case 2: MH_TSR(2); break;
+                case 4: MH_TSR(4); break;
+                case 8: MH_TSR(8); break;
+                default: MH_TSR(16); break;
+            }
+#undef MH_TSR
+        } else {  // one block per row
+            const int nq = Bq <= 2048 ? 8 : 16;
+            dim3 g((unsigned)A), b(kRThreads);
+#define MH_TSR(NQ) hipLaunchKernelGGL((k_tstd_rowreg<4, NQ>), g, b, 0, st, res, x, A, B)
+            if (nq == 8) MH_TSR(8);
+            else MH_TSR(16);
+#undef MH_TSR
+        }
+        return finish("mh_tstd");
+    }
+    // scratch: the line means, then the partials of whichever pass splits
+    const size_t nmu = pad64((size_t)(A * C));
+    const size_t t = tmp_floats_t<RSum>(A, B, C, true);
+    float* base = nullptr;
+    MH_TRY(scratch((nmu + t) * sizeof(float), reinterpret_cast<void**>(&base)));
+    float* mu = base;
+    float* tmp = t ? base + nmu : nullptr;
+    const float div = (float)B;  // tmean: / Scalar[f32](count), and variance / count
+    MH_TRY(reduce_abc(RED_SUM, EPI_MEAN, x, A, B, C, mu, nullptr, div, tmp));
+    const int64_t n = A * B * C;
+    if (n < ((int64_t)1 << 32)) {
+        LdSqDev<false> ld{x, mu, B * C, C, make_fastdiv((uint32_t)(B * C > 0 ? B * C : 1)), make_fastdiv((uint32_t)C)};
+        MH_TRY((reduce_t<RSum, LdSqDev<false>>(ld, al16(x), EPI_STD, A, B, C, res, nullptr, div, tmp)));
+    } else {
+        LdSqDev<true> ld{x, mu, B * C, C, FastDiv{}, FastDiv{}};
+        MH_TRY((reduce_t<RSum, LdSqDev<true>>(ld, al16(x), EPI_STD, A, B, C, res, nullptr, div, tmp)));
+    }
+    return finish("mh_tstd");
 }
 
 int mh_reduce_bwd_accum(int op, float* grad, const float* x, const mh_shape* psx, const float* ug,

@@ -3,11 +3,12 @@
 Mirrors the reference interface so that its callers read the same:
   * ``OP`` ids and ``forward_op`` / ``backward_op`` (mantle/autograd/ops/ops.mojo:52-101,
     243-311, 355-463);
-  * the op structs ``ADD SUB MUL DIV EXP LOG POW SUM MEAN MAX SIGMOID RELU TANH`` with
-    ``result_shape`` and ``forward`` (mantle/autograd/ops/basics.mojo, mlops.mojo);
+  * the op structs ``ADD SUB MUL DIV EXP LOG POW SUM MEAN MAX SIGMOID RELU TANH FMA CLIP
+    LEAKYRELU`` with ``result_shape`` and ``forward`` (mantle/autograd/ops/basics.mojo,
+    mlops.mojo);
   * the tensorutils primitives ``fill``, ``elwise_transform``, ``elwise_pow``, ``elwise_op``,
     ``broadcast_shapes``, ``get_reduce_shape``, ``accumulate_grad``, ``tsum``, ``tmean``,
-    ``tmax`` (mantle/core/tensorutils.mojo).
+    ``tmax``, ``tstd`` (mantle/core/tensorutils.mojo).
 
 Every call runs the gfx950 kernels of libmantle_hip.so on device-resident ``Tensor``s.
 Errors the reference only prints (non-broadcastable shapes, unknown ops) raise
@@ -26,14 +27,25 @@ class OP:
     ADD, SUB, MUL, DIV, EXP, LOG, POW = 0, 1, 2, 3, 4, 5, 6
     SUM, MEAN, MAX = 8, 9, 10
     SIGMOID, RELU, TANH = 13, 14, 15
+    FMA, CLIP, LEAKYRELU = 19, 20, 28
 
     NAMES = {0: "ADD", 1: "SUB", 2: "MUL", 3: "DIV", 4: "EXP", 5: "LOG", 6: "POW", 8: "SUM",
-             9: "MEAN", 10: "MAX", 13: "SIGMOID", 14: "RELU", 15: "TANH"}
+             9: "MEAN", 10: "MAX", 13: "SIGMOID", 14: "RELU", 15: "TANH", 19: "FMA", 20: "CLIP",
+             28: "LEAKYRELU"}
 
 
 BINARY = (OP.ADD, OP.SUB, OP.MUL, OP.DIV)
 UNARY = (OP.EXP, OP.LOG, OP.SIGMOID, OP.RELU, OP.TANH)
 REDUCE = (OP.SUM, OP.MEAN, OP.MAX)
+ATTR_UNARY = (OP.LEAKYRELU, OP.CLIP)
+
+FLT_MAX = 3.4028234663852886e38  # max_finite[f32]; CLIP's absent bounds are -/+ this
+
+
+def _attr(attributes, name: str):
+    if attributes is None or not isinstance(attributes, dict):
+        return None
+    return attributes.get(name)
 
 
 def _axis(attributes) -> int:
@@ -107,6 +119,15 @@ def tmean(t: Tensor, axis: int = -1, res: Optional[Tensor] = None) -> Tensor:
 
 def tmax(t: Tensor, axis: int = -1, res: Optional[Tensor] = None) -> Tensor:
     return _reduce(OP.MAX, t, axis, res)
+
+
+def tstd(t: Tensor, axis: int = -1, res: Optional[Tensor] = None) -> Tensor:
+    """tstd, tensorutils.mojo:724-741 (all elements, shape (1)) and :776-840 (one axis):
+    population standard deviation. Each output reads the line tmean reads."""
+    if res is None:
+        res = Tensor(TensorShape(1) if axis < 0 else get_reduce_shape(t.shape(), axis))
+    _lib.call("mh_tstd", res.ptr, t.ptr, t.shape().c(), int(axis))
+    return res
 
 
 # ---------------------------------------------------------------------------------------
@@ -210,9 +231,64 @@ class MAX(_Reduce):
     op = OP.MAX
 
 
+class FMA:
+    """FMA, basics.mojo:758-817: fma(t1, t2, t3) over three equal shapes."""
+    op = OP.FMA
+
+    @staticmethod
+    def result_shape(t1_shape, t2_shape, t3_shape) -> TensorShape:
+        return as_shape(t1_shape)
+
+    @staticmethod
+    def forward(res: Tensor, t1: Tensor, t2: Tensor, t3: Tensor) -> None:
+        if not (t1.shape() == t2.shape() == t3.shape() == res.shape()):
+            raise _lib.MantleHipError(_lib.ERR_SHAPE, "FMA needs four equal shapes")
+        _lib.call("mh_fma_fwd", res.ptr, t1.ptr, t2.ptr, t3.ptr, t1.num_elements())
+
+
+class LEAKYRELU:
+    """LEAKYRELU, mlops.mojo:128-186; attribute ``negative_slope`` (required)."""
+    op = OP.LEAKYRELU
+
+    @staticmethod
+    def result_shape(t1_shape, attributes=None) -> TensorShape:
+        return as_shape(t1_shape)
+
+    @staticmethod
+    def slope(attributes) -> float:
+        v = _attr(attributes, "negative_slope")
+        if v is None:
+            raise _lib.MantleHipError(_lib.ERR_INVALID, "LEAKYRELU needs the negative_slope attribute")
+        return float(v)
+
+    @classmethod
+    def forward(cls, res: Tensor, t1: Tensor, attributes=None) -> None:
+        _lib.call("mh_leakyrelu_fwd", res.ptr, t1.ptr, t1.num_elements(), cls.slope(attributes))
+
+
+class CLIP:
+    """CLIP, mlops.mojo:236-299; attributes ``min`` / ``max`` (absent: min_finite /
+    max_finite)."""
+    op = OP.CLIP
+
+    @staticmethod
+    def result_shape(t1_shape, attributes=None) -> TensorShape:
+        return as_shape(t1_shape)
+
+    @staticmethod
+    def bounds(attributes):
+        lo, hi = _attr(attributes, "min"), _attr(attributes, "max")
+        return (-FLT_MAX if lo is None else float(lo)), (FLT_MAX if hi is None else float(hi))
+
+    @classmethod
+    def forward(cls, res: Tensor, t1: Tensor, attributes=None) -> None:
+        lo, hi = cls.bounds(attributes)
+        _lib.call("mh_clip_fwd", res.ptr, t1.ptr, t1.num_elements(), lo, hi)
+
+
 STRUCTS = {OP.ADD: ADD, OP.SUB: SUB, OP.MUL: MUL, OP.DIV: DIV, OP.EXP: EXP, OP.LOG: LOG,
            OP.POW: POW, OP.SUM: SUM, OP.MEAN: MEAN, OP.MAX: MAX, OP.SIGMOID: SIGMOID,
-           OP.RELU: RELU, OP.TANH: TANH}
+           OP.RELU: RELU, OP.TANH: TANH, OP.FMA: FMA, OP.LEAKYRELU: LEAKYRELU, OP.CLIP: CLIP}
 
 
 def static_result_shape(op: int, *shapes, attributes=None) -> TensorShape:
@@ -220,7 +296,7 @@ def static_result_shape(op: int, *shapes, attributes=None) -> TensorShape:
     s = STRUCTS.get(op)
     if s is None:
         raise _lib.MantleHipError(_lib.ERR_OP, f"Operator {op} not found.")
-    if op in REDUCE:
+    if op in REDUCE or op in ATTR_UNARY:
         return s.result_shape(shapes[0], attributes)
     return s.result_shape(*shapes)
 
@@ -228,9 +304,16 @@ def static_result_shape(op: int, *shapes, attributes=None) -> TensorShape:
 # ---------------------------------------------------------------------------------------
 # dispatch
 # ---------------------------------------------------------------------------------------
-def forward_op(op: int, res: Tensor, t1: Tensor, t2: Optional[Tensor] = None, attributes=None) -> None:
-    """forward_op, ops.mojo:243-311: writes op(t1[, t2]) into the preallocated res."""
-    if op in BINARY or op == OP.POW:
+def forward_op(op: int, res: Tensor, t1: Tensor, t2: Optional[Tensor] = None, attributes=None,
+               t3: Optional[Tensor] = None) -> None:
+    """forward_op, ops.mojo:243-341: writes op(t1[, t2[, t3]]) into the preallocated res."""
+    if op == OP.FMA:
+        if t2 is None or t3 is None:
+            raise _lib.MantleHipError(_lib.ERR_INVALID, "FMA needs three operands")
+        FMA.forward(res, t1, t2, t3)
+    elif op in ATTR_UNARY:
+        STRUCTS[op].forward(res, t1, attributes)
+    elif op in BINARY or op == OP.POW:
         if t2 is None:
             raise _lib.MantleHipError(_lib.ERR_INVALID, f"{OP.NAMES[op]} needs two operands")
         STRUCTS[op].forward(res, t1, t2)
@@ -243,14 +326,28 @@ def forward_op(op: int, res: Tensor, t1: Tensor, t2: Optional[Tensor] = None, at
 
 
 def backward_op(tensor_id: int, op: int, ug: Tensor, t1: Tensor, t2: Optional[Tensor] = None,
-                grad: Optional[Tensor] = None, attributes=None) -> None:
-    """backward_op, ops.mojo:355-463: grad += the gradient of operand ``tensor_id``.
+                grad: Optional[Tensor] = None, attributes=None, t3: Optional[Tensor] = None) -> None:
+    """backward_op, ops.mojo:355-497: grad += the gradient of operand ``tensor_id``.
 
     Signature order follows the reference's binary form (ug, t1, t2, grad); for unary and
-    reduce ops pass ``t2=None`` and ``grad`` by keyword or positionally."""
+    reduce ops pass ``t2=None`` and ``grad`` by keyword or positionally; FMA's third operand
+    goes in ``t3`` (its gradient does not read it)."""
     if grad is None:
         raise _lib.MantleHipError(_lib.ERR_NULL, "backward_op needs the grad tensor")
-    if op in BINARY:
+    if op == OP.FMA:
+        if t2 is None or not (ug.shape() == t1.shape() == t2.shape() == grad.shape()):
+            raise _lib.MantleHipError(_lib.ERR_SHAPE, "FMA backward needs equal shapes")
+        _lib.call("mh_fma_bwd_accum", int(tensor_id), grad.ptr, ug.ptr, t1.ptr, t2.ptr, t1.num_elements())
+    elif op in ATTR_UNARY:
+        if ug.shape() != t1.shape() or grad.shape() != t1.shape():
+            raise _lib.MantleHipError(_lib.ERR_SHAPE, "ug / grad shape differs from the operand shape")
+        if op == OP.LEAKYRELU:
+            _lib.call("mh_leakyrelu_bwd_accum", grad.ptr, t1.ptr, ug.ptr, t1.num_elements(),
+                      LEAKYRELU.slope(attributes))
+        else:
+            lo, hi = CLIP.bounds(attributes)
+            _lib.call("mh_clip_bwd_accum", grad.ptr, t1.ptr, ug.ptr, t1.num_elements(), lo, hi)
+    elif op in BINARY:
         _lib.call("mh_binary_bwd_accum", int(op), int(tensor_id), grad.ptr, grad.shape().c(), ug.ptr,
                   ug.shape().c(), t1.ptr, t1.shape().c(), t2.ptr, t2.shape().c())
     elif op == OP.POW:

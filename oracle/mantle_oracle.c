@@ -678,3 +678,112 @@ void or_adam_step(float* param, const float* grad, float* m, float* v, int64_t n
         param[j] = param[j] - lr * (mj / (sqrtf(vj) + eps)); /* :130-132 */
     }
 }
+
+/* ------------------------------------------------------------------------------------ */
+/* FMA, LEAKYRELU, CLIP                                                                  */
+/* ------------------------------------------------------------------------------------ */
+/* FMA.forward, basics.mojo:768-788: t1.fma(t2, t3), one rounding (C fmaf is exact-then-round). */
+void or_fma_fwd(float* res, const float* t1, const float* t2, const float* t3, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) res[i] = fmaf(t1[i], t2[i], t3[i]);
+}
+
+/* FMA.backward, basics.mojo:790-817 (id 0: ug * t2, id 1: ug * t1, id 2: ug), accumulated by
+ * the ternary backward_op, ops.mojo:466-497 (accumulate_grad, grad = grad + rg). */
+int or_fma_bwd_accum(int tensor_id, float* grad, const float* ug, const float* t1, const float* t2, int64_t n) {
+    if (tensor_id < 0 || tensor_id > 2) return OR_ERR_OP;
+    for (int64_t i = 0; i < n; ++i) {
+        const float rg = tensor_id == 0 ? ug[i] * t2[i] : tensor_id == 1 ? ug[i] * t1[i] : ug[i];
+        grad[i] = grad[i] + rg;
+    }
+    return OR_OK;
+}
+
+/* LEAKYRELU, mlops.mojo:128-186: fwd x > 0 ? x : x * slope; bwd (x > 0 ? 1 : slope) * ug. */
+void or_leakyrelu_fwd(float* res, const float* x, int64_t n, float slope) {
+    for (int64_t i = 0; i < n; ++i) res[i] = x[i] > 0.0f ? x[i] : x[i] * slope;
+}
+void or_leakyrelu_bwd_accum(float* grad, const float* x, const float* ug, int64_t n, float slope) {
+    for (int64_t i = 0; i < n; ++i) grad[i] = grad[i] + (x[i] > 0.0f ? 1.0f : slope) * ug[i];
+}
+
+/* min / max as LLVM minnum / maxnum: a NaN operand yields the other one; on equal operands
+ * the first is returned. */
+static inline float or_minnum(float a, float b) { return (b < a || a != a) ? b : a; }
+static inline float or_maxnum(float a, float b) { return (b > a || a != a) ? b : a; }
+
+/* CLIP, mlops.mojo:238-299: fwd max(min(x, hi), lo); bwd (x >= lo && x <= hi) ? ug : 0.
+ * Absent attributes are min_finite / max_finite (the caller passes -FLT_MAX / FLT_MAX). */
+void or_clip_fwd(float* res, const float* x, int64_t n, float lo, float hi) {
+    for (int64_t i = 0; i < n; ++i) res[i] = or_maxnum(or_minnum(x[i], hi), lo);
+}
+void or_clip_bwd_accum(float* grad, const float* x, const float* ug, int64_t n, float lo, float hi) {
+    for (int64_t i = 0; i < n; ++i) grad[i] = grad[i] + ((x[i] >= lo && x[i] <= hi) ? ug[i] : 0.0f);
+}
+
+/* ------------------------------------------------------------------------------------ */
+/* tstd                                                                                  */
+/* ------------------------------------------------------------------------------------ */
+/* tstd (all elements), tensorutils.mojo:724-741: mu = tmean(t); variance accumulates, chunk
+ * by chunk of nelts, (diff * diff).reduce_add() (width-1 tail steps one element each); the
+ * result is sqrt(variance / f32(n)). */
+float or_tstd_all(const float* t, int64_t n) {
+    const float mu = or_reduce_all(OR_SUM, t, n) / (float)n;
+    const int w = g_nelts;
+    const int64_t full = n - n % w;
+    float var = 0.0f, m[64];
+    int64_t i = 0;
+    for (; i < full; i += w) {
+        for (int k = 0; k < w; ++k) {
+            const float d = t[i + k] - mu;
+            m[k] = d * d;
+        }
+        var = var + lanes_combine(OR_SUM, m, w);
+    }
+    for (; i < n; ++i) {
+        const float d = t[i] - mu;
+        var = var + d * d;
+    }
+    return sqrtf(var / (float)n);
+}
+
+/* tstd (one axis), tensorutils.mojo:776-840: mu = tmean(t, axis); per output line the
+ * squared deviations accumulate chunk by chunk as above, then res /= f32(dim) and sqrt.
+ * The reference addresses line i as sum over k != axis of (i % shape[k]) * stride[k] and
+ * loads nelts contiguous elements even when the axis is not the last; both only agree with
+ * the line i for a last-axis reduction of a rank-2 tensor (its tests use lines of equal
+ * spread, where any line gives the expected value). This restatement reads line i as
+ * tmean does: base = (i % s) + (i / s) * (s * d), elements base + j * s. */
+int or_tstd_axis(float* res, const float* t, const or_shape* s, int axis) {
+    if (!shape_ok(s)) return OR_ERR_RANK;
+    if (axis < 0 || axis >= s->rank) return OR_ERR_SHAPE;
+    int64_t sa = 1;
+    for (int i = s->rank - 1; i > axis; --i) sa *= s->dims[i];
+    const int64_t d = s->dims[axis];
+    int64_t nout = 1;
+    for (int i = 0; i < s->rank; ++i)
+        if (i != axis) nout *= s->dims[i];
+    float* mu = (float*)malloc(sizeof(float) * (size_t)(nout ? nout : 1));
+    if (!mu) return OR_ERR_SHAPE;
+    int rc = or_reduce_axis(OR_MEAN, mu, t, s, axis);
+    const int w = g_nelts;
+    const int64_t full = d - d % w;
+    for (int64_t i = 0; rc == OR_OK && i < nout; ++i) {
+        const int64_t base = (i % sa) + (i / sa) * (sa * d);
+        float var = 0.0f, m[64];
+        int64_t j = 0;
+        for (; j < full; j += w) {
+            for (int k = 0; k < w; ++k) {
+                const float df = t[base + (j + k) * sa] - mu[i];
+                m[k] = df * df;
+            }
+            var = var + lanes_combine(OR_SUM, m, w);
+        }
+        for (; j < d; ++j) {
+            const float df = t[base + j * sa] - mu[i];
+            var = var + df * df;
+        }
+        res[i] = sqrtf(var / (float)d);
+    }
+    free(mu);
+    return rc;
+}

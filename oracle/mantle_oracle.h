@@ -91,6 +91,25 @@ int or_backward_op(int tensor_id, int op, const float* ug, const or_shape* sug,
 void or_adam_step(float* param, const float* grad, float* m, float* v, int64_t n, float lr,
                   float beta1, float beta2, float eps, int64_t iter);
 
+/* ---- adjacent elementwise ops (basics.mojo:759-817, mlops.mojo:128-186, 238-299) ----
+ * FMA uses fmaf (one rounding). CLIP's min / max follow LLVM minnum / maxnum, so a NaN input
+ * clips to hi; the NaN behaviour of Mojo's SIMD min / max is PARITY UNPINNED (finite and
+ * infinite inputs are pinned by brute-force comparisons in tests/test_oracle.py). */
+void or_fma_fwd(float* res, const float* t1, const float* t2, const float* t3, int64_t n);
+int or_fma_bwd_accum(int tensor_id, float* grad, const float* ug, const float* t1, const float* t2, int64_t n);
+void or_leakyrelu_fwd(float* res, const float* x, int64_t n, float slope);
+void or_leakyrelu_bwd_accum(float* grad, const float* x, const float* ug, int64_t n, float slope);
+void or_clip_fwd(float* res, const float* x, int64_t n, float lo, float hi);
+void or_clip_bwd_accum(float* grad, const float* x, const float* ug, int64_t n, float lo, float hi);
+
+/* ---- tstd (tensorutils.mojo:724-741, 776-840) ----
+ * Standard deviation over all elements or one axis (population: divide by the count).
+ * The axis form reads each output line correctly, where the reference's index arithmetic
+ * does not for most shapes (see the C source); pinned by the reference's own expected
+ * values and by fp64 standard deviations. */
+float or_tstd_all(const float* t, int64_t n);
+int or_tstd_axis(float* res, const float* t, const or_shape* s, int axis);
+
 #ifdef __cplusplus
 }
 #endif

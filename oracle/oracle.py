@@ -20,7 +20,9 @@ _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 ADD, SUB, MUL, DIV, EXP, LOG, POW = 0, 1, 2, 3, 4, 5, 6
 SUM, MEAN, MAX = 8, 9, 10
 SIGMOID, RELU, TANH = 13, 14, 15
+FMA, CLIP, LEAKYRELU = 19, 20, 28
 
+FLT_MAX = float(np.finfo(np.float32).max)
 MAX_RANK = 8
 
 
@@ -79,6 +81,14 @@ def lib():
              [ctypes.c_int, ctypes.c_int, f32p, shp, f32p, shp, f32p, shp, ctypes.c_int, f32p]),
             ("or_adam_step", None, [f32p, f32p, f32p, f32p, i64, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                                     ctypes.c_float, i64]),
+            ("or_fma_fwd", None, [f32p, f32p, f32p, f32p, i64]),
+            ("or_fma_bwd_accum", ctypes.c_int, [ctypes.c_int, f32p, f32p, f32p, f32p, i64]),
+            ("or_leakyrelu_fwd", None, [f32p, f32p, i64, ctypes.c_float]),
+            ("or_leakyrelu_bwd_accum", None, [f32p, f32p, f32p, i64, ctypes.c_float]),
+            ("or_clip_fwd", None, [f32p, f32p, i64, ctypes.c_float, ctypes.c_float]),
+            ("or_clip_bwd_accum", None, [f32p, f32p, f32p, i64, ctypes.c_float, ctypes.c_float]),
+            ("or_tstd_all", ctypes.c_float, [f32p, i64]),
+            ("or_tstd_axis", ctypes.c_int, [f32p, f32p, shp, ctypes.c_int]),
         ]:
             fn = getattr(L, name)
             fn.restype = res
@@ -262,3 +272,59 @@ def adam_step(param, grad, m, v, iter_: int, lr=0.001, beta1=0.9, beta2=0.999, e
     lib().or_adam_step(_ptr(p), _ptr(g), _ptr(mm), _ptr(vv), p.size, float(lr), float(beta1), float(beta2),
                        float(eps), int(iter_))
     return p, mm, vv
+
+
+def fma_fwd(t1, t2, t3) -> np.ndarray:
+    """FMA.forward (basics.mojo:768-788)."""
+    a, b, c = _f32(t1), _f32(t2), _f32(t3)
+    r = np.zeros_like(a)
+    lib().or_fma_fwd(_ptr(r), _ptr(a), _ptr(b), _ptr(c), a.size)
+    return r
+
+
+def fma_bwd_accum(tensor_id: int, grad, ug, t1, t2) -> np.ndarray:
+    """FMA.backward (basics.mojo:790-817) accumulated into a copy of grad."""
+    g, u, a, b = _f32(grad).copy(), _f32(ug), _f32(t1), _f32(t2)
+    _check(lib().or_fma_bwd_accum(int(tensor_id), _ptr(g), _ptr(u), _ptr(a), _ptr(b), g.size), "or_fma_bwd_accum")
+    return g
+
+
+def leakyrelu_fwd(x, slope: float) -> np.ndarray:
+    """LEAKYRELU.forward (mlops.mojo:134-156)."""
+    x = _f32(x)
+    r = np.zeros_like(x)
+    lib().or_leakyrelu_fwd(_ptr(r), _ptr(x), x.size, float(slope))
+    return r
+
+
+def leakyrelu_bwd_accum(grad, x, ug, slope: float) -> np.ndarray:
+    """LEAKYRELU.backward (mlops.mojo:158-186) accumulated into a copy of grad."""
+    g, x, u = _f32(grad).copy(), _f32(x), _f32(ug)
+    lib().or_leakyrelu_bwd_accum(_ptr(g), _ptr(x), _ptr(u), g.size, float(slope))
+    return g
+
+
+def clip_fwd(x, lo: float = -FLT_MAX, hi: float = FLT_MAX) -> np.ndarray:
+    """CLIP.forward (mlops.mojo:243-266)."""
+    x = _f32(x)
+    r = np.zeros_like(x)
+    lib().or_clip_fwd(_ptr(r), _ptr(x), x.size, float(lo), float(hi))
+    return r
+
+
+def clip_bwd_accum(grad, x, ug, lo: float = -FLT_MAX, hi: float = FLT_MAX) -> np.ndarray:
+    """CLIP.backward (mlops.mojo:268-299) accumulated into a copy of grad."""
+    g, x, u = _f32(grad).copy(), _f32(x), _f32(ug)
+    lib().or_clip_bwd_accum(_ptr(g), _ptr(x), _ptr(u), g.size, float(lo), float(hi))
+    return g
+
+
+def tstd(x, axis=None) -> np.ndarray:
+    """tstd (tensorutils.mojo:724-741 all elements, :776-840 one axis); returns the reduced
+    tensor ((1,) for all elements)."""
+    x = _f32(x)
+    if axis is None or axis < 0:
+        return np.array([lib().or_tstd_all(_ptr(x), x.size)], np.float32)
+    r = np.zeros(reduced_shape(x.shape, axis), np.float32)
+    _check(lib().or_tstd_axis(_ptr(r), _ptr(x), make_shape(x.shape), int(axis)), "or_tstd_axis")
+    return r

@@ -13,6 +13,8 @@ import json
 import math
 import os
 
+import numpy as np
+
 T = "tests/mojo/"
 
 
@@ -140,6 +142,34 @@ fwd("tu_mean_ax1_3x4x5", D + ":740-756,764", "MEAN", ar([3, 4, 5]),
     data([3, 1, 5], [v + 0.5 for v in [8, 9, 10, 11, 12, 28, 29, 30, 31, 32, 48, 49, 50, 51, 52]]), axis=1)
 fwd("tu_sum_ax2_3x4x5", D + ":773-786", "SUM", ar([3, 4, 5]), data([3, 4, 1], list(range(15, 291, 25))), axis=2)
 fwd("tu_mean_ax2_3x4x5", D + ":788-801", "MEAN", ar([3, 4, 5]), data([3, 4, 1], list(range(3, 59, 5))), axis=2)
+# tstd (test_tensorutils.mojo:204-210, 228-232, 249-253, 269-275; SumMeanStdData expected_std,
+# test_tensorutils_data.mojo:711, 760, 804). The all-element expectations are the test's own
+# f32 loop: sqrt(sum((f32(i + 1) - mean)^2) / n).
+
+
+def f32_std_loop(n):
+    mean = np.float32(sum(range(1, n + 1))) / np.float32(n)
+    acc = np.float32(0)
+    for i in range(n):
+        d = np.float32(i + 1) - mean
+        acc = np.float32(acc + d * d)
+    return float(np.sqrt(np.float32(acc / np.float32(n))))
+
+
+def tstd_case(id_, src, t1, expected, axis=None, tol="almost"):
+    cases.append({"id": id_, "source": src, "kind": "tstd", "t1": t1, "axis": axis, "expected": expected,
+                  "tol": tol})
+
+
+tstd_case("tu_std_all_2x10", T + "test_tensorutils.mojo:204-210", ar([2, 10]), fill([1], f32_std_loop(20)), tol="exact")
+tstd_case("tu_std_ax0_2x10", T + "test_tensorutils.mojo:228-232", ar([2, 10]), fill([1, 10], 5.0), axis=0)
+tstd_case("tu_std_ax1_2x10", T + "test_tensorutils.mojo:249-253", ar([2, 10]), fill([2, 1], 2.8722813129425049), axis=1)
+tstd_case("tu_std_all_3x4x5", T + "test_tensorutils.mojo:269-275", ar([3, 4, 5]), fill([1], f32_std_loop(60)),
+          tol="exact")
+tstd_case("tu_std_ax0_3x4x5", D + ":711", ar([3, 4, 5]), fill([1, 4, 5], 16.32993162), axis=0)
+tstd_case("tu_std_ax1_3x4x5", D + ":760", ar([3, 4, 5]), fill([3, 1, 5], 5.59016994), axis=1)
+tstd_case("tu_std_ax2_3x4x5", D + ":804", ar([3, 4, 5]), fill([3, 4, 1], 1.41421356), axis=2)
+
 cases.append({"id": "tu_accum_36", "source": T + "test_tensorutils.mojo:397-407", "kind": "accumulate",
               "grad_shape": [2, 1, 1], "rg": fill([2, 3, 4], 3.0), "expected": fill([2, 1, 1], 36.0), "tol": "exact"})
 cases.append({"id": "tu_accum_24_noncompliant", "source": T + "test_tensorutils.mojo:409-414", "kind": "accumulate",
@@ -167,6 +197,28 @@ cases.append({"id": "loss_ce_perfect", "source": T + "test_loss.mojo:86-127", "k
 cases.append({"id": "loss_ce_imperfect", "source": T + "test_loss.mojo:130-171", "kind": "graph",
               "graph": "crossentropy", "t1": data([2, 3], [0.1, 0.2, 0.7, 0.7, 0.2, 0.1]),
               "t2": data([2, 3], [0, 1, 0, 0, 0, 1]), "expected": fill([1], 1.31794953), "tol": "almost6"})
+
+# ---- FMA (test_ops.mojo:256-271), LEAKYRELU and CLIP (test_mlops.mojo:91-135, 161-248) ----
+cases.append({"id": "ops_fma", "source": T + "test_ops.mojo:256-271", "kind": "forward", "op": "FMA",
+              "t1": fill(S23, 1.0), "t2": fill(S23, 2.0), "t3": fill(S23, 3.0), "axis": None,
+              "expected": fill(S23, 5.0), "tol": "exact"})
+LR_X = data(S23, [3, 3, 3, -3, -3, -3])
+SLOPE = {"negative_slope": 0.1}
+fwd("ml_leakyrelu", T + "test_mlops.mojo:91-110", "LEAKYRELU", LR_X, data(S23, [3, 3, 3, -0.3, -0.3, -0.3]))
+cases[-1]["attrs"] = SLOPE
+bwd("ml_leakyrelu_bw", T + "test_mlops.mojo:113-135", "LEAKYRELU", LR_X, fill(S23, 5.0),
+    data(S23, [5, 5, 5, 0.5, 0.5, 0.5]))
+cases[-1]["attrs"] = SLOPE
+CL_X = data(S23, [i - 3 for i in range(6)])
+for tag, attrs, fexp, bexp in [
+        ("none", {}, [-3, -2, -1, 0, 1, 2], [5] * 6),
+        ("min", {"min": -1.1}, [-1.1, -1.1, -1, 0, 1, 2], [0, 0, 5, 5, 5, 5]),
+        ("max", {"max": 1.1}, [-3, -2, -1, 0, 1, 1.1], [5, 5, 5, 5, 5, 0]),
+        ("minmax", {"min": -1.1, "max": 1.1}, [-1.1, -1.1, -1, 0, 1, 1.1], [0, 0, 5, 5, 5, 0])]:
+    fwd(f"ml_clip_{tag}", T + "test_mlops.mojo:161-203", "CLIP", CL_X, data(S23, fexp))
+    cases[-1]["attrs"] = attrs
+    bwd(f"ml_clip_bw_{tag}", T + "test_mlops.mojo:206-248", "CLIP", CL_X, fill(S23, 5.0), data(S23, bexp))
+    cases[-1]["attrs"] = attrs
 
 here = os.path.dirname(os.path.abspath(__file__))
 with open(os.path.join(here, "reference_fixtures.json"), "w") as f:

@@ -559,3 +559,92 @@ def test_adam_step_misaligned_views(gpu, off, n):
         assert_bitexact(got[2], vo, f"v it {it}")
         for j in (0, 2, 3):  # nothing written before the view
             assert not owners[j].to_numpy()[:off[j]].any()
+
+
+# ---------------------------------------------------------------------------------------
+# FMA (basics.mojo:759-817), LEAKYRELU (mlops.mojo:128-186), CLIP (mlops.mojo:238-299)
+# ---------------------------------------------------------------------------------------
+ADJ_SIZES = [1, 3, 4, 5, 1023, 65537, 1 << 20]
+
+
+def _adj_inputs(n, seed):
+    x = synth.normal((n,), 0, 3, seed)
+    x[: min(n, 7)] = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1.1, -1.1], np.float32)[: min(n, 7)]
+    return x
+
+
+@pytest.mark.parametrize("n", ADJ_SIZES)
+def test_fma_parity(gpu, n):
+    a, b, c = (synth.normal((n,), 0, 1, 1100 + k) for k in range(3))
+    assert_bitexact(gpu.forward(OPS["FMA"], a, b, t3=c), O.fma_fwd(a, b, c), "fma fwd")
+    ug, g0 = synth.normal((n,), 0, 1, 1104), synth.normal((n,), 0, 1, 1105)
+    for tid in range(3):
+        m = gpu.m
+        g = gpu.T(g0)
+        m.backward_op(tid, m.OP.FMA, gpu.T(ug), gpu.T(a), gpu.T(b), g, t3=gpu.T(c))
+        assert_bitexact(g.to_numpy(), O.fma_bwd_accum(tid, g0, ug, a, b), f"fma bwd {tid}")
+
+
+@pytest.mark.parametrize("n", ADJ_SIZES)
+def test_leakyrelu_clip_parity(gpu, n):
+    x, ug, g0 = _adj_inputs(n, 1110), synth.normal((n,), 0, 1, 1111), synth.normal((n,), 0, 1, 1112)
+    for slope in (0.1, 0.0, -0.5):
+        at = {"negative_slope": slope}
+        assert_bitexact(gpu.forward(OPS["LEAKYRELU"], x, attrs=at), O.leakyrelu_fwd(x, slope), f"leaky {slope}")
+        assert_bitexact(gpu.backward(0, OPS["LEAKYRELU"], ug, x, grad=g0, attrs=at),
+                        O.leakyrelu_bwd_accum(g0, x, ug, slope), f"leaky bwd {slope}")
+    for at in ({}, {"min": -1.1}, {"max": 1.1}, {"min": -1.1, "max": 1.1}, {"min": 0.0, "max": 0.0}):
+        lo, hi = at.get("min", -O.FLT_MAX), at.get("max", O.FLT_MAX)
+        assert_bitexact(gpu.forward(OPS["CLIP"], x, attrs=at), O.clip_fwd(x, lo, hi), f"clip {at}")
+        assert_bitexact(gpu.backward(0, OPS["CLIP"], ug, x, grad=g0, attrs=at),
+                        O.clip_bwd_accum(g0, x, ug, lo, hi), f"clip bwd {at}")
+
+
+def test_adjacent_ops_unaligned_and_errors(gpu):
+    m = gpu.m
+    n = 10007
+    x = _adj_inputs(n, 1120)
+    base = gpu.T(np.concatenate([[0], x]).astype(np.float32))
+    vx = m.Tensor(m.TensorShape(n), _ptr=base.ptr + 4, _owner=base)
+    r = m.Tensor(m.TensorShape(n))
+    m.forward_op(m.OP.CLIP, r, vx, attributes={"min": -2.0, "max": 0.5})
+    assert_bitexact(r.to_numpy(), O.clip_fwd(x, -2.0, 0.5), "unaligned clip")
+    m.forward_op(m.OP.FMA, r, vx, vx, t3=vx)
+    assert_bitexact(r.to_numpy(), O.fma_fwd(x, x, x), "unaligned fma")
+    L = m.lib()
+    assert L.mh_fma_bwd_accum(3, r.ptr, r.ptr, r.ptr, r.ptr, n) == m._lib.ERR_INVALID
+    with pytest.raises(m.MantleHipError):
+        m.forward_op(m.OP.LEAKYRELU, r, vx)  # negative_slope is required
+
+
+# ---------------------------------------------------------------------------------------
+# tstd (tensorutils.mojo:724-741, 776-840)
+# ---------------------------------------------------------------------------------------
+TSTD_CASES = [((87, 73, 107), 0), ((87, 73, 107), 1), ((87, 73, 107), 2), ((87, 73, 107), None),
+              ((1024, 1024), 0), ((1024, 1024), 1), ((64, 512, 1024), 2), ((4099, 10), 1), ((2, 10), 0),
+              ((3, 4, 5), 1), ((1,), None), ((5,), 0), ((2, 70000), 1), ((70000, 3), 0), ((1 << 22,), None),
+              ((1000, 20), 1), ((513, 32), 1), ((40, 33), 1), ((3, 4100), 1), ((300, 256), 0),
+              ((33, 512, 128), 1), ((9000, 64), 0), ((5, 1, 7), 1), ((7, 4), 1), ((9, 8), 1), ((6, 4096), 1),
+              ((5, 16384), 1), ((3, 12000), 1), ((2, 3, 16388), 2)]
+
+
+@pytest.mark.parametrize("shape,axis", TSTD_CASES, ids=[f"{s}-ax{a}" for s, a in TSTD_CASES])
+def test_tstd_parity(gpu, shape, axis):
+    x = synth.normal(shape, 1.5, 2, 1130)
+    red = (1,) if axis is None else tuple(1 if i == axis else d for i, d in enumerate(shape))
+    ex = (x.astype(np.float64).std() if axis is None else x.astype(np.float64).std(axis=axis, keepdims=True))
+    ex = np.asarray(ex).reshape(red)
+    got = gpu.tstd(x, axis)
+    assert got.shape == red
+    assert_sum_close(got, ORC.tstd(x, axis), ex, f"tstd {shape} axis {axis}")
+
+
+def test_tstd_unaligned(gpu):
+    m = gpu.m
+    x = synth.normal((1000, 256), 0, 1, 1131)
+    base = gpu.T(np.concatenate([[0], x.reshape(-1)]).astype(np.float32))
+    vx = m.Tensor(m.TensorShape(1000, 256), _ptr=base.ptr + 4, _owner=base)
+    for ax in (0, 1, -1):
+        a = None if ax < 0 else ax
+        ex = np.asarray(x.astype(np.float64).std(axis=a, keepdims=a is not None)).reshape(ORC.tstd(x, a).shape)
+        assert_sum_close(m.tstd(vx, ax).to_numpy(), ORC.tstd(x, a), ex, f"unaligned tstd axis {ax}")

@@ -397,3 +397,91 @@ def test_adam_bias_correction_uses_square_and_multiply_power():
     bc = np.float32(1) - np.float32(b1 * np.float32(b1 * b1))
     assert O.lib().or_powi(b1, 3) == np.float32(b1 * np.float32(b1 * b1))
     del p2, bc, z
+
+
+# ---------------------------------------------------------------------------------------
+# FMA, LEAKYRELU, CLIP (basics.mojo:759-817, mlops.mojo:128-186, 238-299)
+# ---------------------------------------------------------------------------------------
+def test_fma_is_one_rounding():
+    rng = np.random.default_rng(40)
+    a, b, c = (rng.standard_normal(100000).astype(np.float32) for _ in range(3))
+    got = O.fma_fwd(a, b, c)
+    # a*b is exact in fp64 (48 significant bits); one fp64 add then the f32 rounding agrees
+    # with the exact single rounding except at an f32 tie after the fp64 rounding (~2^-29)
+    ref = (a.astype(np.float64) * b + c).astype(np.float32)
+    assert_bitexact(got, ref, "fma vs fp64")
+    unfused = (a * b) + c
+    assert (got != unfused).sum() > 100  # a two-rounding product-then-add would match this
+    assert_bitexact(O.fma_fwd(a, b, np.zeros_like(c)), a * b, "fma(a, b, 0) = a*b")
+    ug, g0 = rng.standard_normal(1000).astype(np.float32), rng.standard_normal(1000).astype(np.float32)
+    assert_bitexact(O.fma_bwd_accum(0, g0, ug, a[:1000], b[:1000]), g0 + ug * b[:1000], "fma bwd 0")
+    assert_bitexact(O.fma_bwd_accum(1, g0, ug, a[:1000], b[:1000]), g0 + ug * a[:1000], "fma bwd 1")
+    assert_bitexact(O.fma_bwd_accum(2, g0, ug, a[:1000], b[:1000]), g0 + ug, "fma bwd 2")
+
+
+def test_leakyrelu_identities_and_derivative():
+    rng = np.random.default_rng(41)
+    x = (rng.standard_normal(20000) * 4).astype(np.float32)
+    assert_bitexact(O.leakyrelu_fwd(x, 1.0), x, "slope 1 is the identity")
+    for slope in (0.1, 0.01, -0.5, 3.0):
+        y = O.leakyrelu_fwd(x, slope)
+        assert_bitexact(O.leakyrelu_fwd(x * 4, slope), y * 4, "positive homogeneity (x4 exact)")
+        assert_bitexact(y[x > 0], x[x > 0], "identity on positives")
+        # backward = d fwd / dx, from fp64 central differences away from the kink
+        h = 1e-3
+        sel = np.abs(x) > 1e-2
+        xd = x[sel].astype(np.float64)
+        yd = np.where(xd > 0, xd, xd * np.float64(np.float32(slope)))
+        deriv = (np.where(xd + h > 0, xd + h, (xd + h) * np.float64(np.float32(slope)))
+                 - np.where(xd - h > 0, xd - h, (xd - h) * np.float64(np.float32(slope)))) / (2 * h)
+        assert np.allclose(y[sel], yd, rtol=1e-6)
+        ug = np.ones(sel.sum(), np.float32)
+        gb = O.leakyrelu_bwd_accum(np.zeros_like(ug), x[sel], ug, slope)
+        np.testing.assert_allclose(gb, deriv, rtol=1e-6)
+
+
+def test_clip_against_numpy_and_special_values():
+    rng = np.random.default_rng(42)
+    x = (rng.standard_normal(20000) * 3).astype(np.float32)
+    for lo, hi in [(-1.1, 1.1), (-O.FLT_MAX, O.FLT_MAX), (0.0, 2.5), (-0.5, -0.5)]:
+        lo32, hi32 = np.float32(lo), np.float32(hi)
+        y = O.clip_fwd(x, lo, hi)
+        assert_bitexact(y, np.clip(x, lo32, hi32), f"clip [{lo}, {hi}]")
+        assert_bitexact(O.clip_fwd(y, lo, hi), y, "idempotent")
+        ug = rng.standard_normal(x.size).astype(np.float32)
+        inside = np.clip(x, lo32, hi32) == x
+        assert_bitexact(O.clip_bwd_accum(np.zeros_like(x), x, ug, lo, hi), np.where(inside, ug, 0) + 0.0, "clip bwd")
+    sp = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, O.FLT_MAX, -O.FLT_MAX], np.float32)
+    y = O.clip_fwd(sp)  # absent attributes: min_finite / max_finite
+    assert_bitexact(y[1:], np.array([O.FLT_MAX, -O.FLT_MAX, 0.0, -0.0, O.FLT_MAX, -O.FLT_MAX], np.float32), "default")
+    assert y[0] == np.float32(O.FLT_MAX)  # minnum(NaN, hi) = hi
+    g = O.clip_bwd_accum(np.zeros(7, np.float32), sp, np.ones(7, np.float32))
+    assert_bitexact(g, np.array([0, 0, 0, 1, 1, 1, 1], np.float32), "default bwd: inf and NaN outside")
+
+
+# ---------------------------------------------------------------------------------------
+# tstd (tensorutils.mojo:724-741, 776-840)
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("nelts", [8, 32])
+def test_tstd_against_fp64(nelts):
+    O.set_nelts(nelts)
+    rng = np.random.default_rng(43)
+    for shape in [(5,), (100,), (2, 10), (37, 63), (7, 40, 3), (3, 4, 5), (1, 70), (70, 1), (4, 1, 9)]:
+        x = (rng.standard_normal(shape) * 2 + 1).astype(np.float32)
+        ref = np.array([x.astype(np.float64).std()])
+        assert_sum_close(O.tstd(x), ref, ref, f"all {shape}")
+        for ax in range(len(shape)):
+            got = O.tstd(x, ax)
+            ref = x.astype(np.float64).std(axis=ax, keepdims=True)
+            np.testing.assert_allclose(got, ref, rtol=2e-6, atol=1e-7, err_msg=f"{shape} axis {ax}")
+
+
+def test_tstd_lines_are_tmean_lines():
+    """Each output is the spread of its own line: lines of distinct spreads, so reading any
+    other line (the reference's `i % shape[k]` addressing) would fail here."""
+    a = np.arange(1, 9, dtype=np.float32)
+    x = np.stack([np.array([-s, s], np.float32) * 1 for s in a]).reshape(2, 4, 2)  # line (i, j) = +/- a
+    got = O.tstd(x, 2).reshape(-1)
+    np.testing.assert_array_equal(got, a)
+    y = np.transpose(x, (2, 0, 1)).copy()  # the same lines along axis 0
+    np.testing.assert_array_equal(O.tstd(y, 0).reshape(-1), a)

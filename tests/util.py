@@ -17,7 +17,8 @@ if ROOT not in sys.path:
 from oracle import oracle as O  # noqa: E402  (test infrastructure: the checker)
 
 OPS = {"ADD": 0, "SUB": 1, "MUL": 2, "DIV": 3, "EXP": 4, "LOG": 5, "POW": 6, "SUM": 8, "MEAN": 9,
-       "MAX": 10, "SIGMOID": 13, "RELU": 14, "TANH": 15}
+       "MAX": 10, "SIGMOID": 13, "RELU": 14, "TANH": 15, "FMA": 19, "CLIP": 20, "LEAKYRELU": 28}
+FMA, CLIP, LEAKYRELU = 19, 20, 28
 BINARY = (0, 1, 2, 3)
 UNARY = (4, 5, 13, 14, 15)
 REDUCE = (8, 9, 10)
@@ -117,14 +118,35 @@ def assert_almost(got, ref, what="", rtol=1e-5, atol=1e-5):
 # ---------------------------------------------------------------------------------------
 # engines
 # ---------------------------------------------------------------------------------------
+def _clip_bounds(attrs):
+    attrs = attrs or {}
+    return float(attrs.get("min", -O.FLT_MAX)), float(attrs.get("max", O.FLT_MAX))
+
+
 class OracleEngine:
     name = "oracle"
 
-    def forward(self, op, t1, t2=None, axis=None):
+    def forward(self, op, t1, t2=None, axis=None, attrs=None, t3=None):
+        if op == FMA:
+            return O.fma_fwd(t1, t2, t3)
+        if op == LEAKYRELU:
+            return O.leakyrelu_fwd(t1, attrs["negative_slope"])
+        if op == CLIP:
+            return O.clip_fwd(t1, *_clip_bounds(attrs))
         return O.forward_op(op, t1, t2, axis)
 
-    def backward(self, tensor_id, op, ug, t1, t2=None, axis=None, grad=None):
+    def backward(self, tensor_id, op, ug, t1, t2=None, axis=None, grad=None, attrs=None):
+        if op in (FMA, LEAKYRELU, CLIP):
+            g = np.zeros(np.shape(t1), np.float32) if grad is None else grad
+            if op == FMA:
+                return O.fma_bwd_accum(tensor_id, g, ug, t1, t2)
+            if op == LEAKYRELU:
+                return O.leakyrelu_bwd_accum(g, t1, ug, attrs["negative_slope"])
+            return O.clip_bwd_accum(g, t1, ug, *_clip_bounds(attrs))
         return O.backward_op(tensor_id, op, ug, t1, t2, grad=grad, axis=axis)
+
+    def tstd(self, t1, axis=None):
+        return O.tstd(t1, axis)
 
 
 class GpuEngine:
@@ -139,26 +161,38 @@ class GpuEngine:
     def T(self, a):
         return self.m.Tensor.from_numpy(np.asarray(a, dtype=np.float32))
 
-    def forward(self, op, t1, t2=None, axis=None):
+    @staticmethod
+    def _attrs(axis, attrs):
+        if axis is None and not attrs:
+            return None
+        d = dict(attrs or {})
+        if axis is not None:
+            d["axis"] = axis
+        return d
+
+    def forward(self, op, t1, t2=None, axis=None, attrs=None, t3=None):
         m = self.m
         a = self.T(t1)
         b = self.T(t2) if t2 is not None else None
-        shapes = [a.shape()] + ([b.shape()] if b is not None else [])
-        attrs = None if axis is None else {"axis": axis}
-        res = m.Tensor(m.static_result_shape(op, *shapes, attributes=attrs))
-        m.forward_op(op, res, a, b, attributes=attrs)
+        c = self.T(t3) if t3 is not None else None
+        shapes = [x.shape() for x in (a, b, c) if x is not None]
+        at = self._attrs(axis, attrs)
+        res = m.Tensor(m.static_result_shape(op, *shapes, attributes=at))
+        m.forward_op(op, res, a, b, attributes=at, t3=c)
         return res.to_numpy()
 
-    def backward(self, tensor_id, op, ug, t1, t2=None, axis=None, grad=None):
+    def backward(self, tensor_id, op, ug, t1, t2=None, axis=None, grad=None, attrs=None):
         m = self.m
         a = self.T(t1)
         b = self.T(t2) if t2 is not None else None
         u = self.T(ug)
-        gshape = np.asarray(t1 if tensor_id == 0 or t2 is None else t2).shape or (1,)
+        gshape = np.asarray(t1 if tensor_id != 1 or t2 is None else t2).shape or (1,)
         g = self.T(np.zeros(gshape, np.float32) if grad is None else grad)
-        attrs = None if axis is None else {"axis": axis}
-        m.backward_op(tensor_id, op, u, a, b, g, attributes=attrs)
+        m.backward_op(tensor_id, op, u, a, b, g, attributes=self._attrs(axis, attrs))
         return g.to_numpy()
+
+    def tstd(self, t1, axis=None):
+        return self.m.tstd(self.T(t1), -1 if axis is None else axis).to_numpy()
 
 
 # ---------------------------------------------------------------------------------------
@@ -250,18 +284,22 @@ def check_fixture(eng, case):
             assert_almost(got, exp, what)
 
     kind = case["kind"]
+    attrs = case.get("attrs")
     if kind == "forward":
         op = OPS[case["op"]]
-        got = eng.forward(op, spec_to_array(case["t1"]), spec_to_array(case["t2"]), case["axis"])
+        got = eng.forward(op, spec_to_array(case["t1"]), spec_to_array(case["t2"]), case["axis"], attrs=attrs,
+                          t3=spec_to_array(case.get("t3")))
         cmp(got, spec_to_array(case["expected"]), case["id"])
     elif kind == "backward":
         op = OPS[case["op"]]
         t1, t2, ug = spec_to_array(case["t1"]), spec_to_array(case["t2"]), spec_to_array(case["ug"])
-        g1 = eng.backward(0, op, ug, t1, t2, case["axis"])
+        g1 = eng.backward(0, op, ug, t1, t2, case["axis"], attrs=attrs)
         cmp(g1, spec_to_array(case["grad1"]), case["id"] + " grad1")
         if case.get("grad2") is not None:
-            g2 = eng.backward(1, op, ug, t1, t2, case["axis"])
+            g2 = eng.backward(1, op, ug, t1, t2, case["axis"], attrs=attrs)
             cmp(g2, spec_to_array(case["grad2"]), case["id"] + " grad2")
+    elif kind == "tstd":
+        cmp(eng.tstd(spec_to_array(case["t1"]), case["axis"]), spec_to_array(case["expected"]), case["id"])
     elif kind == "graph":
         cmp(run_fixture_graph(eng, case), spec_to_array(case["expected"]), case["id"])
     else:
