@@ -418,8 +418,26 @@ def run_c5(L, reps, rows=1 << 20, classes=10):
              ("fused.bwd", lambda: L.mh_softmax_log_mul_mean_bwd_accum(p["g_logits"], p["logits"], p["onehot"],
                                                                        p["g_loss"], rows, classes), 4 * F + 4)]
     mf = time_ops(d, fused, reps)
+    # the same graph through the native executor: Model.forward (inputs copied into the
+    # arena from device memory, then the 8 nodes) and Model.backward (loss seed + 10 calls)
+    import mantle_amd as mm
+    g = mm.Graph()
+    s_lg, s_oh = g.input((rows, classes), trainable=True), g.input((rows, classes))
+    s_mx = g.op(mm.OP.MAX, s_lg, attributes={"axis": 1})
+    s_e = g.op(mm.OP.EXP, g.op(mm.OP.SUB, s_lg, s_mx))
+    s_sm = g.op(mm.OP.DIV, s_e, g.op(mm.OP.SUM, s_e, attributes={"axis": 1}))
+    g.loss(g.op(mm.OP.MEAN, g.op(mm.OP.MUL, g.op(mm.OP.LOG, s_sm), s_oh)))
+    model = mm.Model(g)
+    tab = (ctypes.c_void_p * 2)(p["logits"], p["onehot"])
+    fwd_bytes = sum(b for _, _, b in fwd) + 2 * 2 * F  # + the two input copies
+    bwd_bytes = sum(b for _, _, b in bwd)
+    model_ops = [("model.forward", lambda: L.mh_model_forward(model._h, 2, tab, 1), fwd_bytes),
+                 ("model.backward", lambda: L.mh_model_backward(model._h, 0, None, 0), bwd_bytes)]
+    mmed = time_ops(d, model_ops, reps, setup=lambda: chk(L, L.mh_model_zero_grad(model._h), "zero_grad"))
+    del model, g
     d.free()
     return {"shape": [rows, classes], "elements": E,
+            "model": op_report(model_ops, mmed), "model_total": total_report(model_ops, mmed),
             "fused": op_report(fused, mf), "fused_total": total_report(fused, mf),
             "fwd": op_report(fwd, med), "bwd": op_report(bwd, med),
             "fwd_total": total_report(fwd, med), "bwd_total": total_report(bwd, med),
@@ -712,7 +730,8 @@ def main():
     L = lib()
     n = 1 << args.log2n
     log(f"init, n = 2^{args.log2n}")
-    chk(L, L.mh_init(0, 1), "mh_init")  # MH_INIT_ASYNC: no host sync per call
+    from mantle_amd import init as mh_init_py
+    mh_init_py(0, asynchronous=True)  # MH_INIT_ASYNC: no host sync per call (and mantle_amd knows it)
     r = run_c2(L, n, args.steps, args.warmup) if args.steps > 0 else None
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "f32",

@@ -47,7 +47,8 @@ typedef struct {
 /* Op ids: the same numbers as Mantle's OP registry (mantle/autograd/ops/ops.mojo:57-83). */
 enum mh_op {
     MH_ADD = 0, MH_SUB = 1, MH_MUL = 2, MH_DIV = 3, MH_EXP = 4, MH_LOG = 5, MH_POW = 6,
-    MH_SUM = 8, MH_MEAN = 9, MH_MAX = 10, MH_SIGMOID = 13, MH_RELU = 14, MH_TANH = 15
+    MH_SUM = 8, MH_MEAN = 9, MH_MAX = 10, MH_SIGMOID = 13, MH_RELU = 14, MH_TANH = 15,
+    MH_FMA = 19, MH_CLIP = 20, MH_LEAKYRELU = 28
 };
 
 enum mh_status {
@@ -214,6 +215,79 @@ int mh_softmax_log_mul_mean_fwd(float* loss, const float* x, const float* target
  * target, updates grad_x, in one pass. */
 int mh_softmax_log_mul_mean_bwd_accum(float* grad_x, const float* x, const float* target,
                                       const float* ug, int64_t rows, int64_t classes);
+
+/* ---- graph and model: Graph (mantle/autograd/graph.mojo:33-217), Model
+ * (mantle/nn/model.mojo:55-340) and its Collections (mantle/autograd/collection.mojo:24-224)
+ * in device memory ---- */
+
+/* AttributeVector entries of the ops on this path (mantle/autograd/attributes.mojo): the
+ * reduce "axis", LEAKYRELU "negative_slope", CLIP "min" / "max"; flags say which are set. */
+#define MH_ATTR_AXIS 1
+#define MH_ATTR_NEGATIVE_SLOPE 2
+#define MH_ATTR_MIN 4
+#define MH_ATTR_MAX 8
+typedef struct {
+    int32_t flags;
+    int32_t axis;
+    float negative_slope;
+    float min_val;
+    float max_val;
+} mh_attrs;
+
+enum mh_symbol_kind { MH_SYM_INPUT = 0, MH_SYM_PARAM = 1, MH_SYM_NODE = 2 };
+enum mh_copy_from { MH_FROM_HOST = 0, MH_FROM_DEVICE = 1 };
+/* mh_model_create flag: run an ADD whose output only feeds the RELU node right after it as
+ * the fused bias + RELU kernels (every tensor and grad slot still holds the op-by-op value). */
+#define MH_MODEL_FUSE_BIAS_RELU 1u
+
+typedef struct mh_graph mh_graph;
+typedef struct mh_model mh_model;
+
+/* Graph() and its builders: input (graph.mojo:85-86), param with optional data (:88-94;
+ * without data the parameter is zero, model.mojo:371-373), scalar (:96-97: a shape-(1)
+ * non-trainable parameter), op (:110-129: result shape from static_result_shape, trainable
+ * if any operand is, :212-217), out (:104-105) and loss (:107-108). Symbols are numbered in
+ * creation order. Host-only calls: no device is needed. */
+int mh_graph_create(mh_graph** out);
+int mh_graph_destroy(mh_graph* g);
+int mh_graph_input(mh_graph* g, const mh_shape* shape, int trainable, int32_t* sym);
+int mh_graph_param(mh_graph* g, const mh_shape* shape, int trainable, const float* data, int64_t ndata,
+                   int32_t* sym);
+int mh_graph_scalar(mh_graph* g, float value, int32_t* sym);
+int mh_graph_op(mh_graph* g, int op, int32_t noperands, const int32_t* operands, const mh_attrs* attrs,
+                int32_t* sym);
+int mh_graph_out(mh_graph* g, int32_t sym);
+int mh_graph_loss(mh_graph* g, int32_t sym);
+int mh_graph_symbol(const mh_graph* g, int32_t sym, mh_shape* shape, int* trainable, int* kind);
+int mh_graph_counts(const mh_graph* g, int32_t* nsymbols, int32_t* nnodes, int32_t* ninputs, int32_t* nparams,
+                    int32_t* noutputs);
+
+/* Model(g) (model.mojo:58-78 with allocate_tensor_memory / allocate_grad_memory, :332-395):
+ * one device arena for every symbol's tensor and one for every trainable symbol's gradient,
+ * zeroed, parameters with data copied in. The graph is copied: it may be destroyed after. */
+int mh_model_create(const mh_graph* g, uint64_t flags, mh_model** out);
+int mh_model_destroy(mh_model* m);
+
+/* Model.forward (model.mojo:80-96, execute :113-171): copies the inputs (in graph input
+ * order, from host or device memory) into their slots and runs every node. Read the loss
+ * through mh_model_tensor. */
+int mh_model_forward(mh_model* m, int32_t ninputs, const float* const* inputs, int from);
+/* Model.inference (model.mojo:98-111): runs the nodes up to the last one that writes a
+ * graph output (n_inference_nodes, model.mojo:39-48). */
+int mh_model_inference(mh_model* m, int32_t ninputs, const float* const* inputs, int from);
+/* Model.backward (model.mojo:173-330): with nupper == 0 the loss gradient is filled with
+ * 1.0, else the last node's output gradient is set to upper_grads[0]; then every node in
+ * reverse order accumulates into the gradient of each trainable operand. Gradients
+ * accumulate across calls until mh_model_zero_grad, as in the reference. */
+int mh_model_backward(mh_model* m, int32_t nupper, const float* const* upper_grads, int from);
+/* Collection.__getitem__ (collection.mojo:194-200) of parameters.tensors / .grads: the
+ * device address of a symbol's slot (aliasing, like share()). */
+int mh_model_tensor(mh_model* m, int32_t sym, float** dptr);
+int mh_model_grad(mh_model* m, int32_t sym, float** dptr);
+/* parameters.grads.set_zero (collection.mojo:221-224): one fill over the gradient arena. */
+int mh_model_zero_grad(mh_model* m);
+int mh_model_info(const mh_model* m, int32_t* n_inference_nodes, int64_t* tensor_bytes, int64_t* grad_bytes,
+                  int32_t* fused_pairs);
 
 /* ---- optimizer ---- */
 

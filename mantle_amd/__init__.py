@@ -8,6 +8,8 @@ the CPU: if the library is missing or the device is absent, calls raise.
 from ._lib import MantleHipError, lib  # noqa: F401
 from .tensor import Tensor, TensorShape, init, sync  # noqa: F401
 from .optim import Adam  # noqa: F401
+from .graph import Graph, Symbol  # noqa: F401
+from .model import Collection, Model, Parameters  # noqa: F401
 from .ops import (  # noqa: F401
     OP, ADD, SUB, MUL, DIV, EXP, LOG, POW, SUM, MEAN, MAX, SIGMOID, RELU, TANH, FMA, CLIP, LEAKYRELU,
     forward_op, backward_op, backward_op_both, broadcast_shapes, get_reduce_shape, fill,
@@ -16,7 +18,7 @@ from .ops import (  # noqa: F401
 )
 
 __all__ = [
-    "Adam", "MantleHipError", "Tensor", "TensorShape", "init", "sync", "OP", "forward_op", "backward_op",
+    "Adam", "Collection", "Graph", "Model", "Parameters", "Symbol", "MantleHipError", "Tensor", "TensorShape", "init", "sync", "OP", "forward_op", "backward_op",
     "backward_op_both", "broadcast_shapes", "get_reduce_shape", "fill", "elwise_transform",
     "elwise_op", "accumulate_grad", "tsum", "tmean", "tmax", "tstd", "static_result_shape", "bias_relu_forward",
     "bias_relu_backward", "softmax_log_mul_mean_forward", "softmax_log_mul_mean_backward",

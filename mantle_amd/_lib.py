@@ -41,6 +41,18 @@ class mh_reduce_plan_info(ctypes.Structure):
                 ("b", ctypes.c_int64 * MAX_RANK), ("c", ctypes.c_int64 * MAX_RANK)]
 
 
+class mh_attrs(ctypes.Structure):
+    """AttributeVector entries of the ops on this path (mantle/autograd/attributes.mojo)."""
+    _fields_ = [("flags", ctypes.c_int32), ("axis", ctypes.c_int32), ("negative_slope", ctypes.c_float),
+                ("min_val", ctypes.c_float), ("max_val", ctypes.c_float)]
+
+
+ATTR_AXIS, ATTR_NEGATIVE_SLOPE, ATTR_MIN, ATTR_MAX = 1, 2, 4, 8
+SYM_INPUT, SYM_PARAM, SYM_NODE = 0, 1, 2
+FROM_HOST, FROM_DEVICE = 0, 1
+MODEL_FUSE_BIAS_RELU = 1
+
+
 class MantleHipError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"[{code}] {msg}")
@@ -107,6 +119,25 @@ SIGNATURES = {
     "mh_event_destroy": [_VP],
     "mh_event_record": [_VP],
     "mh_event_elapsed_ms": [ctypes.POINTER(_F), _VP, _VP],
+    "mh_graph_create": [ctypes.POINTER(_VP)],
+    "mh_graph_destroy": [_VP],
+    "mh_graph_input": [_VP, _S, _I, ctypes.POINTER(ctypes.c_int32)],
+    "mh_graph_param": [_VP, _S, _I, _VP, _I64, ctypes.POINTER(ctypes.c_int32)],
+    "mh_graph_scalar": [_VP, _F, ctypes.POINTER(ctypes.c_int32)],
+    "mh_graph_op": [_VP, _I, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(mh_attrs), ctypes.POINTER(ctypes.c_int32)],
+    "mh_graph_out": [_VP, ctypes.c_int32],
+    "mh_graph_loss": [_VP, ctypes.c_int32],
+    "mh_graph_symbol": [_VP, ctypes.c_int32, _S, ctypes.POINTER(_I), ctypes.POINTER(_I)],
+    "mh_graph_counts": [_VP, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)],
+    "mh_model_create": [_VP, ctypes.c_uint64, ctypes.POINTER(_VP)],
+    "mh_model_destroy": [_VP],
+    "mh_model_forward": [_VP, ctypes.c_int32, ctypes.POINTER(_VP), _I],
+    "mh_model_inference": [_VP, ctypes.c_int32, ctypes.POINTER(_VP), _I],
+    "mh_model_backward": [_VP, ctypes.c_int32, ctypes.POINTER(_VP), _I],
+    "mh_model_tensor": [_VP, ctypes.c_int32, ctypes.POINTER(_VP)],
+    "mh_model_grad": [_VP, ctypes.c_int32, ctypes.POINTER(_VP)],
+    "mh_model_zero_grad": [_VP],
+    "mh_model_info": [_VP, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_int32)],
     "mh_plan_binary": [_S, _S, _S, ctypes.POINTER(mh_plan_info)],
     "mh_plan_unbroadcast": [_S, _S, ctypes.POINTER(mh_reduce_plan_info)],
 }

@@ -1,7 +1,8 @@
 """Adam over device-resident parameters: a mirror of mantle/nn/optim.mojo:51-149.
 
-``Adam(params, lr, beta1, beta2, epsilon)`` takes the trainable parameters as (param, grad)
-``Tensor`` pairs (the reference takes them from the graph's Parameters collection) and keeps
+``Adam(params, lr, beta1, beta2, epsilon)`` takes a model's ``Parameters`` (its graph's
+trainable parameters, get_trainable_parameters, optim.mojo:27-44) or (param, grad) ``Tensor``
+pairs, and keeps
 the momentum and rms tensors, zero-initialised, beside them. ``step()`` increments ``iter``
 and updates every parameter with one ``mh_adam_step_multi`` launch per 64 tensors;
 ``zero_grad()`` zeroes the gradients (``Collection.set_zero``, collection.mojo:221-224).
@@ -16,8 +17,14 @@ from .tensor import Tensor
 
 
 class Adam:
-    def __init__(self, params: Sequence[Tuple[Tensor, Tensor]], lr: float = 0.001, beta1: float = 0.9,
-                 beta2: float = 0.999, epsilon: float = 1e-8):
+    def __init__(self, params, lr: float = 0.001, beta1: float = 0.9, beta2: float = 0.999,
+                 epsilon: float = 1e-8):
+        """``params``: a model's ``Parameters`` (its graph's trainable parameters, as
+        ``Adam[g](model.parameters, ...)`` takes them), or (param, grad) Tensor pairs."""
+        self._collection = None
+        if hasattr(params, "tensors") and hasattr(params, "grads") and hasattr(params, "graph"):
+            self._collection = params
+            params = [(params.tensors[s], params.grads[s]) for s in params.graph.trainable_parameters()]
         self.params: List[Tuple[Tensor, Tensor]] = list(params)
         for p, g in self.params:
             if p.shape() != g.shape():
@@ -29,6 +36,10 @@ class Adam:
         self.rms_grads = [Tensor(p.shape()) for p, _ in self.params]
 
     def zero_grad(self) -> None:
+        """Adam.zero_grad (optim.mojo:90-92): parameters.grads.set_zero()."""
+        if self._collection is not None:
+            self._collection.grads.set_zero()
+            return
         for _, g in self.params:
             g.zero()
 

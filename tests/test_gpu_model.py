@@ -1,0 +1,264 @@
+"""The native Graph / Model executor (mh_graph_*, mh_model_*; mantle/autograd/graph.mojo,
+mantle/nn/model.mojo, mantle/autograd/collection.mojo) against the op-by-op execution of the
+same graphs: every tensor and gradient slot must hold the same bits, since both run the same
+kernels in the same node order."""
+import numpy as np
+import pytest
+
+from mantle_amd import synth
+from util import (O, OPS, GpuEngine, Graph, OracleEngine, assert_bitexact, assert_sum_close, config5_nodes,
+                  native_graph)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    return GpuEngine()
+
+
+def _compare(gpu, nodes, values, trainable, params=(), seed=None, fuse=False, what="", summed=None):
+    """`summed` = {grad name: (source grad name, axes)}: gradients that are sums over axes of
+    another gradient in a different fixed order (the fused bias gradient), checked in the
+    rtol class against the fp64 sum."""
+    m = gpu.m
+    ref = Graph(nodes, trainable)
+    vals = ref.forward(gpu, values)
+    grads = ref.backward(gpu, vals, seed)
+    g, syms, inputs = native_graph(m, nodes, values, trainable, params)
+    last = nodes[-1][3]
+    if seed is None:
+        g.loss(syms[last])
+    g.out(syms[last])
+    model = m.Model(g, fuse_bias_relu=fuse)
+    ins = [values[n] for n in inputs]
+    if seed is None:
+        loss = model.forward(*ins)
+        assert_bitexact(loss.to_numpy(), vals[last], f"{what} loss")
+        model.backward()
+    else:
+        model.inference(*ins)
+        model.backward(seed)
+    for name, sym in syms.items():
+        assert_bitexact(model.parameters.tensors[sym].to_numpy().reshape(np.shape(vals[name])), vals[name],
+                        f"{what} tensor {name}")
+        if not sym.trainable:
+            continue
+        got = model.parameters.grads[sym].to_numpy().reshape(np.shape(grads[name]))
+        if summed and name in summed:
+            src, axes = summed[name]
+            terms = np.asarray(grads[src], np.float64)
+            ex = terms.sum(axis=axes).reshape(got.shape)
+            assert_sum_close(got, grads[name], ex, f"{what} grad {name}",
+                             terms_abs=np.abs(terms).sum(axis=axes).reshape(got.shape))
+        else:
+            assert_bitexact(got, grads[name], f"{what} grad {name}")
+    return model, syms, vals, grads
+
+
+def _bias_relu_nodes():
+    return [(OPS["ADD"], ["x", "bias"], None, "y"), (OPS["RELU"], ["y"], None, "r")]
+
+
+@pytest.mark.parametrize("fuse", [False, True])
+@pytest.mark.parametrize("xshape,bshape", [((32, 32), (1, 32)), ((16, 32, 28, 28), (1, 32, 1, 1))])
+def test_model_bias_relu_configs(gpu, fuse, xshape, bshape):
+    """Configs 1 and 3: ADD(x, bias) -> RELU with an upper gradient, x a trainable input and
+    bias a trainable parameter; fused or not, every slot matches."""
+    values = {"x": synth.normal(xshape, 0, 1, 1200), "bias": synth.normal(bshape, 0, 0.1, 1201)}
+    seed = synth.normal(xshape, 0, 1, 1202)
+    axes = tuple(i for i, d in enumerate(bshape) if d == 1)
+    model, *_ = _compare(gpu, _bias_relu_nodes(), values, ["x", "bias"], params=["bias"], seed=seed, fuse=fuse,
+                         what=f"fuse={fuse}", summed={"bias": ("y", axes)} if fuse else None)
+    assert model.info()["fused_pairs"] == (1 if fuse else 0)
+
+
+def test_model_config5_chain(gpu):
+    rows, classes = 4099, 10
+    logits = synth.normal((rows, classes), 0, 2, 1210)
+    cls = np.floor(synth.uniform((rows,), 0, 1, 1211) * classes).astype(np.int64)
+    onehot = np.zeros((rows, classes), np.float32)
+    onehot[np.arange(rows), cls] = 1
+    _compare(gpu, config5_nodes(), {"logits": logits, "onehot": onehot}, ["logits"], what="c5")
+
+
+def test_model_every_op(gpu):
+    """One graph over every op of the path (broadcast, scalar, reduce, POW, FMA, CLIP,
+    LEAKYRELU) with trainable parameters and a shared operand."""
+    m = gpu.m
+    x = synth.normal((37, 20), 0, 1, 1220)
+    w = synth.normal((1, 20), 0, 1, 1221)
+    g = m.Graph()
+    sx = g.input((37, 20), trainable=True)
+    sw = g.param((1, 20), init=w)
+    a = g.op(m.OP.MUL, sx, sw)
+    b = g.op(m.OP.ADD, a, sx)                    # sx used twice
+    c = g.op(m.OP.TANH, b)
+    d = g.op(m.OP.SIGMOID, c)
+    e = g.op(m.OP.FMA, c, d, b)
+    f = g.op(m.OP.LEAKYRELU, e, attributes={"negative_slope": 0.2})
+    h = g.op(m.OP.CLIP, f, attributes={"min": -0.5, "max": 1.5})
+    k = g.op(m.OP.MAX, h, attributes={"axis": 1})
+    q = g.op(m.OP.SUB, h, k)
+    r = g.op(m.OP.EXP, q)
+    s = g.op(m.OP.POW, r, 2.0)
+    t = g.op(m.OP.DIV, s, g.op(m.OP.SUM, s, attributes={"axis": 0}))
+    u = g.op(m.OP.MUL, t, t)                     # same symbol twice
+    loss = g.op(m.OP.MEAN, u)
+    g.loss(loss)
+    g.out(loss)
+    model = m.Model(g)
+    got = model.forward(x).to_numpy()
+    model.backward()
+    # op by op on the GPU engine, same order
+    E = gpu
+    va = E.forward(OPS["MUL"], x, w)
+    vb = E.forward(OPS["ADD"], va, x)
+    vc = E.forward(OPS["TANH"], vb)
+    vd = E.forward(OPS["SIGMOID"], vc)
+    ve = E.forward(OPS["FMA"], vc, vd, t3=vb)
+    vf = E.forward(OPS["LEAKYRELU"], ve, attrs={"negative_slope": 0.2})
+    vh = E.forward(OPS["CLIP"], vf, attrs={"min": -0.5, "max": 1.5})
+    vk = E.forward(OPS["MAX"], vh, axis=1)
+    vq = E.forward(OPS["SUB"], vh, vk)
+    vr = E.forward(OPS["EXP"], vq)
+    two = np.array([2.0], np.float32)
+    vs = E.forward(OPS["POW"], vr, two)
+    vsum = E.forward(OPS["SUM"], vs, axis=0)
+    vt = E.forward(OPS["DIV"], vs, vsum)
+    vu = E.forward(OPS["MUL"], vt, vt)
+    vl = E.forward(OPS["MEAN"], vu)
+    assert_bitexact(got, vl, "loss")
+    z = lambda v: np.zeros(np.shape(v), np.float32)  # noqa: E731
+    gl = np.ones(1, np.float32)
+    gu = E.backward(0, OPS["MEAN"], gl, vu, grad=z(vu))
+    gt = E.backward(0, OPS["MUL"], gu, vt, vt, grad=z(vt))
+    gt = E.backward(1, OPS["MUL"], gu, vt, vt, grad=gt)
+    gs = E.backward(0, OPS["DIV"], gt, vs, vsum, grad=z(vs))
+    gsum = E.backward(1, OPS["DIV"], gt, vs, vsum, grad=z(vsum))
+    gs = E.backward(0, OPS["SUM"], gsum, vs, axis=0, grad=gs)
+    gr = E.backward(0, OPS["POW"], gs, vr, two, grad=z(vr))
+    gq = E.backward(0, OPS["EXP"], gr, vq, grad=z(vq))
+    gh = E.backward(0, OPS["SUB"], gq, vh, vk, grad=z(vh))
+    gk = E.backward(1, OPS["SUB"], gq, vh, vk, grad=z(vk))
+    gh = E.backward(0, OPS["MAX"], gk, vh, axis=1, grad=gh)
+    gf = E.backward(0, OPS["CLIP"], gh, vf, grad=z(vf), attrs={"min": -0.5, "max": 1.5})
+    ge = E.backward(0, OPS["LEAKYRELU"], gf, ve, grad=z(ve), attrs={"negative_slope": 0.2})
+    gc = O.fma_bwd_accum(0, z(vc), ge, vc, vd)
+    gd = O.fma_bwd_accum(1, z(vd), ge, vc, vd)
+    gb = O.fma_bwd_accum(2, z(vb), ge, vc, vd)
+    gc = E.backward(0, OPS["SIGMOID"], gd, vc, grad=gc)
+    gb = E.backward(0, OPS["TANH"], gc, vb, grad=gb)
+    ga = E.backward(0, OPS["ADD"], gb, va, x, grad=z(va))
+    gx = E.backward(1, OPS["ADD"], gb, va, x, grad=z(x))
+    gx = E.backward(0, OPS["MUL"], ga, x, w, grad=gx)
+    gw = E.backward(1, OPS["MUL"], ga, x, w, grad=z(w))
+    P = model.parameters
+    assert_bitexact(P.grads[sx].to_numpy(), gx, "grad x")
+    assert_bitexact(P.grads[sw].to_numpy(), gw, "grad w")
+    assert_bitexact(P.grads[b].to_numpy(), gb, "grad b (FMA operand 3 and TANH)")
+    assert_bitexact(P.grads[e].to_numpy(), ge, "grad e")
+    assert_bitexact(P.grads[t].to_numpy(), gt, "grad t (MUL of a symbol with itself)")
+
+
+def test_model_grads_accumulate_until_zero_grad(gpu):
+    m = gpu.m
+    values = {"x": synth.normal((64, 48), 0, 1, 1230), "bias": synth.normal((1, 48), 0, 0.1, 1231)}
+    nodes = _bias_relu_nodes() + [(OPS["MEAN"], ["r"], None, "l")]
+    g, syms, inputs = native_graph(m, nodes, values, ["x", "bias"], params=["bias"])
+    g.loss(syms["l"])
+    model = m.Model(g)
+    model.forward(values["x"])
+    model.backward()
+    g1 = model.parameters.grads[syms["bias"]].to_numpy()
+    model.backward()
+    g2 = model.parameters.grads[syms["bias"]].to_numpy()
+    # nothing clears the intermediate gradients either (model.mojo:176-180 refills only the
+    # loss gradient): grads[r] becomes 2c, grads[y] 3c', and the bias gradient g1 + 3 g1
+    np.testing.assert_allclose(g2, 4 * g1, rtol=1e-5)
+    model.parameters.grads.set_zero()
+    assert not model.parameters.grads[syms["bias"]].to_numpy().any()
+    model.backward()
+    assert_bitexact(model.parameters.grads[syms["bias"]].to_numpy(), g1, "after zero_grad")
+
+
+def test_model_inference_stops_at_last_output(gpu):
+    m = gpu.m
+    x = synth.normal((10, 6), 0, 1, 1240)
+    g = m.Graph()
+    sx = g.input((10, 6))
+    a = g.op(m.OP.EXP, sx)
+    g.out(a)
+    b = g.op(m.OP.SUM, a)  # after the last output: not run by inference
+    g.loss(b)
+    model = m.Model(g)
+    outs = model.inference(x)
+    assert_bitexact(outs[0].to_numpy(), O.elwise_transform(OPS["EXP"], x), "inference output")
+    assert not model.parameters.tensors[b].to_numpy().any()
+    assert model.info()["n_inference_nodes"] == 1
+    model.forward(x)
+    assert model.parameters.tensors[b].to_numpy()[0] != 0
+
+
+def test_model_device_inputs_and_errors(gpu):
+    m = gpu.m
+    x = synth.normal((8, 8), 0, 1, 1250)
+    g = m.Graph()
+    sx = g.input((8, 8), trainable=True)
+    l = g.op(m.OP.SUM, g.op(m.OP.RELU, sx))
+    g.loss(l)
+    model = m.Model(g)
+    a = model.forward(m.Tensor.from_numpy(x)).to_numpy()
+    b = model.forward(x).to_numpy()
+    assert_bitexact(a, b, "device and host inputs")
+    with pytest.raises(m.MantleHipError):
+        model.forward()
+    with pytest.raises(m.MantleHipError):
+        model.forward(np.zeros(63, np.float32))
+    g2 = m.Graph()
+    s2 = g2.input((4,))
+    g2.op(m.OP.EXP, s2)
+    m2 = m.Model(g2, inference_only=True)
+    with pytest.raises(m.MantleHipError):
+        m2.inference(np.zeros(4, np.float32))  # no graph output
+    with pytest.raises(m.MantleHipError):
+        m2.backward()  # no loss
+
+
+def test_model_training_with_adam(gpu):
+    """Model + Adam(model.parameters): three steps against the same steps with the op-by-op
+    graph and Adam over (param, grad) pairs."""
+    m = gpu.m
+    x = synth.normal((128, 32), 0, 1, 1260)
+    w0 = synth.normal((1, 32), 0, 0.5, 1261)
+    b0 = synth.normal((1, 32), 0, 0.1, 1262)
+    g = m.Graph()
+    sx = g.input((128, 32))
+    sw = g.param((1, 32), init=w0)
+    sb = g.param((1, 32), init=b0)
+    h = g.op(m.OP.RELU, g.op(m.OP.ADD, g.op(m.OP.MUL, sx, sw), sb))
+    l = g.op(m.OP.MEAN, g.op(m.OP.MUL, h, h))
+    g.loss(l)
+    model = m.Model(g)  # unfused: bit-identical gradients, so bit-identical steps
+    opt = m.Adam(model.parameters, lr=0.01)
+    nodes = [(OPS["MUL"], ["x", "w"], None, "a"), (OPS["ADD"], ["a", "b"], None, "y"), (OPS["RELU"], ["y"], None, "h"),
+             (OPS["MUL"], ["h", "h"], None, "hh"), (OPS["MEAN"], ["hh"], None, "l")]
+    ref = Graph(nodes, ["w", "b"])
+    w, b = w0.copy(), b0.copy()
+    tw, tb = m.Tensor.from_numpy(w), m.Tensor.from_numpy(b)
+    gw, gb = m.Tensor(m.TensorShape(1, 32)), m.Tensor(m.TensorShape(1, 32))
+    ref_opt = m.Adam([(tw, gw), (tb, gb)], lr=0.01)
+    for it in range(3):
+        opt.zero_grad()
+        model.forward(x)
+        model.backward()
+        opt.step()
+        ref_opt.zero_grad()
+        vals = ref.forward(gpu, {"x": x, "w": tw.to_numpy(), "b": tb.to_numpy()})
+        grads = ref.backward(gpu, vals)
+        m._lib.call("mh_memcpy_h2d", gw.ptr, np.ascontiguousarray(grads["w"]).ctypes.data, 32 * 4)
+        m._lib.call("mh_memcpy_h2d", gb.ptr, np.ascontiguousarray(grads["b"]).ctypes.data, 32 * 4)
+        ref_opt.step()
+        assert_bitexact(model.parameters.tensors[sw].to_numpy(), tw.to_numpy(), f"w step {it}")
+        assert_bitexact(model.parameters.tensors[sb].to_numpy(), tb.to_numpy(), f"b step {it}")
+    assert opt.iter == 3

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from mantle_amd import synth
-from util import (O, OPS, GpuEngine, Graph, OracleEngine, assert_bitexact, assert_sum_close, assert_ulp,
+from util import (O, OPS, GpuEngine, Graph, OracleEngine, config5_nodes, assert_bitexact, assert_sum_close, assert_ulp,
                   check_fixture, load_fixtures)
 
 pytestmark = pytest.mark.gpu
@@ -381,13 +381,6 @@ def test_fused_bias_relu_shapes(gpu, sx, sb, keep_gy):
     mag = np.abs(gyd).sum(axis=red).reshape(sb) + np.abs(gb0)
     assert_sum_close(tgb.to_numpy(), ORC.backward(1, OPS["ADD"], gy, x, bias, grad=gb0), ex, "fused grad bias",
                      terms_abs=mag)
-
-
-def config5_nodes():
-    # MAX(ax1) -> SUB -> EXP -> SUM(ax1) -> DIV -> LOG -> MUL(onehot) -> MEAN
-    from util import softmax_nodes
-    return softmax_nodes("logits", 1) + [(OPS["LOG"], ["sm"], None, "lp"), (OPS["MUL"], ["lp", "onehot"], None, "t"),
-                                         (OPS["MEAN"], ["t"], None, "loss")]
 
 
 def config5_inputs(n, seed=0):

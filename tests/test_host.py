@@ -147,3 +147,48 @@ def test_python_mirror_broadcast_and_result_shapes():
     assert static_result_shape(OP.POW, (4, 5), (1,)).dims == (4, 5)
     with pytest.raises(mantle_amd.MantleHipError):
         broadcast_shapes((3,), (4,))
+
+
+# ---------------------------------------------------------------------------------------
+# graph builder (host-only: mh_graph_*)
+# ---------------------------------------------------------------------------------------
+def test_graph_builder_shapes_and_trainable():
+    import mantle_amd as m
+    g = m.Graph()
+    x = g.input((32, 32))
+    b = g.param((1, 32), init=np.zeros(32, np.float32))
+    y = g.op(m.OP.ADD, x, b)
+    assert (y.shape.dims, y.trainable) == ((32, 32), True)  # trainable if any operand is
+    z = g.op(m.OP.EXP, x)
+    assert not z.trainable
+    s0 = g.op(m.OP.SUM, y, attributes={"axis": 0})
+    assert s0.shape.dims == (1, 32)
+    sa = g.op(m.OP.MEAN, y)
+    assert sa.shape.dims == (1,)
+    p = g.op(m.OP.POW, y, 2.0)  # a float operand becomes a graph scalar
+    assert p.shape.dims == (32, 32) and g.params[-1].shape.dims == (1,) and not g.params[-1].trainable
+    f = g.op(m.OP.FMA, y, y, x)
+    c = g.op(m.OP.CLIP, f, attributes={"min": -1.0})
+    lr = g.op(m.OP.LEAKYRELU, c, attributes={"negative_slope": 0.1})
+    assert lr.shape.dims == (32, 32)
+    assert [s.name for s in g.symbols] == list(range(len(g.symbols)))
+    assert g.trainable_parameters() == [b]
+
+
+@pytest.mark.parametrize("build", [
+    lambda m, g, x: g.op(m.OP.ADD, x, g.input((4,))),                   # not broadcastable
+    lambda m, g, x: g.op(m.OP.POW, x, x),                               # exponent not shape (1)
+    lambda m, g, x: g.op(m.OP.LEAKYRELU, x),                            # negative_slope missing
+    lambda m, g, x: g.op(m.OP.FMA, x, x, g.input((4,))),                # FMA shapes differ
+    lambda m, g, x: g.op(m.OP.SUM, x, attributes={"axis": 2}),          # axis out of range
+    lambda m, g, x: g.op(7, x, x),                                      # DOT: not on this path
+    lambda m, g, x: g.op(m.OP.EXP, x, x),                               # arity
+    lambda m, g, x: g.param((2, 2), init=[1.0, 2.0]),                   # init size
+    lambda m, g, x: g.op(m.OP.SUM, x, attributes={"dim": 0}),           # unknown attribute
+])
+def test_graph_builder_rejects(build):
+    import mantle_amd as m
+    g = m.Graph()
+    x = g.input((5, 3))
+    with pytest.raises(m.MantleHipError):
+        build(m, g, x)

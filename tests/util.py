@@ -234,12 +234,40 @@ class Graph:
         return grads
 
 
+def native_graph(m, nodes, values, trainable=(), params=()):
+    """The util Graph node list as a mantle_amd.Graph: names not produced by a node become
+    inputs (in order of first use), or parameters holding their value when listed in
+    `params`; node outputs are op symbols. Returns (graph, {name: Symbol}, [input names])."""
+    g = m.Graph()
+    syms, inputs = {}, []
+    produced = {n[3] for n in nodes}
+    for op, ins, ax, out in nodes:
+        for name in ins:
+            if name in syms or name in produced:
+                continue
+            shape = np.asarray(values[name]).shape or (1,)
+            if name in params:
+                syms[name] = g.param(shape, init=values[name], trainable=name in trainable)
+            else:
+                syms[name] = g.input(shape, trainable=name in trainable)
+                inputs.append(name)
+        attrs = {"axis": ax} if ax is not None else None
+        syms[out] = g.op(op, *[syms[i] for i in ins], attributes=attrs)
+    return g, syms, inputs
+
+
 def softmax_nodes(x, axis, prefix=""):
     """Softmax graph, mantle/nn/activations.mojo:74-87."""
     p = prefix
     return [(OPS["MAX"], [x], axis, p + "max"), (OPS["SUB"], [x, p + "max"], None, p + "xm"),
             (OPS["EXP"], [p + "xm"], None, p + "e"), (OPS["SUM"], [p + "e"], axis, p + "s"),
             (OPS["DIV"], [p + "e", p + "s"], None, p + "sm")]
+
+
+def config5_nodes():
+    """Config 5: MAX(ax1) -> SUB -> EXP -> SUM(ax1) -> DIV -> LOG -> MUL(onehot) -> MEAN."""
+    return softmax_nodes("logits", 1) + [(OPS["LOG"], ["sm"], None, "lp"), (OPS["MUL"], ["lp", "onehot"], None, "t"),
+                                         (OPS["MEAN"], ["t"], None, "loss")]
 
 
 def logsoftmax_nodes(x, axis, prefix=""):
