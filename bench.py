@@ -21,6 +21,8 @@ The other configs are measured after the headline step and reported under "workl
         tensors through the multi-tensor entry point, 28 B/elem;
   adj   FMA / LEAKYRELU / CLIP forward and backward over 2^28 elements, and tstd over
         [8192, 8192] (axis 0, axis 1, all);
+  rows  row-fused CrossEntropyLoss ([2^20, 10], [32768, 1000]), Softmax and LogSoftmax
+        ([32768, 1000]), forward and backward;
   copy  a plain 1 GiB device copy (the library's copy kernel): the practical streaming rate.
 Tensors smaller than the 256 MB Infinity Cache are timed with the cache flushed before each
 op (a 1 GiB read sweep between ops, outside the timed events).
@@ -512,6 +514,40 @@ def run_adj(L, reps):
     return {"elements": n, **op_report(ops, med)}
 
 
+def run_rows(L, reps):
+    """Row-fused graphs: CrossEntropyLoss over [2^20, 10] and [32768, 1000]; Softmax and
+    LogSoftmax over [32768, 1000]. Bytes: loss forward 8 B/elem (x, target), loss backward
+    16 (x, target, grad_x read and written), Softmax / LogSoftmax forward 8 (x, out) and
+    backward 16 (x, grad_out, grad_x read and written)."""
+    d = Dev(L)
+    p = d.ptrs
+    ops = []
+    for rows, k in ((1 << 20, 10), (32768, 1000)):
+        n = rows * k
+        tag = f"{rows}x{k}"
+        for nm in ("x", "t", "o", "g"):
+            d.zeros(f"{nm}{tag}", n)
+        d.zeros(f"loss{tag}", 1)
+        d.zeros(f"ug{tag}", 1)
+        chk(L, L.mh_rand_normal(p[f"x{tag}"], n, 21, 0.0, 2.0), "rand")
+        chk(L, L.mh_rand_uniform(p[f"t{tag}"], n, 22, 0.0, 1.0), "rand")
+        chk(L, L.mh_fill(p[f"ug{tag}"], 1.0, 1), "fill")
+        ops += [(f"cross_entropy.fwd.{tag}", lambda tag=tag, r=rows, k=k: L.mh_cross_entropy_fwd(
+                    p[f"loss{tag}"], p[f"x{tag}"], p[f"t{tag}"], r, k), 8 * n + 4),
+                (f"cross_entropy.bwd.{tag}", lambda tag=tag, r=rows, k=k: L.mh_cross_entropy_bwd_accum(
+                    p[f"g{tag}"], p[f"x{tag}"], p[f"t{tag}"], p[f"ug{tag}"], r, k), 16 * n + 4)]
+        if k == 1000:
+            for nm, f, b in (("softmax", L.mh_softmax_fwd, L.mh_softmax_bwd_accum),
+                             ("logsoftmax", L.mh_logsoftmax_fwd, L.mh_logsoftmax_bwd_accum)):
+                ops += [(f"{nm}.fwd.{tag}", lambda tag=tag, r=rows, k=k, f=f: f(p[f"o{tag}"], p[f"x{tag}"], r, k), 8 * n),
+                        (f"{nm}.bwd.{tag}", lambda tag=tag, r=rows, k=k, b=b: b(p[f"g{tag}"], p[f"x{tag}"], p[f"t{tag}"],
+                                                                              r, k), 16 * n)]
+    chk(L, L.mh_sync(), "sync")
+    med = time_ops(d, ops, reps)
+    d.free()
+    return op_report(ops, med)
+
+
 def run_copy(L, reps):
     d = Dev(L)
     n = 1 << 28
@@ -696,8 +732,9 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--log2n", type=int, default=28)
-    ap.add_argument("--workloads", default="c3,c4,c5,adam,adj,copy",
-                    help="extra workloads after the headline step (comma list of c3,c4,c5,adam,adj,copy; 'none')")
+    ap.add_argument("--workloads", default="c3,c4,c5,adam,adj,rows,copy",
+                    help="extra workloads after the headline step (comma list of c3,c4,c5,adam,adj,rows,copy; "
+                         "'none')")
     ap.add_argument("--reps", type=int, default=10, help="repetitions per op of the extra workloads")
     ap.add_argument("--cpu-log2n", type=int, default=24)
     ap.add_argument("--cpu-reps", type=int, default=2)
@@ -763,7 +800,7 @@ def main():
     wl = [w for w in args.workloads.split(",") if w and w != "none"]
     runners = {"c3": lambda: run_c3(L, args.reps), "c4": lambda: run_c4(L, args.reps),
                "c5": lambda: run_c5(L, args.reps), "adam": lambda: run_adam(L, args.reps),
-               "adj": lambda: run_adj(L, args.reps),
+               "adj": lambda: run_adj(L, args.reps), "rows": lambda: run_rows(L, args.reps),
                "copy": lambda: run_copy(L, args.reps)}
     if wl:
         out["workloads"] = {}

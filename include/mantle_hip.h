@@ -200,7 +200,7 @@ int mh_bias_relu_fwd(float* y, float* r, const float* x, const mh_shape* sx, con
 int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const float* y,
                            const float* ug, const mh_shape* sx, const mh_shape* sbias);
 
-/* Row-fused forward of the classifier-head graph over x [rows, classes] (classes <= 32):
+/* Row-fused forward of the classifier-head graph over x [rows, classes] (classes <= 2047):
  *   MAX(x, axis 1) -> SUB -> EXP -> SUM(axis 1) -> DIV -> LOG -> MUL(target) -> MEAN
  * i.e. Softmax (mantle/nn/activations.mojo:74-87) followed by LOG, MUL and MEAN
  * (basics.mojo:288-309, 94-129, 428-506): loss[0] = mean(log(softmax(x)) * target), with no
@@ -215,6 +215,30 @@ int mh_softmax_log_mul_mean_fwd(float* loss, const float* x, const float* target
  * target, updates grad_x, in one pass. */
 int mh_softmax_log_mul_mean_bwd_accum(float* grad_x, const float* x, const float* target,
                                       const float* ug, int64_t rows, int64_t classes);
+
+/* Row-fused graphs over the last axis of x [rows, classes], classes <= 2047 (longer rows
+ * return MH_ERR_INVALID: use the op-by-op entry points). Outputs and gradients are
+ * bit-identical to the op-by-op forward_op / backward_op calls for finite inputs (each row
+ * sum runs in the order the library's row reductions use for that length); only a loss's
+ * all-element sum runs in another order (rtol class).
+ *
+ * Softmax (mantle/nn/activations.mojo:74-87): MAX(axis) -> SUB -> EXP -> SUM(axis) -> DIV.
+ * The backward takes grad_out, the gradient of the Softmax output, and accumulates into
+ * grad_x what the graph's five backward nodes give from zeroed intermediate gradients. */
+int mh_softmax_fwd(float* out, const float* x, int64_t rows, int64_t classes);
+int mh_softmax_bwd_accum(float* grad_x, const float* x, const float* grad_out, int64_t rows, int64_t classes);
+
+/* LogSoftmax (activations.mojo:94-108): MAX(axis) -> SUB -> EXP -> SUM(axis) -> LOG ->
+ * SUB(x - max, log sum). Backward as for Softmax. */
+int mh_logsoftmax_fwd(float* out, const float* x, int64_t rows, int64_t classes);
+int mh_logsoftmax_bwd_accum(float* grad_x, const float* x, const float* grad_out, int64_t rows, int64_t classes);
+
+/* CrossEntropyLoss (mantle/nn/loss.mojo:45-61) of predictions x [rows, classes] against
+ * target: LogSoftmax(x, axis 1) -> MUL(target, .) -> SUM -> MUL(., f32(-1 / rows)); loss is a
+ * device scalar. The backward takes ug, the gradient of the loss (a device scalar). */
+int mh_cross_entropy_fwd(float* loss, const float* x, const float* target, int64_t rows, int64_t classes);
+int mh_cross_entropy_bwd_accum(float* grad_x, const float* x, const float* target, const float* ug, int64_t rows,
+                               int64_t classes);
 
 /* ---- graph and model: Graph (mantle/autograd/graph.mojo:33-217), Model
  * (mantle/nn/model.mojo:55-340) and its Collections (mantle/autograd/collection.mojo:24-224)

@@ -15,11 +15,15 @@ from .ops import (  # noqa: F401
     forward_op, backward_op, backward_op_both, broadcast_shapes, get_reduce_shape, fill,
     elwise_transform, elwise_op, accumulate_grad, tsum, tmean, tmax, tstd, static_result_shape,
     bias_relu_forward, bias_relu_backward, softmax_log_mul_mean_forward, softmax_log_mul_mean_backward,
+    softmax_forward, softmax_backward, logsoftmax_forward, logsoftmax_backward, cross_entropy_forward,
+    cross_entropy_backward,
 )
 
 __all__ = [
     "Adam", "Collection", "Graph", "Model", "Parameters", "Symbol", "MantleHipError", "Tensor", "TensorShape", "init", "sync", "OP", "forward_op", "backward_op",
     "backward_op_both", "broadcast_shapes", "get_reduce_shape", "fill", "elwise_transform",
     "elwise_op", "accumulate_grad", "tsum", "tmean", "tmax", "tstd", "static_result_shape", "bias_relu_forward",
-    "bias_relu_backward", "softmax_log_mul_mean_forward", "softmax_log_mul_mean_backward",
+    "bias_relu_backward", "softmax_log_mul_mean_forward", "softmax_log_mul_mean_backward", "softmax_forward",
+    "softmax_backward", "logsoftmax_forward", "logsoftmax_backward", "cross_entropy_forward",
+    "cross_entropy_backward",
 ]

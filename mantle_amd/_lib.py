@@ -103,6 +103,12 @@ SIGNATURES = {
     "mh_bias_relu_bwd_accum": [_VP, _VP, _VP, _VP, _VP, _S, _S],
     "mh_softmax_log_mul_mean_fwd": [_VP, _VP, _VP, _I64, _I64],
     "mh_softmax_log_mul_mean_bwd_accum": [_VP, _VP, _VP, _VP, _I64, _I64],
+    "mh_softmax_fwd": [_VP, _VP, _I64, _I64],
+    "mh_softmax_bwd_accum": [_VP, _VP, _VP, _I64, _I64],
+    "mh_logsoftmax_fwd": [_VP, _VP, _I64, _I64],
+    "mh_logsoftmax_bwd_accum": [_VP, _VP, _VP, _I64, _I64],
+    "mh_cross_entropy_fwd": [_VP, _VP, _VP, _I64, _I64],
+    "mh_cross_entropy_bwd_accum": [_VP, _VP, _VP, _VP, _I64, _I64],
     "mh_fma_fwd": [_VP, _VP, _VP, _VP, _I64],
     "mh_fma_bwd_accum": [_I, _VP, _VP, _VP, _VP, _I64],
     "mh_leakyrelu_fwd": [_VP, _VP, _I64, _F],

@@ -154,6 +154,7 @@ __device__ __forceinline__ void epi_store(float* out, float*, int64_t o, float v
         case EPI_MEAN: out[o] = v / div; break;
         case EPI_ACCUM: out[o] = out[o] + v; break;
         case EPI_STD: out[o] = __builtin_sqrtf(v / div); break;
+        case EPI_SCALE: out[o] = v * div; break;
         default: out[o] = out[o] + (-v); break;
     }
 }

@@ -1,22 +1,46 @@
-// mh_softmax.hip -- row-fused forward and backward of the classifier-head graph
+// mh_softmax.hip -- row-fused forward and backward of Mantle's row graphs over the last axis
+// of x [rows, classes]:
 //
-//   MAX(x, axis 1) -> SUB -> EXP -> SUM(axis 1) -> DIV -> LOG -> MUL(target) -> MEAN
+//   Softmax      (mantle/nn/activations.mojo:74-87)
+//                MAX(axis) -> SUB -> EXP -> SUM(axis) -> DIV                    -> out
+//   LogSoftmax   (activations.mojo:94-108)
+//                MAX(axis) -> SUB -> EXP -> SUM(axis) -> LOG -> SUB(xm, ls)     -> out
+//   CrossEntropyLoss (mantle/nn/loss.mojo:45-61)
+//                LogSoftmax -> MUL(target, .) -> SUM -> MUL(., f32(-1 / rows))  -> loss
+//   the config-5 head
+//                Softmax -> LOG -> MUL(., target) -> MEAN                       -> loss
 //
-// over x [rows, classes]: Mantle's Softmax (mantle/nn/activations.mojo:74-87) followed by LOG,
-// MUL and MEAN (mantle/autograd/ops/basics.mojo:288-309, 94-129, 428-506). Op by op that is 8
-// forward and 10 backward kernels and about 14 passes over [rows, classes]; here the forward
-// reads x and target once and the backward reads x and target and updates grad_x once.
+// Op by op each graph is 5-9 forward and 7-10 backward kernels and 8-14 passes over
+// [rows, classes]; fused, the forward reads x (and the target) once and the backward reads
+// x, the target or upstream gradient, and updates grad_x once.
 //
-// Every per-element value is computed with the same expression, in the same order, as the
-// op-by-op chain, and every gradient accumulation happens in Model.backward's node order
-// (model.mojo:194-330), so grad_x is bit-identical to the ten backward_op calls starting from
-// zeroed intermediate grads. Row sums run in element order (as both the reference's scalar
-// tail loop and the op-by-op GPU path do for rows this short). Only the final MEAN over all
-// elements sums in another order (the rtol class).
+// Every per-element value uses the same expression, in the same order, as the op-by-op
+// chain, every gradient accumulates in Model.backward's node order (model.mojo:194-330), and
+// every row sum runs in the order the library's own row reductions use for that row length,
+// so grad_x (and the Softmax / LogSoftmax outputs) are bit-identical to the op-by-op
+// backward_op calls starting from zeroed intermediate gradients, for finite inputs. The row
+// reductions' orders:
+//   classes <= 64    element order from +0 (k_rows_lds / k_rows_thread): one thread per row,
+//                    the row in registers, LDS staging of coalesced loads;
+//   64 < classes < 2048
+//                    k_rows_wave's order (per lane, quads lane + 64 q accumulated in groups
+//                    of four, the tail into the first group, the sixteen partials summed in
+//                    order, then an xor butterfly; lane-strided elements when classes is not
+//                    a multiple of 4): one wavefront per row, the row across its lanes.
+// Only the all-element sum of a loss graph (MEAN or SUM) runs in another order (the rtol
+// class).
 //
-// One thread owns one row, held in registers (loops unrolled to 8, 16 or 32 classes); a block
-// of 256 threads stages RB rows (256, fewer when wide rows would exceed 64 KB of LDS) of each
-// operand in LDS with coalesced loads (rows of up to 32 classes).
+// Backward, per element, in node order (0 + v is an accumulation into a zeroed gradient):
+//   Softmax    g_sm given                       | head graph: g_t = 0 + c * ug; g_lp = 0 + g_t * t;
+//                                               |             g_sm = 0 + g_lp / sm
+//              DIV 0: g_e = 0 + g_sm / s;  DIV 1: g_s = 0 + sum((-e) / (s * s) * g_sm)
+//   LogSoftmax g_lsm given                      | cross entropy: g_ret = 0 + ug * c;
+//                                               |   g_tl = 0 + 1 * g_ret; g_lsm = 0 + g_tl * t
+//              SUB 0: g_xm = 0 + g_lsm;  SUB 1: g_ls = 0 + (-sum(g_lsm));  LOG: g_s = 0 + g_ls / s
+//   then       SUM: rg = 1 * g_s ((1 * g_s) * g_s over one class, tensorutils.mojo:380-393)
+//              EXP: g_xm = g_xm + e * (g_e + rg)
+//              SUB(x, max): grad_x += g_xm;  g_max = 0 + (-sum(g_xm))
+//              MAX: grad_x += (x == max ? fl(1 / count) * g_max : 0)
 #include <cfloat>
 
 #include "mh_internal.h"
@@ -24,18 +48,30 @@
 
 namespace mh {
 
+enum RowGraph : int { G_SMLM = 0, G_CE = 1, G_SOFTMAX = 2, G_LOGSOFTMAX = 3 };
+
 constexpr int kSThreads = 256;
-constexpr int kSMaxClasses = 32;
+constexpr int kSThreadMax = 64;         // rows up to this length: one thread per row
+constexpr int kSWaveMax = 2047;         // longer rows (up to this): one wavefront per row
+constexpr int kSLaneElems = 32;         // per-lane slots of the wavefront engine (64 * 32 > 2047)
 constexpr int64_t kSLdsFloats = 16384;  // 64 KB of tiles per block
 
-// Rows per block: 256, halved until `tiles` tiles of rb * K floats fit the LDS budget.
+// Graphs whose backward starts from g_sm (DIV) rather than g_lsm (SUB).
+template <int V>
+constexpr bool from_softmax() {
+    return V == G_SMLM || V == G_SOFTMAX;
+}
+
+__device__ __forceinline__ float max_simd(float a, float b) { return a > b ? a : b; }
+
+// Rows per block of the thread engine: 256, halved until `tiles` tiles of rb * K floats fit.
 static inline int rows_per_block(int tiles, int64_t K) {
     int rb = kSThreads;
-    while (rb > 64 && (int64_t)tiles * rb * K > kSLdsFloats) rb >>= 1;
+    while (rb > 32 && (int64_t)tiles * rb * K > kSLdsFloats) rb >>= 1;
     return rb;
 }
 
-// Copies rows [r0, r0 + rows) of a [*, K] array into LDS (16-byte aligned source: float4).
+// Copies `cnt` floats from src + base into LDS (16-byte aligned source: float4), and back.
 __device__ __forceinline__ void stage_tile(float* dst, const float* __restrict__ src, int64_t base, int cnt,
                                            bool al) {
     const int t = threadIdx.x;
@@ -49,7 +85,20 @@ __device__ __forceinline__ void stage_tile(float* dst, const float* __restrict__
     for (int i = done + t; i < cnt; i += kSThreads) dst[i] = src[base + i];
 }
 
-__device__ __forceinline__ float block_sum_rows(float v, float* ws) {
+__device__ __forceinline__ void unstage_tile(float* __restrict__ dst, const float* src, int64_t base, int cnt,
+                                             bool al) {
+    const int t = threadIdx.x;
+    int done = 0;
+    if (al) {
+        const int nq = cnt >> 2;
+        float4* d4 = reinterpret_cast<float4*>(dst + base);
+        for (int i = t; i < nq; i += kSThreads) d4[i] = reinterpret_cast<const float4*>(src)[i];
+        done = nq << 2;
+    }
+    for (int i = done + t; i < cnt; i += kSThreads) dst[base + i] = src[i];
+}
+
+__device__ __forceinline__ float block_sum(float v, float* ws) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m);
     if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = v;
@@ -57,22 +106,38 @@ __device__ __forceinline__ float block_sum_rows(float v, float* ws) {
     return ((ws[0] + ws[1]) + ws[2]) + ws[3];
 }
 
-// Forward: part[block] = sum over the block's rows of sum_j log(softmax(x)_j) * target_j.
-// The row lives in registers (KM >= K: loops unrolled, elements j >= K skipped); LDS only
-// stages the coalesced loads.
-template <int KM>
+// The upstream gradient of the row part, per element: g_sm (from_softmax) or g_lsm.
+template <int V>
+__device__ __forceinline__ float upstream(float u, float e, float s, float gconst) {
+    if constexpr (V == G_SMLM) {
+        const float glp = 0.0f + gconst * u;  // MUL backward, operand 0 (gconst = g_t)
+        return 0.0f + glp / (e / s);          // LOG backward
+    } else if constexpr (V == G_CE) {
+        return 0.0f + gconst * u;  // MUL(target, .) backward, operand 1 (gconst = g_tl)
+    } else {
+        return u;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// thread engine: rows of at most KM (<= 64) elements, element-order row sums
+// ---------------------------------------------------------------------------------------
+// Forward. Loss graphs write a block partial of the all-element sum; Softmax / LogSoftmax
+// write the output tile (through LDS, coalesced).
+template <int V, int KM>
 __global__ void __launch_bounds__(kSThreads)
-    k_smlm_fwd(const float* __restrict__ x, const float* __restrict__ tg, int64_t rows, int K, int rb, bool al,
-               float* __restrict__ part) {
+    k_rowt_fwd(const float* __restrict__ x, const float* __restrict__ tg, float* __restrict__ out, int64_t rows,
+               int K, int rb, bool al, float* __restrict__ part) {
     extern __shared__ float4 smem4[];
     __shared__ float ws[4];
+    constexpr bool LOSS = V == G_SMLM || V == G_CE;
     float* xs = reinterpret_cast<float*>(smem4);
     float* ts = xs + rb * K;
     const int64_t r0 = (int64_t)blockIdx.x * rb;
     const int nr = (int)((rows - r0) < rb ? (rows - r0) : rb);
     const int64_t base = r0 * K;
     stage_tile(xs, x, base, nr * K, al);
-    stage_tile(ts, tg, base, nr * K, al);
+    if (LOSS) stage_tile(ts, tg, base, nr * K, al);
     __syncthreads();
     float rowsum = 0.0f;
     const int t = threadIdx.x;
@@ -80,81 +145,83 @@ __global__ void __launch_bounds__(kSThreads)
         float xr[KM], e[KM];
 #pragma unroll
         for (int j = 0; j < KM; ++j) xr[j] = j < K ? xs[t * K + j] : 0.0f;
-        float m = -FLT_MAX;  // MAX.forward: reduce with max_simd from min_finite
+        float m = -FLT_MAX;  // MAX.forward: max_simd from min_finite, element order
 #pragma unroll
         for (int j = 0; j < KM; ++j)
-            if (j < K) m = m > xr[j] ? m : xr[j];
-        float s = 0.0f;  // SUM.forward over the row, in element order
+            if (j < K) m = max_simd(m, xr[j]);
+        float s = 0.0f;  // SUB, EXP, SUM.forward
 #pragma unroll
         for (int j = 0; j < KM; ++j) {
             if (j < K) {
-                e[j] = mexp(xr[j] - m);  // SUB.forward, EXP.forward
+                e[j] = mexp(xr[j] - m);
                 s = s + e[j];
             }
         }
+        const float ls = (V == G_CE || V == G_LOGSOFTMAX) ? mlog(s) : 0.0f;  // LOG.forward of the sum
 #pragma unroll
         for (int j = 0; j < KM; ++j) {
             if (j < K) {
-                const float sm = e[j] / s;                 // DIV.forward
-                const float lp = mlog(sm);                 // LOG.forward
-                rowsum = rowsum + lp * ts[t * K + j];      // MUL.forward, then the MEAN's sum
+                if constexpr (V == G_SMLM) {
+                    rowsum = rowsum + mlog(e[j] / s) * ts[t * K + j];  // DIV, LOG, MUL, the MEAN's sum
+                } else if constexpr (V == G_CE) {
+                    rowsum = rowsum + ts[t * K + j] * ((xr[j] - m) - ls);  // SUB(xm, ls), MUL(target, .)
+                } else if constexpr (V == G_SOFTMAX) {
+                    xs[t * K + j] = e[j] / s;  // DIV.forward
+                } else {
+                    xs[t * K + j] = (xr[j] - m) - ls;  // SUB(xm, ls).forward
+                }
             }
         }
     }
-    const float tot = block_sum_rows(rowsum, ws);
-    if (t == 0) part[blockIdx.x] = tot;
+    if constexpr (LOSS) {
+        const float tot = block_sum(rowsum, ws);
+        if (t == 0) part[blockIdx.x] = tot;
+    } else {
+        __syncthreads();
+        unstage_tile(out, xs, base, nr * K, al);
+    }
 }
 
-// Backward from ug = d loss (shape (1)), accumulated into grad_x:
-//   MEAN  : g_t   = 0 + f32(1/f64(N)) * ug
-//   MUL   : g_lp  = 0 + g_t * target                      (target not trainable)
-//   LOG   : g_sm  = 0 + g_lp / sm
-//   DIV 0 : g_e   = 0 + g_sm / s
-//   DIV 1 : g_s   = 0 + sum_j ((-e_j) / (s * s)) * g_sm_j
-//   SUM   : g_e   = g_e + 1 * g_s   ((1 * g_s) * g_s for one class: see below)
-//   EXP   : g_xm  = 0 + exp(xm) * g_e
-//   SUB 0 : grad_x = grad_x + g_xm
-//   SUB 1 : g_max = 0 + (-sum_j g_xm_j)
-//   MAX   : grad_x = grad_x + (x == m ? fl(1/count) * g_max : 0)
-// Registers hold the row (KM >= K); LDS stages x, target and grad_x (written back in place).
-template <int KM>
+// Backward, accumulated into grad_x. `up` is the target (loss graphs) or the upstream
+// gradient of the output (Softmax / LogSoftmax); `ug` the loss gradient (shape (1)); `c` the
+// graph constant: f32(1 / f64(rows * classes)) for the MEAN, f32(-1 / f64(rows)) for the
+// cross-entropy scale.
+template <int V, int KM>
 __global__ void __launch_bounds__(kSThreads)
-    k_smlm_bwd(float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ tg,
-               const float* __restrict__ ug, int64_t rows, int K, int rb, bool al, float cmean) {
+    k_rowt_bwd(float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ up,
+               const float* __restrict__ ug, int64_t rows, int K, int rb, bool al, float c) {
     extern __shared__ float4 smem4[];
     float* xs = reinterpret_cast<float*>(smem4);
-    float* ts = xs + rb * K;
-    float* gs = ts + rb * K;
+    float* us = xs + rb * K;
+    float* gs = us + rb * K;
     const int64_t r0 = (int64_t)blockIdx.x * rb;
     const int nr = (int)((rows - r0) < rb ? (rows - r0) : rb);
     const int64_t base = r0 * K;
     const int cnt = nr * K;
     stage_tile(xs, x, base, cnt, al);
-    stage_tile(ts, tg, base, cnt, al);
+    stage_tile(us, up, base, cnt, al);
     stage_tile(gs, g, base, cnt, al);
     __syncthreads();
     const int t = threadIdx.x;
     if (t < nr) {
-        float xr[KM], e[KM], w[KM];
+        float xr[KM], e[KM], pre[KM];
 #pragma unroll
         for (int j = 0; j < KM; ++j) xr[j] = j < K ? xs[t * K + j] : 0.0f;
-        // forward values: the row max as MAX.forward takes it (max_simd from min_finite),
-        // e = exp(x - m), s = sum e; and, as MAX.backward recomputes it, the max with its
-        // count (an element that is neither above nor below the running max -- equal, or
-        // NaN -- adds to the count)
+        // the forward row max (MAX.forward) and, as MAX.backward recomputes it, the max with
+        // its count (an element neither above nor below the running max adds to the count)
         float m = -FLT_MAX, mb = -FLT_MAX;
-        uint32_t c = 0;
+        uint32_t cntm = 0;
 #pragma unroll
         for (int j = 0; j < KM; ++j) {
             if (j < K) {
                 const float v = xr[j];
-                m = m > v ? m : v;
+                m = max_simd(m, v);
                 if (mb > v) {
                 } else if (v > mb) {
                     mb = v;
-                    c = 1;
+                    cntm = 1;
                 } else {
-                    c += 1;
+                    cntm += 1;
                 }
             }
         }
@@ -166,66 +233,429 @@ __global__ void __launch_bounds__(kSThreads)
                 s = s + e[j];
             }
         }
-        const float gt = 0.0f + cmean * ug[0];  // MEAN backward (all elements)
-        const float s2 = s * s;
-        float acc = 0.0f;
+        const float gconst = V == G_SMLM ? 0.0f + c * ug[0]                       // MEAN backward
+                             : V == G_CE ? 0.0f + 1.0f * (0.0f + ug[0] * c)       // MUL(., c), SUM backward
+                                         : 0.0f;
+        // pre: g_e after DIV (from_softmax), or g_xm after SUB(xm, ls)
+        float acc = 0.0f, gS;
+        if constexpr (from_softmax<V>()) {
+            const float s2 = s * s;
 #pragma unroll
-        for (int j = 0; j < KM; ++j) {
-            if (j < K) {
-                const float sm = e[j] / s;
-                const float glp = 0.0f + gt * ts[t * K + j];  // MUL backward, operand 0
-                const float gsm = 0.0f + glp / sm;            // LOG backward
-                w[j] = 0.0f + gsm / s;                        // DIV backward, operand 0: g_e
-                acc = acc + ((-e[j]) / s2) * gsm;             // DIV backward, operand 1
+            for (int j = 0; j < KM; ++j) {
+                if (j < K) {
+                    const float gsm = upstream<V>(us[t * K + j], e[j], s, gconst);
+                    pre[j] = 0.0f + gsm / s;
+                    acc = acc + ((-e[j]) / s2) * gsm;
+                }
             }
+            gS = 0.0f + acc;
+        } else {
+#pragma unroll
+            for (int j = 0; j < KM; ++j) {
+                if (j < K) {
+                    const float glsm = upstream<V>(us[t * K + j], e[j], s, gconst);
+                    pre[j] = 0.0f + glsm;
+                    acc = acc + glsm;
+                }
+            }
+            gS = 0.0f + (0.0f + (-acc)) / s;
         }
-        const float gS = 0.0f + acc;
-        // SUM backward: rg = 1 * g_s, except over a size-1 axis (K == 1), where the reduced
-        // shape equals the input shape and accumulate_op applies the multiply twice
-        // (tensorutils.mojo:380-393): rg = (1 * g_s) * g_s
         const float rgs = K == 1 ? (1.0f * gS) * gS : 1.0f * gS;
         float acc2 = 0.0f;
 #pragma unroll
         for (int j = 0; j < KM; ++j) {
             if (j < K) {
-                const float ge = w[j] + rgs;  // SUM backward
-                w[j] = 0.0f + e[j] * ge;      // EXP backward: g_xm
-                acc2 = acc2 + w[j];
+                if constexpr (from_softmax<V>()) pre[j] = 0.0f + e[j] * (pre[j] + rgs);
+                else pre[j] = pre[j] + e[j] * (0.0f + rgs);
+                acc2 = acc2 + pre[j];
             }
         }
-        const float gmax = 0.0f + (-acc2);          // SUB backward, operand 1
-        const float sg = (1.0f / (float)c) * gmax;  // MAX backward factor
+        const float sg = (1.0f / (float)cntm) * (0.0f + (-acc2));  // SUB 1, then the MAX factor
 #pragma unroll
         for (int j = 0; j < KM; ++j) {
             if (j < K) {
-                const float a = gs[t * K + j] + w[j];           // SUB backward, operand 0
-                gs[t * K + j] = a + (xr[j] == mb ? sg : 0.0f);  // MAX backward
+                const float a = gs[t * K + j] + pre[j];
+                gs[t * K + j] = a + (xr[j] == mb ? sg : 0.0f);
             }
         }
     }
     __syncthreads();
-    // write the grad tile back
-    if (al) {
-        const int nq = cnt >> 2;
-        float4* g4 = reinterpret_cast<float4*>(g + base);
-        for (int i = t; i < nq; i += kSThreads) g4[i] = reinterpret_cast<const float4*>(gs)[i];
-        for (int i = (nq << 2) + t; i < cnt; i += kSThreads) g[base + i] = gs[i];
+    unstage_tile(g, gs, base, cnt, al);
+}
+
+// ---------------------------------------------------------------------------------------
+// wavefront engine: 64 < classes <= 2047, one wavefront per row, k_rows_wave's order
+// ---------------------------------------------------------------------------------------
+// Lane slot i holds element 4 (lane + 64 (i / 4)) + i % 4 (VEC: classes % 4 == 0, quads
+// lane + 64 q) or lane + 64 i (otherwise).
+template <bool VEC>
+__device__ __forceinline__ int slot_elem(int lane, int i) {
+    return VEC ? 4 * (lane + 64 * (i >> 2)) + (i & 3) : lane + 64 * i;
+}
+
+struct OpAdd {
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct OpMax {
+    __device__ float operator()(float a, float b) const { return a > b ? a : b; }
+};
+
+// One row's reduction in the order of k_rows_wave<R, LD, VEC> with a single chunk.
+template <bool VEC, int NE, class OP>
+__device__ __forceinline__ float wave_row_reduce(const float* v, int lane, int K, float init, OP op) {
+    float acc = init;
+    if constexpr (VEC) {
+        constexpr int NQ = NE / 4;
+        const int nq = K >> 2;
+        float a4[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a4[u][j] = init;
+        int done = 0;  // quads taken by the four-quad main loop (a prefix of the groups)
+#pragma unroll
+        for (int q0 = 0; q0 + 3 < NQ; q0 += 4) {
+            if (lane + 64 * (q0 + 3) < nq) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) a4[u][j] = op(a4[u][j], v[(q0 + u) * 4 + j]);
+                done = q0 + 4;
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            if (q >= done && lane + 64 * q < nq) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a4[0][j] = op(a4[0][j], v[q * 4 + j]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = op(acc, a4[u][j]);
     } else {
-        for (int i = t; i < cnt; i += kSThreads) g[base + i] = gs[i];
+#pragma unroll
+        for (int i = 0; i < NE; ++i)
+            if (lane + 64 * i < K) acc = op(acc, v[i]);
+    }
+#pragma unroll
+    for (int mm = 32; mm >= 1; mm >>= 1) acc = op(acc, __shfl_xor(acc, mm));
+    return acc;
+}
+
+template <bool VEC, int NE>
+__device__ __forceinline__ void load_row(float* v, const float* __restrict__ src, int lane, int K, bool al) {
+    if (VEC && al) {
+#pragma unroll
+        for (int q = 0; q < NE / 4; ++q) {
+            const int qi = lane + 64 * q;
+            if (4 * qi < K) {
+                const float4 f = reinterpret_cast<const float4*>(src)[qi];
+                v[4 * q] = f.x;
+                v[4 * q + 1] = f.y;
+                v[4 * q + 2] = f.z;
+                v[4 * q + 3] = f.w;
+            } else {
+                v[4 * q] = v[4 * q + 1] = v[4 * q + 2] = v[4 * q + 3] = 0.0f;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+            const int k = slot_elem<VEC>(lane, i);
+            v[i] = k < K ? src[k] : 0.0f;
+        }
     }
 }
 
-static int check_smlm(const char* what, const float* x, const float* tg, int64_t rows, int64_t classes) {
+template <bool VEC, int NE>
+__device__ __forceinline__ void store_row(float* __restrict__ dst, const float* v, int lane, int K, bool al) {
+    if (VEC && al) {
+#pragma unroll
+        for (int q = 0; q < NE / 4; ++q) {
+            const int qi = lane + 64 * q;
+            if (4 * qi < K)
+                reinterpret_cast<float4*>(dst)[qi] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+            const int k = slot_elem<VEC>(lane, i);
+            if (k < K) dst[k] = v[i];
+        }
+    }
+}
+
+// Row max (MAX.forward's order), e = exp(x - m) and s = sum e (SUM.forward's order).
+template <bool VEC, int NE>
+__device__ __forceinline__ void wave_row_softmax(const float* xv, float* e, int lane, int K, float* m_out,
+                                                 float* s_out) {
+    const float m = wave_row_reduce<VEC, NE>(xv, lane, K, -FLT_MAX, OpMax{});
+#pragma unroll
+    for (int i = 0; i < NE; ++i) e[i] = slot_elem<VEC>(lane, i) < K ? mexp(xv[i] - m) : 0.0f;
+    *m_out = m;
+    *s_out = wave_row_reduce<VEC, NE>(e, lane, K, 0.0f, OpAdd{});
+}
+
+template <int V, bool VEC, int NE>
+__global__ void __launch_bounds__(kSThreads)
+    k_roww_fwd(const float* __restrict__ x, const float* __restrict__ tg, float* __restrict__ out, int64_t rows,
+               int K, bool al, float* __restrict__ part) {
+    __shared__ float ws[4];
+    constexpr bool LOSS = V == G_SMLM || V == G_CE;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    float rowsum = 0.0f;
+    if (row < rows) {  // uniform per wavefront
+        const int64_t base = row * (int64_t)K;
+        float xv[NE], e[NE];
+        load_row<VEC, NE>(xv, x + base, lane, K, al);
+        float m, s;
+        wave_row_softmax<VEC, NE>(xv, e, lane, K, &m, &s);
+        const float ls = (V == G_CE || V == G_LOGSOFTMAX) ? mlog(s) : 0.0f;
+        if constexpr (LOSS) {
+            float tv[NE];
+            load_row<VEC, NE>(tv, tg + base, lane, K, al);
+#pragma unroll
+            for (int i = 0; i < NE; ++i) {
+                if (slot_elem<VEC>(lane, i) < K) {
+                    if constexpr (V == G_SMLM) rowsum = rowsum + mlog(e[i] / s) * tv[i];
+                    else rowsum = rowsum + tv[i] * ((xv[i] - m) - ls);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NE; ++i) xv[i] = V == G_SOFTMAX ? e[i] / s : (xv[i] - m) - ls;
+            store_row<VEC, NE>(out + base, xv, lane, K, al);
+        }
+    }
+    if constexpr (LOSS) {  // every wavefront reaches the barrier
+        const float tot = block_sum(rowsum, ws);
+        if (threadIdx.x == 0) part[blockIdx.x] = tot;
+    }
+}
+
+template <int V, bool VEC, int NE>
+__global__ void __launch_bounds__(kSThreads)
+    k_roww_bwd(float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ up,
+               const float* __restrict__ ug, int64_t rows, int K, bool al, float c) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // uniform per wavefront; no block barrier below
+    const int64_t base = row * (int64_t)K;
+    float xv[NE], e[NE], pre[NE], tmp[NE];
+    load_row<VEC, NE>(xv, x + base, lane, K, al);
+    float m, s;
+    wave_row_softmax<VEC, NE>(xv, e, lane, K, &m, &s);
+    // the max with its count, as MAX.backward recomputes it (lane order, then a butterfly)
+    float mb = -FLT_MAX;
+    uint32_t cntm = 0;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        if (slot_elem<VEC>(lane, i) < K) {
+            const float v = xv[i];
+            if (mb > v) {
+            } else if (v > mb) {
+                mb = v;
+                cntm = 1;
+            } else {
+                cntm += 1;
+            }
+        }
+    }
+#pragma unroll
+    for (int mm = 32; mm >= 1; mm >>= 1) {
+        const float om = __shfl_xor(mb, mm);
+        const uint32_t oc = (uint32_t)__shfl_xor((int)cntm, mm);
+        if (mb > om) {
+        } else if (om > mb) {
+            mb = om;
+            cntm = oc;
+        } else {
+            cntm += oc;
+        }
+    }
+    load_row<VEC, NE>(tmp, up + base, lane, K, al);
+    const float gconst = V == G_SMLM ? 0.0f + c * ug[0] : V == G_CE ? 0.0f + 1.0f * (0.0f + ug[0] * c) : 0.0f;
+    float gS;
+    if constexpr (from_softmax<V>()) {
+        const float s2 = s * s;
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+            const float gsm = upstream<V>(tmp[i], e[i], s, gconst);
+            pre[i] = 0.0f + gsm / s;
+            tmp[i] = ((-e[i]) / s2) * gsm;
+        }
+        gS = 0.0f + wave_row_reduce<VEC, NE>(tmp, lane, K, 0.0f, OpAdd{});
+    } else {
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+            const float glsm = upstream<V>(tmp[i], e[i], s, gconst);
+            pre[i] = 0.0f + glsm;
+            tmp[i] = glsm;
+        }
+        gS = 0.0f + (0.0f + (-wave_row_reduce<VEC, NE>(tmp, lane, K, 0.0f, OpAdd{}))) / s;
+    }
+    const float rgs = 1.0f * gS;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        if constexpr (from_softmax<V>()) pre[i] = 0.0f + e[i] * (pre[i] + rgs);
+        else pre[i] = pre[i] + e[i] * (0.0f + rgs);
+    }
+    const float sg = (1.0f / (float)cntm) * (0.0f + (-wave_row_reduce<VEC, NE>(pre, lane, K, 0.0f, OpAdd{})));
+    load_row<VEC, NE>(tmp, g + base, lane, K, al);
+#pragma unroll
+    for (int i = 0; i < NE; ++i) tmp[i] = (tmp[i] + pre[i]) + (xv[i] == mb ? sg : 0.0f);
+    store_row<VEC, NE>(g + base, tmp, lane, K, al);
+}
+
+// ---------------------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------------------
+static inline bool al16s(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+static int check_rows(const char* what, int64_t rows, int64_t classes) {
     if (rows < 0 || classes < 0) return fail(MH_ERR_INVALID, "%s: negative size", what);
-    if (classes > kSMaxClasses)
-        return fail(MH_ERR_INVALID, "%s: %lld classes; the fused kernels take rows of at most %d (use the op-by-op path)",
-                    what, (long long)classes, kSMaxClasses);
-    if (rows > 0 && classes > 0 && (!x || !tg)) return fail(MH_ERR_NULL, "%s: null tensor", what);
+    if (classes > kSWaveMax)
+        return fail(MH_ERR_INVALID, "%s: %lld classes; the fused row kernels take rows of at most %d (use the op-by-op path)",
+                    what, (long long)classes, kSWaveMax);
     if ((double)rows * (double)classes > 9.0e15) return fail(MH_ERR_OVERFLOW, "%s: size overflow", what);
     return MH_OK;
 }
 
-static inline bool al16s(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+template <int V>
+static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows, int K, float* part,
+                      int64_t* nblocks_out) {
+    hipStream_t st = ctx().stream;
+    constexpr bool LOSS = V == G_SMLM || V == G_CE;
+    const bool al = al16s(x) && (!LOSS || al16s(tg)) && (LOSS || al16s(out));
+    if (K <= kSThreadMax) {
+        const int rb = rows_per_block(LOSS ? 2 : 1, K);
+        const int64_t nb = (rows + rb - 1) / rb;
+        if (nb > 0x7fffffff) return fail(MH_ERR_OVERFLOW, "too many rows");
+        *nblocks_out = nb;
+        const size_t lds = (LOSS ? 2 : 1) * (size_t)rb * (size_t)K * sizeof(float);
+        dim3 g((unsigned)nb), b(kSThreads);
+#define MH_RT(KM) hipLaunchKernelGGL((k_rowt_fwd<V, KM>), g, b, lds, st, x, tg, out, rows, K, rb, al, part)
+        if (K <= 8) MH_RT(8);
+        else if (K <= 16) MH_RT(16);
+        else if (K <= 32) MH_RT(32);
+        else MH_RT(64);
+#undef MH_RT
+        return MH_OK;
+    }
+    const int64_t nb = (rows + 3) / 4;
+    if (nb > 0x7fffffff) return fail(MH_ERR_OVERFLOW, "too many rows");
+    *nblocks_out = nb;
+    dim3 g((unsigned)nb), b(kSThreads);
+#define MH_RW(VEC, NE) hipLaunchKernelGGL((k_roww_fwd<V, VEC, NE>), g, b, 0, st, x, tg, out, rows, K, al, part)
+    if (K % 4 == 0) {
+        if (K <= 1024) MH_RW(true, 16);
+        else MH_RW(true, kSLaneElems);
+    } else {
+        if (K <= 1024) MH_RW(false, 16);
+        else MH_RW(false, kSLaneElems);
+    }
+#undef MH_RW
+    return MH_OK;
+}
+
+template <int V>
+static int launch_bwd(float* gx, const float* x, const float* up, const float* ug, int64_t rows, int K, float c) {
+    hipStream_t st = ctx().stream;
+    const bool al = al16s(x) && al16s(up) && al16s(gx);
+    if (K <= kSThreadMax) {
+        const int rb = rows_per_block(3, K);
+        const int64_t nb = (rows + rb - 1) / rb;
+        if (nb > 0x7fffffff) return fail(MH_ERR_OVERFLOW, "too many rows");
+        const size_t lds = 3 * (size_t)rb * (size_t)K * sizeof(float);
+        dim3 g((unsigned)nb), b(kSThreads);
+#define MH_RT(KM) hipLaunchKernelGGL((k_rowt_bwd<V, KM>), g, b, lds, st, gx, x, up, ug, rows, K, rb, al, c)
+        if (K <= 8) MH_RT(8);
+        else if (K <= 16) MH_RT(16);
+        else if (K <= 32) MH_RT(32);
+        else MH_RT(64);
+#undef MH_RT
+        return MH_OK;
+    }
+    const int64_t nb = (rows + 3) / 4;
+    if (nb > 0x7fffffff) return fail(MH_ERR_OVERFLOW, "too many rows");
+    dim3 g((unsigned)nb), b(kSThreads);
+#define MH_RW(VEC, NE) hipLaunchKernelGGL((k_roww_bwd<V, VEC, NE>), g, b, 0, st, gx, x, up, ug, rows, K, al, c)
+    if (K % 4 == 0) {
+        if (K <= 1024) MH_RW(true, 16);
+        else MH_RW(true, kSLaneElems);
+    } else {
+        if (K <= 1024) MH_RW(false, 16);
+        else MH_RW(false, kSLaneElems);
+    }
+#undef MH_RW
+    return MH_OK;
+}
+
+// Loss graphs: block partials, then the all-element sum with the graph's epilogue.
+template <int V>
+static int loss_fwd(const char* what, float* loss, const float* x, const float* tg, int64_t rows, int64_t K) {
+    MH_TRY(check_rows(what, rows, K));
+    if (!loss) return fail(MH_ERR_NULL, "%s: null loss", what);
+    if (rows * K > 0 && (!x || !tg)) return fail(MH_ERR_NULL, "%s: null tensor", what);
+    MH_TRY(require_init());
+    const int64_t n = rows * K;
+    if (n == 0) {  // MEAN of nothing: 0 / 0; the cross-entropy sum of nothing: 0 * f32(-1/rows)
+        const float v = V == G_SMLM ? __builtin_nanf("") : 0.0f * (float)(-1.0 / (double)rows);
+        MH_TRY(mh_fill(loss, v, 1));
+        return finish(what);
+    }
+    const int64_t nb_max = K <= kSThreadMax ? (rows + 31) / 32 : (rows + 3) / 4;
+    const size_t np = ((size_t)nb_max + 63) & ~(size_t)63;
+    const size_t t = reduce_abc_tmp_floats(RED_SUM, 1, nb_max, 1);
+    float* part = nullptr;
+    MH_TRY(scratch((np + t + 64) * sizeof(float), reinterpret_cast<void**>(&part)));
+    int64_t nb = 0;
+    MH_TRY(launch_fwd<V>(x, tg, nullptr, rows, (int)K, part, &nb));
+    if (V == G_SMLM)  // MEAN.forward: the sum of every element / f32(N)
+        MH_TRY(reduce_abc(RED_SUM, EPI_MEAN, part, 1, nb, 1, loss, nullptr, (float)n, part + np));
+    else  // SUM.forward, then MUL(., f32(-1 / f64(rows))) (loss.mojo:58-59)
+        MH_TRY(reduce_abc(RED_SUM, EPI_SCALE, part, 1, nb, 1, loss, nullptr, (float)(-1.0 / (double)rows),
+                          part + np));
+    return finish(what);
+}
+
+template <int V>
+static int loss_bwd(const char* what, float* gx, const float* x, const float* tg, const float* ug, int64_t rows,
+                    int64_t K) {
+    MH_TRY(check_rows(what, rows, K));
+    const int64_t n = rows * K;
+    if (n == 0) return MH_OK;
+    if (!gx || !x || !tg || !ug) return fail(MH_ERR_NULL, "%s: null tensor", what);
+    MH_TRY(require_init());
+    const float c = V == G_SMLM ? (float)(1.0 / (double)n)      // MEAN.backward, basics.mojo:470-487
+                                : (float)(-1.0 / (double)rows);  // the scale of loss.mojo:59
+    MH_TRY(launch_bwd<V>(gx, x, tg, ug, rows, (int)K, c));
+    return finish(what);
+}
+
+template <int V>
+static int map_fwd(const char* what, float* out, const float* x, int64_t rows, int64_t K) {
+    MH_TRY(check_rows(what, rows, K));
+    if (rows * K == 0) return MH_OK;
+    if (!out || !x) return fail(MH_ERR_NULL, "%s: null tensor", what);
+    MH_TRY(require_init());
+    int64_t nb = 0;
+    MH_TRY(launch_fwd<V>(x, nullptr, out, rows, (int)K, nullptr, &nb));
+    return finish(what);
+}
+
+template <int V>
+static int map_bwd(const char* what, float* gx, const float* x, const float* gout, int64_t rows, int64_t K) {
+    MH_TRY(check_rows(what, rows, K));
+    if (rows * K == 0) return MH_OK;
+    if (!gx || !x || !gout) return fail(MH_ERR_NULL, "%s: null tensor", what);
+    MH_TRY(require_init());
+    MH_TRY(launch_bwd<V>(gx, x, gout, nullptr, rows, (int)K, 0.0f));
+    return finish(what);
+}
 
 }  // namespace mh
 
@@ -234,52 +664,37 @@ using namespace mh;
 extern "C" {
 
 int mh_softmax_log_mul_mean_fwd(float* loss, const float* x, const float* target, int64_t rows, int64_t classes) {
-    MH_TRY(check_smlm("mh_softmax_log_mul_mean_fwd", x, target, rows, classes));
-    if (!loss) return fail(MH_ERR_NULL, "mh_softmax_log_mul_mean_fwd: null loss");
-    MH_TRY(require_init());
-    const int64_t n = rows * classes;
-    if (n == 0) return mh_fill(loss, __builtin_nanf(""), 1);  // the mean of no elements: 0 / 0
-    const int rb = rows_per_block(2, classes);
-    const int64_t nblocks = (rows + rb - 1) / rb;
-    if (nblocks > 0x7fffffff) return fail(MH_ERR_OVERFLOW, "mh_softmax_log_mul_mean_fwd: too many rows");
-    const size_t np = ((size_t)nblocks + 63) & ~(size_t)63;
-    const size_t t = reduce_abc_tmp_floats(RED_SUM, 1, nblocks, 1);
-    float* part = nullptr;
-    MH_TRY(scratch((np + t + 64) * sizeof(float), reinterpret_cast<void**>(&part)));
-    const bool al = al16s(x) && al16s(target);
-    const size_t lds = 2 * (size_t)rb * (size_t)classes * sizeof(float);
-    dim3 g((unsigned)nblocks), b(kSThreads);
-    hipStream_t st = ctx().stream;
-    if (classes <= 8) hipLaunchKernelGGL(k_smlm_fwd<8>, g, b, lds, st, x, target, rows, (int)classes, rb, al, part);
-    else if (classes <= 16) hipLaunchKernelGGL(k_smlm_fwd<16>, g, b, lds, st, x, target, rows, (int)classes, rb, al, part);
-    else hipLaunchKernelGGL(k_smlm_fwd<32>, g, b, lds, st, x, target, rows, (int)classes, rb, al, part);
-    // MEAN.forward: the sum of every element divided by f32(N)
-    MH_TRY(reduce_abc(RED_SUM, EPI_MEAN, part, 1, nblocks, 1, loss, nullptr, (float)n, part + np));
-    return finish("mh_softmax_log_mul_mean_fwd");
+    return loss_fwd<G_SMLM>("mh_softmax_log_mul_mean_fwd", loss, x, target, rows, classes);
 }
 
 int mh_softmax_log_mul_mean_bwd_accum(float* grad_x, const float* x, const float* target, const float* ug,
                                       int64_t rows, int64_t classes) {
-    MH_TRY(check_smlm("mh_softmax_log_mul_mean_bwd_accum", x, target, rows, classes));
-    const int64_t n = rows * classes;
-    if (n == 0) return MH_OK;
-    if (!grad_x || !ug) return fail(MH_ERR_NULL, "mh_softmax_log_mul_mean_bwd_accum: null tensor");
-    MH_TRY(require_init());
-    const int rb = rows_per_block(3, classes);
-    const int64_t nblocks = (rows + rb - 1) / rb;
-    if (nblocks > 0x7fffffff) return fail(MH_ERR_OVERFLOW, "mh_softmax_log_mul_mean_bwd_accum: too many rows");
-    const bool al = al16s(x) && al16s(target) && al16s(grad_x);
-    const size_t lds = 3 * (size_t)rb * (size_t)classes * sizeof(float);
-    const float cmean = (float)(1.0 / (double)n);  // MEAN.backward, basics.mojo:470-487
-    dim3 g((unsigned)nblocks), b(kSThreads);
-    hipStream_t st = ctx().stream;
-    if (classes <= 8)
-        hipLaunchKernelGGL(k_smlm_bwd<8>, g, b, lds, st, grad_x, x, target, ug, rows, (int)classes, rb, al, cmean);
-    else if (classes <= 16)
-        hipLaunchKernelGGL(k_smlm_bwd<16>, g, b, lds, st, grad_x, x, target, ug, rows, (int)classes, rb, al, cmean);
-    else
-        hipLaunchKernelGGL(k_smlm_bwd<32>, g, b, lds, st, grad_x, x, target, ug, rows, (int)classes, rb, al, cmean);
-    return finish("mh_softmax_log_mul_mean_bwd_accum");
+    return loss_bwd<G_SMLM>("mh_softmax_log_mul_mean_bwd_accum", grad_x, x, target, ug, rows, classes);
+}
+
+int mh_cross_entropy_fwd(float* loss, const float* x, const float* target, int64_t rows, int64_t classes) {
+    return loss_fwd<G_CE>("mh_cross_entropy_fwd", loss, x, target, rows, classes);
+}
+
+int mh_cross_entropy_bwd_accum(float* grad_x, const float* x, const float* target, const float* ug, int64_t rows,
+                               int64_t classes) {
+    return loss_bwd<G_CE>("mh_cross_entropy_bwd_accum", grad_x, x, target, ug, rows, classes);
+}
+
+int mh_softmax_fwd(float* out, const float* x, int64_t rows, int64_t classes) {
+    return map_fwd<G_SOFTMAX>("mh_softmax_fwd", out, x, rows, classes);
+}
+
+int mh_softmax_bwd_accum(float* grad_x, const float* x, const float* grad_out, int64_t rows, int64_t classes) {
+    return map_bwd<G_SOFTMAX>("mh_softmax_bwd_accum", grad_x, x, grad_out, rows, classes);
+}
+
+int mh_logsoftmax_fwd(float* out, const float* x, int64_t rows, int64_t classes) {
+    return map_fwd<G_LOGSOFTMAX>("mh_logsoftmax_fwd", out, x, rows, classes);
+}
+
+int mh_logsoftmax_bwd_accum(float* grad_x, const float* x, const float* grad_out, int64_t rows, int64_t classes) {
+    return map_bwd<G_LOGSOFTMAX>("mh_logsoftmax_bwd_accum", grad_x, x, grad_out, rows, classes);
 }
 
 }  // extern "C"

@@ -413,3 +413,44 @@ def softmax_log_mul_mean_backward(grad_x: Tensor, x: Tensor, target: Tensor, ug:
     if target.shape() != x.shape() or grad_x.shape() != x.shape() or ug.num_elements() != 1:
         raise _lib.MantleHipError(_lib.ERR_SHAPE, "grad_x and target must match x; ug holds one element")
     _lib.call("mh_softmax_log_mul_mean_bwd_accum", grad_x.ptr, x.ptr, target.ptr, ug.ptr, rows, classes)
+
+
+def _rows_classes(t: Tensor):
+    k = t.shape()[t.rank() - 1] if t.rank() else 1
+    return (t.num_elements() // k if k else 0), k
+
+
+def softmax_forward(out: Tensor, x: Tensor) -> None:
+    """Softmax over the last axis (activations.mojo:74-87), one fused pass."""
+    r, k = _rows_classes(x)
+    _lib.call("mh_softmax_fwd", out.ptr, x.ptr, r, k)
+
+
+def softmax_backward(grad_x: Tensor, x: Tensor, grad_out: Tensor) -> None:
+    """grad_x += the five Softmax backward nodes' contribution from grad_out."""
+    r, k = _rows_classes(x)
+    _lib.call("mh_softmax_bwd_accum", grad_x.ptr, x.ptr, grad_out.ptr, r, k)
+
+
+def logsoftmax_forward(out: Tensor, x: Tensor) -> None:
+    """LogSoftmax over the last axis (activations.mojo:94-108), one fused pass."""
+    r, k = _rows_classes(x)
+    _lib.call("mh_logsoftmax_fwd", out.ptr, x.ptr, r, k)
+
+
+def logsoftmax_backward(grad_x: Tensor, x: Tensor, grad_out: Tensor) -> None:
+    r, k = _rows_classes(x)
+    _lib.call("mh_logsoftmax_bwd_accum", grad_x.ptr, x.ptr, grad_out.ptr, r, k)
+
+
+def cross_entropy_forward(loss: Tensor, x: Tensor, target: Tensor) -> None:
+    """CrossEntropyLoss (loss.mojo:45-61) of x [rows, classes] against target, one fused pass."""
+    if x.shape() != target.shape():
+        raise _lib.MantleHipError(_lib.ERR_SHAPE, "x and target differ in shape")
+    r, k = _rows_classes(x)
+    _lib.call("mh_cross_entropy_fwd", loss.ptr, x.ptr, target.ptr, r, k)
+
+
+def cross_entropy_backward(grad_x: Tensor, x: Tensor, target: Tensor, ug: Tensor) -> None:
+    r, k = _rows_classes(x)
+    _lib.call("mh_cross_entropy_bwd_accum", grad_x.ptr, x.ptr, target.ptr, ug.ptr, r, k)

@@ -409,7 +409,8 @@ def test_config5_classifier_chain_small(gpu):
         assert_ulp(gg[k], go[k], 2, f"grad {k}")
 
 
-SMLM_CASES = [(4099, 10), (1, 1), (3, 2), (257, 3), (1000, 16), (513, 17), (300, 32), (64, 1), (7, 5), (2048, 10)]
+SMLM_CASES = [(4099, 10), (1, 1), (3, 2), (257, 3), (1000, 16), (513, 17), (300, 32), (64, 1), (7, 5), (2048, 10),
+              (40, 33), (20, 64), (9, 65), (8, 128), (5, 130), (3, 1000), (2, 2047)]
 
 
 @pytest.mark.parametrize("rows,classes", SMLM_CASES, ids=[f"{r}x{c}" for r, c in SMLM_CASES])
@@ -456,11 +457,74 @@ def test_fused_softmax_log_mul_mean(gpu, rows, classes, ugv):
     assert_bitexact(tz.to_numpy(), gr["logits"], "fused grad from zero")
 
 
-def test_fused_softmax_rejects_wide_rows(gpu):
+def test_fused_row_graphs_reject_wide_rows(gpu):
     m = gpu.m
-    x = gpu.T(np.zeros((4, 33), np.float32))
+    x = gpu.T(np.zeros((2, 2048), np.float32))
     with pytest.raises(m.MantleHipError):
         m.softmax_log_mul_mean_forward(m.Tensor(m.TensorShape(1)), x, x)
+    with pytest.raises(m.MantleHipError):
+        m.cross_entropy_forward(m.Tensor(m.TensorShape(1)), x, x)
+    with pytest.raises(m.MantleHipError):
+        m.softmax_forward(m.Tensor(m.TensorShape(2, 2048)), x)
+
+
+# Row lengths around every engine boundary: 1-64 one thread per row (element-order sums),
+# 65-2047 one wavefront per row (the row-reduction kernel's order; multiples of 4 and not).
+ROW_CASES = [(300, 1), (7, 2), (257, 3), (100, 10), (33, 31), (65, 32), (40, 33), (17, 63), (16, 64), (9, 65),
+             (11, 66), (8, 100), (6, 128), (5, 130), (4, 257), (3, 1000), (2, 1024), (3, 1025), (2, 2044),
+             (2, 2047), (1000, 10)]
+
+
+@pytest.mark.parametrize("rows,classes", ROW_CASES, ids=[f"{r}x{c}" for r, c in ROW_CASES])
+def test_fused_row_graphs(gpu, rows, classes):
+    """Softmax, LogSoftmax and CrossEntropyLoss fused (one kernel each way) against the
+    op-by-op graphs on the GPU: outputs and gradients bit-identical, accumulated into a
+    non-zero grad_x; the cross-entropy loss in the sum class."""
+    from util import cross_entropy_nodes, logsoftmax_nodes, softmax_nodes
+    m = gpu.m
+    x = synth.normal((rows, classes), 0, 2, 1300)
+    if classes > 1:
+        synth.inject_ties(x, 1, 1301)
+    g0 = synth.normal((rows, classes), 0, 1, 1302)
+    gout = synth.normal((rows, classes), 0, 1, 1303)
+    tx = gpu.T(x)
+    for name, nodes, out_name, fwd, bwd in [
+            ("softmax", softmax_nodes("x", 1), "sm", m.softmax_forward, m.softmax_backward),
+            ("logsoftmax", logsoftmax_nodes("x", 1), "lsm", m.logsoftmax_forward, m.logsoftmax_backward)]:
+        g = Graph(nodes, ["x"])
+        v = g.forward(gpu, {"x": x})
+        out = m.Tensor(m.TensorShape(rows, classes))
+        fwd(out, tx)
+        assert_bitexact(out.to_numpy(), v[out_name], f"{name} forward")
+        gr = g.backward(gpu, v, seed=gout, init={"x": g0})
+        tg = gpu.T(g0)
+        bwd(tg, tx, gpu.T(gout))
+        assert_bitexact(tg.to_numpy(), gr["x"], f"{name} backward")
+    # cross entropy with soft targets and a non-unit loss gradient
+    target = synth.uniform((rows, classes), 0, 1, 1304)
+    cn = np.array([np.float32(-1.0 / rows)], np.float32)
+    g = Graph(cross_entropy_nodes("x", "target"), ["x"])
+    v = g.forward(gpu, {"x": x, "target": target, "cN": cn})
+    loss = m.Tensor(m.TensorShape(1))
+    m.cross_entropy_forward(loss, tx, gpu.T(target))
+    tl64 = v["tl"].astype(np.float64)
+    assert_sum_close(loss.to_numpy(), v["loss"], np.array([tl64.sum() * float(cn[0])]), "cross-entropy loss",
+                     terms_abs=np.array([np.abs(tl64).sum() * abs(float(cn[0]))]))
+    seed = np.array([0.7], np.float32)
+    gr = g.backward(gpu, v, seed=seed, init={"x": g0})
+    tg = gpu.T(g0)
+    m.cross_entropy_backward(tg, tx, gpu.T(target), gpu.T(seed))
+    assert_bitexact(tg.to_numpy(), gr["x"], "cross-entropy backward")
+
+
+def test_fused_cross_entropy_matches_reference_fixtures(gpu):
+    """test_loss.mojo:86-171: 0.76794958 and 1.31794953 (its 'almost6' tolerance)."""
+    m = gpu.m
+    x = np.array([[0.1, 0.2, 0.7], [0.7, 0.2, 0.1]], np.float32)
+    for t, exp in [([[0, 0, 1], [1, 0, 0]], 0.76794958), ([[0, 1, 0], [0, 0, 1]], 1.31794953)]:
+        loss = m.Tensor(m.TensorShape(1))
+        m.cross_entropy_forward(loss, gpu.T(x), gpu.T(np.array(t, np.float32)))
+        np.testing.assert_allclose(loss.to_numpy()[0], exp, rtol=1e-5, atol=1e-8)
 
 
 # ---------------------------------------------------------------------------------------

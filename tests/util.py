@@ -218,10 +218,13 @@ class Graph:
             vals[out] = eng.forward(op, t1, t2, ax)
         return vals
 
-    def backward(self, eng, vals, seed=None):
+    def backward(self, eng, vals, seed=None, init=None):
         """Model.backward (model.mojo:173-330): seed the last node's grad (1.0 for a loss, else
-        `seed`), then reverse node order, operands gated on trainable."""
+        `seed`), then reverse node order, operands gated on trainable. `init` gives starting
+        values of chosen grads (zero otherwise)."""
         grads = {k: np.zeros(np.asarray(v).shape, np.float32) for k, v in vals.items() if k in self.trainable}
+        for k, v in (init or {}).items():
+            grads[k] = np.asarray(v, np.float32).copy()
         last = self.nodes[-1][3]
         grads[last] = np.ones(np.asarray(vals[last]).shape, np.float32) if seed is None else \
             np.asarray(seed, np.float32).copy()
@@ -262,6 +265,15 @@ def softmax_nodes(x, axis, prefix=""):
     return [(OPS["MAX"], [x], axis, p + "max"), (OPS["SUB"], [x, p + "max"], None, p + "xm"),
             (OPS["EXP"], [p + "xm"], None, p + "e"), (OPS["SUM"], [p + "e"], axis, p + "s"),
             (OPS["DIV"], [p + "e", p + "s"], None, p + "sm")]
+
+
+def cross_entropy_nodes(x, target, prefix=""):
+    """CrossEntropyLoss graph, mantle/nn/loss.mojo:45-61: LogSoftmax(axis 1), MUL(target, .),
+    SUM, MUL(., cN) with cN the graph scalar f32(-1 / rows)."""
+    p = prefix
+    return logsoftmax_nodes(x, 1, p) + [(OPS["MUL"], [target, p + "lsm"], None, p + "tl"),
+                                        (OPS["SUM"], [p + "tl"], None, p + "ret"),
+                                        (OPS["MUL"], [p + "ret", p + "cN"], None, p + "loss")]
 
 
 def config5_nodes():
