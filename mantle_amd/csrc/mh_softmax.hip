@@ -42,6 +42,7 @@
 //              SUB(x, max): grad_x += g_xm;  g_max = 0 + (-sum(g_xm))
 //              MAX: grad_x += (x == max ? fl(1 / count) * g_max : 0)
 #include <cfloat>
+#include <unordered_map>
 
 #include "mh_internal.h"
 #include "mh_math.h"
@@ -284,6 +285,289 @@ __global__ void __launch_bounds__(kSThreads)
 }
 
 // ---------------------------------------------------------------------------------------
+// in-kernel end of a loss's all-element sum (grids of at most 64 * 32 blocks)
+// ---------------------------------------------------------------------------------------
+// Block b publishes its partial with an agent-scope store, waits for it to complete, and
+// takes a ticket on the counter of its group of 32 blocks; the group's last arrival sums the
+// group's partials (lane i loads partial i, an xor butterfly adds them), publishes the group
+// sum the same way and takes a ticket on the top counter, whose last arrival sums the group
+// sums and writes the loss (MEAN: / f32(N); cross entropy: * f32(-1 / rows)). Every sum runs
+// in an order fixed by block indices alone, so the loss does not depend on which block ends
+// last, and every counter is back at zero when the kernel ends. Counters sit one per 128-byte
+// line; called by the 64 lanes of the block's first wavefront.
+constexpr int kTailGroup = 32;
+constexpr int64_t kTailStride = 32;
+constexpr int64_t kTailMaxBlocks = 64 * kTailGroup;
+
+template <int V>
+__device__ __forceinline__ void loss_tail(float tot, float* part, uint32_t* tickets, float* loss, float lscale) {
+    const int lane = threadIdx.x & 63;
+    const int b = blockIdx.x, nparts = gridDim.x;
+    const int grp = b / kTailGroup, g0 = grp * kTailGroup;
+    const int members = (nparts - g0) < kTailGroup ? (nparts - g0) : kTailGroup;
+    const int ngroups = (nparts + kTailGroup - 1) / kTailGroup;
+    uint32_t tk = 0;
+    if (lane == 0) {
+        __hip_atomic_store(&part[b], tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        tk = __hip_atomic_fetch_add(&tickets[(1 + grp) * kTailStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    tk = __shfl(tk, 0);
+    if (tk != (uint32_t)(members - 1)) return;  // uniform across the wavefront
+    float v = lane < members ? __hip_atomic_load(&part[g0 + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+#pragma unroll
+    for (int mm = 32; mm >= 1; mm >>= 1) v = v + __shfl_xor(v, mm);
+    if (lane == 0) {
+        __hip_atomic_store(&tickets[(1 + grp) * kTailStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&part[nparts + grp], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        tk = __hip_atomic_fetch_add(&tickets[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    tk = __shfl(tk, 0);
+    if (tk != (uint32_t)(ngroups - 1)) return;
+    float w = lane < ngroups ? __hip_atomic_load(&part[nparts + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                             : 0.0f;
+#pragma unroll
+    for (int mm = 32; mm >= 1; mm >>= 1) w = w + __shfl_xor(w, mm);
+    if (lane == 0) {
+        __hip_atomic_store(&tickets[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        loss[0] = V == G_SMLM ? w / lscale : w * lscale;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// pipelined thread engine: rows of at most 16 classes, 16-byte aligned operands
+// ---------------------------------------------------------------------------------------
+// A persistent grid walks 256-row tiles; while a block computes tile i from LDS, the loads of
+// its next tile are already in flight into registers, so the chip never alternates between
+// a whole-grid load phase and a whole-grid compute phase. A tile is at most 4096 floats (four
+// float4 per thread per operand); rows are computed exactly as in k_rowt_fwd / k_rowt_bwd.
+constexpr int kPQ = 4;  // float4 per thread per operand tile (q0..q3 below)
+
+// Four float4 of one operand tile per thread, as named registers (an array here ends up in
+// scratch memory).
+typedef float vf4 __attribute__((ext_vector_type(4)));
+struct TileRegs {
+    vf4 q0, q1, q2, q3;
+    float tail;
+};
+
+// Loads tile floats [0, cnt) at src + base into registers: quad i of the tile goes to thread
+// i % 256, slot i / 256; the cnt % 4 tail floats to threads 0..2.
+__device__ __forceinline__ void tile_load(TileRegs& r, const float* __restrict__ src, int64_t base, int cnt) {
+    const int t = threadIdx.x;
+    const int nq = cnt >> 2;
+    const vf4* s4 = reinterpret_cast<const vf4*>(src + base);
+    if (t < nq) r.q0 = s4[t];
+    if (t + kSThreads < nq) r.q1 = s4[t + kSThreads];
+    if (t + 2 * kSThreads < nq) r.q2 = s4[t + 2 * kSThreads];
+    if (t + 3 * kSThreads < nq) r.q3 = s4[t + 3 * kSThreads];
+    const int tl = (nq << 2) + t;
+    if (t < 4 && tl < cnt) r.tail = src[base + tl];
+}
+
+__device__ __forceinline__ void tile_to_lds(float* dst, const TileRegs& r, int cnt) {
+    const int t = threadIdx.x;
+    const int nq = cnt >> 2;
+    vf4* d4 = reinterpret_cast<vf4*>(dst);
+    if (t < nq) d4[t] = r.q0;
+    if (t + kSThreads < nq) d4[t + kSThreads] = r.q1;
+    if (t + 2 * kSThreads < nq) d4[t + 2 * kSThreads] = r.q2;
+    if (t + 3 * kSThreads < nq) d4[t + 3 * kSThreads] = r.q3;
+    const int tl = (nq << 2) + t;
+    if (t < 4 && tl < cnt) dst[tl] = r.tail;
+}
+
+template <int V, int KM>
+__global__ void __launch_bounds__(kSThreads)
+    k_rowp_fwd(const float* __restrict__ x, const float* __restrict__ tg, float* __restrict__ out, int64_t rows,
+               int K, float* __restrict__ part, uint32_t* tickets, float* loss, float lscale) {
+    __shared__ float4 xs4[kPQ * kSThreads], ts4[kPQ * kSThreads];
+    __shared__ float ws[4];
+    constexpr bool LOSS = V == G_SMLM || V == G_CE;
+    float* xs = reinterpret_cast<float*>(xs4);
+    float* ts = reinterpret_cast<float*>(ts4);
+    const int64_t ntiles = (rows + kSThreads - 1) / kSThreads;
+    const int t = threadIdx.x;
+    TileRegs rx{}, rt{};
+    float rowsum = 0.0f;
+    int64_t tile = blockIdx.x;
+    if (tile < ntiles) {
+        const int64_t r0 = tile * kSThreads;
+        const int cnt = (int)(((rows - r0) < kSThreads ? (rows - r0) : kSThreads) * K);
+        tile_load(rx, x, r0 * K, cnt);
+        if (LOSS) tile_load(rt, tg, r0 * K, cnt);
+    }
+    for (; tile < ntiles; tile += gridDim.x) {
+        const int64_t r0 = tile * kSThreads;
+        const int nr = (int)((rows - r0) < kSThreads ? (rows - r0) : kSThreads);
+        const int cnt = nr * K;
+        tile_to_lds(xs, rx, cnt);
+        if (LOSS) tile_to_lds(ts, rt, cnt);
+        __syncthreads();
+        const int64_t nxt = tile + gridDim.x;  // the next tile's loads overlap this tile's work
+        if (nxt < ntiles) {
+            const int64_t n0 = nxt * kSThreads;
+            const int ncnt = (int)(((rows - n0) < kSThreads ? (rows - n0) : kSThreads) * K);
+            tile_load(rx, x, n0 * K, ncnt);
+            if (LOSS) tile_load(rt, tg, n0 * K, ncnt);
+        }
+        if (t < nr) {
+            float xr[KM], e[KM];
+#pragma unroll
+            for (int j = 0; j < KM; ++j) xr[j] = j < K ? xs[t * K + j] : 0.0f;
+            float m = -FLT_MAX;
+#pragma unroll
+            for (int j = 0; j < KM; ++j)
+                if (j < K) m = max_simd(m, xr[j]);
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KM; ++j) {
+                if (j < K) {
+                    e[j] = mexp(xr[j] - m);
+                    s = s + e[j];
+                }
+            }
+            const float ls = (V == G_CE || V == G_LOGSOFTMAX) ? mlog(s) : 0.0f;
+#pragma unroll
+            for (int j = 0; j < KM; ++j) {
+                if (j < K) {
+                    if constexpr (V == G_SMLM) rowsum = rowsum + mlog(e[j] / s) * ts[t * K + j];
+                    else if constexpr (V == G_CE) rowsum = rowsum + ts[t * K + j] * ((xr[j] - m) - ls);
+                    else if constexpr (V == G_SOFTMAX) xs[t * K + j] = e[j] / s;
+                    else xs[t * K + j] = (xr[j] - m) - ls;
+                }
+            }
+        }
+        __syncthreads();
+        if (!LOSS) {
+            unstage_tile(out, xs, r0 * K, cnt, true);
+            __syncthreads();
+        }
+    }
+    if constexpr (LOSS) {
+        const float tot = block_sum(rowsum, ws);
+        if (tickets == nullptr) {  // the host reduces the partials
+            if (t == 0) part[blockIdx.x] = tot;
+        } else if (t < 64) {
+            loss_tail<V>(tot, part, tickets, loss, lscale);
+        }
+    }
+}
+
+template <int V, int KM>
+__global__ void __launch_bounds__(kSThreads)
+    k_rowp_bwd(float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ up,
+               const float* __restrict__ ug, int64_t rows, int K, float c) {
+    __shared__ float4 xs4[kPQ * kSThreads], us4[kPQ * kSThreads], gs4[kPQ * kSThreads];
+    float* xs = reinterpret_cast<float*>(xs4);
+    float* us = reinterpret_cast<float*>(us4);
+    float* gs = reinterpret_cast<float*>(gs4);
+    const int64_t ntiles = (rows + kSThreads - 1) / kSThreads;
+    const int t = threadIdx.x;
+    const float gconst = V == G_SMLM ? 0.0f + c * ug[0] : V == G_CE ? 0.0f + 1.0f * (0.0f + ug[0] * c) : 0.0f;
+    TileRegs rx{}, ru{}, rg{};
+    int64_t tile = blockIdx.x;
+    if (tile < ntiles) {
+        const int64_t r0 = tile * kSThreads;
+        const int cnt = (int)(((rows - r0) < kSThreads ? (rows - r0) : kSThreads) * K);
+        tile_load(rx, x, r0 * K, cnt);
+        tile_load(ru, up, r0 * K, cnt);
+        tile_load(rg, g, r0 * K, cnt);
+    }
+    for (; tile < ntiles; tile += gridDim.x) {
+        const int64_t r0 = tile * kSThreads;
+        const int nr = (int)((rows - r0) < kSThreads ? (rows - r0) : kSThreads);
+        const int cnt = nr * K;
+        tile_to_lds(xs, rx, cnt);
+        tile_to_lds(us, ru, cnt);
+        tile_to_lds(gs, rg, cnt);
+        __syncthreads();
+        const int64_t nxt = tile + gridDim.x;
+        if (nxt < ntiles) {
+            const int64_t n0 = nxt * kSThreads;
+            const int ncnt = (int)(((rows - n0) < kSThreads ? (rows - n0) : kSThreads) * K);
+            tile_load(rx, x, n0 * K, ncnt);
+            tile_load(ru, up, n0 * K, ncnt);
+            tile_load(rg, g, n0 * K, ncnt);
+        }
+        if (t < nr) {
+            float xr[KM], e[KM], pre[KM];
+#pragma unroll
+            for (int j = 0; j < KM; ++j) xr[j] = j < K ? xs[t * K + j] : 0.0f;
+            float m = -FLT_MAX, mb = -FLT_MAX;
+            uint32_t cntm = 0;
+#pragma unroll
+            for (int j = 0; j < KM; ++j) {
+                if (j < K) {
+                    const float v = xr[j];
+                    m = max_simd(m, v);
+                    if (mb > v) {
+                    } else if (v > mb) {
+                        mb = v;
+                        cntm = 1;
+                    } else {
+                        cntm += 1;
+                    }
+                }
+            }
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KM; ++j) {
+                if (j < K) {
+                    e[j] = mexp(xr[j] - m);
+                    s = s + e[j];
+                }
+            }
+            float acc = 0.0f, gS;
+            if constexpr (from_softmax<V>()) {
+                const float s2 = s * s;
+#pragma unroll
+                for (int j = 0; j < KM; ++j) {
+                    if (j < K) {
+                        const float gsm = upstream<V>(us[t * K + j], e[j], s, gconst);
+                        pre[j] = 0.0f + gsm / s;
+                        acc = acc + ((-e[j]) / s2) * gsm;
+                    }
+                }
+                gS = 0.0f + acc;
+            } else {
+#pragma unroll
+                for (int j = 0; j < KM; ++j) {
+                    if (j < K) {
+                        const float glsm = upstream<V>(us[t * K + j], e[j], s, gconst);
+                        pre[j] = 0.0f + glsm;
+                        acc = acc + glsm;
+                    }
+                }
+                gS = 0.0f + (0.0f + (-acc)) / s;
+            }
+            const float rgs = K == 1 ? (1.0f * gS) * gS : 1.0f * gS;
+            float acc2 = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KM; ++j) {
+                if (j < K) {
+                    if constexpr (from_softmax<V>()) pre[j] = 0.0f + e[j] * (pre[j] + rgs);
+                    else pre[j] = pre[j] + e[j] * (0.0f + rgs);
+                    acc2 = acc2 + pre[j];
+                }
+            }
+            const float sg = (1.0f / (float)cntm) * (0.0f + (-acc2));
+#pragma unroll
+            for (int j = 0; j < KM; ++j) {
+                if (j < K) {
+                    const float a = gs[t * K + j] + pre[j];
+                    gs[t * K + j] = a + (xr[j] == mb ? sg : 0.0f);
+                }
+            }
+        }
+        __syncthreads();
+        unstage_tile(g, gs, r0 * K, cnt, true);
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 // wavefront engine: 64 < classes <= 2047, one wavefront per row, k_rows_wave's order
 // ---------------------------------------------------------------------------------------
 // Lane slot i holds element 4 (lane + 64 (i / 4)) + i % 4 (VEC: classes % 4 == 0, quads
@@ -515,6 +799,19 @@ __global__ void __launch_bounds__(kSThreads)
 // ---------------------------------------------------------------------------------------
 static inline bool al16s(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// Blocks of a persistent kernel: as many as can be resident at once (queried once per
+// kernel), so no block waits for another to finish.
+static int64_t pipe_grid(const void* kernel) {
+    static std::unordered_map<const void*, int> resident;
+    auto it = resident.find(kernel);
+    if (it == resident.end()) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kSThreads, 0) != hipSuccess || n < 1) n = 1;
+        it = resident.emplace(kernel, n).first;
+    }
+    return (int64_t)it->second * ctx().num_cus;
+}
+
 static int check_rows(const char* what, int64_t rows, int64_t classes) {
     if (rows < 0 || classes < 0) return fail(MH_ERR_INVALID, "%s: negative size", what);
     if (classes > kSWaveMax)
@@ -524,12 +821,31 @@ static int check_rows(const char* what, int64_t rows, int64_t classes) {
     return MH_OK;
 }
 
+// Loss graphs on the pipelined path finish the sum in the kernel when `loss` is given (and
+// set *done); otherwise they leave block partials in `part`.
 template <int V>
 static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows, int K, float* part,
-                      int64_t* nblocks_out) {
+                      int64_t* nblocks_out, float* loss = nullptr, float lscale = 0.0f, bool* done = nullptr) {
     hipStream_t st = ctx().stream;
     constexpr bool LOSS = V == G_SMLM || V == G_CE;
     const bool al = al16s(x) && (!LOSS || al16s(tg)) && (LOSS || al16s(out));
+    if (K <= 16 && al) {  // persistent, pipelined
+        const void* kern = K <= 8 ? reinterpret_cast<const void*>(&k_rowp_fwd<V, 8>)
+                                  : reinterpret_cast<const void*>(&k_rowp_fwd<V, 16>);
+        const int64_t ntiles = (rows + kSThreads - 1) / kSThreads;
+        const int64_t pg = pipe_grid(kern);
+        const int64_t nb = ntiles < pg ? ntiles : pg;
+        *nblocks_out = nb;
+        uint32_t* tk = nullptr;
+        if (LOSS && loss && nb <= kTailMaxBlocks) {
+            MH_TRY(tickets((1 + nb / kTailGroup + 1) * kTailStride, &tk));
+            if (done) *done = true;
+        }
+        dim3 g((unsigned)nb), b(kSThreads);
+        if (K <= 8) hipLaunchKernelGGL((k_rowp_fwd<V, 8>), g, b, 0, st, x, tg, out, rows, K, part, tk, loss, lscale);
+        else hipLaunchKernelGGL((k_rowp_fwd<V, 16>), g, b, 0, st, x, tg, out, rows, K, part, tk, loss, lscale);
+        return MH_OK;
+    }
     if (K <= kSThreadMax) {
         const int rb = rows_per_block(LOSS ? 2 : 1, K);
         const int64_t nb = (rows + rb - 1) / rb;
@@ -565,6 +881,17 @@ template <int V>
 static int launch_bwd(float* gx, const float* x, const float* up, const float* ug, int64_t rows, int K, float c) {
     hipStream_t st = ctx().stream;
     const bool al = al16s(x) && al16s(up) && al16s(gx);
+    if (K <= 16 && al) {  // persistent, pipelined
+        const void* kern = K <= 8 ? reinterpret_cast<const void*>(&k_rowp_bwd<V, 8>)
+                                  : reinterpret_cast<const void*>(&k_rowp_bwd<V, 16>);
+        const int64_t ntiles = (rows + kSThreads - 1) / kSThreads;
+        const int64_t pg = pipe_grid(kern);
+        const int64_t nb = ntiles < pg ? ntiles : pg;
+        dim3 g((unsigned)nb), b(kSThreads);
+        if (K <= 8) hipLaunchKernelGGL((k_rowp_bwd<V, 8>), g, b, 0, st, gx, x, up, ug, rows, K, c);
+        else hipLaunchKernelGGL((k_rowp_bwd<V, 16>), g, b, 0, st, gx, x, up, ug, rows, K, c);
+        return MH_OK;
+    }
     if (K <= kSThreadMax) {
         const int rb = rows_per_block(3, K);
         const int64_t nb = (rows + rb - 1) / rb;
@@ -607,13 +934,16 @@ static int loss_fwd(const char* what, float* loss, const float* x, const float* 
         MH_TRY(mh_fill(loss, v, 1));
         return finish(what);
     }
-    const int64_t nb_max = K <= kSThreadMax ? (rows + 31) / 32 : (rows + 3) / 4;
+    const int64_t nb_max = K <= kSThreadMax ? (rows + 31) / 32 : (rows + 3) / 4;  // >= any grid used
     const size_t np = ((size_t)nb_max + 63) & ~(size_t)63;
     const size_t t = reduce_abc_tmp_floats(RED_SUM, 1, nb_max, 1);
     float* part = nullptr;
     MH_TRY(scratch((np + t + 64) * sizeof(float), reinterpret_cast<void**>(&part)));
     int64_t nb = 0;
-    MH_TRY(launch_fwd<V>(x, tg, nullptr, rows, (int)K, part, &nb));
+    bool done = false;
+    const float lscale = V == G_SMLM ? (float)n : (float)(-1.0 / (double)rows);
+    MH_TRY(launch_fwd<V>(x, tg, nullptr, rows, (int)K, part, &nb, loss, lscale, &done));
+    if (done) return finish(what);
     if (V == G_SMLM)  // MEAN.forward: the sum of every element / f32(N)
         MH_TRY(reduce_abc(RED_SUM, EPI_MEAN, part, 1, nb, 1, loss, nullptr, (float)n, part + np));
     else  // SUM.forward, then MUL(., f32(-1 / f64(rows))) (loss.mojo:58-59)
