@@ -776,6 +776,9 @@ int mh_binary_bwd_accum(int op, int tensor_id, float* grad, const mh_shape* psgr
         MH_TRY(unbroadcast_accum_scratch(grad, sgrad, ug, sug, op == MH_SUB && tensor_id == 1, tmp));
         return finish("mh_binary_bwd_accum");
     }
+    bool done = false;  // rg summed as it is computed, when the shapes allow it
+    MH_TRY(unbroadcast_binrg(op, tensor_id, divs, grad, sgrad, ug, sug, t1, s1, t2, s2, &done));
+    if (done) return finish("mh_binary_bwd_accum");
     const size_t n = (size_t)numel(sug);
     const size_t rg_floats = (n + 63) & ~(size_t)63;
     float* base = nullptr;

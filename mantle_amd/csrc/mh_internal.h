@@ -192,6 +192,12 @@ size_t unbroadcast_scratch_floats(const mh_shape& sgrad, const mh_shape& srg);
 int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* rg,
                               const mh_shape& srg, bool negate, float* tmp);
 int plan_unbroadcast(const mh_shape& sgrad, const mh_shape& srg, mh_reduce_plan_info* info);
+// grad += un-broadcast(rg) of a broadcast MUL / DIV backward with rg computed inside the
+// reduction (single-step plans whose per-element operand has the full shape); *done says
+// whether it ran.
+int unbroadcast_binrg(int op, int id, bool divs, float* grad, const mh_shape& sgrad, const float* ug,
+                      const mh_shape& sug, const float* t1, const mh_shape& s1, const float* t2,
+                      const mh_shape& s2, bool* done);
 
 // Elementwise helpers used by the reduction and fused entry points.
 int map_max_route(float* grad, const mh_shape& sx, const float* x, const mh_shape& sline,

@@ -145,6 +145,69 @@ struct LdSqDev {
     }
 };
 
+// The rg of a broadcast MUL / DIV backward, computed inside the un-broadcast reduction
+// instead of being materialised (the expressions of FBinRg: MUL ug * other; DIV operand 0
+// ug / t2; operand 1 ((-t1) / (t2 * t2)) * ug, or (f * t1) * ug with f = -1 / (s * s) for
+// a scalar t2). `a` is the full-shape operand; `t2` of DIV's operand 1 has the grad's shape
+// and is read at the element's output line (i / (B*C)) * C + i % C. get4 takes a quad in
+// one row (C == 1) or over four consecutive lines (C % 4 == 0), with 16-byte loads when
+// `al`, else four scalar loads, so the reduction runs in the same order either way.
+template <int OP, int ID, bool DIVS, bool BIG>
+struct LdBinRg {
+    const float* ug;
+    const float* a;
+    const float* t2;
+    int64_t BC, C;
+    FastDiv fbc, fc;
+    bool al;
+    float f;
+    __device__ void setup() {
+        if constexpr (DIVS) {
+            const float t = t2[0];
+            f = -1.0f / (t * t);
+        }
+    }
+    __device__ int64_t line(int64_t i) const {
+        if constexpr (BIG) {
+            return (i / BC) * C + i % C;
+        } else {
+            const uint32_t u = (uint32_t)i;
+            const uint32_t c = u - fdiv(u, fc) * (uint32_t)C;
+            return (int64_t)fdiv(u, fbc) * C + c;
+        }
+    }
+    __device__ float term(float u, float av, float d) const {
+        if constexpr (OP == MH_MUL) return u * av;
+        else if constexpr (ID == 0) return u / av;
+        else if constexpr (DIVS) return (f * av) * u;
+        else return ((-av) / (d * d)) * u;
+    }
+    __device__ float get(int64_t i) const {
+        const float d = (OP == MH_DIV && ID == 1 && !DIVS) ? t2[line(i)] : 0.0f;
+        return term(ug[i], a[i], d);
+    }
+    __device__ void get4(int64_t i, float* o) const {
+        float4 u, v;
+        if (al) {
+            u = *reinterpret_cast<const float4*>(ug + i);
+            v = *reinterpret_cast<const float4*>(a + i);
+        } else {
+            u = make_float4(ug[i], ug[i + 1], ug[i + 2], ug[i + 3]);
+            v = make_float4(a[i], a[i + 1], a[i + 2], a[i + 3]);
+        }
+        float4 d = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if constexpr (OP == MH_DIV && ID == 1 && !DIVS) {
+            const int64_t l = line(i);
+            if (C == 1) d = make_float4(t2[l], t2[l], t2[l], t2[l]);
+            else d = make_float4(t2[l], t2[l + 1], t2[l + 2], t2[l + 3]);
+        }
+        o[0] = term(u.x, v.x, d.x);
+        o[1] = term(u.y, v.y, d.y);
+        o[2] = term(u.z, v.z, d.z);
+        o[3] = term(u.w, v.w, d.w);
+    }
+};
+
 // ---------------------------------------------------------------------------------------
 // epilogues
 // ---------------------------------------------------------------------------------------
@@ -225,6 +288,30 @@ __global__ void __launch_bounds__(kRThreads)
         typename R::T acc = R::init();
         for (int j = 0; j < B; ++j) acc = R::comb(acc, R::lift(tile[t * B + j]));
         epi_store(out, out2, (int64_t)blockIdx.x * kRThreads + t, acc, epi, div);
+    }
+}
+
+// Short rows (C == 1, B <= BMAX) through any loader: the block's threads compute the values
+// of rows [r0, r0 + 256) at consecutive element indices (coalesced, ld.get handles any
+// position), stage them in LDS, then thread t reduces row r0 + t in element order -- the
+// order of k_rows_lds and k_rows_thread.
+template <class R, class LD, int BMAX>
+__global__ void __launch_bounds__(kRThreads)
+    k_rows_lds_ld(LD ld, int64_t nrows, int B, float* out, float* out2, int epi, float div) {
+    using T = typename R::T;
+    __shared__ T tile[kRThreads * BMAX];
+    ld.setup();
+    const int64_t r0 = (int64_t)blockIdx.x * kRThreads;
+    const int64_t rows = (nrows - r0) < kRThreads ? (nrows - r0) : kRThreads;
+    const int64_t base = r0 * B;
+    const int cnt = (int)(rows * B);
+    for (int i = threadIdx.x; i < cnt; i += kRThreads) tile[i] = ld.get(base + i);
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < rows) {
+        T acc = R::init();
+        for (int j = 0; j < B; ++j) acc = R::comb(acc, tile[t * B + j]);
+        epi_store(out, out2, r0 + t, acc, epi, div);
     }
 }
 
@@ -765,6 +852,20 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
                     return MH_OK;
                 }
             }
+            constexpr int kMaxLds = sizeof(typename R::T) == 4 ? 64 : 32;  // tile of at most 64 KB
+            if (B <= kMaxLds && A <= ((int64_t)1 << 40)) {  // any loader: LDS-staged, element order
+                const unsigned blocks = (unsigned)((A + kRThreads - 1) / kRThreads);
+                if (B <= 16)
+                    hipLaunchKernelGGL((k_rows_lds_ld<R, LD, 16>), dim3(blocks), dim3(kRThreads), 0, st, ld, A,
+                                       (int)B, out, out2, epi, div);
+                else if (B <= 32)
+                    hipLaunchKernelGGL((k_rows_lds_ld<R, LD, 32>), dim3(blocks), dim3(kRThreads), 0, st, ld, A,
+                                       (int)B, out, out2, epi, div);
+                else if constexpr (kMaxLds == 64)
+                    hipLaunchKernelGGL((k_rows_lds_ld<R, LD, 64>), dim3(blocks), dim3(kRThreads), 0, st, ld, A,
+                                       (int)B, out, out2, epi, div);
+                return MH_OK;
+            }
             int64_t blocks = (A + kRThreads - 1) / kRThreads;
             if (blocks > 65536) blocks = 65536;
             hipLaunchKernelGGL((k_rows_thread<R, LD>), dim3((unsigned)blocks), dim3(kRThreads), 0, st, ld, A,
@@ -948,6 +1049,67 @@ int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* r
                           0.0f, part));
         src = dst;
     }
+    return MH_OK;
+}
+
+template <int OP, int ID, bool DIVS, bool BIG>
+static int binrg_reduce(float* grad, const float* ug, const float* a, const float* t2, int64_t A, int64_t B,
+                        int64_t C, bool al, float* tmp) {
+    LdBinRg<OP, ID, DIVS, BIG> ld{};
+    ld.ug = ug;
+    ld.a = a;
+    ld.t2 = t2;
+    ld.BC = B * C;
+    ld.C = C;
+    if (!BIG) {
+        ld.fbc = make_fastdiv((uint32_t)(B * C > 0 ? B * C : 1));
+        ld.fc = make_fastdiv((uint32_t)C);
+    }
+    ld.al = al;
+    // vec_ok: the loader reads quads at any alignment, so the kernels (and the summation
+    // order) are those of a materialised, aligned rg
+    return reduce_t<RSum, LdBinRg<OP, ID, DIVS, BIG>>(ld, true, EPI_ACCUM, A, B, C, grad, nullptr, 0.0f, tmp);
+}
+
+template <int OP, int ID, bool DIVS>
+static int binrg_reduce_n(float* grad, const float* ug, const float* a, const float* t2, int64_t A, int64_t B,
+                          int64_t C, bool al, float* tmp) {
+    if (A * B * C < ((int64_t)1 << 32)) return binrg_reduce<OP, ID, DIVS, false>(grad, ug, a, t2, A, B, C, al, tmp);
+    return binrg_reduce<OP, ID, DIVS, true>(grad, ug, a, t2, A, B, C, al, tmp);
+}
+
+int unbroadcast_binrg(int op, int id, bool divs, float* grad, const mh_shape& sgrad, const float* ug,
+                      const mh_shape& sug, const float* t1, const mh_shape& s1, const float* t2,
+                      const mh_shape& s2, bool* done) {
+    *done = false;
+    if (op != MH_MUL && op != MH_DIV) return MH_OK;
+    // the operand read at every element must have the full shape
+    const float* a = id == 0 ? t2 : t1;
+    if (!shape_eq(id == 0 ? s2 : s1, sug)) return MH_OK;
+    mh_reduce_plan_info p;
+    MH_TRY(plan_unbroadcast(sgrad, sug, &p));
+    if (p.nsteps > 1) return MH_OK;
+    int64_t A = numel(sug), B = 1, C = 1;  // only size-1 dims differ: element for element
+    if (p.nsteps == 1) {
+        A = p.a[0];
+        B = p.b[0];
+        C = p.c[0];
+    }
+    float* tmp = nullptr;
+    const size_t t = tmp_floats_t<RSum>(A, B, C, true);
+    if (t) MH_TRY(scratch((t + 64) * sizeof(float), reinterpret_cast<void**>(&tmp)));
+    const bool al = al16(ug) && al16(a);
+    if (op == MH_MUL) {
+        if (id == 0) MH_TRY((binrg_reduce_n<MH_MUL, 0, false>(grad, ug, a, t2, A, B, C, al, tmp)));
+        else MH_TRY((binrg_reduce_n<MH_MUL, 1, false>(grad, ug, a, t2, A, B, C, al, tmp)));
+    } else if (id == 0) {
+        MH_TRY((binrg_reduce_n<MH_DIV, 0, false>(grad, ug, a, t2, A, B, C, al, tmp)));
+    } else if (divs) {
+        MH_TRY((binrg_reduce_n<MH_DIV, 1, true>(grad, ug, a, t2, A, B, C, al, tmp)));
+    } else {
+        MH_TRY((binrg_reduce_n<MH_DIV, 1, false>(grad, ug, a, t2, A, B, C, al, tmp)));
+    }
+    *done = true;
     return MH_OK;
 }
 
