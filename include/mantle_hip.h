@@ -310,6 +310,13 @@ int mh_model_tensor(mh_model* m, int32_t sym, float** dptr);
 int mh_model_grad(mh_model* m, int32_t sym, float** dptr);
 /* parameters.grads.set_zero (collection.mojo:221-224): one fill over the gradient arena. */
 int mh_model_zero_grad(mh_model* m);
+/* The trainable parameters (graph params with trainable set, get_trainable_parameters,
+ * optim.mojo:27-44) occupy the start of the tensor arena, and their gradients the start of
+ * the gradient arena, in the same order and slot sizes: two parallel spans of n floats
+ * (padding between slots is zero in both). mh_adam_step over the two spans updates every
+ * parameter in one launch; padding stays zero. NULL spans and n = 0 without trainable
+ * parameters. */
+int mh_model_param_span(mh_model* m, float** params, float** grads, int64_t* n);
 int mh_model_info(const mh_model* m, int32_t* n_inference_nodes, int64_t* tensor_bytes, int64_t* grad_bytes,
                   int32_t* fused_pairs);
 

@@ -143,6 +143,7 @@ SIGNATURES = {
     "mh_model_tensor": [_VP, ctypes.c_int32, ctypes.POINTER(_VP)],
     "mh_model_grad": [_VP, ctypes.c_int32, ctypes.POINTER(_VP)],
     "mh_model_zero_grad": [_VP],
+    "mh_model_param_span": [_VP, ctypes.POINTER(_VP), ctypes.POINTER(_VP), ctypes.POINTER(_I64)],
     "mh_model_info": [_VP, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_int32)],
     "mh_plan_binary": [_S, _S, _S, ctypes.POINTER(mh_plan_info)],
     "mh_plan_unbroadcast": [_S, _S, ctypes.POINTER(mh_reduce_plan_info)],

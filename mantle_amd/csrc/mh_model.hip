@@ -48,6 +48,7 @@ struct mh_model {
     std::vector<float*> t;  // per symbol: its tensor slot
     std::vector<float*> gr;  // per symbol: its gradient slot (nullptr if not trainable)
     int32_t n_inference = -1;
+    size_t param_span = 0;  // floats of the trainable-parameter span at the start of both arenas
     std::vector<int> fuse;  // per node: 1 = ADD fused with the next node (RELU), 2 = that RELU
 };
 
@@ -390,13 +391,22 @@ int mh_model_create(const mh_graph* g, uint64_t flags, mh_model** out) {
     m->flags = flags;
     const size_t ns = g->syms.size();
     std::vector<size_t> toff(ns), goff(ns, (size_t)-1);
-    for (size_t s = 0; s < ns; ++s) {  // allocate_tensor_memory / allocate_grad_memory
-        toff[s] = m->arena_floats;
-        m->arena_floats += slot_floats(g->syms[s].shape);
-        if (g->syms[s].trainable) {
-            goff[s] = m->grad_floats;
-            m->grad_floats += slot_floats(g->syms[s].shape);
+    // allocate_tensor_memory / allocate_grad_memory. The trainable parameters come first in
+    // both arenas, in the same order with the same slot sizes, so that parameters and their
+    // gradients form two parallel spans an optimizer updates in one launch; then every other
+    // symbol in creation order.
+    auto is_tparam = [&](size_t s) { return g->syms[s].kind == MH_SYM_PARAM && g->syms[s].trainable; };
+    for (int pass = 0; pass < 2; ++pass) {
+        for (size_t s = 0; s < ns; ++s) {
+            if (is_tparam(s) != (pass == 0)) continue;
+            toff[s] = m->arena_floats;
+            m->arena_floats += slot_floats(g->syms[s].shape);
+            if (g->syms[s].trainable) {
+                goff[s] = m->grad_floats;
+                m->grad_floats += slot_floats(g->syms[s].shape);
+            }
         }
+        if (pass == 0) m->param_span = m->arena_floats;
     }
     int rc = MH_OK;
     if (m->arena_floats) rc = mh_malloc(reinterpret_cast<void**>(&m->arena), m->arena_floats * sizeof(float));
@@ -509,6 +519,14 @@ int mh_model_zero_grad(mh_model* m) {
     if (!m) return fail(MH_ERR_NULL, "mh_model_zero_grad: null model");
     if (!m->grad_arena) return MH_OK;
     return mh_zero(m->grad_arena, (int64_t)m->grad_floats);
+}
+
+int mh_model_param_span(mh_model* m, float** params, float** grads, int64_t* n) {
+    if (!m || !params || !grads || !n) return fail(MH_ERR_NULL, "mh_model_param_span: null argument");
+    *params = m->param_span ? m->arena : nullptr;
+    *grads = m->param_span ? m->grad_arena : nullptr;
+    *n = (int64_t)m->param_span;
+    return MH_OK;
 }
 
 int mh_model_info(const mh_model* m, int32_t* n_inference_nodes, int64_t* tensor_bytes, int64_t* grad_bytes,

@@ -68,6 +68,14 @@ class Parameters:
         self.tensors = Collection(model, grads=False)
         self.grads = Collection(model, grads=True)
         self.graph = model.graph
+        self._m = model
+
+    def param_span(self):
+        """(params, grads, n): the device spans holding every trainable parameter and its
+        gradient, in the same layout; None without trainable parameters."""
+        p, g, n = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_int64()
+        _lib.call("mh_model_param_span", self._m._h, ctypes.byref(p), ctypes.byref(g), ctypes.byref(n))
+        return (p.value, g.value, n.value) if n.value else None
 
 
 class Model:

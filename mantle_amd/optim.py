@@ -22,8 +22,12 @@ class Adam:
         """``params``: a model's ``Parameters`` (its graph's trainable parameters, as
         ``Adam[g](model.parameters, ...)`` takes them), or (param, grad) Tensor pairs."""
         self._collection = None
+        self._span = None  # (params, grads, n) of a model's contiguous trainable span
         if hasattr(params, "tensors") and hasattr(params, "grads") and hasattr(params, "graph"):
             self._collection = params
+            span = params.param_span()
+            if span is not None:
+                self._span = span
             params = [(params.tensors[s], params.grads[s]) for s in params.graph.trainable_parameters()]
         self.params: List[Tuple[Tensor, Tensor]] = list(params)
         for p, g in self.params:
@@ -31,9 +35,19 @@ class Adam:
                 raise _lib.MantleHipError(_lib.ERR_SHAPE, "a parameter and its gradient differ in shape")
         self.lr, self.beta1, self.beta2, self.epsilon = float(lr), float(beta1), float(beta2), float(epsilon)
         self.iter = 0
-        # allocate_rms_and_momentum (optim.mojo:142-149): zero-initialised, one per parameter
-        self.momentum_grads = [Tensor(p.shape()) for p, _ in self.params]
-        self.rms_grads = [Tensor(p.shape()) for p, _ in self.params]
+        # allocate_rms_and_momentum (optim.mojo:142-149): zero-initialised, one per parameter;
+        # over a model's span, two span-sized buffers whose slices are the per-parameter tensors
+        if self._span is not None:
+            _, _, n = self._span
+            self._m_span, self._v_span = Tensor(n), Tensor(n)
+            offs = [p.ptr - self._span[0] for p, _ in self.params]
+            self.momentum_grads = [Tensor(p.shape(), _ptr=self._m_span.ptr + o, _owner=self._m_span)
+                                   for (p, _), o in zip(self.params, offs)]
+            self.rms_grads = [Tensor(p.shape(), _ptr=self._v_span.ptr + o, _owner=self._v_span)
+                              for (p, _), o in zip(self.params, offs)]
+        else:
+            self.momentum_grads = [Tensor(p.shape()) for p, _ in self.params]
+            self.rms_grads = [Tensor(p.shape()) for p, _ in self.params]
 
     def zero_grad(self) -> None:
         """Adam.zero_grad (optim.mojo:90-92): parameters.grads.set_zero()."""
@@ -45,6 +59,11 @@ class Adam:
 
     def step(self) -> None:
         self.iter += 1
+        if self._span is not None:  # every parameter of the model in one launch
+            p, g, n = self._span
+            _lib.call("mh_adam_step", p, g, self._m_span.ptr, self._v_span.ptr, n, self.lr, self.beta1, self.beta2,
+                      self.epsilon, self.iter)
+            return
         n = len(self.params)
         if n == 0:
             return

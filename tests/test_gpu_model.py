@@ -262,3 +262,52 @@ def test_model_training_with_adam(gpu):
         assert_bitexact(model.parameters.tensors[sw].to_numpy(), tw.to_numpy(), f"w step {it}")
         assert_bitexact(model.parameters.tensors[sb].to_numpy(), tb.to_numpy(), f"b step {it}")
     assert opt.iter == 3
+
+
+def test_model_param_span_layout_and_single_launch_adam(gpu):
+    """Trainable parameters sit first in the tensor arena and their grads first in the grad
+    arena, at the same offsets; Adam over the span matches Adam per tensor, and the padding
+    between slots stays zero."""
+    m = gpu.m
+    g = m.Graph()
+    x = g.input((6, 7))
+    shapes = [(3, 7), (1, 7), (2, 3, 7)]
+    ps = [g.param(s, init=synth.normal(s, 0, 1, 1270 + i)) for i, s in enumerate(shapes)]
+    frozen = g.param((1, 7), init=np.ones(7, np.float32), trainable=False)
+    a = g.op(m.OP.MUL, x, ps[1])
+    b = g.op(m.OP.ADD, a, frozen)
+    c = g.op(m.OP.MEAN, g.op(m.OP.MUL, b, b))
+    d = g.op(m.OP.SUM, g.op(m.OP.MUL, ps[0], ps[0]))
+    e = g.op(m.OP.MEAN, g.op(m.OP.TANH, ps[2]))
+    loss = g.op(m.OP.ADD, g.op(m.OP.ADD, c, d), e)
+    g.loss(loss)
+    model = m.Model(g)
+    span_p, span_g, n = model.parameters.param_span()
+    P = model.parameters
+    offs = []
+    for s in ps:
+        tp, tg = P.tensors[s].ptr, P.grads[s].ptr
+        assert span_p <= tp < span_p + 4 * n and tg - span_g == tp - span_p
+        offs.append((tp - span_p) // 4)
+    assert not (span_p <= P.tensors[frozen].ptr < span_p + 4 * n)
+    opt = m.Adam(model.parameters, lr=0.05)
+    # the same updates through per-tensor Adam on copies
+    cp = [m.Tensor.from_numpy(P.tensors[s].to_numpy()) for s in ps]
+    cg = [m.Tensor(m.TensorShape(*s.shape.dims)) for s in ps]
+    ref = m.Adam(list(zip(cp, cg)), lr=0.05)
+    xv = synth.normal((6, 7), 0, 1, 1280)
+    for it in range(3):
+        opt.zero_grad()
+        model.forward(xv)
+        model.backward()
+        for s, t in zip(ps, cg):
+            m._lib.call("mh_memcpy_d2d", t.ptr, P.grads[s].ptr, s.shape.num_elements() * 4)
+        opt.step()
+        ref.step()
+        for s, t in zip(ps, cp):
+            assert_bitexact(P.tensors[s].to_numpy(), t.to_numpy(), f"param {s} step {it}")
+    whole = m.Tensor(m.TensorShape(n), _ptr=span_p, _owner=model).to_numpy()
+    used = np.zeros(n, bool)
+    for s, o in zip(ps, offs):
+        used[o:o + s.shape.num_elements()] = True
+    assert not whole[~used].any(), "padding between parameter slots changed"
