@@ -23,6 +23,8 @@ The other configs are measured after the headline step and reported under "workl
         [8192, 8192] (axis 0, axis 1, all);
   rows  row-fused CrossEntropyLoss ([2^20, 10], [32768, 1000]), Softmax and LogSoftmax
         ([32768, 1000]), forward and backward;
+  graph a training step (zero_grad, forward, backward) through the native Model, eager against
+        HIP-graph replay, for config 1's graph (with a MEAN loss) and config 5's chain;
   copy  a plain 1 GiB device copy (the library's copy kernel): the practical streaming rate.
 Tensors smaller than the 256 MB Infinity Cache are timed with the cache flushed before each
 op (a 1 GiB read sweep between ops, outside the timed events).
@@ -548,6 +550,74 @@ def run_rows(L, reps):
     return op_report(ops, med)
 
 
+def run_graph(L, reps, steps=200):
+    """One training step (zero_grad, forward, backward) of a model through the native executor,
+    eager against HIP-graph replay: config 1's ADD(bias) -> RELU graph with a MEAN loss (the
+    launch-bound case) and config 5's head chain. Wall time per step on the host (inputs copied
+    from device buffers into their slots every step), one synchronisation per `steps` steps."""
+    import time
+    import mantle_amd as mm
+    from mantle_amd import synth
+    out = {}
+
+    def c1():
+        g = mm.Graph()
+        x = g.input((32, 32), trainable=True)
+        b = g.param((1, 32), init=synth.normal((1, 32), 0, 0.1, 51))
+        g.loss(g.op(mm.OP.MEAN, g.op(mm.OP.RELU, g.op(mm.OP.ADD, x, b))))
+        return g, [synth.normal((32, 32), 0, 1, 52)]
+
+    def c5():
+        rows = 1 << 20
+        g = mm.Graph()
+        lg, oh = g.input((rows, 10), trainable=True), g.input((rows, 10))
+        mx = g.op(mm.OP.MAX, lg, attributes={"axis": 1})
+        e = g.op(mm.OP.EXP, g.op(mm.OP.SUB, lg, mx))
+        sm = g.op(mm.OP.DIV, e, g.op(mm.OP.SUM, e, attributes={"axis": 1}))
+        g.loss(g.op(mm.OP.MEAN, g.op(mm.OP.MUL, g.op(mm.OP.LOG, sm), oh)))
+        onehot = np.zeros((rows, 10), np.float32)
+        onehot[np.arange(rows), synth.integers((rows,), 0, 10, 54)] = 1
+        return g, [synth.normal((rows, 10), 0, 2, 53), onehot]
+
+    for name, make, n in (("c1", c1, steps), ("c5", c5, max(steps // 10, 10))):
+        g, inputs = make()
+        res = {}
+        for mode in ("eager", "graph"):
+            model = mm.Model(g)
+            srcs = [mm.Tensor.from_numpy(v) for v in inputs]  # the step's inputs, already on the device
+            tab = (ctypes.c_void_p * len(srcs))(*[t.ptr for t in srcs])
+            slots = [(model.parameters.tensors[sym].ptr, t.ptr, t.num_elements() * 4) for sym, t in zip(g.inputs, srcs)]
+            h = model._h
+            if mode == "graph":
+                for dst, src, nb in slots:
+                    chk(L, L.mh_memcpy_d2d(dst, src, nb), "copy")
+                model.capture("forward")
+                model.capture("backward")
+
+                def step():  # inputs into their slots, then the two graphs
+                    chk(L, L.mh_model_zero_grad(h), "zero_grad")
+                    for dst, src, nb in slots:
+                        chk(L, L.mh_memcpy_d2d(dst, src, nb), "copy")
+                    chk(L, L.mh_model_replay(h, 0), "replay fwd")
+                    chk(L, L.mh_model_replay(h, 1), "replay bwd")
+            else:
+                def step():  # Model.forward copies the inputs in, then every node; Model.backward
+                    chk(L, L.mh_model_zero_grad(h), "zero_grad")
+                    chk(L, L.mh_model_forward(h, len(srcs), tab, 1), "fwd")
+                    chk(L, L.mh_model_backward(h, 0, None, 0), "bwd")
+            for _ in range(3):
+                step()
+            chk(L, L.mh_sync(), "sync")
+            t0 = time.perf_counter()
+            for _ in range(n):
+                step()
+            chk(L, L.mh_sync(), "sync")
+            res[mode] = round((time.perf_counter() - t0) / n * 1e6, 2)
+            del model, srcs
+        out[name] = {"us_per_step": res, "speedup": round(res["eager"] / res["graph"], 2)}
+    return out
+
+
 def run_copy(L, reps):
     d = Dev(L)
     n = 1 << 28
@@ -732,9 +802,9 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--log2n", type=int, default=28)
-    ap.add_argument("--workloads", default="c3,c4,c5,adam,adj,rows,copy",
-                    help="extra workloads after the headline step (comma list of c3,c4,c5,adam,adj,rows,copy; "
-                         "'none')")
+    ap.add_argument("--workloads", default="c3,c4,c5,adam,adj,rows,graph,copy",
+                    help="extra workloads after the headline step (comma list of c3,c4,c5,adam,adj,rows,graph,"
+                         "copy; 'none')")
     ap.add_argument("--reps", type=int, default=10, help="repetitions per op of the extra workloads")
     ap.add_argument("--cpu-log2n", type=int, default=24)
     ap.add_argument("--cpu-reps", type=int, default=2)
@@ -801,6 +871,7 @@ def main():
     runners = {"c3": lambda: run_c3(L, args.reps), "c4": lambda: run_c4(L, args.reps),
                "c5": lambda: run_c5(L, args.reps), "adam": lambda: run_adam(L, args.reps),
                "adj": lambda: run_adj(L, args.reps), "rows": lambda: run_rows(L, args.reps),
+               "graph": lambda: run_graph(L, args.reps),
                "copy": lambda: run_copy(L, args.reps)}
     if wl:
         out["workloads"] = {}

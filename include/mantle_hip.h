@@ -310,6 +310,17 @@ int mh_model_tensor(mh_model* m, int32_t sym, float** dptr);
 int mh_model_grad(mh_model* m, int32_t sym, float** dptr);
 /* parameters.grads.set_zero (collection.mojo:221-224): one fill over the gradient arena. */
 int mh_model_zero_grad(mh_model* m);
+/* HIP-graph form of the two passes: mh_model_capture runs the pass once (library buffers
+ * reach their sizes), then records its launches on the library stream into a graph;
+ * mh_model_replay launches the graph. MH_PASS_FORWARD is every node (inputs are not part of
+ * it: write them into their slots first, through mh_model_tensor); MH_PASS_BACKWARD seeds
+ * the loss gradient with 1.0 and runs every node in reverse. The graph holds kernel launches
+ * only (no memset or host-copy nodes). Capturing again replaces the graph. */
+#define MH_PASS_FORWARD 0
+#define MH_PASS_BACKWARD 1
+int mh_model_capture(mh_model* m, int pass);
+int mh_model_replay(mh_model* m, int pass);
+
 /* The trainable parameters (graph params with trainable set, get_trainable_parameters,
  * optim.mojo:27-44) occupy the start of the tensor arena, and their gradients the start of
  * the gradient arena, in the same order and slot sizes: two parallel spans of n floats

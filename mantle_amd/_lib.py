@@ -51,6 +51,7 @@ ATTR_AXIS, ATTR_NEGATIVE_SLOPE, ATTR_MIN, ATTR_MAX = 1, 2, 4, 8
 SYM_INPUT, SYM_PARAM, SYM_NODE = 0, 1, 2
 FROM_HOST, FROM_DEVICE = 0, 1
 MODEL_FUSE_BIAS_RELU = 1
+PASS_FORWARD, PASS_BACKWARD = 0, 1
 
 
 class MantleHipError(RuntimeError):
@@ -143,6 +144,8 @@ SIGNATURES = {
     "mh_model_tensor": [_VP, ctypes.c_int32, ctypes.POINTER(_VP)],
     "mh_model_grad": [_VP, ctypes.c_int32, ctypes.POINTER(_VP)],
     "mh_model_zero_grad": [_VP],
+    "mh_model_capture": [_VP, _I],
+    "mh_model_replay": [_VP, _I],
     "mh_model_param_span": [_VP, ctypes.POINTER(_VP), ctypes.POINTER(_VP), ctypes.POINTER(_I64)],
     "mh_model_info": [_VP, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_int32)],
     "mh_plan_binary": [_S, _S, _S, ctypes.POINTER(mh_plan_info)],

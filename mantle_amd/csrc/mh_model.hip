@@ -49,7 +49,8 @@ struct mh_model {
     std::vector<float*> gr;  // per symbol: its gradient slot (nullptr if not trainable)
     int32_t n_inference = -1;
     size_t param_span = 0;  // floats of the trainable-parameter span at the start of both arenas
-    std::vector<int> fuse;  // per node: 1 = ADD fused with the next node (RELU), 2 = that RELU
+    std::vector<int> fuse;
+    hipGraphExec_t graph[2] = {nullptr, nullptr};  // captured passes (MH_PASS_FORWARD / _BACKWARD)  // per node: 1 = ADD fused with the next node (RELU), 2 = that RELU
 };
 
 namespace mh {
@@ -262,6 +263,34 @@ static int write_inputs(mh_model* m, int32_t ninputs, const float* const* inputs
     return MH_OK;
 }
 
+// The ops of one pass, enqueued on the library stream (no synchronisation): forward = every
+// node; backward = the loss gradient seeded with 1.0, then every node in reverse.
+static int check_pass(const mh_model* m, int pass) {
+    if (pass == MH_PASS_FORWARD) return MH_OK;
+    if (pass != MH_PASS_BACKWARD) return fail(MH_ERR_INVALID, "unknown pass %d", pass);
+    if (m->g.loss < 0) return fail(MH_ERR_INVALID, "backward pass: the graph has no loss symbol");
+    if (!m->gr[m->g.loss]) return fail(MH_ERR_INVALID, "backward pass: the loss is not trainable");
+    return MH_OK;
+}
+
+static int enqueue_pass(mh_model* m, int pass) {
+    const mh_graph& g = m->g;
+    if (pass == MH_PASS_FORWARD) {
+        for (size_t i = 0; i < g.nodes.size(); ++i) MH_TRY(run_forward_node(m, i));
+        return MH_OK;
+    }
+    MH_TRY(mh_fill(m->gr[g.loss], 1.0f, numel(g.syms[g.loss].shape)));  // model.mojo:176-180
+    for (size_t k = g.nodes.size(); k-- > 0;) MH_TRY(run_backward_node(m, k));
+    return MH_OK;
+}
+
+static void drop_graphs(mh_model* m) {
+    for (auto& e : m->graph) {
+        if (e) (void)hipGraphExecDestroy(e);
+        e = nullptr;
+    }
+}
+
 static int execute(mh_model* m, int32_t nodes, const char* what) {
     PassScope ps;
     for (int32_t i = 0; i < nodes; ++i) MH_TRY(run_forward_node(m, (size_t)i));
@@ -447,6 +476,7 @@ int mh_model_create(const mh_graph* g, uint64_t flags, mh_model** out) {
 
 int mh_model_destroy(mh_model* m) {
     if (!m) return MH_OK;
+    drop_graphs(m);
     int rc = MH_OK;
     if (m->arena) rc = mh_free(m->arena);
     if (m->grad_arena) {
@@ -498,6 +528,43 @@ int mh_model_backward(mh_model* m, int32_t nupper, const float* const* upper_gra
         MH_HIP(hipStreamSynchronize(ctx().stream));
     }
     return ps.end("mh_model_backward");
+}
+
+int mh_model_capture(mh_model* m, int pass) {
+    if (!m) return fail(MH_ERR_NULL, "mh_model_capture: null model");
+    MH_TRY(require_init());
+    MH_TRY(check_pass(m, pass));
+    hipStream_t st = ctx().stream;
+    {  // run the pass once: library buffers reach the sizes the pass needs before capture
+        PassScope ps;
+        MH_TRY(enqueue_pass(m, pass));
+        MH_HIP(hipStreamSynchronize(st));
+    }
+    PassScope ps;
+    MH_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    const int rc = enqueue_pass(m, pass);
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(st, &graph);
+    if (rc != MH_OK || e != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc != MH_OK ? rc : hip_check(e, "mh_model_capture: hipStreamEndCapture");
+    }
+    hipGraphExec_t exec = nullptr;
+    const hipError_t e2 = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    MH_HIP(e2);
+    if (m->graph[pass]) (void)hipGraphExecDestroy(m->graph[pass]);
+    m->graph[pass] = exec;
+    return MH_OK;
+}
+
+int mh_model_replay(mh_model* m, int pass) {
+    if (!m) return fail(MH_ERR_NULL, "mh_model_replay: null model");
+    MH_TRY(require_init());
+    if (pass != MH_PASS_FORWARD && pass != MH_PASS_BACKWARD) return fail(MH_ERR_INVALID, "unknown pass %d", pass);
+    if (!m->graph[pass]) return fail(MH_ERR_INVALID, "mh_model_replay: pass %d has not been captured", pass);
+    MH_HIP(hipGraphLaunch(m->graph[pass], ctx().stream));
+    return finish("mh_model_replay");
 }
 
 int mh_model_tensor(mh_model* m, int32_t sym, float** dptr) {

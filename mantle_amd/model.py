@@ -146,6 +146,22 @@ class Model:
         else:
             _lib.call("mh_model_backward", self._h, 0, None, _lib.FROM_HOST)
 
+    # ---- HIP-graph replay of the passes ----
+    _PASSES = {"forward": _lib.PASS_FORWARD, "backward": _lib.PASS_BACKWARD}
+
+    def capture(self, pass_: str) -> None:
+        """Records the forward pass (every node) or the backward pass (loss seed + every node
+        in reverse) as a HIP graph; the pass runs once eagerly first."""
+        _lib.call("mh_model_capture", self._h, self._PASSES[pass_])
+
+    def replay(self, pass_: str) -> Optional[Tensor]:
+        """Launches the captured pass; write inputs into parameters.tensors first. The forward
+        pass returns the loss slot."""
+        _lib.call("mh_model_replay", self._h, self._PASSES[pass_])
+        if pass_ == "forward" and self.graph.loss_out is not None:
+            return self.parameters.tensors[self.graph.loss_out]
+        return None
+
     def info(self) -> dict:
         n, tb, gb, fp = ctypes.c_int32(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int32()
         _lib.call("mh_model_info", self._h, ctypes.byref(n), ctypes.byref(tb), ctypes.byref(gb), ctypes.byref(fp))

@@ -311,3 +311,60 @@ def test_model_param_span_layout_and_single_launch_adam(gpu):
     for s, o in zip(ps, offs):
         used[o:o + s.shape.num_elements()] = True
     assert not whole[~used].any(), "padding between parameter slots changed"
+
+
+@pytest.mark.parametrize("which", ["bias_relu_fused", "config5"])
+def test_model_graph_replay_matches_eager(gpu, which):
+    """Captured forward / backward passes replayed three times, with new inputs, zero_grad
+    and host reads between replays; every replay bit-identical to an eager model."""
+    m = gpu.m
+    if which == "bias_relu_fused":
+        nodes = _bias_relu_nodes() + [(OPS["MEAN"], ["r"], None, "l")]
+        shape = (64, 32, 7, 7)
+        values = {"x": synth.normal(shape, 0, 1, 1290), "bias": synth.normal((1, 32, 1, 1), 0, 0.1, 1291)}
+        trainable, params, fuse = ["x", "bias"], ["bias"], True
+        new_inputs = lambda it: {"x": synth.normal(shape, 0, 1, 1300 + it)}  # noqa: E731
+    else:
+        nodes = config5_nodes()
+        rows = 4099
+        onehot = np.zeros((rows, 10), np.float32)
+        onehot[np.arange(rows), synth.integers((rows,), 0, 10, 1292)] = 1
+        values = {"logits": synth.normal((rows, 10), 0, 2, 1293), "onehot": onehot}
+        trainable, params, fuse = ["logits"], [], False
+        new_inputs = lambda it: {"logits": synth.normal((rows, 10), 0, 2, 1310 + it), "onehot": onehot}  # noqa: E731
+    models = []
+    for _ in range(2):
+        g, syms, inputs = native_graph(m, nodes, values, trainable, params)
+        g.loss(syms[nodes[-1][3]])
+        models.append((g, syms, inputs, m.Model(g, fuse_bias_relu=fuse)))
+    (_, syms_a, inputs, eager), (_, syms_b, _, graphed) = models
+    graphed.capture("forward")
+    graphed.capture("backward")
+    for it in range(3):
+        iv = new_inputs(it)
+        eager.parameters.grads.set_zero()
+        la = eager.forward(*[iv[n] for n in inputs]).to_numpy()
+        eager.backward()
+        for n in inputs:
+            graphed.parameters.tensors[syms_b[n]] = iv[n]
+        graphed.parameters.grads.set_zero()
+        lb = graphed.replay("forward").to_numpy()
+        graphed.replay("backward")
+        assert_bitexact(lb, la, f"{which} loss, replay {it}")
+        for name, sa in syms_a.items():
+            sb = syms_b[name]
+            assert_bitexact(graphed.parameters.tensors[sb].to_numpy(), eager.parameters.tensors[sa].to_numpy(),
+                            f"{which} tensor {name}, replay {it}")
+            if sa.trainable:
+                assert_bitexact(graphed.parameters.grads[sb].to_numpy(), eager.parameters.grads[sa].to_numpy(),
+                                f"{which} grad {name}, replay {it}")
+
+
+def test_model_replay_requires_capture(gpu):
+    m = gpu.m
+    g = m.Graph()
+    x = g.input((4, 4), trainable=True)
+    g.loss(g.op(m.OP.SUM, x))
+    model = m.Model(g)
+    with pytest.raises(m.MantleHipError):
+        model.replay("forward")
