@@ -438,10 +438,19 @@ def run_c5(L, reps, rows=1 << 20, classes=10):
     model_ops = [("model.forward", lambda: L.mh_model_forward(model._h, 2, tab, 1), fwd_bytes),
                  ("model.backward", lambda: L.mh_model_backward(model._h, 0, None, 0), bwd_bytes)]
     mmed = time_ops(d, model_ops, reps, setup=lambda: chk(L, L.mh_model_zero_grad(model._h), "zero_grad"))
-    del model, g
+    # the same graph with its head run as the row-fused kernels (MH_MODEL_FUSE_ROWS)
+    fmodel = mm.Model(g, fuse_rows=True)
+    # bytes the fused model moves: the two input copies (read + write, 4F) and the row kernel's
+    # x and target (2F) forward; x, target and grad_x read and written (4F) backward
+    fused_model_ops = [("model_fused.forward", lambda: L.mh_model_forward(fmodel._h, 2, tab, 1), 6 * F + 4),
+                       ("model_fused.backward", lambda: L.mh_model_backward(fmodel._h, 0, None, 0), 4 * F + 4)]
+    fmed = time_ops(d, fused_model_ops, reps, setup=lambda: chk(L, L.mh_model_zero_grad(fmodel._h), "zero_grad"))
+    del model, fmodel, g
     d.free()
     return {"shape": [rows, classes], "elements": E,
             "model": op_report(model_ops, mmed), "model_total": total_report(model_ops, mmed),
+            "model_fused_rows": op_report(fused_model_ops, fmed),
+            "model_fused_rows_total": total_report(fused_model_ops, fmed),
             "fused": op_report(fused, mf), "fused_total": total_report(fused, mf),
             "fwd": op_report(fwd, med), "bwd": op_report(bwd, med),
             "fwd_total": total_report(fwd, med), "bwd_total": total_report(bwd, med),

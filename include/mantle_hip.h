@@ -263,6 +263,14 @@ enum mh_copy_from { MH_FROM_HOST = 0, MH_FROM_DEVICE = 1 };
 /* mh_model_create flag: run an ADD whose output only feeds the RELU node right after it as
  * the fused bias + RELU kernels (every tensor and grad slot still holds the op-by-op value). */
 #define MH_MODEL_FUSE_BIAS_RELU 1u
+/* mh_model_create flag: run the node groups nn.Softmax, nn.LogSoftmax, nn.CrossEntropyLoss
+ * (activations.mojo:74-108, loss.mojo:45-61) and Softmax -> LOG -> MUL(target) -> MEAN over
+ * the last axis (at most 2047 classes) as one row-fused kernel each way, when the group's
+ * nodes are consecutive and its intermediates are read by the group alone. The group's
+ * output (or loss) and grad_x get the op-by-op values; the intermediate tensor and gradient
+ * slots are not written, and the backward assumes their gradients start at zero (as after
+ * mh_model_zero_grad). */
+#define MH_MODEL_FUSE_ROWS 2u
 
 typedef struct mh_graph mh_graph;
 typedef struct mh_model mh_model;
@@ -328,8 +336,9 @@ int mh_model_replay(mh_model* m, int pass);
  * parameter in one launch; padding stays zero. NULL spans and n = 0 without trainable
  * parameters. */
 int mh_model_param_span(mh_model* m, float** params, float** grads, int64_t* n);
+/* fused_groups: bias + RELU pairs plus row groups the model runs fused. */
 int mh_model_info(const mh_model* m, int32_t* n_inference_nodes, int64_t* tensor_bytes, int64_t* grad_bytes,
-                  int32_t* fused_pairs);
+                  int32_t* fused_groups);
 
 /* ---- optimizer ---- */
 

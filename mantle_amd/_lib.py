@@ -51,6 +51,7 @@ ATTR_AXIS, ATTR_NEGATIVE_SLOPE, ATTR_MIN, ATTR_MAX = 1, 2, 4, 8
 SYM_INPUT, SYM_PARAM, SYM_NODE = 0, 1, 2
 FROM_HOST, FROM_DEVICE = 0, 1
 MODEL_FUSE_BIAS_RELU = 1
+MODEL_FUSE_ROWS = 2
 PASS_FORWARD, PASS_BACKWARD = 0, 1
 
 

@@ -192,6 +192,12 @@ size_t unbroadcast_scratch_floats(const mh_shape& sgrad, const mh_shape& srg);
 int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* rg,
                               const mh_shape& srg, bool negate, float* tmp);
 int plan_unbroadcast(const mh_shape& sgrad, const mh_shape& srg, mh_reduce_plan_info* info);
+// The cross-entropy graph (loss.mojo:45-61) with its final scale given (the value of the
+// graph scalar it multiplies by); mh_cross_entropy_* use f32(-1 / rows).
+int cross_entropy_fwd_c(float* loss, const float* x, const float* tg, int64_t rows, int64_t K, float scale);
+int cross_entropy_bwd_c(float* gx, const float* x, const float* tg, const float* ug, int64_t rows, int64_t K,
+                        float scale);
+
 // grad += un-broadcast(rg) of a broadcast MUL / DIV backward with rg computed inside the
 // reduction (single-step plans whose per-element operand has the full shape); *done says
 // whether it ran.

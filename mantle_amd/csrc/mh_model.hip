@@ -49,7 +49,16 @@ struct mh_model {
     std::vector<float*> gr;  // per symbol: its gradient slot (nullptr if not trainable)
     int32_t n_inference = -1;
     size_t param_span = 0;  // floats of the trainable-parameter span at the start of both arenas
-    std::vector<int> fuse;
+    std::vector<int> fuse;  // per node: kFuseAdd / kFuseRelu (bias + RELU), kFuseRow (row group)
+    struct RowGroup {
+        int graph;  // 0 head (Softmax, LOG, MUL, MEAN), 1 cross entropy, 2 Softmax, 3 LogSoftmax
+        int first, last;
+        int32_t x, target, out;
+        int64_t rows, K;
+        float scale;  // cross entropy: the graph scalar of its last MUL
+    };
+    std::vector<RowGroup> rows;
+    std::vector<int> row_of;  // per node: its RowGroup, or -1
     hipGraphExec_t graph[2] = {nullptr, nullptr};  // captured passes (MH_PASS_FORWARD / _BACKWARD)  // per node: 1 = ADD fused with the next node (RELU), 2 = that RELU
 };
 
@@ -152,14 +161,134 @@ static int32_t inference_nodes(const mh_graph& g) {
     return -1;
 }
 
+constexpr int kFuseAdd = 1, kFuseRelu = 2, kFuseRow = 3;
+constexpr int64_t kRowMaxClasses = 2047;  // the fused row kernels' limit
+
+// Row groups (MH_MODEL_FUSE_ROWS): consecutive nodes that nn.Softmax / nn.LogSoftmax /
+// nn.CrossEntropyLoss emit (activations.mojo:74-108, loss.mojo:45-61), or the config-5 head
+// (Softmax, LOG, MUL by a target, MEAN), over the last axis, whose intermediates are read by
+// the group alone and are neither graph outputs nor the loss.
+static void plan_row_groups(mh_model* m) {
+    const mh_graph& g = m->g;
+    const size_t nn = g.nodes.size();
+    std::vector<std::vector<int>> users(g.syms.size());
+    for (size_t j = 0; j < nn; ++j)
+        for (int k = 0; k < g.nodes[j].nin; ++k) users[g.nodes[j].in[k]].push_back((int)j);
+    auto exported = [&](int32_t sym) {
+        if (g.loss == sym) return true;
+        for (int32_t o : g.outputs)
+            if (o == sym) return true;
+        return false;
+    };
+    // every reader of `sym` lies in [first, last], and it is not exported
+    auto local = [&](int32_t sym, int first, int last) {
+        if (exported(sym)) return false;
+        for (int j : users[sym])
+            if (j < first || j > last) return false;
+        return true;
+    };
+    auto node_is = [&](size_t j, int op) { return j < nn && g.nodes[j].op == op && m->fuse[j] == 0; };
+    auto axis_last = [&](const mh_graph::Node& nd, const mh_shape& s) {
+        return (nd.attrs.flags & MH_ATTR_AXIS) && nd.attrs.axis == s.rank - 1;
+    };
+    for (size_t i = 0; i + 4 < nn; ++i) {
+        const mh_graph::Node& n0 = g.nodes[i];
+        if (!node_is(i, MH_MAX)) continue;
+        const int32_t x = n0.in[0];
+        const mh_shape& sx = g.syms[x].shape;
+        if (!axis_last(n0, sx)) continue;
+        const int64_t K = sx.dims[sx.rank - 1];
+        if (K < 1 || K > kRowMaxClasses) continue;
+        const mh_graph::Node &n1 = g.nodes[i + 1], &n2 = g.nodes[i + 2], &n3 = g.nodes[i + 3];
+        if (!node_is(i + 1, MH_SUB) || n1.in[0] != x || n1.in[1] != n0.out) continue;
+        if (!node_is(i + 2, MH_EXP) || n2.in[0] != n1.out) continue;
+        if (!node_is(i + 3, MH_SUM) || n3.in[0] != n2.out || !axis_last(n3, sx)) continue;
+        mh_model::RowGroup rg{};
+        rg.x = x;
+        rg.rows = numel(sx) / K;
+        rg.K = K;
+        rg.first = (int)i;
+        const mh_graph::Node& n4 = g.nodes[i + 4];
+        int32_t core_out;
+        if (node_is(i + 4, MH_DIV) && n4.in[0] == n2.out && n4.in[1] == n3.out) {
+            rg.graph = 2;  // Softmax
+            rg.last = (int)i + 4;
+        } else if (node_is(i + 4, MH_LOG) && n4.in[0] == n3.out && node_is(i + 5, MH_SUB) &&
+                   g.nodes[i + 5].in[0] == n1.out && g.nodes[i + 5].in[1] == n4.out) {
+            rg.graph = 3;  // LogSoftmax
+            rg.last = (int)i + 5;
+        } else {
+            continue;
+        }
+        core_out = g.nodes[rg.last].out;
+        rg.out = core_out;
+        // a loss on top: the head (Softmax, LOG, MUL(target), MEAN) or the cross entropy
+        // (LogSoftmax, MUL(target), SUM, MUL(scalar)), target not trainable, x of rank 2 for
+        // the cross entropy (its axis 1)
+        auto mul_target = [&](size_t j, int32_t v, int32_t* t) {
+            if (!node_is(j, MH_MUL)) return false;
+            const mh_graph::Node& nd = g.nodes[j];
+            const int32_t o = nd.in[0] == v ? nd.in[1] : nd.in[1] == v ? nd.in[0] : -1;
+            if (o < 0 || o == v || g.syms[o].trainable || !shape_eq(g.syms[o].shape, sx)) return false;
+            *t = o;
+            return true;
+        };
+        int32_t t = -1;
+        const size_t L = (size_t)rg.last;
+        if (rg.graph == 2 && node_is(L + 1, MH_LOG) && g.nodes[L + 1].in[0] == core_out &&
+            mul_target(L + 2, g.nodes[L + 1].out, &t) && node_is(L + 3, MH_MEAN) &&
+            g.nodes[L + 3].in[0] == g.nodes[L + 2].out && !(g.nodes[L + 3].attrs.flags & MH_ATTR_AXIS)) {
+            mh_model::RowGroup h = rg;
+            h.graph = 0;
+            h.last = (int)L + 3;
+            h.target = t;
+            h.out = g.nodes[L + 3].out;
+            if (local(core_out, h.first, h.last) && local(g.nodes[L + 1].out, h.first, h.last) &&
+                local(g.nodes[L + 2].out, h.first, h.last))
+                rg = h;
+        } else if (rg.graph == 3 && sx.rank == 2 && mul_target(L + 1, core_out, &t) && node_is(L + 2, MH_SUM) &&
+                   g.nodes[L + 2].in[0] == g.nodes[L + 1].out && !(g.nodes[L + 2].attrs.flags & MH_ATTR_AXIS) &&
+                   node_is(L + 3, MH_MUL) && g.nodes[L + 3].in[0] == g.nodes[L + 2].out) {
+            const int32_t c = g.nodes[L + 3].in[1];
+            const mh_graph::Sym& cs = g.syms[c];
+            if (cs.kind == MH_SYM_PARAM && !cs.trainable && cs.init_off >= 0 && is_scalar_shape(cs.shape)) {
+                mh_model::RowGroup h = rg;
+                h.graph = 1;
+                h.last = (int)L + 3;
+                h.target = t;
+                h.out = g.nodes[L + 3].out;
+                h.scale = g.init_data[(size_t)cs.init_off];
+                if (local(core_out, h.first, h.last) && local(g.nodes[L + 1].out, h.first, h.last) &&
+                    local(g.nodes[L + 2].out, h.first, h.last))
+                    rg = h;
+            }
+        }
+        // the core's intermediates: MAX, SUB, EXP, SUM (and LOG of LogSoftmax) outputs
+        bool ok = true;
+        for (int j = rg.first; j < (rg.graph == 3 || rg.graph == 1 ? rg.first + 5 : rg.first + 4) && ok; ++j)
+            ok = local(g.nodes[j].out, rg.first, rg.last);
+        if (!ok) continue;
+        const int id = (int)m->rows.size();
+        m->rows.push_back(rg);
+        for (int j = rg.first; j <= rg.last; ++j) {
+            m->fuse[j] = kFuseRow;
+            m->row_of[j] = id;
+        }
+        i = (size_t)rg.last;
+    }
+}
+
 static void plan_fusion(mh_model* m) {
     const mh_graph& g = m->g;
     m->fuse.assign(g.nodes.size(), 0);
+    m->row_of.assign(g.nodes.size(), -1);
+    m->rows.clear();
+    if (m->flags & MH_MODEL_FUSE_ROWS) plan_row_groups(m);
     if (!(m->flags & MH_MODEL_FUSE_BIAS_RELU)) return;
     for (size_t i = 0; i + 1 < g.nodes.size(); ++i) {
         const mh_graph::Node& a = g.nodes[i];
         const mh_graph::Node& r = g.nodes[i + 1];
-        if (a.op != MH_ADD || r.op != MH_RELU || r.in[0] != a.out || m->fuse[i]) continue;
+        if (a.op != MH_ADD || r.op != MH_RELU || r.in[0] != a.out || m->fuse[i] || m->fuse[i + 1]) continue;
         // the ADD output is read by this RELU only, and is not a graph output or the loss
         bool only = g.loss != a.out;
         for (size_t j = 0; j < g.nodes.size() && only; ++j)
@@ -173,8 +302,8 @@ static void plan_fusion(mh_model* m) {
         const mh_shape& sb = g.syms[a.in[1]].shape;
         const mh_shape& sy = g.syms[a.out].shape;
         if (!shape_eq(sx, sy) || shape_eq(sb, sy) || !broadcasts_to(sb, sy)) continue;
-        m->fuse[i] = 1;
-        m->fuse[i + 1] = 2;
+        m->fuse[i] = kFuseAdd;
+        m->fuse[i + 1] = kFuseRelu;
     }
 }
 
@@ -186,11 +315,21 @@ static int run_forward_node(mh_model* m, size_t i) {
     const float* a = m->t[nd.in[0]];
     const mh_shape& sa = g.syms[nd.in[0]].shape;
     const int64_t n = numel(so);
-    if (m->fuse[i] == 1) {  // ADD + the RELU after it: writes both outputs
+    if (m->fuse[i] == kFuseRow) {  // a row group runs as one kernel at its first node
+        const mh_model::RowGroup& r = m->rows[m->row_of[i]];
+        if ((int)i != r.first) return MH_OK;
+        switch (r.graph) {
+            case 0: return mh_softmax_log_mul_mean_fwd(m->t[r.out], m->t[r.x], m->t[r.target], r.rows, r.K);
+            case 1: return cross_entropy_fwd_c(m->t[r.out], m->t[r.x], m->t[r.target], r.rows, r.K, r.scale);
+            case 2: return mh_softmax_fwd(m->t[r.out], m->t[r.x], r.rows, r.K);
+            default: return mh_logsoftmax_fwd(m->t[r.out], m->t[r.x], r.rows, r.K);
+        }
+    }
+    if (m->fuse[i] == kFuseAdd) {  // ADD + the RELU after it: writes both outputs
         const mh_graph::Node& r = g.nodes[i + 1];
         return mh_bias_relu_fwd(res, m->t[r.out], a, &sa, m->t[nd.in[1]], &g.syms[nd.in[1]].shape);
     }
-    if (m->fuse[i] == 2) return MH_OK;
+    if (m->fuse[i] == kFuseRelu) return MH_OK;
     if (is_binary(nd.op)) return mh_binary_fwd(nd.op, res, &so, a, &sa, m->t[nd.in[1]], &g.syms[nd.in[1]].shape);
     if (nd.op == MH_POW) return mh_pow_fwd(res, a, n, m->t[nd.in[1]]);
     if (is_unary(nd.op)) return mh_unary_fwd(nd.op, res, a, n);
@@ -209,14 +348,25 @@ static int run_backward_node(mh_model* m, size_t i) {
     if (!ug) return MH_OK;  // no trainable operand
     const mh_shape& so = g.syms[nd.out].shape;
     const int32_t* in = nd.in;
-    if (m->fuse[i] == 2) {  // RELU, then the ADD before it
+    if (m->fuse[i] == kFuseRow) {  // a row group's backward runs at its last node
+        const mh_model::RowGroup& r = m->rows[m->row_of[i]];
+        if ((int)i != r.last) return MH_OK;
+        float* gx = m->gr[r.x];
+        switch (r.graph) {
+            case 0: return mh_softmax_log_mul_mean_bwd_accum(gx, m->t[r.x], m->t[r.target], ug, r.rows, r.K);
+            case 1: return cross_entropy_bwd_c(gx, m->t[r.x], m->t[r.target], ug, r.rows, r.K, r.scale);
+            case 2: return mh_softmax_bwd_accum(gx, m->t[r.x], ug, r.rows, r.K);
+            default: return mh_logsoftmax_bwd_accum(gx, m->t[r.x], ug, r.rows, r.K);
+        }
+    }
+    if (m->fuse[i] == kFuseRelu) {  // RELU, then the ADD before it
         const mh_graph::Node& a = g.nodes[i - 1];
         float* gy = m->gr[a.out];
         float* gx = m->gr[a.in[0]];
         float* gb = m->gr[a.in[1]];
         return mh_bias_relu_bwd_accum(gy, gx, gb, m->t[a.out], ug, &so, &g.syms[a.in[1]].shape);
     }
-    if (m->fuse[i] == 1) return MH_OK;
+    if (m->fuse[i] == kFuseAdd) return MH_OK;
     const float* t1 = m->t[in[0]];
     const mh_shape& s1 = g.syms[in[0]].shape;
     const int64_t n1 = numel(s1);
@@ -501,7 +651,9 @@ int mh_model_inference(mh_model* m, int32_t ninputs, const float* const* inputs,
     MH_TRY(write_inputs(m, ninputs, inputs, where));
     int32_t nodes = m->n_inference;
     // a fused ADD + RELU pair is never split by the inference cut
-    if (nodes > 0 && nodes < (int32_t)m->fuse.size() && m->fuse[nodes - 1] == 1) ++nodes;
+    if (nodes > 0 && nodes < (int32_t)m->fuse.size() && m->fuse[nodes - 1] == kFuseAdd) ++nodes;
+    if (nodes > 0 && nodes < (int32_t)m->fuse.size() && m->fuse[nodes - 1] == kFuseRow)
+        nodes = m->rows[m->row_of[nodes - 1]].last + 1;  // never cut a row group
     return execute(m, nodes, "mh_model_inference");
 }
 
@@ -597,15 +749,16 @@ int mh_model_param_span(mh_model* m, float** params, float** grads, int64_t* n) 
 }
 
 int mh_model_info(const mh_model* m, int32_t* n_inference_nodes, int64_t* tensor_bytes, int64_t* grad_bytes,
-                  int32_t* fused_pairs) {
+                  int32_t* fused_groups) {
     if (!m) return fail(MH_ERR_NULL, "mh_model_info: null model");
     if (n_inference_nodes) *n_inference_nodes = m->n_inference;
     if (tensor_bytes) *tensor_bytes = (int64_t)(m->arena_floats * sizeof(float));
     if (grad_bytes) *grad_bytes = (int64_t)(m->grad_floats * sizeof(float));
-    if (fused_pairs) {
+    if (fused_groups) {
         int32_t c = 0;
-        for (int f : m->fuse) c += f == 1;
-        *fused_pairs = c;
+        for (int f : m->fuse) c += f == kFuseAdd;
+        c += (int32_t)m->rows.size();
+        *fused_groups = c;
     }
     return MH_OK;
 }

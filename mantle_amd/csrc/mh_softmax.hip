@@ -922,15 +922,18 @@ static int launch_bwd(float* gx, const float* x, const float* up, const float* u
 }
 
 // Loss graphs: block partials, then the all-element sum with the graph's epilogue.
+// `cscale` of the cross entropy: the graph scalar it multiplies by (NaN: f32(-1 / rows)).
 template <int V>
-static int loss_fwd(const char* what, float* loss, const float* x, const float* tg, int64_t rows, int64_t K) {
+static int loss_fwd(const char* what, float* loss, const float* x, const float* tg, int64_t rows, int64_t K,
+                    float cscale = __builtin_nanf("")) {
     MH_TRY(check_rows(what, rows, K));
     if (!loss) return fail(MH_ERR_NULL, "%s: null loss", what);
     if (rows * K > 0 && (!x || !tg)) return fail(MH_ERR_NULL, "%s: null tensor", what);
     MH_TRY(require_init());
     const int64_t n = rows * K;
-    if (n == 0) {  // MEAN of nothing: 0 / 0; the cross-entropy sum of nothing: 0 * f32(-1/rows)
-        const float v = V == G_SMLM ? __builtin_nanf("") : 0.0f * (float)(-1.0 / (double)rows);
+    const float ce = cscale == cscale ? cscale : (float)(-1.0 / (double)rows);
+    if (n == 0) {  // MEAN of nothing: 0 / 0; the cross-entropy sum of nothing: 0 * the scale
+        const float v = V == G_SMLM ? __builtin_nanf("") : 0.0f * ce;
         MH_TRY(mh_fill(loss, v, 1));
         return finish(what);
     }
@@ -941,27 +944,26 @@ static int loss_fwd(const char* what, float* loss, const float* x, const float* 
     MH_TRY(scratch((np + t + 64) * sizeof(float), reinterpret_cast<void**>(&part)));
     int64_t nb = 0;
     bool done = false;
-    const float lscale = V == G_SMLM ? (float)n : (float)(-1.0 / (double)rows);
+    const float lscale = V == G_SMLM ? (float)n : ce;
     MH_TRY(launch_fwd<V>(x, tg, nullptr, rows, (int)K, part, &nb, loss, lscale, &done));
     if (done) return finish(what);
     if (V == G_SMLM)  // MEAN.forward: the sum of every element / f32(N)
         MH_TRY(reduce_abc(RED_SUM, EPI_MEAN, part, 1, nb, 1, loss, nullptr, (float)n, part + np));
     else  // SUM.forward, then MUL(., f32(-1 / f64(rows))) (loss.mojo:58-59)
-        MH_TRY(reduce_abc(RED_SUM, EPI_SCALE, part, 1, nb, 1, loss, nullptr, (float)(-1.0 / (double)rows),
-                          part + np));
+        MH_TRY(reduce_abc(RED_SUM, EPI_SCALE, part, 1, nb, 1, loss, nullptr, ce, part + np));
     return finish(what);
 }
 
 template <int V>
 static int loss_bwd(const char* what, float* gx, const float* x, const float* tg, const float* ug, int64_t rows,
-                    int64_t K) {
+                    int64_t K, float cscale = __builtin_nanf("")) {
     MH_TRY(check_rows(what, rows, K));
     const int64_t n = rows * K;
     if (n == 0) return MH_OK;
     if (!gx || !x || !tg || !ug) return fail(MH_ERR_NULL, "%s: null tensor", what);
     MH_TRY(require_init());
-    const float c = V == G_SMLM ? (float)(1.0 / (double)n)      // MEAN.backward, basics.mojo:470-487
-                                : (float)(-1.0 / (double)rows);  // the scale of loss.mojo:59
+    const float c = V == G_SMLM ? (float)(1.0 / (double)n)  // MEAN.backward, basics.mojo:470-487
+                                : (cscale == cscale ? cscale : (float)(-1.0 / (double)rows));  // loss.mojo:59
     MH_TRY(launch_bwd<V>(gx, x, tg, ug, rows, (int)K, c));
     return finish(what);
 }
@@ -985,6 +987,15 @@ static int map_bwd(const char* what, float* gx, const float* x, const float* gou
     MH_TRY(require_init());
     MH_TRY(launch_bwd<V>(gx, x, gout, nullptr, rows, (int)K, 0.0f));
     return finish(what);
+}
+
+int cross_entropy_fwd_c(float* loss, const float* x, const float* tg, int64_t rows, int64_t K, float scale) {
+    return loss_fwd<G_CE>("cross entropy (graph)", loss, x, tg, rows, K, scale);
+}
+
+int cross_entropy_bwd_c(float* gx, const float* x, const float* tg, const float* ug, int64_t rows, int64_t K,
+                        float scale) {
+    return loss_bwd<G_CE>("cross entropy backward (graph)", gx, x, tg, ug, rows, K, scale);
 }
 
 }  // namespace mh

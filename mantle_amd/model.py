@@ -79,11 +79,15 @@ class Parameters:
 
 
 class Model:
-    def __init__(self, g: Graph, inference_only: bool = False, fuse_bias_relu: bool = False):
+    def __init__(self, g: Graph, inference_only: bool = False, fuse_bias_relu: bool = False,
+                 fuse_rows: bool = False):
+        """fuse_bias_relu: ADD(bias) -> RELU pairs run fused (every slot still written).
+        fuse_rows: Softmax / LogSoftmax / CrossEntropyLoss node groups run as one row kernel
+        each way (their intermediate slots are not written; gradients assume zero_grad)."""
         ensure_init()
         self.graph = g
         h = ctypes.c_void_p()
-        flags = _lib.MODEL_FUSE_BIAS_RELU if fuse_bias_relu else 0
+        flags = (_lib.MODEL_FUSE_BIAS_RELU if fuse_bias_relu else 0) | (_lib.MODEL_FUSE_ROWS if fuse_rows else 0)
         _lib.call("mh_model_create", g.handle, flags, ctypes.byref(h))
         self._h = h.value
         self.parameters = Parameters(self)
@@ -166,4 +170,4 @@ class Model:
         n, tb, gb, fp = ctypes.c_int32(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int32()
         _lib.call("mh_model_info", self._h, ctypes.byref(n), ctypes.byref(tb), ctypes.byref(gb), ctypes.byref(fp))
         return {"n_inference_nodes": n.value, "tensor_bytes": tb.value, "grad_bytes": gb.value,
-                "fused_pairs": fp.value}
+                "fused_groups": fp.value}

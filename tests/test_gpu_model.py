@@ -70,7 +70,7 @@ def test_model_bias_relu_configs(gpu, fuse, xshape, bshape):
     axes = tuple(i for i, d in enumerate(bshape) if d == 1)
     model, *_ = _compare(gpu, _bias_relu_nodes(), values, ["x", "bias"], params=["bias"], seed=seed, fuse=fuse,
                          what=f"fuse={fuse}", summed={"bias": ("y", axes)} if fuse else None)
-    assert model.info()["fused_pairs"] == (1 if fuse else 0)
+    assert model.info()["fused_groups"] == (1 if fuse else 0)
 
 
 def test_model_config5_chain(gpu):
@@ -368,3 +368,88 @@ def test_model_replay_requires_capture(gpu):
     model = m.Model(g)
     with pytest.raises(m.MantleHipError):
         model.replay("forward")
+
+
+
+def _ce_graph(m, rows, classes, x_tr=True, extra=False):
+    """nn.CrossEntropyLoss's nodes (loss.mojo:45-61) over x [rows, classes] (with `extra`, a
+    second use of the Softmax output keeps that group unfused in its loss form)."""
+    g = m.Graph()
+    x = g.input((rows, classes), trainable=x_tr)
+    t = g.input((rows, classes))
+    mx = g.op(m.OP.MAX, x, attributes={"axis": 1})
+    xm = g.op(m.OP.SUB, x, mx)
+    e = g.op(m.OP.EXP, xm)
+    s = g.op(m.OP.SUM, e, attributes={"axis": 1})
+    ls = g.op(m.OP.LOG, s)
+    lsm = g.op(m.OP.SUB, xm, ls)
+    tl = g.op(m.OP.MUL, t, lsm)
+    ret = g.op(m.OP.SUM, tl)
+    loss = g.op(m.OP.MUL, ret, -1.0 / rows)
+    if extra:
+        loss = g.op(m.OP.ADD, loss, g.op(m.OP.MEAN, g.op(m.OP.MUL, lsm, lsm)))
+    g.loss(loss)
+    return g, x, t
+
+
+@pytest.mark.parametrize("rows,classes", [(4099, 10), (300, 130), (64, 1000), (7, 1)])
+def test_model_fused_rows_cross_entropy_and_head(gpu, rows, classes):
+    """MH_MODEL_FUSE_ROWS: the cross-entropy group (and the config-5 head) fused against the
+    same model op by op: loss in the sum class, grad_x bit-identical."""
+    m = gpu.m
+    xv = synth.normal((rows, classes), 0, 2, 1400)
+    tv = synth.uniform((rows, classes), 0, 1, 1401)
+    for build in ("ce", "ce_extra", "head"):
+        results = []
+        for fuse in (False, True):
+            if build == "head":
+                g, syms, inputs = native_graph(m, config5_nodes(), {"logits": xv, "onehot": tv}, ["logits"])
+                g.loss(syms["loss"])
+                x = syms["logits"]
+                feed = [xv, tv]
+            else:
+                g, x, _ = _ce_graph(m, rows, classes, extra=build == "ce_extra")
+                feed = [xv, tv]
+            model = m.Model(g, fuse_rows=fuse)
+            loss = model.forward(*feed).to_numpy()
+            model.backward()
+            results.append((loss, model.parameters.grads[x].to_numpy(), model.info()["fused_groups"]))
+        (l0, g0, f0), (l1, g1, f1) = results
+        assert f0 == 0 and f1 == 1, (build, f0, f1)
+        np.testing.assert_allclose(l1, l0, rtol=2e-5, atol=1e-7, err_msg=f"{build} loss")
+        assert_bitexact(g1, g0, f"{build} grad_x")
+
+
+@pytest.mark.parametrize("classes", [10, 257])
+def test_model_fused_rows_softmax_inside_a_graph(gpu, classes):
+    """A Softmax group whose output feeds later nodes: the output slot and every gradient
+    outside the group are bit-identical to the unfused model."""
+    m = gpu.m
+    rows = 513
+    xv = synth.normal((rows, classes), 0, 2, 1410)
+    wv = synth.normal((1, classes), 0, 1, 1411)
+    outs = []
+    for fuse in (False, True):
+        g = m.Graph()
+        x = g.input((rows, classes), trainable=True)
+        w = g.param((1, classes), init=wv)
+        h = g.op(m.OP.MUL, x, w)
+        mx = g.op(m.OP.MAX, h, attributes={"axis": 1})
+        e = g.op(m.OP.EXP, g.op(m.OP.SUB, h, mx))
+        sm = g.op(m.OP.DIV, e, g.op(m.OP.SUM, e, attributes={"axis": 1}))
+        loss = g.op(m.OP.SUM, g.op(m.OP.TANH, sm))
+        g.loss(loss)
+        g.out(sm)
+        model = m.Model(g, fuse_rows=fuse)
+        l = model.forward(xv).to_numpy()
+        model.backward()
+        P = model.parameters
+        outs.append((l, P.tensors[sm].to_numpy(), P.grads[x].to_numpy(), P.grads[w].to_numpy(),
+                     model.info()["fused_groups"], model.inference(xv)[0].to_numpy()))
+    (l0, s0, gx0, gw0, f0, i0), (l1, s1, gx1, gw1, f1, i1) = outs
+    assert (f0, f1) == (0, 1)
+    assert_bitexact(s1, s0, "softmax output")
+    assert_bitexact(l1, l0, "loss")
+    assert_bitexact(gx1, gx0, "grad x")
+    assert_bitexact(gw1, gw0, "grad w")
+    assert_bitexact(i1, i0, "inference output")
