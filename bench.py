@@ -763,6 +763,14 @@ def stats_summary(stats_csv, command, bench_json=None):
                   f"In the bench run of the same tree, `bench.py` (HIP events on the library stream) timed `{rf['kernel']}` "
                   f"at {rf['avg_launch_ms'] * 1e3:.1f} us per launch: {rf['achieved']} GB/s of algorithmic bytes "
                   f"({rf['bytes_per_launch']} B per launch), {rf['frac']:.3f} of 8 TB/s."]
+        prefix = C2_KERNEL.get(rf["kernel"])
+        match = [r for r in rows if prefix and r["Name"].startswith(prefix)]
+        if match:
+            avg = float(match[0]["AverageNs"]) / 1e3
+            ev = rf["avg_launch_ms"] * 1e3
+            lines.append(f"rocprofv3 averages `{match[0]['Name'].split('(')[0]}` at {avg:.1f} us over its "
+                         f"{match[0]['Calls']} launches (the table above), {abs(avg - ev) / ev * 100:.1f} % from the "
+                         f"event timing.")
     os.makedirs(os.path.dirname(TRAFFIC_JSON), exist_ok=True)
     with open(os.path.join(os.path.dirname(TRAFFIC_JSON), "bench_kernel_stats.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
