@@ -1010,6 +1010,80 @@ int plan_unbroadcast(const mh_shape& sgrad, const mh_shape& srg, mh_reduce_plan_
     return MH_OK;
 }
 
+// ---------------------------------------------------------------------------------------
+// the plane form of an un-broadcast, [N, C, S] -> [C] (a per-channel bias gradient), in one
+// launch
+// ---------------------------------------------------------------------------------------
+// One wavefront per (plane p = n * C + c, chunk k of QC quads): lanes sum their quads in
+// order, a butterfly adds the lanes, and the partial goes to part[(n * K + k) * C + c] with an
+// agent-scope store. The wave waits for the store, then takes a ticket on channel c's counter
+// (one per 128-byte line); the channel's last arrival sums its N * K partials in index order
+// (lane-strided, then a butterfly) and accumulates grad[c] (negated for SUB's operand 1), then
+// resets the counter. Used where the partials per channel are few enough for their tickets
+// not to queue (kPlanesMaxArrivals).
+constexpr int64_t kPlanesTicketStride = 32;
+constexpr int64_t kPlanesMaxArrivals = 4096;
+constexpr int64_t kPlanesMaxQuads = 1024;
+
+template <bool NEG>
+__global__ void __launch_bounds__(kRThreads)
+    k_unb_planes(float* __restrict__ grad, const float* __restrict__ rg, int64_t C, int64_t Sq, int64_t QC,
+                 int64_t K, int64_t nwaves, float* part, uint32_t* tickets) {
+    const int lane = threadIdx.x & 63;
+    const int64_t v = (int64_t)blockIdx.x * (kRThreads / 64) + (threadIdx.x >> 6);
+    if (v >= nwaves) return;  // uniform per wavefront; no barrier follows
+    const int64_t p = v / K, k = v - p * K;
+    const int64_t q0 = p * Sq + k * QC;
+    const int64_t rem = Sq - k * QC;
+    const int64_t cnt = rem < QC ? rem : QC;
+    const float4* r4 = reinterpret_cast<const float4*>(rg);
+    float acc = 0.0f;
+    for (int64_t i = lane; i < cnt; i += 64) {
+        const float4 q = r4[q0 + i];
+        acc = (((acc + q.x) + q.y) + q.z) + q.w;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
+    const int64_t n = p / C, c = p - n * C;
+    const int64_t nper = nwaves / C;  // partials per channel: N * K
+    uint32_t ticket = 0;
+    if (lane == 0) {
+        __hip_atomic_store(&part[(n * K + k) * C + c], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        ticket = __hip_atomic_fetch_add(&tickets[c * kPlanesTicketStride], 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    }
+    ticket = __shfl(ticket, 0);
+    if (ticket != (uint32_t)(nper - 1)) return;
+    float s = 0.0f;
+    for (int64_t i = lane; i < nper; i += 64)
+        s = s + __hip_atomic_load(&part[i * C + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s = s + __shfl_xor(s, m);
+    if (lane == 0) {
+        grad[c] = NEG ? grad[c] + (-s) : grad[c] + s;
+        __hip_atomic_store(&tickets[c * kPlanesTicketStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+struct PlaneForm {
+    int64_t N, C, S, Sq, QC, K, nwaves;
+};
+
+// The plan [N*C, S, 1] then [1, N, C] with S a multiple of 4 and at least 64.
+static bool plane_form(const mh_reduce_plan_info& p, PlaneForm* f) {
+    if (p.nsteps != 2 || p.c[0] != 1 || p.a[1] != 1 || p.a[0] != p.b[1] * p.c[1]) return false;
+    f->N = p.b[1];
+    f->C = p.c[1];
+    f->S = p.b[0];
+    if (f->S % 4 != 0 || f->S < 64 || f->N * f->C < 1) return false;
+    f->Sq = f->S / 4;
+    f->QC = f->Sq < kPlanesMaxQuads ? f->Sq : kPlanesMaxQuads;
+    f->K = (f->Sq + f->QC - 1) / f->QC;
+    f->nwaves = f->N * f->C * f->K;
+    return f->N * f->K <= kPlanesMaxArrivals && (f->nwaves + 3) / 4 <= 0x7fffffff;
+}
+
 size_t unbroadcast_scratch_floats(const mh_shape& sgrad, const mh_shape& srg) {
     mh_reduce_plan_info p;
     if (plan_unbroadcast(sgrad, srg, &p) != MH_OK) return 0;
@@ -1021,7 +1095,13 @@ size_t unbroadcast_scratch_floats(const mh_shape& sgrad, const mh_shape& srg) {
         if (o > bmax) bmax = o;
     }
     auto pad = [](size_t v) { return (v + 63) & ~(size_t)63; };
-    return pad(tmax) + 2 * pad(bmax) + 64;
+    size_t need = pad(tmax) + 2 * pad(bmax) + 64;
+    PlaneForm pf;
+    if (plane_form(p, &pf)) {  // the one-launch plane form's partials
+        const size_t np = pad((size_t)(pf.N * pf.K * pf.C)) + 64;
+        if (np > need) need = np;
+    }
+    return need;
 }
 
 int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* rg, const mh_shape& srg,
@@ -1031,6 +1111,19 @@ int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* r
     const int final_epi = negate ? EPI_ACCUM_NEG : EPI_ACCUM;
     if (p.nsteps == 0)  // only size-1 dims differ: same element order
         return reduce_abc(RED_SUM, final_epi, rg, numel(srg), 1, 1, grad, nullptr, 0.0f, nullptr);
+    PlaneForm pf;
+    if (al16(rg) && plane_form(p, &pf)) {  // a per-channel bias gradient: one launch
+        uint32_t* tk = nullptr;
+        MH_TRY(tickets(pf.C * kPlanesTicketStride, &tk));
+        dim3 g((unsigned)((pf.nwaves + 3) / 4)), b(kRThreads);
+        if (negate)
+            hipLaunchKernelGGL(k_unb_planes<true>, g, b, 0, ctx().stream, grad, rg, pf.C, pf.Sq, pf.QC, pf.K,
+                               pf.nwaves, tmp, tk);
+        else
+            hipLaunchKernelGGL(k_unb_planes<false>, g, b, 0, ctx().stream, grad, rg, pf.C, pf.Sq, pf.QC, pf.K,
+                               pf.nwaves, tmp, tk);
+        return MH_OK;
+    }
     size_t tmax = 0, bmax = 0;
     for (int i = 0; i < p.nsteps; ++i) {
         size_t t = reduce_abc_tmp_floats(RED_SUM, p.a[i], p.b[i], p.c[i]);

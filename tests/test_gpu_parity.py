@@ -705,3 +705,33 @@ def test_tstd_unaligned(gpu):
         a = None if ax < 0 else ax
         ex = np.asarray(x.astype(np.float64).std(axis=a, keepdims=a is not None)).reshape(ORC.tstd(x, a).shape)
         assert_sum_close(m.tstd(vx, ax).to_numpy(), ORC.tstd(x, a), ex, f"unaligned tstd axis {ax}")
+
+
+@pytest.mark.parametrize("xshape", [(16, 32, 8, 8), (8, 32, 28, 28), (3, 5, 16, 4), (300, 3, 64, 1)])
+def test_bias_gradient_plane_form(gpu, xshape):
+    """Broadcast backward into a per-channel operand [1, C, 1, 1] (the one-launch plane form
+    of the un-broadcast when H*W is a multiple of 4 and at least 64): every binary op's
+    operand-1 gradient against the oracle in the sum class, called twice in a row (the
+    arrival counters start at zero again), and accumulate_grad directly."""
+    m = gpu.m
+    C = xshape[1]
+    bshape = (1, C) + (1,) * (len(xshape) - 2)
+    x = synth.normal(xshape, 0, 1, 1500)
+    b = synth.uniform(bshape, 0.5, 2, 1501)
+    ug = synth.normal(xshape, 0, 1, 1502)
+    g0 = synth.normal(bshape, 0, 1, 1503)
+    red = tuple(i for i in range(len(xshape)) if bshape[i] == 1)
+    rg = {"ADD": ug, "SUB": -ug, "MUL": ug * x, "DIV": ((-x) / (b * b)) * ug}
+    for name in ("ADD", "SUB", "MUL", "DIV"):
+        exp = O.backward_op(1, OPS[name], ug, x, b, grad=g0)
+        r64 = rg[name].astype(np.float64)
+        ex = r64.sum(axis=red, keepdims=True) + g0
+        mag = np.abs(r64).sum(axis=red, keepdims=True) + np.abs(g0)
+        for rep in range(2):
+            got = gpu.backward(1, OPS[name], ug, x, b, grad=g0)
+            assert_sum_close(got, exp, ex, f"{name} bias grad {xshape} call {rep}", terms_abs=mag)
+    tg = gpu.T(g0)
+    m.accumulate_grad(tg, gpu.T(ug))
+    assert_sum_close(tg.to_numpy(), O.accumulate_grad(g0, ug),
+                     ug.astype(np.float64).sum(axis=red, keepdims=True) + g0, "accumulate_grad",
+                     terms_abs=np.abs(ug.astype(np.float64)).sum(axis=red, keepdims=True) + np.abs(g0))
