@@ -120,6 +120,64 @@ __device__ __forceinline__ float upstream(float u, float e, float s, float gcons
     }
 }
 
+// The head graph's zero-target shortcut. An element whose target is +-0 adds
+// log(e / s) * 0 = +-0 to the loss sum, and in the backward gets g_sm = 0 + (0 + g_t * 0) / (e / s)
+// = +0, so g_e = 0 + g_sm / s = +0 and its DIV-1 term ((-e) / (s * s)) * g_sm = -0, whenever g_t is
+// finite and e / s is a positive finite number: e >= 2^-100 guarantees that, as s lies in
+// [1, classes]. A sum that starts at +0 never becomes -0 and is unchanged by adding a zero, so
+// skipping such an element's divisions and log changes no bit of any result; every other
+// element (a nonzero target, e below the bound, NaN) takes the full expression.
+constexpr float kSkipMinE = 0x1p-100f;
+
+__device__ __forceinline__ bool smlm_skip(float t, float e) { return t == 0.0f && e >= kSkipMinE; }
+
+// Thread engines, head-graph forward of one row (x and target slots xr / tr in LDS): adds
+// log(e_j / s) * t_j to acc in element order over the elements the shortcut keeps. They are
+// listed first, so that a wavefront evaluates the log once per kept element of its busiest
+// lane rather than once per class; e_j is recomputed from x (the same bits as e[j]).
+template <int KM>
+__device__ __forceinline__ float smlm_fwd_row(float acc, const float* xr, const float* tr, const float (&e)[KM],
+                                              float m, float s, int K) {
+    uint64_t need = 0;
+#pragma unroll
+    for (int j = 0; j < KM; ++j)
+        if (j < K && !smlm_skip(tr[j], e[j])) need |= 1ull << j;
+    while (need != 0) {
+        const int j = __builtin_ctzll(need);
+        need &= need - 1;
+        acc = acc + mlog(mexp(xr[j] - m) / s) * tr[j];  // DIV, LOG, MUL, the MEAN's sum
+    }
+    return acc;
+}
+
+// Thread engines, head-graph backward of one row up to the DIV-1 row sum, which it returns:
+// pre[j] = g_e of every element (+0 where the shortcut skips). The target slots ur are
+// overwritten with g_e of the kept elements. skip_ok: g_t is finite.
+template <int KM>
+__device__ __forceinline__ float smlm_bwd_row(float (&pre)[KM], const float* xr, float* ur, const float (&e)[KM],
+                                              float m, float s, float gconst, bool skip_ok, int K) {
+    const float s2 = s * s;
+    uint64_t need = 0;
+#pragma unroll
+    for (int j = 0; j < KM; ++j)
+        if (j < K && !(skip_ok && smlm_skip(ur[j], e[j]))) need |= 1ull << j;
+    float acc = 0.0f;
+    for (uint64_t nd = need; nd != 0; nd &= nd - 1) {
+        const int j = __builtin_ctzll(nd);
+        const float ej = mexp(xr[j] - m);
+        const float gsm = upstream<G_SMLM>(ur[j], ej, s, gconst);
+        ur[j] = 0.0f + gsm / s;
+        acc = acc + ((-ej) / s2) * gsm;
+    }
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+        float p = 0.0f;
+        if (j < K && ((need >> j) & 1)) p = ur[j];
+        pre[j] = p;
+    }
+    return acc;
+}
+
 // ---------------------------------------------------------------------------------------
 // thread engine: rows of at most KM (<= 64) elements, element-order row sums
 // ---------------------------------------------------------------------------------------
@@ -159,12 +217,11 @@ __global__ void __launch_bounds__(kSThreads)
             }
         }
         const float ls = (V == G_CE || V == G_LOGSOFTMAX) ? mlog(s) : 0.0f;  // LOG.forward of the sum
+        if constexpr (V == G_SMLM) rowsum = smlm_fwd_row<KM>(rowsum, xs + t * K, ts + t * K, e, m, s, K);
 #pragma unroll
         for (int j = 0; j < KM; ++j) {
-            if (j < K) {
-                if constexpr (V == G_SMLM) {
-                    rowsum = rowsum + mlog(e[j] / s) * ts[t * K + j];  // DIV, LOG, MUL, the MEAN's sum
-                } else if constexpr (V == G_CE) {
+            if (V != G_SMLM && j < K) {
+                if constexpr (V == G_CE) {
                     rowsum = rowsum + ts[t * K + j] * ((xr[j] - m) - ls);  // SUB(xm, ls), MUL(target, .)
                 } else if constexpr (V == G_SOFTMAX) {
                     xs[t * K + j] = e[j] / s;  // DIV.forward
@@ -239,7 +296,10 @@ __global__ void __launch_bounds__(kSThreads)
                                          : 0.0f;
         // pre: g_e after DIV (from_softmax), or g_xm after SUB(xm, ls)
         float acc = 0.0f, gS;
-        if constexpr (from_softmax<V>()) {
+        if constexpr (V == G_SMLM) {
+            const bool skip_ok = gconst - gconst == 0.0f;
+            gS = 0.0f + smlm_bwd_row<KM>(pre, xs + t * K, us + t * K, e, m, s, gconst, skip_ok, K);
+        } else if constexpr (from_softmax<V>()) {
             const float s2 = s * s;
 #pragma unroll
             for (int j = 0; j < KM; ++j) {
@@ -429,11 +489,11 @@ __global__ void __launch_bounds__(kSThreads)
                 }
             }
             const float ls = (V == G_CE || V == G_LOGSOFTMAX) ? mlog(s) : 0.0f;
+            if constexpr (V == G_SMLM) rowsum = smlm_fwd_row<KM>(rowsum, xs + t * K, ts + t * K, e, m, s, K);
 #pragma unroll
             for (int j = 0; j < KM; ++j) {
-                if (j < K) {
-                    if constexpr (V == G_SMLM) rowsum = rowsum + mlog(e[j] / s) * ts[t * K + j];
-                    else if constexpr (V == G_CE) rowsum = rowsum + ts[t * K + j] * ((xr[j] - m) - ls);
+                if (V != G_SMLM && j < K) {
+                    if constexpr (V == G_CE) rowsum = rowsum + ts[t * K + j] * ((xr[j] - m) - ls);
                     else if constexpr (V == G_SOFTMAX) xs[t * K + j] = e[j] / s;
                     else xs[t * K + j] = (xr[j] - m) - ls;
                 }
@@ -466,6 +526,7 @@ __global__ void __launch_bounds__(kSThreads)
     const int64_t ntiles = (rows + kSThreads - 1) / kSThreads;
     const int t = threadIdx.x;
     const float gconst = V == G_SMLM ? 0.0f + c * ug[0] : V == G_CE ? 0.0f + 1.0f * (0.0f + ug[0] * c) : 0.0f;
+    const bool skip_ok = gconst - gconst == 0.0f;  // g_t finite (the head graph's zero-target shortcut)
     TileRegs rx{}, ru{}, rg{};
     int64_t tile = blockIdx.x;
     if (tile < ntiles) {
@@ -520,7 +581,9 @@ __global__ void __launch_bounds__(kSThreads)
                 }
             }
             float acc = 0.0f, gS;
-            if constexpr (from_softmax<V>()) {
+            if constexpr (V == G_SMLM) {
+                gS = 0.0f + smlm_bwd_row<KM>(pre, xs + t * K, us + t * K, e, m, s, gconst, skip_ok, K);
+            } else if constexpr (from_softmax<V>()) {
                 const float s2 = s * s;
 #pragma unroll
                 for (int j = 0; j < KM; ++j) {
@@ -704,7 +767,9 @@ __global__ void __launch_bounds__(kSThreads)
 #pragma unroll
             for (int i = 0; i < NE; ++i) {
                 if (slot_elem<VEC>(lane, i) < K) {
-                    if constexpr (V == G_SMLM) rowsum = rowsum + mlog(e[i] / s) * tv[i];
+                    if constexpr (V == G_SMLM) {
+                        if (!smlm_skip(tv[i], e[i])) rowsum = rowsum + mlog(e[i] / s) * tv[i];
+                    }
                     else rowsum = rowsum + tv[i] * ((xv[i] - m) - ls);
                 }
             }
@@ -765,11 +830,17 @@ __global__ void __launch_bounds__(kSThreads)
     float gS;
     if constexpr (from_softmax<V>()) {
         const float s2 = s * s;
+        const bool skip_ok = V == G_SMLM && gconst - gconst == 0.0f;
 #pragma unroll
         for (int i = 0; i < NE; ++i) {
-            const float gsm = upstream<V>(tmp[i], e[i], s, gconst);
-            pre[i] = 0.0f + gsm / s;
-            tmp[i] = ((-e[i]) / s2) * gsm;
+            if (skip_ok && (slot_elem<VEC>(lane, i) >= K || smlm_skip(tmp[i], e[i]))) {
+                pre[i] = 0.0f;  // the values of the full expression (slots past the row are unused)
+                tmp[i] = -0.0f;
+            } else {
+                const float gsm = upstream<V>(tmp[i], e[i], s, gconst);
+                pre[i] = 0.0f + gsm / s;
+                tmp[i] = ((-e[i]) / s2) * gsm;
+            }
         }
         gS = 0.0f + wave_row_reduce<VEC, NE>(tmp, lane, K, 0.0f, OpAdd{});
     } else {

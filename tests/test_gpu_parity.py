@@ -413,22 +413,15 @@ SMLM_CASES = [(4099, 10), (1, 1), (3, 2), (257, 3), (1000, 16), (513, 17), (300,
               (40, 33), (20, 64), (9, 65), (8, 128), (5, 130), (3, 1000), (2, 2047)]
 
 
-@pytest.mark.parametrize("rows,classes", SMLM_CASES, ids=[f"{r}x{c}" for r, c in SMLM_CASES])
-@pytest.mark.parametrize("ugv", [1.0, -0.37])
-def test_fused_softmax_log_mul_mean(gpu, rows, classes, ugv):
-    """mh_softmax_log_mul_mean_fwd / _bwd_accum against the op-by-op graph: the loss in the sum
-    class, the gradient bit-exact -- including its accumulation into a non-zero grad_x, which
-    the graph does as grad_x + g_xm (SUB) and then + the MAX routing. Rows shorter than the
-    oracle's 32 SIMD lanes sum in element order on every path, so the oracle is the
-    reference; at 32 classes its row sums follow the lane order, so the bit-exact reference
-    is the GPU op-by-op chain and the oracle is met within the sum class."""
+def _check_fused_head(gpu, logits, onehot, ugv):
+    """The fused config-5 head (mh_softmax_log_mul_mean_fwd / _bwd_accum) against the op-by-op
+    graph: the loss in the sum class (both NaN where the graph's is), the gradient bit-exact,
+    accumulated into a non-zero grad_x and from zero. Rows shorter than the oracle's 32 SIMD
+    lanes sum in element order on every path, so the oracle is the reference; from 32 classes
+    its row sums follow the lane order, so the bit-exact reference is the GPU op-by-op chain
+    and the oracle is met within the sum class."""
     m = gpu.m
-    logits = synth.normal((rows, classes), 0, 2, 61)
-    if classes > 1:
-        synth.inject_ties(logits, 1, 62)
-    cls = synth.integers((rows,), 0, classes, 63)
-    onehot = np.zeros((rows, classes), np.float32)
-    onehot[np.arange(rows), cls] = 1.0
+    rows, classes = logits.shape
     g = Graph(config5_nodes(), ["logits"])
     seed = np.array([ugv], np.float32)
     vo = g.forward(ORC, {"logits": logits, "onehot": onehot})
@@ -438,14 +431,19 @@ def test_fused_softmax_log_mul_mean(gpu, rows, classes, ugv):
         ref_eng = gpu
         vr = g.forward(gpu, {"logits": logits, "onehot": onehot})
         gr = g.backward(gpu, vr, seed)
-        np.testing.assert_allclose(gr["logits"], go["logits"], rtol=1e-4,
-                                   atol=1e-4 * float(np.abs(go["logits"]).max()))
+        fin = np.isfinite(go["logits"])
+        assert (np.isfinite(gr["logits"]) == fin).all()
+        np.testing.assert_allclose(gr["logits"][fin], go["logits"][fin], rtol=1e-4,
+                                   atol=1e-4 * float(np.abs(go["logits"][fin]).max(initial=0)))
     tl, to = gpu.T(logits), gpu.T(onehot)
     loss = m.Tensor(m.TensorShape(1))
     m.softmax_log_mul_mean_forward(loss, tl, to)
-    t64 = vo["t"].astype(np.float64)
-    assert_sum_close(loss.to_numpy(), vo["loss"], np.array([t64.mean()]), "fused loss",
-                     terms_abs=np.array([np.abs(t64).mean()]))
+    if np.isnan(vo["loss"]).any():
+        assert np.isnan(loss.to_numpy()).all(), "fused loss should be NaN"
+    else:
+        t64 = vo["t"].astype(np.float64)
+        assert_sum_close(loss.to_numpy(), vo["loss"], np.array([t64.mean()]), "fused loss",
+                         terms_abs=np.array([np.abs(t64).mean()]))
     g0 = synth.normal((rows, classes), 0, 1, 64)
     tg = gpu.T(g0)
     m.softmax_log_mul_mean_backward(tg, tl, to, gpu.T(seed))
@@ -455,6 +453,54 @@ def test_fused_softmax_log_mul_mean(gpu, rows, classes, ugv):
     tz = m.Tensor(m.TensorShape(rows, classes))
     m.softmax_log_mul_mean_backward(tz, tl, to, gpu.T(seed))
     assert_bitexact(tz.to_numpy(), gr["logits"], "fused grad from zero")
+
+
+@pytest.mark.parametrize("rows,classes", SMLM_CASES, ids=[f"{r}x{c}" for r, c in SMLM_CASES])
+@pytest.mark.parametrize("ugv", [1.0, -0.37])
+def test_fused_softmax_log_mul_mean(gpu, rows, classes, ugv):
+    """The fused head on one-hot targets (ties injected) against the op-by-op graph."""
+    logits = synth.normal((rows, classes), 0, 2, 61)
+    if classes > 1:
+        synth.inject_ties(logits, 1, 62)
+    cls = synth.integers((rows,), 0, classes, 63)
+    onehot = np.zeros((rows, classes), np.float32)
+    onehot[np.arange(rows), cls] = 1.0
+    _check_fused_head(gpu, logits, onehot, ugv)
+
+
+HEAD_SKIP_CASES = [(4099, 10), (1000, 16), (513, 17), (300, 40), (9, 130), (3, 1000)]
+
+
+@pytest.mark.parametrize("rows,classes", HEAD_SKIP_CASES, ids=[f"{r}x{c}" for r, c in HEAD_SKIP_CASES])
+@pytest.mark.parametrize("case", ["sparse", "tiny_e", "clamped", "nan", "inf_ug"])
+def test_fused_head_zero_target_shortcut(gpu, rows, classes, case):
+    """The fused head skips the divisions and log of zero-target elements whose e is at least
+    2^-100. Targets here are sparse with +0 and -0 zeros, non-unit nonzero values, all-zero and
+    dense rows; "tiny_e" puts elements 60-95 below the row max (e on both sides of 2^-100, down
+    to subnormal), "clamped" 110 below it and -inf (exp's argument clamp: e is the subnormal
+    exp(-88.376...)), "nan" NaN logits (NaN rows and a NaN loss), "inf_ug" an infinite loss
+    gradient (g_t not finite: no skipping)."""
+    logits = synth.normal((rows, classes), 0, 2, 71)
+    u = synth.uniform((rows, classes), 0, 1, 72)
+    onehot = np.where(u < 0.08, np.float32(1.0), np.where(u < 0.12, np.float32(-0.0), np.float32(0.0)))
+    onehot = onehot.astype(np.float32)
+    onehot[u > 0.97] = np.float32(0.3)
+    onehot[u < 0.01] = np.float32(-2.0)
+    onehot[::7] = 0.0          # all-zero rows
+    onehot[3::11] = u[3::11]   # dense rows
+    if case in ("tiny_e", "clamped", "nan"):
+        mx = logits.max(axis=1)
+        cols = synth.integers((rows,), 0, classes, 73)
+        gaps = {"tiny_e": [60.0, 69.0, 69.4, 70.0, 80.0, 95.0], "clamped": [110.0, np.inf],
+                "nan": [np.nan]}[case]
+        for k, r in enumerate(range(0, rows, 2)):
+            gap = gaps[k % len(gaps)]
+            c = int(cols[r])
+            if logits[r, c] == mx[r]:
+                continue  # keep the row max in place
+            logits[r, c] = np.float32(mx[r] - gap)
+    ugv = np.float32(np.inf) if case == "inf_ug" else 0.61
+    _check_fused_head(gpu, logits, onehot, ugv)
 
 
 def test_fused_row_graphs_reject_wide_rows(gpu):
