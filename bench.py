@@ -25,9 +25,21 @@ The other configs are measured after the headline step and reported under "workl
         ([32768, 1000]), forward and backward;
   graph a training step (zero_grad, forward, backward) through the native Model, eager against
         HIP-graph replay, for config 1's graph (with a MEAN loss) and config 5's chain;
-  copy  a plain 1 GiB device copy (the library's copy kernel): the practical streaming rate.
-Tensors smaller than the 256 MB Infinity Cache are timed with the cache flushed before each
-op (a 1 GiB read sweep between ops, outside the timed events).
+  copy  the library's copy kernel over 1 GiB and over one config-3 and one config-5 tensor:
+        the practical streaming rate at each size.
+Workload ops (c3, c4, c5 op by op and fused, rows) get two figures:
+  ms            streamed: R launches back to back on the stream over S buffer sets (S copies
+                of the op's tensors, S chosen so that the other sets' traffic between two
+                uses of one set is at least twice the 256 MB Infinity Cache, so every launch
+                reads cold operands), after a cache flush long enough for the host to queue
+                all R launches behind it; ms = elapsed / R. This is the op's rate inside a
+                step, where launches follow each other;
+  ms_isolated   one launch on set 0 between two events, the caches flushed before it (a 1 GiB
+                read sweep outside the events): it adds the event and dispatch latency of a
+                lone launch, which the copy workload's `isolated_floor_ms` (a one-element
+                fill timed this way) shows.
+`frac` uses ms, `frac_isolated` ms_isolated. The model / chain / adam / adj / graph timings
+are single bracketed launches or passes as described at each.
 
 `roofline.traffic` is filled from profiles/traffic.json when that summary of the rocprofv3
 FETCH_SIZE / WRITE_SIZE runs is present (see `--pmc-summary`), else null.
@@ -156,20 +168,108 @@ def time_ops(d, ops, reps, flush=True, setup=None):
     return {k: statistics.median(v[1:]) for k, v in times.items()}
 
 
-def op_report(ops, med):
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+
+
+def replicate(d, names, min_bytes_per_op):
+    """Buffer sets for streamed timing: set 0 is d.ptrs, sets 1.. hold device copies of the
+    named buffers (other names shared). The count makes the traffic of the other sets'
+    launches between two uses of one set at least twice the Infinity Cache for the lightest
+    op, so that every launch reads operands evicted from every cache."""
+    L = d.L
+    count = max(2, 1 + -(-2 * MALL_BYTES // int(min_bytes_per_op)))
+    sizes = {name: n for name, n in names}
+    sets = [dict(d.ptrs)]
+    for s in range(1, count):
+        P = dict(d.ptrs)
+        for name, n in sizes.items():
+            q = d.alloc(f"{name}#{s}", n)
+            chk(L, L.mh_memcpy_d2d(q, d.ptrs[name], 4 * n), f"copy {name}")
+            P[name] = q
+        sets.append(P)
+    chk(L, L.mh_sync(), "sync")
+    return sets
+
+
+def time_ops_streamed(d, ops, sets, reps, min_launches=24):
+    """ops: [(label, fn(P), bytes)]. Per op: R launches back to back on the stream, launch i
+    on buffer set i % len(sets), between two events after a flush of the caches; the figure
+    is elapsed / R, the median over `reps` such regions (after one warm-up region). The
+    flush runs long enough for the host to queue all R launches behind it (it is repeated
+    when queueing took longer in the warm-up), so the GPU never waits for the host: this is
+    the op's rate inside a step, where launches follow each other on the stream, without
+    the event and dispatch latency of a single bracketed launch."""
+    L = d.L
+    S = len(sets)
+    R = S * max(1, -(-min_launches // S))
+    e0, e1 = d.event(), d.event()
+    ms = ctypes.c_float()
+    out = {}
+    t0 = time.perf_counter()
+    d.flush()
+    chk(L, L.mh_sync(), "sync")
+    flush_s = time.perf_counter() - t0
+    for label, fn, _ in ops:
+        nflush, vals = 1, []
+        for rep in range(reps + 1):
+            for _ in range(nflush):
+                d.flush()
+            chk(L, L.mh_event_record(e0), "record")
+            th = time.perf_counter()
+            for i in range(R):
+                chk(L, fn(sets[i % S]), label)
+            host_s = time.perf_counter() - th
+            chk(L, L.mh_event_record(e1), "record")
+            chk(L, L.mh_sync(), "sync")
+            chk(L, L.mh_event_elapsed_ms(ctypes.byref(ms), e0, e1), "elapsed")
+            if rep == 0:
+                nflush = 1 + int(1.5 * host_s / max(flush_s, 1e-6))
+            else:
+                vals.append(ms.value / R)
+        out[label] = statistics.median(vals)
+    return out
+
+
+def isolated_floor(d, reps):
+    """The isolated method's floor: a one-element fill timed like an op (flush, then one
+    launch between two events)."""
+    L = d.L
+    buf = d.zeros("_floor", 1)
+    med = time_ops(d, [("floor", lambda: L.mh_fill(buf, 0.0, 1), 4)], reps)
+    return round(med["floor"], 4)
+
+
+def op_report(ops, med, iso=None):
     out = {}
     for label, _, nbytes in ops:
         t = med[label]
         gbs = nbytes / (t * 1e-3) / 1e9
         out[label] = {"ms": round(t, 4), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+        if iso is not None:
+            ti = iso[label]
+            out[label]["ms_isolated"] = round(ti, 4)
+            out[label]["frac_isolated"] = round(nbytes / (ti * 1e-3) / 1e9 / PEAK_GBS, 4)
     return out
 
 
-def total_report(ops, med):
+def total_report(ops, med, iso=None):
     tot_b = sum(b for _, _, b in ops)
     tot_t = sum(med[label] for label, _, _ in ops)
     gbs = tot_b / (tot_t * 1e-3) / 1e9
-    return {"bytes": tot_b, "ms": round(tot_t, 4), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+    out = {"bytes": tot_b, "ms": round(tot_t, 4), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+    if iso is not None:
+        ti = sum(iso[label] for label, _, _ in ops)
+        out["ms_isolated"] = round(ti, 4)
+        out["frac_isolated"] = round(tot_b / (ti * 1e-3) / 1e9 / PEAK_GBS, 4)
+    return out
+
+
+def time_both(d, ops, sets, reps, flush=True, setup=None):
+    """Streamed figures over `sets` and isolated ones on set 0 (ops take the set's pointers)."""
+    streamed = time_ops_streamed(d, ops, sets, reps)
+    iso = time_ops(d, [(label, (lambda fn=fn: fn(sets[0])), b) for label, fn, b in ops], reps, flush=flush,
+                   setup=setup)
+    return streamed, iso
 
 
 # ---------------------------------------------------------------------------------------
@@ -260,7 +360,6 @@ def run_c3(L, reps):
     shape, bshape = (256, 32, 28, 28), (1, 32, 1, 1)
     n, nb = int(np.prod(shape)), 32
     d = Dev(L)
-    p = d.ptrs
     d.upload("x", synth.normal(shape, 0, 1, 11))
     d.upload("bias", synth.normal(bshape, 0, 0.1, 12))
     d.upload("ug", synth.normal(shape, 0, 1, 13))
@@ -270,22 +369,25 @@ def run_c3(L, reps):
     sx, sb = make_shape(shape), make_shape(bshape)
     chk(L, L.mh_sync(), "sync")
     B = 4 * n
-    fused = [("bias_relu.fwd", lambda: L.mh_bias_relu_fwd(p["y"], p["r"], p["x"], sx, p["bias"], sb), 3 * B + 128),
-             ("bias_relu.bwd", lambda: L.mh_bias_relu_bwd_accum(None, p["gx"], p["gb"], p["y"], p["ug"], sx, sb),
+    fused = [("bias_relu.fwd", lambda P: L.mh_bias_relu_fwd(P["y"], P["r"], P["x"], sx, P["bias"], sb), 3 * B + 128),
+             ("bias_relu.bwd", lambda P: L.mh_bias_relu_bwd_accum(None, P["gx"], P["gb"], P["y"], P["ug"], sx, sb),
               4 * B + 256)]
-    opbyop = [("ADD.fwd", lambda: L.mh_binary_fwd(0, p["y"], sx, p["x"], sx, p["bias"], sb), 2 * B + 128),
-              ("RELU.fwd", lambda: L.mh_unary_fwd(14, p["r"], p["y"], n), 2 * B),
-              ("RELU.bwd", lambda: L.mh_unary_bwd_accum(14, p["gy"], p["y"], p["ug"], n), 4 * B),
-              ("ADD.bwd_x", lambda: L.mh_binary_bwd_accum(0, 0, p["gx"], sx, p["gy"], sx, p["x"], sx, p["bias"], sb),
+    opbyop = [("ADD.fwd", lambda P: L.mh_binary_fwd(0, P["y"], sx, P["x"], sx, P["bias"], sb), 2 * B + 128),
+              ("RELU.fwd", lambda P: L.mh_unary_fwd(14, P["r"], P["y"], n), 2 * B),
+              ("RELU.bwd", lambda P: L.mh_unary_bwd_accum(14, P["gy"], P["y"], P["ug"], n), 4 * B),
+              ("ADD.bwd_x", lambda P: L.mh_binary_bwd_accum(0, 0, P["gx"], sx, P["gy"], sx, P["x"], sx, P["bias"], sb),
                3 * B),
-              ("ADD.bwd_bias", lambda: L.mh_binary_bwd_accum(0, 1, p["gb"], sb, p["gy"], sx, p["x"], sx, p["bias"], sb),
-               B + 256)]
-    mf = time_ops(d, fused, reps)
-    mo = time_ops(d, opbyop, reps)
+              ("ADD.bwd_bias", lambda P: L.mh_binary_bwd_accum(0, 1, P["gb"], sb, P["gy"], sx, P["x"], sx, P["bias"],
+                                                               sb), B + 256)]
+    for label, fn, _ in fused + opbyop:  # real intermediates in the copied sets
+        chk(L, fn(d.ptrs), label)
+    sets = replicate(d, [(k, n) for k in ("x", "ug", "y", "r", "gy", "gx")] + [("bias", nb), ("gb", nb)], B + 256)
+    mf, mfi = time_both(d, fused, sets, reps)
+    mo, moi = time_both(d, opbyop, sets, reps)
     d.free()
-    return {"shape": [list(shape), list(bshape)], "elements": n,
-            "fused": op_report(fused, mf), "fused_total": total_report(fused, mf),
-            "op_by_op": op_report(opbyop, mo), "op_by_op_total": total_report(opbyop, mo)}
+    return {"shape": [list(shape), list(bshape)], "elements": n, "buffer_sets": len(sets),
+            "fused": op_report(fused, mf, mfi), "fused_total": total_report(fused, mf, mfi),
+            "op_by_op": op_report(opbyop, mo, moi), "op_by_op_total": total_report(opbyop, mo, moi)}
 
 
 # ---------------------------------------------------------------------------------------
@@ -295,8 +397,7 @@ def run_c4(L, reps):
     from mantle_amd import synth
     from mantle_amd._lib import make_shape
     d = Dev(L)
-    p = d.ptrs
-    ops = []
+    ops, bufs = [], []
     cases = [("8192x8192", (8192, 8192), 0, "n"), ("8192x8192", (8192, 8192), 1, "n"),
              ("8192x8192", (8192, 8192), -1, "n"), ("64x512x1024", (64, 512, 1024), 2, "u")]
     for tag, shape, axis, dist in cases:
@@ -314,25 +415,28 @@ def run_c4(L, reps):
         d.upload(f"ug_{name}", synth.normal(red, 0, 1, 43))
         d.zeros(f"res_{name}", m)
         d.zeros(f"g_{name}", n)
+        bufs += [(name, n), (f"g_{name}", n), (f"ug_{name}", m), (f"res_{name}", m)]
         s = make_shape(shape)
         ax = "all" if axis < 0 else f"ax{axis}"
         for op in ("SUM", "MEAN", "MAX"):
             o = OP_ID[op]
             ops.append((f"{tag}.{ax}.{op}.fwd",
-                        lambda o=o, name=name, s=s, axis=axis: L.mh_reduce_fwd(o, p[f"res_{name}"], p[name], s, axis),
+                        lambda P, o=o, name=name, s=s, axis=axis: L.mh_reduce_fwd(o, P[f"res_{name}"], P[name], s, axis),
                         4 * n + 4 * m))
         for op in ("SUM", "MEAN", "MAX"):
             o = OP_ID[op]
             nb = (12 * n + 8 * m) if op == "MAX" else (8 * n + 4 * m)
             ops.append((f"{tag}.{ax}.{op}.bwd",
-                        lambda o=o, name=name, s=s, axis=axis: L.mh_reduce_bwd_accum(o, p[f"g_{name}"], p[name], s,
-                                                                                     p[f"ug_{name}"], axis), nb))
+                        lambda P, o=o, name=name, s=s, axis=axis: L.mh_reduce_bwd_accum(o, P[f"g_{name}"], P[name], s,
+                                                                                        P[f"ug_{name}"], axis), nb))
     chk(L, L.mh_sync(), "sync")
-    med = time_ops(d, ops, reps)
+    sets = replicate(d, bufs, min(b for _, _, b in ops))
+    med, iso = time_both(d, ops, sets, reps)
     d.free()
     fwd = [o for o in ops if o[0].endswith(".fwd")]
     bwd = [o for o in ops if o[0].endswith(".bwd")]
-    return {"ops": op_report(ops, med), "fwd_total": total_report(fwd, med), "bwd_total": total_report(bwd, med)}
+    return {"buffer_sets": len(sets), "ops": op_report(ops, med, iso), "fwd_total": total_report(fwd, med, iso),
+            "bwd_total": total_report(bwd, med, iso)}
 
 
 # ---------------------------------------------------------------------------------------
@@ -365,31 +469,31 @@ def run_c5(L, reps, rows=1 << 20, classes=10):
     SE, SN, S1 = make_shape((rows, classes)), make_shape((rows, 1)), make_shape((1,))
     F, R = 4 * E, 4 * N
     fwd = [
-        ("MAX.fwd", lambda: L.mh_reduce_fwd(10, p["max"], p["logits"], SE, 1), F + R),
-        ("SUB.fwd", lambda: L.mh_binary_fwd(1, p["xm"], SE, p["logits"], SE, p["max"], SN), 2 * F + R),
-        ("EXP.fwd", lambda: L.mh_unary_fwd(4, p["e"], p["xm"], E), 2 * F),
-        ("SUM.fwd", lambda: L.mh_reduce_fwd(8, p["s"], p["e"], SE, 1), F + R),
-        ("DIV.fwd", lambda: L.mh_binary_fwd(3, p["sm"], SE, p["e"], SE, p["s"], SN), 2 * F + R),
-        ("LOG.fwd", lambda: L.mh_unary_fwd(5, p["lp"], p["sm"], E), 2 * F),
-        ("MUL.fwd", lambda: L.mh_binary_fwd(2, p["t"], SE, p["lp"], SE, p["onehot"], SE), 3 * F),
-        ("MEAN.fwd", lambda: L.mh_reduce_fwd(9, p["loss"], p["t"], SE, -1), F + 4),
+        ("MAX.fwd", lambda P: L.mh_reduce_fwd(10, P["max"], P["logits"], SE, 1), F + R),
+        ("SUB.fwd", lambda P: L.mh_binary_fwd(1, P["xm"], SE, P["logits"], SE, P["max"], SN), 2 * F + R),
+        ("EXP.fwd", lambda P: L.mh_unary_fwd(4, P["e"], P["xm"], E), 2 * F),
+        ("SUM.fwd", lambda P: L.mh_reduce_fwd(8, P["s"], P["e"], SE, 1), F + R),
+        ("DIV.fwd", lambda P: L.mh_binary_fwd(3, P["sm"], SE, P["e"], SE, P["s"], SN), 2 * F + R),
+        ("LOG.fwd", lambda P: L.mh_unary_fwd(5, P["lp"], P["sm"], E), 2 * F),
+        ("MUL.fwd", lambda P: L.mh_binary_fwd(2, P["t"], SE, P["lp"], SE, P["onehot"], SE), 3 * F),
+        ("MEAN.fwd", lambda P: L.mh_reduce_fwd(9, P["loss"], P["t"], SE, -1), F + 4),
     ]
     bwd = [
-        ("MEAN.bwd", lambda: L.mh_reduce_bwd_accum(9, p["g_t"], p["t"], SE, p["g_loss"], -1), 2 * F + 4),
-        ("MUL.bwd0", lambda: L.mh_binary_bwd_accum(2, 0, p["g_lp"], SE, p["g_t"], SE, p["lp"], SE, p["onehot"], SE),
+        ("MEAN.bwd", lambda P: L.mh_reduce_bwd_accum(9, P["g_t"], P["t"], SE, P["g_loss"], -1), 2 * F + 4),
+        ("MUL.bwd0", lambda P: L.mh_binary_bwd_accum(2, 0, P["g_lp"], SE, P["g_t"], SE, P["lp"], SE, P["onehot"], SE),
          4 * F),
-        ("LOG.bwd", lambda: L.mh_unary_bwd_accum(5, p["g_sm"], p["sm"], p["g_lp"], E), 4 * F),
-        ("DIV.bwd0", lambda: L.mh_binary_bwd_accum(3, 0, p["g_e"], SE, p["g_sm"], SE, p["e"], SE, p["s"], SN),
+        ("LOG.bwd", lambda P: L.mh_unary_bwd_accum(5, P["g_sm"], P["sm"], P["g_lp"], E), 4 * F),
+        ("DIV.bwd0", lambda P: L.mh_binary_bwd_accum(3, 0, P["g_e"], SE, P["g_sm"], SE, P["e"], SE, P["s"], SN),
          3 * F + R),
-        ("DIV.bwd1", lambda: L.mh_binary_bwd_accum(3, 1, p["g_s"], SN, p["g_sm"], SE, p["e"], SE, p["s"], SN),
+        ("DIV.bwd1", lambda P: L.mh_binary_bwd_accum(3, 1, P["g_s"], SN, P["g_sm"], SE, P["e"], SE, P["s"], SN),
          2 * F + 3 * R),
-        ("SUM.bwd", lambda: L.mh_reduce_bwd_accum(8, p["g_e"], p["e"], SE, p["g_s"], 1), 2 * F + R),
-        ("EXP.bwd", lambda: L.mh_unary_bwd_accum(4, p["g_xm"], p["xm"], p["g_e"], E), 4 * F),
-        ("SUB.bwd0", lambda: L.mh_binary_bwd_accum(1, 0, p["g_logits"], SE, p["g_xm"], SE, p["logits"], SE,
-                                                   p["max"], SN), 3 * F),
-        ("SUB.bwd1", lambda: L.mh_binary_bwd_accum(1, 1, p["g_max"], SN, p["g_xm"], SE, p["logits"], SE,
-                                                   p["max"], SN), F + 2 * R),
-        ("MAX.bwd", lambda: L.mh_reduce_bwd_accum(10, p["g_logits"], p["logits"], SE, p["g_max"], 1), 3 * F + 2 * R),
+        ("SUM.bwd", lambda P: L.mh_reduce_bwd_accum(8, P["g_e"], P["e"], SE, P["g_s"], 1), 2 * F + R),
+        ("EXP.bwd", lambda P: L.mh_unary_bwd_accum(4, P["g_xm"], P["xm"], P["g_e"], E), 4 * F),
+        ("SUB.bwd0", lambda P: L.mh_binary_bwd_accum(1, 0, P["g_logits"], SE, P["g_xm"], SE, P["logits"], SE,
+                                                   P["max"], SN), 3 * F),
+        ("SUB.bwd1", lambda P: L.mh_binary_bwd_accum(1, 1, P["g_max"], SN, P["g_xm"], SE, P["logits"], SE,
+                                                   P["max"], SN), F + 2 * R),
+        ("MAX.bwd", lambda P: L.mh_reduce_bwd_accum(10, P["g_logits"], P["logits"], SE, P["g_max"], 1), 3 * F + 2 * R),
     ]
 
     def zero_grads():  # optim.zero_grad + the loss-grad seed (model.mojo:178-180)
@@ -399,8 +503,13 @@ def run_c5(L, reps, rows=1 << 20, classes=10):
             chk(L, L.mh_zero(p[k], N), "zero")
         chk(L, L.mh_fill(p["g_loss"], 1.0, 1), "seed")
 
+    zero_grads()
+    for label, fn, _ in fwd + bwd:  # real intermediates (and the loss-grad seed) in the copied sets
+        chk(L, fn(p), label)
     chk(L, L.mh_sync(), "sync")
-    med = time_ops(d, fwd + bwd, reps, flush=False, setup=zero_grads)
+    sets = replicate(d, [(k, E) for k in ("logits", "onehot", "xm", "e", "sm", "lp", "t") + grads_full] +
+                     [(k, N) for k in ("max", "s") + grads_row] + [("loss", 1), ("g_loss", 1)], F + 4)
+    med, iso = time_both(d, fwd + bwd, sets, reps, flush=False, setup=zero_grads)
     # the whole chain between two events (includes host launch gaps), caches flushed first
     e0, e1 = d.event(), d.event()
     ms = ctypes.c_float()
@@ -410,18 +519,18 @@ def run_c5(L, reps, rows=1 << 20, classes=10):
         d.flush()
         chk(L, L.mh_event_record(e0), "record")
         for label, fn, _ in fwd + bwd:
-            chk(L, fn(), label)
+            chk(L, fn(p), label)
         chk(L, L.mh_event_record(e1), "record")
         chk(L, L.mh_sync(), "sync")
         chk(L, L.mh_event_elapsed_ms(ctypes.byref(ms), e0, e1), "elapsed")
         chain.append(ms.value)
     chain_ms = statistics.median(chain[1:])
     # the same graph row-fused: 8 B/elem forward (logits, onehot), 16 B/elem backward
-    fused = [("fused.fwd", lambda: L.mh_softmax_log_mul_mean_fwd(p["loss"], p["logits"], p["onehot"], rows, classes),
+    fused = [("fused.fwd", lambda P: L.mh_softmax_log_mul_mean_fwd(P["loss"], P["logits"], P["onehot"], rows, classes),
               2 * F + 4),
-             ("fused.bwd", lambda: L.mh_softmax_log_mul_mean_bwd_accum(p["g_logits"], p["logits"], p["onehot"],
-                                                                       p["g_loss"], rows, classes), 4 * F + 4)]
-    mf = time_ops(d, fused, reps)
+             ("fused.bwd", lambda P: L.mh_softmax_log_mul_mean_bwd_accum(P["g_logits"], P["logits"], P["onehot"],
+                                                                       P["g_loss"], rows, classes), 4 * F + 4)]
+    mf, mfi = time_both(d, fused, sets, reps)
     # the same graph through the native executor: Model.forward (inputs copied into the
     # arena from device memory, then the 8 nodes) and Model.backward (loss seed + 10 calls)
     import mantle_amd as mm
@@ -451,9 +560,10 @@ def run_c5(L, reps, rows=1 << 20, classes=10):
             "model": op_report(model_ops, mmed), "model_total": total_report(model_ops, mmed),
             "model_fused_rows": op_report(fused_model_ops, fmed),
             "model_fused_rows_total": total_report(fused_model_ops, fmed),
-            "fused": op_report(fused, mf), "fused_total": total_report(fused, mf),
-            "fwd": op_report(fwd, med), "bwd": op_report(bwd, med),
-            "fwd_total": total_report(fwd, med), "bwd_total": total_report(bwd, med),
+            "fused": op_report(fused, mf, mfi), "fused_total": total_report(fused, mf, mfi),
+            "buffer_sets": len(sets),
+            "fwd": op_report(fwd, med, iso), "bwd": op_report(bwd, med, iso),
+            "fwd_total": total_report(fwd, med, iso), "bwd_total": total_report(bwd, med, iso),
             "chain_ms": round(chain_ms, 4), "chain_rows_per_s": round(rows / (chain_ms * 1e-3), 1),
             "fused_min_bytes": 24 * E}
 
@@ -532,7 +642,7 @@ def run_rows(L, reps):
     backward 16 (x, grad_out, grad_x read and written)."""
     d = Dev(L)
     p = d.ptrs
-    ops = []
+    ops, bufs = [], []
     for rows, k in ((1 << 20, 10), (32768, 1000)):
         n = rows * k
         tag = f"{rows}x{k}"
@@ -540,23 +650,27 @@ def run_rows(L, reps):
             d.zeros(f"{nm}{tag}", n)
         d.zeros(f"loss{tag}", 1)
         d.zeros(f"ug{tag}", 1)
+        bufs += [(f"{nm}{tag}", n) for nm in ("x", "t", "o", "g")] + [(f"loss{tag}", 1), (f"ug{tag}", 1)]
         chk(L, L.mh_rand_normal(p[f"x{tag}"], n, 21, 0.0, 2.0), "rand")
         chk(L, L.mh_rand_uniform(p[f"t{tag}"], n, 22, 0.0, 1.0), "rand")
         chk(L, L.mh_fill(p[f"ug{tag}"], 1.0, 1), "fill")
-        ops += [(f"cross_entropy.fwd.{tag}", lambda tag=tag, r=rows, k=k: L.mh_cross_entropy_fwd(
-                    p[f"loss{tag}"], p[f"x{tag}"], p[f"t{tag}"], r, k), 8 * n + 4),
-                (f"cross_entropy.bwd.{tag}", lambda tag=tag, r=rows, k=k: L.mh_cross_entropy_bwd_accum(
-                    p[f"g{tag}"], p[f"x{tag}"], p[f"t{tag}"], p[f"ug{tag}"], r, k), 16 * n + 4)]
+        ops += [(f"cross_entropy.fwd.{tag}", lambda P, tag=tag, r=rows, k=k: L.mh_cross_entropy_fwd(
+                    P[f"loss{tag}"], P[f"x{tag}"], P[f"t{tag}"], r, k), 8 * n + 4),
+                (f"cross_entropy.bwd.{tag}", lambda P, tag=tag, r=rows, k=k: L.mh_cross_entropy_bwd_accum(
+                    P[f"g{tag}"], P[f"x{tag}"], P[f"t{tag}"], P[f"ug{tag}"], r, k), 16 * n + 4)]
         if k == 1000:
             for nm, f, b in (("softmax", L.mh_softmax_fwd, L.mh_softmax_bwd_accum),
                              ("logsoftmax", L.mh_logsoftmax_fwd, L.mh_logsoftmax_bwd_accum)):
-                ops += [(f"{nm}.fwd.{tag}", lambda tag=tag, r=rows, k=k, f=f: f(p[f"o{tag}"], p[f"x{tag}"], r, k), 8 * n),
-                        (f"{nm}.bwd.{tag}", lambda tag=tag, r=rows, k=k, b=b: b(p[f"g{tag}"], p[f"x{tag}"], p[f"t{tag}"],
+                ops += [(f"{nm}.fwd.{tag}", lambda P, tag=tag, r=rows, k=k, f=f: f(P[f"o{tag}"], P[f"x{tag}"], r, k), 8 * n),
+                        (f"{nm}.bwd.{tag}", lambda P, tag=tag, r=rows, k=k, b=b: b(P[f"g{tag}"], P[f"x{tag}"], P[f"t{tag}"],
                                                                               r, k), 16 * n)]
     chk(L, L.mh_sync(), "sync")
-    med = time_ops(d, ops, reps)
+    for label, fn, _ in ops:  # real outputs and gradients in the copied sets
+        chk(L, fn(d.ptrs), label)
+    sets = replicate(d, bufs, min(b for _, _, b in ops))
+    med, iso = time_both(d, ops, sets, reps)
     d.free()
-    return op_report(ops, med)
+    return {"buffer_sets": len(sets), **op_report(ops, med, iso)}
 
 
 def run_graph(L, reps, steps=200):
@@ -628,13 +742,25 @@ def run_graph(L, reps, steps=200):
 
 
 def run_copy(L, reps):
+    """The library's copy kernel over 1 GiB (the practical streaming rate at the headline's
+    size) and over one tensor of config 3 and of config 5 (the practical rate at those sizes,
+    streamed and isolated like their ops), and the isolated method's floor."""
     d = Dev(L)
     n = 1 << 28
     src, dst = d.zeros("src", n), d.zeros("dst", n)
     ops = [("copy_1GiB", lambda: L.mh_memcpy_d2d(dst, src, 4 * n), 8 * n)]
     med = time_ops(d, ops, reps, flush=False)
+    out = op_report(ops, med)
+    for tag, m in (("copy_c3_tensor", 6422528), ("copy_c5_tensor", 10485760)):
+        d.zeros(f"s_{tag}", m)
+        d.zeros(f"d_{tag}", m)
+        small = [(tag, lambda P, tag=tag, m=m: L.mh_memcpy_d2d(P[f"d_{tag}"], P[f"s_{tag}"], 4 * m), 8 * m)]
+        sets = replicate(d, [(f"s_{tag}", m), (f"d_{tag}", m)], 8 * m)
+        sm, si = time_both(d, small, sets, reps)
+        out.update(op_report(small, sm, si))
+    out["isolated_floor_ms"] = isolated_floor(d, reps)
     d.free()
-    return op_report(ops, med)
+    return out
 
 
 # ---------------------------------------------------------------------------------------

@@ -248,6 +248,71 @@ __global__ void __launch_bounds__(kThreads)
     }
 }
 
+// Row-broadcast engine: output [rows, K] with K >= 4 and fewer than 2^31 elements, every
+// IN_BCAST operand a contiguous per-row vector ([rows, 1], as a row max or row sum is), the
+// output and FULL operands 16-byte aligned. One quad per thread: the quad's first row comes
+// from one fast division, and as K >= 4 at most one row boundary falls inside it, so a row
+// operand is read once, or twice where the quad crosses into the next row. kinds holds two
+// bits of InKind per operand. Element values are the same single operations as every engine.
+template <class F, int NIN, bool ACCUM>
+__global__ void __launch_bounds__(kThreads)
+    k_rowbc4(float* __restrict__ out, InPtrs<NIN> in, int kinds, int64_t n, uint32_t K, FastDiv fk, DevScal ds,
+             F f) {
+    constexpr int NA = NIN > 0 ? NIN : 1;
+    f.setup(ds);
+    float sv[NA];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) sv[k] = ((kinds >> (2 * k)) & 3) == IN_SCALAR ? in.p[k][0] : 0.0f;
+    const int64_t nq = n >> 2;
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
+        const uint32_t e0 = (uint32_t)(q << 2);
+        const uint32_t r0 = fdiv(e0, fk);
+        const uint32_t c0 = e0 - r0 * K;
+        const int jc = c0 + 3 >= K ? (int)(K - c0) : 4;  // first element of the quad in row r0 + 1
+        float v[4][NA];
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) {
+            const int kind = (kinds >> (2 * k)) & 3;
+            if (kind == IN_SCALAR) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j][k] = sv[k];
+            } else if (kind == IN_FULL) {
+                const vf4 t = reinterpret_cast<const vf4*>(in.p[k])[q];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j][k] = t[j];
+            } else {
+                const float a = in.p[k][r0];
+                const float b = jc < 4 ? in.p[k][r0 + 1] : a;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j][k] = j < jc ? a : b;
+            }
+        }
+        vf4 o = vf4{0.f, 0.f, 0.f, 0.f};
+        if (ACCUM) o = reinterpret_cast<const vf4*>(out)[q];
+        vf4 r;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float fv = f(v[j]);
+            r[j] = ACCUM ? o[j] + fv : fv;
+        }
+        reinterpret_cast<vf4*>(out)[q] = r;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        for (int64_t i = nq << 2; i < n; ++i) {
+            const int64_t row = i / (int64_t)K;
+            float v[NA];
+#pragma unroll
+            for (int k = 0; k < NIN; ++k) {
+                const int kind = (kinds >> (2 * k)) & 3;
+                v[k] = kind == IN_SCALAR ? sv[k] : (kind == IN_FULL ? in.p[k][i] : in.p[k][row]);
+            }
+            const float fv = f(v);
+            out[i] = ACCUM ? out[i] + fv : fv;
+        }
+    }
+}
+
 // Broadcast engine, 128-bit path: the output and every FULL operand stream as flat float4
 // quads whatever the shape (all must be 16-byte aligned); only the broadcast operands are
 // gathered, with 32-bit offsets below 2^31 elements and a decode loop bounded by MAXR.
@@ -474,6 +539,18 @@ static int run_map(float* out, const ElwPlan& pl, const float* const* ptrs, cons
         if (pl.kind[k] == IN_BCAST) al_b = al_b && aligned16(ptrs[k]);
     if (al) {
         dim3 g(grid_for(pl.n >> 2, kThreads)), b(kThreads);
+        bool rowform = !big && pl.rank == 2 && pl.dims[1] >= 4;  // [rows, K] with per-row operands
+        int kinds = 0;
+        for (int k = 0; k < NIN; ++k) {
+            if (pl.kind[k] == IN_BCAST && !(pl.st[k][0] == 1 && pl.st[k][1] == 0)) rowform = false;
+            kinds |= pl.kind[k] << (2 * k);
+        }
+        if (rowform) {
+            const uint32_t K = (uint32_t)pl.dims[1];
+            hipLaunchKernelGGL((k_rowbc4<F, NIN, ACCUM>), g, b, 0, st, out, in, kinds, pl.n, K, make_fastdiv(K), ds,
+                               f);
+            return MH_OK;
+        }
         const bool inner4 = pl.vec_ok && al_b;
         if (big) {  // 64-bit offsets, any rank
             if (inner4) hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, true, true, MH_MAX_RANK>), g, b, 0, st, out, in, pl, ds, f);

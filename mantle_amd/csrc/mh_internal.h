@@ -12,6 +12,10 @@
 
 namespace mh {
 
+// A float4 as a clang vector type: arrays and struct members of it stay in registers, where
+// HIP's union float4 can be put in scratch memory.
+typedef float vf4 __attribute__((ext_vector_type(4)));
+
 // ---------------------------------------------------------------------------------------
 // context
 // ---------------------------------------------------------------------------------------

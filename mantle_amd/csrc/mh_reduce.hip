@@ -1014,41 +1014,68 @@ int plan_unbroadcast(const mh_shape& sgrad, const mh_shape& srg, mh_reduce_plan_
 // the plane form of an un-broadcast, [N, C, S] -> [C] (a per-channel bias gradient), in one
 // launch
 // ---------------------------------------------------------------------------------------
-// One wavefront per (plane p = n * C + c, chunk k of QC quads): lanes sum their quads in
-// order, a butterfly adds the lanes, and the partial goes to part[(n * K + k) * C + c] with an
-// agent-scope store. The wave waits for the store, then takes a ticket on channel c's counter
-// (one per 128-byte line); the channel's last arrival sums its N * K partials in index order
-// (lane-strided, then a butterfly) and accumulates grad[c] (negated for SUB's operand 1), then
-// resets the counter. Used where the partials per channel are few enough for their tickets
-// not to queue (kPlanesMaxArrivals).
+// One wavefront per (channel c, group of G planes n = g * G .. g * G + G - 1, chunk k of QC
+// quads of each plane): lanes sum their quads of each plane in order, the planes in order
+// (two planes' loads in flight together), a butterfly adds the lanes, and the partial goes to
+// part[(g * K + k) * C + c] with an agent-scope store. The wave waits for the store, then
+// takes a ticket on channel c's counter (one per 128-byte line); the channel's last arrival
+// sums its NG * K partials in index order (lane-strided, then a butterfly) and accumulates
+// grad[c] (negated for SUB's operand 1), then resets the counter. G is chosen so that each
+// counter sees at most about kPlanesArrivals tickets: arrivals on one counter serialize.
 constexpr int64_t kPlanesTicketStride = 32;
+constexpr int64_t kPlanesArrivals = 64;
 constexpr int64_t kPlanesMaxArrivals = 4096;
 constexpr int64_t kPlanesMaxQuads = 1024;
 
 template <bool NEG>
 __global__ void __launch_bounds__(kRThreads)
-    k_unb_planes(float* __restrict__ grad, const float* __restrict__ rg, int64_t C, int64_t Sq, int64_t QC,
-                 int64_t K, int64_t nwaves, float* part, uint32_t* tickets) {
+    k_unb_planes(float* __restrict__ grad, const float* __restrict__ rg, int64_t N, int64_t C, int64_t Sq,
+                 int64_t QC, int64_t K, int64_t G, int64_t nwaves, float* part, uint32_t* tickets) {
     const int lane = threadIdx.x & 63;
     const int64_t v = (int64_t)blockIdx.x * (kRThreads / 64) + (threadIdx.x >> 6);
     if (v >= nwaves) return;  // uniform per wavefront; no barrier follows
-    const int64_t p = v / K, k = v - p * K;
-    const int64_t q0 = p * Sq + k * QC;
+    const int64_t c = v % C, gk = v / C;
+    const int64_t g = gk / K, k = gk - g * K;
     const int64_t rem = Sq - k * QC;
     const int64_t cnt = rem < QC ? rem : QC;
-    const float4* r4 = reinterpret_cast<const float4*>(rg);
+    const int64_t n0 = g * G, n1 = n0 + G < N ? n0 + G : N;
+    // the lane's quads lane + 64 u of a 256-quad step at `base`, added in order
+    auto add_step = [&](float a, const vf4 (&q)[4], int64_t base) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (base + lane + 64 * u < cnt) a = (((a + q[u].x) + q[u].y) + q[u].z) + q[u].w;
+        return a;
+    };
+    auto load_step = [&](vf4 (&q)[4], const vf4* r, int64_t base) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (base + lane + 64 * u < cnt) q[u] = r[base + lane + 64 * u];
+    };
+    auto add_rest = [&](float a, const vf4* r) {  // the plane's steps after the first
+        for (int64_t base = 256; base < cnt; base += 256) {
+            vf4 q[4];
+            load_step(q, r, base);
+            a = add_step(a, q, base);
+        }
+        return a;
+    };
     float acc = 0.0f;
-    for (int64_t i = lane; i < cnt; i += 64) {
-        const float4 q = r4[q0 + i];
-        acc = (((acc + q.x) + q.y) + q.z) + q.w;
+    for (int64_t n = n0; n < n1; n += 2) {  // planes in order; two planes' first steps in flight together
+        const bool two = n + 1 < n1;
+        const vf4* ra = reinterpret_cast<const vf4*>(rg) + (n * C + c) * Sq + k * QC;
+        const vf4* rb = ra + C * Sq;
+        vf4 qa[4], qb[4];
+        load_step(qa, ra, 0);
+        if (two) load_step(qb, rb, 0);
+        acc = add_rest(add_step(acc, qa, 0), ra);
+        if (two) acc = add_rest(add_step(acc, qb, 0), rb);
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
-    const int64_t n = p / C, c = p - n * C;
-    const int64_t nper = nwaves / C;  // partials per channel: N * K
+    const int64_t nper = nwaves / C;  // partials per channel: NG * K
     uint32_t ticket = 0;
     if (lane == 0) {
-        __hip_atomic_store(&part[(n * K + k) * C + c], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&part[gk * C + c], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_s_waitcnt(0);
         ticket = __hip_atomic_fetch_add(&tickets[c * kPlanesTicketStride], 1u, __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
@@ -1067,7 +1094,7 @@ __global__ void __launch_bounds__(kRThreads)
 }
 
 struct PlaneForm {
-    int64_t N, C, S, Sq, QC, K, nwaves;
+    int64_t N, C, S, Sq, QC, K, G, NG, nwaves;
 };
 
 // The plan [N*C, S, 1] then [1, N, C] with S a multiple of 4 and at least 64.
@@ -1080,8 +1107,11 @@ static bool plane_form(const mh_reduce_plan_info& p, PlaneForm* f) {
     f->Sq = f->S / 4;
     f->QC = f->Sq < kPlanesMaxQuads ? f->Sq : kPlanesMaxQuads;
     f->K = (f->Sq + f->QC - 1) / f->QC;
-    f->nwaves = f->N * f->C * f->K;
-    return f->N * f->K <= kPlanesMaxArrivals && (f->nwaves + 3) / 4 <= 0x7fffffff;
+    f->G = (f->N * f->K + kPlanesArrivals - 1) / kPlanesArrivals;  // planes per wave
+    if (f->G < 1) f->G = 1;
+    f->NG = (f->N + f->G - 1) / f->G;
+    f->nwaves = f->NG * f->K * f->C;
+    return f->NG * f->K <= kPlanesMaxArrivals && (f->nwaves + 3) / 4 <= 0x7fffffff;
 }
 
 size_t unbroadcast_scratch_floats(const mh_shape& sgrad, const mh_shape& srg) {
@@ -1098,7 +1128,7 @@ size_t unbroadcast_scratch_floats(const mh_shape& sgrad, const mh_shape& srg) {
     size_t need = pad(tmax) + 2 * pad(bmax) + 64;
     PlaneForm pf;
     if (plane_form(p, &pf)) {  // the one-launch plane form's partials
-        const size_t np = pad((size_t)(pf.N * pf.K * pf.C)) + 64;
+        const size_t np = pad((size_t)(pf.NG * pf.K * pf.C)) + 64;
         if (np > need) need = np;
     }
     return need;
@@ -1117,11 +1147,11 @@ int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* r
         MH_TRY(tickets(pf.C * kPlanesTicketStride, &tk));
         dim3 g((unsigned)((pf.nwaves + 3) / 4)), b(kRThreads);
         if (negate)
-            hipLaunchKernelGGL(k_unb_planes<true>, g, b, 0, ctx().stream, grad, rg, pf.C, pf.Sq, pf.QC, pf.K,
-                               pf.nwaves, tmp, tk);
+            hipLaunchKernelGGL(k_unb_planes<true>, g, b, 0, ctx().stream, grad, rg, pf.N, pf.C, pf.Sq, pf.QC, pf.K,
+                               pf.G, pf.nwaves, tmp, tk);
         else
-            hipLaunchKernelGGL(k_unb_planes<false>, g, b, 0, ctx().stream, grad, rg, pf.C, pf.Sq, pf.QC, pf.K,
-                               pf.nwaves, tmp, tk);
+            hipLaunchKernelGGL(k_unb_planes<false>, g, b, 0, ctx().stream, grad, rg, pf.N, pf.C, pf.Sq, pf.QC,
+                               pf.K, pf.G, pf.nwaves, tmp, tk);
         return MH_OK;
     }
     size_t tmax = 0, bmax = 0;

@@ -406,7 +406,6 @@ constexpr int kPQ = 4;  // float4 per thread per operand tile (q0..q3 below)
 
 // Four float4 of one operand tile per thread, as named registers (an array here ends up in
 // scratch memory).
-typedef float vf4 __attribute__((ext_vector_type(4)));
 struct TileRegs {
     vf4 q0, q1, q2, q3;
     float tail;

@@ -49,7 +49,7 @@ BIN_SHAPES = [((37, 63, 107), (37, 63, 107)), ((37, 63, 107), (37, 63, 1)), ((37
               ((4, 32, 7, 7), (1, 32, 1, 1)), ((4099, 10), (4099, 1)), ((8, 1, 5), (1, 6, 1)),
               ((3,), (3,)), ((1,), (1,)), ((7, 5), (5,)), ((2, 1, 3, 1, 5), (1, 4, 3, 6, 1)),
               ((5, 3), (5, 1)), ((7, 2), (1, 2)), ((9, 1, 3), (9, 4, 1)), ((1023, 6), (1023, 1)),
-              ((65, 4), (65, 1))]
+              ((65, 4), (65, 1)), ((1001, 5), (1001, 1)), ((6, 2, 13), (6, 2, 1))]
 
 
 def _binary_inputs(sa, sb, seed):
@@ -348,7 +348,8 @@ def test_fused_bias_relu_matches_op_by_op(gpu):
 
 
 FUSED_SHAPES = [((8, 32, 28, 28), (1, 32, 1, 1)), ((2, 3, 64), (3, 1)), ((5, 300), (5, 1)), ((4, 6, 96), (1,)),
-                ((3, 7, 10), (1, 7, 1)), ((64, 40), (1, 40)), ((2, 3, 4, 80), (1, 3, 4, 1)), ((3, 2, 20000), (1, 2, 1))]
+                ((3, 7, 10), (1, 7, 1)), ((64, 40), (1, 40)), ((2, 3, 4, 80), (1, 3, 4, 1)), ((3, 2, 20000), (1, 2, 1)),
+                ((100, 3, 64), (1, 3, 1)), ((33, 2, 5000), (1, 2, 1))]
 
 
 @pytest.mark.parametrize("sx,sb", FUSED_SHAPES, ids=[f"{a}+{b}" for a, b in FUSED_SHAPES])
