@@ -88,61 +88,84 @@ __global__ void __launch_bounds__(kFThreads)
     }
 }
 
-// Backward over [N, C, S] planes, S % 4 == 0. One wavefront per (plane, chunk): wave
-// v = blockIdx.x * 4 + wave covers chunk k = v % K of plane p = v / K (p = n * C + c), i.e.
-// quads [k * QC, min((k + 1) * QC, Sq)) of the plane, QC <= 1024 (<= 16 quads per lane).
+// Backward over [N, C, S] planes, S % 4 == 0. One wavefront per (channel c, group g of G
+// planes n = g * G .. g * G + G - 1, chunk k of QC quads of each plane, QC <= 1024), wave
+// v = blockIdx.x * 4 + wave with c = v % C, g * K + k = v / C; the planes in order, four quads
+// per lane in flight per stream:
 //   rg = (y > 0 ? 1 : 0) * ug            RELU.backward (mlops.mojo:118-123)
 //   g  = g_y + rg  (0 + rg without g_y)  accumulate_grad into the grad of y (ops.mojo:405)
 //   grad_x = grad_x + g                  ADD backward_op, operand 0 (ops.mojo:457-461)
-//   part[(n * K + k) * C + c] = sum of g over the chunk: each lane sums its quads in order,
-//   then a butterfly across the wave.
+//   part[(g * K + k) * C + c] = sum of g over the wave's quads: each lane sums its quads in
+//   order, plane by plane, then a butterfly across the wave.
 // The bias gradient (ADD's operand-1 un-broadcast) completes in the same launch: every wave
 // publishes its partial with an agent-scope store, waits for that store to complete, then
 // takes a ticket on its channel; the wave that takes the channel's last ticket reads the
-// channel's N * K partials with agent-scope loads, adds them in a fixed order into
-// grad_bias[c] and resets the ticket. No wave waits for another.
+// channel's NG * K partials with agent-scope loads, adds them in a fixed order into
+// grad_bias[c] and resets the ticket. No wave waits for another. G keeps the tickets per
+// channel counter near kArrivals (arrivals on one counter serialize).
+constexpr int64_t kArrivals = 64;
+
 template <bool HAS_GY, bool HAS_GX, bool HAS_PART>
 __global__ void __launch_bounds__(kFThreads)
     k_bias_relu_bwd_planes(float* __restrict__ gy, float* __restrict__ gx, const float* __restrict__ y,
-                           const float* __restrict__ ug, int64_t C, int64_t Sq, int64_t QC, int64_t K,
-                           int64_t nwaves, float* part, uint32_t* tickets, float* grad_bias) {
+                           const float* __restrict__ ug, int64_t N, int64_t C, int64_t Sq, int64_t QC, int64_t K,
+                           int64_t G, int64_t nwaves, float* part, uint32_t* tickets, float* grad_bias) {
     const int lane = threadIdx.x & 63;
     const int64_t v = (int64_t)blockIdx.x * (kFThreads / 64) + (threadIdx.x >> 6);
     if (v >= nwaves) return;  // uniform per wavefront; no barrier follows
-    const int64_t p = v / K, k = v - p * K;
-    const int64_t q0 = p * Sq + k * QC;
+    const int64_t c = v % C, gk = v / C;
+    const int64_t g = gk / K, k = gk - g * K;
     const int64_t rem = Sq - k * QC;
     const int64_t cnt = rem < QC ? rem : QC;
+    const int64_t n0 = g * G, n1 = n0 + G < N ? n0 + G : N;
+    constexpr int U = 4;
+    const vf4* y4 = reinterpret_cast<const vf4*>(y);
+    const vf4* u4 = reinterpret_cast<const vf4*>(ug);
+    vf4* gy4 = reinterpret_cast<vf4*>(gy);
+    vf4* gx4 = reinterpret_cast<vf4*>(gx);
     float acc = 0.0f;
-    for (int64_t i = lane; i < cnt; i += 64) {
-        const int64_t q = q0 + i;
-        const float4 yv = reinterpret_cast<const float4*>(y)[q];
-        const float4 uv = reinterpret_cast<const float4*>(ug)[q];
-        float4 gv = make_float4(0.f, 0.f, 0.f, 0.f), xv = gv;
-        if (HAS_GY) gv = reinterpret_cast<const float4*>(gy)[q];
-        if (HAS_GX) xv = reinterpret_cast<const float4*>(gx)[q];
-        float g[4], o[4];
+    for (int64_t n = n0; n < n1; ++n) {
+        const int64_t q0 = (n * C + c) * Sq + k * QC;
+        for (int64_t base = 0; base < cnt; base += 64 * U) {  // the lane's quads in ascending order
+            vf4 yv[U], uv[U], gv[U], xv[U];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float rg = (comp(yv, j) > 0.0f ? 1.0f : 0.0f) * comp(uv, j);
-            g[j] = comp(gv, j) + rg;
-            o[j] = comp(xv, j) + g[j];
+            for (int u = 0; u < U; ++u) {
+                const int64_t i = base + lane + 64 * u;
+                gv[u] = xv[u] = vf4{0.f, 0.f, 0.f, 0.f};
+                if (i < cnt) {
+                    yv[u] = y4[q0 + i];
+                    uv[u] = u4[q0 + i];
+                    if (HAS_GY) gv[u] = gy4[q0 + i];
+                    if (HAS_GX) xv[u] = gx4[q0 + i];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t i = base + lane + 64 * u;
+                if (i >= cnt) continue;
+                vf4 gg, o;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float rg = (yv[u][j] > 0.0f ? 1.0f : 0.0f) * uv[u][j];
+                    gg[j] = gv[u][j] + rg;
+                    o[j] = xv[u][j] + gg[j];
+                }
+                if (HAS_GY) gy4[q0 + i] = gg;
+                if (HAS_GX) gx4[q0 + i] = o;
+                if (HAS_PART) acc = (((acc + gg[0]) + gg[1]) + gg[2]) + gg[3];
+            }
         }
-        if (HAS_GY) reinterpret_cast<float4*>(gy)[q] = make_float4(g[0], g[1], g[2], g[3]);
-        if (HAS_GX) reinterpret_cast<float4*>(gx)[q] = make_float4(o[0], o[1], o[2], o[3]);
-        if (HAS_PART) acc = (((acc + g[0]) + g[1]) + g[2]) + g[3];
     }
     if (HAS_PART) {
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
-        const int64_t n = p / C, c = p - n * C;
-        const int64_t nper = nwaves / C;  // partials per channel: N * K
+        const int64_t nper = nwaves / C;  // partials per channel: NG * K
         uint32_t ticket = 0;
         if (lane == 0) {
             // The partial is an agent-scope store (coherent across XCDs by itself), so the
             // ticket needs only to follow its completion, not a release of every earlier
             // store (which would write back this XCD's whole L2 once per wave).
-            __hip_atomic_store(&part[(n * K + k) * C + c], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&part[gk * C + c], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __builtin_amdgcn_s_waitcnt(0);
             ticket = __hip_atomic_fetch_add(&tickets[c * kTicketStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -245,23 +268,25 @@ int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const fl
     // planes of at least 64 elements (16 quads), so that a block has work for its waves
     const bool planes = al && plane_form(pl, &N, &C, &S) && S % 4 == 0 && S >= 64;
     const int64_t Sq = S / 4;
-    const int64_t QC = Sq < 1024 ? Sq : 1024;  // quads per wavefront
+    const int64_t QC = Sq < 1024 ? Sq : 1024;  // quads per plane chunk
     const int64_t K = planes ? (Sq + QC - 1) / QC : 0;
-    const int64_t nwaves = N * C * K;
+    const int64_t G = planes ? (N * K + kArrivals - 1) / kArrivals : 0;  // planes per wavefront
+    const int64_t NG = planes ? (N + G - 1) / G : 0;
+    const int64_t nwaves = NG * K * C;
     const int64_t nblocks = (nwaves + 3) / 4;
     if (planes && nblocks <= 0x7fffffff) {
         float* part = nullptr;
         uint32_t* tk = nullptr;
         const bool has_part = grad_bias != nullptr;
         if (has_part) {
-            MH_TRY(scratch(((size_t)(N * K * C) + 64) * sizeof(float), reinterpret_cast<void**>(&part)));
+            MH_TRY(scratch(((size_t)nwaves + 64) * sizeof(float), reinterpret_cast<void**>(&part)));
             MH_TRY(tickets(C * kTicketStride, &tk));
         }
         hipStream_t st = ctx().stream;
         dim3 g((unsigned)nblocks), b(kFThreads);
-#define MH_BRB(GY, GX, PT)                                                                                  \
-    hipLaunchKernelGGL((k_bias_relu_bwd_planes<GY, GX, PT>), g, b, 0, st, g_y, grad_x, y, ug, C, Sq, QC, K, nwaves, \
-                       part, tk, grad_bias)
+#define MH_BRB(GY, GX, PT)                                                                                       \
+    hipLaunchKernelGGL((k_bias_relu_bwd_planes<GY, GX, PT>), g, b, 0, st, g_y, grad_x, y, ug, N, C, Sq, QC, K, G, \
+                       nwaves, part, tk, grad_bias)
         const int sel = (g_y ? 4 : 0) | (grad_x ? 2 : 0) | (has_part ? 1 : 0);
         switch (sel) {
             case 0: return MH_OK;  // nothing to produce
