@@ -4,10 +4,12 @@
 // read-modify-written for "grad = grad + rg") and up to four input streams, each FULL (same
 // shape as the output), SCALAR (one element, loaded once per thread) or BCAST (strided in the
 // collapsed output space). Same-shape work takes the float4 path: 256-thread blocks, one
-// 128-bit access per stream per thread, all loads issued before any arithmetic. Broadcast work
-// decodes the output coordinate of each quad with precomputed fast divisors; an inner
-// dimension divisible by 4 keeps 128-bit accesses for every operand whose inner stride is 0
-// or 1.
+// 128-bit access per stream per thread, all loads issued before any arithmetic. Two common
+// broadcast forms of a [rows, K] output have engines of their own: per-row operands ([rows, 1],
+// K >= 4: one fast division per quad) and per-column operands ([1, K], K % 4 == 0: one fast
+// modulo per quad). Other broadcasts decode the output coordinate of each quad with
+// precomputed fast divisors; an inner dimension divisible by 4 keeps 128-bit accesses for
+// every operand whose inner stride is 0 or 1.
 #include "mh_internal.h"
 #include "mh_math.h"
 
@@ -313,6 +315,46 @@ __global__ void __launch_bounds__(kThreads)
     }
 }
 
+// Column-broadcast engine: output [rows, C] with C % 4 == 0 and fewer than 2^31 elements,
+// every IN_BCAST operand a contiguous per-column vector ([1, C], as a column max or a bias
+// is), all operands and the output 16-byte aligned. One quad per thread in flat order (one
+// sequential stream, as for same-shape operands); the quad's column quad is q mod C/4 (one
+// fast division), whose operand quads are small enough to stay in L2.
+template <class F, int NIN, bool ACCUM>
+__global__ void __launch_bounds__(kThreads)
+    k_colbc4(float* __restrict__ out, InPtrs<NIN> in, int kinds, int64_t nq, uint32_t Cq, FastDiv fcq, DevScal ds,
+             F f) {
+    constexpr int NA = NIN > 0 ? NIN : 1;
+    f.setup(ds);
+    float sv[NA];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) sv[k] = ((kinds >> (2 * k)) & 3) == IN_SCALAR ? in.p[k][0] : 0.0f;
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
+        const uint32_t cq = (uint32_t)q - fdiv((uint32_t)q, fcq) * Cq;
+        vf4 t[NA];
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) {
+            const int kind = (kinds >> (2 * k)) & 3;
+            if (kind == IN_FULL) t[k] = reinterpret_cast<const vf4*>(in.p[k])[q];
+            else if (kind == IN_BCAST) t[k] = reinterpret_cast<const vf4*>(in.p[k])[cq];
+            else t[k] = vf4{sv[k], sv[k], sv[k], sv[k]};
+        }
+        vf4 o = vf4{0.f, 0.f, 0.f, 0.f};
+        if (ACCUM) o = reinterpret_cast<const vf4*>(out)[q];
+        vf4 r;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float v[NA];
+#pragma unroll
+            for (int k = 0; k < NIN; ++k) v[k] = t[k][j];
+            const float fv = f(v);
+            r[j] = ACCUM ? o[j] + fv : fv;
+        }
+        reinterpret_cast<vf4*>(out)[q] = r;
+    }
+}
+
 // Broadcast engine, 128-bit path: the output and every FULL operand stream as flat float4
 // quads whatever the shape (all must be 16-byte aligned); only the broadcast operands are
 // gathered, with 32-bit offsets below 2^31 elements and a decode loop bounded by MAXR.
@@ -549,6 +591,16 @@ static int run_map(float* out, const ElwPlan& pl, const float* const* ptrs, cons
             const uint32_t K = (uint32_t)pl.dims[1];
             hipLaunchKernelGGL((k_rowbc4<F, NIN, ACCUM>), g, b, 0, st, out, in, kinds, pl.n, K, make_fastdiv(K), ds,
                                f);
+            return MH_OK;
+        }
+        // [rows, C] with per-column operands ([1, C]), C % 4 == 0
+        bool colform = !big && pl.rank == 2 && pl.dims[1] % 4 == 0 && al_b;
+        for (int k = 0; k < NIN; ++k)
+            if (pl.kind[k] == IN_BCAST && !(pl.st[k][0] == 0 && pl.st[k][1] == 1)) colform = false;
+        if (colform) {
+            const uint32_t Cq = (uint32_t)(pl.dims[1] / 4);
+            hipLaunchKernelGGL((k_colbc4<F, NIN, ACCUM>), g, b, 0, st, out, in, kinds, pl.n >> 2, Cq, make_fastdiv(Cq),
+                               ds, f);
             return MH_OK;
         }
         const bool inner4 = pl.vec_ok && al_b;
