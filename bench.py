@@ -239,7 +239,11 @@ def isolated_floor(d, reps):
     return round(med["floor"], 4)
 
 
-def op_report(ops, med, iso=None):
+def op_report(ops, med, iso=None, hbm=None):
+    """Per op: ms, GB/s and frac of its algorithmic bytes; with `iso`, the isolated figures;
+    with `hbm` ({label: bytes}), the bytes the op moves where they are fewer than the
+    algorithmic count (a sparse accumulation that stores only the quads it changes) and the
+    rate of those bytes."""
     out = {}
     for label, _, nbytes in ops:
         t = med[label]
@@ -249,6 +253,9 @@ def op_report(ops, med, iso=None):
             ti = iso[label]
             out[label]["ms_isolated"] = round(ti, 4)
             out[label]["frac_isolated"] = round(nbytes / (ti * 1e-3) / 1e9 / PEAK_GBS, 4)
+        if hbm and label in hbm:
+            hg = hbm[label] / (t * 1e-3) / 1e9
+            out[label].update({"hbm_bytes": hbm[label], "GB/s_hbm": round(hg, 1), "frac_hbm": round(hg / PEAK_GBS, 4)})
     return out
 
 
@@ -397,7 +404,7 @@ def run_c4(L, reps):
     from mantle_amd import synth
     from mantle_amd._lib import make_shape
     d = Dev(L)
-    ops, bufs = [], []
+    ops, bufs, hbm = [], [], {}
     cases = [("8192x8192", (8192, 8192), 0, "n"), ("8192x8192", (8192, 8192), 1, "n"),
              ("8192x8192", (8192, 8192), -1, "n"), ("64x512x1024", (64, 512, 1024), 2, "u")]
     for tag, shape, axis, dist in cases:
@@ -423,6 +430,10 @@ def run_c4(L, reps):
             ops.append((f"{tag}.{ax}.{op}.fwd",
                         lambda P, o=o, name=name, s=s, axis=axis: L.mh_reduce_fwd(o, P[f"res_{name}"], P[name], s, axis),
                         4 * n + 4 * m))
+        # MAX backward reads x (twice where the line max is a separate pass: axis 0, all) and
+        # grad, and stores only the grad quads that hold a line maximum (at most m of them)
+        two_pass = axis in (0, -1)
+        hbm[f"{tag}.{ax}.MAX.bwd"] = (12 * n if two_pass else 8 * n) + 4 * m + 16 * m
         for op in ("SUM", "MEAN", "MAX"):
             o = OP_ID[op]
             nb = (12 * n + 8 * m) if op == "MAX" else (8 * n + 4 * m)
@@ -435,7 +446,7 @@ def run_c4(L, reps):
     d.free()
     fwd = [o for o in ops if o[0].endswith(".fwd")]
     bwd = [o for o in ops if o[0].endswith(".bwd")]
-    return {"buffer_sets": len(sets), "ops": op_report(ops, med, iso), "fwd_total": total_report(fwd, med, iso),
+    return {"buffer_sets": len(sets), "ops": op_report(ops, med, iso, hbm), "fwd_total": total_report(fwd, med, iso),
             "bwd_total": total_report(bwd, med, iso)}
 
 

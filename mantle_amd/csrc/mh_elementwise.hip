@@ -143,6 +143,14 @@ struct FMaxRoute {
     __device__ float operator()(const float* v) const { return v[0] == v[1] ? v[2] * v[3] : 0.0f; }
 };
 
+// Accumulating functors whose contribution is +0 almost everywhere: the engines store a quad
+// only when its bits change (bits_differ4), which leaves memory exactly as storing every quad
+// would, without writing back the untouched ones.
+template <class F>
+constexpr bool kSparseAccum = false;
+template <>
+constexpr bool kSparseAccum<FMaxRoute> = true;
+
 struct FFma {  // FMA.forward, basics.mojo:782-786: t1.fma(t2, t3), a single rounding
     __device__ void setup(const DevScal&) {}
     __device__ float operator()(const float* v) const { return __builtin_fmaf(v[0], v[1], v[2]); }
@@ -219,6 +227,7 @@ __global__ void __launch_bounds__(kThreads)
             r[j] = f(v);
             if (ACCUM) r[j] = comp(ov, j) + r[j];
         }
+        if (ACCUM && kSparseAccum<F> && !bits_differ4(ov.x, ov.y, ov.z, ov.w, r[0], r[1], r[2], r[3])) continue;
         reinterpret_cast<float4*>(out)[q] = make_float4(r[0], r[1], r[2], r[3]);
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
@@ -298,6 +307,7 @@ __global__ void __launch_bounds__(kThreads)
             const float fv = f(v[j]);
             r[j] = ACCUM ? o[j] + fv : fv;
         }
+        if (ACCUM && kSparseAccum<F> && !bits_differ4(o[0], o[1], o[2], o[3], r[0], r[1], r[2], r[3])) continue;
         reinterpret_cast<vf4*>(out)[q] = r;
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
@@ -351,6 +361,7 @@ __global__ void __launch_bounds__(kThreads)
             const float fv = f(v);
             r[j] = ACCUM ? o[j] + fv : fv;
         }
+        if (ACCUM && kSparseAccum<F> && !bits_differ4(o[0], o[1], o[2], o[3], r[0], r[1], r[2], r[3])) continue;
         reinterpret_cast<vf4*>(out)[q] = r;
     }
 }
@@ -451,6 +462,7 @@ __global__ void __launch_bounds__(kThreads)
             r[j] = f(v[j]);
             if (ACCUM) r[j] = comp(o, j) + r[j];
         }
+        if (ACCUM && kSparseAccum<F> && !bits_differ4(o.x, o.y, o.z, o.w, r[0], r[1], r[2], r[3])) continue;
         reinterpret_cast<float4*>(out)[q] = make_float4(r[0], r[1], r[2], r[3]);
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {

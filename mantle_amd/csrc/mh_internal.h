@@ -129,6 +129,16 @@ __device__ __forceinline__ float comp(const float4& q, int j) {
     return j == 0 ? q.x : (j == 1 ? q.y : (j == 2 ? q.z : q.w));
 }
 
+// True when some element of quad b differs in its bits from the same element of quad a, so
+// that storing b over a changes memory. Sparse accumulations store only such quads: MAX
+// backward adds +0 away from the line maxima, and x + 0 has the bits of x unless x is -0 (then
+// +0) or a signalling NaN (then quieted), both of which this test catches.
+__device__ __forceinline__ bool bits_differ4(float a0, float a1, float a2, float a3, float b0, float b1, float b2,
+                                             float b3) {
+    return ((__float_as_uint(a0) ^ __float_as_uint(b0)) | (__float_as_uint(a1) ^ __float_as_uint(b1)) |
+            (__float_as_uint(a2) ^ __float_as_uint(b2)) | (__float_as_uint(a3) ^ __float_as_uint(b3))) != 0u;
+}
+
 // Offset type of the broadcast engine: 32-bit below 2^31 output elements (every operand is
 // no larger than the output, so its offsets fit too).
 template <bool BIG>

@@ -341,7 +341,7 @@ __global__ void __launch_bounds__(kRThreads)
     const int nq = cnt >> 2;
     float4* g4 = reinterpret_cast<float4*>(grad + base);
     for (int i = t; i < nq; i += kRThreads) {
-        float4 g = g4[i];
+        const float4 o = g4[i];
         float r[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -349,11 +349,8 @@ __global__ void __launch_bounds__(kRThreads)
             const int row = (int)fdiv((uint32_t)e, fdB);
             r[j] = tile[e] == sm[row] ? sg[row] : 0.0f;
         }
-        g.x = g.x + r[0];
-        g.y = g.y + r[1];
-        g.z = g.z + r[2];
-        g.w = g.w + r[3];
-        g4[i] = g;
+        const float4 g = make_float4(o.x + r[0], o.y + r[1], o.z + r[2], o.w + r[3]);
+        if (bits_differ4(o.x, o.y, o.z, o.w, g.x, g.y, g.z, g.w)) g4[i] = g;  // a sparse accumulation
     }
     for (int e = (nq << 2) + t; e < cnt; e += kRThreads) {
         const int row = (int)fdiv((uint32_t)e, fdB);
@@ -626,12 +623,10 @@ __global__ void __launch_bounds__(kRThreads)
     for (int k = 0; k < NQ; ++k) {
         const int64_t qi = tr + (int64_t)k * NT;
         if (qi < Bq) {
-            float4 o = g4[qi];
-            o.x = o.x + (v[k].x == m ? g : 0.0f);
-            o.y = o.y + (v[k].y == m ? g : 0.0f);
-            o.z = o.z + (v[k].z == m ? g : 0.0f);
-            o.w = o.w + (v[k].w == m ? g : 0.0f);
-            g4[qi] = o;
+            const float4 o = g4[qi];
+            const float4 n = make_float4(o.x + (v[k].x == m ? g : 0.0f), o.y + (v[k].y == m ? g : 0.0f),
+                                         o.z + (v[k].z == m ? g : 0.0f), o.w + (v[k].w == m ? g : 0.0f));
+            if (bits_differ4(o.x, o.y, o.z, o.w, n.x, n.y, n.z, n.w)) g4[qi] = n;  // a sparse accumulation
         }
     }
 }

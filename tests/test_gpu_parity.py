@@ -215,6 +215,35 @@ def test_reduce_fwd_bwd_parity(gpu, shape, axis):
         assert_bitexact(got, ORC.backward(0, OPS[name], ug, x, axis=axis, grad=g0), f"{name} bwd")
 
 
+MAX_SPARSE_CASES = [((1024, 1024), 0), ((4099, 10), 1), ((300, 20), 1), ((64, 512), 1), ((9, 2052), 1),
+                    ((87, 73, 107), None), ((87, 73, 107), 1), ((4, 8, 1024), 0), ((2, 5000, 132), 1)]
+
+
+@pytest.mark.parametrize("shape,axis", MAX_SPARSE_CASES, ids=[f"{s}-ax{a}" for s, a in MAX_SPARSE_CASES])
+def test_max_backward_sparse_stores_keep_every_bit(gpu, shape, axis):
+    """MAX backward stores only the quads whose bits change (it adds +0 away from the line
+    maxima). The gradient it accumulates into holds -0 (which + 0 turns into +0, so those
+    quads must be stored), +0 and NaN away from the maxima: bit-exact against the oracle on
+    every routing path (column, short-row, register-row, all-element and generic forms)."""
+    x = synth.normal(shape, 0, 1, 710)
+    if axis is not None and shape[axis] > 1:
+        synth.inject_ties(x, axis, 711)
+    else:
+        x.reshape(-1)[x.size // 2] = x.max()
+    red_shape = (1,) if axis is None else tuple(1 if i == axis else d for i, d in enumerate(shape))
+    ug = synth.normal(red_shape, 0, 1, 712)
+    g0 = synth.normal(shape, 0, 1, 713).reshape(-1)
+    g0[::3] = np.float32(-0.0)
+    g0[1::7] = np.float32(0.0)
+    g0[2::11] = np.float32(np.nan)
+    g0 = g0.reshape(shape)
+    got = gpu.backward(0, OPS["MAX"], ug, x, axis=axis, grad=g0)
+    ref = ORC.backward(0, OPS["MAX"], ug, x, axis=axis, grad=g0)
+    assert_bitexact(got, ref, "MAX bwd")  # bits, so the sign of every zero too
+    r3 = ref.reshape(-1)[::3]
+    assert ((r3 == 0) & ~np.signbit(r3)).any(), "no -0 turned into +0: the case is not exercised"
+
+
 def test_reductions_are_deterministic(gpu):
     m = gpu.m
     x = gpu.T(synth.normal((4096, 4096), 0, 1, 710))
