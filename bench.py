@@ -878,6 +878,47 @@ C2_KERNEL = {"ADD.bwd": "void mh::k_bwd2_same4<0>", "SUB.bwd": "void mh::k_bwd2_
              "POW.bwd_exp": "void mh::k_rows_wave<mh::RSum, mh::LdPowGrad,"}
 
 
+# workload kernels for the traffic table: (op, kernel-name prefix, launch grid in threads,
+# algorithmic bytes of the kernel, note)
+_N3, _N4, _N5 = 6422528, 1 << 26, 10485760
+WL_KERNELS = [
+    ("c3 bias_relu.fwd (fused)", "void mh::k_bias_relu_fwd4<true, false>", 1605632, 12 * _N3 + 128, ""),
+    ("c3 bias_relu.bwd (fused)", "void mh::k_bias_relu_bwd_planes<false, true, true>", 131072, 16 * _N3 + 256,
+     "grad_x read and written, bias gradient in the same launch"),
+    ("c3 ADD.bwd_bias", "void mh::k_unb_planes<false>", 131072, 4 * _N3 + 256, "one launch, arrival tickets"),
+    ("c4 [8192,8192] axis 0 MAX.fwd", "void mh::k_cols<mh::RMax, mh::LdPlain<mh::RMax>, true>", 131072,
+     4 * _N4, "first of two launches (split partials)"),
+    ("c4 [8192,8192] axis 0 MAX.bwd, route", "void mh::k_colbc4<mh::FMaxRoute, 4, true>", 16777216, 12 * _N4,
+     "stores only quads holding a line maximum"),
+    ("c4 [8192,8192] axis 0 SUM.bwd", "void mh::k_colbc4<mh::FScaleBcast<false>, 1, true>", 16777216, 8 * _N4, ""),
+    ("c4 [8192,8192] axis 1 MAX.bwd", "void mh::k_max_bwd_rowreg<4, 8>", 2097152, 12 * _N4,
+     "one pass; stores only quads holding a line maximum"),
+    ("c4 [8192,8192] all MAX.bwd, route", "void mh::k_same4<mh::FMaxRoute, 4, true>", 16777216, 12 * _N4,
+     "stores only quads holding the maximum"),
+    ("c4 [64,512,1024] axis 2 MAX.bwd", "void mh::k_max_bwd_rowreg<1, 4>", 2097152, 12 * (1 << 25),
+     "one pass; stores only quads holding a line maximum"),
+    ("c5 SUB.fwd [N,10] - [N,1]", "void mh::k_rowbc4<mh::FBin<1>, 2, false>", 2621440, 8 * _N5 + 4 * (_N5 // 10), ""),
+    ("c5 DIV.bwd0", "void mh::k_rowbc4<mh::FBinRg<3, 0, false>, 2, true>", 2621440, 12 * _N5 + 4 * (_N5 // 10), ""),
+    ("c5 MAX.bwd (rows of 10)", "void mh::k_max_bwd_rows<16>", 1048576, 12 * _N5 + 8 * (_N5 // 10),
+     "stores only quads holding a row maximum (most quads, at 10 classes)"),
+    ("c5 fused head forward", "void mh::k_rowp_fwd<0, 16>", 262144, 8 * _N5, "logits and targets read once"),
+    ("c5 fused head backward", "void mh::k_rowp_bwd<0, 16>", 196608, 16 * _N5, ""),
+    ("CrossEntropy [32768,1000] backward", "void mh::k_roww_bwd<1, true, 16>", 2097152, 16 * 32768000, ""),
+]
+
+
+# (workload, group, op label, kernel-name prefix) of single-shape workload kernels whose
+# rocprofv3 duration the stats summary sets beside the bench's figures
+WL_STATS = [("c3", "op_by_op", "ADD.bwd_bias", "void mh::k_unb_planes<false>"),
+            ("c3", "fused", "bias_relu.fwd", "void mh::k_bias_relu_fwd4<true, false>"),
+            ("c3", "fused", "bias_relu.bwd", "void mh::k_bias_relu_bwd_planes<false, true, true>"),
+            ("c4", "ops", "8192x8192.ax1.MAX.bwd", "void mh::k_max_bwd_rowreg<4, 8>"),
+            ("c5", "fused", "fused.fwd", "void mh::k_rowp_fwd<0, 16>"),
+            ("c5", "fused", "fused.bwd", "void mh::k_rowp_bwd<0, 16>"),
+            ("c5", "fwd", "SUB.fwd", "void mh::k_rowbc4<mh::FBin<1>, 2, false>"),
+            ("c5", "fwd", "DIV.fwd", "void mh::k_rowbc4<mh::FBin<3>, 2, false>")]
+
+
 def stats_summary(stats_csv, command, bench_json=None):
     """Writes profiles/bench_kernel_stats.md from a rocprofv3 --kernel-trace --stats
     kernel_stats.csv (durations in microseconds), with the command that made it."""
@@ -908,6 +949,22 @@ def stats_summary(stats_csv, command, bench_json=None):
             lines.append(f"rocprofv3 averages `{match[0]['Name'].split('(')[0]}` at {avg:.1f} us over its "
                          f"{match[0]['Calls']} launches (the table above), {abs(avg - ev) / ev * 100:.1f} % from the "
                          f"event timing.")
+        wl = json.load(open(bench_json)).get("workloads", {})
+        rows_cmp = []
+        for w, group, label, prefix in WL_STATS:
+            rec = wl.get(w, {}).get(group, {}).get(label)
+            match = [r for r in rows if r["Name"].startswith(prefix)]
+            if rec and len(match) == 1:
+                avg = float(match[0]["AverageNs"]) / 1e3
+                rows_cmp.append(f"| {w} {label} | `{prefix.replace('void ', '')}` | {avg:.2f} | {rec['ms'] * 1e3:.2f} | "
+                                f"{rec['ms_isolated'] * 1e3:.2f} |")
+        if rows_cmp:
+            lines += ["", "## Workload kernels: rocprofv3 against the bench's two timings", "",
+                      "A kernel of one launch shape in the bench: rocprofv3's average duration, the bench's streamed "
+                      "figure (launches back to back over rotating cold buffers, elapsed / launches) and its isolated "
+                      "one (a single launch between two events after a cache flush).", "",
+                      "| Op | Kernel | rocprofv3 avg us | streamed us | isolated us |", "|---|---|---:|---:|---:|",
+                      *rows_cmp]
     os.makedirs(os.path.dirname(TRAFFIC_JSON), exist_ok=True)
     with open(os.path.join(os.path.dirname(TRAFFIC_JSON), "bench_kernel_stats.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
@@ -935,6 +992,18 @@ def traffic_summary_md(commands):
         short = k.split("(")[0].replace("void ", "")
         lines.append(f"| {label} | `{short}` | {(v['fetch_bytes'] or 0) / 1e9:.3f} | {(v['write_bytes'] or 0) / 1e9:.3f} | "
                      f"{v['hbm_bytes'] / 1e9:.3f} | {alg[label] * 2 ** 28 / 1e9:.3f} |")
+    lines += ["", "Workload kernels (the launch of the named shape; algorithmic bytes of that kernel: inputs read "
+              "once, outputs written once, accumulators read and written):", "",
+              "| Workload op | Kernel | Fetch GB | Write GB | HBM GB | Algorithmic GB | Note |",
+              "|---|---|---:|---:|---:|---:|---|"]
+    for label, key, grid, nbytes, note in WL_KERNELS:
+        hits = [v for k, v in t["kernels"].items() if k.startswith(key) and str(grid) in v["by_grid"]]
+        if len(hits) != 1:
+            continue
+        v = hits[0]["by_grid"][str(grid)]
+        short = key.replace("void ", "")
+        lines.append(f"| {label} | `{short}` | {(v['fetch_bytes'] or 0) / 1e9:.4f} | {(v['write_bytes'] or 0) / 1e9:.4f} | "
+                     f"{v['hbm_bytes'] / 1e9:.4f} | {nbytes / 1e9:.4f} | {note} |")
     with open(os.path.join(os.path.dirname(TRAFFIC_JSON), "traffic.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
 
