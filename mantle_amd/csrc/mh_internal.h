@@ -189,7 +189,6 @@ enum Epi : int {
     EPI_MEAN = 1,      // out = v / (float)len
     EPI_ACCUM = 2,     // out = out + v
     EPI_ACCUM_NEG = 3,  // out = out + (-v)
-    EPI_STD = 4,        // out = sqrt(v / (float)len)
     EPI_SCALE = 5       // out = v * div
 };
 // Reduce x viewed as [A, B, C] over B into out[A*C] (out2: fl(1/count) for RED_MAXCNT).

@@ -105,46 +105,6 @@ struct LdPowGrad {
     }
 };
 
-// tstd's second pass (tensorutils.mojo:724-741, 776-840): (x - mu) * (x - mu) with mu the
-// mean of the element's line. Element i of [A, B, C] (reduced over B) is on line
-// (i / (B*C)) * C + i % C; BIG = false divides with 32-bit fast divisors.
-template <bool BIG>
-struct LdSqDev {
-    const float* x;
-    const float* mu;
-    int64_t BC, C;
-    FastDiv fbc, fc;
-    __device__ void setup() {}
-    __device__ int64_t line(int64_t i) const {
-        if constexpr (BIG) {
-            return (i / BC) * C + i % C;
-        } else {
-            const uint32_t u = (uint32_t)i;
-            const uint32_t c = u - fdiv(u, fc) * (uint32_t)C;
-            return (int64_t)fdiv(u, fbc) * C + c;
-        }
-    }
-    __device__ float term(int64_t i, float xv) const {
-        const float d = xv - mu[line(i)];
-        return d * d;
-    }
-    __device__ float get(int64_t i) const { return term(i, x[i]); }
-    // A vector quad lies in one row (C == 1: one line) or across four columns (C % 4 == 0:
-    // four consecutive lines, a 16-byte aligned run of mu), so its lines take one division.
-    __device__ void get4(int64_t i, float* o) const {
-        const float4 q = *reinterpret_cast<const float4*>(x + i);
-        const int64_t l = line(i);
-        float4 m;
-        if (C == 1) m = make_float4(mu[l], mu[l], mu[l], mu[l]);
-        else m = *reinterpret_cast<const float4*>(mu + l);
-        float d;
-        d = q.x - m.x; o[0] = d * d;
-        d = q.y - m.y; o[1] = d * d;
-        d = q.z - m.z; o[2] = d * d;
-        d = q.w - m.w; o[3] = d * d;
-    }
-};
-
 // The rg of a broadcast MUL / DIV backward, computed inside the un-broadcast reduction
 // instead of being materialised (the expressions of FBinRg: MUL ug * other; DIV operand 0
 // ug / t2; operand 1 ((-t1) / (t2 * t2)) * ug, or (f * t1) * ug with f = -1 / (s * s) for
@@ -216,7 +176,6 @@ __device__ __forceinline__ void epi_store(float* out, float*, int64_t o, float v
         case EPI_STORE: out[o] = v; break;
         case EPI_MEAN: out[o] = v / div; break;
         case EPI_ACCUM: out[o] = out[o] + v; break;
-        case EPI_STD: out[o] = __builtin_sqrtf(v / div); break;
         case EPI_SCALE: out[o] = v * div; break;
         default: out[o] = out[o] + (-v); break;
     }
@@ -631,60 +590,246 @@ __global__ void __launch_bounds__(kRThreads)
     }
 }
 
-// tstd over rows held in registers (B % 4 == 0, B <= 16384): the row is read once, its
-// mean and then its squared deviations come from registers. WPR waves per row.
+// ---------------------------------------------------------------------------------------
+// tstd: one pass over x, fp64 moments
+// ---------------------------------------------------------------------------------------
+// The reference takes each line's mean in fp32, then sums the squared deviations from it
+// (tensorutils.mojo:723-840): two passes over x. Here each line's moments about its first
+// element K are accumulated in fp64 in one pass, S1 = sum(x - K) and S2 = sum((x - K)^2)
+// (x - K of two fp32 values is exact in fp64), and the squared deviations from the mean are
+// S2 - S1^2 / B. The fp64 rounding of that difference is about 2^-53 ((mean - K) / std)^2
+// relative, far under the fp32 rounding of the reference's own two passes, so the result is
+// in the sum class. The epilogue is the reference's: sqrt(f32(variance) / f32(B)).
+struct Mom {
+    double s1, s2;
+};
+constexpr int64_t kMomMaxSplit = 4096;  // row chunks per row at most (longer chunks beyond)
+
+__device__ __forceinline__ void mom_add(Mom& m, float v, double K) {
+    const double d = (double)v - K;
+    m.s1 = m.s1 + d;
+    m.s2 = __builtin_fma(d, d, m.s2);
+}
+
+__device__ __forceinline__ Mom mom_wave(Mom m) {
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1) {
+        m.s1 = m.s1 + __shfl_xor(m.s1, k);
+        m.s2 = m.s2 + __shfl_xor(m.s2, k);
+    }
+    return m;
+}
+
+__device__ __forceinline__ float mom_std(const Mom& m, int64_t B) {
+    double v = m.s2 - m.s1 * m.s1 / (double)B;
+    if (v < 0.0) v = 0.0;  // rounding of a zero variance (NaN passes through)
+    return __builtin_sqrtf((float)v / (float)B);
+}
+
+// tstd over rows of B % 4 == 0, B <= 16384 elements: WPR waves per row, the row's quads
+// loaded together, fp64 moments (above) summed per lane in quad order, then the butterfly and
+// the waves in order.
 template <int WPR, int NQ>
 __global__ void __launch_bounds__(kRThreads)
     k_tstd_rowreg(float* __restrict__ res, const float* __restrict__ x, int64_t nrows, int64_t B) {
-    __shared__ float ws[4];
+    __shared__ Mom ws[4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t row = WPR == 1 ? (int64_t)blockIdx.x * 4 + w : (int64_t)blockIdx.x;
     if (row >= nrows) return;  // WPR == 1: uniform per wave, and that path has no barrier
     const int tr = WPR == 1 ? lane : (int)threadIdx.x;
     constexpr int NT = 64 * WPR;
     const int64_t Bq = B >> 2;
-    const float4* x4 = reinterpret_cast<const float4*>(x + row * B);
-    float4 v[NQ];
-    float acc = 0.0f;
+    const vf4* x4 = reinterpret_cast<const vf4*>(x + row * B);
+    const float kf = x[row * B];
+    const double K = (double)kf;
+    vf4 v[NQ];  // a quad past the row holds K: x - K = 0 adds nothing to either moment
 #pragma unroll
     for (int k = 0; k < NQ; ++k) {
         const int64_t qi = tr + (int64_t)k * NT;
-        if (qi < Bq) {
-            v[k] = x4[qi];
-            acc = acc + v[k].x;
-            acc = acc + v[k].y;
-            acc = acc + v[k].z;
-            acc = acc + v[k].w;
-        }
+        v[k] = qi < Bq ? x4[qi] : vf4{kf, kf, kf, kf};
     }
-    acc = wave_reduce<RSum>(acc);
-    if (WPR == 4) {
-        if (lane == 0) ws[w] = acc;
-        __syncthreads();
-        acc = ((ws[0] + ws[1]) + ws[2]) + ws[3];
-        __syncthreads();  // ws is reused below
-    }
-    const float fb = (float)B;
-    const float mu = acc / fb;  // tmean: sum / Scalar[f32](count)
-    float sq = 0.0f;
+    Mom m{0.0, 0.0};
 #pragma unroll
-    for (int k = 0; k < NQ; ++k) {
-        const int64_t qi = tr + (int64_t)k * NT;
-        if (qi < Bq) {
-            float d;
-            d = v[k].x - mu; sq = sq + d * d;
-            d = v[k].y - mu; sq = sq + d * d;
-            d = v[k].z - mu; sq = sq + d * d;
-            d = v[k].w - mu; sq = sq + d * d;
+    for (int k = 0; k < NQ; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mom_add(m, v[k][j], K);
+    m = mom_wave(m);
+    if (WPR == 4) {
+        if (lane == 0) ws[w] = m;
+        __syncthreads();
+        m = ws[0];
+        for (int k = 1; k < 4; ++k) {
+            m.s1 = m.s1 + ws[k].s1;
+            m.s2 = m.s2 + ws[k].s2;
         }
     }
-    sq = wave_reduce<RSum>(sq);
-    if (WPR == 4) {
-        if (lane == 0) ws[w] = sq;
-        __syncthreads();
-        sq = ((ws[0] + ws[1]) + ws[2]) + ws[3];
+    if (tr == 0) res[row] = mom_std(m, B);
+}
+
+// Rows: block vr = r * S + s sums elements [s * L, min((s + 1) * L, B)) of row r (VEC: two
+// quads per thread in flight), its four waves in order; S == 1 writes the row's result,
+// S > 1 the partial part[vr].
+template <bool VEC>
+__global__ void __launch_bounds__(kRThreads)
+    k_tstd_mom_rows(float* __restrict__ res, const float* __restrict__ x, int64_t B, int64_t L, int64_t S,
+                    Mom* __restrict__ part) {
+    __shared__ Mom ws[4];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int64_t vr = blockIdx.x;
+    const int64_t r = vr / S, s = vr - r * S;
+    const int64_t start = r * B + s * L;
+    const int64_t rem = B - s * L;
+    const int64_t len = rem < L ? rem : L;
+    const float kf = x[r * B];
+    const double K = (double)kf;
+    Mom m{0.0, 0.0};
+    if (VEC) {
+        const int64_t nq = len >> 2;
+        const vf4* x4 = reinterpret_cast<const vf4*>(x + start);
+        for (int64_t q = t; q < nq; q += 2 * kRThreads) {
+            const vf4 a = x4[q];
+            // a quad past the chunk holds K: x - K = 0 adds nothing to either moment
+            const vf4 b = q + kRThreads < nq ? x4[q + kRThreads] : vf4{kf, kf, kf, kf};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) mom_add(m, a[j], K);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) mom_add(m, b[j], K);
+        }
+    } else {
+        for (int64_t j = t; j < len; j += kRThreads) mom_add(m, x[start + j], K);
     }
-    if (tr == 0) res[row] = __builtin_sqrtf(sq / fb);
+    m = mom_wave(m);
+    if (lane == 0) ws[w] = m;
+    __syncthreads();
+    if (t == 0) {
+        Mom tot = ws[0];
+        for (int k = 1; k < 4; ++k) {
+            tot.s1 = tot.s1 + ws[k].s1;
+            tot.s2 = tot.s2 + ws[k].s2;
+        }
+        if (S == 1) res[r] = mom_std(tot, B);
+        else part[vr] = tot;
+    }
+}
+
+// Strided axis over [A, B, C]: thread = a quad (VEC) or one element of the [A, C] output,
+// rows [s * rps, min((s + 1) * rps, B)) of split s = blockIdx.y in order, 4 rows in flight;
+// K is the line's element at row 0. S == 1 writes the result, S > 1 partials at
+// s * (A * C) + o.
+template <bool VEC>
+__global__ void __launch_bounds__(kRThreads)
+    k_tstd_mom_cols(float* __restrict__ res, const float* __restrict__ x, int64_t A, int64_t B, int64_t C,
+                    int64_t rps, int64_t S, Mom* __restrict__ part) {
+    constexpr int W = VEC ? 4 : 1;
+    const int64_t AC = A * C;
+    const int64_t o = ((int64_t)blockIdx.x * kRThreads + threadIdx.x) * W;
+    if (o >= AC) return;
+    const int64_t a = o / C, c = o - a * C;
+    const int64_t s = blockIdx.y;
+    const int64_t b0 = s * rps;
+    const int64_t b1 = b0 + rps < B ? b0 + rps : B;
+    const int64_t base = a * B * C + c;
+    auto load = [&](int64_t b, float* v) {
+        if (VEC) {
+            const vf4 q = *reinterpret_cast<const vf4*>(x + base + b * C);
+#pragma unroll
+            for (int j = 0; j < W; ++j) v[j] = q[j];
+        } else {
+            v[0] = x[base + b * C];
+        }
+    };
+    double K[W];
+    {
+        float v0[W];
+        load(0, v0);
+#pragma unroll
+        for (int j = 0; j < W; ++j) K[j] = (double)v0[j];
+    }
+    Mom m[W];
+#pragma unroll
+    for (int j = 0; j < W; ++j) m[j] = Mom{0.0, 0.0};
+    int64_t b = b0;
+    for (; b + 3 < b1; b += 4) {
+        float v[4][W];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) load(b + u, v[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < W; ++j) mom_add(m[j], v[u][j], K[j]);
+    }
+    for (; b < b1; ++b) {
+        float v[W];
+        load(b, v);
+#pragma unroll
+        for (int j = 0; j < W; ++j) mom_add(m[j], v[j], K[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+        if (S == 1) res[o + j] = mom_std(m[j], B);
+        else part[s * AC + o + j] = m[j];
+    }
+}
+
+// Combines of the split partials, in split order. Rows: one block per row, S partials
+// contiguous (thread-strided, then the waves' butterflies and the four waves in order).
+// Columns: one thread per line, partials at stride nlines.
+__global__ void __launch_bounds__(kRThreads)
+    k_tstd_mom_combine_rows(float* __restrict__ res, const Mom* __restrict__ part, int64_t S, int64_t B) {
+    __shared__ Mom ws[4];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const Mom* p = part + (int64_t)blockIdx.x * S;
+    Mom m{0.0, 0.0};
+    int64_t i = t;
+    for (; i + 3 * kRThreads < S; i += 4 * kRThreads) {  // four partials in flight, added in order
+        Mom q[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) q[u] = p[i + u * kRThreads];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            m.s1 = m.s1 + q[u].s1;
+            m.s2 = m.s2 + q[u].s2;
+        }
+    }
+    for (; i < S; i += kRThreads) {
+        m.s1 = m.s1 + p[i].s1;
+        m.s2 = m.s2 + p[i].s2;
+    }
+    m = mom_wave(m);
+    if (lane == 0) ws[w] = m;
+    __syncthreads();
+    if (t == 0) {
+        Mom tot = ws[0];
+        for (int k = 1; k < 4; ++k) {
+            tot.s1 = tot.s1 + ws[k].s1;
+            tot.s2 = tot.s2 + ws[k].s2;
+        }
+        res[blockIdx.x] = mom_std(tot, B);
+    }
+}
+
+__global__ void __launch_bounds__(kRThreads)
+    k_tstd_mom_combine_cols(float* __restrict__ res, const Mom* __restrict__ part, int64_t nlines, int64_t S,
+                            int64_t B) {
+    const int64_t l = (int64_t)blockIdx.x * kRThreads + threadIdx.x;
+    if (l >= nlines) return;
+    Mom m{0.0, 0.0};
+    int64_t s = 0;
+    for (; s + 3 < S; s += 4) {  // four partials in flight, added in order
+        Mom q[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) q[u] = part[(s + u) * nlines + l];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            m.s1 = m.s1 + q[u].s1;
+            m.s2 = m.s2 + q[u].s2;
+        }
+    }
+    for (; s < S; ++s) {
+        m.s1 = m.s1 + part[s * nlines + l].s1;
+        m.s2 = m.s2 + part[s * nlines + l].s2;
+    }
+    res[l] = mom_std(m, B);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1326,23 +1471,45 @@ int mh_tstd(float* res, const float* x, const mh_shape* psx, int32_t axis) {
         }
         return finish("mh_tstd");
     }
-    // scratch: the line means, then the partials of whichever pass splits
-    const size_t nmu = pad64((size_t)(A * C));
-    const size_t t = tmp_floats_t<RSum>(A, B, C, true);
-    float* base = nullptr;
-    MH_TRY(scratch((nmu + t) * sizeof(float), reinterpret_cast<void**>(&base)));
-    float* mu = base;
-    float* tmp = t ? base + nmu : nullptr;
-    const float div = (float)B;  // tmean: / Scalar[f32](count), and variance / count
-    MH_TRY(reduce_abc(RED_SUM, EPI_MEAN, x, A, B, C, mu, nullptr, div, tmp));
-    const int64_t n = A * B * C;
-    if (n < ((int64_t)1 << 32)) {
-        LdSqDev<false> ld{x, mu, B * C, C, make_fastdiv((uint32_t)(B * C > 0 ? B * C : 1)), make_fastdiv((uint32_t)C)};
-        MH_TRY((reduce_t<RSum, LdSqDev<false>>(ld, al16(x), EPI_STD, A, B, C, res, nullptr, div, tmp)));
-    } else {
-        LdSqDev<true> ld{x, mu, B * C, C, FastDiv{}, FastDiv{}};
-        MH_TRY((reduce_t<RSum, LdSqDev<true>>(ld, al16(x), EPI_STD, A, B, C, res, nullptr, div, tmp)));
+    if (B == 0) return mh_fill(res, __builtin_nanf(""), A * C);  // the reference divides 0 by 0
+    hipStream_t st = ctx().stream;
+    if (C == 1) {  // rows (all elements: one row): block chunks of kRowChunk elements or more,
+                   // at most kMomMaxSplit per row so that the combine stays short
+        int64_t L = kRowChunk;
+        if ((B + L - 1) / L > kMomMaxSplit) L = ((B + kMomMaxSplit - 1) / kMomMaxSplit + 3) & ~(int64_t)3;
+        const int64_t S = (B + L - 1) / L;
+        if (S == 1) L = B;
+        Mom* part = nullptr;
+        if (S > 1) MH_TRY(scratch((size_t)(A * S) * sizeof(Mom), reinterpret_cast<void**>(&part)));
+        const bool vec = al16(x) && B % 4 == 0;
+        dim3 g((unsigned)(A * S)), b(kRThreads);
+        if (vec) hipLaunchKernelGGL(k_tstd_mom_rows<true>, g, b, 0, st, res, x, B, L, S, part);
+        else hipLaunchKernelGGL(k_tstd_mom_rows<false>, g, b, 0, st, res, x, B, L, S, part);
+        if (S > 1) hipLaunchKernelGGL(k_tstd_mom_combine_rows, dim3((unsigned)A), b, 0, st, res, part, S, B);
+        return finish("mh_tstd");
     }
+    // strided axis: the column layout of the wide reductions (a thread per column quad, about
+    // two blocks per CU, row splits of at least 32 rows)
+    const bool vec = al16(x) && C % 4 == 0;
+    const int64_t W = vec ? 4 : 1;
+    const int64_t items = A * C / W;
+    const int64_t bx = (items + kRThreads - 1) / kRThreads;
+    int64_t S = (2 * (int64_t)ctx().num_cus + bx - 1) / bx;
+    int64_t maxS = B / 32;
+    if (maxS < 1) maxS = 1;
+    if (S > maxS) S = maxS;
+    if (S > 65535) S = 65535;
+    if (S < 1) S = 1;
+    const int64_t rps = (B + S - 1) / S;
+    S = (B + rps - 1) / rps;
+    Mom* part = nullptr;
+    if (S > 1) MH_TRY(scratch((size_t)(S * A * C) * sizeof(Mom), reinterpret_cast<void**>(&part)));
+    dim3 g((unsigned)bx, (unsigned)S), b(kRThreads);
+    if (vec) hipLaunchKernelGGL(k_tstd_mom_cols<true>, g, b, 0, st, res, x, A, B, C, rps, S, part);
+    else hipLaunchKernelGGL(k_tstd_mom_cols<false>, g, b, 0, st, res, x, A, B, C, rps, S, part);
+    if (S > 1)
+        hipLaunchKernelGGL(k_tstd_mom_combine_cols, dim3((unsigned)((A * C + kRThreads - 1) / kRThreads)), b, 0, st,
+                           res, part, A * C, S, B);
     return finish("mh_tstd");
 }
 

@@ -772,6 +772,34 @@ def test_tstd_parity(gpu, shape, axis):
     assert_sum_close(got, ORC.tstd(x, axis), ex, f"tstd {shape} axis {axis}")
 
 
+TSTD_OFFSET_CASES = [((1000, 256), 0), ((1000, 256), 1), ((1000, 256), None), ((37, 63, 107), 1),
+                     ((3, 40000), 1), ((2, 3, 20002), 2)]
+
+
+@pytest.mark.parametrize("shape,axis", TSTD_OFFSET_CASES, ids=[f"{s}-ax{a}" for s, a in TSTD_OFFSET_CASES])
+def test_tstd_large_mean_small_spread(gpu, shape, axis):
+    """Lines whose mean is 10^5 of their spread (mean 1000, std 0.01): the one-pass fp64
+    moments about each line's first element against the oracle's fp32 two passes, in the sum
+    class (which accepts the result closer to the fp64 standard deviation of the same fp32
+    values)."""
+    x = synth.normal(shape, 1000.0, 0.01, 1140)
+    red = (1,) if axis is None else tuple(1 if i == axis else d for i, d in enumerate(shape))
+    ex = (x.astype(np.float64).std() if axis is None else x.astype(np.float64).std(axis=axis, keepdims=True))
+    ex = np.asarray(ex).reshape(red)
+    got = gpu.tstd(x, axis)
+    assert_sum_close(got, ORC.tstd(x, axis), ex, f"tstd {shape} axis {axis}")
+    np.testing.assert_allclose(got, ex, rtol=1e-4)
+
+
+def test_tstd_of_empty_lines_is_nan(gpu):
+    """Lines of length 0: the reference divides 0 by 0 (tensorutils.mojo:735-744, 836-838)."""
+    for shape, axis in (((3, 0), 1), ((0,), None), ((2, 0, 5), 1)):
+        x = np.zeros(shape, np.float32)
+        ref = ORC.tstd(x, axis)
+        got = gpu.tstd(x, axis)
+        assert got.shape == ref.shape and np.isnan(ref).all() and np.isnan(got).all(), (shape, axis)
+
+
 def test_tstd_unaligned(gpu):
     m = gpu.m
     x = synth.normal((1000, 256), 0, 1, 1131)
