@@ -106,6 +106,11 @@ int mh_unary_fwd(int op, float* res, const float* x, int64_t n);
  * device pointer of the shape-(1) graph scalar t2. */
 int mh_pow_fwd(float* res, const float* x, int64_t n, const float* exponent);
 
+/* elwise_pow, tensorutils.mojo:226-239: res = powi(x, n_int) with the integer exponent
+ * given by the caller (Mojo's `SIMD ** Int`: square-and-multiply from 1, 1 / result for a
+ * negative exponent). */
+int mh_powi_fwd(float* res, const float* x, int32_t n_int, int64_t n);
+
 /* SUM/MEAN/MAX forward: SUM.forward (basics.mojo:393-406), MEAN.forward (:440-452),
  * MAX.forward (:521-534) -> reduce all (tensorutils.mojo:564-598, tsum/tmean/tmax
  * :694-720, :850-862) or reduce axis (:622-684, :746-772, :865-876). axis = -1 reduces all

@@ -13,7 +13,7 @@ from .model import Collection, Model, Parameters  # noqa: F401
 from .ops import (  # noqa: F401
     OP, ADD, SUB, MUL, DIV, EXP, LOG, POW, SUM, MEAN, MAX, SIGMOID, RELU, TANH, FMA, CLIP, LEAKYRELU,
     forward_op, backward_op, backward_op_both, broadcast_shapes, get_reduce_shape, fill,
-    elwise_transform, elwise_op, accumulate_grad, tsum, tmean, tmax, tstd, static_result_shape,
+    elwise_transform, elwise_pow, elwise_op, accumulate_grad, tsum, tmean, tmax, tstd, static_result_shape,
     bias_relu_forward, bias_relu_backward, softmax_log_mul_mean_forward, softmax_log_mul_mean_backward,
     softmax_forward, softmax_backward, logsoftmax_forward, logsoftmax_backward, cross_entropy_forward,
     cross_entropy_backward,
@@ -22,7 +22,7 @@ from .ops import (  # noqa: F401
 __all__ = [
     "Adam", "Collection", "Graph", "Model", "Parameters", "Symbol", "MantleHipError", "Tensor", "TensorShape", "init", "sync", "OP", "forward_op", "backward_op",
     "backward_op_both", "broadcast_shapes", "get_reduce_shape", "fill", "elwise_transform",
-    "elwise_op", "accumulate_grad", "tsum", "tmean", "tmax", "tstd", "static_result_shape", "bias_relu_forward",
+    "elwise_pow", "elwise_op", "accumulate_grad", "tsum", "tmean", "tmax", "tstd", "static_result_shape", "bias_relu_forward",
     "bias_relu_backward", "softmax_log_mul_mean_forward", "softmax_log_mul_mean_backward", "softmax_forward",
     "softmax_backward", "logsoftmax_forward", "logsoftmax_backward", "cross_entropy_forward",
     "cross_entropy_backward",

@@ -61,6 +61,12 @@ struct FPowi {  // POW.forward: powi(x, Int(t2[0])), basics.mojo:320-327
     __device__ float operator()(const float* v) const { return mpowi(v[0], n); }
 };
 
+struct FPowiN {  // elwise_pow with its integer exponent given, tensorutils.mojo:226-239
+    int64_t n;
+    __device__ void setup(const DevScal&) {}
+    __device__ float operator()(const float* v) const { return mpowi(v[0], n); }
+};
+
 template <int OP>
 struct FUnBwd {  // v[0] = x, v[1] = ug: the rg of each unary struct backward
     __device__ void setup(const DevScal&) {}
@@ -838,6 +844,19 @@ int mh_pow_fwd(float* res, const float* x, int64_t n, const float* exponent) {
     const float* p[1] = {x};
     MH_TRY((run_map<FPowi, 1, false>(res, pl, p, scal1(exponent), FPowi{})));
     return finish("mh_pow_fwd");
+}
+
+int mh_powi_fwd(float* res, const float* x, int32_t n_int, int64_t n) {
+    if (n < 0) return fail(MH_ERR_INVALID, "mh_powi_fwd: negative count");
+    if (n == 0) return MH_OK;
+    if (!res || !x) return fail(MH_ERR_NULL, "mh_powi_fwd: null tensor");
+    MH_TRY(require_init());
+    mh_shape s = flat_shape(n);
+    ElwPlan pl;
+    MH_TRY(build_elw_plan(s, 1, &s, &pl));
+    const float* p[1] = {x};
+    MH_TRY((run_map<FPowiN, 1, false>(res, pl, p, DevScal{}, FPowiN{(int64_t)n_int})));
+    return finish("mh_powi_fwd");
 }
 
 int mh_unary_bwd_accum(int op, float* grad, const float* x, const float* ug, int64_t n) {

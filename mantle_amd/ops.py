@@ -91,6 +91,15 @@ def elwise_transform(op: int, res: Tensor, t: Tensor) -> None:
     _lib.call("mh_unary_fwd", int(op), res.ptr, t.ptr, t.num_elements())
 
 
+def elwise_pow(res: Tensor, t: Tensor, n: int) -> None:
+    """elwise_pow, tensorutils.mojo:226-239: res = t ** n for an integer n (square and
+    multiply; 1 / result for negative n)."""
+    n = int(n)
+    if not -(1 << 31) <= n < (1 << 31):
+        raise ValueError(f"elwise_pow: exponent {n} outside int32")
+    _lib.call("mh_powi_fwd", res.ptr, t.ptr, n, t.num_elements())
+
+
 def elwise_op(op: int, res: Tensor, t1: Tensor, t2: Tensor) -> None:
     """elwise_op dispatcher, tensorutils.mojo:242-357."""
     _lib.call("mh_binary_fwd", int(op), res.ptr, res.shape().c(), t1.ptr, t1.shape().c(), t2.ptr,

@@ -162,6 +162,22 @@ def test_device_pow_matches_oracle_bitwise(gpu):
                         f"pow bwd x {e}")
 
 
+def test_elwise_pow_integer_exponents(gpu):
+    """mh_powi_fwd (elwise_pow with a given Int exponent) bit-exact against the oracle's
+    square-and-multiply, negative exponents included, on a ragged length with 0, +-inf, NaN
+    and negative bases."""
+    m = gpu.m
+    x = synth.uniform((4099,), -3, 3, 1150)
+    x[:6] = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1.0], np.float32)
+    tx = gpu.T(x)
+    for n in (-3, -1, 0, 1, 2, 3, 5, 17, 40):
+        res = m.Tensor(tx.shape())
+        m.elwise_pow(res, tx, n)
+        assert_bitexact(res.to_numpy(), O.elwise_pow(x, n), f"x^{n}")
+    with pytest.raises(ValueError):
+        m.elwise_pow(m.Tensor(tx.shape()), tx, 1 << 40)
+
+
 @pytest.mark.parametrize("e", [2.37, 0.61, 1.0, 2.0, -1.5, 3.9])
 def test_pow_parity(gpu, e):
     n = (1 << 18) + 7
