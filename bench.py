@@ -777,6 +777,24 @@ def run_copy(L, reps):
 # ---------------------------------------------------------------------------------------
 # CPU baseline
 # ---------------------------------------------------------------------------------------
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cores_available() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
 def cpu_baseline(n_sample: int, reps: int, expo: float):
     """The CPU restatement (oracle/, single thread, like the reference's elementwise paths)
     on the same op sequence over a bounded sample; GB/s with the same byte accounting."""
@@ -808,7 +826,7 @@ def cpu_baseline(n_sample: int, reps: int, expo: float):
         best = dt if best is None else min(best, dt)
     bytes_per_elem = sum(b for _, b in step_plan())
     return {"value": round(bytes_per_elem * n_sample / best / 1e9, 3), "unit": "GB/s", "cores": 1,
-            "kind": "port",
+            "kind": "port", "host_cpu": _cpu_model(), "host_cores_available": _cores_available(),
             "sample": f"same op sequence on {n_sample} elements per tensor (1/{(1 << 28) // n_sample} of the "
                       f"workload), best of {reps}, {best:.2f} s per pass; single-threaded C restatement "
                       f"(oracle/mantle_oracle.c, -O3)"}

@@ -260,6 +260,58 @@ def test_max_backward_sparse_stores_keep_every_bit(gpu, shape, axis):
     assert ((r3 == 0) & ~np.signbit(r3)).any(), "no -0 turned into +0: the case is not exercised"
 
 
+RANK8_A, RANK8_B = (2, 1, 3, 1, 2, 1, 2, 5), (1, 2, 1, 2, 1, 3, 1, 5)
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3], ids=["ADD", "SUB", "MUL", "DIV"])
+def test_rank8_broadcast(gpu, op):
+    """MAX_RANK = 8 (core/tensor.mojo:20): a broadcast over every other axis of two rank-8
+    operands, forward bit-exact and both operands' gradients (un-broadcast over four axes)."""
+    a, b = _binary_inputs(RANK8_A, RANK8_B, 160 + op)
+    assert_bitexact(gpu.forward(op, a, b), ORC.forward(op, a, b), f"rank-8 fwd op{op}")
+    out_shape = np.broadcast_shapes(RANK8_A, RANK8_B)
+    ug = synth.normal(out_shape, 0, 1, 170 + op)
+    for k, shape in ((0, RANK8_A), (1, RANK8_B)):
+        g0 = synth.normal(shape, 0, 1, 180 + k)
+        got = gpu.backward(k, op, ug, a, b, grad=g0)
+        ref = ORC.backward(k, op, ug, a, b, grad=g0)
+        A, B, U = (v.astype(np.float64) for v in (a, b, ug))
+        rg = {0: U, 1: (U if k == 0 else -U), 2: (U * B if k == 0 else U * A),
+              3: (U / B if k == 0 else -A / (B * B) * U)}[op]
+        red = tuple(i for i, d in enumerate(shape) if d == 1 and out_shape[i] != 1)
+        ex = rg.sum(axis=red, keepdims=True) + g0.astype(np.float64)
+        mag = np.abs(rg).sum(axis=red, keepdims=True) + np.abs(g0)
+        assert_sum_close(got, ref, ex, f"rank-8 bwd op{op} id{k}", terms_abs=mag)
+
+
+@pytest.mark.parametrize("axis", [0, 3, 6, 7, None])
+def test_rank8_reductions(gpu, axis):
+    """SUM / MEAN / MAX forward and backward and tstd over one axis (or all) of a rank-8
+    tensor with ties injected."""
+    shape = (2, 3, 2, 3, 2, 3, 2, 7)
+    x = synth.normal(shape, 0, 1, 190)
+    if axis is not None:
+        synth.inject_ties(x, axis, 191)
+    red = (1,) if axis is None else tuple(1 if i == axis else d for i, d in enumerate(shape))
+    kd = dict(axis=axis, keepdims=True) if axis is not None else {}
+    x64 = x.astype(np.float64)
+    ex = np.asarray(x64.sum(**kd)).reshape(red)
+    mag = np.asarray(np.abs(x64).sum(**kd)).reshape(red)
+    d = x.size if axis is None else shape[axis]
+    assert_sum_close(gpu.forward(OPS["SUM"], x, axis=axis), ORC.forward(OPS["SUM"], x, axis=axis), ex, "sum",
+                     terms_abs=mag)
+    assert_sum_close(gpu.forward(OPS["MEAN"], x, axis=axis), ORC.forward(OPS["MEAN"], x, axis=axis), ex / d, "mean",
+                     terms_abs=mag / d)
+    assert_bitexact(gpu.forward(OPS["MAX"], x, axis=axis), ORC.forward(OPS["MAX"], x, axis=axis), "max")
+    ug = synth.normal(red, 0, 1, 192)
+    g0 = synth.normal(shape, 0, 1, 193)
+    for name in ("SUM", "MEAN", "MAX"):
+        assert_bitexact(gpu.backward(0, OPS[name], ug, x, axis=axis, grad=g0),
+                        ORC.backward(0, OPS[name], ug, x, axis=axis, grad=g0), f"{name} bwd")
+    sd = np.asarray(x64.std(**kd)).reshape(red)
+    assert_sum_close(gpu.tstd(x, axis), ORC.tstd(x, axis), sd, "tstd")
+
+
 def test_reductions_are_deterministic(gpu):
     m = gpu.m
     x = gpu.T(synth.normal((4096, 4096), 0, 1, 710))
