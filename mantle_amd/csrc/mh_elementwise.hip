@@ -372,6 +372,50 @@ __global__ void __launch_bounds__(kThreads)
     }
 }
 
+// Plane-broadcast engine: output [N, C, S] with S % 4 == 0 and fewer than 2^31 elements,
+// every IN_BCAST operand a per-channel vector ([1, C, 1], as an NCHW bias is), the output and
+// FULL operands 16-byte aligned. One quad per thread in flat order; a quad lies in one plane
+// (S % 4 == 0), whose channel is (q / (S / 4)) mod C (two fast divisions).
+template <class F, int NIN, bool ACCUM>
+__global__ void __launch_bounds__(kThreads)
+    k_planebc4(float* __restrict__ out, InPtrs<NIN> in, int kinds, int64_t nq, uint32_t C, FastDiv fsq, FastDiv fc,
+               DevScal ds, F f) {
+    constexpr int NA = NIN > 0 ? NIN : 1;
+    f.setup(ds);
+    float sv[NA];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) sv[k] = ((kinds >> (2 * k)) & 3) == IN_SCALAR ? in.p[k][0] : 0.0f;
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
+        const uint32_t p = fdiv((uint32_t)q, fsq);
+        const uint32_t c = p - fdiv(p, fc) * C;
+        vf4 t[NA];
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) {
+            const int kind = (kinds >> (2 * k)) & 3;
+            if (kind == IN_FULL) {
+                t[k] = reinterpret_cast<const vf4*>(in.p[k])[q];
+            } else {
+                const float b = kind == IN_BCAST ? in.p[k][c] : sv[k];
+                t[k] = vf4{b, b, b, b};
+            }
+        }
+        vf4 o = vf4{0.f, 0.f, 0.f, 0.f};
+        if (ACCUM) o = reinterpret_cast<const vf4*>(out)[q];
+        vf4 r;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float v[NA];
+#pragma unroll
+            for (int k = 0; k < NIN; ++k) v[k] = t[k][j];
+            const float fv = f(v);
+            r[j] = ACCUM ? o[j] + fv : fv;
+        }
+        if (ACCUM && kSparseAccum<F> && !bits_differ4(o[0], o[1], o[2], o[3], r[0], r[1], r[2], r[3])) continue;
+        reinterpret_cast<vf4*>(out)[q] = r;
+    }
+}
+
 // Broadcast engine, 128-bit path: the output and every FULL operand stream as flat float4
 // quads whatever the shape (all must be 16-byte aligned); only the broadcast operands are
 // gathered, with 32-bit offsets below 2^31 elements and a decode loop bounded by MAXR.
@@ -615,6 +659,16 @@ static int run_map(float* out, const ElwPlan& pl, const float* const* ptrs, cons
         bool colform = !big && pl.rank == 2 && pl.dims[1] % 4 == 0 && al_b;
         for (int k = 0; k < NIN; ++k)
             if (pl.kind[k] == IN_BCAST && !(pl.st[k][0] == 0 && pl.st[k][1] == 1)) colform = false;
+        // [N, C, S] with per-channel operands ([1, C, 1]), S % 4 == 0
+        bool planeform = !big && pl.rank == 3 && pl.dims[2] % 4 == 0;
+        for (int k = 0; k < NIN; ++k)
+            if (pl.kind[k] == IN_BCAST && !(pl.st[k][0] == 0 && pl.st[k][1] == 1 && pl.st[k][2] == 0)) planeform = false;
+        if (planeform) {
+            const uint32_t C = (uint32_t)pl.dims[1], Sq = (uint32_t)(pl.dims[2] / 4);
+            hipLaunchKernelGGL((k_planebc4<F, NIN, ACCUM>), g, b, 0, st, out, in, kinds, pl.n >> 2, C,
+                               make_fastdiv(Sq), make_fastdiv(C), ds, f);
+            return MH_OK;
+        }
         if (colform) {
             const uint32_t Cq = (uint32_t)(pl.dims[1] / 4);
             hipLaunchKernelGGL((k_colbc4<F, NIN, ACCUM>), g, b, 0, st, out, in, kinds, pl.n >> 2, Cq, make_fastdiv(Cq),

@@ -88,6 +88,28 @@ __global__ void __launch_bounds__(kFThreads)
     }
 }
 
+// Forward over [N, C, S] planes (S % 4 == 0, fewer than 2^31 elements; the bias indexed by C,
+// or a scalar with C == 1): one quad per thread in flat order, its channel
+// (q / (S / 4)) mod C from two fast divisions.
+__global__ void __launch_bounds__(kFThreads)
+    k_bias_relu_fwd_planes(float* __restrict__ y, float* __restrict__ r, const float* __restrict__ x,
+                           const float* __restrict__ bias, int64_t nq, uint32_t C, FastDiv fsq, FastDiv fc) {
+    const int64_t stride = (int64_t)gridDim.x * kFThreads;
+    for (int64_t q = (int64_t)blockIdx.x * kFThreads + threadIdx.x; q < nq; q += stride) {
+        const uint32_t p = fdiv((uint32_t)q, fsq);
+        const float bv = bias[p - fdiv(p, fc) * C];
+        const vf4 xv = reinterpret_cast<const vf4*>(x)[q];
+        vf4 yv, rv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            yv[j] = xv[j] + bv;  // ADD.forward
+            rv[j] = mrelu(yv[j]);  // RELU.forward
+        }
+        reinterpret_cast<vf4*>(y)[q] = yv;
+        reinterpret_cast<vf4*>(r)[q] = rv;
+    }
+}
+
 // Backward over [N, C, S] planes, S % 4 == 0. One wavefront per (channel c, group g of G
 // planes n = g * G .. g * G + G - 1, chunk k of QC quads of each plane, QC <= 1024), wave
 // v = blockIdx.x * 4 + wave with c = v % C, g * K + k = v / C; the planes in order, four quads
@@ -237,6 +259,12 @@ int mh_bias_relu_fwd(float* y, float* r, const float* x, const mh_shape* psx, co
     if (blocks > 0x7fffffff) blocks = 0x7fffffff;
     dim3 g((unsigned)blocks), b(kFThreads);
     hipStream_t st = ctx().stream;
+    int64_t N = 0, C = 0, S = 0;
+    if (!big && pl.kind[1] != IN_FULL && plane_form(pl, &N, &C, &S) && S % 4 == 0) {
+        hipLaunchKernelGGL(k_bias_relu_fwd_planes, g, b, 0, st, y, r, x, bias, n >> 2, (uint32_t)C,
+                           make_fastdiv((uint32_t)(S / 4)), make_fastdiv((uint32_t)C));
+        return finish("mh_bias_relu_fwd");
+    }
     if (inner4) {
         if (big) hipLaunchKernelGGL((k_bias_relu_fwd4<true, true>), g, b, 0, st, y, r, x, bias, pl);
         else hipLaunchKernelGGL((k_bias_relu_fwd4<true, false>), g, b, 0, st, y, r, x, bias, pl);
