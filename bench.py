@@ -1069,7 +1069,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
         print(f"bench.py: this build runs the op layer on one GPU; --gpus {args.gpus} "
-              f"(WORLD_SIZE={world}) is not supported. Multi-GPU sharding is described in DESIGN.md.",
+              f"(WORLD_SIZE={world}) is not supported: every op family would shard by contiguous slices "
+              f"with exchanges of at most 32 KB, and only one GPU's share is built and measured.",
               file=sys.stderr)
         sys.exit(2)
     rank = int(os.environ.get("RANK", "0"))
