@@ -900,7 +900,8 @@ C2_KERNEL = {"ADD.bwd": "void mh::k_bwd2_same4<0>", "SUB.bwd": "void mh::k_bwd2_
 # algorithmic bytes of the kernel, note)
 _N3, _N4, _N5 = 6422528, 1 << 26, 10485760
 WL_KERNELS = [
-    ("c3 bias_relu.fwd (fused)", "void mh::k_bias_relu_fwd4<true, false>", 1605632, 12 * _N3 + 128, ""),
+    ("c3 bias_relu.fwd (fused)", "mh::k_bias_relu_fwd_planes", 1605632, 12 * _N3 + 128, ""),
+    ("c3 ADD.fwd", "void mh::k_planebc4<mh::FBin<0>, 2, false>", 1605632, 8 * _N3 + 128, ""),
     ("c3 bias_relu.bwd (fused)", "void mh::k_bias_relu_bwd_planes<false, true, true>", 131072, 16 * _N3 + 256,
      "grad_x read and written, bias gradient in the same launch"),
     ("c3 ADD.bwd_bias", "void mh::k_unb_planes<false>", 131072, 4 * _N3 + 256, "one launch, arrival tickets"),
@@ -928,7 +929,8 @@ WL_KERNELS = [
 # (workload, group, op label, kernel-name prefix) of single-shape workload kernels whose
 # rocprofv3 duration the stats summary sets beside the bench's figures
 WL_STATS = [("c3", "op_by_op", "ADD.bwd_bias", "void mh::k_unb_planes<false>"),
-            ("c3", "fused", "bias_relu.fwd", "void mh::k_bias_relu_fwd4<true, false>"),
+            ("c3", "fused", "bias_relu.fwd", "mh::k_bias_relu_fwd_planes"),
+            ("c3", "op_by_op", "ADD.fwd", "void mh::k_planebc4<mh::FBin<0>, 2, false>"),
             ("c3", "fused", "bias_relu.bwd", "void mh::k_bias_relu_bwd_planes<false, true, true>"),
             ("c4", "ops", "8192x8192.ax1.MAX.bwd", "void mh::k_max_bwd_rowreg<4, 8>"),
             ("c5", "fused", "fused.fwd", "void mh::k_rowp_fwd<0, 16>"),
