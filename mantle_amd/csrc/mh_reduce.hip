@@ -393,15 +393,16 @@ __global__ void __launch_bounds__(kRThreads)
 #pragma unroll
     for (int j = 0; j < W; ++j) acc[j] = R::init();
     int64_t b = b0;
-    for (; b + 3 < b1; b += 4) {
-        T v[4][W];
+    constexpr int RU = VEC ? 2 : 4;  // rows in flight
+    for (; b + RU - 1 < b1; b += RU) {
+        T v[RU][W];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < RU; ++u) {
             if (VEC) ld.get4(base + (b + u) * C, v[u]);
             else v[u][0] = ld.get(base + (b + u) * C);
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < RU; ++u)
 #pragma unroll
             for (int j = 0; j < W; ++j) acc[j] = R::comb(acc[j], v[u][j]);
     }
@@ -887,15 +888,15 @@ static ColSplit strip_split(int64_t A, int64_t B, int64_t C, int64_t* nstrips) {
 }
 
 // Wide strided reductions (C % 4 == 0, at least 256 column quads): one thread per column
-// quad (k_cols, 4 rows in flight), 128 rows per block when the chip is full anyway: about 2
-// blocks per CU, each thread with a long run of rows, streamed best in a sweep of layouts
-// on gfx950 (blocks of few rows, or a strip of 64 quads per block, were 5-10 % slower).
+// quad (k_cols, 2 rows in flight), about four blocks per CU (64-row splits at [8192, 8192]):
+// the best of a sweep of tile shapes on gfx950 (50.4 us against 52 us for 4 rows in flight
+// over 128-row splits; 8 rows in flight, whole-row blocks or strips of 64 quads were slower).
 static bool use_wide_cols(int64_t C, bool vec) { return vec && C % 4 == 0 && (C >> 2) >= 256; }
 static ColSplit wide_split(int64_t A, int64_t B, int64_t C) {
     ColSplit cs;
     cs.vec = true;
     const int64_t bx = (A * (C >> 2) + kRThreads - 1) / kRThreads;
-    const int64_t target = 2 * (int64_t)ctx().num_cus;
+    const int64_t target = 4 * (int64_t)ctx().num_cus;
     int64_t S = (target + bx - 1) / bx;
     int64_t maxS = B / 32;
     if (maxS < 1) maxS = 1;
@@ -1488,8 +1489,9 @@ int mh_tstd(float* res, const float* x, const mh_shape* psx, int32_t axis) {
         if (S > 1) hipLaunchKernelGGL(k_tstd_mom_combine_rows, dim3((unsigned)A), b, 0, st, res, part, S, B);
         return finish("mh_tstd");
     }
-    // strided axis: the column layout of the wide reductions (a thread per column quad, about
-    // two blocks per CU, row splits of at least 32 rows)
+    // strided axis: a thread per column quad, about two blocks per CU, row splits of at least 32
+    // rows, 4 rows in flight (the fp64 accumulation runs best on these longer runs: 61.7 us at
+    // [8192, 8192] axis 0, 67.3 us with k_cols's 2 rows over 64-row splits)
     const bool vec = al16(x) && C % 4 == 0;
     const int64_t W = vec ? 4 : 1;
     const int64_t items = A * C / W;
