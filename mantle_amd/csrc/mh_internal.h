@@ -189,7 +189,13 @@ enum Epi : int {
     EPI_MEAN = 1,      // out = v / (float)len
     EPI_ACCUM = 2,     // out = out + v
     EPI_ACCUM_NEG = 3,  // out = out + (-v)
-    EPI_SCALE = 5       // out = v * div
+    EPI_SCALE = 5,      // out = v * div
+    // out = ((out + x0) + x1) + ... (x negated for _NEG): a shape-aware gradient accumulation
+    // walks the full-shape gradient serially, so each row's values add into the gradient one
+    // at a time. Kernels with one thread per row do exactly that; the others add the finished
+    // sum (EPI_ACCUM / EPI_ACCUM_NEG).
+    EPI_SEQ_ACCUM = 6,
+    EPI_SEQ_ACCUM_NEG = 7
 };
 // Reduce x viewed as [A, B, C] over B into out[A*C] (out2: fl(1/count) for RED_MAXCNT).
 // `div` is the float divisor of EPI_MEAN; `tmp` holds split partials

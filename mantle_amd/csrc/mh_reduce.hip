@@ -177,8 +177,27 @@ __device__ __forceinline__ void epi_store(float* out, float*, int64_t o, float v
         case EPI_MEAN: out[o] = v / div; break;
         case EPI_ACCUM: out[o] = out[o] + v; break;
         case EPI_SCALE: out[o] = v * div; break;
+        case EPI_SEQ_ACCUM:
+        case EPI_SEQ_ACCUM_NEG: out[o] = v; break;  // v started from out[o] (row_start)
         default: out[o] = out[o] + (-v); break;
     }
+}
+// The start and the values of a row that one thread sums in element order: for the serial
+// accumulation epilogues (sums only) out[o] and each value negated for _NEG, else R::init()
+// and the values as they are.
+template <class R>
+__device__ __forceinline__ typename R::T row_start(int epi, const float* out, int64_t o) {
+    if constexpr (std::is_same<R, RSum>::value) {
+        if (epi == EPI_SEQ_ACCUM || epi == EPI_SEQ_ACCUM_NEG) return out[o];
+    }
+    return R::init();
+}
+template <class R>
+__device__ __forceinline__ typename R::T row_val(int epi, typename R::T v) {
+    if constexpr (std::is_same<R, RSum>::value) {
+        if (epi == EPI_SEQ_ACCUM_NEG) return -v;
+    }
+    return v;
 }
 __device__ __forceinline__ void epi_store(float* out, float* out2, int64_t o, MC v, int, float) {
     out[o] = v.m;
@@ -208,9 +227,9 @@ __global__ void __launch_bounds__(kRThreads)
     ld.setup();
     const int64_t stride = (int64_t)gridDim.x * kRThreads;
     for (int64_t r = (int64_t)blockIdx.x * kRThreads + threadIdx.x; r < nrows; r += stride) {
-        typename R::T acc = R::init();
+        typename R::T acc = row_start<R>(epi, out, r);
         const int64_t base = r * B;
-        for (int64_t j = 0; j < B; ++j) acc = R::comb(acc, ld.get(base + j));
+        for (int64_t j = 0; j < B; ++j) acc = R::comb(acc, row_val<R>(epi, ld.get(base + j)));
         epi_store(out, out2, r, acc, epi, div);
     }
 }
@@ -244,9 +263,10 @@ __global__ void __launch_bounds__(kRThreads)
     __syncthreads();
     const int t = threadIdx.x;
     if (t < rows) {
-        typename R::T acc = R::init();
-        for (int j = 0; j < B; ++j) acc = R::comb(acc, R::lift(tile[t * B + j]));
-        epi_store(out, out2, (int64_t)blockIdx.x * kRThreads + t, acc, epi, div);
+        const int64_t o = (int64_t)blockIdx.x * kRThreads + t;
+        typename R::T acc = row_start<R>(epi, out, o);
+        for (int j = 0; j < B; ++j) acc = R::comb(acc, row_val<R>(epi, R::lift(tile[t * B + j])));
+        epi_store(out, out2, o, acc, epi, div);
     }
 }
 
@@ -268,8 +288,8 @@ __global__ void __launch_bounds__(kRThreads)
     __syncthreads();
     const int t = threadIdx.x;
     if (t < rows) {
-        T acc = R::init();
-        for (int j = 0; j < B; ++j) acc = R::comb(acc, tile[t * B + j]);
+        T acc = row_start<R>(epi, out, r0 + t);
+        for (int j = 0; j < B; ++j) acc = R::comb(acc, row_val<R>(epi, tile[t * B + j]));
         epi_store(out, out2, r0 + t, acc, epi, div);
     }
 }
@@ -979,6 +999,10 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
                     float* out2, float div, float* tmp, bool nosplit = false, bool combine = false) {
     if (A * C == 0) return MH_OK;
     hipStream_t st = ctx().stream;
+    if (!(C == 1 && B <= 64)) {  // serial accumulation only where one thread sums a row
+        if (epi == EPI_SEQ_ACCUM) epi = EPI_ACCUM;
+        else if (epi == EPI_SEQ_ACCUM_NEG) epi = EPI_ACCUM_NEG;
+    }
     if (C == 1) {
         if (B <= 64) {
             if constexpr (std::is_same<LD, LdPlain<R>>::value) {
@@ -1279,7 +1303,10 @@ int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* r
                               bool negate, float* tmp) {
     mh_reduce_plan_info p;
     MH_TRY(plan_unbroadcast(sgrad, srg, &p));
-    const int final_epi = negate ? EPI_ACCUM_NEG : EPI_ACCUM;
+    // one reduction step: each gradient element's values are one line of rg, which the
+    // thread-per-row kernels add into it in order, as the reference's serial walk does
+    const int final_epi = p.nsteps <= 1 ? (negate ? EPI_SEQ_ACCUM_NEG : EPI_SEQ_ACCUM)
+                                        : (negate ? EPI_ACCUM_NEG : EPI_ACCUM);
     if (p.nsteps == 0)  // only size-1 dims differ: same element order
         return reduce_abc(RED_SUM, final_epi, rg, numel(srg), 1, 1, grad, nullptr, 0.0f, nullptr);
     PlaneForm pf;
@@ -1316,6 +1343,45 @@ int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* r
     return MH_OK;
 }
 
+// Short rows (C == 1, B <= BMAX) of a broadcast MUL / DIV backward's un-broadcast: the block
+// stages ug and the full-shape operand of rows [r0, r0 + 256) in LDS with 16-byte loads (one
+// contiguous run each), then thread t adds row r0 + t's terms one at a time into its
+// gradient (EPI_SEQ_ACCUM), with DIV's divisor read once per row: the terms and order of the
+// generic loader path (k_rows_lds_ld over LdBinRg), so the same bits, without a row lookup
+// per element. ug and the operand 16-byte aligned.
+template <int OP, int ID, bool DIVS, int BMAX>
+__global__ void __launch_bounds__(kRThreads)
+    k_rows_binrg(LdBinRg<OP, ID, DIVS, false> ld, float* __restrict__ grad, int64_t nrows, int B) {
+    __shared__ float4 us4[kRThreads * BMAX / 4], as4[kRThreads * BMAX / 4];
+    float* us = reinterpret_cast<float*>(us4);
+    float* as = reinterpret_cast<float*>(as4);
+    ld.setup();
+    const int t = threadIdx.x;
+    const int64_t r0 = (int64_t)blockIdx.x * kRThreads;
+    const int64_t rows = (nrows - r0) < kRThreads ? (nrows - r0) : kRThreads;
+    const int64_t base = r0 * B;
+    const int cnt = (int)(rows * B);
+    const int nq = cnt >> 2;
+    const float4* u4 = reinterpret_cast<const float4*>(ld.ug + base);
+    const float4* a4 = reinterpret_cast<const float4*>(ld.a + base);
+    for (int i = t; i < nq; i += kRThreads) {
+        us4[i] = u4[i];
+        as4[i] = a4[i];
+    }
+    for (int i = (nq << 2) + t; i < cnt; i += kRThreads) {
+        us[i] = ld.ug[base + i];
+        as[i] = ld.a[base + i];
+    }
+    __syncthreads();
+    if (t < rows) {
+        const int64_t row = r0 + t;
+        const float d = (OP == MH_DIV && ID == 1 && !DIVS) ? ld.t2[row] : 0.0f;
+        float acc = grad[row];  // EPI_SEQ_ACCUM
+        for (int j = 0; j < B; ++j) acc = acc + ld.term(us[t * B + j], as[t * B + j], d);
+        grad[row] = acc;
+    }
+}
+
 template <int OP, int ID, bool DIVS, bool BIG>
 static int binrg_reduce(float* grad, const float* ug, const float* a, const float* t2, int64_t A, int64_t B,
                         int64_t C, bool al, float* tmp) {
@@ -1330,9 +1396,21 @@ static int binrg_reduce(float* grad, const float* ug, const float* a, const floa
         ld.fc = make_fastdiv((uint32_t)C);
     }
     ld.al = al;
+    if constexpr (!BIG) {
+        if (C == 1 && B <= 32 && al && A <= ((int64_t)1 << 40)) {  // short rows, staged as quads
+            const unsigned blocks = (unsigned)((A + kRThreads - 1) / kRThreads);
+            if (B <= 16)
+                hipLaunchKernelGGL((k_rows_binrg<OP, ID, DIVS, 16>), dim3(blocks), dim3(kRThreads), 0, ctx().stream,
+                                   ld, grad, A, (int)B);
+            else
+                hipLaunchKernelGGL((k_rows_binrg<OP, ID, DIVS, 32>), dim3(blocks), dim3(kRThreads), 0, ctx().stream,
+                                   ld, grad, A, (int)B);
+            return MH_OK;
+        }
+    }
     // vec_ok: the loader reads quads at any alignment, so the kernels (and the summation
     // order) are those of a materialised, aligned rg
-    return reduce_t<RSum, LdBinRg<OP, ID, DIVS, BIG>>(ld, true, EPI_ACCUM, A, B, C, grad, nullptr, 0.0f, tmp);
+    return reduce_t<RSum, LdBinRg<OP, ID, DIVS, BIG>>(ld, true, EPI_SEQ_ACCUM, A, B, C, grad, nullptr, 0.0f, tmp);
 }
 
 template <int OP, int ID, bool DIVS>

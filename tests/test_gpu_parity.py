@@ -83,6 +83,24 @@ def test_binary_fwd_bwd_parity(gpu, op, sa, sb):
             assert_sum_close(got, ref, ex, f"bwd op{op} id{k}", terms_abs=mag)
 
 
+ROW_UNB_CASES = [(1, 1), (255, 3), (257, 4), (4099, 10), (300, 16), (513, 17), (1000, 31), (7, 5)]
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3], ids=["ADD", "SUB", "MUL", "DIV"])
+@pytest.mark.parametrize("rows,k", ROW_UNB_CASES, ids=[f"{r}x{k}" for r, k in ROW_UNB_CASES])
+def test_row_unbroadcast_short_rows_bitexact(gpu, op, rows, k):
+    """[rows, k] (op) [rows, 1]: each operand's gradient through the un-broadcast of rows
+    shorter than the SIMD width, which the reference (and the oracle) sums in element order,
+    so the gradients are bit-exact for either operand order and every op."""
+    for sa, sb in (((rows, k), (rows, 1)), ((rows, 1), (rows, k))):
+        a, b = _binary_inputs(sa, sb, 700 + op + k)
+        ug = synth.normal((rows, k), 0, 1, 710 + rows)
+        for tid, shape in ((0, sa), (1, sb)):
+            g0 = synth.normal(shape, 0, 1, 720 + tid)
+            got = gpu.backward(tid, op, ug, a, b, grad=g0)
+            assert_bitexact(got, ORC.backward(tid, op, ug, a, b, grad=g0), f"{sa}x{sb} op{op} id{tid}")
+
+
 @pytest.mark.parametrize("op", [0, 1, 2, 3], ids=["ADD", "SUB", "MUL", "DIV"])
 def test_binary_bwd_both_operands_fused(gpu, op):
     m = gpu.m
