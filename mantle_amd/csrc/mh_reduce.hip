@@ -390,6 +390,31 @@ __global__ void __launch_bounds__(kRThreads)
     }
 }
 
+// Short columns (B <= 64) of a serial accumulation (EPI_SEQ_ACCUM / _NEG): one thread per
+// output element walks its B values in row order, eight loads in flight, adding each into the
+// output one at a time (row_start / row_val) in one launch with no split.
+template <class R, class LD>
+__global__ void __launch_bounds__(kRThreads)
+    k_cols_seq(LD ld, int64_t A, int64_t B, int64_t C, float* out, float* out2, int epi, float div) {
+    ld.setup();
+    using T = typename R::T;
+    const int64_t o = (int64_t)blockIdx.x * kRThreads + threadIdx.x;
+    if (o >= A * C) return;
+    const int64_t a = o / C, c = o - a * C;
+    const int64_t base = a * B * C + c;
+    T acc = row_start<R>(epi, out, o);
+    int64_t b = 0;
+    for (; b + 7 < B; b += 8) {
+        T v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = ld.get(base + (b + u) * C);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = R::comb(acc, row_val<R>(epi, v[u]));
+    }
+    for (; b < B; ++b) acc = R::comb(acc, row_val<R>(epi, ld.get(base + b * C)));
+    epi_store(out, out2, o, acc, epi, div);
+}
+
 // Column reduction: item = a quad (VEC) or one element of the flattened [A, C] output; the
 // rows [b0, b1) of split blockIdx.y. S == 1 writes the epilogue, S > 1 writes partials at
 // s * (A * C) + o.
@@ -999,7 +1024,13 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
                     float* out2, float div, float* tmp, bool nosplit = false, bool combine = false) {
     if (A * C == 0) return MH_OK;
     hipStream_t st = ctx().stream;
-    if (!(C == 1 && B <= 64)) {  // serial accumulation only where one thread sums a row
+    if (C > 1 && B <= 64 && (epi == EPI_SEQ_ACCUM || epi == EPI_SEQ_ACCUM_NEG) && A * C < ((int64_t)1 << 38)) {
+        const unsigned blocks = (unsigned)((A * C + kRThreads - 1) / kRThreads);
+        hipLaunchKernelGGL((k_cols_seq<R, LD>), dim3(blocks), dim3(kRThreads), 0, st, ld, A, B, C, out, out2, epi,
+                           div);
+        return MH_OK;
+    }
+    if (!(C == 1 && B <= 64)) {  // serial accumulation only where one thread sums a line
         if (epi == EPI_SEQ_ACCUM) epi = EPI_ACCUM;
         else if (epi == EPI_SEQ_ACCUM_NEG) epi = EPI_ACCUM_NEG;
     }

@@ -83,18 +83,24 @@ def test_binary_fwd_bwd_parity(gpu, op, sa, sb):
             assert_sum_close(got, ref, ex, f"bwd op{op} id{k}", terms_abs=mag)
 
 
-ROW_UNB_CASES = [(1, 1), (255, 3), (257, 4), (4099, 10), (300, 16), (513, 17), (1000, 31), (7, 5)]
+# (full shape, broadcast operand): un-broadcasts that are one reduction along lines of at
+# most 64 elements -- rows, columns, and middle axes
+SEQ_UNB_CASES = [((1, 1), (1, 1)), ((255, 3), (255, 1)), ((257, 4), (257, 1)), ((4099, 10), (4099, 1)),
+                 ((300, 16), (300, 1)), ((513, 17), (513, 1)), ((1000, 31), (1000, 1)), ((7, 5), (7, 1)),
+                 ((300, 64), (300, 1)), ((32, 32), (1, 32)), ((7, 2), (1, 2)), ((64, 1000), (1, 1000)),
+                 ((9, 4, 3), (9, 1, 3)), ((5, 33, 257), (5, 1, 257)), ((40, 4096), (4096,)), ((3, 7), (7,))]
 
 
 @pytest.mark.parametrize("op", [0, 1, 2, 3], ids=["ADD", "SUB", "MUL", "DIV"])
-@pytest.mark.parametrize("rows,k", ROW_UNB_CASES, ids=[f"{r}x{k}" for r, k in ROW_UNB_CASES])
-def test_row_unbroadcast_short_rows_bitexact(gpu, op, rows, k):
-    """[rows, k] (op) [rows, 1]: each operand's gradient through the un-broadcast of rows
-    shorter than the SIMD width, which the reference (and the oracle) sums in element order,
-    so the gradients are bit-exact for either operand order and every op."""
-    for sa, sb in (((rows, k), (rows, 1)), ((rows, 1), (rows, k))):
-        a, b = _binary_inputs(sa, sb, 700 + op + k)
-        ug = synth.normal((rows, k), 0, 1, 710 + rows)
+@pytest.mark.parametrize("full,small", SEQ_UNB_CASES, ids=[f"{f}-{s}" for f, s in SEQ_UNB_CASES])
+def test_short_line_unbroadcast_bitexact(gpu, op, full, small):
+    """full (op) small in both operand orders: the broadcast operand's gradient is an
+    un-broadcast along lines of at most 64 elements, which the reference's accumulate_grad
+    adds into the gradient one value at a time in row-major order, as the GPU's
+    thread-per-line kernels do -- so every gradient is bit-exact against the oracle."""
+    for sa, sb in ((full, small), (small, full)):
+        a, b = _binary_inputs(sa, sb, 700 + op + len(full))
+        ug = synth.normal(full, 0, 1, 710 + full[0])
         for tid, shape in ((0, sa), (1, sb)):
             g0 = synth.normal(shape, 0, 1, 720 + tid)
             got = gpu.backward(tid, op, ug, a, b, grad=g0)
