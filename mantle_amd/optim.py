@@ -16,6 +16,21 @@ from . import _lib
 from .tensor import Tensor
 
 
+class SymbolTensors(list):
+    """Adam's momentum / rms tensors, one per parameter in order; indexable by position or, for
+    an Adam built from a model's parameters, by the parameter's Symbol (as the reference's
+    ``optim.momentum_grads[sym]`` collections are)."""
+
+    def __init__(self, tensors, symbols=None):
+        super().__init__(tensors)
+        self.symbols = list(symbols) if symbols is not None else None
+
+    def __getitem__(self, key):
+        if self.symbols is not None and hasattr(key, "name") and hasattr(key, "shape"):
+            return super().__getitem__(self.symbols.index(key))
+        return super().__getitem__(key)
+
+
 class Adam:
     def __init__(self, params, lr: float = 0.001, beta1: float = 0.9, beta2: float = 0.999,
                  epsilon: float = 1e-8):
@@ -23,12 +38,14 @@ class Adam:
         ``Adam[g](model.parameters, ...)`` takes them), or (param, grad) Tensor pairs."""
         self._collection = None
         self._span = None  # (params, grads, n) of a model's contiguous trainable span
+        self.symbols = None  # the trainable parameters' symbols, for a model's parameters
         if hasattr(params, "tensors") and hasattr(params, "grads") and hasattr(params, "graph"):
             self._collection = params
             span = params.param_span()
             if span is not None:
                 self._span = span
-            params = [(params.tensors[s], params.grads[s]) for s in params.graph.trainable_parameters()]
+            self.symbols = params.graph.trainable_parameters()
+            params = [(params.tensors[s], params.grads[s]) for s in self.symbols]
         self.params: List[Tuple[Tensor, Tensor]] = list(params)
         for p, g in self.params:
             if p.shape() != g.shape():
@@ -41,13 +58,15 @@ class Adam:
             _, _, n = self._span
             self._m_span, self._v_span = Tensor(n), Tensor(n)
             offs = [p.ptr - self._span[0] for p, _ in self.params]
-            self.momentum_grads = [Tensor(p.shape(), _ptr=self._m_span.ptr + o, _owner=self._m_span)
-                                   for (p, _), o in zip(self.params, offs)]
-            self.rms_grads = [Tensor(p.shape(), _ptr=self._v_span.ptr + o, _owner=self._v_span)
-                              for (p, _), o in zip(self.params, offs)]
+            mom = [Tensor(p.shape(), _ptr=self._m_span.ptr + o, _owner=self._m_span)
+                   for (p, _), o in zip(self.params, offs)]
+            rms = [Tensor(p.shape(), _ptr=self._v_span.ptr + o, _owner=self._v_span)
+                   for (p, _), o in zip(self.params, offs)]
         else:
-            self.momentum_grads = [Tensor(p.shape()) for p, _ in self.params]
-            self.rms_grads = [Tensor(p.shape()) for p, _ in self.params]
+            mom = [Tensor(p.shape()) for p, _ in self.params]
+            rms = [Tensor(p.shape()) for p, _ in self.params]
+        self.momentum_grads = SymbolTensors(mom, self.symbols)
+        self.rms_grads = SymbolTensors(rms, self.symbols)
 
     def zero_grad(self) -> None:
         """Adam.zero_grad (optim.mojo:90-92): parameters.grads.set_zero()."""
