@@ -922,8 +922,8 @@ WL_KERNELS = [
      8 * _N5 + 12 * (_N5 // 10), "the rg terms computed in the loader, added into the gradient in row order"),
     ("c5 MAX.bwd (rows of 10)", "void mh::k_max_bwd_rows<16>", 1048576, 12 * _N5 + 8 * (_N5 // 10),
      "stores only quads holding a row maximum (most quads, at 10 classes)"),
-    ("c5 fused head forward", "void mh::k_rowp_fwd<0, 16>", 262144, 8 * _N5, "logits and targets read once"),
-    ("c5 fused head backward", "void mh::k_rowp_bwd<0, 16>", 196608, 16 * _N5, ""),
+    ("c5 fused head forward", "void mh::k_rowp_fwd<0, 10>", 262144, 8 * _N5, "logits and targets read once"),
+    ("c5 fused head backward", "void mh::k_rowp_bwd<0, 10>", 196608, 16 * _N5, ""),
     ("CrossEntropy [32768,1000] backward", "void mh::k_roww_bwd<1, true, 16>", 2097152, 16 * 32768000, ""),
 ]
 
@@ -935,8 +935,8 @@ WL_STATS = [("c3", "op_by_op", "ADD.bwd_bias", "void mh::k_unb_planes<false>"),
             ("c3", "op_by_op", "ADD.fwd", "void mh::k_planebc4<mh::FBin<0>, 2, false>"),
             ("c3", "fused", "bias_relu.bwd", "void mh::k_bias_relu_bwd_planes<false, true, true>"),
             ("c4", "ops", "8192x8192.ax1.MAX.bwd", "void mh::k_max_bwd_rowreg<4, 8>"),
-            ("c5", "fused", "fused.fwd", "void mh::k_rowp_fwd<0, 16>"),
-            ("c5", "fused", "fused.bwd", "void mh::k_rowp_bwd<0, 16>"),
+            ("c5", "fused", "fused.fwd", "void mh::k_rowp_fwd<0, 10>"),
+            ("c5", "fused", "fused.bwd", "void mh::k_rowp_bwd<0, 10>"),
             ("c5", "fwd", "SUB.fwd", "void mh::k_rowbc4<mh::FBin<1>, 2, false>"),
             ("c5", "fwd", "DIV.fwd", "void mh::k_rowbc4<mh::FBin<3>, 2, false>"),
             ("c5", "bwd", "DIV.bwd1", "void mh::k_rows_binrg<3, 1, false, 16>")]

@@ -402,6 +402,9 @@ __device__ __forceinline__ void loss_tail(float tot, float* part, uint32_t* tick
 // its next tile are already in flight into registers, so the chip never alternates between
 // a whole-grid load phase and a whole-grid compute phase. A tile is at most 4096 floats (four
 // float4 per thread per operand); rows are computed exactly as in k_rowt_fwd / k_rowt_bwd.
+// Each class count 1..16 has its own kernel (KM = K at compile time: every loop over a row
+// unrolled without per-class guards), 5-6 % faster at 10 classes than one kernel for all
+// counts up to 16.
 constexpr int kPQ = 4;  // float4 per thread per operand tile (q0..q3 below)
 
 // Four float4 of one operand tile per thread, as named registers (an array here ends up in
@@ -440,7 +443,8 @@ __device__ __forceinline__ void tile_to_lds(float* dst, const TileRegs& r, int c
 template <int V, int KM>
 __global__ void __launch_bounds__(kSThreads)
     k_rowp_fwd(const float* __restrict__ x, const float* __restrict__ tg, float* __restrict__ out, int64_t rows,
-               int K, float* __restrict__ part, uint32_t* tickets, float* loss, float lscale) {
+               float* __restrict__ part, uint32_t* tickets, float* loss, float lscale) {
+    constexpr int K = KM;  // compiled for the exact class count
     __shared__ float4 xs4[kPQ * kSThreads], ts4[kPQ * kSThreads];
     __shared__ float ws[4];
     constexpr bool LOSS = V == G_SMLM || V == G_CE;
@@ -517,7 +521,8 @@ __global__ void __launch_bounds__(kSThreads)
 template <int V, int KM>
 __global__ void __launch_bounds__(kSThreads)
     k_rowp_bwd(float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ up,
-               const float* __restrict__ ug, int64_t rows, int K, float c) {
+               const float* __restrict__ ug, int64_t rows, float c) {
+    constexpr int K = KM;  // compiled for the exact class count
     __shared__ float4 xs4[kPQ * kSThreads], us4[kPQ * kSThreads], gs4[kPQ * kSThreads];
     float* xs = reinterpret_cast<float*>(xs4);
     float* us = reinterpret_cast<float*>(us4);
@@ -869,6 +874,10 @@ __global__ void __launch_bounds__(kSThreads)
 // ---------------------------------------------------------------------------------------
 static inline bool al16s(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// The class counts with a persistent row kernel of their own.
+#define MH_ROWP_CLASSES(X) \
+    X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11) X(12) X(13) X(14) X(15) X(16)
+
 // Blocks of a persistent kernel: as many as can be resident at once (queried once per
 // kernel), so no block waits for another to finish.
 static int64_t pipe_grid(const void* kernel) {
@@ -900,8 +909,14 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
     constexpr bool LOSS = V == G_SMLM || V == G_CE;
     const bool al = al16s(x) && (!LOSS || al16s(tg)) && (LOSS || al16s(out));
     if (K <= 16 && al) {  // persistent, pipelined
-        const void* kern = K <= 8 ? reinterpret_cast<const void*>(&k_rowp_fwd<V, 8>)
-                                  : reinterpret_cast<const void*>(&k_rowp_fwd<V, 16>);
+        const void* kern = nullptr;
+        switch (K) {
+#define MH_K(KK) \
+    case KK: kern = reinterpret_cast<const void*>(&k_rowp_fwd<V, KK>); break;
+            MH_ROWP_CLASSES(MH_K)
+#undef MH_K
+            default: return fail(MH_ERR_INVALID, "row kernel: %d classes", K);
+        }
         const int64_t ntiles = (rows + kSThreads - 1) / kSThreads;
         const int64_t pg = pipe_grid(kern);
         const int64_t nb = ntiles < pg ? ntiles : pg;
@@ -912,8 +927,12 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
             if (done) *done = true;
         }
         dim3 g((unsigned)nb), b(kSThreads);
-        if (K <= 8) hipLaunchKernelGGL((k_rowp_fwd<V, 8>), g, b, 0, st, x, tg, out, rows, K, part, tk, loss, lscale);
-        else hipLaunchKernelGGL((k_rowp_fwd<V, 16>), g, b, 0, st, x, tg, out, rows, K, part, tk, loss, lscale);
+        switch (K) {
+#define MH_K(KK) \
+    case KK: hipLaunchKernelGGL((k_rowp_fwd<V, KK>), g, b, 0, st, x, tg, out, rows, part, tk, loss, lscale); break;
+            MH_ROWP_CLASSES(MH_K)
+#undef MH_K
+        }
         return MH_OK;
     }
     if (K <= kSThreadMax) {
@@ -952,14 +971,24 @@ static int launch_bwd(float* gx, const float* x, const float* up, const float* u
     hipStream_t st = ctx().stream;
     const bool al = al16s(x) && al16s(up) && al16s(gx);
     if (K <= 16 && al) {  // persistent, pipelined
-        const void* kern = K <= 8 ? reinterpret_cast<const void*>(&k_rowp_bwd<V, 8>)
-                                  : reinterpret_cast<const void*>(&k_rowp_bwd<V, 16>);
+        const void* kern = nullptr;
+        switch (K) {
+#define MH_K(KK) \
+    case KK: kern = reinterpret_cast<const void*>(&k_rowp_bwd<V, KK>); break;
+            MH_ROWP_CLASSES(MH_K)
+#undef MH_K
+            default: return fail(MH_ERR_INVALID, "row kernel: %d classes", K);
+        }
         const int64_t ntiles = (rows + kSThreads - 1) / kSThreads;
         const int64_t pg = pipe_grid(kern);
         const int64_t nb = ntiles < pg ? ntiles : pg;
         dim3 g((unsigned)nb), b(kSThreads);
-        if (K <= 8) hipLaunchKernelGGL((k_rowp_bwd<V, 8>), g, b, 0, st, gx, x, up, ug, rows, K, c);
-        else hipLaunchKernelGGL((k_rowp_bwd<V, 16>), g, b, 0, st, gx, x, up, ug, rows, K, c);
+        switch (K) {
+#define MH_K(KK) \
+    case KK: hipLaunchKernelGGL((k_rowp_bwd<V, KK>), g, b, 0, st, gx, x, up, ug, rows, c); break;
+            MH_ROWP_CLASSES(MH_K)
+#undef MH_K
+        }
         return MH_OK;
     }
     if (K <= kSThreadMax) {
