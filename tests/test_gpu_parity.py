@@ -531,8 +531,10 @@ def test_config5_classifier_chain_small(gpu):
         assert_ulp(gg[k], go[k], 2, f"grad {k}")
 
 
+# every class count up to 16 has a kernel of its own: each appears at least once
 SMLM_CASES = [(4099, 10), (1, 1), (3, 2), (257, 3), (1000, 16), (513, 17), (300, 32), (64, 1), (7, 5), (2048, 10),
-              (40, 33), (20, 64), (9, 65), (8, 128), (5, 130), (3, 1000), (2, 2047)]
+              (40, 33), (20, 64), (9, 65), (8, 128), (5, 130), (3, 1000), (2, 2047)] + \
+             [(259 + k, k) for k in (4, 6, 7, 8, 9, 11, 12, 13, 14, 15)]
 
 
 def _check_fused_head(gpu, logits, onehot, ugv):
@@ -637,10 +639,11 @@ def test_fused_row_graphs_reject_wide_rows(gpu):
 
 
 # Row lengths around every engine boundary: 1-64 one thread per row (element-order sums),
-# 65-2047 one wavefront per row (the row-reduction kernel's order; multiples of 4 and not).
+# 65-2047 one wavefront per row (the row-reduction kernel's order; multiples of 4 and not);
+# every class count up to 16 (a kernel of its own each) appears.
 ROW_CASES = [(300, 1), (7, 2), (257, 3), (100, 10), (33, 31), (65, 32), (40, 33), (17, 63), (16, 64), (9, 65),
              (11, 66), (8, 100), (6, 128), (5, 130), (4, 257), (3, 1000), (2, 1024), (3, 1025), (2, 2044),
-             (2, 2047), (1000, 10)]
+             (2, 2047), (1000, 10)] + [(259 + k, k) for k in (4, 5, 6, 7, 8, 9, 11, 12, 13, 14, 15, 16)]
 
 
 @pytest.mark.parametrize("rows,classes", ROW_CASES, ids=[f"{r}x{c}" for r, c in ROW_CASES])
