@@ -63,10 +63,14 @@ def _optim_entries(optim, kind: int) -> List[Tuple[int, Tensor]]:
     return [(s.name, t) for s, t in zip(syms, tensors)]
 
 
-def _entry_bytes(symbol_id: int, kind: int, t: Tensor) -> bytes:
+def _write_entry(f, symbol_id: int, kind: int, t: Tensor) -> None:
+    """checkpoint.mojo:81-108: the header, then the slot's elements downloaded and written as
+    they are (little-endian fp32, no second host copy)."""
     dims = t.shape().dims
-    head = struct.pack("<IBI", symbol_id, kind, len(dims)) + struct.pack(f"<{len(dims)}I", *dims)
-    return head + t.to_numpy().astype("<f4", copy=False).tobytes()
+    f.write(struct.pack("<IBI", symbol_id, kind, len(dims)) + struct.pack(f"<{len(dims)}I", *dims))
+    a = np.ascontiguousarray(t.to_numpy(), dtype="<f4").reshape(-1)
+    if a.size:
+        f.write(memoryview(a).cast("B"))
 
 
 def _write(path: str, iter: int, model: Sequence[Tuple[int, Tensor]],
@@ -74,9 +78,9 @@ def _write(path: str, iter: int, model: Sequence[Tuple[int, Tensor]],
     with open(path, "wb") as f:
         f.write(struct.pack("<5I", CHECKPOINT_MAGIC, CHECKPOINT_VERSION, int(iter), len(model), len(optim)))
         for sid, t in model:
-            f.write(_entry_bytes(sid, OPTIM_KIND_NONE, t))
+            _write_entry(f, sid, OPTIM_KIND_NONE, t)
         for sid, kind, t in optim:
-            f.write(_entry_bytes(sid, kind, t))
+            _write_entry(f, sid, kind, t)
 
 
 def save_checkpoint(path: str, parameters, iter: int = 0) -> None:
