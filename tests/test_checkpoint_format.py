@@ -122,3 +122,17 @@ def test_load_skips_unknown_symbols_and_optimizer_entries(tmp_path):
     open(path, "wb").write(data)
     info = ck.load_checkpoint(path, params)
     assert info == ck.CheckpointInfo(3, True)
+
+
+def test_adam_state_indexable_by_symbol():
+    """Adam's momentum / rms lists answer to a parameter's Symbol as the reference's
+    collections do (optim.momentum_grads[param_sym]), and to positions as before."""
+    from mantle_amd.optim import SymbolTensors
+    a, b = Symbol(3, TensorShape(2), True), Symbol(5, TensorShape(4), True)
+    ta, tb = _Slot([1, 2]), _Slot([3, 4, 5, 6])
+    st = SymbolTensors([ta, tb], [a, b])
+    assert st[b] is tb and st[a] is ta and st[0] is ta and st[-1] is tb and len(st) == 2
+    with pytest.raises(ValueError):
+        st[Symbol(9, TensorShape(1), True)]
+    plain = SymbolTensors([ta])  # built from (param, grad) pairs: positions only
+    assert plain[0] is ta
