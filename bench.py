@@ -617,8 +617,8 @@ def run_adam(L, reps):
 
 def run_adj(L, reps):
     """FMA, LEAKYRELU and CLIP forward / backward over 2^28 elements, and tstd over
-    [8192, 8192] (axis 0, axis 1, all elements; x read twice: the mean, then the squared
-    deviations, 4 B/elem algorithmic)."""
+    [8192, 8192] (axis 0, axis 1, all elements; x read once for both fp64 moments, 4 B/elem
+    algorithmic)."""
     from mantle_amd._lib import make_shape
     d = Dev(L)
     n = 1 << 28
