@@ -41,8 +41,9 @@ __device__ __forceinline__ float mexp_core(float xc) {
 
 __device__ __forceinline__ float mexp(float x) {
     const float lo = -88.3762626647949f, hi = 88.3762626647950f;
-    float xc = x;
-    if (__builtin_expect(!(x >= lo && x <= hi), 0)) xc = x < lo ? lo : hi;  // clamp (NaN: see below)
+    // clamp without a branch: min / max return the number for a NaN operand, so a NaN x
+    // evaluates the core at a bound and the select below returns x itself
+    const float xc = __builtin_fminf(__builtin_fmaxf(x, lo), hi);
     const float e = mexp_core(xc);
     return x != x ? x : e;
 }
