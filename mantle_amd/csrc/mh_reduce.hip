@@ -465,6 +465,49 @@ __global__ void __launch_bounds__(kRThreads)
     }
 }
 
+// Combine of S split partials [S, n] (n % 4 == 0) in one launch with few memory round trips:
+// a block is 16 column quads x 16 row groups; group r adds the partial rows
+// [r * rpg, min((r + 1) * rpg, S)) in order, eight rows' loads in flight, and group 0 adds the
+// 16 group results in group order from LDS and writes the epilogue.
+template <class R, class LD>
+__global__ void __launch_bounds__(kRThreads)
+    k_parts_comb(LD ld, int64_t S, int64_t n, int64_t rpg, float* out, float* out2, int epi, float div) {
+    using T = typename R::T;
+    __shared__ T lds[16][16][4];
+    ld.setup();
+    const int q = threadIdx.x & 15, r = threadIdx.x >> 4;
+    const int64_t o = ((int64_t)blockIdx.x * 16 + q) * 4;
+    const bool active = o < n;
+    T acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = R::init();
+    if (active) {
+        const int64_t s0 = r * rpg;
+        const int64_t s1 = s0 + rpg < S ? s0 + rpg : S;
+        for (int64_t s = s0; s < s1; s += 8) {
+            T v[8][4];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (s + u < s1) ld.get4((s + u) * n + o, v[u]);
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (s + u < s1)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[j] = R::comb(acc[j], v[u][j]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) lds[r][q][j] = acc[j];
+    __syncthreads();
+    if (r == 0 && active) {
+        for (int rr = 1; rr < 16; ++rr)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = R::comb(acc[j], lds[rr][q][j]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) epi_store(out, out2, o + j, acc[j], epi, div);
+    }
+}
+
 // Rows of >= 2048 elements: one block (4 waves) per (row, chunk) of L = 2048 elements, two
 // quads per thread in flight (small one-shot blocks stream best on gfx950). Block
 // vr = r * S + s covers elements [r*B + s*L, r*B + min((s+1)*L, B)); the four wave results
@@ -1093,11 +1136,12 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
         const int64_t items = A * C / 4;
         dim3 g((unsigned)((items + kRThreads - 1) / kRThreads), (unsigned)cs.S), b(kRThreads);
         hipLaunchKernelGGL((k_cols<R, LD, true>), g, b, 0, st, ld, A, B, C, cs.rps, cs.S, out, out2, epi, div, tmp);
-        if (cs.S > 1) {  // combine the split partials with the strip kernel (4 waves per quad)
+        if (cs.S > 1) {  // combine the split partials in one launch (k_parts_comb)
             using PL = PartLoader<R>;
-            const int64_t np = cs.S * A * C;
-            return reduce_t<R, typename PL::type>(PL::make(tmp, np), true, epi, 1, cs.S, A * C, out, out2, div,
-                                                  nullptr, true);
+            const int64_t n = A * C, np = cs.S * n;
+            const unsigned cb = (unsigned)((n / 4 + 15) / 16);
+            hipLaunchKernelGGL((k_parts_comb<R, typename PL::type>), dim3(cb), dim3(kRThreads), 0, st,
+                               PL::make(tmp, np), cs.S, n, (cs.S + 15) / 16, out, out2, epi, div);
         }
         return MH_OK;
     }
