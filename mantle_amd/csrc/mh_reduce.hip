@@ -418,7 +418,7 @@ __global__ void __launch_bounds__(kRThreads)
 // Column reduction: item = a quad (VEC) or one element of the flattened [A, C] output; the
 // rows [b0, b1) of split blockIdx.y. S == 1 writes the epilogue, S > 1 writes partials at
 // s * (A * C) + o.
-template <class R, class LD, bool VEC>
+template <class R, class LD, bool VEC, bool SPLIT_X = false>
 __global__ void __launch_bounds__(kRThreads)
     k_cols(LD ld, int64_t A, int64_t B, int64_t C, int64_t rps, int64_t S, float* out, float* out2,
            int epi, float div, float* part) {
@@ -426,11 +426,11 @@ __global__ void __launch_bounds__(kRThreads)
     using T = typename R::T;
     constexpr int W = VEC ? 4 : 1;
     const int64_t AC = A * C;
-    const int64_t item = (int64_t)blockIdx.x * kRThreads + threadIdx.x;
+    const int64_t item = (int64_t)(SPLIT_X ? blockIdx.y : blockIdx.x) * kRThreads + threadIdx.x;
     const int64_t o = item * W;
     if (o >= AC) return;
     const int64_t a = o / C, c = o - a * C;
-    const int64_t s = blockIdx.y;
+    const int64_t s = SPLIT_X ? blockIdx.x : blockIdx.y;
     const int64_t b0 = s * rps;
     const int64_t b1 = (b0 + rps < B) ? b0 + rps : B;
     const int64_t base = a * B * C + c;
@@ -1134,8 +1134,9 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
     if (!nosplit && use_wide_cols(C, vec_ok)) {
         ColSplit cs = wide_split(A, B, C);
         const int64_t items = A * C / 4;
-        dim3 g((unsigned)((items + kRThreads - 1) / kRThreads), (unsigned)cs.S), b(kRThreads);
-        hipLaunchKernelGGL((k_cols<R, LD, true>), g, b, 0, st, ld, A, B, C, cs.rps, cs.S, out, out2, epi, div, tmp);
+        dim3 g((unsigned)cs.S, (unsigned)((items + kRThreads - 1) / kRThreads)), b(kRThreads);
+        hipLaunchKernelGGL((k_cols<R, LD, true, true>), g, b, 0, st, ld, A, B, C, cs.rps, cs.S, out, out2, epi, div,
+                           tmp);
         if (cs.S > 1) {  // combine the split partials in one launch (k_parts_comb)
             using PL = PartLoader<R>;
             const int64_t n = A * C, np = cs.S * n;
