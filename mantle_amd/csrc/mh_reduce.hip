@@ -862,7 +862,7 @@ __global__ void __launch_bounds__(kRThreads)
 
 // Combines of the split partials, in split order. Rows: one block per row, S partials
 // contiguous (thread-strided, then the waves' butterflies and the four waves in order).
-// Columns: one thread per line, partials at stride nlines.
+// Columns: partials at stride nlines, a block per 16 lines (below).
 __global__ void __launch_bounds__(kRThreads)
     k_tstd_mom_combine_rows(float* __restrict__ res, const Mom* __restrict__ part, int64_t S, int64_t B) {
     __shared__ Mom ws[4];
@@ -900,25 +900,40 @@ __global__ void __launch_bounds__(kRThreads)
 __global__ void __launch_bounds__(kRThreads)
     k_tstd_mom_combine_cols(float* __restrict__ res, const Mom* __restrict__ part, int64_t nlines, int64_t S,
                             int64_t B) {
-    const int64_t l = (int64_t)blockIdx.x * kRThreads + threadIdx.x;
-    if (l >= nlines) return;
+    // a block is 16 lines x 16 partial groups; group r adds the partials
+    // [r * rpg, min((r + 1) * rpg, S)) in order, eight in flight, then group 0 adds the 16
+    // group sums in group order from LDS
+    __shared__ Mom lds[16][16];
+    const int q = threadIdx.x & 15, r = threadIdx.x >> 4;
+    const int64_t l = (int64_t)blockIdx.x * 16 + q;
+    const bool active = l < nlines;
     Mom m{0.0, 0.0};
-    int64_t s = 0;
-    for (; s + 3 < S; s += 4) {  // four partials in flight, added in order
-        Mom q[4];
+    if (active) {
+        const int64_t rpg = (S + 15) / 16;
+        const int64_t s0 = r * rpg;
+        const int64_t s1 = s0 + rpg < S ? s0 + rpg : S;
+        for (int64_t s = s0; s < s1; s += 8) {
+            Mom v[8];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) q[u] = part[(s + u) * nlines + l];
+            for (int u = 0; u < 8; ++u)
+                if (s + u < s1) v[u] = part[(s + u) * nlines + l];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            m.s1 = m.s1 + q[u].s1;
-            m.s2 = m.s2 + q[u].s2;
+            for (int u = 0; u < 8; ++u)
+                if (s + u < s1) {
+                    m.s1 = m.s1 + v[u].s1;
+                    m.s2 = m.s2 + v[u].s2;
+                }
         }
     }
-    for (; s < S; ++s) {
-        m.s1 = m.s1 + part[s * nlines + l].s1;
-        m.s2 = m.s2 + part[s * nlines + l].s2;
+    lds[r][q] = m;
+    __syncthreads();
+    if (r == 0 && active) {
+        for (int rr = 1; rr < 16; ++rr) {
+            m.s1 = m.s1 + lds[rr][q].s1;
+            m.s2 = m.s2 + lds[rr][q].s2;
+        }
+        res[l] = mom_std(m, B);
     }
-    res[l] = mom_std(m, B);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1664,7 +1679,7 @@ int mh_tstd(float* res, const float* x, const mh_shape* psx, int32_t axis) {
     if (vec) hipLaunchKernelGGL(k_tstd_mom_cols<true>, g, b, 0, st, res, x, A, B, C, rps, S, part);
     else hipLaunchKernelGGL(k_tstd_mom_cols<false>, g, b, 0, st, res, x, A, B, C, rps, S, part);
     if (S > 1)
-        hipLaunchKernelGGL(k_tstd_mom_combine_cols, dim3((unsigned)((A * C + kRThreads - 1) / kRThreads)), b, 0, st,
+        hipLaunchKernelGGL(k_tstd_mom_combine_cols, dim3((unsigned)((A * C + 15) / 16)), b, 0, st,
                            res, part, A * C, S, B);
     return finish("mh_tstd");
 }
