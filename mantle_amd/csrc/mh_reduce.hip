@@ -465,6 +465,47 @@ __global__ void __launch_bounds__(kRThreads)
     }
 }
 
+// A pass over chunk partials (a row of at most kCombineMax elements per block, one block per
+// row): 1024 threads, each with all of its (up to eight) quads' loads in flight, so the row
+// takes one memory round trip; the sixteen wave results combine in wave order.
+constexpr int kCombThreads = 1024;
+template <class R, class LD, bool VEC>
+__global__ void __launch_bounds__(kCombThreads)
+    k_row_comb(LD ld, int64_t B, float* out, float* out2, int epi, float div) {
+    using T = typename R::T;
+    __shared__ T ws[kCombThreads / 64];
+    ld.setup();
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int64_t r = blockIdx.x, start = r * B;
+    T acc = R::init();
+    if (VEC) {
+        constexpr int U = 8;  // kCombineMax / (4 * kCombThreads)
+        T v[U][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t e = ((int64_t)u * kCombThreads + t) * 4;
+            if (e < B) ld.get4(start + e, v[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t e = ((int64_t)u * kCombThreads + t) * 4;
+            if (e < B)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc = R::comb(acc, v[u][j]);
+        }
+    } else {
+        for (int64_t e = t; e < B; e += kCombThreads) acc = R::comb(acc, ld.get(start + e));
+    }
+    acc = wave_reduce<R>(acc);
+    if (lane == 0) ws[w] = acc;
+    __syncthreads();
+    if (t == 0) {
+        T tot = ws[0];
+        for (int k = 1; k < kCombThreads / 64; ++k) tot = R::comb(tot, ws[k]);
+        epi_store(out, out2, r, tot, epi, div);
+    }
+}
+
 // Combine of S split partials [S, n] (n % 4 == 0) in one launch with few memory round trips:
 // a block is 16 column quads x 16 row groups; group r adds the partial rows
 // [r * rpg, min((r + 1) * rpg, S)) in order, eight rows' loads in flight, and group 0 adds the
@@ -1022,7 +1063,8 @@ static inline size_t pad64(size_t v) { return (v + 63) & ~(size_t)63; }
 // row, longer rows kRowChunk-element block chunks whose partials reduce again the same way.
 // A pass over partials (`combine`) takes rows of up to kCombineMax elements in one block
 // each (one launch for the combine instead of a chain).
-constexpr int64_t kCombineMax = 16384;
+constexpr int64_t kCombineMax = 32768;
+static_assert(kCombineMax == 8 * 4 * kCombThreads, "k_row_comb loads eight quads per thread");
 static inline bool rows_chunked(int64_t B) { return B >= 2048; }
 static inline int64_t row_chunks(int64_t B, bool combine) {
     if (combine && B <= kCombineMax) return 1;
@@ -1134,6 +1176,12 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
             return MH_OK;
         }
         const int64_t S = row_chunks(B, combine);
+        if (combine && S == 1 && A <= 0x7fffffff) {  // one block per row (k_row_comb)
+            dim3 g((unsigned)A), b(kCombThreads);
+            if (vec) hipLaunchKernelGGL((k_row_comb<R, LD, true>), g, b, 0, st, ld, B, out, out2, epi, div);
+            else hipLaunchKernelGGL((k_row_comb<R, LD, false>), g, b, 0, st, ld, B, out, out2, epi, div);
+            return MH_OK;
+        }
         const int64_t L = S == 1 ? B : kRowChunk;
         const int64_t nv = A * S;
         dim3 g((unsigned)nv), b(kRThreads);
