@@ -228,7 +228,10 @@ RED_CASES = [((87, 73, 107), 0), ((87, 73, 107), 1), ((87, 73, 107), 2), ((87, 7
              ((1000, 20), 1), ((513, 32), 1), ((1001, 3), 1), ((300, 1), 1), ((257, 16), 1), ((40, 33), 1),
              ((30,), None), ((2, 3, 17), 2), ((5, 16384), 1), ((3, 4100), 1), ((7, 2052), 1), ((16, 36), 1),
              ((300, 256), 0), ((33, 512, 128), 1), ((4, 8, 1024), 0), ((2, 5000, 132), 1), ((9000, 64), 0),
-             ((3, 12000), None)]
+             ((3, 12000), None),
+             # chunk-partial combines of 16386 (odd quads: the scalar pass) and 20000 partials, and
+             # a wide column split whose last partial group is short
+             ((2048 * 16385 + 4,), None), ((2048 * 20000,), None), ((3, 3000, 1024), 1)]
 
 
 @pytest.mark.parametrize("shape,axis", RED_CASES, ids=[f"{s}-ax{a}" for s, a in RED_CASES])
