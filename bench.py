@@ -240,27 +240,31 @@ def isolated_floor(d, reps):
 
 
 def op_report(ops, med, iso=None, hbm=None):
-    """Per op: ms, GB/s and frac of its algorithmic bytes; with `iso`, the isolated figures;
-    with `hbm` ({label: bytes}), the bytes the op moves where they are fewer than the
-    algorithmic count (a sparse accumulation that stores only the quads it changes) and the
-    rate of those bytes."""
+    """Per op: ms, GB/s and frac of its algorithmic bytes; with `iso`, the isolated figures.
+    With `hbm` ({label: bytes}): ops that move fewer bytes than the algorithmic count (a sparse
+    accumulation that stores only the quads it changes) report GB/s and frac over the bytes
+    they move, which cannot pass the peak, and the algorithmic rate beside them as
+    GB/s_effective / frac_effective."""
     out = {}
     for label, _, nbytes in ops:
         t = med[label]
-        gbs = nbytes / (t * 1e-3) / 1e9
+        moved = hbm[label] if hbm and label in hbm else nbytes
+        gbs = moved / (t * 1e-3) / 1e9
         out[label] = {"ms": round(t, 4), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
         if iso is not None:
             ti = iso[label]
             out[label]["ms_isolated"] = round(ti, 4)
-            out[label]["frac_isolated"] = round(nbytes / (ti * 1e-3) / 1e9 / PEAK_GBS, 4)
-        if hbm and label in hbm:
-            hg = hbm[label] / (t * 1e-3) / 1e9
-            out[label].update({"hbm_bytes": hbm[label], "GB/s_hbm": round(hg, 1), "frac_hbm": round(hg / PEAK_GBS, 4)})
+            out[label]["frac_isolated"] = round(moved / (ti * 1e-3) / 1e9 / PEAK_GBS, 4)
+        if moved != nbytes:
+            eg = nbytes / (t * 1e-3) / 1e9
+            out[label].update({"algorithmic_bytes": nbytes, "hbm_bytes": moved, "GB/s_effective": round(eg, 1),
+                               "frac_effective": round(eg / PEAK_GBS, 4)})
     return out
 
 
-def total_report(ops, med, iso=None):
-    tot_b = sum(b for _, _, b in ops)
+def total_report(ops, med, iso=None, hbm=None):
+    """Sum over ops of op_report's bytes (moved bytes for sparse ops) and times."""
+    tot_b = sum(hbm[label] if hbm and label in hbm else b for label, _, b in ops)
     tot_t = sum(med[label] for label, _, _ in ops)
     gbs = tot_b / (tot_t * 1e-3) / 1e9
     out = {"bytes": tot_b, "ms": round(tot_t, 4), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
@@ -447,7 +451,7 @@ def run_c4(L, reps):
     fwd = [o for o in ops if o[0].endswith(".fwd")]
     bwd = [o for o in ops if o[0].endswith(".bwd")]
     return {"buffer_sets": len(sets), "ops": op_report(ops, med, iso, hbm), "fwd_total": total_report(fwd, med, iso),
-            "bwd_total": total_report(bwd, med, iso)}
+            "bwd_total": total_report(bwd, med, iso, hbm)}
 
 
 # ---------------------------------------------------------------------------------------

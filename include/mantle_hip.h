@@ -131,7 +131,9 @@ int mh_binary_bwd_accum(int op, int tensor_id, float* grad, const mh_shape* sgra
 /* Both operand gradients of a same-shape ADD/SUB/MUL/DIV in one pass (the two
  * backward_op calls that Model.backward makes when both operands are trainable,
  * model.mojo:233-270). Requires s1 == s2 == sug; either grad pointer may be NULL to skip
- * that operand. */
+ * that operand. grad1 == grad2 (one symbol as both operands, x * x) accumulates both
+ * gradients into it, operand 0's first: grad = (grad + rg0) + rg1, as the two calls do.
+ * Gradient ranges that overlap without being equal run as the two calls, id 0 then id 1. */
 int mh_binary_bwd_accum2(int op, float* grad1, float* grad2, const float* ug,
                          const float* t1, const float* t2, const mh_shape* s);
 

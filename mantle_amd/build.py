@@ -78,6 +78,27 @@ def build_hip(verbose: bool = False) -> str:
     return LIB
 
 
+def build_hip_host_sanitized() -> str:
+    """libmantle_hip.so with AddressSanitizer and UBSan on the host code only (the shape checks,
+    launch planning, graph builder and model bookkeeping), into mantle_amd/_san/. The GPU code
+    is built as usual (GPU sanitizers are not used). For tests/sanitize_cpu.py."""
+    hipcc = _hipcc()
+    out_dir = os.path.join(PKG, "_san")
+    os.makedirs(out_dir, exist_ok=True)
+    san = ["-g", "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+           "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer"]
+    srcs = sources()
+    objs = [os.path.join(out_dir, os.path.basename(s)[:-4] + ".o") for s in srcs]
+    jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")) or 1)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        for f in [ex.submit(_run, [hipcc, *HIP_FLAGS, *san, "-c", s, "-o", o]) for s, o in zip(srcs, objs)]:
+            f.result()
+    lib = os.path.join(out_dir, "libmantle_hip.so")
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-Xarch_host", "-fsanitize=address", "-Xarch_host",
+          "-fsanitize=undefined", "-o", lib, *objs])
+    return lib
+
+
 def build_oracle() -> str:
     """Build the CPU restatement used by the tests as the parity checker."""
     _run(["make", "-s", "-C", os.path.join(ROOT, "oracle")])

@@ -556,8 +556,10 @@ __global__ void __launch_bounds__(kThreads)
 
 // Fused two-operand backward of a same-shape binary op (both backward_op calls of
 // ops.mojo:408-463 with equal shapes): g1 = g1 + rg0, g2 = g2 + rg1. One quad per thread per
-// iteration, as k_same4.
-template <int OP>
+// iteration, as k_same4. ALIAS: both operands are one symbol (x * x, x + x), so both calls
+// accumulate into one gradient, id 0 first (model.mojo:233-270): g1 = (g1 + rg0) + rg1, and
+// g2 is not used.
+template <int OP, bool ALIAS = false>
 __global__ void __launch_bounds__(kThreads)
     k_bwd2_same4(float* __restrict__ g1, float* __restrict__ g2, const float* __restrict__ ug,
                  const float* __restrict__ a, const float* __restrict__ b, int64_t n) {
@@ -574,7 +576,7 @@ __global__ void __launch_bounds__(kThreads)
             vb = reinterpret_cast<const float4*>(b)[q];
         }
         const float4 v1 = reinterpret_cast<const float4*>(g1)[q];
-        const float4 v2 = reinterpret_cast<const float4*>(g2)[q];
+        const float4 v2 = ALIAS ? v1 : reinterpret_cast<const float4*>(g2)[q];
         float r1[4], r2[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -584,18 +586,26 @@ __global__ void __launch_bounds__(kThreads)
             float x0[3] = {uu, bb, 0.0f};  // id0 reads t2
             float x1[3] = {uu, aa, bb};    // id1 reads t1 (and t2 for DIV)
             r1[j] = comp(v1, j) + f0(x0);
-            r2[j] = comp(v2, j) + f1(x1);
+            r2[j] = ALIAS ? r1[j] + f1(x1) : comp(v2, j) + f1(x1);
         }
-        reinterpret_cast<float4*>(g1)[q] = make_float4(r1[0], r1[1], r1[2], r1[3]);
-        reinterpret_cast<float4*>(g2)[q] = make_float4(r2[0], r2[1], r2[2], r2[3]);
+        if (ALIAS) {
+            reinterpret_cast<float4*>(g1)[q] = make_float4(r2[0], r2[1], r2[2], r2[3]);
+        } else {
+            reinterpret_cast<float4*>(g1)[q] = make_float4(r1[0], r1[1], r1[2], r1[3]);
+            reinterpret_cast<float4*>(g2)[q] = make_float4(r2[0], r2[1], r2[2], r2[3]);
+        }
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         for (int64_t i = nq << 2; i < n; ++i) {
             const float aa = NEED_AB ? a[i] : 0.0f, bb = NEED_AB ? b[i] : 0.0f;
             float x0[3] = {ug[i], bb, 0.0f};
             float x1[3] = {ug[i], aa, bb};
-            g1[i] = g1[i] + f0(x0);
-            g2[i] = g2[i] + f1(x1);
+            if (ALIAS) {
+                g1[i] = (g1[i] + f0(x0)) + f1(x1);
+            } else {
+                g1[i] = g1[i] + f0(x0);
+                g2[i] = g2[i] + f1(x1);
+            }
         }
     }
 }
@@ -1009,9 +1019,15 @@ int mh_binary_bwd_accum2(int op, float* grad1, float* grad2, const float* ug, co
     MH_TRY(check_op_binary(op));
     MH_TRY(check_shape(s, "shape"));
     if (!grad1 && !grad2) return MH_OK;
-    if (!grad1 || !grad2 || is_scalar_shape(s) || numel(s) == 0 ||
+    const int64_t nel = numel(s);
+    // the two gradient ranges: the same tensor (one fused pass, id 0's sum first), or
+    // overlapping without being equal (the two backward_op calls one after the other)
+    const bool alias = grad1 && grad1 == grad2;
+    const bool overlap = grad1 && grad2 && !alias && grad1 < grad2 + nel && grad2 < grad1 + nel;
+    if (!grad1 || !grad2 || overlap || is_scalar_shape(s) || nel == 0 ||
         !(aligned16(grad1) && aligned16(grad2) && aligned16(ug) && aligned16(t1) && aligned16(t2))) {
-        // one operand, a graph scalar (DIV's scalar rule), empty or unaligned: per operand
+        // one operand, overlapping grads, a graph scalar (DIV's scalar rule), empty or
+        // unaligned: per operand, id 0 then id 1 (model.mojo:233-270)
         if (grad1) MH_TRY(mh_binary_bwd_accum(op, 0, grad1, &s, ug, &s, t1, &s, t2, &s));
         if (grad2) MH_TRY(mh_binary_bwd_accum(op, 1, grad2, &s, ug, &s, t1, &s, t2, &s));
         return MH_OK;
@@ -1019,9 +1035,18 @@ int mh_binary_bwd_accum2(int op, float* grad1, float* grad2, const float* ug, co
     const bool need_ab = op == MH_MUL || op == MH_DIV;
     if (!ug || (need_ab && (!t1 || !t2))) return fail(MH_ERR_NULL, "mh_binary_bwd_accum2: null tensor");
     MH_TRY(require_init());
-    const int64_t n = numel(s);
+    const int64_t n = nel;
     dim3 g(grid_for(n >> 2, kThreads)), b(kThreads);
     hipStream_t st = ctx().stream;
+    if (alias) {  // g2 is not read: pass a null pointer so no access can go through it
+        switch (op) {
+            case MH_ADD: hipLaunchKernelGGL((k_bwd2_same4<MH_ADD, true>), g, b, 0, st, grad1, nullptr, ug, t1, t2, n); break;
+            case MH_SUB: hipLaunchKernelGGL((k_bwd2_same4<MH_SUB, true>), g, b, 0, st, grad1, nullptr, ug, t1, t2, n); break;
+            case MH_MUL: hipLaunchKernelGGL((k_bwd2_same4<MH_MUL, true>), g, b, 0, st, grad1, nullptr, ug, t1, t2, n); break;
+            default: hipLaunchKernelGGL((k_bwd2_same4<MH_DIV, true>), g, b, 0, st, grad1, nullptr, ug, t1, t2, n); break;
+        }
+        return finish("mh_binary_bwd_accum2");
+    }
     switch (op) {
         case MH_ADD: hipLaunchKernelGGL(k_bwd2_same4<MH_ADD>, g, b, 0, st, grad1, grad2, ug, t1, t2, n); break;
         case MH_SUB: hipLaunchKernelGGL(k_bwd2_same4<MH_SUB>, g, b, 0, st, grad1, grad2, ug, t1, t2, n); break;

@@ -193,6 +193,9 @@ __global__ void __launch_bounds__(kFThreads)
         }
         ticket = __shfl(ticket, 0);
         if (ticket == (uint32_t)(nper - 1)) {  // the channel's last partial: sum them all
+            // acquire: the other waves' partials (stored before their tickets) are visible
+            // to the loads below; one cache invalidate, on the last arriver only
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
             float s = 0.0f;
             for (int64_t i = lane; i < nper; i += 64)
                 s = s + __hip_atomic_load(&part[i * C + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

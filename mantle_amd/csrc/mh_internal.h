@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <cstring>
 #include <type_traits>
+#include <vector>
 
 #include "../../include/mantle_hip.h"
 
@@ -31,18 +32,34 @@ struct Context {
     uint32_t* tickets = nullptr;  // zeroed arrival counters of single-launch reductions
     int64_t ntickets = 0;
     int num_cus = 256;
+    // Captured HIP graphs hold the addresses of scratch, stage and tickets. While any exists,
+    // a buffer that grows is retired (kept allocated) instead of freed, so that every graph
+    // still points at live memory; retired buffers are freed when the last graph is
+    // released, or at mh_shutdown.
+    int64_t graphs_live = 0;
+    std::vector<void*> retired;
+    uint64_t epoch = 0;  // bumped by every mh_init: a graph replays only in its own epoch
 };
 Context& ctx();
+// A captured graph that holds library buffer addresses comes into / goes out of existence;
+// graph_release takes the epoch the graph was captured in (graphs of an earlier epoch no
+// longer count: mh_shutdown freed what they pointed at).
+void graph_retain();
+int graph_release(uint64_t epoch);
 
 // Error reporting: records a thread-local message and returns `code`.
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-// Wraps every HIP runtime call. MANTLE_HIP_FAIL_AT=<n> makes the n-th wrapped call fail
-// (failure-path tests without a GPU fault).
+// Checks the result of a HIP runtime call.
 int hip_check(hipError_t e, const char* what);
-#define MH_HIP(call)                                      \
-    do {                                                  \
-        int rc__ = ::mh::hip_check((call), #call);        \
-        if (rc__ != MH_OK) return rc__;                   \
+// Failure injection for failure-path tests without a GPU fault: with MANTLE_HIP_FAIL_AT=<n>
+// in the environment at mh_init, the n-th HIP call wrapped by MH_HIP after that init is not
+// made and fails with MH_ERR_HIP instead, as if the runtime had refused it.
+int hip_inject(const char* what);
+#define MH_HIP(call)                                        \
+    do {                                                    \
+        int rc__ = ::mh::hip_inject(#call);                 \
+        if (rc__ == MH_OK) rc__ = ::mh::hip_check((call), #call); \
+        if (rc__ != MH_OK) return rc__;                     \
     } while (0)
 #define MH_TRY(expr)                    \
     do {                                \

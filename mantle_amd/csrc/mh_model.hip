@@ -59,7 +59,8 @@ struct mh_model {
     };
     std::vector<RowGroup> rows;
     std::vector<int> row_of;  // per node: its RowGroup, or -1
-    hipGraphExec_t graph[2] = {nullptr, nullptr};  // captured passes (MH_PASS_FORWARD / _BACKWARD)  // per node: 1 = ADD fused with the next node (RELU), 2 = that RELU
+    hipGraphExec_t graph[2] = {nullptr, nullptr};  // captured passes (MH_PASS_FORWARD / _BACKWARD)
+    uint64_t graph_epoch[2] = {0, 0};               // the mh_init epoch each was captured in
 };
 
 namespace mh {
@@ -375,8 +376,9 @@ static int run_backward_node(mh_model* m, size_t i) {
         const mh_shape& s2 = g.syms[in[1]].shape;
         float* g1 = m->gr[in[0]];
         float* g2 = m->gr[in[1]];
-        if (g1 && g2 && in[0] != in[1] && shape_eq(s1, s2) && shape_eq(s1, so))
-            return mh_binary_bwd_accum2(nd.op, g1, g2, ug, t1, t2, &s1);  // same result, one pass
+        // same result, one pass (also for one symbol used twice: one gradient, id 0's part first)
+        if (g1 && g2 && shape_eq(s1, s2) && shape_eq(s1, so))
+            return mh_binary_bwd_accum2(nd.op, g1, g2, ug, t1, t2, &s1);
         if (g1) MH_TRY(mh_binary_bwd_accum(nd.op, 0, g1, &s1, ug, &so, t1, &s1, t2, &s2));
         if (g2) MH_TRY(mh_binary_bwd_accum(nd.op, 1, g2, &s2, ug, &so, t1, &s1, t2, &s2));
         return MH_OK;
@@ -435,9 +437,12 @@ static int enqueue_pass(mh_model* m, int pass) {
 }
 
 static void drop_graphs(mh_model* m) {
-    for (auto& e : m->graph) {
-        if (e) (void)hipGraphExecDestroy(e);
-        e = nullptr;
+    for (int p = 0; p < 2; ++p) {
+        if (m->graph[p]) {
+            (void)hipGraphExecDestroy(m->graph[p]);
+            (void)graph_release(m->graph_epoch[p]);
+        }
+        m->graph[p] = nullptr;
     }
 }
 
@@ -705,8 +710,13 @@ int mh_model_capture(mh_model* m, int pass) {
     const hipError_t e2 = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);
     MH_HIP(e2);
-    if (m->graph[pass]) (void)hipGraphExecDestroy(m->graph[pass]);
+    if (m->graph[pass]) {
+        (void)hipGraphExecDestroy(m->graph[pass]);
+        (void)graph_release(m->graph_epoch[pass]);
+    }
+    graph_retain();
     m->graph[pass] = exec;
+    m->graph_epoch[pass] = ctx().epoch;
     return MH_OK;
 }
 
@@ -715,6 +725,9 @@ int mh_model_replay(mh_model* m, int pass) {
     MH_TRY(require_init());
     if (pass != MH_PASS_FORWARD && pass != MH_PASS_BACKWARD) return fail(MH_ERR_INVALID, "unknown pass %d", pass);
     if (!m->graph[pass]) return fail(MH_ERR_INVALID, "mh_model_replay: pass %d has not been captured", pass);
+    if (m->graph_epoch[pass] != ctx().epoch)
+        return fail(MH_ERR_INVALID, "mh_model_replay: pass %d was captured before the last mh_shutdown; capture it again",
+                    pass);
     MH_HIP(hipGraphLaunch(m->graph[pass], ctx().stream));
     return finish("mh_model_replay");
 }

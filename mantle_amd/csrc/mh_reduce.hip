@@ -1194,7 +1194,9 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
         }
         return MH_OK;
     }
-    if (!nosplit && use_wide_cols(C, vec_ok)) {
+    // the wide layout puts the column-quad blocks on grid y (at most 65535 blocks there);
+    // larger outputs take the k_cols launch below (quad blocks on x, splits on y)
+    if (!nosplit && use_wide_cols(C, vec_ok) && (A * C / 4 + kRThreads - 1) / kRThreads <= 65535) {
         ColSplit cs = wide_split(A, B, C);
         const int64_t items = A * C / 4;
         dim3 g((unsigned)cs.S, (unsigned)((items + kRThreads - 1) / kRThreads)), b(kRThreads);
@@ -1386,6 +1388,9 @@ __global__ void __launch_bounds__(kRThreads)
     }
     ticket = __shfl(ticket, 0);
     if (ticket != (uint32_t)(nper - 1)) return;
+    // acquire on the last arriver only: the partials stored before the other tickets are
+    // visible to the loads below
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     float s = 0.0f;
     for (int64_t i = lane; i < nper; i += 64)
         s = s + __hip_atomic_load(&part[i * C + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -15,7 +15,7 @@ Context& ctx() {
 
 static thread_local char g_err[512] = "";
 static long g_fail_at = -2;  // -2: env not read yet, -1: no injection
-static long g_hip_calls = 0;
+static long g_hip_calls = 0;  // MH_HIP calls since the environment was last read
 
 int fail(int code, const char* fmt, ...) {
     va_list ap;
@@ -25,14 +25,21 @@ int fail(int code, const char* fmt, ...) {
     return code;
 }
 
-int hip_check(hipError_t e, const char* what) {
-    if (g_fail_at == -2) {
-        const char* s = getenv("MANTLE_HIP_FAIL_AT");
-        g_fail_at = s ? atol(s) : -1;
-    }
+static void read_fail_env() {
+    const char* s = getenv("MANTLE_HIP_FAIL_AT");
+    g_fail_at = s ? atol(s) : -1;
+    g_hip_calls = 0;
+}
+
+int hip_inject(const char* what) {
+    if (g_fail_at == -2) read_fail_env();
     ++g_hip_calls;
     if (g_fail_at > 0 && g_hip_calls == g_fail_at)
         return fail(MH_ERR_HIP, "%s: injected failure (MANTLE_HIP_FAIL_AT=%ld)", what, g_fail_at);
+    return MH_OK;
+}
+
+int hip_check(hipError_t e, const char* what) {
     if (e != hipSuccess) return fail(MH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
     return MH_OK;
 }
@@ -51,14 +58,52 @@ int finish(const char* what) {
     return MH_OK;
 }
 
-static int grow(void** buf, size_t* have, size_t bytes, void** out) {
+// Gives up a library buffer that is being replaced: freed, or retired while a captured graph
+// may still use it.
+static int drop_buffer(void* buf) {
     Context& c = ctx();
+    if (!buf) return MH_OK;
+    if (c.graphs_live > 0) {
+        c.retired.push_back(buf);
+        return MH_OK;
+    }
+    int rc = hip_inject("hipStreamSynchronize");
+    if (rc == MH_OK) rc = hip_check(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    if (rc == MH_OK) rc = hip_inject("hipFree");
+    if (rc == MH_OK) rc = hip_check(hipFree(buf), "hipFree");
+    if (rc != MH_OK) c.retired.push_back(buf);  // not freed here: mh_shutdown frees it
+    return rc;
+}
+
+static int free_retired() {
+    Context& c = ctx();
+    if (c.retired.empty()) return MH_OK;
+    if (c.stream) MH_HIP(hipStreamSynchronize(c.stream));
+    int rc = MH_OK;
+    for (void* p : c.retired) {
+        const int r = hip_check(hipFree(p), "hipFree(retired library buffer)");
+        if (rc == MH_OK) rc = r;
+    }
+    c.retired.clear();
+    return rc;
+}
+
+void graph_retain() { ++ctx().graphs_live; }
+
+int graph_release(uint64_t epoch) {
+    Context& c = ctx();
+    if (!c.initialized || epoch != c.epoch || c.graphs_live <= 0) return MH_OK;
+    if (--c.graphs_live == 0) return free_retired();
+    return MH_OK;
+}
+
+static int grow(void** buf, size_t* have, size_t bytes, void** out) {
     if (bytes > *have) {
         if (*buf) {
-            MH_HIP(hipStreamSynchronize(c.stream));
-            MH_HIP(hipFree(*buf));
+            void* old = *buf;
             *buf = nullptr;
             *have = 0;
+            MH_TRY(drop_buffer(old));
         }
         size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
         want = (want + 255) & ~(size_t)255;
@@ -79,19 +124,25 @@ int tickets(int64_t n, uint32_t** out) {
     if (n > c.ntickets) {
         int64_t want = n < 65536 ? 65536 : n;
         if (c.tickets) {
-            MH_HIP(hipStreamSynchronize(c.stream));
-            MH_HIP(hipFree(c.tickets));
+            void* old = c.tickets;
             c.tickets = nullptr;
             c.ntickets = 0;
+            MH_TRY(drop_buffer(old));  // a retired ticket buffer stays all-zero: kernels reset what they take
         }
-        MH_HIP(hipMalloc(reinterpret_cast<void**>(&c.tickets), (size_t)want * sizeof(uint32_t)));
-        c.ntickets = want;
+        uint32_t* nb = nullptr;
+        MH_HIP(hipMalloc(reinterpret_cast<void**>(&nb), (size_t)want * sizeof(uint32_t)));
         // all-zero bits: a fill kernel of 0.0f (no memset node if a caller captures a graph)
         const uint64_t saved = c.flags;
         c.flags |= MH_INIT_ASYNC;
-        const int rc = launch_fill(reinterpret_cast<float*>(c.tickets), 0.0f, want);
+        const int rc = launch_fill(reinterpret_cast<float*>(nb), 0.0f, want);
         c.flags = saved;
-        MH_TRY(rc);
+        if (rc != MH_OK) {  // never keep counters that may not be zero
+            (void)hipStreamSynchronize(c.stream);
+            (void)hipFree(nb);
+            return rc;
+        }
+        c.tickets = nb;
+        c.ntickets = want;
     }
     *out = c.tickets;
     return MH_OK;
@@ -359,6 +410,7 @@ int mh_device_count(int* count) {
 
 int mh_init(int device, uint64_t flags) {
     Context& c = ctx();
+    read_fail_env();  // failure injection counts from here
     if (c.initialized) {
         if (c.device == device) {
             c.flags = flags;
@@ -380,6 +432,7 @@ int mh_init(int device, uint64_t flags) {
     c.num_cus = prop.multiProcessorCount;
     c.device = device;
     c.flags = flags;
+    ++c.epoch;
     c.initialized = true;
     return MH_OK;
 }
@@ -397,6 +450,8 @@ int mh_shutdown(void) {
     if (c.tickets) MH_HIP(hipFree(c.tickets));
     c.tickets = nullptr;
     c.ntickets = 0;
+    MH_TRY(free_retired());  // graphs captured before this point can no longer replay (epoch)
+    c.graphs_live = 0;
     MH_HIP(hipStreamDestroy(c.stream));
     c.stream = nullptr;
     c.initialized = false;

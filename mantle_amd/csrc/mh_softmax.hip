@@ -374,6 +374,8 @@ __device__ __forceinline__ void loss_tail(float tot, float* part, uint32_t* tick
     }
     tk = __shfl(tk, 0);
     if (tk != (uint32_t)(members - 1)) return;  // uniform across the wavefront
+    // acquire on the group's last arriver: the members' partials are visible below
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     float v = lane < members ? __hip_atomic_load(&part[g0 + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
 #pragma unroll
     for (int mm = 32; mm >= 1; mm >>= 1) v = v + __shfl_xor(v, mm);
@@ -385,6 +387,7 @@ __device__ __forceinline__ void loss_tail(float tot, float* part, uint32_t* tick
     }
     tk = __shfl(tk, 0);
     if (tk != (uint32_t)(ngroups - 1)) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the group sums are visible below
     float w = lane < ngroups ? __hip_atomic_load(&part[nparts + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                              : 0.0f;
 #pragma unroll

@@ -378,7 +378,9 @@ def backward_op(tensor_id: int, op: int, ug: Tensor, t1: Tensor, t2: Optional[Te
 
 def backward_op_both(op: int, ug: Tensor, t1: Tensor, t2: Tensor, grad1: Optional[Tensor],
                      grad2: Optional[Tensor]) -> None:
-    """Both backward_op calls of a same-shape binary op in one fused pass."""
+    """Both backward_op calls of a same-shape binary op in one fused pass. grad1 and grad2 may be
+    the same tensor (an op over one symbol twice, x * x): both gradients then accumulate into it,
+    operand 0's first, as the two calls of Model.backward do (model.mojo:233-270)."""
     if t1.shape() != t2.shape() or ug.shape() != t1.shape():
         if grad1 is not None:
             backward_op(0, op, ug, t1, t2, grad1)

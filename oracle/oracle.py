@@ -14,7 +14,8 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# MANTLE_ORACLE_LIB: another build of the same source (the sanitizer build, oracle/_san/)
+_LIB_PATH = os.environ.get("MANTLE_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 
 # Mantle OP ids (mantle/autograd/ops/ops.mojo:57-83).
 ADD, SUB, MUL, DIV, EXP, LOG, POW = 0, 1, 2, 3, 4, 5, 6

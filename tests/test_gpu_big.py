@@ -92,3 +92,26 @@ def test_broadcasts_past_2_31(m):
     m.backward_op(1, m.OP.SUB, ug, y, mxr, g)
     for r0 in (0, R2 - 8):
         assert (_slice(m, g, r0, 8) == np.float32(-10.0)).all(), r0
+
+
+def test_axis0_reduce_past_the_wide_column_grid(m):
+    """Axis-0 SUM and MAX of [4, C] with C / 4 = 16 777 217 column quads: 65 537 blocks of 256,
+    past the 65 535 the wide column layout can put on grid y, so the reduction takes the other
+    column launch. Column slices at the start, middle and end are checked against the four
+    downloaded rows: MAX bit-exact, SUM within the rtol class of the fp64 sum (4 terms)."""
+    from util import assert_sum_close
+    C = 67_108_868
+    print(f"[big] axis-0 reduce of [4, {C}]", flush=True)
+    x = _rand(m, (4, C), 41)
+    s = m.Tensor(m.TensorShape(1, C))
+    mx = m.Tensor(m.TensorShape(1, C))
+    m.forward_op(m.OP.SUM, s, x, attributes={"axis": 0})
+    m.forward_op(m.OP.MAX, mx, x, attributes={"axis": 0})
+    for start in (0, C // 2 + 1, C - 70):
+        rows = np.stack([_slice(m, x, r * C + start, 70) for r in range(4)])
+        want_max = rows.max(axis=0)
+        assert (_slice(m, mx, start, 70).view(np.uint32) == want_max.view(np.uint32)).all(), start
+        seq = ((rows[0] + rows[1]) + rows[2]) + rows[3]
+        r64 = rows.astype(np.float64)
+        assert_sum_close(_slice(m, s, start, 70), seq, r64.sum(axis=0), f"column sums at {start}",
+                         terms_abs=np.abs(r64).sum(axis=0))

@@ -47,3 +47,155 @@ def test_shutdown_then_init_again():
     third = run()  # counters left at zero by the second run
     for a, b in zip(first, third):
         assert (np.asarray(a).view(np.uint32) == np.asarray(b).view(np.uint32)).all()
+
+
+def _sequence(m, L):
+    """init, a device-generated [8192, 4096] input, an axis-0 SUM (library scratch), a config-3
+    shaped bias gradient (arrival counters), a download, frees and shutdown, stopping at the
+    first call that fails. Returns (name of the failing call or None, its code, its message,
+    the downloaded sums)."""
+    import ctypes
+    allocated = []
+    sums = np.zeros(4096, np.float32)
+    fail = (None, 0, "")
+
+    def call(name, *args):
+        rc = getattr(L, name)(*args)
+        if rc != 0:
+            raise _Stop(name, rc, L.mh_last_error().decode())
+
+    try:
+        call("mh_init", 0, 0)
+        ptrs = {}
+        for key, n in (("x", 8192 * 4096), ("res", 4096), ("ug", 8 * 32 * 28 * 28), ("gb", 32)):
+            p = ctypes.c_void_p()
+            call("mh_malloc", ctypes.byref(p), n * 4)
+            allocated.append(p.value)
+            ptrs[key] = p.value
+        call("mh_rand_uniform", ptrs["x"], 8192 * 4096, 5, ctypes.c_float(-1.0), ctypes.c_float(1.0))
+        call("mh_rand_normal", ptrs["ug"], 8 * 32 * 28 * 28, 6, ctypes.c_float(0.0), ctypes.c_float(1.0))
+        call("mh_zero", ptrs["gb"], 32)
+        sx = m.TensorShape(8192, 4096).c()
+        call("mh_reduce_fwd", 8, ptrs["res"], ptrs["x"], ctypes.byref(sx), 0)
+        s_ug, s_b = m.TensorShape(8, 32, 28, 28).c(), m.TensorShape(1, 32, 1, 1).c()
+        call("mh_binary_bwd_accum", 0, 1, ptrs["gb"], ctypes.byref(s_b), ptrs["ug"], ctypes.byref(s_ug),
+             ptrs["ug"], ctypes.byref(s_ug), ptrs["gb"], ctypes.byref(s_b))
+        call("mh_memcpy_d2h", sums.ctypes.data, ptrs["res"], 4096 * 4)
+    except _Stop as e:
+        fail = e.args
+    for p in allocated:  # a failed free is retried: each injected failure happens once
+        if L.mh_free(p) != 0:
+            assert L.mh_free(p) == 0
+    if L.mh_shutdown() != 0:
+        assert L.mh_shutdown() == 0, L.mh_last_error().decode()
+    return fail + (sums,)
+
+
+class _Stop(Exception):
+    pass
+
+
+def test_injected_hip_failures_return_cleanly():
+    """MANTLE_HIP_FAIL_AT=k makes the k-th HIP runtime call after mh_init fail without being
+    made. For every k up to the length of a whole sequence of library calls, exactly the call
+    that reaches it returns MH_ERR_HIP with a message naming the injection (no crash, no
+    fault); the frees and mh_shutdown afterwards succeed (retried once where the injection hit
+    them), the device memory in use returns to its level before the loop, and a clean run
+    after all of them gives the same bits as the first."""
+    import ctypes
+    import os
+    hip = ctypes.CDLL("/opt/rocm/lib/libamdhip64.so")
+
+    def free_bytes():
+        free, total = ctypes.c_size_t(), ctypes.c_size_t()
+        assert hip.hipDeviceSynchronize() == 0
+        assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+        return free.value
+
+    eng = GpuEngine()
+    m = eng.m
+    L = m.lib()
+    m._lib.call("mh_shutdown")
+    free0 = free_bytes()
+    hit = []
+    try:
+        os.environ["MANTLE_HIP_FAIL_AT"] = "0"
+        name, code, msg, clean = _sequence(m, L)
+        assert name is None, (name, code, msg)
+        for k in range(1, 200):
+            os.environ["MANTLE_HIP_FAIL_AT"] = str(k)
+            print(f"[fail-at] k={k}", flush=True)
+            name, code, msg, _ = _sequence(m, L)
+            if name is None:
+                break
+            assert code == -7 and "injected failure" in msg, (k, name, code, msg)
+            hit.append(name)
+        else:
+            raise AssertionError("the sequence never ran clean")
+        os.environ["MANTLE_HIP_FAIL_AT"] = "0"
+        name, code, msg, again = _sequence(m, L)
+        assert name is None
+    finally:
+        os.environ.pop("MANTLE_HIP_FAIL_AT", None)
+        m.init(0)
+    assert (again.view(np.uint32) == clean.view(np.uint32)).all()
+    # the injection reached the init, the allocations, the growth of scratch and counters and
+    # the end-of-call checks
+    assert {"mh_init", "mh_malloc", "mh_reduce_fwd", "mh_binary_bwd_accum"} <= set(hit), sorted(set(hit))
+    drift = free0 - free_bytes()
+    print(f"[fail-at] {len(hit)} injected failures, free-memory drift {drift} bytes", flush=True)
+    assert drift < (8 << 20), drift
+
+
+def test_graph_replay_survives_buffer_growth_and_refuses_after_shutdown():
+    """A captured pass keeps using the library buffers it was captured with: an op that grows
+    scratch between capture and replay (an axis-0 SUM of [8192, 8192], 4 MiB of partials) leaves
+    every replay bit-identical to the eager passes. After mh_shutdown and mh_init the replay is
+    refused with an error (its buffers are gone) until the pass is captured again."""
+    from util import config5_nodes, native_graph
+    eng = GpuEngine()
+    m = eng.m
+    rows = 4099
+    onehot = np.zeros((rows, 10), np.float32)
+    onehot[np.arange(rows), synth.integers((rows,), 0, 10, 1600)] = 1
+    values = {"logits": synth.normal((rows, 10), 0, 2, 1601), "onehot": onehot}
+    models = []
+    for _ in range(2):
+        g, syms, inputs = native_graph(m, config5_nodes(), values, ["logits"])
+        g.loss(syms["loss"])
+        models.append((syms, inputs, m.Model(g)))
+    (syms_a, inputs, eager), (syms_b, _, graphed) = models
+    big = m.Tensor(m.TensorShape(8192, 8192))
+    colsum = m.Tensor(m.TensorShape(1, 8192))
+
+    def grow():
+        m.forward_op(m.OP.SUM, colsum, big, attributes={"axis": 0})
+
+    def check(it):
+        lx = synth.normal((rows, 10), 0, 2, 1610 + it)
+        eager.parameters.grads.set_zero()
+        la = eager.forward(lx, onehot).to_numpy()
+        eager.backward()
+        graphed.parameters.tensors[syms_b["logits"]] = lx
+        graphed.parameters.grads.set_zero()
+        lb = graphed.replay("forward").to_numpy()
+        graphed.replay("backward")
+        assert (lb.view(np.uint32) == la.view(np.uint32)).all(), it
+        ga = eager.parameters.grads[syms_a["logits"]].to_numpy()
+        gb = graphed.parameters.grads[syms_b["logits"]].to_numpy()
+        assert (ga.view(np.uint32) == gb.view(np.uint32)).all(), it
+
+    graphed.parameters.tensors[syms_b["onehot"]] = onehot  # inputs are not part of a captured pass
+    graphed.capture("forward")
+    grow()  # scratch grows past what the forward graph was captured with
+    graphed.capture("backward")
+    check(0)
+    grow()
+    check(1)
+    m._lib.call("mh_shutdown")
+    m.init(0)
+    with pytest.raises(m.MantleHipError):
+        graphed.replay("forward")
+    graphed.capture("forward")
+    graphed.capture("backward")
+    check(2)

@@ -120,6 +120,34 @@ def test_binary_bwd_both_operands_fused(gpu, op):
     assert_bitexact(tg2.to_numpy(), ORC.backward(1, op, ug, a, b, grad=g2), "fused id1")
 
 
+@pytest.mark.parametrize("n", [(1 << 16) + 3, 5, 4096])
+@pytest.mark.parametrize("op", [0, 1, 2, 3], ids=["ADD", "SUB", "MUL", "DIV"])
+def test_binary_bwd_both_operands_one_symbol(gpu, op, n):
+    """x + x, x * x ...: both operands are one symbol, so Model.backward's two backward_op calls
+    (model.mojo:233-270) accumulate into one gradient, operand 0's first. The fused entry point
+    given the same gradient twice must match those two calls on the oracle bit for bit; so must
+    two gradient views that overlap without being equal (one element apart), which run as the
+    two calls in order."""
+    m = gpu.m
+    x = synth.uniform((n,), 0.5, 2, 410 + op)
+    ug = synth.normal((n,), 0, 1, 411)
+    g0 = synth.normal((n,), 0, 1, 412)
+    exp = ORC.backward(1, op, ug, x, x, grad=ORC.backward(0, op, ug, x, x, grad=g0))
+    tx, tu, tg = gpu.T(x), gpu.T(ug), gpu.T(g0)
+    m.backward_op_both(op, tu, tx, tx, tg, tg)
+    assert_bitexact(tg.to_numpy(), exp, "one gradient for both operands")
+    # overlapping views: grad1 = buf[0:n], grad2 = buf[1:n+1]
+    buf0 = synth.normal((n + 1,), 0, 1, 413)
+    buf = gpu.T(buf0)
+    v1 = m.Tensor(m.TensorShape(n), _ptr=buf.ptr, _owner=buf)
+    v2 = m.Tensor(m.TensorShape(n), _ptr=buf.ptr + 4, _owner=buf)
+    m.backward_op_both(op, tu, tx, tx, v1, v2)
+    e = buf0.copy()
+    e[:n] = ORC.backward(0, op, ug, x, x, grad=e[:n])
+    e[1:] = ORC.backward(1, op, ug, x, x, grad=e[1:])
+    assert_bitexact(buf.to_numpy(), e, "overlapping gradient views")
+
+
 # ---------------------------------------------------------------------------------------
 # unary ops and POW on the config-2 distributions
 # ---------------------------------------------------------------------------------------

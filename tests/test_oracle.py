@@ -150,6 +150,39 @@ def test_tanh_formula_bound_and_symmetry():
     assert (np.sign(t) == np.sign(x)).all() and (np.abs(t) <= 1).all()
 
 
+def _exp_rn(v):
+    """exp correctly rounded to float32 (fp64 exp, then one rounding)."""
+    return np.exp(np.asarray(v, np.float64)).astype(np.float32)
+
+
+def test_tanh_is_the_exp_cancellation_formula():
+    """TANH.tanh, mlops.mojo:195-201, is (e^x - e^-x) / (e^x + e^-x) in float32, not a library
+    tanh. Two properties fix that formula independently of the oracle's code:
+    - for x in (2^-20, 2^-13), e^x rounds to 1 + k 2^-23 and e^-x to 1 - j 2^-24, their sum to
+      exactly 2, so the result is an exact multiple of 2^-25 (a correctly rounded tanh, ~x, is
+      one in about 1 of 2^5..2^12 cases only by chance);
+    - wherever the oracle's exp is the correctly rounded exp at both x and -x, its tanh has the
+      bits of that formula evaluated in numpy float32 arithmetic over np.exp's values."""
+    rng = np.random.default_rng(12)
+    x = np.exp2(rng.uniform(-20, -13, 100_000)).astype(np.float32)
+    t = O.elwise_transform(O.TANH, x)
+    q = t.astype(np.float64) * 2.0 ** 25
+    assert (q == np.round(q)).all(), "tanh near 0 is not quantised to 2^-25"
+    lib = np.tanh(x.astype(np.float64)).astype(np.float32).astype(np.float64) * 2.0 ** 25
+    assert (lib == np.round(lib)).mean() < 0.01  # the signature tells the two apart
+    assert np.abs(t.astype(np.float64) - np.tanh(x.astype(np.float64))).max() <= 2.0 ** -24
+    for xs in (x, (rng.standard_normal(400_000) * 3).astype(np.float32),
+               rng.uniform(-12, 12, 200_000).astype(np.float32)):
+        xs = np.concatenate([xs, -xs])
+        ts = O.elwise_transform(O.TANH, xs)
+        ep, em = _exp_rn(xs), _exp_rn(-xs)
+        with np.errstate(over="ignore", invalid="ignore"):
+            formula = (ep - em) / (ep + em)
+        same = (O.elwise_transform(O.EXP, xs) == ep) & (O.elwise_transform(O.EXP, -xs) == em)
+        assert same.mean() > 0.5, same.mean()
+        assert_bitexact(ts[same], formula[same], "tanh vs the reference formula")
+
+
 def test_powi_is_square_and_multiply():
     rng = np.random.default_rng(11)
     x = rng.uniform(0.1, 4, 1000).astype(np.float32)
