@@ -117,6 +117,17 @@ int mh_powi_fwd(float* res, const float* x, int32_t n_int, int64_t n);
  * elements into res[0]; otherwise res has get_reduce_shape(sx, axis) (:601-619). */
 int mh_reduce_fwd(int op, float* res, const float* x, const mh_shape* sx, int32_t axis);
 
+/* mh_reduce_fwd without any device allocation. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP-graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same kernels and results as mh_reduce_fwd, but the
+ * split partials live in a fixed 16 MiB device array per GPU (held from library load until
+ * the process ends) instead of library scratch; shapes whose partials would need more return
+ * MH_ERR_OVERFLOW before any device work (every reduction over a non-last axis fits, and
+ * last-axis or all-element reductions of up to 2^32 elements). All calls in a process share
+ * its GPU's array: calls that overlap on one GPU (issued from several host threads) race, and
+ * must not be made. */
+int mh_reduce_fwd_noalloc(int op, float* res, const float* x, const mh_shape* sx, int32_t axis);
+
 /* ---- backward (accumulating) ---- */
 
 /* backward_op for ADD/SUB/MUL/DIV (ops.mojo:408-463): the struct backward of operand

@@ -96,6 +96,7 @@ SIGNATURES = {
     "mh_pow_fwd": [_VP, _VP, _I64, _VP],
     "mh_powi_fwd": [_VP, _VP, ctypes.c_int32, _I64],
     "mh_reduce_fwd": [_I, _VP, _VP, _S, ctypes.c_int32],
+    "mh_reduce_fwd_noalloc": [_I, _VP, _VP, _S, ctypes.c_int32],
     "mh_binary_bwd_accum": [_I, _I, _VP, _S, _VP, _S, _VP, _S, _VP, _S],
     "mh_binary_bwd_accum2": [_I, _VP, _VP, _VP, _VP, _VP, _S],
     "mh_unary_bwd_accum": [_I, _VP, _VP, _VP, _I64],

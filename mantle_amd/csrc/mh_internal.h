@@ -83,6 +83,11 @@ int stage(size_t bytes, void** out);
 // At least n zeroed arrival counters. A kernel that takes tickets leaves every one it
 // touched at zero again when it ends (the last arrival resets it).
 int tickets(int64_t n, uint32_t** out);
+// The no-allocation scratch: a fixed device array of kNoAllocScratchBytes per GPU, shared by
+// every call on that GPU (contents are whatever the last call left). `bytes` beyond the size
+// fail with MH_ERR_OVERFLOW; the address is the current device's, resolved at mh_init.
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+int noalloc_scratch(size_t bytes, float** out);
 
 // ---------------------------------------------------------------------------------------
 // shapes

@@ -1659,6 +1659,29 @@ int mh_reduce_fwd(int op, float* res, const float* x, const mh_shape* psx, int32
     return finish("mh_reduce_fwd");
 }
 
+int mh_reduce_fwd_noalloc(int op, float* res, const float* x, const mh_shape* psx, int32_t axis) {
+    MH_SHAPE_ARG(sx);
+    MH_TRY(check_reduce_args(op, sx, axis));
+    int64_t A, B, C;
+    abc_of(sx, axis, &A, &B, &C);
+    if (A * C == 0) return MH_OK;
+    const int rop = op == MH_MAX ? RED_MAX : RED_SUM;
+    // the largest partial buffer any launcher for [A, B, C] may use, checked before anything else
+    const size_t t = reduce_abc_tmp_floats(rop, A, B, C);
+    if (t * sizeof(float) > kNoAllocScratchBytes)
+        return fail(MH_ERR_OVERFLOW, "mh_reduce_fwd_noalloc: [%lld, %lld, %lld] needs %zu bytes of partials, more "
+                    "than the %zu of the no-allocation scratch (use mh_reduce_fwd)", (long long)A, (long long)B,
+                    (long long)C, t * sizeof(float), kNoAllocScratchBytes);
+    if (!res || (!x && B > 0)) return fail(MH_ERR_NULL, "mh_reduce_fwd_noalloc: null tensor");
+    MH_TRY(require_init());
+    float* tmp = nullptr;
+    if (t) MH_TRY(noalloc_scratch(t * sizeof(float), &tmp));  // partials are written before they are read
+    const int epi = op == MH_MEAN ? EPI_MEAN : EPI_STORE;
+    const float div = op == MH_MEAN ? (float)B : 0.0f;
+    MH_TRY(reduce_abc(rop, epi, x, A, B, C, res, nullptr, div, tmp));
+    return finish("mh_reduce_fwd_noalloc");
+}
+
 int mh_tstd(float* res, const float* x, const mh_shape* psx, int32_t axis) {
     MH_SHAPE_ARG(sx);
     MH_TRY(check_shape(sx, "x"));

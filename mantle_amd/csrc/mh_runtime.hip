@@ -6,7 +6,26 @@
 
 #include "mh_internal.h"
 
+// Scratch of the no-allocation entry points: 16 MiB of device memory per GPU, reserved when the
+// library's code object loads on that GPU and held until the process ends. Host code never
+// uses this name as an address: mh_init resolves the device's copy with hipGetSymbolAddress.
+static __device__ __align__(256) float noalloc_scratch_buf[mh::kNoAllocScratchBytes / sizeof(float)];
+
 namespace mh {
+
+constexpr int kMaxDevices = 64;
+static float* g_noalloc_ptr[kMaxDevices];  // per device: the address of noalloc_scratch_buf there
+
+int noalloc_scratch(size_t bytes, float** out) {
+    if (bytes > kNoAllocScratchBytes)
+        return fail(MH_ERR_OVERFLOW, "needs %zu bytes of scratch, more than the %zu of the no-allocation scratch",
+                    bytes, kNoAllocScratchBytes);
+    MH_TRY(require_init());
+    float* p = g_noalloc_ptr[ctx().device];
+    if (!p) return fail(MH_ERR_NOT_INIT, "the no-allocation scratch was not resolved on device %d", ctx().device);
+    *out = p;
+    return MH_OK;
+}
 
 Context& ctx() {
     static Context c;
@@ -428,6 +447,12 @@ int mh_init(int device, uint64_t flags) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(MH_ERR_NO_DEVICE, "mh_init: device %d is %s, this library is built for gfx950",
                     device, prop.gcnArchName);
+    if (device >= kMaxDevices) return fail(MH_ERR_NO_DEVICE, "mh_init: device %d beyond %d", device, kMaxDevices);
+    if (!g_noalloc_ptr[device]) {  // this device's copy of the no-allocation scratch (device current)
+        void* p = nullptr;
+        MH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch_buf)));
+        g_noalloc_ptr[device] = static_cast<float*>(p);
+    }
     MH_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
     c.num_cus = prop.multiProcessorCount;
     c.device = device;

@@ -41,6 +41,16 @@ def test_status_strings():
 S = _lib.make_shape
 
 
+def test_noalloc_reduce_refuses_oversized_partials_on_the_host():
+    """mh_reduce_fwd_noalloc checks its partials against the fixed 16 MiB scratch before
+    anything else (no device needed): an all-element SUM of 2^34 elements needs 32 MiB."""
+    L = _lib.lib()
+    assert L.mh_reduce_fwd_noalloc(8, None, None, S((1 << 34,)), -1) == _lib.ERR_OVERFLOW
+    assert b"no-allocation scratch" in L.mh_last_error()
+    # within the scratch, the call goes on to the usual checks (null tensors here)
+    assert L.mh_reduce_fwd_noalloc(8, None, None, S((8192, 8192)), 0) == _lib.ERR_NULL
+
+
 def test_shape_errors_before_device_work():
     L = _lib.lib()
     # non-broadcastable (the reference only prints, tensorutils.mojo:116-122)

@@ -1,0 +1,79 @@
+"""mh_reduce_fwd_noalloc (the no-allocation form of mh_reduce_fwd, for callers that cannot
+allocate device memory) against mh_reduce_fwd through the C ABI: the same kernels, so the same
+bits, on two calls in a row with the second smaller, for SUM / MEAN / MAX over axis 0, the last
+axis and all elements. The no-allocation calls run first, and the device's free memory does not
+drop across them (mh_reduce_fwd would allocate 8 MiB of partials for the first shape in a
+fresh library); a small call before them has the runtime load the kernels' code object."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from mantle_amd import synth
+from util import GpuEngine
+
+pytestmark = pytest.mark.gpu
+
+HIP = "/opt/rocm/lib/libamdhip64.so"
+
+
+def _free_bytes():
+    hip = ctypes.CDLL(HIP)
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipDeviceSynchronize() == 0
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+@pytest.mark.parametrize("axis_kind", ["axis0", "last", "all"])
+def test_noalloc_matches_reduce_fwd(axis_kind):
+    print(f"\n[noalloc] {axis_kind}", flush=True)
+    eng = GpuEngine()
+    m = eng.m
+    L = m.lib()
+    big = m.Tensor(m.TensorShape(8192, 8192))
+    m._lib.call("mh_rand_normal", big.ptr, big.num_elements(), 77, 0.0, 1.0)
+    small_np = synth.normal((777, 300), 0, 1, 78)
+    small = eng.T(small_np)
+    cases = [(big, (8192, 8192)), (small, (777, 300))]  # the second call is smaller
+    axis = {"axis0": 0, "last": 1, "all": -1}[axis_kind]
+    outs = {}
+    f0 = _free_bytes()
+    for op in (8, 9, 10):  # SUM, MEAN, MAX
+        for k, (t, shape) in enumerate(cases):
+            rshape = (1,) if axis < 0 else tuple(1 if i == axis else d for i, d in enumerate(shape))
+            r = m.Tensor(m.TensorShape(*rshape))
+            outs[(op, k)] = r
+    # one small call first: the HIP runtime loads a module's code object on the first launch of
+    # one of its kernels, which takes device memory once per process (not the entry point's)
+    warm = m.Tensor(m.TensorShape(1))
+    m._lib.check(L.mh_reduce_fwd_noalloc(8, warm.ptr, small.ptr, m.TensorShape(777 * 300).c(), -1), "warm-up")
+    f1 = _free_bytes()  # result tensors allocated above, outside the measured span
+    for op in (8, 9, 10):
+        for k, (t, shape) in enumerate(cases):
+            m._lib.check(L.mh_reduce_fwd_noalloc(op, outs[(op, k)].ptr, t.ptr, m.TensorShape(*shape).c(), axis),
+                         f"noalloc op {op} call {k}")
+    f2 = _free_bytes()
+    assert f1 - f2 < (1 << 20), f"free memory dropped by {f1 - f2} bytes across the no-allocation calls"
+    for op in (8, 9, 10):
+        for k, (t, shape) in enumerate(cases):
+            got = outs[(op, k)].to_numpy()
+            ref = m.Tensor(outs[(op, k)].shape())
+            m._lib.check(L.mh_reduce_fwd(op, ref.ptr, t.ptr, m.TensorShape(*shape).c(), axis), "reduce_fwd")
+            assert (got.view(np.uint32) == ref.to_numpy().view(np.uint32)).all(), (axis_kind, op, k)
+    assert f0 >= f1
+
+
+def test_noalloc_rejects_partials_beyond_its_scratch():
+    eng = GpuEngine()
+    m = eng.m
+    L = m.lib()
+    x = m.Tensor(m.TensorShape(4))
+    res = m.Tensor(m.TensorShape(1))
+    # an all-element reduction of 2^34 elements would need 32 MiB of chunk partials: refused on
+    # the host before any device work (x is never read)
+    rc = L.mh_reduce_fwd_noalloc(8, res.ptr, x.ptr, m.TensorShape(1 << 34).c(), -1)
+    assert rc == m._lib.ERR_OVERFLOW
+    assert b"no-allocation scratch" in L.mh_last_error()
