@@ -799,9 +799,20 @@ def _cores_available() -> int:
         return os.cpu_count() or 1
 
 
-def cpu_baseline(n_sample: int, reps: int, expo: float):
-    """The CPU restatement (oracle/, single thread, like the reference's elementwise paths)
-    on the same op sequence over a bounded sample; GB/s with the same byte accounting."""
+def _median_pass(fn, reps: int):
+    """Median wall time of `reps` calls of fn after one untimed warm-up call."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def _cpu_c2(n_sample: int, reps: int, expo: float):
+    """Config 2's op sequence on n_sample elements per tensor, one thread (the reference's
+    elementwise paths are single-threaded)."""
     from oracle import oracle as O
     from mantle_amd import synth
     a = synth.uniform((n_sample,), -1, 1, 1)
@@ -811,29 +822,161 @@ def cpu_baseline(n_sample: int, reps: int, expo: float):
     xs["TANH"] = xs["SIGMOID"] = xs["RELU"] = synth.normal((n_sample,), 0, 3, 6)
     xp = synth.uniform((n_sample,), 0.1, 4, 7)
     e = np.array([expo], np.float32)
-    ga = np.zeros(n_sample, np.float32)
-    best = None
-    for _ in range(reps):
-        t0 = time.perf_counter()
+    res = np.zeros(n_sample, np.float32)
+    ga, gb = np.zeros(n_sample, np.float32), np.zeros(n_sample, np.float32)
+    ge = np.zeros(1, np.float32)
+
+    def one_pass():
         for op in BINARY:
             o = OP_ID[op]
-            O.forward_op(o, a, b)
-            ga = O.backward_op(0, o, ug, a, b, grad=ga)
-            ga = O.backward_op(1, o, ug, a, b, grad=ga)
+            O.forward_op_into(o, res, a, b)
+            O.backward_op_into(0, o, ga, ug, a, b)
+            O.backward_op_into(1, o, gb, ug, a, b)
         for op in UNARY:
-            O.forward_op(OP_ID[op], xs[op])
-            ga = O.backward_op(0, OP_ID[op], ug, xs[op], grad=ga)
-        O.forward_op(6, xp, e)
-        ga = O.backward_op(0, 6, ug, xp, e, grad=ga)
-        O.backward_op(1, 6, ug, xp, e)
-        dt = time.perf_counter() - t0
-        best = dt if best is None else min(best, dt)
-    bytes_per_elem = sum(b for _, b in step_plan())
-    return {"value": round(bytes_per_elem * n_sample / best / 1e9, 3), "unit": "GB/s", "cores": 1,
-            "kind": "port", "host_cpu": _cpu_model(), "host_cores_available": _cores_available(),
-            "sample": f"same op sequence on {n_sample} elements per tensor (1/{(1 << 28) // n_sample} of the "
-                      f"workload), best of {reps}, {best:.2f} s per pass; single-threaded C restatement "
-                      f"(oracle/mantle_oracle.c, -O3)"}
+            O.forward_op_into(OP_ID[op], res, xs[op])
+            O.backward_op_into(0, OP_ID[op], ga, ug, xs[op])
+        O.forward_op_into(6, res, xp, e)
+        O.backward_op_into(0, 6, ga, ug, xp, e)
+        O.backward_op_into(1, 6, ge, ug, xp, e)
+
+    t = _median_pass(one_pass, reps)
+    nbytes = sum(bb for _, bb in step_plan()) * n_sample
+    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "ms_per_pass": round(t * 1e3, 2),
+            "sample": f"config-2 op sequence (fwd, both backward operands, POW's exponent gradient) on "
+                      f"{n_sample} elements per tensor (1/{(1 << 28) // n_sample} of the workload), median of "
+                      f"{reps} passes after 1 warm-up; single-threaded C restatement (oracle/, -O3), results "
+                      f"and gradients in preallocated arrays"}
+
+
+def _cpu_c3(reps: int):
+    """Config 3 op by op at full size ([256,32,28,28] + [1,32,1,1]), one thread."""
+    from oracle import oracle as O
+    from mantle_amd import synth
+    shape, bshape = (256, 32, 28, 28), (1, 32, 1, 1)
+    n = int(np.prod(shape))
+    x, bias, ug = synth.normal(shape, 0, 1, 11), synth.normal(bshape, 0, 0.1, 12), synth.normal(shape, 0, 1, 13)
+    y, r = np.zeros(shape, np.float32), np.zeros(shape, np.float32)
+    gy, gx, gb = np.zeros(shape, np.float32), np.zeros(shape, np.float32), np.zeros(bshape, np.float32)
+
+    def one_pass():
+        O.forward_op_into(0, y, x, bias)
+        O.forward_op_into(14, r, y)
+        O.backward_op_into(0, 14, gy, ug, y)
+        O.backward_op_into(0, 0, gx, gy, x, bias)
+        O.backward_op_into(1, 0, gb, gy, x, bias)
+
+    t = _median_pass(one_pass, reps)
+    B = 4 * n
+    nbytes = (2 * B + 128) + 2 * B + 4 * B + 3 * B + (B + 256)  # the GPU op-by-op accounting
+    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "ms_per_pass": round(t * 1e3, 2),
+            "sample": f"config 3 op by op at full size (ADD, RELU forward; RELU, ADD x and bias backward), "
+                      f"median of {reps} after 1 warm-up; single-threaded like the reference's elementwise, "
+                      f"broadcast and accumulate_grad paths"}
+
+
+def _cpu_c4(reps: int, threads: int, rows: int = 1024):
+    """Config 4's reductions on a [rows, 8192] sample of the [8192, 8192] workload: axis
+    forwards over a pool of `threads` (the reference's parallelize over outputs,
+    tensorutils.mojo:682), all-element forwards and every backward on one thread."""
+    from oracle import oracle as O
+    from mantle_amd import synth
+    shape = (rows, 8192)
+    n = rows * 8192
+    x = synth.normal(shape, 0, 1, 40)
+    out = {}
+    for axis in (0, 1, -1):
+        red = (1,) if axis < 0 else tuple(1 if i == axis else d for i, d in enumerate(shape))
+        m = int(np.prod(red))
+        ug = synth.normal(red, 0, 1, 43)
+        g = np.zeros(shape, np.float32)
+        res = np.zeros(red, np.float32)
+        ax = "all" if axis < 0 else f"ax{axis}"
+        for op, name in ((8, "SUM"), (9, "MEAN"), (10, "MAX")):
+            if axis >= 0:
+                tf = _median_pass(lambda op=op, axis=axis: O.reduce_axis_mt(op, x, axis, threads), reps)
+                fc = threads
+            else:
+                tf = _median_pass(lambda op=op: O.forward_op_into(op, res, x, None, -1), reps)
+                fc = 1
+            tb = _median_pass(lambda op=op, axis=axis, ug=ug: O.backward_op_into(0, op, g, ug, x, None, axis), reps)
+            fb, bb = 4 * n + 4 * m, (12 * n + 8 * m) if name == "MAX" else (8 * n + 4 * m)
+            out[f"{ax}.{name}.fwd"] = {"GB/s": round(fb / tf / 1e9, 3), "ms": round(tf * 1e3, 2), "cores": fc}
+            out[f"{ax}.{name}.bwd"] = {"GB/s": round(bb / tb / 1e9, 3), "ms": round(tb * 1e3, 2), "cores": 1}
+    fwd = [v for k, v in out.items() if k.endswith(".fwd")]
+    tot_b = sum(v["GB/s"] * v["ms"] for v in out.values())  # GB/s * ms = MB
+    tot_ms = sum(v["ms"] for v in out.values())
+    return {"value": round(tot_b / tot_ms, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "fwd_GB/s": round(sum(v["GB/s"] * v["ms"] for v in fwd) / sum(v["ms"] for v in fwd), 3),
+            "ops": out,
+            "sample": f"SUM/MEAN/MAX over axis 0, axis 1 and all of a [{rows}, 8192] sample ({rows / 8192:.3g} of "
+                      f"the [8192, 8192] workload), forward and backward, median of {reps} after 1 warm-up each; "
+                      f"axis forwards on {threads} threads (outputs split as the reference's parallelize), "
+                      f"all-element forwards and backwards single-threaded as in the reference"}
+
+
+def _cpu_c5(reps: int, threads: int, rows: int = 1 << 17, classes: int = 10):
+    """Config 5's chain op by op on `rows` rows: the two axis-1 reductions on `threads` threads,
+    the rest single-threaded, as in the reference."""
+    from oracle import oracle as O
+    from mantle_amd import synth
+    E, N = rows * classes, rows
+    lg = synth.normal((rows, classes), 0, 2, 31)
+    oh = np.zeros((rows, classes), np.float32)
+    oh[np.arange(rows), synth.integers((rows,), 0, classes, 32)] = 1.0
+    full = lambda: np.zeros((rows, classes), np.float32)  # noqa: E731
+    xm, e, sm, lp, t = full(), full(), full(), full(), full()
+    g = {k: full() for k in ("logits", "xm", "e", "sm", "lp", "t")}
+    gmax, gs = np.zeros((rows, 1), np.float32), np.zeros((rows, 1), np.float32)
+    gl = np.ones(1, np.float32)
+    loss = np.zeros(1, np.float32)
+    st = {}
+
+    def one_pass():
+        mx = O.reduce_axis_mt(10, lg, 1, threads)
+        O.forward_op_into(1, xm, lg, mx)
+        O.forward_op_into(4, e, xm)
+        s = O.reduce_axis_mt(8, e, 1, threads)
+        O.forward_op_into(3, sm, e, s)
+        O.forward_op_into(5, lp, sm)
+        O.forward_op_into(2, t, lp, oh)
+        O.forward_op_into(9, loss, t, None, -1)
+        O.backward_op_into(0, 9, g["t"], gl, t, None, -1)
+        O.backward_op_into(0, 2, g["lp"], g["t"], lp, oh)
+        O.backward_op_into(0, 5, g["sm"], g["lp"], sm)
+        O.backward_op_into(0, 3, g["e"], g["sm"], e, s)
+        O.backward_op_into(1, 3, gs, g["sm"], e, s)
+        O.backward_op_into(0, 8, g["e"], gs, e, None, 1)
+        O.backward_op_into(0, 4, g["xm"], g["e"], xm)
+        O.backward_op_into(0, 1, g["logits"], g["xm"], lg, mx)
+        O.backward_op_into(1, 1, gmax, g["xm"], lg, mx)
+        O.backward_op_into(0, 10, g["logits"], gmax, lg, None, 1)
+        st["ok"] = True
+
+    t_pass = _median_pass(one_pass, reps)
+    F, R = 4 * E, 4 * N
+    fwd_b = (F + R) + (2 * F + R) + 2 * F + (F + R) + (2 * F + R) + 2 * F + 3 * F + (F + 4)
+    bwd_b = (2 * F + 4) + 4 * F + 4 * F + (3 * F + R) + (2 * F + 3 * R) + (2 * F + R) + 4 * F + 3 * F + (F + 2 * R) + \
+        (3 * F + 2 * R)
+    return {"value": round((fwd_b + bwd_b) / t_pass / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "ms_per_pass": round(t_pass * 1e3, 2), "rows_per_s": round(rows / t_pass, 1),
+            "sample": f"config-5 chain op by op (8 forward, 10 backward calls) on [{rows}, {classes}] "
+                      f"(1/{(1 << 20) // rows} of the rows), median of {reps} after 1 warm-up; the two axis-1 "
+                      f"reduction forwards on {threads} threads, every other call single-threaded, as in "
+                      f"the reference; the GPU op-by-op byte accounting"}
+
+
+def cpu_baseline(n_sample: int, reps: int, expo: float):
+    """The CPU restatement (oracle/) timed on the host's cores, beside the GPU figures: config 2
+    (the headline metric: `value`), and configs 3-5 under `configs`, each a bounded sample with
+    the GPU workload's byte accounting and the reference's threading (one thread except the axis
+    reductions, which run on the cores available to the job)."""
+    threads = _cores_available()
+    out = _cpu_c2(n_sample, reps, expo)
+    out.update({"host_cpu": _cpu_model(), "host_cores_available": threads})
+    out["configs"] = {"c3": _cpu_c3(reps), "c4": _cpu_c4(reps, threads), "c5": _cpu_c5(reps, threads)}
+    return out
 
 
 # ---------------------------------------------------------------------------------------
@@ -1056,8 +1199,8 @@ def main():
                     help="extra workloads after the headline step (comma list of c3,c4,c5,adam,adj,rows,graph,"
                          "copy; 'none')")
     ap.add_argument("--reps", type=int, default=10, help="repetitions per op of the extra workloads")
-    ap.add_argument("--cpu-log2n", type=int, default=24)
-    ap.add_argument("--cpu-reps", type=int, default=2)
+    ap.add_argument("--cpu-log2n", type=int, default=23)
+    ap.add_argument("--cpu-reps", type=int, default=5, help="timed passes of each CPU baseline (after 1 warm-up)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write profiles/traffic.json and traffic.md from two rocprofv3 --pmc runs and exit")

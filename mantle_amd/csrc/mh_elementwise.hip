@@ -222,8 +222,8 @@ __global__ void __launch_bounds__(kThreads)
         float4 ov;
 #pragma unroll
         for (int k = 0; k < NIN; ++k)
-            if (!((smask >> k) & 1)) iv[k] = reinterpret_cast<const float4*>(in.p[k])[q];
-        if (ACCUM) ov = reinterpret_cast<const float4*>(out)[q];
+            if (!((smask >> k) & 1)) iv[k] = ld_nt4(in.p[k], q);
+        if (ACCUM) ov = ld_nt4(out, q);
         float r[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -234,7 +234,7 @@ __global__ void __launch_bounds__(kThreads)
             if (ACCUM) r[j] = comp(ov, j) + r[j];
         }
         if (ACCUM && kSparseAccum<F> && !bits_differ4(ov.x, ov.y, ov.z, ov.w, r[0], r[1], r[2], r[3])) continue;
-        reinterpret_cast<float4*>(out)[q] = make_float4(r[0], r[1], r[2], r[3]);
+        st_nt4(out, q, make_float4(r[0], r[1], r[2], r[3]));
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         for (int64_t i = nq << 2; i < n; ++i) {
@@ -259,9 +259,9 @@ __global__ void __launch_bounds__(kThreads)
     for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
         float v[NIN > 0 ? NIN : 1];
 #pragma unroll
-        for (int k = 0; k < NIN; ++k) v[k] = ((smask >> k) & 1) ? sv[k] : in.p[k][i];
+        for (int k = 0; k < NIN; ++k) v[k] = ((smask >> k) & 1) ? sv[k] : ld_nt(in.p[k] + i);
         float r = f(v);
-        out[i] = ACCUM ? out[i] + r : r;
+        st_nt(out + i, ACCUM ? ld_nt(out + i) + r : r);
     }
 }
 
@@ -295,7 +295,7 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) v[j][k] = sv[k];
             } else if (kind == IN_FULL) {
-                const vf4 t = reinterpret_cast<const vf4*>(in.p[k])[q];
+                const vf4 t = ld_ntv(in.p[k], q);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) v[j][k] = t[j];
             } else {
@@ -306,7 +306,7 @@ __global__ void __launch_bounds__(kThreads)
             }
         }
         vf4 o = vf4{0.f, 0.f, 0.f, 0.f};
-        if (ACCUM) o = reinterpret_cast<const vf4*>(out)[q];
+        if (ACCUM) o = ld_ntv(out, q);
         vf4 r;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -314,7 +314,7 @@ __global__ void __launch_bounds__(kThreads)
             r[j] = ACCUM ? o[j] + fv : fv;
         }
         if (ACCUM && kSparseAccum<F> && !bits_differ4(o[0], o[1], o[2], o[3], r[0], r[1], r[2], r[3])) continue;
-        reinterpret_cast<vf4*>(out)[q] = r;
+        st_ntv(out, q, r);
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         for (int64_t i = nq << 2; i < n; ++i) {
@@ -352,12 +352,12 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
             const int kind = (kinds >> (2 * k)) & 3;
-            if (kind == IN_FULL) t[k] = reinterpret_cast<const vf4*>(in.p[k])[q];
+            if (kind == IN_FULL) t[k] = ld_ntv(in.p[k], q);
             else if (kind == IN_BCAST) t[k] = reinterpret_cast<const vf4*>(in.p[k])[cq];
             else t[k] = vf4{sv[k], sv[k], sv[k], sv[k]};
         }
         vf4 o = vf4{0.f, 0.f, 0.f, 0.f};
-        if (ACCUM) o = reinterpret_cast<const vf4*>(out)[q];
+        if (ACCUM) o = ld_ntv(out, q);
         vf4 r;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -368,7 +368,7 @@ __global__ void __launch_bounds__(kThreads)
             r[j] = ACCUM ? o[j] + fv : fv;
         }
         if (ACCUM && kSparseAccum<F> && !bits_differ4(o[0], o[1], o[2], o[3], r[0], r[1], r[2], r[3])) continue;
-        reinterpret_cast<vf4*>(out)[q] = r;
+        st_ntv(out, q, r);
     }
 }
 
@@ -394,14 +394,14 @@ __global__ void __launch_bounds__(kThreads)
         for (int k = 0; k < NIN; ++k) {
             const int kind = (kinds >> (2 * k)) & 3;
             if (kind == IN_FULL) {
-                t[k] = reinterpret_cast<const vf4*>(in.p[k])[q];
+                t[k] = ld_ntv(in.p[k], q);
             } else {
                 const float b = kind == IN_BCAST ? in.p[k][c] : sv[k];
                 t[k] = vf4{b, b, b, b};
             }
         }
         vf4 o = vf4{0.f, 0.f, 0.f, 0.f};
-        if (ACCUM) o = reinterpret_cast<const vf4*>(out)[q];
+        if (ACCUM) o = ld_ntv(out, q);
         vf4 r;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -412,7 +412,7 @@ __global__ void __launch_bounds__(kThreads)
             r[j] = ACCUM ? o[j] + fv : fv;
         }
         if (ACCUM && kSparseAccum<F> && !bits_differ4(o[0], o[1], o[2], o[3], r[0], r[1], r[2], r[3])) continue;
-        reinterpret_cast<vf4*>(out)[q] = r;
+        st_ntv(out, q, r);
     }
 }
 
@@ -464,7 +464,7 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) v[j][k] = sv[k];
             } else if (pl.kind[k] == IN_FULL) {
-                const float4 t = reinterpret_cast<const float4*>(in.p[k])[q];
+                const float4 t = ld_nt4(in.p[k], q);
                 v[0][k] = t.x; v[1][k] = t.y; v[2][k] = t.z; v[3][k] = t.w;
             } else if (INNER4) {
                 if (pl.st[k][inner] == 1) {
@@ -505,7 +505,7 @@ __global__ void __launch_bounds__(kThreads)
                     if (pl.kind[k] == IN_BCAST) v[j][k] = in.p[k][oj[k]];
             }
         }
-        const float4 o = ACCUM ? reinterpret_cast<const float4*>(out)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 o = ACCUM ? ld_nt4(out, q) : make_float4(0.f, 0.f, 0.f, 0.f);
         float r[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -513,7 +513,7 @@ __global__ void __launch_bounds__(kThreads)
             if (ACCUM) r[j] = comp(o, j) + r[j];
         }
         if (ACCUM && kSparseAccum<F> && !bits_differ4(o.x, o.y, o.z, o.w, r[0], r[1], r[2], r[3])) continue;
-        reinterpret_cast<float4*>(out)[q] = make_float4(r[0], r[1], r[2], r[3]);
+        st_nt4(out, q, make_float4(r[0], r[1], r[2], r[3]));
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         for (int64_t i = nq << 2; i < pl.n; ++i) {
@@ -569,14 +569,14 @@ __global__ void __launch_bounds__(kThreads)
     FBinRg<OP, 0, false> f0;
     FBinRg<OP, 1, false> f1;
     for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
-        const float4 vu = reinterpret_cast<const float4*>(ug)[q];
+        const float4 vu = ld_nt4(ug, q);
         float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vb = va;
         if (NEED_AB) {
-            va = reinterpret_cast<const float4*>(a)[q];
-            vb = reinterpret_cast<const float4*>(b)[q];
+            va = ld_nt4(a, q);
+            vb = ld_nt4(b, q);
         }
-        const float4 v1 = reinterpret_cast<const float4*>(g1)[q];
-        const float4 v2 = ALIAS ? v1 : reinterpret_cast<const float4*>(g2)[q];
+        const float4 v1 = ld_nt4(g1, q);
+        const float4 v2 = ALIAS ? v1 : ld_nt4(g2, q);
         float r1[4], r2[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -589,10 +589,10 @@ __global__ void __launch_bounds__(kThreads)
             r2[j] = ALIAS ? r1[j] + f1(x1) : comp(v2, j) + f1(x1);
         }
         if (ALIAS) {
-            reinterpret_cast<float4*>(g1)[q] = make_float4(r2[0], r2[1], r2[2], r2[3]);
+            st_nt4(g1, q, make_float4(r2[0], r2[1], r2[2], r2[3]));
         } else {
-            reinterpret_cast<float4*>(g1)[q] = make_float4(r1[0], r1[1], r1[2], r1[3]);
-            reinterpret_cast<float4*>(g2)[q] = make_float4(r2[0], r2[1], r2[2], r2[3]);
+            st_nt4(g1, q, make_float4(r1[0], r1[1], r1[2], r1[3]));
+            st_nt4(g2, q, make_float4(r2[0], r2[1], r2[2], r2[3]));
         }
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {

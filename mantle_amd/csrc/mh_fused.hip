@@ -38,7 +38,7 @@ __global__ void __launch_bounds__(kFThreads)
         if (kb == IN_SCALAR) {
             bv[0] = bv[1] = bv[2] = bv[3] = sb;
         } else if (kb == IN_FULL) {
-            const float4 t = reinterpret_cast<const float4*>(bias)[q];
+            const float4 t = ld_nt4(bias, q);
             bv[0] = t.x; bv[1] = t.y; bv[2] = t.z; bv[3] = t.w;
         } else {
             off_type<BIG> off[4][2];
@@ -65,15 +65,15 @@ __global__ void __launch_bounds__(kFThreads)
                 }
             }
         }
-        const float4 xv = reinterpret_cast<const float4*>(x)[q];
+        const float4 xv = ld_nt4(x, q);
         float yv[4], rv[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             yv[j] = comp(xv, j) + bv[j];
             rv[j] = mrelu(yv[j]);
         }
-        reinterpret_cast<float4*>(y)[q] = make_float4(yv[0], yv[1], yv[2], yv[3]);
-        reinterpret_cast<float4*>(r)[q] = make_float4(rv[0], rv[1], rv[2], rv[3]);
+        st_nt4(y, q, make_float4(yv[0], yv[1], yv[2], yv[3]));
+        st_nt4(r, q, make_float4(rv[0], rv[1], rv[2], rv[3]));
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         for (int64_t i = nq << 2; i < pl.n; ++i) {
@@ -98,15 +98,15 @@ __global__ void __launch_bounds__(kFThreads)
     for (int64_t q = (int64_t)blockIdx.x * kFThreads + threadIdx.x; q < nq; q += stride) {
         const uint32_t p = fdiv((uint32_t)q, fsq);
         const float bv = bias[p - fdiv(p, fc) * C];
-        const vf4 xv = reinterpret_cast<const vf4*>(x)[q];
+        const vf4 xv = ld_ntv(x, q);
         vf4 yv, rv;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             yv[j] = xv[j] + bv;  // ADD.forward
             rv[j] = mrelu(yv[j]);  // RELU.forward
         }
-        reinterpret_cast<vf4*>(y)[q] = yv;
-        reinterpret_cast<vf4*>(r)[q] = rv;
+        st_ntv(y, q, yv);
+        st_ntv(r, q, rv);
     }
 }
 
@@ -141,10 +141,6 @@ __global__ void __launch_bounds__(kFThreads)
     const int64_t cnt = rem < QC ? rem : QC;
     const int64_t n0 = g * G, n1 = n0 + G < N ? n0 + G : N;
     constexpr int U = 4;
-    const vf4* y4 = reinterpret_cast<const vf4*>(y);
-    const vf4* u4 = reinterpret_cast<const vf4*>(ug);
-    vf4* gy4 = reinterpret_cast<vf4*>(gy);
-    vf4* gx4 = reinterpret_cast<vf4*>(gx);
     float acc = 0.0f;
     for (int64_t n = n0; n < n1; ++n) {
         const int64_t q0 = (n * C + c) * Sq + k * QC;
@@ -155,10 +151,10 @@ __global__ void __launch_bounds__(kFThreads)
                 const int64_t i = base + lane + 64 * u;
                 gv[u] = xv[u] = vf4{0.f, 0.f, 0.f, 0.f};
                 if (i < cnt) {
-                    yv[u] = y4[q0 + i];
-                    uv[u] = u4[q0 + i];
-                    if (HAS_GY) gv[u] = gy4[q0 + i];
-                    if (HAS_GX) xv[u] = gx4[q0 + i];
+                    yv[u] = ld_ntv(y, q0 + i);
+                    uv[u] = ld_ntv(ug, q0 + i);
+                    if (HAS_GY) gv[u] = ld_ntv(gy, q0 + i);
+                    if (HAS_GX) xv[u] = ld_ntv(gx, q0 + i);
                 }
             }
 #pragma unroll
@@ -172,8 +168,8 @@ __global__ void __launch_bounds__(kFThreads)
                     gg[j] = gv[u][j] + rg;
                     o[j] = xv[u][j] + gg[j];
                 }
-                if (HAS_GY) gy4[q0 + i] = gg;
-                if (HAS_GX) gx4[q0 + i] = o;
+                if (HAS_GY) st_ntv(gy, q0 + i, gg);
+                if (HAS_GX) st_ntv(gx, q0 + i, o);
                 if (HAS_PART) acc = (((acc + gg[0]) + gg[1]) + gg[2]) + gg[3];
             }
         }

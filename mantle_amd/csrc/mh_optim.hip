@@ -64,17 +64,17 @@ __device__ __forceinline__ void adam1(float& p, float g, float& m, float& v, con
 __device__ __forceinline__ void adam_unit(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
                                           float* __restrict__ v, int64_t e0, int cnt, bool vec, const AdamScal& s) {
     if (cnt == 4 && vec) {
-        float4 pp = *reinterpret_cast<float4*>(p + e0);
-        const float4 gg = *reinterpret_cast<const float4*>(g + e0);
-        float4 mm = *reinterpret_cast<float4*>(m + e0);
-        float4 vv = *reinterpret_cast<float4*>(v + e0);
+        float4 pp = ld_nt4(p + e0, 0);
+        const float4 gg = ld_nt4(g + e0, 0);
+        float4 mm = ld_nt4(m + e0, 0);
+        float4 vv = ld_nt4(v + e0, 0);
         adam1(pp.x, gg.x, mm.x, vv.x, s);
         adam1(pp.y, gg.y, mm.y, vv.y, s);
         adam1(pp.z, gg.z, mm.z, vv.z, s);
         adam1(pp.w, gg.w, mm.w, vv.w, s);
-        *reinterpret_cast<float4*>(p + e0) = pp;
-        *reinterpret_cast<float4*>(m + e0) = mm;
-        *reinterpret_cast<float4*>(v + e0) = vv;
+        st_nt4(p + e0, 0, pp);
+        st_nt4(m + e0, 0, mm);
+        st_nt4(v + e0, 0, vv);
     } else {
         for (int j = 0; j < cnt; ++j) {
             float pp = p[e0 + j], mm = m[e0 + j], vv = v[e0 + j];

@@ -68,9 +68,9 @@ template <class R>
 struct LdPlain {
     const float* x;
     __device__ void setup() {}
-    __device__ typename R::T get(int64_t i) const { return R::lift(x[i]); }
+    __device__ typename R::T get(int64_t i) const { return R::lift(ld_nt(x + i)); }
     __device__ void get4(int64_t i, typename R::T* o) const {
-        float4 q = *reinterpret_cast<const float4*>(x + i);
+        float4 q = ld_nt4(x + i, 0);
         o[0] = R::lift(q.x); o[1] = R::lift(q.y); o[2] = R::lift(q.z); o[3] = R::lift(q.w);
     }
 };
@@ -97,10 +97,10 @@ struct LdPowGrad {
         const float lg = __builtin_isinf(lx) ? 0.0f : lx;
         return (mpowf_lg(xv, a, lx) * lg) * u;
     }
-    __device__ float get(int64_t i) const { return term(x[i], ug[i]); }
+    __device__ float get(int64_t i) const { return term(ld_nt(x + i), ld_nt(ug + i)); }
     __device__ void get4(int64_t i, float* o) const {
-        float4 q = *reinterpret_cast<const float4*>(x + i);
-        float4 u = *reinterpret_cast<const float4*>(ug + i);
+        float4 q = ld_nt4(x + i, 0);
+        float4 u = ld_nt4(ug + i, 0);
         o[0] = term(q.x, u.x); o[1] = term(q.y, u.y); o[2] = term(q.z, u.z); o[3] = term(q.w, u.w);
     }
 };
@@ -144,16 +144,16 @@ struct LdBinRg {
     }
     __device__ float get(int64_t i) const {
         const float d = (OP == MH_DIV && ID == 1 && !DIVS) ? t2[line(i)] : 0.0f;
-        return term(ug[i], a[i], d);
+        return term(ld_nt(ug + i), ld_nt(a + i), d);
     }
     __device__ void get4(int64_t i, float* o) const {
         float4 u, v;
         if (al) {
-            u = *reinterpret_cast<const float4*>(ug + i);
-            v = *reinterpret_cast<const float4*>(a + i);
+            u = ld_nt4(ug + i, 0);
+            v = ld_nt4(a + i, 0);
         } else {
-            u = make_float4(ug[i], ug[i + 1], ug[i + 2], ug[i + 3]);
-            v = make_float4(a[i], a[i + 1], a[i + 2], a[i + 3]);
+            u = make_float4(ld_nt(ug + i), ld_nt(ug + i + 1), ld_nt(ug + i + 2), ld_nt(ug + i + 3));
+            v = make_float4(ld_nt(a + i), ld_nt(a + i + 1), ld_nt(a + i + 2), ld_nt(a + i + 3));
         }
         float4 d = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if constexpr (OP == MH_DIV && ID == 1 && !DIVS) {
@@ -246,9 +246,8 @@ __device__ __forceinline__ int64_t stage_rows(float* tile, const float* __restri
     const int64_t base = r0 * B;
     const int cnt = (int)(rows * B);
     const int nq = cnt >> 2;
-    const float4* x4 = reinterpret_cast<const float4*>(x + base);
-    for (int i = threadIdx.x; i < nq; i += kRThreads) reinterpret_cast<float4*>(tile)[i] = x4[i];
-    for (int i = (nq << 2) + threadIdx.x; i < cnt; i += kRThreads) tile[i] = x[base + i];
+    for (int i = threadIdx.x; i < nq; i += kRThreads) reinterpret_cast<float4*>(tile)[i] = ld_nt4(x + base, i);
+    for (int i = (nq << 2) + threadIdx.x; i < cnt; i += kRThreads) tile[i] = ld_nt(x + base + i);
     *rows_out = rows;
     return base;
 }
@@ -318,9 +317,9 @@ __global__ void __launch_bounds__(kRThreads)
     __syncthreads();
     const int cnt = (int)(rows * B);
     const int nq = cnt >> 2;
-    float4* g4 = reinterpret_cast<float4*>(grad + base);
+    float* gb = grad + base;
     for (int i = t; i < nq; i += kRThreads) {
-        const float4 o = g4[i];
+        const float4 o = ld_nt4(gb, i);
         float r[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -329,7 +328,7 @@ __global__ void __launch_bounds__(kRThreads)
             r[j] = tile[e] == sm[row] ? sg[row] : 0.0f;
         }
         const float4 g = make_float4(o.x + r[0], o.y + r[1], o.z + r[2], o.w + r[3]);
-        if (bits_differ4(o.x, o.y, o.z, o.w, g.x, g.y, g.z, g.w)) g4[i] = g;  // a sparse accumulation
+        if (bits_differ4(o.x, o.y, o.z, o.w, g.x, g.y, g.z, g.w)) st_nt4(gb, i, g);  // a sparse accumulation
     }
     for (int e = (nq << 2) + t; e < cnt; e += kRThreads) {
         const int row = (int)fdiv((uint32_t)e, fdB);
@@ -684,14 +683,14 @@ __global__ void __launch_bounds__(kRThreads)
     const int tr = WPR == 1 ? lane : (int)threadIdx.x;
     constexpr int NT = 64 * WPR;
     const int64_t Bq = B >> 2;
-    const float4* x4 = reinterpret_cast<const float4*>(x + row * B);
+    const float* xr = x + row * B;
     float4 v[NQ];
     MC acc = RMaxCnt::init();
 #pragma unroll
     for (int k = 0; k < NQ; ++k) {
         const int64_t qi = tr + (int64_t)k * NT;
         if (qi < Bq) {
-            v[k] = x4[qi];
+            v[k] = ld_nt4(xr, qi);
             acc = RMaxCnt::comb(acc, RMaxCnt::lift(v[k].x));
             acc = RMaxCnt::comb(acc, RMaxCnt::lift(v[k].y));
             acc = RMaxCnt::comb(acc, RMaxCnt::lift(v[k].z));
@@ -707,15 +706,15 @@ __global__ void __launch_bounds__(kRThreads)
     const float f = 1.0f / (float)acc.c;  // basics.mojo:609
     const float g = f * ug[row];
     const float m = acc.m;
-    float4* g4 = reinterpret_cast<float4*>(grad + row * B);
+    float* gr = grad + row * B;
 #pragma unroll
     for (int k = 0; k < NQ; ++k) {
         const int64_t qi = tr + (int64_t)k * NT;
         if (qi < Bq) {
-            const float4 o = g4[qi];
+            const float4 o = ld_nt4(gr, qi);
             const float4 n = make_float4(o.x + (v[k].x == m ? g : 0.0f), o.y + (v[k].y == m ? g : 0.0f),
                                          o.z + (v[k].z == m ? g : 0.0f), o.w + (v[k].w == m ? g : 0.0f));
-            if (bits_differ4(o.x, o.y, o.z, o.w, n.x, n.y, n.z, n.w)) g4[qi] = n;  // a sparse accumulation
+            if (bits_differ4(o.x, o.y, o.z, o.w, n.x, n.y, n.z, n.w)) st_nt4(gr, qi, n);  // a sparse accumulation
         }
     }
 }
@@ -769,14 +768,14 @@ __global__ void __launch_bounds__(kRThreads)
     const int tr = WPR == 1 ? lane : (int)threadIdx.x;
     constexpr int NT = 64 * WPR;
     const int64_t Bq = B >> 2;
-    const vf4* x4 = reinterpret_cast<const vf4*>(x + row * B);
+    const float* xr = x + row * B;
     const float kf = x[row * B];
     const double K = (double)kf;
     vf4 v[NQ];  // a quad past the row holds K: x - K = 0 adds nothing to either moment
 #pragma unroll
     for (int k = 0; k < NQ; ++k) {
         const int64_t qi = tr + (int64_t)k * NT;
-        v[k] = qi < Bq ? x4[qi] : vf4{kf, kf, kf, kf};
+        v[k] = qi < Bq ? ld_ntv(xr, qi) : vf4{kf, kf, kf, kf};
     }
     Mom m{0.0, 0.0};
 #pragma unroll
@@ -815,18 +814,18 @@ __global__ void __launch_bounds__(kRThreads)
     Mom m{0.0, 0.0};
     if (VEC) {
         const int64_t nq = len >> 2;
-        const vf4* x4 = reinterpret_cast<const vf4*>(x + start);
+        const float* xs = x + start;
         for (int64_t q = t; q < nq; q += 2 * kRThreads) {
-            const vf4 a = x4[q];
+            const vf4 a = ld_ntv(xs, q);
             // a quad past the chunk holds K: x - K = 0 adds nothing to either moment
-            const vf4 b = q + kRThreads < nq ? x4[q + kRThreads] : vf4{kf, kf, kf, kf};
+            const vf4 b = q + kRThreads < nq ? ld_ntv(xs, q + kRThreads) : vf4{kf, kf, kf, kf};
 #pragma unroll
             for (int j = 0; j < 4; ++j) mom_add(m, a[j], K);
 #pragma unroll
             for (int j = 0; j < 4; ++j) mom_add(m, b[j], K);
         }
     } else {
-        for (int64_t j = t; j < len; j += kRThreads) mom_add(m, x[start + j], K);
+        for (int64_t j = t; j < len; j += kRThreads) mom_add(m, ld_nt(x + start + j), K);
     }
     m = mom_wave(m);
     if (lane == 0) ws[w] = m;
@@ -861,11 +860,11 @@ __global__ void __launch_bounds__(kRThreads)
     const int64_t base = a * B * C + c;
     auto load = [&](int64_t b, float* v) {
         if (VEC) {
-            const vf4 q = *reinterpret_cast<const vf4*>(x + base + b * C);
+            const vf4 q = ld_ntv(x + base + b * C, 0);
 #pragma unroll
             for (int j = 0; j < W; ++j) v[j] = q[j];
         } else {
-            v[0] = x[base + b * C];
+            v[0] = ld_nt(x + base + b * C);
         }
     };
     double K[W];
@@ -1355,7 +1354,7 @@ __global__ void __launch_bounds__(kRThreads)
     auto load_step = [&](vf4 (&q)[4], const vf4* r, int64_t base) {
 #pragma unroll
         for (int u = 0; u < 4; ++u)
-            if (base + lane + 64 * u < cnt) q[u] = r[base + lane + 64 * u];
+            if (base + lane + 64 * u < cnt) q[u] = __builtin_nontemporal_load(r + base + lane + 64 * u);
     };
     auto add_rest = [&](float a, const vf4* r) {  // the plane's steps after the first
         for (int64_t base = 256; base < cnt; base += 256) {
@@ -1506,15 +1505,13 @@ __global__ void __launch_bounds__(kRThreads)
     const int64_t base = r0 * B;
     const int cnt = (int)(rows * B);
     const int nq = cnt >> 2;
-    const float4* u4 = reinterpret_cast<const float4*>(ld.ug + base);
-    const float4* a4 = reinterpret_cast<const float4*>(ld.a + base);
     for (int i = t; i < nq; i += kRThreads) {
-        us4[i] = u4[i];
-        as4[i] = a4[i];
+        us4[i] = ld_nt4(ld.ug + base, i);
+        as4[i] = ld_nt4(ld.a + base, i);
     }
     for (int i = (nq << 2) + t; i < cnt; i += kRThreads) {
-        us[i] = ld.ug[base + i];
-        as[i] = ld.a[base + i];
+        us[i] = ld_nt(ld.ug + base + i);
+        as[i] = ld_nt(ld.a + base + i);
     }
     __syncthreads();
     if (t < rows) {

@@ -336,8 +336,7 @@ __global__ void __launch_bounds__(256) k_fill(float* __restrict__ t, float v, in
     const int64_t nq = n >> 2;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    float4* t4 = reinterpret_cast<float4*>(t);
-    for (int64_t q = i; q < nq; q += stride) t4[q] = make_float4(v, v, v, v);
+    for (int64_t q = i; q < nq; q += stride) st_nt4(t, q, make_float4(v, v, v, v));
     if (i == 0)
         for (int64_t j = nq << 2; j < n; ++j) t[j] = v;
 }
@@ -349,7 +348,8 @@ __global__ void __launch_bounds__(256) k_fill_scalar(float* __restrict__ t, floa
 
 __global__ void __launch_bounds__(256) k_copy(float4* __restrict__ dst, const float4* __restrict__ src, int64_t nq) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < nq; q += stride) dst[q] = src[q];
+    for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < nq; q += stride)
+        st_ntv(reinterpret_cast<float*>(dst), q, ld_ntv(reinterpret_cast<const float*>(src), q));
 }
 
 // Counter-based SplitMix64 (Steele, Lea & Flood, "Fast splittable pseudorandom number

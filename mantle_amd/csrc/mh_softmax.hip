@@ -79,11 +79,10 @@ __device__ __forceinline__ void stage_tile(float* dst, const float* __restrict__
     int done = 0;
     if (al) {
         const int nq = cnt >> 2;
-        const float4* s4 = reinterpret_cast<const float4*>(src + base);
-        for (int i = t; i < nq; i += kSThreads) reinterpret_cast<float4*>(dst)[i] = s4[i];
+        for (int i = t; i < nq; i += kSThreads) reinterpret_cast<float4*>(dst)[i] = ld_nt4(src + base, i);
         done = nq << 2;
     }
-    for (int i = done + t; i < cnt; i += kSThreads) dst[i] = src[base + i];
+    for (int i = done + t; i < cnt; i += kSThreads) dst[i] = ld_nt(src + base + i);
 }
 
 __device__ __forceinline__ void unstage_tile(float* __restrict__ dst, const float* src, int64_t base, int cnt,
@@ -92,11 +91,10 @@ __device__ __forceinline__ void unstage_tile(float* __restrict__ dst, const floa
     int done = 0;
     if (al) {
         const int nq = cnt >> 2;
-        float4* d4 = reinterpret_cast<float4*>(dst + base);
-        for (int i = t; i < nq; i += kSThreads) d4[i] = reinterpret_cast<const float4*>(src)[i];
+        for (int i = t; i < nq; i += kSThreads) st_nt4(dst + base, i, reinterpret_cast<const float4*>(src)[i]);
         done = nq << 2;
     }
-    for (int i = done + t; i < cnt; i += kSThreads) dst[base + i] = src[i];
+    for (int i = done + t; i < cnt; i += kSThreads) st_nt(dst + base + i, src[i]);
 }
 
 __device__ __forceinline__ float block_sum(float v, float* ws) {
@@ -422,13 +420,13 @@ struct TileRegs {
 __device__ __forceinline__ void tile_load(TileRegs& r, const float* __restrict__ src, int64_t base, int cnt) {
     const int t = threadIdx.x;
     const int nq = cnt >> 2;
-    const vf4* s4 = reinterpret_cast<const vf4*>(src + base);
-    if (t < nq) r.q0 = s4[t];
-    if (t + kSThreads < nq) r.q1 = s4[t + kSThreads];
-    if (t + 2 * kSThreads < nq) r.q2 = s4[t + 2 * kSThreads];
-    if (t + 3 * kSThreads < nq) r.q3 = s4[t + 3 * kSThreads];
+    const float* sb = src + base;
+    if (t < nq) r.q0 = ld_ntv(sb, t);
+    if (t + kSThreads < nq) r.q1 = ld_ntv(sb, t + kSThreads);
+    if (t + 2 * kSThreads < nq) r.q2 = ld_ntv(sb, t + 2 * kSThreads);
+    if (t + 3 * kSThreads < nq) r.q3 = ld_ntv(sb, t + 3 * kSThreads);
     const int tl = (nq << 2) + t;
-    if (t < 4 && tl < cnt) r.tail = src[base + tl];
+    if (t < 4 && tl < cnt) r.tail = ld_nt(sb + tl);
 }
 
 __device__ __forceinline__ void tile_to_lds(float* dst, const TileRegs& r, int cnt) {
@@ -705,7 +703,7 @@ __device__ __forceinline__ void load_row(float* v, const float* __restrict__ src
         for (int q = 0; q < NE / 4; ++q) {
             const int qi = lane + 64 * q;
             if (4 * qi < K) {
-                const float4 f = reinterpret_cast<const float4*>(src)[qi];
+                const float4 f = ld_nt4(src, qi);
                 v[4 * q] = f.x;
                 v[4 * q + 1] = f.y;
                 v[4 * q + 2] = f.z;
@@ -718,7 +716,7 @@ __device__ __forceinline__ void load_row(float* v, const float* __restrict__ src
 #pragma unroll
         for (int i = 0; i < NE; ++i) {
             const int k = slot_elem<VEC>(lane, i);
-            v[i] = k < K ? src[k] : 0.0f;
+            v[i] = k < K ? ld_nt(src + k) : 0.0f;
         }
     }
 }
@@ -730,13 +728,13 @@ __device__ __forceinline__ void store_row(float* __restrict__ dst, const float* 
         for (int q = 0; q < NE / 4; ++q) {
             const int qi = lane + 64 * q;
             if (4 * qi < K)
-                reinterpret_cast<float4*>(dst)[qi] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+                st_nt4(dst, qi, make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]));
         }
     } else {
 #pragma unroll
         for (int i = 0; i < NE; ++i) {
             const int k = slot_elem<VEC>(lane, i);
-            if (k < K) dst[k] = v[i];
+            if (k < K) st_nt(dst + k, v[i]);
         }
     }
 }

@@ -15,6 +15,7 @@
 
 #include <float.h>
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -381,21 +382,13 @@ float or_reduce_all(int op, const float* t, int64_t n) {
 /* reduce (one axis), tensorutils.mojo:622-684, with tsum :746-757, tmean :760-772 (sum,
  * then accumulate_op[div] by f32(dim)) and tmax :865-876. Output i reads
  * base = (i % s) + (i / s) * (s * d), lanes over j as in or_reduce_all. */
-int or_reduce_axis(int op, float* res, const float* t, const or_shape* s, int axis) {
-    if (!shape_ok(s)) return OR_ERR_RANK;
-    if (axis < 0 || axis >= s->rank) return OR_ERR_SHAPE;
-    if (op != OR_SUM && op != OR_MEAN && op != OR_MAX) return OR_ERR_OP;
-    int64_t sa = 1;
-    for (int i = s->rank - 1; i > axis; --i) sa *= s->dims[i];
-    const int64_t d = s->dims[axis];
-    int64_t nout = 1;
-    for (int i = 0; i < s->rank; ++i)
-        if (i != axis) nout *= s->dims[i];
+/* Outputs [i0, i1) of an axis reduce: the body of parallel_reduce (tensorutils.mojo:651-680). */
+static void reduce_axis_range(int op, float* res, const float* t, int64_t sa, int64_t d, int64_t i0, int64_t i1) {
     const int w = g_nelts;
     const int rop = op == OR_MAX ? OR_MAX : OR_SUM;
     const float start = op == OR_MAX ? -FLT_MAX : 0.0f;
     const int64_t full = d - d % w;
-    for (int64_t i = 0; i < nout; ++i) {
+    for (int64_t i = i0; i < i1; ++i) {
         float m[64];
         for (int k = 0; k < w; ++k) m[k] = start;
         const int64_t base = (i % sa) + (i / sa) * (sa * d);
@@ -411,10 +404,75 @@ int or_reduce_axis(int op, float* res, const float* t, const or_shape* s, int ax
         }
         res[i] = lanes_combine(rop, m, w);
     }
-    if (op == OR_MEAN) {
+    if (op == OR_MEAN) { /* tmean: accumulate_op[div] by f32(dim) (tensorutils.mojo:760-772) */
         const float fd = (float)d;
-        for (int64_t i = 0; i < nout; ++i) res[i] = res[i] / fd;
+        for (int64_t i = i0; i < i1; ++i) res[i] = res[i] / fd;
     }
+}
+
+static int axis_geometry(int op, const or_shape* s, int axis, int64_t* sa, int64_t* d, int64_t* nout) {
+    if (!shape_ok(s)) return OR_ERR_RANK;
+    if (axis < 0 || axis >= s->rank) return OR_ERR_SHAPE;
+    if (op != OR_SUM && op != OR_MEAN && op != OR_MAX) return OR_ERR_OP;
+    *sa = 1;
+    for (int i = s->rank - 1; i > axis; --i) *sa *= s->dims[i];
+    *d = s->dims[axis];
+    *nout = 1;
+    for (int i = 0; i < s->rank; ++i)
+        if (i != axis) *nout *= s->dims[i];
+    return OR_OK;
+}
+
+/* reduce along an axis (tensorutils.mojo:622-684): output i reads the line starting at
+ * base = (i % s) + (i / s) * (s * d), lanes over j as in or_reduce_all. */
+int or_reduce_axis(int op, float* res, const float* t, const or_shape* s, int axis) {
+    int64_t sa, d, nout;
+    const int rc = axis_geometry(op, s, axis, &sa, &d, &nout);
+    if (rc != OR_OK) return rc;
+    reduce_axis_range(op, res, t, sa, d, 0, nout);
+    return OR_OK;
+}
+
+typedef struct {
+    int op;
+    float* res;
+    const float* t;
+    int64_t sa, d, i0, i1;
+} axis_job;
+
+static void* axis_worker(void* p) {
+    const axis_job* j = (const axis_job*)p;
+    reduce_axis_range(j->op, j->res, j->t, j->sa, j->d, j->i0, j->i1);
+    return NULL;
+}
+
+/* The same reduction with its outputs spread over `nthreads` threads in contiguous blocks, as
+ * parallelize[parallel_reduce](num_elements / dim(axis)) does (tensorutils.mojo:682). Every
+ * output is computed exactly as by or_reduce_axis, so the results are identical. */
+int or_reduce_axis_mt(int op, float* res, const float* t, const or_shape* s, int axis, int nthreads) {
+    int64_t sa, d, nout;
+    const int rc = axis_geometry(op, s, axis, &sa, &d, &nout);
+    if (rc != OR_OK) return rc;
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    if ((int64_t)nthreads > nout) nthreads = nout > 0 ? (int)nout : 1;
+    pthread_t th[256];
+    int running[256] = {0};
+    axis_job jobs[256];
+    const int64_t per = (nout + nthreads - 1) / nthreads;
+    int blocks = 0;
+    for (int k = 0; k < nthreads; ++k) {
+        const int64_t i0 = k * per, i1 = i0 + per < nout ? i0 + per : nout;
+        if (i0 >= i1) break;
+        jobs[k] = (axis_job){op, res, t, sa, d, i0, i1};
+        blocks = k + 1;
+        if (k == 0) continue; /* the calling thread takes block 0 */
+        if (pthread_create(&th[k], NULL, axis_worker, &jobs[k]) == 0) running[k] = 1;
+        else axis_worker(&jobs[k]); /* no thread: run the block here */
+    }
+    if (blocks > 0) axis_worker(&jobs[0]);
+    for (int k = 1; k < blocks; ++k)
+        if (running[k]) pthread_join(th[k], NULL);
     return OR_OK;
 }
 

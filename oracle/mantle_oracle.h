@@ -74,6 +74,9 @@ int or_elwise_op(int op, float* res, const float* t1, const or_shape* s1,
 int or_accumulate_grad(float* grad, const or_shape* sg, const float* rg, const or_shape* srg);
 float or_reduce_all(int op, const float* t, int64_t n);
 int or_reduce_axis(int op, float* res, const float* t, const or_shape* s, int axis);
+/* or_reduce_axis with its outputs split over nthreads threads (the reference's parallelize
+ * over outputs, tensorutils.mojo:682); identical results. For the CPU baseline. */
+int or_reduce_axis_mt(int op, float* res, const float* t, const or_shape* s, int axis, int nthreads);
 
 /* ---- op-level dispatch (mantle/autograd/ops/ops.mojo:243-311, 355-463) ----
  * axis < 0 means "no axis attribute" (reduce over all elements). */

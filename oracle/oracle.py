@@ -76,6 +76,7 @@ def lib():
             ("or_accumulate_grad", ctypes.c_int, [f32p, shp, f32p, shp]),
             ("or_reduce_all", ctypes.c_float, [ctypes.c_int, f32p, i64]),
             ("or_reduce_axis", ctypes.c_int, [ctypes.c_int, f32p, f32p, shp, ctypes.c_int]),
+            ("or_reduce_axis_mt", ctypes.c_int, [ctypes.c_int, f32p, f32p, shp, ctypes.c_int, ctypes.c_int]),
             ("or_forward_op", ctypes.c_int,
              [ctypes.c_int, f32p, f32p, shp, f32p, shp, ctypes.c_int]),
             ("or_backward_op", ctypes.c_int,
@@ -198,6 +199,16 @@ def reduce_all(op: int, x) -> np.float32:
     return np.float32(lib().or_reduce_all(op, _ptr(x), x.size))
 
 
+def reduce_axis_mt(op: int, x, axis: int, nthreads: int) -> np.ndarray:
+    """SUM/MEAN/MAX along `axis` with the outputs spread over `nthreads` threads
+    (tensorutils.mojo:682 parallelize); the result keeps the reduced axis as size 1."""
+    x = _f32(x)
+    res = np.zeros(reduced_shape(x.shape, axis), np.float32)
+    _check(lib().or_reduce_axis_mt(op, _ptr(res), _ptr(x), make_shape(x.shape), int(axis), int(nthreads)),
+           "reduce_axis_mt")
+    return res
+
+
 def reduced_shape(shape, axis):
     if axis is None or axis < 0:
         return (1,)
@@ -255,6 +266,25 @@ def backward_op(tensor_id: int, op: int, ug, t1, t2=None, grad=None, axis=None) 
         ax, _ptr(g))
     _check(rc, f"backward_op({tensor_id}, {op})")
     return g
+
+
+def forward_op_into(op: int, res: np.ndarray, t1: np.ndarray, t2: np.ndarray = None, axis: int = -1) -> None:
+    """forward_op into a preallocated float32 result (as Model's arena slots are); contiguous
+    float32 inputs only, no copies. For the timed CPU baseline."""
+    rc = lib().or_forward_op(op, _ptr(res), _ptr(t1), make_shape(t1.shape or (1,)),
+                             _ptr(t2) if t2 is not None else None,
+                             make_shape(t2.shape or (1,)) if t2 is not None else None, int(axis))
+    _check(rc, f"forward_op({op})")
+
+
+def backward_op_into(tensor_id: int, op: int, grad: np.ndarray, ug: np.ndarray, t1: np.ndarray,
+                     t2: np.ndarray = None, axis: int = -1) -> None:
+    """backward_op accumulating into `grad` in place (ops.mojo:355-463); contiguous float32
+    arrays only, no copies. For the timed CPU baseline."""
+    rc = lib().or_backward_op(tensor_id, op, _ptr(ug), make_shape(ug.shape or (1,)), _ptr(t1),
+                              make_shape(t1.shape or (1,)), _ptr(t2) if t2 is not None else None,
+                              make_shape(t2.shape or (1,)) if t2 is not None else None, int(axis), _ptr(grad))
+    _check(rc, f"backward_op({tensor_id}, {op})")
 
 
 def backward_op_rc(tensor_id: int, op: int, ug, t1, t2=None, axis=None) -> int:

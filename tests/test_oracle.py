@@ -518,3 +518,13 @@ def test_tstd_lines_are_tmean_lines():
     np.testing.assert_array_equal(got, a)
     y = np.transpose(x, (2, 0, 1)).copy()  # the same lines along axis 0
     np.testing.assert_array_equal(O.tstd(y, 0).reshape(-1), a)
+
+
+@pytest.mark.parametrize("shape,axis", [((64, 37), 0), ((37, 64), 1), ((5, 7, 33), 1), ((3, 1), 0), ((1000, 3), 0)])
+@pytest.mark.parametrize("nthreads", [1, 3, 8])
+def test_threaded_axis_reduce_is_identical(shape, axis, nthreads):
+    """The CPU baseline's threaded axis reduce (outputs split over a pool, tensorutils.mojo:682)
+    gives the serial restatement's bits: every output is computed the same way."""
+    x = np.random.default_rng(13).standard_normal(shape).astype(np.float32)
+    for op in (O.SUM, O.MEAN, O.MAX):
+        assert_bitexact(O.reduce_axis_mt(op, x, axis, nthreads), O.forward_op(op, x, axis=axis), f"op {op}")
