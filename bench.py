@@ -690,8 +690,8 @@ def run_rows(L, reps):
 
 def run_graph(L, reps, steps=200):
     """One training step (zero_grad, forward, backward) of a model through the native executor,
-    eager against HIP-graph replay: config 1's ADD(bias) -> RELU graph with a MEAN loss (the
-    launch-bound case) and config 5's head chain. Wall time per step on the host (inputs copied
+    eager against the replay of the step captured as one HIP graph (MH_PASS_STEP): config 1's
+    ADD(bias) -> RELU graph with a MEAN loss (the launch-bound case) and config 5's head chain. Wall time per step on the host (inputs copied
     from device buffers into their slots every step), one synchronisation per `steps` steps."""
     import time
     import mantle_amd as mm
@@ -729,15 +729,12 @@ def run_graph(L, reps, steps=200):
             if mode == "graph":
                 for dst, src, nb in slots:
                     chk(L, L.mh_memcpy_d2d(dst, src, nb), "copy")
-                model.capture("forward")
-                model.capture("backward")
+                model.capture("step")
 
-                def step():  # inputs into their slots, then the two graphs
-                    chk(L, L.mh_model_zero_grad(h), "zero_grad")
+                def step():  # inputs into their slots, then one graph: zero_grad, forward, backward
                     for dst, src, nb in slots:
                         chk(L, L.mh_memcpy_d2d(dst, src, nb), "copy")
-                    chk(L, L.mh_model_replay(h, 0), "replay fwd")
-                    chk(L, L.mh_model_replay(h, 1), "replay bwd")
+                    chk(L, L.mh_model_replay(h, 2), "replay step")
             else:
                 def step():  # Model.forward copies the inputs in, then every node; Model.backward
                     chk(L, L.mh_model_zero_grad(h), "zero_grad")

@@ -336,14 +336,21 @@ int mh_model_tensor(mh_model* m, int32_t sym, float** dptr);
 int mh_model_grad(mh_model* m, int32_t sym, float** dptr);
 /* parameters.grads.set_zero (collection.mojo:221-224): one fill over the gradient arena. */
 int mh_model_zero_grad(mh_model* m);
-/* HIP-graph form of the two passes: mh_model_capture runs the pass once (library buffers
- * reach their sizes), then records its launches on the library stream into a graph;
- * mh_model_replay launches the graph. MH_PASS_FORWARD is every node (inputs are not part of
- * it: write them into their slots first, through mh_model_tensor); MH_PASS_BACKWARD seeds
- * the loss gradient with 1.0 and runs every node in reverse. The graph holds kernel launches
- * only (no memset or host-copy nodes). Capturing again replaces the graph. */
+/* HIP-graph form of the passes: mh_model_capture runs the pass once (library buffers reach
+ * their sizes), then records its launches on the library stream into a graph; mh_model_replay
+ * launches the graph. MH_PASS_FORWARD is every node (inputs are not part of it: write them into
+ * their slots first, through mh_model_tensor); MH_PASS_BACKWARD seeds the loss gradient with 1.0
+ * and runs every node in reverse; MH_PASS_STEP is a training step's device work in one graph:
+ * the gradient arena zeroed (mh_model_zero_grad), then the forward and backward passes. A graph
+ * launch costs the host about as much as launching a handful of kernels, so a step replays
+ * fastest as one MH_PASS_STEP graph. The graph holds kernel launches only (no memset or
+ * host-copy nodes). Capturing again replaces the graph. A captured graph keeps the library
+ * buffers it was recorded with (a library buffer that grows while any graph exists is kept,
+ * and freed once no captured graph is left); after mh_shutdown and mh_init, replay returns
+ * MH_ERR_INVALID until the pass is captured again. */
 #define MH_PASS_FORWARD 0
 #define MH_PASS_BACKWARD 1
+#define MH_PASS_STEP 2
 int mh_model_capture(mh_model* m, int pass);
 int mh_model_replay(mh_model* m, int pass);
 

@@ -52,7 +52,7 @@ SYM_INPUT, SYM_PARAM, SYM_NODE = 0, 1, 2
 FROM_HOST, FROM_DEVICE = 0, 1
 MODEL_FUSE_BIAS_RELU = 1
 MODEL_FUSE_ROWS = 2
-PASS_FORWARD, PASS_BACKWARD = 0, 1
+PASS_FORWARD, PASS_BACKWARD, PASS_STEP = 0, 1, 2
 
 
 class MantleHipError(RuntimeError):

@@ -59,8 +59,8 @@ struct mh_model {
     };
     std::vector<RowGroup> rows;
     std::vector<int> row_of;  // per node: its RowGroup, or -1
-    hipGraphExec_t graph[2] = {nullptr, nullptr};  // captured passes (MH_PASS_FORWARD / _BACKWARD)
-    uint64_t graph_epoch[2] = {0, 0};               // the mh_init epoch each was captured in
+    hipGraphExec_t graph[3] = {nullptr, nullptr, nullptr};  // captured passes (MH_PASS_FORWARD / _BACKWARD / _STEP)
+    uint64_t graph_epoch[3] = {0, 0, 0};                     // the mh_init epoch each was captured in
 };
 
 namespace mh {
@@ -419,7 +419,7 @@ static int write_inputs(mh_model* m, int32_t ninputs, const float* const* inputs
 // node; backward = the loss gradient seeded with 1.0, then every node in reverse.
 static int check_pass(const mh_model* m, int pass) {
     if (pass == MH_PASS_FORWARD) return MH_OK;
-    if (pass != MH_PASS_BACKWARD) return fail(MH_ERR_INVALID, "unknown pass %d", pass);
+    if (pass != MH_PASS_BACKWARD && pass != MH_PASS_STEP) return fail(MH_ERR_INVALID, "unknown pass %d", pass);
     if (m->g.loss < 0) return fail(MH_ERR_INVALID, "backward pass: the graph has no loss symbol");
     if (!m->gr[m->g.loss]) return fail(MH_ERR_INVALID, "backward pass: the loss is not trainable");
     return MH_OK;
@@ -427,17 +427,18 @@ static int check_pass(const mh_model* m, int pass) {
 
 static int enqueue_pass(mh_model* m, int pass) {
     const mh_graph& g = m->g;
-    if (pass == MH_PASS_FORWARD) {
+    if (pass == MH_PASS_STEP && m->grad_arena)  // parameters.grads.set_zero (collection.mojo:221-224)
+        MH_TRY(mh_zero(m->grad_arena, (int64_t)m->grad_floats));
+    if (pass == MH_PASS_FORWARD || pass == MH_PASS_STEP)
         for (size_t i = 0; i < g.nodes.size(); ++i) MH_TRY(run_forward_node(m, i));
-        return MH_OK;
-    }
+    if (pass == MH_PASS_FORWARD) return MH_OK;
     MH_TRY(mh_fill(m->gr[g.loss], 1.0f, numel(g.syms[g.loss].shape)));  // model.mojo:176-180
     for (size_t k = g.nodes.size(); k-- > 0;) MH_TRY(run_backward_node(m, k));
     return MH_OK;
 }
 
 static void drop_graphs(mh_model* m) {
-    for (int p = 0; p < 2; ++p) {
+    for (int p = 0; p < 3; ++p) {
         if (m->graph[p]) {
             (void)hipGraphExecDestroy(m->graph[p]);
             (void)graph_release(m->graph_epoch[p]);
@@ -723,7 +724,8 @@ int mh_model_capture(mh_model* m, int pass) {
 int mh_model_replay(mh_model* m, int pass) {
     if (!m) return fail(MH_ERR_NULL, "mh_model_replay: null model");
     MH_TRY(require_init());
-    if (pass != MH_PASS_FORWARD && pass != MH_PASS_BACKWARD) return fail(MH_ERR_INVALID, "unknown pass %d", pass);
+    if (pass != MH_PASS_FORWARD && pass != MH_PASS_BACKWARD && pass != MH_PASS_STEP)
+        return fail(MH_ERR_INVALID, "unknown pass %d", pass);
     if (!m->graph[pass]) return fail(MH_ERR_INVALID, "mh_model_replay: pass %d has not been captured", pass);
     if (m->graph_epoch[pass] != ctx().epoch)
         return fail(MH_ERR_INVALID, "mh_model_replay: pass %d was captured before the last mh_shutdown; capture it again",

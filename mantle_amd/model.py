@@ -151,18 +151,19 @@ class Model:
             _lib.call("mh_model_backward", self._h, 0, None, _lib.FROM_HOST)
 
     # ---- HIP-graph replay of the passes ----
-    _PASSES = {"forward": _lib.PASS_FORWARD, "backward": _lib.PASS_BACKWARD}
+    _PASSES = {"forward": _lib.PASS_FORWARD, "backward": _lib.PASS_BACKWARD, "step": _lib.PASS_STEP}
 
     def capture(self, pass_: str) -> None:
-        """Records the forward pass (every node) or the backward pass (loss seed + every node
-        in reverse) as a HIP graph; the pass runs once eagerly first."""
+        """Records the forward pass (every node), the backward pass (loss seed + every node in
+        reverse) or a whole step (zero_grad, forward, backward) as a HIP graph; the pass runs
+        once eagerly first."""
         _lib.call("mh_model_capture", self._h, self._PASSES[pass_])
 
     def replay(self, pass_: str) -> Optional[Tensor]:
         """Launches the captured pass; write inputs into parameters.tensors first. The forward
         pass returns the loss slot."""
         _lib.call("mh_model_replay", self._h, self._PASSES[pass_])
-        if pass_ == "forward" and self.graph.loss_out is not None:
+        if pass_ in ("forward", "step") and self.graph.loss_out is not None:
             return self.parameters.tensors[self.graph.loss_out]
         return None
 

@@ -365,8 +365,9 @@ def test_model_param_span_layout_and_single_launch_adam(gpu):
 
 @pytest.mark.parametrize("which", ["bias_relu_fused", "config5"])
 def test_model_graph_replay_matches_eager(gpu, which):
-    """Captured forward / backward passes replayed three times, with new inputs, zero_grad
-    and host reads between replays; every replay bit-identical to an eager model."""
+    """Captured forward / backward passes and the whole-step graph (zero_grad, forward, backward)
+    replayed in turn with new inputs and host reads between replays; every replay bit-identical
+    to an eager model."""
     m = gpu.m
     if which == "bias_relu_fused":
         nodes = _bias_relu_nodes() + [(OPS["MEAN"], ["r"], None, "l")]
@@ -390,16 +391,20 @@ def test_model_graph_replay_matches_eager(gpu, which):
     (_, syms_a, inputs, eager), (_, syms_b, _, graphed) = models
     graphed.capture("forward")
     graphed.capture("backward")
-    for it in range(3):
+    graphed.capture("step")
+    for it in range(6):
         iv = new_inputs(it)
         eager.parameters.grads.set_zero()
         la = eager.forward(*[iv[n] for n in inputs]).to_numpy()
         eager.backward()
         for n in inputs:
             graphed.parameters.tensors[syms_b[n]] = iv[n]
-        graphed.parameters.grads.set_zero()
-        lb = graphed.replay("forward").to_numpy()
-        graphed.replay("backward")
+        if it % 2 == 0:  # the two pass graphs, zero_grad eager between them
+            graphed.parameters.grads.set_zero()
+            lb = graphed.replay("forward").to_numpy()
+            graphed.replay("backward")
+        else:  # the whole step as one graph (zero_grad inside)
+            lb = graphed.replay("step").to_numpy()
         assert_bitexact(lb, la, f"{which} loss, replay {it}")
         for name, sa in syms_a.items():
             sb = syms_b[name]
