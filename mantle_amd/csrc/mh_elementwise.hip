@@ -3,8 +3,8 @@
 // One engine serves every elementwise entry point: an output stream (written, or
 // read-modify-written for "grad = grad + rg") and up to four input streams, each FULL (same
 // shape as the output), SCALAR (one element, loaded once per thread) or BCAST (strided in the
-// collapsed output space). Same-shape work takes the float4 path: 256-thread blocks, one
-// 128-bit access per stream per thread, all loads issued before any arithmetic. Two common
+// collapsed output space). Same-shape work takes the float4 path: one-wavefront workgroups,
+// one 128-bit access per stream per thread, all loads issued before any arithmetic. Two common
 // broadcast forms of a [rows, K] output have engines of their own: per-row operands ([rows, 1],
 // K >= 4: one fast division per quad) and per-column operands ([1, K], K % 4 == 0: one fast
 // modulo per quad). Other broadcasts decode the output coordinate of each quad with
@@ -15,7 +15,10 @@
 
 namespace mh {
 
-constexpr int kThreads = 256;
+// One wavefront per workgroup: with non-temporal streams, 64-thread workgroups of one quad per
+// thread streamed fastest on gfx950 for every operand count measured (a binary forward at 0.84
+// of peak against 0.80 with 256 threads, the two-gradient backward 0.81 against 0.76).
+constexpr int kThreads = 64;
 
 struct DevScal {
     const float* p[4];

@@ -15,7 +15,8 @@
 
 namespace mh {
 
-constexpr int kFThreads = 256;
+constexpr int kFThreads = 256;     // backward: four waves per workgroup, one per plane group
+constexpr int kFFwdThreads = 64;  // forward: flat quad streams, one-wavefront workgroups
 constexpr int64_t kTicketStride = 32;  // one 128-byte line per channel counter
 
 static inline bool al16f(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -23,7 +24,7 @@ static inline bool al16f(const void* p) { return (reinterpret_cast<uintptr_t>(p)
 // y = x + bias (ADD.forward, basics.mojo:36-43), r = relu(y) (RELU.forward, mlops.mojo:92-97).
 // Plan inputs: 0 = x (FULL), 1 = bias (BCAST, SCALAR or FULL). y, r, x 16-byte aligned.
 template <bool INNER4, bool BIG>
-__global__ void __launch_bounds__(kFThreads)
+__global__ void __launch_bounds__(kFFwdThreads)
     k_bias_relu_fwd4(float* __restrict__ y, float* __restrict__ r, const float* __restrict__ x,
                      const float* __restrict__ bias, ElwPlan pl) {
     const int inner = pl.rank - 1;
@@ -31,8 +32,8 @@ __global__ void __launch_bounds__(kFThreads)
     const int kb = pl.kind[1];
     const float sb = kb == IN_SCALAR ? bias[0] : 0.0f;
     const int64_t nq = pl.n >> 2;
-    const int64_t stride = (int64_t)gridDim.x * kFThreads;
-    for (int64_t q = (int64_t)blockIdx.x * kFThreads + threadIdx.x; q < nq; q += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kFFwdThreads;
+    for (int64_t q = (int64_t)blockIdx.x * kFFwdThreads + threadIdx.x; q < nq; q += stride) {
         const int64_t idx = q * 4;
         float bv[4];
         if (kb == IN_SCALAR) {
@@ -91,11 +92,11 @@ __global__ void __launch_bounds__(kFThreads)
 // Forward over [N, C, S] planes (S % 4 == 0, fewer than 2^31 elements; the bias indexed by C,
 // or a scalar with C == 1): one quad per thread in flat order, its channel
 // (q / (S / 4)) mod C from two fast divisions.
-__global__ void __launch_bounds__(kFThreads)
+__global__ void __launch_bounds__(kFFwdThreads)
     k_bias_relu_fwd_planes(float* __restrict__ y, float* __restrict__ r, const float* __restrict__ x,
                            const float* __restrict__ bias, int64_t nq, uint32_t C, FastDiv fsq, FastDiv fc) {
-    const int64_t stride = (int64_t)gridDim.x * kFThreads;
-    for (int64_t q = (int64_t)blockIdx.x * kFThreads + threadIdx.x; q < nq; q += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kFFwdThreads;
+    for (int64_t q = (int64_t)blockIdx.x * kFFwdThreads + threadIdx.x; q < nq; q += stride) {
         const uint32_t p = fdiv((uint32_t)q, fsq);
         const float bv = bias[p - fdiv(p, fc) * C];
         const vf4 xv = ld_ntv(x, q);
@@ -253,10 +254,10 @@ int mh_bias_relu_fwd(float* y, float* r, const float* x, const mh_shape* psx, co
     }
     const bool big = n >= ((int64_t)1 << 31);
     const bool inner4 = pl.vec_ok && al16f(bias);
-    int64_t blocks = ((n >> 2) + kFThreads - 1) / kFThreads;
+    int64_t blocks = ((n >> 2) + kFFwdThreads - 1) / kFFwdThreads;
     if (blocks < 1) blocks = 1;
     if (blocks > 0x7fffffff) blocks = 0x7fffffff;
-    dim3 g((unsigned)blocks), b(kFThreads);
+    dim3 g((unsigned)blocks), b(kFFwdThreads);
     hipStream_t st = ctx().stream;
     int64_t N = 0, C = 0, S = 0;
     if (!big && pl.kind[1] != IN_FULL && plane_form(pl, &N, &C, &S) && S % 4 == 0) {

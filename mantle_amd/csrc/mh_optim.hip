@@ -20,7 +20,7 @@
 
 namespace mh {
 
-constexpr int kOThreads = 256;
+constexpr int kOThreads = 64;  // one-wavefront workgroups stream fastest on gfx950
 
 struct AdamScal {
     float lr, b1, b2, eps, c1, c2, bc1, bc2;

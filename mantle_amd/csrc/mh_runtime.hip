@@ -384,13 +384,13 @@ static int launch_fill(float* t, float v, int64_t n) {
     if (!t) return fail(MH_ERR_NULL, "fill: null tensor");
     MH_TRY(require_init());
     int64_t work = ((reinterpret_cast<uintptr_t>(t) & 15) == 0) ? (n >> 2) : n;
-    int64_t blocks = (work + 255) / 256;
+    int64_t blocks = (work + 63) / 64;  // one-wavefront workgroups, one quad per thread
     if (blocks < 1) blocks = 1;
-    if (blocks > 65536) blocks = 65536;
+    if (blocks > 0x7fffffff) blocks = 0x7fffffff;
     if ((reinterpret_cast<uintptr_t>(t) & 15) == 0)
-        hipLaunchKernelGGL(k_fill, dim3((unsigned)blocks), dim3(256), 0, ctx().stream, t, v, n);
+        hipLaunchKernelGGL(k_fill, dim3((unsigned)blocks), dim3(64), 0, ctx().stream, t, v, n);
     else
-        hipLaunchKernelGGL(k_fill_scalar, dim3((unsigned)blocks), dim3(256), 0, ctx().stream, t, v, n);
+        hipLaunchKernelGGL(k_fill_scalar, dim3((unsigned)blocks), dim3(64), 0, ctx().stream, t, v, n);
     return finish("fill");
 }
 
@@ -531,9 +531,9 @@ int mh_memcpy_d2d(void* dst, const void* src, size_t bytes) {
     MH_TRY(require_init());
     if (((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) | bytes) & 15) == 0) {
         int64_t nq = (int64_t)(bytes >> 4);
-        int64_t blocks = (nq + 255) / 256;  // one quad per thread (the stride loop covers > 2^31 blocks)
-        if (blocks > 0x7fffffff) blocks = 0x7fffffff;
-        hipLaunchKernelGGL(k_copy, dim3((unsigned)blocks), dim3(256), 0, ctx().stream,
+        int64_t blocks = (nq + 63) / 64;  // one-wavefront workgroups, one quad per thread (the
+        if (blocks > 0x7fffffff) blocks = 0x7fffffff;  // stride loop covers > 2^31 blocks)
+        hipLaunchKernelGGL(k_copy, dim3((unsigned)blocks), dim3(64), 0, ctx().stream,
                            reinterpret_cast<float4*>(dst), reinterpret_cast<const float4*>(src), nq);
     } else {
         MH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx().stream));
