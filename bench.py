@@ -25,8 +25,9 @@ The other configs are measured after the headline step and reported under "workl
         ([32768, 1000]), forward and backward;
   graph a training step (zero_grad, forward, backward) through the native Model, eager against
         HIP-graph replay, for config 1's graph (with a MEAN loss) and config 5's chain;
-  copy  the library's copy kernel over 1 GiB and over one config-3 and one config-5 tensor:
-        the practical streaming rate at each size.
+  copy  the library's copy kernel over 1 GiB and over one config-3 and one config-5 tensor,
+        and an all-element SUM (a read-only pass) over one config-3 tensor, one config-5
+        tensor and the config-5 head's 84 MB: the practical streaming rates at those sizes.
 Workload ops (c3, c4, c5 op by op and fused, rows) get two figures:
   ms            streamed: R launches back to back on the stream over S buffer sets (S copies
                 of the op's tensors, S chosen so that the other sets' traffic between two
@@ -754,9 +755,13 @@ def run_graph(L, reps, steps=200):
 
 
 def run_copy(L, reps):
-    """The library's copy kernel over 1 GiB (the practical streaming rate at the headline's
-    size) and over one tensor of config 3 and of config 5 (the practical rate at those sizes,
-    streamed and isolated like their ops), and the isolated method's floor."""
+    """Practical streaming ceilings: the library's copy kernel over 1 GiB (the headline's size)
+    and over one tensor of config 3 and of config 5; and, for kernels that only read, the
+    library's all-element SUM (one read pass plus a one-block combine) over one config-3 tensor,
+    one config-5 tensor and the config-5 head's two tensors (84 MB, what its fused forward
+    reads). The small sizes are streamed and isolated like their ops; plus the isolated method's
+    floor."""
+    from mantle_amd._lib import make_shape
     d = Dev(L)
     n = 1 << 28
     src, dst = d.zeros("src", n), d.zeros("dst", n)
@@ -770,6 +775,14 @@ def run_copy(L, reps):
         sets = replicate(d, [(f"s_{tag}", m), (f"d_{tag}", m)], 8 * m)
         sm, si = time_both(d, small, sets, reps)
         out.update(op_report(small, sm, si))
+    for tag, m in (("read_c3_tensor", 6422528), ("read_c5_tensor", 10485760), ("read_c5_head", 2 * 10485760)):
+        d.zeros(f"r_{tag}", m)
+        d.zeros(f"o_{tag}", 1)
+        shp = make_shape((m,))
+        rd = [(tag, lambda P, tag=tag, shp=shp: L.mh_reduce_fwd(8, P[f"o_{tag}"], P[f"r_{tag}"], shp, -1), 4 * m + 4)]
+        sets = replicate(d, [(f"r_{tag}", m), (f"o_{tag}", 1)], 4 * m)
+        sm, si = time_both(d, rd, sets, reps)
+        out.update(op_report(rd, sm, si))
     out["isolated_floor_ms"] = isolated_floor(d, reps)
     d.free()
     return out

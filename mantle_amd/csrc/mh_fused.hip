@@ -206,6 +206,93 @@ __global__ void __launch_bounds__(kFThreads)
     }
 }
 
+// Backward over [N, C, S] planes of at least 64 quads, as one flat stream: thread q owns quad q
+// (one-wavefront workgroups), computes
+//   rg = (y > 0 ? 1 : 0) * ug;  g = g_y + rg (0 + rg without g_y);  grad_x = grad_x + g
+// (RELU backward_op, then ADD backward_op operand 0) and adds its quad's g in order. A wave
+// covers 64 consecutive quads, so at most two planes (a plane has >= 64 quads): the wave sums
+// the lanes of its first plane into part[2 w] and those of the next plane into part[2 w + 1]
+// (+0 when there is none), each with an xor butterfly. k_bias_partials_comb then adds every
+// plane's wave partials into grad_bias in a fixed order.
+constexpr int kBFlat = 64;
+
+template <bool HAS_GY, bool HAS_GX, bool HAS_PART>
+__global__ void __launch_bounds__(kBFlat)
+    k_bias_relu_bwd_flat(float* __restrict__ gy, float* __restrict__ gx, const float* __restrict__ y,
+                         const float* __restrict__ ug, int64_t nq, uint32_t Sq, FastDiv fsq, float* part) {
+    const int lane = threadIdx.x;
+    const int64_t q = (int64_t)blockIdx.x * kBFlat + lane;
+    float sum = 0.0f;
+    uint32_t plane = 0;
+    if (q < nq) {
+        const vf4 yv = ld_ntv(y, q), uv = ld_ntv(ug, q);
+        vf4 gv = vf4{0.f, 0.f, 0.f, 0.f}, xv = gv;
+        if (HAS_GY) gv = ld_ntv(gy, q);
+        if (HAS_GX) xv = ld_ntv(gx, q);
+        vf4 gg, o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float rg = (yv[j] > 0.0f ? 1.0f : 0.0f) * uv[j];  // RELU.backward (mlops.mojo:118-123)
+            gg[j] = gv[j] + rg;                                    // accumulate into the grad of y
+            o[j] = xv[j] + gg[j];                                  // ADD backward_op, operand 0
+        }
+        if (HAS_GY) st_ntv(gy, q, gg);
+        if (HAS_GX) st_ntv(gx, q, o);
+        sum = ((gg[0] + gg[1]) + gg[2]) + gg[3];
+        plane = fdiv((uint32_t)q, fsq);
+    }
+    if (HAS_PART) {
+        const uint32_t first = fdiv((uint32_t)((int64_t)blockIdx.x * kBFlat), fsq);
+        float s0 = plane == first ? sum : 0.0f;
+        float s1 = plane == first ? 0.0f : sum;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            s0 = s0 + __shfl_xor(s0, m);
+            s1 = s1 + __shfl_xor(s1, m);
+        }
+        if (lane == 0) {
+            part[2 * (int64_t)blockIdx.x] = s0;
+            part[2 * (int64_t)blockIdx.x + 1] = s1;
+        }
+    }
+}
+
+// grad_bias[c] += the sum of channel c's plane partials written by k_bias_relu_bwd_flat: one
+// 256-thread workgroup per channel; thread t takes the channel's planes n = t, t + 256, ...,
+// loading each plane's wave partials (at most 8 in flight, more one by one) and adding them in
+// wave order; the plane sums add up per thread in order, then per wave (xor butterfly) and
+// across the four waves in order.
+constexpr int kCombPlaneWaves = 8;
+
+__global__ void __launch_bounds__(256)
+    k_bias_partials_comb(float* __restrict__ grad_bias, const float* __restrict__ part, int64_t N, int64_t C,
+                         int64_t Sq) {
+    __shared__ float ws[4];
+    const int64_t c = blockIdx.x;
+    float acc = 0.0f;
+    for (int64_t n = threadIdx.x; n < N; n += 256) {
+        const int64_t p = n * C + c;
+        const int64_t w0 = (p * Sq) / kBFlat, w1 = ((p + 1) * Sq - 1) / kBFlat;
+        float v[kCombPlaneWaves];
+#pragma unroll
+        for (int k = 0; k < kCombPlaneWaves; ++k) {
+            const int64_t w = w0 + k;
+            // slot 0 when the plane is the wave's first, else the wave began in the plane before
+            v[k] = w <= w1 ? part[2 * w + ((w * kBFlat) / Sq == p ? 0 : 1)] : 0.0f;
+        }
+        float sp = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kCombPlaneWaves; ++k) sp = sp + v[k];
+        for (int64_t w = w0 + kCombPlaneWaves; w <= w1; ++w) sp = sp + part[2 * w + ((w * kBFlat) / Sq == p ? 0 : 1)];
+        acc = acc + sp;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
+    if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) grad_bias[c] = grad_bias[c] + (((ws[0] + ws[1]) + ws[2]) + ws[3]);
+}
+
 // [N, C, S] form of x with the bias indexed by C alone, from the collapsed plan of
 // (x, bias); false when the shapes have another form.
 static bool plane_form(const ElwPlan& pl, int64_t* N, int64_t* C, int64_t* S) {
@@ -302,6 +389,34 @@ int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const fl
     const int64_t NG = planes ? (N + G - 1) / G : 0;
     const int64_t nwaves = NG * K * C;
     const int64_t nblocks = (nwaves + 3) / 4;
+    const int64_t nqf = n >> 2;
+    // the flat stream: every wave spans at most two planes, and the combine's threads read at
+    // most a few thousand partials each
+    if (planes && Sq >= kBFlat && n < ((int64_t)1 << 31) && (N + 255) / 256 * (Sq / kBFlat + 2) <= 4096) {
+        const int64_t nw = (nqf + kBFlat - 1) / kBFlat;
+        float* part = nullptr;
+        const bool has_part = grad_bias != nullptr;
+        if (has_part) MH_TRY(scratch(((size_t)(2 * nw) + 64) * sizeof(float), reinterpret_cast<void**>(&part)));
+        hipStream_t st = ctx().stream;
+        dim3 g((unsigned)nw), b(kBFlat);
+        const FastDiv fsq = make_fastdiv((uint32_t)Sq);
+#define MH_BRF(GY, GX, PT) \
+    hipLaunchKernelGGL((k_bias_relu_bwd_flat<GY, GX, PT>), g, b, 0, st, g_y, grad_x, y, ug, nqf, (uint32_t)Sq, fsq, part)
+        const int sel = (g_y ? 4 : 0) | (grad_x ? 2 : 0) | (has_part ? 1 : 0);
+        switch (sel) {
+            case 0: return MH_OK;  // nothing to produce
+            case 1: MH_BRF(false, false, true); break;
+            case 2: MH_BRF(false, true, false); break;
+            case 3: MH_BRF(false, true, true); break;
+            case 4: MH_BRF(true, false, false); break;
+            case 5: MH_BRF(true, false, true); break;
+            case 6: MH_BRF(true, true, false); break;
+            default: MH_BRF(true, true, true); break;
+        }
+#undef MH_BRF
+        if (has_part) hipLaunchKernelGGL(k_bias_partials_comb, dim3((unsigned)C), dim3(256), 0, st, grad_bias, part, N, C, Sq);
+        return finish("mh_bias_relu_bwd_accum");
+    }
     if (planes && nblocks <= 0x7fffffff) {
         float* part = nullptr;
         uint32_t* tk = nullptr;

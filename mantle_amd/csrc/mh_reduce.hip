@@ -25,6 +25,11 @@
 namespace mh {
 
 constexpr int kRThreads = 256;
+// Rows per workgroup of the LDS-staged short-row kernels (one thread per row): one wavefront.
+constexpr int kLdsRows = 64;
+// A launch of one thread per row or output covers at most this many (a grid holds fewer than
+// 2^32 work-items per dimension); larger counts take the grid-stride kernels.
+constexpr int64_t kMaxGridRows = ((int64_t)1 << 32) - 256;
 
 // ---------------------------------------------------------------------------------------
 // reduction policies
@@ -241,28 +246,28 @@ __global__ void __launch_bounds__(kRThreads)
 template <int BMAX>
 __device__ __forceinline__ int64_t stage_rows(float* tile, const float* __restrict__ x, int64_t nrows, int B,
                                               int64_t* rows_out) {
-    const int64_t r0 = (int64_t)blockIdx.x * kRThreads;
-    const int64_t rows = (nrows - r0) < kRThreads ? (nrows - r0) : kRThreads;
+    const int64_t r0 = (int64_t)blockIdx.x * kLdsRows;
+    const int64_t rows = (nrows - r0) < kLdsRows ? (nrows - r0) : kLdsRows;
     const int64_t base = r0 * B;
     const int cnt = (int)(rows * B);
     const int nq = cnt >> 2;
-    for (int i = threadIdx.x; i < nq; i += kRThreads) reinterpret_cast<float4*>(tile)[i] = ld_nt4(x + base, i);
-    for (int i = (nq << 2) + threadIdx.x; i < cnt; i += kRThreads) tile[i] = ld_nt(x + base + i);
+    for (int i = threadIdx.x; i < nq; i += kLdsRows) reinterpret_cast<float4*>(tile)[i] = ld_nt4(x + base, i);
+    for (int i = (nq << 2) + threadIdx.x; i < cnt; i += kLdsRows) tile[i] = ld_nt(x + base + i);
     *rows_out = rows;
     return base;
 }
 
 template <class R, int BMAX>
-__global__ void __launch_bounds__(kRThreads)
+__global__ void __launch_bounds__(kLdsRows)
     k_rows_lds(const float* __restrict__ x, int64_t nrows, int B, float* out, float* out2, int epi, float div) {
-    __shared__ float4 tile4[kRThreads * BMAX / 4];
+    __shared__ float4 tile4[kLdsRows * BMAX / 4];
     float* tile = reinterpret_cast<float*>(tile4);
     int64_t rows;
     stage_rows<BMAX>(tile, x, nrows, B, &rows);
     __syncthreads();
     const int t = threadIdx.x;
     if (t < rows) {
-        const int64_t o = (int64_t)blockIdx.x * kRThreads + t;
+        const int64_t o = (int64_t)blockIdx.x * kLdsRows + t;
         typename R::T acc = row_start<R>(epi, out, o);
         for (int j = 0; j < B; ++j) acc = R::comb(acc, row_val<R>(epi, R::lift(tile[t * B + j])));
         epi_store(out, out2, o, acc, epi, div);
@@ -274,16 +279,16 @@ __global__ void __launch_bounds__(kRThreads)
 // position), stage them in LDS, then thread t reduces row r0 + t in element order -- the
 // order of k_rows_lds and k_rows_thread.
 template <class R, class LD, int BMAX>
-__global__ void __launch_bounds__(kRThreads)
+__global__ void __launch_bounds__(kLdsRows)
     k_rows_lds_ld(LD ld, int64_t nrows, int B, float* out, float* out2, int epi, float div) {
     using T = typename R::T;
-    __shared__ T tile[kRThreads * BMAX];
+    __shared__ T tile[kLdsRows * BMAX];
     ld.setup();
-    const int64_t r0 = (int64_t)blockIdx.x * kRThreads;
-    const int64_t rows = (nrows - r0) < kRThreads ? (nrows - r0) : kRThreads;
+    const int64_t r0 = (int64_t)blockIdx.x * kLdsRows;
+    const int64_t rows = (nrows - r0) < kLdsRows ? (nrows - r0) : kLdsRows;
     const int64_t base = r0 * B;
     const int cnt = (int)(rows * B);
-    for (int i = threadIdx.x; i < cnt; i += kRThreads) tile[i] = ld.get(base + i);
+    for (int i = threadIdx.x; i < cnt; i += kLdsRows) tile[i] = ld.get(base + i);
     __syncthreads();
     const int t = threadIdx.x;
     if (t < rows) {
@@ -297,11 +302,11 @@ __global__ void __launch_bounds__(kRThreads)
 // the row max m and count c from the LDS tile, then grad[i] = grad[i] + (x[i] == m ?
 // fl(1/c) * ug[row] : 0), x read once from HBM.
 template <int BMAX>
-__global__ void __launch_bounds__(kRThreads)
+__global__ void __launch_bounds__(kLdsRows)
     k_max_bwd_rows(float* __restrict__ grad, const float* __restrict__ x, const float* __restrict__ ug,
                    int64_t nrows, int B, FastDiv fdB) {
-    __shared__ float4 tile4[kRThreads * BMAX / 4];
-    __shared__ float sm[kRThreads], sg[kRThreads];
+    __shared__ float4 tile4[kLdsRows * BMAX / 4];
+    __shared__ float sm[kLdsRows], sg[kLdsRows];
     float* tile = reinterpret_cast<float*>(tile4);
     int64_t rows;
     const int64_t base = stage_rows<BMAX>(tile, x, nrows, B, &rows);
@@ -312,13 +317,13 @@ __global__ void __launch_bounds__(kRThreads)
         for (int j = 0; j < B; ++j) acc = RMaxCnt::comb(acc, RMaxCnt::lift(tile[t * B + j]));
         const float f = 1.0f / (float)acc.c;  // basics.mojo:609
         sm[t] = acc.m;
-        sg[t] = f * ug[(int64_t)blockIdx.x * kRThreads + t];
+        sg[t] = f * ug[(int64_t)blockIdx.x * kLdsRows + t];
     }
     __syncthreads();
     const int cnt = (int)(rows * B);
     const int nq = cnt >> 2;
     float* gb = grad + base;
-    for (int i = t; i < nq; i += kRThreads) {
+    for (int i = t; i < nq; i += kLdsRows) {
         const float4 o = ld_nt4(gb, i);
         float r[4];
 #pragma unroll
@@ -330,7 +335,7 @@ __global__ void __launch_bounds__(kRThreads)
         const float4 g = make_float4(o.x + r[0], o.y + r[1], o.z + r[2], o.w + r[3]);
         if (bits_differ4(o.x, o.y, o.z, o.w, g.x, g.y, g.z, g.w)) st_nt4(gb, i, g);  // a sparse accumulation
     }
-    for (int e = (nq << 2) + t; e < cnt; e += kRThreads) {
+    for (int e = (nq << 2) + t; e < cnt; e += kLdsRows) {
         const int row = (int)fdiv((uint32_t)e, fdB);
         grad[base + e] = grad[base + e] + (tile[e] == sm[row] ? sg[row] : 0.0f);
     }
@@ -1123,7 +1128,7 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
                     float* out2, float div, float* tmp, bool nosplit = false, bool combine = false) {
     if (A * C == 0) return MH_OK;
     hipStream_t st = ctx().stream;
-    if (C > 1 && B <= 64 && (epi == EPI_SEQ_ACCUM || epi == EPI_SEQ_ACCUM_NEG) && A * C < ((int64_t)1 << 38)) {
+    if (C > 1 && B <= 64 && (epi == EPI_SEQ_ACCUM || epi == EPI_SEQ_ACCUM_NEG) && A * C < kMaxGridRows) {
         const unsigned blocks = (unsigned)((A * C + kRThreads - 1) / kRThreads);
         hipLaunchKernelGGL((k_cols_seq<R, LD>), dim3(blocks), dim3(kRThreads), 0, st, ld, A, B, C, out, out2, epi,
                            div);
@@ -1136,28 +1141,28 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
     if (C == 1) {
         if (B <= 64) {
             if constexpr (std::is_same<LD, LdPlain<R>>::value) {
-                if (B <= 32 && vec_ok && A <= ((int64_t)1 << 40)) {
-                    const unsigned blocks = (unsigned)((A + kRThreads - 1) / kRThreads);
+                if (B <= 32 && vec_ok && A < kMaxGridRows) {
+                    const unsigned blocks = (unsigned)((A + kLdsRows - 1) / kLdsRows);
                     if (B <= 16)
-                        hipLaunchKernelGGL((k_rows_lds<R, 16>), dim3(blocks), dim3(kRThreads), 0, st, ld.x, A,
+                        hipLaunchKernelGGL((k_rows_lds<R, 16>), dim3(blocks), dim3(kLdsRows), 0, st, ld.x, A,
                                            (int)B, out, out2, epi, div);
                     else
-                        hipLaunchKernelGGL((k_rows_lds<R, 32>), dim3(blocks), dim3(kRThreads), 0, st, ld.x, A,
+                        hipLaunchKernelGGL((k_rows_lds<R, 32>), dim3(blocks), dim3(kLdsRows), 0, st, ld.x, A,
                                            (int)B, out, out2, epi, div);
                     return MH_OK;
                 }
             }
             constexpr int kMaxLds = sizeof(typename R::T) == 4 ? 64 : 32;  // tile of at most 64 KB
-            if (B <= kMaxLds && A <= ((int64_t)1 << 40)) {  // any loader: LDS-staged, element order
-                const unsigned blocks = (unsigned)((A + kRThreads - 1) / kRThreads);
+            if (B <= kMaxLds && A < kMaxGridRows) {  // any loader: LDS-staged, element order
+                const unsigned blocks = (unsigned)((A + kLdsRows - 1) / kLdsRows);
                 if (B <= 16)
-                    hipLaunchKernelGGL((k_rows_lds_ld<R, LD, 16>), dim3(blocks), dim3(kRThreads), 0, st, ld, A,
+                    hipLaunchKernelGGL((k_rows_lds_ld<R, LD, 16>), dim3(blocks), dim3(kLdsRows), 0, st, ld, A,
                                        (int)B, out, out2, epi, div);
                 else if (B <= 32)
-                    hipLaunchKernelGGL((k_rows_lds_ld<R, LD, 32>), dim3(blocks), dim3(kRThreads), 0, st, ld, A,
+                    hipLaunchKernelGGL((k_rows_lds_ld<R, LD, 32>), dim3(blocks), dim3(kLdsRows), 0, st, ld, A,
                                        (int)B, out, out2, epi, div);
                 else if constexpr (kMaxLds == 64)
-                    hipLaunchKernelGGL((k_rows_lds_ld<R, LD, 64>), dim3(blocks), dim3(kRThreads), 0, st, ld, A,
+                    hipLaunchKernelGGL((k_rows_lds_ld<R, LD, 64>), dim3(blocks), dim3(kLdsRows), 0, st, ld, A,
                                        (int)B, out, out2, epi, div);
                 return MH_OK;
             }
@@ -1493,23 +1498,23 @@ int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* r
 // generic loader path (k_rows_lds_ld over LdBinRg), so the same bits, without a row lookup
 // per element. ug and the operand 16-byte aligned.
 template <int OP, int ID, bool DIVS, int BMAX>
-__global__ void __launch_bounds__(kRThreads)
+__global__ void __launch_bounds__(kLdsRows)
     k_rows_binrg(LdBinRg<OP, ID, DIVS, false> ld, float* __restrict__ grad, int64_t nrows, int B) {
-    __shared__ float4 us4[kRThreads * BMAX / 4], as4[kRThreads * BMAX / 4];
+    __shared__ float4 us4[kLdsRows * BMAX / 4], as4[kLdsRows * BMAX / 4];
     float* us = reinterpret_cast<float*>(us4);
     float* as = reinterpret_cast<float*>(as4);
     ld.setup();
     const int t = threadIdx.x;
-    const int64_t r0 = (int64_t)blockIdx.x * kRThreads;
-    const int64_t rows = (nrows - r0) < kRThreads ? (nrows - r0) : kRThreads;
+    const int64_t r0 = (int64_t)blockIdx.x * kLdsRows;
+    const int64_t rows = (nrows - r0) < kLdsRows ? (nrows - r0) : kLdsRows;
     const int64_t base = r0 * B;
     const int cnt = (int)(rows * B);
     const int nq = cnt >> 2;
-    for (int i = t; i < nq; i += kRThreads) {
+    for (int i = t; i < nq; i += kLdsRows) {
         us4[i] = ld_nt4(ld.ug + base, i);
         as4[i] = ld_nt4(ld.a + base, i);
     }
-    for (int i = (nq << 2) + t; i < cnt; i += kRThreads) {
+    for (int i = (nq << 2) + t; i < cnt; i += kLdsRows) {
         us[i] = ld_nt(ld.ug + base + i);
         as[i] = ld_nt(ld.a + base + i);
     }
@@ -1538,13 +1543,13 @@ static int binrg_reduce(float* grad, const float* ug, const float* a, const floa
     }
     ld.al = al;
     if constexpr (!BIG) {
-        if (C == 1 && B <= 32 && al && A <= ((int64_t)1 << 40)) {  // short rows, staged as quads
-            const unsigned blocks = (unsigned)((A + kRThreads - 1) / kRThreads);
+        if (C == 1 && B <= 32 && al && A < kMaxGridRows) {  // short rows, staged as quads
+            const unsigned blocks = (unsigned)((A + kLdsRows - 1) / kLdsRows);
             if (B <= 16)
-                hipLaunchKernelGGL((k_rows_binrg<OP, ID, DIVS, 16>), dim3(blocks), dim3(kRThreads), 0, ctx().stream,
+                hipLaunchKernelGGL((k_rows_binrg<OP, ID, DIVS, 16>), dim3(blocks), dim3(kLdsRows), 0, ctx().stream,
                                    ld, grad, A, (int)B);
             else
-                hipLaunchKernelGGL((k_rows_binrg<OP, ID, DIVS, 32>), dim3(blocks), dim3(kRThreads), 0, ctx().stream,
+                hipLaunchKernelGGL((k_rows_binrg<OP, ID, DIVS, 32>), dim3(blocks), dim3(kLdsRows), 0, ctx().stream,
                                    ld, grad, A, (int)B);
             return MH_OK;
         }
@@ -1776,15 +1781,15 @@ int mh_reduce_bwd_accum(int op, float* grad, const float* x, const mh_shape* psx
         } else {  // basics.mojo:489-506
             MH_TRY(map_scale_bcast(grad, sx, ug, sug, (float)(1.0 / (double)B), shape_eq(sx, sug)));
         }
-    } else if (C == 1 && B >= 1 && B <= 32 && A <= ((int64_t)1 << 40) && al16(x) && al16(grad)) {
+    } else if (C == 1 && B >= 1 && B <= 32 && A < kMaxGridRows && al16(x) && al16(grad)) {
         // MAX over short last-axis rows: one pass (max, count and routing per LDS tile)
-        const unsigned blocks = (unsigned)((A + kRThreads - 1) / kRThreads);
+        const unsigned blocks = (unsigned)((A + kLdsRows - 1) / kLdsRows);
         const FastDiv fdB = make_fastdiv((uint32_t)B);
         if (B <= 16)
-            hipLaunchKernelGGL(k_max_bwd_rows<16>, dim3(blocks), dim3(kRThreads), 0, ctx().stream, grad, x, ug, A,
+            hipLaunchKernelGGL(k_max_bwd_rows<16>, dim3(blocks), dim3(kLdsRows), 0, ctx().stream, grad, x, ug, A,
                                (int)B, fdB);
         else
-            hipLaunchKernelGGL(k_max_bwd_rows<32>, dim3(blocks), dim3(kRThreads), 0, ctx().stream, grad, x, ug, A,
+            hipLaunchKernelGGL(k_max_bwd_rows<32>, dim3(blocks), dim3(kLdsRows), 0, ctx().stream, grad, x, ug, A,
                                (int)B, fdB);
     } else if (C == 1 && B % 4 == 0 && B <= 16384 && al16(x) && al16(grad) && A < ((int64_t)1 << 31)) {
         // MAX over rows held in registers: one pass
