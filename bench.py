@@ -1040,8 +1040,8 @@ def pmc_summary(fetch_csv, write_csv, copy_bytes=8 << 28):
 
 
 # label of a config-2 op -> prefix of its kernel's name (the 2^28-element launch)
-C2_KERNEL = {"ADD.bwd": "void mh::k_bwd2_same4<0>", "SUB.bwd": "void mh::k_bwd2_same4<1>",
-             "MUL.bwd": "void mh::k_bwd2_same4<2>", "DIV.bwd": "void mh::k_bwd2_same4<3>",
+C2_KERNEL = {"ADD.bwd": "void mh::k_bwd2_same4<0, false>", "SUB.bwd": "void mh::k_bwd2_same4<1, false>",
+             "MUL.bwd": "void mh::k_bwd2_same4<2, false>", "DIV.bwd": "void mh::k_bwd2_same4<3, false>",
              "ADD.fwd": "void mh::k_same4<mh::FBin<0>,", "SUB.fwd": "void mh::k_same4<mh::FBin<1>,",
              "MUL.fwd": "void mh::k_same4<mh::FBin<2>,", "DIV.fwd": "void mh::k_same4<mh::FBin<3>,",
              "EXP.fwd": "void mh::k_same4<mh::FUn<4>,", "LOG.fwd": "void mh::k_same4<mh::FUn<5>,",
@@ -1050,7 +1050,7 @@ C2_KERNEL = {"ADD.bwd": "void mh::k_bwd2_same4<0>", "SUB.bwd": "void mh::k_bwd2_
              "LOG.bwd": "void mh::k_same4<mh::FUnBwd<5>,", "SIGMOID.bwd": "void mh::k_same4<mh::FUnBwd<13>,",
              "RELU.bwd": "void mh::k_same4<mh::FUnBwd<14>,", "TANH.bwd": "void mh::k_same4<mh::FUnBwd<15>,",
              "POW.fwd": "void mh::k_same4<mh::FPowi,", "POW.bwd_x": "void mh::k_same4<mh::FPowBwdX,",
-             "POW.bwd_exp": "void mh::k_rows_wave<mh::RSum, mh::LdPowGrad,"}
+             "POW.bwd_exp": "void mh::k_rows_block<mh::RSum, mh::LdPowGrad,"}
 
 
 # workload kernels for the traffic table: (op, kernel-name prefix, launch grid in threads,
@@ -1059,8 +1059,10 @@ _N3, _N4, _N5 = 6422528, 1 << 26, 10485760
 WL_KERNELS = [
     ("c3 bias_relu.fwd (fused)", "mh::k_bias_relu_fwd_planes", 1605632, 12 * _N3 + 128, ""),
     ("c3 ADD.fwd", "void mh::k_planebc4<mh::FBin<0>, 2, false>", 1605632, 8 * _N3 + 128, ""),
-    ("c3 bias_relu.bwd (fused)", "void mh::k_bias_relu_bwd_planes<false, true, true>", 131072, 16 * _N3 + 256,
-     "grad_x read and written, bias gradient in the same launch"),
+    ("c3 bias_relu.bwd (fused), stream", "void mh::k_bias_relu_bwd_flat<false, true, true>", 1605632, 16 * _N3,
+     "grad_x read and written; two bias partials per wave"),
+    ("c3 bias_relu.bwd (fused), combine", "mh::k_bias_partials_comb", 8192, 8 * (_N3 // 256) + 256,
+     "the wave partials (two per 64 quads) read, 32 bias values updated"),
     ("c3 ADD.bwd_bias", "void mh::k_unb_planes<false>", 131072, 4 * _N3 + 256, "one launch, arrival tickets"),
     ("c4 [8192,8192] axis 0 MAX.fwd", "void mh::k_cols<mh::RMax, mh::LdPlain<mh::RMax>, true>", 131072,
      4 * _N4, "first of two launches (split partials)"),
@@ -1090,7 +1092,8 @@ WL_KERNELS = [
 WL_STATS = [("c3", "op_by_op", "ADD.bwd_bias", "void mh::k_unb_planes<false>"),
             ("c3", "fused", "bias_relu.fwd", "mh::k_bias_relu_fwd_planes"),
             ("c3", "op_by_op", "ADD.fwd", "void mh::k_planebc4<mh::FBin<0>, 2, false>"),
-            ("c3", "fused", "bias_relu.bwd", "void mh::k_bias_relu_bwd_planes<false, true, true>"),
+            ("c3", "fused", "bias_relu.bwd", ("void mh::k_bias_relu_bwd_flat<false, true, true>",
+                                              "mh::k_bias_partials_comb")),
             ("c4", "ops", "8192x8192.ax1.MAX.bwd", "void mh::k_max_bwd_rowreg<4, 8>"),
             ("c5", "fused", "fused.fwd", "void mh::k_rowp_fwd<0, 10>"),
             ("c5", "fused", "fused.bwd", "void mh::k_rowp_bwd<0, 10>"),
@@ -1131,12 +1134,14 @@ def stats_summary(stats_csv, command, bench_json=None):
                          f"event timing.")
         wl = json.load(open(bench_json)).get("workloads", {})
         rows_cmp = []
-        for w, group, label, prefix in WL_STATS:
+        for w, group, label, prefixes in WL_STATS:  # an op of two launches sums their averages
             rec = wl.get(w, {}).get(group, {}).get(label)
-            match = [r for r in rows if r["Name"].startswith(prefix)]
-            if rec and len(match) == 1:
-                avg = float(match[0]["AverageNs"]) / 1e3
-                rows_cmp.append(f"| {w} {label} | `{prefix.replace('void ', '')}` | {avg:.2f} | {rec['ms'] * 1e3:.2f} | "
+            prefixes = prefixes if isinstance(prefixes, tuple) else (prefixes,)
+            matches = [[r for r in rows if r["Name"].startswith(pf)] for pf in prefixes]
+            if rec and all(len(m) == 1 for m in matches):
+                avg = sum(float(m[0]["AverageNs"]) for m in matches) / 1e3
+                names = " + ".join(f"`{pf.replace('void ', '')}`" for pf in prefixes)
+                rows_cmp.append(f"| {w} {label} | {names} | {avg:.2f} | {rec['ms'] * 1e3:.2f} | "
                                 f"{rec['ms_isolated'] * 1e3:.2f} |")
         if rows_cmp:
             lines += ["", "## Workload kernels: rocprofv3 against the bench's two timings", "",
@@ -1188,6 +1193,45 @@ def traffic_summary_md(commands):
         f.write("\n".join(lines) + "\n")
 
 
+VALU_KERNELS = [  # (label, kernel-name prefix, elements per dispatch)
+    ("c5 fused head forward [2^20, 10]", "void mh::k_rowp_fwd<0, 10>", _N5),
+    ("c5 fused head backward [2^20, 10]", "void mh::k_rowp_bwd<0, 10>", _N5),
+    ("c2 POW exponent gradient (2^28)", "void mh::k_rows_block<mh::RSum, mh::LdPowGrad, true>", 1 << 28),
+    ("c2 POW x gradient (2^28)", "void mh::k_same4<mh::FPowBwdX, 2, true>", 1 << 28),
+    ("c2 TANH backward (2^28)", "void mh::k_same4<mh::FUnBwd<15>, 2, true>", 1 << 28),
+    ("c2 MUL backward, both operands (2^28)", "void mh::k_bwd2_same4<2, false>", 1 << 28),
+    ("c2 ADD forward (2^28)", "void mh::k_same4<mh::FBin<0>, 2, false>", 1 << 28),
+]
+
+
+def valu_summary(csv_paths, command):
+    """Writes profiles/valu_per_element.md from rocprofv3 --pmc SQ_INSTS_VALU SQ_WAVES runs:
+    wave-level VALU instructions per element (SQ_INSTS_VALU * 64 / elements) of the kernels in
+    VALU_KERNELS (median over each kernel's dispatches of the named size)."""
+    vals = {}
+    for path in csv_paths:
+        for r in csv.DictReader(open(path, newline="")):
+            vals.setdefault((r["Kernel_Name"], r["Counter_Name"]), []).append(float(r["Counter_Value"]))
+    lines = ["# VALU instructions per element (rocprofv3 SQ_INSTS_VALU)", "",
+             "Commands (run from the repository root on one MI355X):", "", "```", *command, "```", "",
+             "SQ_INSTS_VALU counts wave-level vector ALU instructions, summed over the device; one covers 64 lanes, "
+             "so VALU per element = SQ_INSTS_VALU x 64 / elements. At 256 CUs issuing one wave-level VALU "
+             "instruction per cycle each at 2.4 GHz (614 G/s), the last column is the time that instruction count "
+             "alone would take.", "",
+             "| Kernel (workload) | Kernel | SQ_INSTS_VALU | SQ_WAVES | VALU / element | VALU time at 614 G/s (us) |",
+             "|---|---|---:|---:|---:|---:|"]
+    for label, prefix, n in VALU_KERNELS:
+        keys = [k for k in vals if k[0].startswith(prefix) and k[1] == "SQ_INSTS_VALU"]
+        if len(keys) != 1:
+            continue
+        v = statistics.median(vals[keys[0]])
+        w = statistics.median(vals.get((keys[0][0], "SQ_WAVES"), [0]))
+        lines.append(f"| {label} | `{prefix.replace('void ', '')}` | {v:.0f} | {w:.0f} | {v * 64 / n:.1f} | "
+                     f"{v / 614e9 * 1e6:.2f} |")
+    with open(os.path.join(os.path.dirname(TRAFFIC_JSON), "valu_per_element.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
 def traffic_for(label):
     if not os.path.exists(TRAFFIC_JSON):
         return None
@@ -1218,7 +1262,13 @@ def main():
                     help="write profiles/bench_kernel_stats.md from a rocprofv3 --stats run and exit")
     ap.add_argument("--command", default="", help="the rocprofv3 command(s) a summary records (';'-separated)")
     ap.add_argument("--bench-json", default=None, help="a bench JSON line of the same tree (for --stats-summary)")
+    ap.add_argument("--valu-summary", nargs="+", metavar="PMC_CSV",
+                    help="write profiles/valu_per_element.md from rocprofv3 --pmc SQ_INSTS_VALU SQ_WAVES runs and exit")
     args = ap.parse_args()
+    if args.valu_summary:
+        valu_summary(args.valu_summary, [c.strip() for c in args.command.split(";") if c.strip()] +
+                     [f"python bench.py --valu-summary {' '.join(args.valu_summary)}"])
+        return
     if args.pmc_summary:
         s = pmc_summary(*args.pmc_summary)
         traffic_summary_md([c.strip() for c in args.command.split(";") if c.strip()] +
