@@ -272,12 +272,15 @@ __global__ void __launch_bounds__(kThreads)
 // IN_BCAST operand a contiguous per-row vector ([rows, 1], as a row max or row sum is), the
 // output and FULL operands 16-byte aligned. One quad per thread: the quad's first row comes
 // from one fast division, and as K >= 4 at most one row boundary falls inside it, so a row
-// operand is read once, or twice where the quad crosses into the next row. kinds holds two
-// bits of InKind per operand. Element values are the same single operations as every engine.
+// operand contributes its values at rows r0 and r0 + 1. Both are loaded unconditionally (the
+// second from an index clamped to the last row, used only where the quad reaches that row),
+// so the two loads are in flight together: loading the second under a branch made every
+// quad wait for the first before issuing it. kinds holds two bits of InKind per operand.
+// Element values are the same single operations as every engine.
 template <class F, int NIN, bool ACCUM>
 __global__ void __launch_bounds__(kThreads)
-    k_rowbc4(float* __restrict__ out, InPtrs<NIN> in, int kinds, int64_t n, uint32_t K, FastDiv fk, DevScal ds,
-             F f) {
+    k_rowbc4(float* __restrict__ out, InPtrs<NIN> in, int kinds, int64_t n, uint32_t K, uint32_t last_row,
+             FastDiv fk, DevScal ds, F f) {
     constexpr int NA = NIN > 0 ? NIN : 1;
     f.setup(ds);
     float sv[NA];
@@ -290,6 +293,7 @@ __global__ void __launch_bounds__(kThreads)
         const uint32_t r0 = fdiv(e0, fk);
         const uint32_t c0 = e0 - r0 * K;
         const int jc = c0 + 3 >= K ? (int)(K - c0) : 4;  // first element of the quad in row r0 + 1
+        const uint32_t r1 = r0 < last_row ? r0 + 1 : last_row;
         float v[4][NA];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
@@ -303,7 +307,7 @@ __global__ void __launch_bounds__(kThreads)
                 for (int j = 0; j < 4; ++j) v[j][k] = t[j];
             } else {
                 const float a = in.p[k][r0];
-                const float b = jc < 4 ? in.p[k][r0 + 1] : a;
+                const float b = in.p[k][r1];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) v[j][k] = j < jc ? a : b;
             }
@@ -664,8 +668,9 @@ static int run_map(float* out, const ElwPlan& pl, const float* const* ptrs, cons
         }
         if (rowform) {
             const uint32_t K = (uint32_t)pl.dims[1];
-            hipLaunchKernelGGL((k_rowbc4<F, NIN, ACCUM>), g, b, 0, st, out, in, kinds, pl.n, K, make_fastdiv(K), ds,
-                               f);
+            const uint32_t last_row = (uint32_t)(pl.n / K) - 1;  // pl.n > 0: empty tensors return earlier
+            hipLaunchKernelGGL((k_rowbc4<F, NIN, ACCUM>), g, b, 0, st, out, in, kinds, pl.n, K, last_row,
+                               make_fastdiv(K), ds, f);
             return MH_OK;
         }
         // [rows, C] with per-column operands ([1, C]), C % 4 == 0

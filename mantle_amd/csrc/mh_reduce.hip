@@ -300,31 +300,57 @@ __global__ void __launch_bounds__(kLdsRows)
 
 // MAX backward over short rows in one pass (basics.mojo:581-615 for a last-axis reduce):
 // the row max m and count c from the LDS tile, then grad[i] = grad[i] + (x[i] == m ?
-// fl(1/c) * ug[row] : 0), x read once from HBM.
+// fl(1/c) * ug[row] : 0), x read once from HBM. Every load of the block (its x quads, its
+// grad quads, its rows' ug) is issued before the first barrier, so a block waits for memory
+// once; the grad quads wait in registers while the rows' maxima are found. Every grad quad
+// is stored, unlike the long-row kernels' sparse stores: with rows of at most 32 elements
+// every 128-byte line holds a row maximum, and 16-byte stores into most lines cost more than
+// writing the lines whole (config 5's rows of 10: 28.6 us sparse, 22.7 us dense).
 template <int BMAX>
 __global__ void __launch_bounds__(kLdsRows)
     k_max_bwd_rows(float* __restrict__ grad, const float* __restrict__ x, const float* __restrict__ ug,
                    int64_t nrows, int B, FastDiv fdB) {
+    constexpr int QPT = BMAX / 4;  // quads per thread: rows * B / 4 <= kLdsRows * BMAX / 4
     __shared__ float4 tile4[kLdsRows * BMAX / 4];
     __shared__ float sm[kLdsRows], sg[kLdsRows];
     float* tile = reinterpret_cast<float*>(tile4);
-    int64_t rows;
-    const int64_t base = stage_rows<BMAX>(tile, x, nrows, B, &rows);
-    __syncthreads();
     const int t = threadIdx.x;
+    const int64_t r0 = (int64_t)blockIdx.x * kLdsRows;
+    const int64_t rows = (nrows - r0) < kLdsRows ? (nrows - r0) : kLdsRows;
+    const int64_t base = r0 * B;
+    const int cnt = (int)(rows * B);
+    const int nq = cnt >> 2;
+    float* gb = grad + base;
+    float4 xq[QPT], gq[QPT];
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+        const int i = t + u * kLdsRows;
+        if (i < nq) {
+            xq[u] = ld_nt4(x + base, i);
+            gq[u] = ld_nt4(gb, i);
+        }
+    }
+    const float ugt = t < rows ? ug[r0 + t] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+        const int i = t + u * kLdsRows;
+        if (i < nq) tile4[i] = xq[u];
+    }
+    for (int i = (nq << 2) + t; i < cnt; i += kLdsRows) tile[i] = ld_nt(x + base + i);
+    __syncthreads();
     if (t < rows) {
         MC acc = RMaxCnt::init();
         for (int j = 0; j < B; ++j) acc = RMaxCnt::comb(acc, RMaxCnt::lift(tile[t * B + j]));
         const float f = 1.0f / (float)acc.c;  // basics.mojo:609
         sm[t] = acc.m;
-        sg[t] = f * ug[(int64_t)blockIdx.x * kLdsRows + t];
+        sg[t] = f * ugt;
     }
     __syncthreads();
-    const int cnt = (int)(rows * B);
-    const int nq = cnt >> 2;
-    float* gb = grad + base;
-    for (int i = t; i < nq; i += kLdsRows) {
-        const float4 o = ld_nt4(gb, i);
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+        const int i = t + u * kLdsRows;
+        if (i >= nq) break;
+        const float4 o = gq[u];
         float r[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -333,7 +359,7 @@ __global__ void __launch_bounds__(kLdsRows)
             r[j] = tile[e] == sm[row] ? sg[row] : 0.0f;
         }
         const float4 g = make_float4(o.x + r[0], o.y + r[1], o.z + r[2], o.w + r[3]);
-        if (bits_differ4(o.x, o.y, o.z, o.w, g.x, g.y, g.z, g.w)) st_nt4(gb, i, g);  // a sparse accumulation
+        st_nt4(gb, i, g);
     }
     for (int e = (nq << 2) + t; e < cnt; e += kLdsRows) {
         const int row = (int)fdiv((uint32_t)e, fdB);
