@@ -4,7 +4,8 @@ The headline line is config 2 of BASELINE.json. A step is one forward + backward
 every config-2 op over 2^28-element fp32 tensors already resident in HBM:
   ADD/SUB/MUL/DIV   fwd (a ~ U(-1,1), b ~ U(0.5,2)) and the backward of both operands,
   EXP (x ~ U(-10,10)), LOG (x ~ U(1e-3,10)), TANH/SIGMOID/RELU (x ~ N(0,3))  fwd and bwd,
-  POW (base ~ U(0.1,4), one seeded scalar exponent ~ U(0.5,3))  fwd, bwd of x, bwd of the exponent.
+  POW (base ~ U(0.1,4), one seeded scalar exponent ~ U(0.5,3))  fwd, and the backward of x and of
+      the exponent (one pass: both operands trainable, as the binary ops' backward).
 Throughput is algorithmic bytes per step / step time (each input read once, each output
 written once, each accumulated gradient read and written). Per-op times come from HIP events
 recorded on the library's stream around each call.
@@ -82,7 +83,9 @@ def step_plan():
         plan += [(f"{op}.fwd", 12), (f"{op}.bwd", BWD2_BYTES[op])]
     for op in UNARY:
         plan += [(f"{op}.fwd", 8), (f"{op}.bwd", 16)]
-    plan += [("POW.fwd", 8), ("POW.bwd_x", 16), ("POW.bwd_exp", 8)]
+    # POW backward of both operands in one pass: x and ug read, grad_x read and written (the
+    # exponent's gradient is a scalar)
+    plan += [("POW.fwd", 8), ("POW.bwd", 16)]
     return plan
 
 
@@ -319,8 +322,7 @@ def make_c2_calls(d, n):
         calls.append((f"{op}.fwd", lambda o=o, x=x: L.mh_unary_fwd(o, p["res"], x, n)))
         calls.append((f"{op}.bwd", lambda o=o, x=x: L.mh_unary_bwd_accum(o, p["gx"], x, p["ug"], n)))
     calls.append(("POW.fwd", lambda: L.mh_pow_fwd(p["res"], p["x_pow"], n, p["exp"])))
-    calls.append(("POW.bwd_x", lambda: L.mh_pow_bwd_accum(0, p["gx"], p["x_pow"], p["exp"], p["ug"], n)))
-    calls.append(("POW.bwd_exp", lambda: L.mh_pow_bwd_accum(1, p["gexp"], p["x_pow"], p["exp"], p["ug"], n)))
+    calls.append(("POW.bwd", lambda: L.mh_pow_bwd_accum2(p["gx"], p["gexp"], p["x_pow"], p["exp"], p["ug"], n)))
     return calls
 
 
@@ -1049,8 +1051,7 @@ C2_KERNEL = {"ADD.bwd": "void mh::k_bwd2_same4<0, false>", "SUB.bwd": "void mh::
              "TANH.fwd": "void mh::k_same4<mh::FUn<15>,", "EXP.bwd": "void mh::k_same4<mh::FUnBwd<4>,",
              "LOG.bwd": "void mh::k_same4<mh::FUnBwd<5>,", "SIGMOID.bwd": "void mh::k_same4<mh::FUnBwd<13>,",
              "RELU.bwd": "void mh::k_same4<mh::FUnBwd<14>,", "TANH.bwd": "void mh::k_same4<mh::FUnBwd<15>,",
-             "POW.fwd": "void mh::k_same4<mh::FPowi,", "POW.bwd_x": "void mh::k_same4<mh::FPowBwdX,",
-             "POW.bwd_exp": "void mh::k_rows_block<mh::RSum, mh::LdPowGrad,"}
+             "POW.fwd": "void mh::k_same4<mh::FPowi,", "POW.bwd": "void mh::k_rows_block<mh::RSum, mh::LdPowGrad,"}
 
 
 # workload kernels for the traffic table: (op, kernel-name prefix, launch grid in threads,
@@ -1196,8 +1197,8 @@ def traffic_summary_md(commands):
 VALU_KERNELS = [  # (label, kernel-name prefix, elements per dispatch)
     ("c5 fused head forward [2^20, 10]", "void mh::k_rowp_fwd<0, 10>", _N5),
     ("c5 fused head backward [2^20, 10]", "void mh::k_rowp_bwd<0, 10>", _N5),
-    ("c2 POW exponent gradient (2^28)", "void mh::k_rows_block<mh::RSum, mh::LdPowGrad, true>", 1 << 28),
-    ("c2 POW x gradient (2^28)", "void mh::k_same4<mh::FPowBwdX, 2, true>", 1 << 28),
+    ("c2 POW backward, x and exponent gradients (2^28)", "void mh::k_rows_block<mh::RSum, mh::LdPowGrad, true>",
+     1 << 28),
     ("c2 TANH backward (2^28)", "void mh::k_same4<mh::FUnBwd<15>, 2, true>", 1 << 28),
     ("c2 MUL backward, both operands (2^28)", "void mh::k_bwd2_same4<2, false>", 1 << 28),
     ("c2 ADD forward (2^28)", "void mh::k_same4<mh::FBin<0>, 2, false>", 1 << 28),

@@ -161,6 +161,14 @@ int mh_unary_bwd_accum(int op, float* grad, const float* x, const float* ug, int
 int mh_pow_bwd_accum(int tensor_id, float* grad, const float* x, const float* exponent,
                      const float* ug, int64_t n);
 
+/* The two POW backward_op calls Model.backward makes when both x and the exponent are
+ * trainable (model.mojo:233-270 with POW.backward, basics.mojo:329-378), in one pass that reads
+ * x and ug once: grad_x as tensor_id 0, grad_exp[0] as tensor_id 1. The results have the bits
+ * of mh_pow_bwd_accum(0, ...) then mh_pow_bwd_accum(1, ...). A null gradient skips its part;
+ * a grad_x that overlaps x, ug, the exponent or grad_exp runs as those two calls in order. */
+int mh_pow_bwd_accum2(float* grad_x, float* grad_exp, const float* x, const float* exponent,
+                      const float* ug, int64_t n);
+
 /* backward_op for SUM/MEAN/MAX (ops.mojo:355-405): SUM.backward (basics.mojo:408-425),
  * MEAN.backward (:454-506), MAX.backward (:536-615, ties split as fl(1/count) * ug),
  * then the same-shape accumulate_grad. ug has the reduced shape (axis >= 0) or (1). */

@@ -101,6 +101,7 @@ SIGNATURES = {
     "mh_binary_bwd_accum2": [_I, _VP, _VP, _VP, _VP, _VP, _S],
     "mh_unary_bwd_accum": [_I, _VP, _VP, _VP, _I64],
     "mh_pow_bwd_accum": [_I, _VP, _VP, _VP, _VP, _I64],
+    "mh_pow_bwd_accum2": [_VP, _VP, _VP, _VP, _VP, _I64],
     "mh_reduce_bwd_accum": [_I, _VP, _VP, _S, _VP, ctypes.c_int32],
     "mh_accumulate_grad": [_VP, _S, _VP, _S],
     "mh_bias_relu_fwd": [_VP, _VP, _VP, _S, _VP, _S],

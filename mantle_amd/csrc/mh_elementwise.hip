@@ -971,6 +971,26 @@ int mh_pow_bwd_accum(int tensor_id, float* grad, const float* x, const float* ex
     return finish("mh_pow_bwd_accum");
 }
 
+int mh_pow_bwd_accum2(float* grad_x, float* grad_exp, const float* x, const float* exponent, const float* ug,
+                      int64_t n) {
+    if (n < 0) return fail(MH_ERR_INVALID, "mh_pow_bwd_accum2: negative count");
+    if (n == 0) return MH_OK;
+    if (!x || !ug || !exponent) return fail(MH_ERR_NULL, "mh_pow_bwd_accum2: null tensor");
+    MH_TRY(require_init());
+    // grad_x written while x, ug, the exponent or grad_exp are read: the two calls in order
+    const auto overlaps = [&](const float* p, int64_t m) {
+        return grad_x && p && p < grad_x + n && grad_x < p + m;
+    };
+    if (!grad_x || !grad_exp || overlaps(x, n) || overlaps(ug, n) || overlaps(exponent, 1) ||
+        overlaps(grad_exp, 1)) {
+        if (grad_x) MH_TRY(mh_pow_bwd_accum(0, grad_x, x, exponent, ug, n));
+        if (grad_exp) MH_TRY(mh_pow_bwd_accum(1, grad_exp, x, exponent, ug, n));
+        return MH_OK;
+    }
+    MH_TRY(pow_exponent_grad(grad_exp, x, exponent, ug, n, grad_x));
+    return finish("mh_pow_bwd_accum2");
+}
+
 int mh_binary_bwd_accum(int op, int tensor_id, float* grad, const mh_shape* psgrad, const float* ug,
                         const mh_shape* psug, const float* t1, const mh_shape* ps1, const float* t2,
                         const mh_shape* ps2) {

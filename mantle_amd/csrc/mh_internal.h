@@ -249,9 +249,10 @@ enum Epi : int {
 size_t reduce_abc_tmp_floats(int op, int64_t A, int64_t B, int64_t C);
 int reduce_abc(int op, int epi, const float* x, int64_t A, int64_t B, int64_t C, float* out,
                float* out2, float div, float* tmp);
-// Sum over all n elements of the POW exponent-gradient term, accumulated into grad[0].
+// Sum over all n elements of the POW exponent-gradient term, accumulated into grad[0]; with
+// grad_x, the x gradient of every element is accumulated into grad_x in the same pass.
 int pow_exponent_grad(float* grad, const float* x, const float* exponent, const float* ug,
-                      int64_t n);
+                      int64_t n, float* grad_x = nullptr);
 // grad += un-broadcast(rg) (or += -un-broadcast(rg)): the chain of single-axis reductions.
 size_t unbroadcast_scratch_floats(const mh_shape& sgrad, const mh_shape& srg);
 int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* rg,

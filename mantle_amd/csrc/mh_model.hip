@@ -383,11 +383,8 @@ static int run_backward_node(mh_model* m, size_t i) {
         if (g2) MH_TRY(mh_binary_bwd_accum(nd.op, 1, g2, &s2, ug, &so, t1, &s1, t2, &s2));
         return MH_OK;
     }
-    if (nd.op == MH_POW) {
-        for (int j = 0; j < 2; ++j)
-            if (m->gr[in[j]]) MH_TRY(mh_pow_bwd_accum(j, m->gr[in[j]], t1, m->t[in[1]], ug, n1));
-        return MH_OK;
-    }
+    if (nd.op == MH_POW)  // both operand gradients in one pass where both are trainable
+        return mh_pow_bwd_accum2(m->gr[in[0]], m->gr[in[1]], t1, m->t[in[1]], ug, n1);
     if (nd.op == MH_FMA) {
         for (int j = 0; j < 3; ++j)
             if (m->gr[in[j]]) MH_TRY(mh_fma_bwd_accum(j, m->gr[in[j]], ug, t1, m->t[in[1]], n1));

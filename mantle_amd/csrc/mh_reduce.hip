@@ -91,22 +91,46 @@ struct LdPairs {  // split partials of RMaxCnt
 };
 
 // POW exponent gradient term (basics.mojo:359-376): powf(x, a) * (isinf(log x) ? 0 : log x) * ug.
+// With gx set, every element the reduction visits (each exactly once: the reduction adds
+// each term once) also takes the x gradient, gx[i] = gx[i] + (a * powf(x[i] + 1e-12, a - 1))
+// * ug[i] (basics.mojo:345-357, FPowBwdX's expression), from the same x and ug loads and,
+// where x + 1e-12 rounds to x, the same log: both POW operand gradients in one pass.
 struct LdPowGrad {
     const float* x;
     const float* ug;
     const float* ap;
     float a;
-    __device__ void setup() { a = ap[0]; }
-    __device__ float term(float xv, float u) const {
-        const float lx = mlog(xv);  // one log serves both the power and the log factor
+    float* gx;
+    float am1;
+    __device__ void setup() {
+        a = ap[0];
+        am1 = a - 1.0f;
+    }
+    __device__ float term(float xv, float u, float lx) const {
         const float lg = __builtin_isinf(lx) ? 0.0f : lx;
         return (mpowf_lg(xv, a, lx) * lg) * u;
     }
-    __device__ float get(int64_t i) const { return term(ld_nt(x + i), ld_nt(ug + i)); }
+    __device__ float xgrad(float xv, float u, float lx) const {
+        const float xe = xv + 1e-12f;
+        const float lxe = xe == xv ? lx : mlog(xe);  // equal values have equal bits here (xe != +-0)
+        return (a * mpowf_lg(xe, am1, lxe)) * u;
+    }
+    __device__ float get(int64_t i) const {
+        const float xv = ld_nt(x + i), u = ld_nt(ug + i);
+        const float g = gx ? ld_nt(gx + i) : 0.0f;
+        const float lx = mlog(xv);  // one log serves the power, the log factor and the x gradient
+        if (gx) st_nt(gx + i, g + xgrad(xv, u, lx));
+        return term(xv, u, lx);
+    }
     __device__ void get4(int64_t i, float* o) const {
-        float4 q = ld_nt4(x + i, 0);
-        float4 u = ld_nt4(ug + i, 0);
-        o[0] = term(q.x, u.x); o[1] = term(q.y, u.y); o[2] = term(q.z, u.z); o[3] = term(q.w, u.w);
+        const float4 q = ld_nt4(x + i, 0);
+        const float4 u = ld_nt4(ug + i, 0);
+        const float4 g = gx ? ld_nt4(gx + i, 0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float l0 = mlog(q.x), l1 = mlog(q.y), l2 = mlog(q.z), l3 = mlog(q.w);
+        if (gx)
+            st_nt4(gx + i, 0, make_float4(g.x + xgrad(q.x, u.x, l0), g.y + xgrad(q.y, u.y, l1),
+                                         g.z + xgrad(q.z, u.z, l2), g.w + xgrad(q.w, u.w, l3)));
+        o[0] = term(q.x, u.x, l0); o[1] = term(q.y, u.y, l1); o[2] = term(q.z, u.z, l2); o[3] = term(q.w, u.w, l3);
     }
 };
 
@@ -1627,12 +1651,14 @@ int unbroadcast_binrg(int op, int id, bool divs, float* grad, const mh_shape& sg
     return MH_OK;
 }
 
-int pow_exponent_grad(float* grad, const float* x, const float* exponent, const float* ug, int64_t n) {
-    LdPowGrad ld{x, ug, exponent, 0.0f};
+int pow_exponent_grad(float* grad, const float* x, const float* exponent, const float* ug, int64_t n,
+                      float* grad_x) {
+    LdPowGrad ld{x, ug, exponent, 0.0f, grad_x, 0.0f};
     const size_t t = tmp_floats_t<RSum>(1, n, 1, true);
     float* tmp = nullptr;
     MH_TRY(scratch((t + 64) * sizeof(float), reinterpret_cast<void**>(&tmp)));
-    return reduce_t<RSum, LdPowGrad>(ld, al16(x) && al16(ug), EPI_ACCUM, 1, n, 1, grad, nullptr, 0.0f, tmp);
+    const bool vec = al16(x) && al16(ug) && (!grad_x || al16(grad_x));
+    return reduce_t<RSum, LdPowGrad>(ld, vec, EPI_ACCUM, 1, n, 1, grad, nullptr, 0.0f, tmp);
 }
 
 // elementwise helpers (mh_elementwise.hip)

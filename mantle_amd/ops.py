@@ -380,7 +380,15 @@ def backward_op_both(op: int, ug: Tensor, t1: Tensor, t2: Tensor, grad1: Optiona
                      grad2: Optional[Tensor]) -> None:
     """Both backward_op calls of a same-shape binary op in one fused pass. grad1 and grad2 may be
     the same tensor (an op over one symbol twice, x * x): both gradients then accumulate into it,
-    operand 0's first, as the two calls of Model.backward do (model.mojo:233-270)."""
+    operand 0's first, as the two calls of Model.backward do (model.mojo:233-270). For POW, t2 is
+    the shape-(1) exponent: grad1 takes x's gradient and grad2 the exponent's, from one read of
+    t1 and ug, with the bits of the two calls."""
+    if op == OP.POW:
+        if t2.shape() != TensorShape(1) or ug.shape() != t1.shape():
+            raise _lib.MantleHipError(_lib.ERR_SHAPE, "POW exponent must be a shape-(1) graph scalar")
+        _lib.call("mh_pow_bwd_accum2", grad1.ptr if grad1 is not None else None,
+                  grad2.ptr if grad2 is not None else None, t1.ptr, t2.ptr, ug.ptr, t1.num_elements())
+        return
     if t1.shape() != t2.shape() or ug.shape() != t1.shape():
         if grad1 is not None:
             backward_op(0, op, ug, t1, t2, grad1)

@@ -247,6 +247,54 @@ def test_pow_parity(gpu, e):
     assert_sum_close(got, ref, np.array([terms.sum()]), f"pow bwd exponent {e}", terms_abs=np.array([np.abs(terms).sum()]))
 
 
+@pytest.mark.parametrize("n", [1, 3, 4, 63, 64, 65, 2047, 2048, 2052, 4099, (1 << 18) + 4, (1 << 20) + 3])
+def test_pow_bwd_both_operands_fused(gpu, n):
+    """mh_pow_bwd_accum2 (x's and the exponent's gradient in one pass) against the two
+    mh_pow_bwd_accum calls bit for bit: the x gradient element by element, the exponent gradient
+    through the same reduction kernels in the same order (every reduction shape the length
+    selects: LDS rows, one wavefront, block chunks with a combine). Bases include values where
+    x + 1e-12 is not x (0, 1e-13, a subnormal), a negative base, NaN and inf; exponents integral
+    and fractional; x, ug and the gradients also as unaligned views. The x gradient also matches
+    the oracle bit for bit and the exponent gradient the oracle's in the sum class."""
+    m = gpu.m
+    pw = OPS["POW"]
+    x = synth.uniform((n,), 0.1, 4, 610 + n % 97)
+    specials = np.array([0.0, 1e-13, 3e-6, 1e-40, -2.0, np.nan, np.inf, 1.0], np.float32)
+    ug = synth.normal((n,), 0, 1, 611)
+    g0 = synth.normal((n,), 0, 1, 612)
+    for e in (2.37, 3.0, -1.5, 0.5):
+        t2 = np.array([e], np.float32)
+        ge0 = np.array([0.25], np.float32)
+        for xs, label in ((x, "clean"), (np.concatenate([specials, x])[:n], "specials")):
+            for off in (0, 1):
+                def view(v, off=off):
+                    buf = gpu.T(np.concatenate([np.zeros(off, np.float32), v]))
+                    return m.Tensor(m.TensorShape(*v.shape), _ptr=buf.ptr + 4 * off, _owner=buf)
+                tx, tu, te = view(xs), view(ug), gpu.T(t2)
+                sx, se = view(g0), gpu.T(ge0)
+                m.backward_op(0, pw, tu, tx, te, sx)
+                m.backward_op(1, pw, tu, tx, te, se)
+                fx, fe = view(g0), gpu.T(ge0)
+                m.backward_op_both(pw, tu, tx, te, fx, fe)
+                what = f"n={n} e={e} {label} off={off}"
+                assert_bitexact(fx.to_numpy(), sx.to_numpy(), f"fused x grad {what}")
+                assert_bitexact(fe.to_numpy(), se.to_numpy(), f"fused exponent grad {what}")
+                if label == "clean" and off == 0:
+                    assert_ulp(fx.to_numpy(), ORC.backward(0, pw, ug, xs, t2, grad=g0), 2, f"x grad vs oracle {what}")
+                    ref = ORC.backward(1, pw, ug, xs, t2, grad=ge0)
+                    X, U = xs.astype(np.float64), ug.astype(np.float64)
+                    terms = X ** np.float64(e) * np.log(X) * U
+                    assert_sum_close(fe.to_numpy(), ref, np.array([0.25 + terms.sum()]), f"exponent grad {what}",
+                                     terms_abs=np.array([0.25 + np.abs(terms).sum()]))
+    # one null gradient: only the other part runs
+    tx, tu, te = gpu.T(x), gpu.T(ug), gpu.T(np.array([2.37], np.float32))
+    fx = gpu.T(g0)
+    m.backward_op_both(pw, tu, tx, te, fx, None)
+    sx = gpu.T(g0)
+    m.backward_op(0, pw, tu, tx, te, sx)
+    assert_bitexact(fx.to_numpy(), sx.to_numpy(), "x grad alone")
+
+
 # ---------------------------------------------------------------------------------------
 # reductions
 # ---------------------------------------------------------------------------------------
