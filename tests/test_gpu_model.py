@@ -214,6 +214,47 @@ def test_model_every_op(gpu, rows):
         assert_bitexact(slots[k].to_numpy(), v, f"grad {k} vs GPU op by op")
 
 
+@pytest.mark.parametrize("shape", [(37, 20), (4099, 7)])
+def test_model_pow_both_operands_trainable(gpu, shape):
+    """POW with a trainable exponent parameter: Model.backward's two POW backward_op calls
+    (model.mojo:233-270) run as one pass (mh_pow_bwd_accum2). x's gradient holds the oracle's
+    bits; the exponent's gradient is in the sum class against the oracle and bit-identical to
+    the GPU's own two separate calls. Two backward passes check that both slots accumulate."""
+    m = gpu.m
+    x = synth.uniform(shape, 0.1, 4, 1300 + shape[0])
+    e = np.array([2.37], np.float32)
+    g = m.Graph()
+    sx = g.input(shape, trainable=True)
+    se = g.param((1,), init=e)
+    p = g.op(m.OP.POW, sx, se)
+    loss = g.op(m.OP.MEAN, p)
+    g.loss(loss)
+    g.out(loss)
+    model = m.Model(g)
+    model.forward(x)
+    model.backward()
+    P = model.parameters
+    pv = ORC.forward(OPS["POW"], x, e)
+    gp = ORC.backward(0, OPS["MEAN"], np.ones(1, np.float32), pv)
+    ox = ORC.backward(0, OPS["POW"], gp, x, e)
+    oe = ORC.backward(1, OPS["POW"], gp, x, e)
+    assert_bitexact(P.grads[sx].to_numpy(), ox, "grad x vs oracle")
+    X = x.astype(np.float64)
+    terms = X ** np.float64(e[0]) * np.log(X) * gp.astype(np.float64)
+    got_e = P.grads[se].to_numpy()
+    assert_sum_close(got_e, oe, np.array([terms.sum()]), "grad exponent vs oracle",
+                     terms_abs=np.array([np.abs(terms).sum()]))
+    ge_sep = gpu.backward(1, OPS["POW"], gp, x, e)
+    assert_bitexact(got_e, ge_sep, "grad exponent vs the separate GPU call")
+    # a second pass clears nothing: the loss seed is set to 1.0 again, p's gradient becomes
+    # 2 gp, and both POW gradients add the terms of that upper gradient
+    model.backward()
+    gp2 = ORC.backward(0, OPS["MEAN"], np.ones(1, np.float32), pv, grad=gp)
+    assert_bitexact(P.grads[sx].to_numpy(), ORC.backward(0, OPS["POW"], gp2, x, e, grad=ox), "grad x, second pass")
+    assert_bitexact(P.grads[se].to_numpy(), gpu.backward(1, OPS["POW"], gp2, x, e, grad=got_e),
+                    "grad exponent, second pass")
+
+
 def test_model_grads_accumulate_until_zero_grad(gpu):
     m = gpu.m
     values = {"x": synth.normal((64, 48), 0, 1, 1230), "bias": synth.normal((1, 48), 0, 0.1, 1231)}
