@@ -127,6 +127,20 @@ __global__ void __launch_bounds__(kOThreads)
         adam_unit_k(p, g, m, v, n, u, um, s);
 }
 
+// The common case of k_adam (all four tensors 16-byte aligned, sh == 0): thread q takes quad q,
+// with no unit arithmetic; the last n % 4 elements go to the thread after the last quad.
+__global__ void __launch_bounds__(kOThreads)
+    k_adam_al(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m, float* __restrict__ v,
+              int64_t n, AdamScal s) {
+    const int64_t q = (int64_t)blockIdx.x * kOThreads + threadIdx.x;
+    const int64_t nq = n >> 2;
+    if (q < nq) {
+        adam_unit(p, g, m, v, 4 * q, 4, true, s);
+    } else if (q == nq && (n & 3) != 0) {
+        adam_unit(p, g, m, v, 4 * q, (int)(n & 3), false, s);
+    }
+}
+
 struct AdamTensor {
     float* p;
     const float* g;
@@ -194,8 +208,12 @@ int mh_adam_step(float* param, const float* grad, float* m, float* v, int64_t n,
     MH_TRY(require_init());
     const AdamScal s = adam_scalars(lr, beta1, beta2, eps, iter);
     const UnitMap um = unit_map(param, grad, m, v);
-    hipLaunchKernelGGL(k_adam, dim3(grid_units(adam_units(n, um.sh))), dim3(kOThreads), 0, ctx().stream, param, grad,
-                       m, v, n, um, s);
+    if (um.vec && um.sh == 0)
+        hipLaunchKernelGGL(k_adam_al, dim3(grid_units((n >> 2) + 1)), dim3(kOThreads), 0, ctx().stream, param, grad,
+                           m, v, n, s);
+    else
+        hipLaunchKernelGGL(k_adam, dim3(grid_units(adam_units(n, um.sh))), dim3(kOThreads), 0, ctx().stream, param,
+                           grad, m, v, n, um, s);
     return finish("mh_adam_step");
 }
 
