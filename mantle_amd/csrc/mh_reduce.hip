@@ -267,16 +267,28 @@ __global__ void __launch_bounds__(kRThreads)
 // 16-byte aligned run of floats -- in LDS with float4 loads, then thread t reduces row r0 + t
 // in element order (the order of the reference's scalar tail loop for rows shorter than
 // its SIMD width).
+// Every quad of the tile is loaded into registers before any is stored to LDS (unrolled over
+// the tile's at most BMAX / 4 quads per thread), so a block waits for memory once.
 template <int BMAX>
 __device__ __forceinline__ int64_t stage_rows(float* tile, const float* __restrict__ x, int64_t nrows, int B,
                                               int64_t* rows_out) {
+    constexpr int QPT = BMAX / 4;  // rows * B / 4 <= kLdsRows * QPT
+    const int t = threadIdx.x;
     const int64_t r0 = (int64_t)blockIdx.x * kLdsRows;
     const int64_t rows = (nrows - r0) < kLdsRows ? (nrows - r0) : kLdsRows;
     const int64_t base = r0 * B;
     const int cnt = (int)(rows * B);
     const int nq = cnt >> 2;
-    for (int i = threadIdx.x; i < nq; i += kLdsRows) reinterpret_cast<float4*>(tile)[i] = ld_nt4(x + base, i);
-    for (int i = (nq << 2) + threadIdx.x; i < cnt; i += kLdsRows) tile[i] = ld_nt(x + base + i);
+    float4 q[QPT];
+#pragma unroll
+    for (int k = 0; k < QPT; ++k)
+        if (t + k * kLdsRows < nq) q[k] = ld_nt4(x + base, t + k * kLdsRows);
+    const int tl = (nq << 2) + t;  // the cnt % 4 tail floats: threads 0..2
+    const float tv = tl < cnt ? ld_nt(x + base + tl) : 0.0f;
+#pragma unroll
+    for (int k = 0; k < QPT; ++k)
+        if (t + k * kLdsRows < nq) reinterpret_cast<float4*>(tile)[t + k * kLdsRows] = q[k];
+    if (tl < cnt) tile[tl] = tv;
     *rows_out = rows;
     return base;
 }
@@ -286,13 +298,14 @@ __global__ void __launch_bounds__(kLdsRows)
     k_rows_lds(const float* __restrict__ x, int64_t nrows, int B, float* out, float* out2, int epi, float div) {
     __shared__ float4 tile4[kLdsRows * BMAX / 4];
     float* tile = reinterpret_cast<float*>(tile4);
+    const int t = threadIdx.x;
+    const int64_t o = (int64_t)blockIdx.x * kLdsRows + t;
+    // the row's starting value (the gradient, for a sequential accumulation) is loaded with the tile
+    typename R::T acc = o < nrows ? row_start<R>(epi, out, o) : R::init();
     int64_t rows;
     stage_rows<BMAX>(tile, x, nrows, B, &rows);
     __syncthreads();
-    const int t = threadIdx.x;
     if (t < rows) {
-        const int64_t o = (int64_t)blockIdx.x * kLdsRows + t;
-        typename R::T acc = row_start<R>(epi, out, o);
         for (int j = 0; j < B; ++j) acc = R::comb(acc, row_val<R>(epi, R::lift(tile[t * B + j])));
         epi_store(out, out2, o, acc, epi, div);
     }
@@ -312,11 +325,19 @@ __global__ void __launch_bounds__(kLdsRows)
     const int64_t rows = (nrows - r0) < kLdsRows ? (nrows - r0) : kLdsRows;
     const int64_t base = r0 * B;
     const int cnt = (int)(rows * B);
-    for (int i = threadIdx.x; i < cnt; i += kLdsRows) tile[i] = ld.get(base + i);
-    __syncthreads();
     const int t = threadIdx.x;
+    // every value of the tile and the row's starting value are loaded before any LDS store
+    // (unrolled over at most BMAX values per thread), so a block waits for memory once
+    T acc = t < rows ? row_start<R>(epi, out, r0 + t) : R::init();
+    T v[BMAX];
+#pragma unroll
+    for (int k = 0; k < BMAX; ++k)
+        if (t + k * kLdsRows < cnt) v[k] = ld.get(base + t + k * kLdsRows);
+#pragma unroll
+    for (int k = 0; k < BMAX; ++k)
+        if (t + k * kLdsRows < cnt) tile[t + k * kLdsRows] = v[k];
+    __syncthreads();
     if (t < rows) {
-        T acc = row_start<R>(epi, out, r0 + t);
         for (int j = 0; j < B; ++j) acc = R::comb(acc, row_val<R>(epi, tile[t * B + j]));
         epi_store(out, out2, r0 + t, acc, epi, div);
     }
@@ -1564,6 +1585,7 @@ int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* r
 template <int OP, int ID, bool DIVS, int BMAX>
 __global__ void __launch_bounds__(kLdsRows)
     k_rows_binrg(LdBinRg<OP, ID, DIVS, false> ld, float* __restrict__ grad, int64_t nrows, int B) {
+    constexpr int QPT = BMAX / 4;  // quads per thread per operand: rows * B / 4 <= kLdsRows * QPT
     __shared__ float4 us4[kLdsRows * BMAX / 4], as4[kLdsRows * BMAX / 4];
     float* us = reinterpret_cast<float*>(us4);
     float* as = reinterpret_cast<float*>(as4);
@@ -1574,19 +1596,35 @@ __global__ void __launch_bounds__(kLdsRows)
     const int64_t base = r0 * B;
     const int cnt = (int)(rows * B);
     const int nq = cnt >> 2;
-    for (int i = t; i < nq; i += kLdsRows) {
-        us4[i] = ld_nt4(ld.ug + base, i);
-        as4[i] = ld_nt4(ld.a + base, i);
+    // every load of the block is issued before the barrier (the tile quads into registers,
+    // the row's divisor and gradient), so a block waits for memory once
+    const bool mine = t < rows;
+    const int64_t row = r0 + t;
+    const float d = (OP == MH_DIV && ID == 1 && !DIVS && mine) ? ld.t2[row] : 0.0f;
+    float acc = mine ? grad[row] : 0.0f;  // EPI_SEQ_ACCUM
+    float4 uq[QPT], aq[QPT];
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+        const int i = t + k * kLdsRows;
+        if (i < nq) {
+            uq[k] = ld_nt4(ld.ug + base, i);
+            aq[k] = ld_nt4(ld.a + base, i);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+        const int i = t + k * kLdsRows;
+        if (i < nq) {
+            us4[i] = uq[k];
+            as4[i] = aq[k];
+        }
     }
     for (int i = (nq << 2) + t; i < cnt; i += kLdsRows) {
         us[i] = ld_nt(ld.ug + base + i);
         as[i] = ld_nt(ld.a + base + i);
     }
     __syncthreads();
-    if (t < rows) {
-        const int64_t row = r0 + t;
-        const float d = (OP == MH_DIV && ID == 1 && !DIVS) ? ld.t2[row] : 0.0f;
-        float acc = grad[row];  // EPI_SEQ_ACCUM
+    if (mine) {
         for (int j = 0; j < B; ++j) acc = acc + ld.term(us[t * B + j], as[t * B + j], d);
         grad[row] = acc;
     }
