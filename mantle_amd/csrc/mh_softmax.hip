@@ -73,16 +73,35 @@ static inline int rows_per_block(int tiles, int64_t K) {
 }
 
 // Copies `cnt` floats from src + base into LDS (16-byte aligned source: float4), and back.
+// Loads go out four per thread before their LDS stores, so a thread waits for memory once per
+// four quads rather than once per quad.
 __device__ __forceinline__ void stage_tile(float* dst, const float* __restrict__ src, int64_t base, int cnt,
                                            bool al) {
     const int t = threadIdx.x;
     int done = 0;
     if (al) {
         const int nq = cnt >> 2;
-        for (int i = t; i < nq; i += kSThreads) reinterpret_cast<float4*>(dst)[i] = ld_nt4(src + base, i);
+        float4* d4 = reinterpret_cast<float4*>(dst);
+        int i = t;
+        for (; i + 3 * kSThreads < nq; i += 4 * kSThreads) {
+            float4 q[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) q[u] = ld_nt4(src + base, i + u * kSThreads);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) d4[i + u * kSThreads] = q[u];
+        }
+        for (; i < nq; i += kSThreads) d4[i] = ld_nt4(src + base, i);
         done = nq << 2;
     }
-    for (int i = done + t; i < cnt; i += kSThreads) dst[i] = ld_nt(src + base + i);
+    int i = done + t;
+    for (; i + 3 * kSThreads < cnt; i += 4 * kSThreads) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = ld_nt(src + base + i + u * kSThreads);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) dst[i + u * kSThreads] = v[u];
+    }
+    for (; i < cnt; i += kSThreads) dst[i] = ld_nt(src + base + i);
 }
 
 __device__ __forceinline__ void unstage_tile(float* __restrict__ dst, const float* src, int64_t base, int cnt,
