@@ -199,3 +199,51 @@ def test_graph_replay_survives_buffer_growth_and_refuses_after_shutdown():
     graphed.capture("forward")
     graphed.capture("backward")
     check(2)
+
+
+def test_async_mode_gives_the_same_bits():
+    """MH_INIT_ASYNC (no stream synchronisation at the end of each call, as bench.py runs):
+    op-by-op calls that grow scratch and take tickets, a native Model training step and the
+    fused rows give the bits of the synchronous mode. Every host boundary (copies to and from
+    the host, frees, scratch growth) synchronises by itself, so nothing else may be needed."""
+    eng = GpuEngine()
+    m = eng.m
+    x = synth.normal((8, 32, 28, 28), 0, 1, 1300)
+    b = synth.normal((1, 32, 1, 1), 0, 0.1, 1301)
+    u = synth.normal((8, 32, 28, 28), 0, 1, 1302)
+    logits = synth.normal((4099, 10), 0, 2, 1303)
+    onehot = np.zeros((4099, 10), np.float32)
+    onehot[np.arange(4099), synth.integers((4099,), 0, 10, 1304)] = 1.0
+    big = synth.normal((3, 700001), 0, 1, 1305)
+
+    def run():
+        tx, tb, tu, tbig = eng.T(x), eng.T(b), eng.T(u), eng.T(big)
+        gb = m.Tensor(tb.shape())
+        m.backward_op(1, m.OP.ADD, tu, tx, tb, gb)
+        s = m.Tensor(m.TensorShape(3))
+        m.forward_op(m.OP.SUM, s, tbig, attributes={"axis": 1})
+        loss = m.Tensor(m.TensorShape(1))
+        m.softmax_log_mul_mean_forward(loss, eng.T(logits), eng.T(onehot))
+        g = m.Graph()
+        sl = g.input((4099, 10), trainable=True)
+        st = g.input((4099, 10))
+        mx = g.op(m.OP.MAX, sl, attributes={"axis": 1})
+        e = g.op(m.OP.EXP, g.op(m.OP.SUB, sl, mx))
+        sm = g.op(m.OP.DIV, e, g.op(m.OP.SUM, e, attributes={"axis": 1}))
+        lo = g.op(m.OP.MEAN, g.op(m.OP.MUL, g.op(m.OP.LOG, sm), st))
+        g.loss(lo)
+        g.out(lo)
+        model = m.Model(g)
+        ml = model.forward(logits, onehot).to_numpy()
+        model.backward()
+        gl = model.parameters.grads[sl].to_numpy()
+        return [v.to_numpy() if hasattr(v, "to_numpy") else v for v in (gb, s, loss, ml, gl)]
+
+    sync_out = run()
+    try:
+        m.init(0, asynchronous=True)
+        async_out = run()
+    finally:
+        m.init(0, asynchronous=False)
+    for k, (a, c) in enumerate(zip(sync_out, async_out)):
+        assert (np.asarray(a).view(np.uint32) == np.asarray(c).view(np.uint32)).all(), k
