@@ -1207,6 +1207,37 @@ VALU_KERNELS = [  # (label, kernel-name prefix, elements per dispatch)
 ]
 
 
+def trace_summary(marker_csv, kernel_csv, command, out_md):
+    """Writes `out_md`: each roctx range of a MANTLE_HIP_TRACE=1 run (rocprofv3 --marker-trace
+    --kernel-trace) in call order with the kernels that ran inside it. A kernel belongs to the
+    innermost range whose host interval contains its execution (the library synchronises at the
+    end of each call unless initialised asynchronous, as the traced program here is not)."""
+    import csv
+    with open(marker_csv) as f:
+        ranges = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Function"]) for r in csv.DictReader(f)]
+    with open(kernel_csv) as f:
+        kernels = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]) for r in csv.DictReader(f)]
+    ranges.sort()
+    inside = {i: [] for i in range(len(ranges))}
+    for ks, ke, kn in kernels:
+        best = None
+        for i, (rs, re_, _) in enumerate(ranges):
+            if rs <= ks and ke <= re_ and (best is None or re_ - rs < ranges[best][1] - ranges[best][0]):
+                best = i
+        if best is not None:
+            inside[best].append((kn, (ke - ks) / 1e3))
+    lines = ["# roctx ranges of a traced run (MANTLE_HIP_TRACE=1)", "",
+             "Commands (run from the repository root on one MI355X):", "", "```", *command, "```", "",
+             "Each entry point that queues GPU work opens a range named after itself (and its op); the "
+             "kernels that ran inside it follow, with their durations in microseconds.", "",
+             "| # | Range | Host us | Kernels (us) |", "|---:|---|---:|---|"]
+    for i, (rs, re_, name) in enumerate(ranges):
+        ks = ", ".join(f"`{n.split('(')[0]}` {d:.1f}" for n, d in inside[i]) or "—"
+        lines.append(f"| {i + 1} | `{name}` | {(re_ - rs) / 1e3:.1f} | {ks} |")
+    with open(out_md, "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
 def valu_summary(csv_paths, command):
     """Writes profiles/valu_per_element.md from rocprofv3 --pmc SQ_INSTS_VALU SQ_WAVES runs:
     wave-level VALU instructions per element (SQ_INSTS_VALU * 64 / elements) of the kernels in
@@ -1265,9 +1296,18 @@ def main():
                     help="write profiles/bench_kernel_stats.md from a rocprofv3 --stats run and exit")
     ap.add_argument("--command", default="", help="the rocprofv3 command(s) a summary records (';'-separated)")
     ap.add_argument("--bench-json", default=None, help="a bench JSON line of the same tree (for --stats-summary)")
+    ap.add_argument("--trace-summary", nargs=2, metavar=("MARKER_CSV", "KERNEL_CSV"),
+                    help="write profiles/trace_ranges_smoke.md from a MANTLE_HIP_TRACE=1 rocprofv3 "
+                         "--marker-trace --kernel-trace run and exit")
     ap.add_argument("--valu-summary", nargs="+", metavar="PMC_CSV",
                     help="write profiles/valu_per_element.md from rocprofv3 --pmc SQ_INSTS_VALU SQ_WAVES runs and exit")
     args = ap.parse_args()
+    if args.trace_summary:
+        out = os.path.join(os.path.dirname(TRAFFIC_JSON), "trace_ranges_smoke.md")
+        trace_summary(args.trace_summary[0], args.trace_summary[1],
+                      [c.strip() for c in args.command.split(";") if c.strip()] +
+                      [f"python bench.py --trace-summary {args.trace_summary[0]} {args.trace_summary[1]}"], out)
+        return
     if args.valu_summary:
         valu_summary(args.valu_summary, [c.strip() for c in args.command.split(";") if c.strip()] +
                      [f"python bench.py --valu-summary {' '.join(args.valu_summary)}"])

@@ -67,6 +67,11 @@ enum mh_status {
 #define MH_INIT_ASYNC 1u /* do not synchronise at the end of each call */
 
 /* ---- context and memory (the device-resident side of Tensor / Collection) ---- */
+/* mh_init also reads two environment variables (again at every call):
+ *   MANTLE_HIP_TRACE=1   every entry point that queues GPU work opens a roctx range named after
+ *                        itself and its op (roctx found with dlopen; absent, tracing stays off);
+ *   MANTLE_HIP_FAIL_AT=k the k-th HIP runtime call after this mh_init fails with MH_ERR_HIP
+ *                        without being made (failure-path tests). */
 int mh_init(int device, uint64_t flags);
 int mh_shutdown(void);
 int mh_sync(void);

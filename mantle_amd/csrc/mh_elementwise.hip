@@ -861,6 +861,7 @@ extern "C" {
 
 int mh_binary_fwd(int op, float* res, const mh_shape* psres, const float* a, const mh_shape* psa,
                   const float* b, const mh_shape* psb) {
+    MH_TRACE_OP("mh_binary_fwd", op);
     MH_SHAPE_ARG(sres);
     MH_SHAPE_ARG(sa);
     MH_SHAPE_ARG(sb);
@@ -887,6 +888,7 @@ int mh_binary_fwd(int op, float* res, const mh_shape* psres, const float* a, con
 }
 
 int mh_unary_fwd(int op, float* res, const float* x, int64_t n) {
+    MH_TRACE_OP("mh_unary_fwd", op);
     MH_TRY(check_op_unary(op));
     if (n < 0) return fail(MH_ERR_INVALID, "mh_unary_fwd: negative count");
     if (n == 0) return MH_OK;
@@ -906,6 +908,7 @@ int mh_unary_fwd(int op, float* res, const float* x, int64_t n) {
 }
 
 int mh_pow_fwd(float* res, const float* x, int64_t n, const float* exponent) {
+    MH_TRACE("mh_pow_fwd");
     if (n < 0) return fail(MH_ERR_INVALID, "mh_pow_fwd: negative count");
     if (n == 0) return MH_OK;
     if (!res || !x || !exponent) return fail(MH_ERR_NULL, "mh_pow_fwd: null tensor");
@@ -919,6 +922,7 @@ int mh_pow_fwd(float* res, const float* x, int64_t n, const float* exponent) {
 }
 
 int mh_powi_fwd(float* res, const float* x, int32_t n_int, int64_t n) {
+    MH_TRACE("mh_powi_fwd");
     if (n < 0) return fail(MH_ERR_INVALID, "mh_powi_fwd: negative count");
     if (n == 0) return MH_OK;
     if (!res || !x) return fail(MH_ERR_NULL, "mh_powi_fwd: null tensor");
@@ -932,6 +936,7 @@ int mh_powi_fwd(float* res, const float* x, int32_t n_int, int64_t n) {
 }
 
 int mh_unary_bwd_accum(int op, float* grad, const float* x, const float* ug, int64_t n) {
+    MH_TRACE_OP("mh_unary_bwd_accum", op);
     MH_TRY(check_op_unary(op));
     if (n < 0) return fail(MH_ERR_INVALID, "mh_unary_bwd_accum: negative count");
     if (n == 0) return MH_OK;
@@ -953,6 +958,7 @@ int mh_unary_bwd_accum(int op, float* grad, const float* x, const float* ug, int
 
 int mh_pow_bwd_accum(int tensor_id, float* grad, const float* x, const float* exponent,
                      const float* ug, int64_t n) {
+    MH_TRACE("mh_pow_bwd_accum");
     if (tensor_id != 0 && tensor_id != 1) return fail(MH_ERR_INVALID, "mh_pow_bwd_accum: tensor_id %d", tensor_id);
     if (n < 0) return fail(MH_ERR_INVALID, "mh_pow_bwd_accum: negative count");
     if (n == 0) return MH_OK;
@@ -973,6 +979,7 @@ int mh_pow_bwd_accum(int tensor_id, float* grad, const float* x, const float* ex
 
 int mh_pow_bwd_accum2(float* grad_x, float* grad_exp, const float* x, const float* exponent, const float* ug,
                       int64_t n) {
+    MH_TRACE("mh_pow_bwd_accum2");
     if (n < 0) return fail(MH_ERR_INVALID, "mh_pow_bwd_accum2: negative count");
     if (n == 0) return MH_OK;
     if (!x || !ug || !exponent) return fail(MH_ERR_NULL, "mh_pow_bwd_accum2: null tensor");
@@ -994,6 +1001,7 @@ int mh_pow_bwd_accum2(float* grad_x, float* grad_exp, const float* x, const floa
 int mh_binary_bwd_accum(int op, int tensor_id, float* grad, const mh_shape* psgrad, const float* ug,
                         const mh_shape* psug, const float* t1, const mh_shape* ps1, const float* t2,
                         const mh_shape* ps2) {
+    MH_TRACE_OP("mh_binary_bwd_accum", op);
     MH_SHAPE_ARG(sgrad);
     MH_SHAPE_ARG(sug);
     MH_SHAPE_ARG(s1);
@@ -1043,6 +1051,7 @@ int mh_binary_bwd_accum(int op, int tensor_id, float* grad, const mh_shape* psgr
 
 int mh_binary_bwd_accum2(int op, float* grad1, float* grad2, const float* ug, const float* t1,
                          const float* t2, const mh_shape* ps) {
+    MH_TRACE_OP("mh_binary_bwd_accum2", op);
     MH_SHAPE_ARG(s);
     MH_TRY(check_op_binary(op));
     MH_TRY(check_shape(s, "shape"));
@@ -1085,6 +1094,7 @@ int mh_binary_bwd_accum2(int op, float* grad1, float* grad2, const float* ug, co
 }
 
 int mh_accumulate_grad(float* grad, const mh_shape* psgrad, const float* rg, const mh_shape* psrg) {
+    MH_TRACE("mh_accumulate_grad");
     MH_SHAPE_ARG(sgrad);
     MH_SHAPE_ARG(srg);
     MH_TRY(check_shape(sgrad, "grad"));
@@ -1136,6 +1146,7 @@ static int flat_map(const char* what, float* out, const float* const* ptrs, int6
 extern "C" {
 
 int mh_fma_fwd(float* res, const float* t1, const float* t2, const float* t3, int64_t n) {
+    MH_TRACE("mh_fma_fwd");
     MH_TRY(flat_check("mh_fma_fwd", n, res && t1 && t2 && t3));
     if (n == 0) return MH_OK;
     const float* p[3] = {t1, t2, t3};
@@ -1143,6 +1154,7 @@ int mh_fma_fwd(float* res, const float* t1, const float* t2, const float* t3, in
 }
 
 int mh_fma_bwd_accum(int tensor_id, float* grad, const float* ug, const float* t1, const float* t2, int64_t n) {
+    MH_TRACE("mh_fma_bwd_accum");
     if (tensor_id < 0 || tensor_id > 2) return fail(MH_ERR_INVALID, "mh_fma_bwd_accum: tensor_id %d", tensor_id);
     const float* other = tensor_id == 0 ? t2 : t1;
     MH_TRY(flat_check("mh_fma_bwd_accum", n, grad && ug && (tensor_id == 2 || other)));
@@ -1153,6 +1165,7 @@ int mh_fma_bwd_accum(int tensor_id, float* grad, const float* ug, const float* t
 }
 
 int mh_leakyrelu_fwd(float* res, const float* x, int64_t n, float negative_slope) {
+    MH_TRACE("mh_leakyrelu_fwd");
     MH_TRY(flat_check("mh_leakyrelu_fwd", n, res && x));
     if (n == 0) return MH_OK;
     const float* p[1] = {x};
@@ -1160,6 +1173,7 @@ int mh_leakyrelu_fwd(float* res, const float* x, int64_t n, float negative_slope
 }
 
 int mh_leakyrelu_bwd_accum(float* grad, const float* x, const float* ug, int64_t n, float negative_slope) {
+    MH_TRACE("mh_leakyrelu_bwd_accum");
     MH_TRY(flat_check("mh_leakyrelu_bwd_accum", n, grad && x && ug));
     if (n == 0) return MH_OK;
     const float* p[2] = {x, ug};
@@ -1167,6 +1181,7 @@ int mh_leakyrelu_bwd_accum(float* grad, const float* x, const float* ug, int64_t
 }
 
 int mh_clip_fwd(float* res, const float* x, int64_t n, float min_val, float max_val) {
+    MH_TRACE("mh_clip_fwd");
     MH_TRY(flat_check("mh_clip_fwd", n, res && x));
     if (n == 0) return MH_OK;
     const float* p[1] = {x};
@@ -1174,6 +1189,7 @@ int mh_clip_fwd(float* res, const float* x, int64_t n, float min_val, float max_
 }
 
 int mh_clip_bwd_accum(float* grad, const float* x, const float* ug, int64_t n, float min_val, float max_val) {
+    MH_TRACE("mh_clip_bwd_accum");
     MH_TRY(flat_check("mh_clip_bwd_accum", n, grad && x && ug));
     if (n == 0) return MH_OK;
     const float* p[2] = {x, ug};

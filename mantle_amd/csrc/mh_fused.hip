@@ -320,6 +320,7 @@ extern "C" {
 
 int mh_bias_relu_fwd(float* y, float* r, const float* x, const mh_shape* psx, const float* bias,
                      const mh_shape* psbias) {
+    MH_TRACE("mh_bias_relu_fwd");
     MH_SHAPE_ARG(sx);
     MH_SHAPE_ARG(sbias);
     MH_TRY(check_shape(sx, "x"));
@@ -364,6 +365,7 @@ int mh_bias_relu_fwd(float* y, float* r, const float* x, const mh_shape* psx, co
 
 int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const float* y, const float* ug,
                            const mh_shape* psx, const mh_shape* psbias) {
+    MH_TRACE("mh_bias_relu_bwd_accum");
     MH_SHAPE_ARG(sx);
     MH_SHAPE_ARG(sbias);
     MH_TRY(check_shape(sx, "x"));

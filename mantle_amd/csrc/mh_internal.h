@@ -67,6 +67,34 @@ int hip_inject(const char* what);
         if (rc__ != MH_OK) return rc__; \
     } while (0)
 
+// Opt-in tracing: with MANTLE_HIP_TRACE=1 in the environment at mh_init, every entry point that
+// queues GPU work opens a roctx range named after itself (and its op) for the duration of the
+// call, so a `rocprofv3 --marker-trace` run shows each call around the kernels it launched.
+// roctx is resolved with dlopen at mh_init; without the variable (or the library) the scopes
+// test one null pointer and do nothing.
+using RoctxPushFn = int (*)(const char*);
+using RoctxPopFn = int (*)();
+extern RoctxPushFn g_roctx_push;
+extern RoctxPopFn g_roctx_pop;
+void trace_init();
+void trace_push_op(const char* fn, int op);  // pushes "fn(OPNAME)"
+struct TraceScope {
+    bool on;
+    explicit TraceScope(const char* fn) : on(g_roctx_push != nullptr) {
+        if (on) g_roctx_push(fn);
+    }
+    TraceScope(const char* fn, int op) : on(g_roctx_push != nullptr) {
+        if (on) trace_push_op(fn, op);
+    }
+    ~TraceScope() {
+        if (on) g_roctx_pop();
+    }
+    TraceScope(const TraceScope&) = delete;
+    TraceScope& operator=(const TraceScope&) = delete;
+};
+#define MH_TRACE(fn) ::mh::TraceScope mh_trace_scope__(fn)
+#define MH_TRACE_OP(fn, op) ::mh::TraceScope mh_trace_scope__(fn, op)
+
 // Copies the shape argument `p<name>` (a const mh_shape* of the C ABI) into a local
 // `name`, rejecting a null pointer.
 #define MH_SHAPE_ARG(name)                                                                  \

@@ -641,6 +641,7 @@ int mh_model_destroy(mh_model* m) {
 }
 
 int mh_model_forward(mh_model* m, int32_t ninputs, const float* const* inputs, int where) {
+    MH_TRACE("mh_model_forward");
     if (!m) return fail(MH_ERR_NULL, "mh_model_forward: null model");
     MH_TRY(require_init());
     MH_TRY(write_inputs(m, ninputs, inputs, where));
@@ -648,6 +649,7 @@ int mh_model_forward(mh_model* m, int32_t ninputs, const float* const* inputs, i
 }
 
 int mh_model_inference(mh_model* m, int32_t ninputs, const float* const* inputs, int where) {
+    MH_TRACE("mh_model_inference");
     if (!m) return fail(MH_ERR_NULL, "mh_model_inference: null model");
     if (m->n_inference < 0) return fail(MH_ERR_INVALID, "mh_model_inference: the graph has no output");
     MH_TRY(require_init());
@@ -661,6 +663,7 @@ int mh_model_inference(mh_model* m, int32_t ninputs, const float* const* inputs,
 }
 
 int mh_model_backward(mh_model* m, int32_t nupper, const float* const* upper_grads, int where) {
+    MH_TRACE("mh_model_backward");
     if (!m) return fail(MH_ERR_NULL, "mh_model_backward: null model");
     MH_TRY(require_init());
     const mh_graph& g = m->g;
@@ -686,6 +689,7 @@ int mh_model_backward(mh_model* m, int32_t nupper, const float* const* upper_gra
 }
 
 int mh_model_capture(mh_model* m, int pass) {
+    MH_TRACE("mh_model_capture");
     if (!m) return fail(MH_ERR_NULL, "mh_model_capture: null model");
     MH_TRY(require_init());
     MH_TRY(check_pass(m, pass));
@@ -719,6 +723,7 @@ int mh_model_capture(mh_model* m, int pass) {
 }
 
 int mh_model_replay(mh_model* m, int pass) {
+    MH_TRACE("mh_model_replay");
     if (!m) return fail(MH_ERR_NULL, "mh_model_replay: null model");
     MH_TRY(require_init());
     if (pass != MH_PASS_FORWARD && pass != MH_PASS_BACKWARD && pass != MH_PASS_STEP)
@@ -747,6 +752,7 @@ int mh_model_grad(mh_model* m, int32_t sym, float** dptr) {
 }
 
 int mh_model_zero_grad(mh_model* m) {
+    MH_TRACE("mh_model_zero_grad");
     if (!m) return fail(MH_ERR_NULL, "mh_model_zero_grad: null model");
     if (!m->grad_arena) return MH_OK;
     return mh_zero(m->grad_arena, (int64_t)m->grad_floats);

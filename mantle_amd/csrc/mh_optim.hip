@@ -201,6 +201,7 @@ extern "C" {
 
 int mh_adam_step(float* param, const float* grad, float* m, float* v, int64_t n, float lr, float beta1,
                  float beta2, float eps, int64_t iter) {
+    MH_TRACE("mh_adam_step");
     MH_TRY(check_hyper("mh_adam_step", lr, beta1, beta2, eps, iter));
     if (n < 0) return fail(MH_ERR_INVALID, "mh_adam_step: negative count");
     if (n == 0) return MH_OK;
@@ -220,6 +221,7 @@ int mh_adam_step(float* param, const float* grad, float* m, float* v, int64_t n,
 int mh_adam_step_multi(int64_t ntensors, float* const* params, const float* const* grads, float* const* m,
                        float* const* v, const int64_t* sizes, float lr, float beta1, float beta2, float eps,
                        int64_t iter) {
+    MH_TRACE("mh_adam_step_multi");
     MH_TRY(check_hyper("mh_adam_step_multi", lr, beta1, beta2, eps, iter));
     if (ntensors < 0) return fail(MH_ERR_INVALID, "mh_adam_step_multi: negative tensor count");
     if (ntensors == 0) return MH_OK;

@@ -1748,6 +1748,7 @@ using namespace mh;
 extern "C" {
 
 int mh_reduce_fwd(int op, float* res, const float* x, const mh_shape* psx, int32_t axis) {
+    MH_TRACE_OP("mh_reduce_fwd", op);
     MH_SHAPE_ARG(sx);
     MH_TRY(check_reduce_args(op, sx, axis));
     int64_t A, B, C;
@@ -1766,6 +1767,7 @@ int mh_reduce_fwd(int op, float* res, const float* x, const mh_shape* psx, int32
 }
 
 int mh_reduce_fwd_noalloc(int op, float* res, const float* x, const mh_shape* psx, int32_t axis) {
+    MH_TRACE_OP("mh_reduce_fwd_noalloc", op);
     MH_SHAPE_ARG(sx);
     MH_TRY(check_reduce_args(op, sx, axis));
     int64_t A, B, C;
@@ -1789,6 +1791,7 @@ int mh_reduce_fwd_noalloc(int op, float* res, const float* x, const mh_shape* ps
 }
 
 int mh_tstd(float* res, const float* x, const mh_shape* psx, int32_t axis) {
+    MH_TRACE("mh_tstd");
     MH_SHAPE_ARG(sx);
     MH_TRY(check_shape(sx, "x"));
     if (axis < -1 || axis >= sx.rank) return fail(MH_ERR_INVALID, "mh_tstd: axis %d outside [-1, %d)", axis, sx.rank);
@@ -1868,6 +1871,7 @@ int mh_tstd(float* res, const float* x, const mh_shape* psx, int32_t axis) {
 
 int mh_reduce_bwd_accum(int op, float* grad, const float* x, const mh_shape* psx, const float* ug,
                         int32_t axis) {
+    MH_TRACE_OP("mh_reduce_bwd_accum", op);
     MH_SHAPE_ARG(sx);
     MH_TRY(check_reduce_args(op, sx, axis));
     const int64_t n = numel(sx);

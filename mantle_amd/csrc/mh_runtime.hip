@@ -1,4 +1,6 @@
 // mh_runtime.hip -- context, errors, memory, events, shape validation and launch planning.
+#include <dlfcn.h>
+
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -42,6 +44,53 @@ int fail(int code, const char* fmt, ...) {
     vsnprintf(g_err, sizeof g_err, fmt, ap);
     va_end(ap);
     return code;
+}
+
+RoctxPushFn g_roctx_push = nullptr;
+RoctxPopFn g_roctx_pop = nullptr;
+
+void trace_init() {
+    const char* s = getenv("MANTLE_HIP_TRACE");
+    if (!s || s[0] == '\0' || s[0] == '0') {
+        g_roctx_push = nullptr;
+        g_roctx_pop = nullptr;
+        return;
+    }
+    static void* h = nullptr;
+    if (!h) h = dlopen("librocprofiler-sdk-roctx.so.1", RTLD_NOW | RTLD_LOCAL);
+    if (!h) h = dlopen("libroctx64.so.4", RTLD_NOW | RTLD_LOCAL);
+    if (!h) return;  // no roctx: tracing stays off
+    auto push = reinterpret_cast<RoctxPushFn>(dlsym(h, "roctxRangePushA"));
+    auto pop = reinterpret_cast<RoctxPopFn>(dlsym(h, "roctxRangePop"));
+    if (push && pop) {
+        g_roctx_pop = pop;
+        g_roctx_push = push;
+    }
+}
+
+static const char* op_name(int op) {
+    switch (op) {
+        case MH_ADD: return "ADD";
+        case MH_SUB: return "SUB";
+        case MH_MUL: return "MUL";
+        case MH_DIV: return "DIV";
+        case MH_EXP: return "EXP";
+        case MH_LOG: return "LOG";
+        case MH_POW: return "POW";
+        case MH_SUM: return "SUM";
+        case MH_MEAN: return "MEAN";
+        case MH_MAX: return "MAX";
+        case MH_SIGMOID: return "SIGMOID";
+        case MH_RELU: return "RELU";
+        case MH_TANH: return "TANH";
+        default: return "?";
+    }
+}
+
+void trace_push_op(const char* fn, int op) {
+    thread_local char name[96];
+    snprintf(name, sizeof(name), "%s(%s)", fn, op_name(op));
+    g_roctx_push(name);
 }
 
 static void read_fail_env() {
@@ -430,6 +479,7 @@ int mh_device_count(int* count) {
 int mh_init(int device, uint64_t flags) {
     Context& c = ctx();
     read_fail_env();  // failure injection counts from here
+    trace_init();
     if (c.initialized) {
         if (c.device == device) {
             c.flags = flags;
@@ -508,6 +558,7 @@ int mh_free(void* dptr) {
 }
 
 int mh_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    MH_TRACE("mh_memcpy_h2d");
     if (bytes == 0) return MH_OK;
     if (!dst || !src) return fail(MH_ERR_NULL, "mh_memcpy_h2d: null pointer");
     MH_TRY(require_init());
@@ -517,6 +568,7 @@ int mh_memcpy_h2d(void* dst, const void* src, size_t bytes) {
 }
 
 int mh_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    MH_TRACE("mh_memcpy_d2h");
     if (bytes == 0) return MH_OK;
     if (!dst || !src) return fail(MH_ERR_NULL, "mh_memcpy_d2h: null pointer");
     MH_TRY(require_init());
@@ -526,6 +578,7 @@ int mh_memcpy_d2h(void* dst, const void* src, size_t bytes) {
 }
 
 int mh_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+    MH_TRACE("mh_memcpy_d2d");
     if (bytes == 0) return MH_OK;
     if (!dst || !src) return fail(MH_ERR_NULL, "mh_memcpy_d2d: null pointer");
     MH_TRY(require_init());
@@ -542,16 +595,19 @@ int mh_memcpy_d2d(void* dst, const void* src, size_t bytes) {
 }
 
 int mh_fill(float* t, float v, int64_t n) {
+    MH_TRACE("mh_fill");
     if (n < 0) return fail(MH_ERR_INVALID, "mh_fill: negative count");
     return launch_fill(t, v, n);
 }
 
 int mh_zero(float* t, int64_t n) {
+    MH_TRACE("mh_zero");
     if (n < 0) return fail(MH_ERR_INVALID, "mh_zero: negative count");
     return launch_fill(t, 0.0f, n);
 }
 
 int mh_rand_uniform(float* t, int64_t n, uint64_t seed, float lo, float hi) {
+    MH_TRACE("mh_rand_uniform");
     if (n < 0) return fail(MH_ERR_INVALID, "mh_rand_uniform: negative count");
     if (n == 0) return MH_OK;
     if (!t) return fail(MH_ERR_NULL, "mh_rand_uniform: null tensor");
@@ -561,6 +617,7 @@ int mh_rand_uniform(float* t, int64_t n, uint64_t seed, float lo, float hi) {
 }
 
 int mh_rand_normal(float* t, int64_t n, uint64_t seed, float mean, float std) {
+    MH_TRACE("mh_rand_normal");
     if (n < 0) return fail(MH_ERR_INVALID, "mh_rand_normal: negative count");
     if (n == 0) return MH_OK;
     if (!t) return fail(MH_ERR_NULL, "mh_rand_normal: null tensor");

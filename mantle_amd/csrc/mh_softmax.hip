@@ -1124,36 +1124,44 @@ using namespace mh;
 extern "C" {
 
 int mh_softmax_log_mul_mean_fwd(float* loss, const float* x, const float* target, int64_t rows, int64_t classes) {
+    MH_TRACE("mh_softmax_log_mul_mean_fwd");
     return loss_fwd<G_SMLM>("mh_softmax_log_mul_mean_fwd", loss, x, target, rows, classes);
 }
 
 int mh_softmax_log_mul_mean_bwd_accum(float* grad_x, const float* x, const float* target, const float* ug,
                                       int64_t rows, int64_t classes) {
+    MH_TRACE("mh_softmax_log_mul_mean_bwd_accum");
     return loss_bwd<G_SMLM>("mh_softmax_log_mul_mean_bwd_accum", grad_x, x, target, ug, rows, classes);
 }
 
 int mh_cross_entropy_fwd(float* loss, const float* x, const float* target, int64_t rows, int64_t classes) {
+    MH_TRACE("mh_cross_entropy_fwd");
     return loss_fwd<G_CE>("mh_cross_entropy_fwd", loss, x, target, rows, classes);
 }
 
 int mh_cross_entropy_bwd_accum(float* grad_x, const float* x, const float* target, const float* ug, int64_t rows,
                                int64_t classes) {
+    MH_TRACE("mh_cross_entropy_bwd_accum");
     return loss_bwd<G_CE>("mh_cross_entropy_bwd_accum", grad_x, x, target, ug, rows, classes);
 }
 
 int mh_softmax_fwd(float* out, const float* x, int64_t rows, int64_t classes) {
+    MH_TRACE("mh_softmax_fwd");
     return map_fwd<G_SOFTMAX>("mh_softmax_fwd", out, x, rows, classes);
 }
 
 int mh_softmax_bwd_accum(float* grad_x, const float* x, const float* grad_out, int64_t rows, int64_t classes) {
+    MH_TRACE("mh_softmax_bwd_accum");
     return map_bwd<G_SOFTMAX>("mh_softmax_bwd_accum", grad_x, x, grad_out, rows, classes);
 }
 
 int mh_logsoftmax_fwd(float* out, const float* x, int64_t rows, int64_t classes) {
+    MH_TRACE("mh_logsoftmax_fwd");
     return map_fwd<G_LOGSOFTMAX>("mh_logsoftmax_fwd", out, x, rows, classes);
 }
 
 int mh_logsoftmax_bwd_accum(float* grad_x, const float* x, const float* grad_out, int64_t rows, int64_t classes) {
+    MH_TRACE("mh_logsoftmax_bwd_accum");
     return map_bwd<G_LOGSOFTMAX>("mh_logsoftmax_bwd_accum", grad_x, x, grad_out, rows, classes);
 }
 

@@ -247,3 +247,39 @@ def test_async_mode_gives_the_same_bits():
         m.init(0, asynchronous=False)
     for k, (a, c) in enumerate(zip(sync_out, async_out)):
         assert (np.asarray(a).view(np.uint32) == np.asarray(c).view(np.uint32)).all(), k
+
+
+def test_trace_ranges_leave_results_unchanged():
+    """MANTLE_HIP_TRACE=1 at mh_init opens a roctx range around every entry point that queues
+    GPU work (nested for the executor's nodes). Without a profiler attached the ranges cost a
+    call each; the results keep their bits, and turning the variable off again (at the next
+    mh_init) closes nothing that was not opened."""
+    import os
+    eng = GpuEngine()
+    m = eng.m
+    a = synth.normal((1000, 37), 0, 1, 1400)
+    b = synth.uniform((1000, 1), 0.5, 2, 1401)
+    u = synth.normal((1000, 37), 0, 1, 1402)
+
+    def run():
+        ta, tb, tu = eng.T(a), eng.T(b), eng.T(u)
+        r = m.Tensor(ta.shape())
+        m.forward_op(m.OP.DIV, r, ta, tb)
+        gb = m.Tensor(tb.shape())
+        m.backward_op(1, m.OP.DIV, tu, ta, tb, gb)
+        s = m.Tensor(m.TensorShape(1000, 1))
+        m.forward_op(m.OP.MAX, s, ta, attributes={"axis": 1})
+        return [t.to_numpy() for t in (r, gb, s)]
+
+    plain = run()
+    try:
+        os.environ["MANTLE_HIP_TRACE"] = "1"
+        m.init(0)
+        traced = run()
+    finally:
+        os.environ.pop("MANTLE_HIP_TRACE", None)
+        m.init(0)
+    again = run()
+    for x, y, z in zip(plain, traced, again):
+        assert (x.view(np.uint32) == y.view(np.uint32)).all()
+        assert (x.view(np.uint32) == z.view(np.uint32)).all()
