@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from mantle_amd import synth
-from util import GpuEngine
+from util import TEST_ASYNC, GpuEngine
 
 pytestmark = pytest.mark.gpu
 
@@ -40,7 +40,7 @@ def test_shutdown_then_init_again():
     m._lib.call("mh_shutdown")
     with pytest.raises(m.MantleHipError):
         m._lib.call("mh_sync")
-    m.init(0)
+    m.init(0, asynchronous=TEST_ASYNC)
     second = run()
     for a, b in zip(first, second):
         assert (np.asarray(a).view(np.uint32) == np.asarray(b).view(np.uint32)).all()
@@ -137,7 +137,7 @@ def test_injected_hip_failures_return_cleanly():
         assert name is None
     finally:
         os.environ.pop("MANTLE_HIP_FAIL_AT", None)
-        m.init(0)
+        m.init(0, asynchronous=TEST_ASYNC)
     assert (again.view(np.uint32) == clean.view(np.uint32)).all()
     # the injection reached the init, the allocations, the growth of scratch and counters and
     # the end-of-call checks
@@ -193,7 +193,7 @@ def test_graph_replay_survives_buffer_growth_and_refuses_after_shutdown():
     grow()
     check(1)
     m._lib.call("mh_shutdown")
-    m.init(0)
+    m.init(0, asynchronous=TEST_ASYNC)
     with pytest.raises(m.MantleHipError):
         graphed.replay("forward")
     graphed.capture("forward")
@@ -244,7 +244,7 @@ def test_async_mode_gives_the_same_bits():
         m.init(0, asynchronous=True)
         async_out = run()
     finally:
-        m.init(0, asynchronous=False)
+        m.init(0, asynchronous=TEST_ASYNC)
     for k, (a, c) in enumerate(zip(sync_out, async_out)):
         assert (np.asarray(a).view(np.uint32) == np.asarray(c).view(np.uint32)).all(), k
 
@@ -274,11 +274,11 @@ def test_trace_ranges_leave_results_unchanged():
     plain = run()
     try:
         os.environ["MANTLE_HIP_TRACE"] = "1"
-        m.init(0)
+        m.init(0, asynchronous=TEST_ASYNC)
         traced = run()
     finally:
         os.environ.pop("MANTLE_HIP_TRACE", None)
-        m.init(0)
+        m.init(0, asynchronous=TEST_ASYNC)
     again = run()
     for x, y, z in zip(plain, traced, again):
         assert (x.view(np.uint32) == y.view(np.uint32)).all()

@@ -149,6 +149,12 @@ class OracleEngine:
         return O.tstd(t1, axis)
 
 
+# MANTLE_TEST_ASYNC=1 runs the GPU tests with the library in MH_INIT_ASYNC mode (no stream
+# synchronisation at the end of each call, as bench.py runs it): every host boundary must
+# synchronise by itself for the results to hold.
+TEST_ASYNC = os.environ.get("MANTLE_TEST_ASYNC") == "1"
+
+
 class GpuEngine:
     """Runs each op through mantle_amd (libmantle_hip.so) with host round trips (tests only)."""
     name = "gpu"
@@ -156,7 +162,7 @@ class GpuEngine:
     def __init__(self):
         import mantle_amd
         self.m = mantle_amd
-        mantle_amd.init(0)
+        mantle_amd.init(0, asynchronous=TEST_ASYNC)
 
     def T(self, a):
         return self.m.Tensor.from_numpy(np.asarray(a, dtype=np.float32))
