@@ -21,7 +21,8 @@
 // backward_op calls starting from zeroed intermediate gradients, for finite inputs. The row
 // reductions' orders:
 //   classes <= 64    element order from +0 (k_rows_lds / k_rows_thread): one thread per row,
-//                    the row in registers, LDS staging of coalesced loads;
+//                    the row in registers, LDS staging of coalesced loads; or (17-64
+//                    classes) P lanes per row carrying each running value across in order;
 //   64 < classes < 2048
 //                    k_rows_wave's order (per lane, quads lane + 64 q accumulated in groups
 //                    of four, the tail into the first group, the sixteen partials summed in
@@ -890,6 +891,255 @@ __global__ void __launch_bounds__(kSThreads)
 }
 
 // ---------------------------------------------------------------------------------------
+// multi-lane engine: rows of 17-64 classes, P = ceil(classes / 16) lanes per row
+// ---------------------------------------------------------------------------------------
+// Lane c of a row's P lanes holds elements [16 c, min(16 c + 16, classes)) in registers, loaded
+// straight from HBM (no LDS tiles, whose size per row held the thread engine to a few waves
+// per CU). Every order-dependent row quantity (the max, the max with its count, every row sum)
+// is carried across the P lanes in element order: lane c starts from the value lane c - 1
+// ended with, so each row sees the same sequence of operations as one thread walking the row
+// (the thread engine's and the library's row reductions' order), and results keep their bits.
+// A wavefront holds 64 / P rows (lanes past 64 / P * P idle), a 256-thread block four times
+// that; a loss graph's all-element sum adds per lane, then per block (the rtol class).
+constexpr int kMNE = 16;  // elements per lane
+
+template <int P>
+struct RowLanes {
+    static constexpr int R = 64 / P;  // rows per wavefront
+    int lane, r, c, cnt;              // lane in the wavefront, row in the wavefront, chunk, elements
+    bool live;                        // this lane holds a chunk of a row that exists
+};
+
+// Shuffles of the values a row chain carries (the running max, max with count, or sum).
+__device__ __forceinline__ float row_chain_shfl(float v, int src) { return __shfl(v, src & 63); }
+struct MaxCount {
+    float m;
+    uint32_t c;
+};
+__device__ __forceinline__ MaxCount row_chain_shfl(MaxCount v, int src) {
+    return MaxCount{__shfl(v.m, src & 63), (uint32_t)__shfl((int)v.c, src & 63)};
+}
+
+// The row's lanes in chunk order run `fold` (which walks the lane's elements in order from the
+// value it is given): lane c starts from lane c - 1's result (init for c == 0). Every lane of
+// the row returns the row's final value (that of its last lane). All lanes of the wavefront
+// take part (the shuffles); `fold` runs only on the lane whose turn it is.
+template <int P, class T, class F>
+__device__ __forceinline__ T row_chain(const RowLanes<P>& L, T init, F fold) {
+    T v = init;
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const T in = row_chain_shfl(v, L.lane - 1);
+        if (L.c == k && L.live) v = fold(k == 0 ? init : in);
+    }
+    return row_chain_shfl(v, L.lane - L.c + (P - 1));
+}
+
+// A lane's chunk straight from HBM with plain (cacheable) loads: a lane's quads are 64 bytes
+// apart from its neighbours', so each load instruction touches pieces of many lines, and the
+// next instructions find those lines in the caches (non-temporal loads fetched them again:
+// the 40-class Softmax forward took 70 us instead of 35). Staging the wavefront's contiguous
+// rows through LDS with coalesced loads was no faster forward and slower backward (its three
+// tiles held the grid to three blocks per CU).
+template <bool VEC>
+__device__ __forceinline__ void load_chunk(float (&v)[kMNE], const float* __restrict__ p, int cnt) {
+    if constexpr (VEC) {  // cnt is a multiple of 4, p 16-byte aligned
+#pragma unroll
+        for (int q = 0; q < kMNE / 4; ++q) {
+            if (4 * q < cnt) {
+                const vf4 t = reinterpret_cast<const vf4*>(p)[q];
+                v[4 * q] = t[0]; v[4 * q + 1] = t[1]; v[4 * q + 2] = t[2]; v[4 * q + 3] = t[3];
+            } else {
+                v[4 * q] = v[4 * q + 1] = v[4 * q + 2] = v[4 * q + 3] = 0.0f;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kMNE; ++j) v[j] = j < cnt ? p[j] : 0.0f;
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void store_chunk(float* __restrict__ p, const float (&v)[kMNE], int cnt) {
+    if constexpr (VEC) {
+#pragma unroll
+        for (int q = 0; q < kMNE / 4; ++q)
+            if (4 * q < cnt) reinterpret_cast<vf4*>(p)[q] = vf4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+    } else {
+#pragma unroll
+        for (int j = 0; j < kMNE; ++j)
+            if (j < cnt) p[j] = v[j];
+    }
+}
+
+template <int P>
+__device__ __forceinline__ RowLanes<P> row_lanes(int64_t rows, int K, int64_t* row_out) {
+    RowLanes<P> L;
+    L.lane = threadIdx.x & 63;
+    L.r = L.lane / P;
+    L.c = L.lane - L.r * P;
+    const int64_t row = ((int64_t)blockIdx.x * (kSThreads / 64) + (threadIdx.x >> 6)) * RowLanes<P>::R + L.r;
+    const int rem = K - kMNE * L.c;
+    L.cnt = rem < 0 ? 0 : (rem < kMNE ? rem : kMNE);
+    L.live = L.r < RowLanes<P>::R && row < rows;
+    *row_out = row;
+    return L;
+}
+
+template <int V, int P, bool VEC>
+__global__ void __launch_bounds__(kSThreads)
+    k_rowm_fwd(const float* __restrict__ x, const float* __restrict__ tg, float* __restrict__ out, int64_t rows,
+               int K, float* __restrict__ part) {
+    __shared__ float ws[4];
+    constexpr bool LOSS = V == G_SMLM || V == G_CE;
+    int64_t row;
+    const RowLanes<P> L = row_lanes<P>(rows, K, &row);
+    const int64_t off = row * (int64_t)K + kMNE * L.c;
+    float xv[kMNE], tv[kMNE], e[kMNE];
+    const int cnt = L.live ? L.cnt : 0;
+    load_chunk<VEC>(xv, x + (L.live ? off : 0), cnt);
+    if constexpr (LOSS) load_chunk<VEC>(tv, tg + (L.live ? off : 0), cnt);
+    // MAX.forward: max_simd from min_finite, element order
+    const float m = row_chain<P>(L, -FLT_MAX, [&](float a) {
+#pragma unroll
+        for (int j = 0; j < kMNE; ++j)
+            if (j < cnt) a = max_simd(a, xv[j]);
+        return a;
+    });
+#pragma unroll
+    for (int j = 0; j < kMNE; ++j) e[j] = j < cnt ? mexp(xv[j] - m) : 0.0f;  // SUB, EXP
+    const float s = row_chain<P>(L, 0.0f, [&](float a) {  // SUM.forward
+#pragma unroll
+        for (int j = 0; j < kMNE; ++j)
+            if (j < cnt) a = a + e[j];
+        return a;
+    });
+    const float ls = (V == G_CE || V == G_LOGSOFTMAX) ? mlog(s) : 0.0f;  // LOG.forward of the sum
+    if constexpr (LOSS) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kMNE; ++j) {
+            if (j < cnt) {
+                if constexpr (V == G_SMLM) {
+                    if (!smlm_skip(tv[j], e[j])) acc = acc + mlog(e[j] / s) * tv[j];  // DIV, LOG, MUL
+                } else {
+                    acc = acc + tv[j] * ((xv[j] - m) - ls);  // SUB(xm, ls), MUL(target, .)
+                }
+            }
+        }
+        const float tot = block_sum(acc, ws);
+        if (threadIdx.x == 0) part[blockIdx.x] = tot;
+    } else {
+#pragma unroll
+        for (int j = 0; j < kMNE; ++j) xv[j] = V == G_SOFTMAX ? e[j] / s : (xv[j] - m) - ls;  // DIV / SUB
+        if (L.live) store_chunk<VEC>(out + off, xv, cnt);
+    }
+}
+
+template <int V, int P, bool VEC>
+__global__ void __launch_bounds__(kSThreads)
+    k_rowm_bwd(float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ up,
+               const float* __restrict__ ug, int64_t rows, int K, float c) {
+    int64_t row;
+    const RowLanes<P> L = row_lanes<P>(rows, K, &row);
+    const int64_t off = row * (int64_t)K + kMNE * L.c;
+    const int cnt = L.live ? L.cnt : 0;
+    float xv[kMNE], uv[kMNE], gv[kMNE], e[kMNE];
+    load_chunk<VEC>(xv, x + (L.live ? off : 0), cnt);
+    load_chunk<VEC>(uv, up + (L.live ? off : 0), cnt);
+    load_chunk<VEC>(gv, g + (L.live ? off : 0), cnt);
+    // the forward row max (MAX.forward) and, as MAX.backward recomputes it, the max with its
+    // count (an element neither above nor below the running max adds to the count)
+    const float m = row_chain<P>(L, -FLT_MAX, [&](float a) {
+#pragma unroll
+        for (int j = 0; j < kMNE; ++j)
+            if (j < cnt) a = max_simd(a, xv[j]);
+        return a;
+    });
+    const MaxCount mc = row_chain<P>(L, MaxCount{-FLT_MAX, 0u}, [&](MaxCount a) {
+#pragma unroll
+        for (int j = 0; j < kMNE; ++j) {
+            if (j < cnt) {
+                const float v = xv[j];
+                if (a.m > v) {
+                } else if (v > a.m) {
+                    a.m = v;
+                    a.c = 1;
+                } else {
+                    a.c += 1;
+                }
+            }
+        }
+        return a;
+    });
+#pragma unroll
+    for (int j = 0; j < kMNE; ++j) e[j] = j < cnt ? mexp(xv[j] - m) : 0.0f;
+    const float s = row_chain<P>(L, 0.0f, [&](float a) {
+#pragma unroll
+        for (int j = 0; j < kMNE; ++j)
+            if (j < cnt) a = a + e[j];
+        return a;
+    });
+    const float gconst = V == G_SMLM ? 0.0f + c * ug[0]                       // MEAN backward
+                         : V == G_CE ? 0.0f + 1.0f * (0.0f + ug[0] * c)       // MUL(., c), SUM backward
+                                     : 0.0f;
+    // pre: g_e after DIV (from_softmax), or g_xm after SUB(xm, ls); uv becomes the row-sum terms
+    float pre[kMNE];
+    bool keep[kMNE];
+    float gS;
+    if constexpr (from_softmax<V>()) {
+        const float s2 = s * s;
+        const bool skip_ok = V == G_SMLM && gconst - gconst == 0.0f;
+#pragma unroll
+        for (int j = 0; j < kMNE; ++j) {
+            keep[j] = j < cnt && !(skip_ok && smlm_skip(uv[j], e[j]));
+            if (keep[j]) {
+                const float gsm = upstream<V>(uv[j], e[j], s, gconst);
+                pre[j] = 0.0f + gsm / s;
+                uv[j] = ((-e[j]) / s2) * gsm;
+            } else {
+                pre[j] = 0.0f;
+            }
+        }
+        gS = 0.0f + row_chain<P>(L, 0.0f, [&](float a) {
+#pragma unroll
+            for (int j = 0; j < kMNE; ++j)
+                if (keep[j]) a = a + uv[j];
+            return a;
+        });
+    } else {
+#pragma unroll
+        for (int j = 0; j < kMNE; ++j) {
+            const float glsm = upstream<V>(uv[j], e[j], s, gconst);
+            pre[j] = 0.0f + glsm;
+            uv[j] = glsm;
+        }
+        gS = 0.0f + (0.0f + (-row_chain<P>(L, 0.0f, [&](float a) {
+                               #pragma unroll
+                               for (int j = 0; j < kMNE; ++j)
+                                   if (j < cnt) a = a + uv[j];
+                               return a;
+                           }))) / s;
+    }
+    const float rgs = 1.0f * gS;  // SUM backward (classes > 1)
+#pragma unroll
+    for (int j = 0; j < kMNE; ++j) {
+        if constexpr (from_softmax<V>()) pre[j] = 0.0f + e[j] * (pre[j] + rgs);
+        else pre[j] = pre[j] + e[j] * (0.0f + rgs);
+    }
+    const float acc2 = row_chain<P>(L, 0.0f, [&](float a) {
+#pragma unroll
+        for (int j = 0; j < kMNE; ++j)
+            if (j < cnt) a = a + pre[j];
+        return a;
+    });
+    const float sg = (1.0f / (float)mc.c) * (0.0f + (-acc2));  // SUB 1, then the MAX factor
+#pragma unroll
+    for (int j = 0; j < kMNE; ++j) gv[j] = (gv[j] + pre[j]) + (xv[j] == mc.m ? sg : 0.0f);
+    if (L.live) store_chunk<VEC>(g + off, gv, cnt);
+}
+
+// ---------------------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------------------
 static inline bool al16s(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -955,6 +1205,23 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
         }
         return MH_OK;
     }
+    // multi-lane engine for rows of whole 16-byte quads (Softmax [8M elements] forward ~31 us for
+    // 20-64 classes against 25-52 us in the thread engine; CrossEntropy faster at every count);
+    // rows of other lengths load lane chunks element by element and stay on the thread engine
+    if (K > 16 && K <= 4 * kMNE && al && K % 4 == 0) {
+        const int P = (K + kMNE - 1) / kMNE;
+        const int64_t rpb = (int64_t)(kSThreads / 64) * (64 / P);
+        const int64_t nb = (rows + rpb - 1) / rpb;
+        if (nb > 0x7fffffff) return fail(MH_ERR_OVERFLOW, "too many rows");
+        *nblocks_out = nb;
+        dim3 g((unsigned)nb), b(kSThreads);
+#define MH_RM(PP) hipLaunchKernelGGL((k_rowm_fwd<V, PP, true>), g, b, 0, st, x, tg, out, rows, K, part)
+        if (P == 2) MH_RM(2);
+        else if (P == 3) MH_RM(3);
+        else MH_RM(4);
+#undef MH_RM
+        return MH_OK;
+    }
     if (K <= kSThreadMax) {
         const int rb = rows_per_block(LOSS ? 2 : 1, K);
         const int64_t nb = (rows + rb - 1) / rb;
@@ -1009,6 +1276,29 @@ static int launch_bwd(float* gx, const float* x, const float* up, const float* u
             MH_ROWP_CLASSES(MH_K)
 #undef MH_K
         }
+        return MH_OK;
+    }
+    // multi-lane engine: rows of whole quads (41-51 us for 20-64 classes over 8M elements,
+    // against 62-149 us in the thread engine), and any row of more than 32 classes (77-82 us
+    // against 92-149 element by element); shorter rows of other lengths stay on the thread engine
+    if (K > 16 && K <= 4 * kMNE && ((al && K % 4 == 0) || K > 32)) {
+        const int P = (K + kMNE - 1) / kMNE;
+        const int64_t rpb = (int64_t)(kSThreads / 64) * (64 / P);
+        const int64_t nb = (rows + rpb - 1) / rpb;
+        if (nb > 0x7fffffff) return fail(MH_ERR_OVERFLOW, "too many rows");
+        const bool vec = al && K % 4 == 0;
+        dim3 g((unsigned)nb), b(kSThreads);
+#define MH_RM(PP, VV) hipLaunchKernelGGL((k_rowm_bwd<V, PP, VV>), g, b, 0, st, gx, x, up, ug, rows, K, c)
+        if (vec) {
+            if (P == 2) MH_RM(2, true);
+            else if (P == 3) MH_RM(3, true);
+            else MH_RM(4, true);
+        } else {
+            if (P == 2) MH_RM(2, false);
+            else if (P == 3) MH_RM(3, false);
+            else MH_RM(4, false);
+        }
+#undef MH_RM
         return MH_OK;
     }
     if (K <= kSThreadMax) {

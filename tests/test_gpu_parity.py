@@ -723,7 +723,8 @@ def test_fused_row_graphs_reject_wide_rows(gpu):
 # every class count up to 16 (a kernel of its own each) appears.
 ROW_CASES = [(300, 1), (7, 2), (257, 3), (100, 10), (33, 31), (65, 32), (40, 33), (17, 63), (16, 64), (9, 65),
              (11, 66), (8, 100), (6, 128), (5, 130), (4, 257), (3, 1000), (2, 1024), (3, 1025), (2, 2044),
-             (2, 2047), (1000, 10)] + [(259 + k, k) for k in (4, 5, 6, 7, 8, 9, 11, 12, 13, 14, 15, 16)]
+             (2, 2047), (1000, 10), (2000, 20), (1500, 48), (777, 47), (1200, 64)] + \
+            [(259 + k, k) for k in (4, 5, 6, 7, 8, 9, 11, 12, 13, 14, 15, 16)]
 
 
 @pytest.mark.parametrize("rows,classes", ROW_CASES, ids=[f"{r}x{c}" for r, c in ROW_CASES])
