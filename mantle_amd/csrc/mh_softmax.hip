@@ -935,15 +935,24 @@ __device__ __forceinline__ T row_chain(const RowLanes<P>& L, T init, F fold) {
     return row_chain_shfl(v, L.lane - L.c + (P - 1));
 }
 
-// A lane's chunk straight from HBM with plain (cacheable) loads: a lane's quads are 64 bytes
-// apart from its neighbours', so each load instruction touches pieces of many lines, and the
-// next instructions find those lines in the caches (non-temporal loads fetched them again:
-// the 40-class Softmax forward took 70 us instead of 35). Staging the wavefront's contiguous
-// rows through LDS with coalesced loads was no faster forward and slower backward (its three
-// tiles held the grid to three blocks per CU).
+// A lane's chunk [off, off + cnt) straight from HBM with plain (cacheable) loads: a lane's
+// quads are 64 bytes from its neighbours', so each load instruction touches pieces of many
+// lines, and the next instructions find those lines in the caches (non-temporal loads fetched
+// them again: the 40-class Softmax forward took 70 us instead of 35). Staging the wavefront's
+// contiguous rows through LDS with coalesced loads was no faster forward and slower backward
+// (its three tiles held the grid to three blocks per CU). Rows of whole quads (VEC) load the
+// chunk's quads; other rows load the aligned quads that cover the chunk (the tensor's last,
+// partial quad element by element) and shift them into place: loading each element on its own
+// made such rows' forward twice as slow. `base` is 16-byte aligned, n the tensor's elements.
+__device__ __forceinline__ float shifted(const float* w, int j, int s) {
+    return s == 0 ? w[j] : s == 1 ? w[j + 1] : s == 2 ? w[j + 2] : w[j + 3];
+}
+
 template <bool VEC>
-__device__ __forceinline__ void load_chunk(float (&v)[kMNE], const float* __restrict__ p, int cnt) {
-    if constexpr (VEC) {  // cnt is a multiple of 4, p 16-byte aligned
+__device__ __forceinline__ void load_chunk(float (&v)[kMNE], const float* __restrict__ base, int64_t off, int cnt,
+                                           int64_t n) {
+    if constexpr (VEC) {  // off and cnt multiples of 4
+        const float* p = base + off;
 #pragma unroll
         for (int q = 0; q < kMNE / 4; ++q) {
             if (4 * q < cnt) {
@@ -954,21 +963,56 @@ __device__ __forceinline__ void load_chunk(float (&v)[kMNE], const float* __rest
             }
         }
     } else {
+        const int64_t a0 = off & ~(int64_t)3;
+        const int s = (int)(off - a0);
+        const int64_t last = off + cnt;  // one past the chunk
+        float w[kMNE + 4];
 #pragma unroll
-        for (int j = 0; j < kMNE; ++j) v[j] = j < cnt ? p[j] : 0.0f;
+        for (int q = 0; q < kMNE / 4 + 1; ++q) {
+            const int64_t e = a0 + 4 * q;
+            if (e < last && e + 3 < n) {
+                const vf4 t = *reinterpret_cast<const vf4*>(base + e);
+                w[4 * q] = t[0]; w[4 * q + 1] = t[1]; w[4 * q + 2] = t[2]; w[4 * q + 3] = t[3];
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w[4 * q + i] = e < last && e + i < n ? base[e + i] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kMNE; ++j) v[j] = j < cnt ? shifted(w, j, s) : 0.0f;
     }
 }
 
+// The chunk back: VEC rows as quads; other rows write the whole quads inside the chunk (this
+// lane's alone) as float4 and the elements before the first and after the last 16-byte
+// boundary one by one (their quads are shared with the neighbouring chunks).
 template <bool VEC>
-__device__ __forceinline__ void store_chunk(float* __restrict__ p, const float (&v)[kMNE], int cnt) {
+__device__ __forceinline__ void store_chunk(float* __restrict__ base, const float (&v)[kMNE], int64_t off, int cnt) {
     if constexpr (VEC) {
+        float* p = base + off;
 #pragma unroll
         for (int q = 0; q < kMNE / 4; ++q)
             if (4 * q < cnt) reinterpret_cast<vf4*>(p)[q] = vf4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
     } else {
+        const int64_t end = off + cnt;
+        const int64_t q0 = (off + 3) & ~(int64_t)3;  // first 16-byte boundary at or after off
+        const int64_t q1 = end & ~(int64_t)3;        // last boundary at or before end
+        const int d = (int)(q0 - off);                // v index of element q0
+        float w[kMNE + 4];                             // v, padded for the shifted reads
 #pragma unroll
-        for (int j = 0; j < kMNE; ++j)
-            if (j < cnt) p[j] = v[j];
+        for (int j = 0; j < kMNE + 4; ++j) w[j] = j < kMNE ? v[j] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < kMNE; ++j) {
+            const int64_t e = off + j;
+            if (j < cnt && (e < q0 || e >= q1)) base[e] = v[j];
+        }
+#pragma unroll
+        for (int k = 0; k < kMNE / 4; ++k) {
+            const int64_t e = q0 + 4 * k;
+            if (e + 4 <= q1)
+                *reinterpret_cast<vf4*>(base + e) = vf4{shifted(w, 4 * k, d), shifted(w, 4 * k + 1, d),
+                                                        shifted(w, 4 * k + 2, d), shifted(w, 4 * k + 3, d)};
+        }
     }
 }
 
@@ -997,8 +1041,9 @@ __global__ void __launch_bounds__(kSThreads)
     const int64_t off = row * (int64_t)K + kMNE * L.c;
     float xv[kMNE], tv[kMNE], e[kMNE];
     const int cnt = L.live ? L.cnt : 0;
-    load_chunk<VEC>(xv, x + (L.live ? off : 0), cnt);
-    if constexpr (LOSS) load_chunk<VEC>(tv, tg + (L.live ? off : 0), cnt);
+    const int64_t n = rows * (int64_t)K;
+    load_chunk<VEC>(xv, x, L.live ? off : 0, cnt, n);
+    if constexpr (LOSS) load_chunk<VEC>(tv, tg, L.live ? off : 0, cnt, n);
     // MAX.forward: max_simd from min_finite, element order
     const float m = row_chain<P>(L, -FLT_MAX, [&](float a) {
 #pragma unroll
@@ -1032,7 +1077,7 @@ __global__ void __launch_bounds__(kSThreads)
     } else {
 #pragma unroll
         for (int j = 0; j < kMNE; ++j) xv[j] = V == G_SOFTMAX ? e[j] / s : (xv[j] - m) - ls;  // DIV / SUB
-        if (L.live) store_chunk<VEC>(out + off, xv, cnt);
+        if (L.live) store_chunk<VEC>(out, xv, off, cnt);
     }
 }
 
@@ -1045,9 +1090,10 @@ __global__ void __launch_bounds__(kSThreads)
     const int64_t off = row * (int64_t)K + kMNE * L.c;
     const int cnt = L.live ? L.cnt : 0;
     float xv[kMNE], uv[kMNE], gv[kMNE], e[kMNE];
-    load_chunk<VEC>(xv, x + (L.live ? off : 0), cnt);
-    load_chunk<VEC>(uv, up + (L.live ? off : 0), cnt);
-    load_chunk<VEC>(gv, g + (L.live ? off : 0), cnt);
+    const int64_t n = rows * (int64_t)K;
+    load_chunk<VEC>(xv, x, L.live ? off : 0, cnt, n);
+    load_chunk<VEC>(uv, up, L.live ? off : 0, cnt, n);
+    load_chunk<VEC>(gv, g, L.live ? off : 0, cnt, n);
     // the forward row max (MAX.forward) and, as MAX.backward recomputes it, the max with its
     // count (an element neither above nor below the running max adds to the count)
     const float m = row_chain<P>(L, -FLT_MAX, [&](float a) {
@@ -1136,7 +1182,7 @@ __global__ void __launch_bounds__(kSThreads)
     const float sg = (1.0f / (float)mc.c) * (0.0f + (-acc2));  // SUB 1, then the MAX factor
 #pragma unroll
     for (int j = 0; j < kMNE; ++j) gv[j] = (gv[j] + pre[j]) + (xv[j] == mc.m ? sg : 0.0f);
-    if (L.live) store_chunk<VEC>(g + off, gv, cnt);
+    if (L.live) store_chunk<VEC>(g, gv, off, cnt);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1205,20 +1251,29 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
         }
         return MH_OK;
     }
-    // multi-lane engine for rows of whole 16-byte quads (Softmax [8M elements] forward ~31 us for
-    // 20-64 classes against 25-52 us in the thread engine; CrossEntropy faster at every count);
-    // rows of other lengths load lane chunks element by element and stay on the thread engine
-    if (K > 16 && K <= 4 * kMNE && al && K % 4 == 0) {
+    // multi-lane engine, aligned operands, over 8M elements: rows of whole 16-byte quads for
+    // 17-64 classes (Softmax 30-32 us against 25-52 us in the thread engine, CrossEntropy faster
+    // at every such count) and loss rows of more than 24 classes (shifted quad loads: 37-41 us
+    // against 46-49 us). Softmax rows that are not whole quads (shifted loads: 39-44 us) and
+    // losses of 17-24 classes stay on the thread engine (25-32 us).
+    if (K > 16 && K <= 4 * kMNE && al && (K % 4 == 0 || (LOSS && K > 24))) {
         const int P = (K + kMNE - 1) / kMNE;
         const int64_t rpb = (int64_t)(kSThreads / 64) * (64 / P);
         const int64_t nb = (rows + rpb - 1) / rpb;
         if (nb > 0x7fffffff) return fail(MH_ERR_OVERFLOW, "too many rows");
         *nblocks_out = nb;
+        const bool vec = K % 4 == 0;
         dim3 g((unsigned)nb), b(kSThreads);
-#define MH_RM(PP) hipLaunchKernelGGL((k_rowm_fwd<V, PP, true>), g, b, 0, st, x, tg, out, rows, K, part)
-        if (P == 2) MH_RM(2);
-        else if (P == 3) MH_RM(3);
-        else MH_RM(4);
+#define MH_RM(PP, VV) hipLaunchKernelGGL((k_rowm_fwd<V, PP, VV>), g, b, 0, st, x, tg, out, rows, K, part)
+        if (vec) {
+            if (P == 2) MH_RM(2, true);
+            else if (P == 3) MH_RM(3, true);
+            else MH_RM(4, true);
+        } else {
+            if (P == 2) MH_RM(2, false);
+            else if (P == 3) MH_RM(3, false);
+            else MH_RM(4, false);
+        }
 #undef MH_RM
         return MH_OK;
     }
@@ -1278,15 +1333,16 @@ static int launch_bwd(float* gx, const float* x, const float* up, const float* u
         }
         return MH_OK;
     }
-    // multi-lane engine: rows of whole quads (41-51 us for 20-64 classes over 8M elements,
-    // against 62-149 us in the thread engine), and any row of more than 32 classes (77-82 us
-    // against 92-149 element by element); shorter rows of other lengths stay on the thread engine
-    if (K > 16 && K <= 4 * kMNE && ((al && K % 4 == 0) || K > 32)) {
+    // multi-lane engine, aligned operands: rows of whole quads (over 8M elements 41-51 us for
+    // 20-64 classes, against 62-149 us in the thread engine) and other rows of more than 24
+    // classes (shifted quad loads: 61-76 us against 69-149); at 17 classes the thread engine
+    // is faster (53 against 90 us)
+    if (K > 16 && K <= 4 * kMNE && al && (K % 4 == 0 || K > 24)) {
         const int P = (K + kMNE - 1) / kMNE;
         const int64_t rpb = (int64_t)(kSThreads / 64) * (64 / P);
         const int64_t nb = (rows + rpb - 1) / rpb;
         if (nb > 0x7fffffff) return fail(MH_ERR_OVERFLOW, "too many rows");
-        const bool vec = al && K % 4 == 0;
+        const bool vec = K % 4 == 0;
         dim3 g((unsigned)nb), b(kSThreads);
 #define MH_RM(PP, VV) hipLaunchKernelGGL((k_rowm_bwd<V, PP, VV>), g, b, 0, st, gx, x, up, ug, rows, K, c)
         if (vec) {

@@ -613,7 +613,8 @@ def test_config5_classifier_chain_small(gpu):
 
 # every class count up to 16 has a kernel of its own: each appears at least once
 SMLM_CASES = [(4099, 10), (1, 1), (3, 2), (257, 3), (1000, 16), (513, 17), (300, 32), (64, 1), (7, 5), (2048, 10),
-              (40, 33), (20, 64), (9, 65), (8, 128), (5, 130), (3, 1000), (2, 2047)] + \
+              (40, 33), (20, 64), (9, 65), (8, 128), (5, 130), (3, 1000), (2, 2047), (777, 47), (1500, 27),
+              (513, 63)] + \
              [(259 + k, k) for k in (4, 6, 7, 8, 9, 11, 12, 13, 14, 15)]
 
 
@@ -672,7 +673,7 @@ def test_fused_softmax_log_mul_mean(gpu, rows, classes, ugv):
     _check_fused_head(gpu, logits, onehot, ugv)
 
 
-HEAD_SKIP_CASES = [(4099, 10), (1000, 16), (513, 17), (300, 40), (9, 130), (3, 1000)]
+HEAD_SKIP_CASES = [(4099, 10), (1000, 16), (513, 17), (300, 40), (301, 47), (9, 130), (3, 1000)]
 
 
 @pytest.mark.parametrize("rows,classes", HEAD_SKIP_CASES, ids=[f"{r}x{c}" for r, c in HEAD_SKIP_CASES])
