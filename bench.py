@@ -437,10 +437,12 @@ def run_c4(L, reps):
             ops.append((f"{tag}.{ax}.{op}.fwd",
                         lambda P, o=o, name=name, s=s, axis=axis: L.mh_reduce_fwd(o, P[f"res_{name}"], P[name], s, axis),
                         4 * n + 4 * m))
-        # MAX backward reads x (twice where the line max is a separate pass: axis 0, all) and
-        # grad, and stores only the grad quads that hold a line maximum (at most m of them)
-        two_pass = axis in (0, -1)
-        hbm[f"{tag}.{ax}.MAX.bwd"] = (12 * n if two_pass else 8 * n) + 4 * m + 16 * m
+        # MAX backward reads x and grad once each and stores only the grad quads that hold a
+        # line maximum (at most m of them). Where the line maxima are a pass of their own
+        # (axis 0, all), the routing pass reads x again only in the splits whose partials say
+        # they hold several maxima of a line (rare); the split partials themselves (under 7 %
+        # of the bytes at these shapes) are not counted
+        hbm[f"{tag}.{ax}.MAX.bwd"] = 8 * n + 4 * m + 16 * m
         for op in ("SUM", "MEAN", "MAX"):
             o = OP_ID[op]
             nb = (12 * n + 8 * m) if op == "MAX" else (8 * n + 4 * m)
@@ -1067,15 +1069,16 @@ WL_KERNELS = [
     ("c3 bias_relu.bwd (fused), combine", "mh::k_bias_partials_comb", 8192, 8 * (_N3 // 256) + 256,
      "the wave partials (two per 64 quads) read, 32 bias values updated"),
     ("c3 ADD.bwd_bias", "void mh::k_unb_planes<false>", 131072, 4 * _N3 + 256, "one launch, arrival tickets"),
-    ("c4 [8192,8192] axis 0 MAX.fwd", "void mh::k_cols<mh::RMax, mh::LdPlain<mh::RMax>, true>", 131072,
+    ("c4 [8192,8192] axis 0 MAX.fwd", "void mh::k_cols<mh::RMax, mh::LdPlain<mh::RMax>, true, true>", 262144,
      4 * _N4, "first of two launches (split partials)"),
-    ("c4 [8192,8192] axis 0 MAX.bwd, route", "void mh::k_colbc4<mh::FMaxRoute, 4, true>", 16777216, 12 * _N4,
-     "stores only quads holding a line maximum"),
+    ("c4 [8192,8192] axis 0 MAX.bwd, route", "void mh::k_max_route_cols<true, true>", 262144, 4 * _N4,
+     "grad read; x read again only in splits holding several maxima of a column; stores only quads "
+     "holding a maximum"),
     ("c4 [8192,8192] axis 0 SUM.bwd", "void mh::k_colbc4<mh::FScaleBcast<false>, 1, true>", 16777216, 8 * _N4, ""),
     ("c4 [8192,8192] axis 1 MAX.bwd", "void mh::k_max_bwd_rowreg<4, 8>", 2097152, 12 * _N4,
      "one pass; stores only quads holding a line maximum"),
-    ("c4 [8192,8192] all MAX.bwd, route", "void mh::k_same4<mh::FMaxRoute, 4, true>", 16777216, 12 * _N4,
-     "stores only quads holding the maximum"),
+    ("c4 [8192,8192] all MAX.bwd, route", "mh::k_max_route_rows", 8388608, 4 * _N4,
+     "grad read; x read again only in the chunk holding the maximum; stores only quads holding it"),
     ("c4 [64,512,1024] axis 2 MAX.bwd", "void mh::k_max_bwd_rowreg<1, 4>", 2097152, 12 * (1 << 25),
      "one pass; stores only quads holding a line maximum"),
     ("c5 SUB.fwd [N,10] - [N,1]", "void mh::k_rowbc4<mh::FBin<1>, 2, false>", 2621440, 8 * _N5 + 4 * (_N5 // 10), ""),

@@ -257,7 +257,9 @@ __device__ __forceinline__ void bcast_decode(const ElwPlan& pl, int64_t idx, off
 // kernels (defined in mh_elementwise.hip / mh_reduce.hip)
 // ---------------------------------------------------------------------------------------
 // Reduction operator and epilogue ids shared by the reduce launchers.
-enum RedOp : int { RED_SUM = 0, RED_MAX = 1, RED_MAXCNT = 2 };
+// RED_MAXCNT_ARG: RED_MAXCNT whose split partials also hold the element index of each split's
+// maximum (x of fewer than 2^32 elements).
+enum RedOp : int { RED_SUM = 0, RED_MAX = 1, RED_MAXCNT = 2, RED_MAXCNT_ARG = 3 };
 enum Epi : int {
     EPI_STORE = 0,     // out = v
     EPI_MEAN = 1,      // out = v / (float)len
@@ -274,9 +276,16 @@ enum Epi : int {
 // Reduce x viewed as [A, B, C] over B into out[A*C] (out2: fl(1/count) for RED_MAXCNT).
 // `div` is the float divisor of EPI_MEAN; `tmp` holds split partials
 // (reduce_abc_tmp_floats(op, A, B, C) floats, may be null when that is 0).
+// `split`, when given, says where the first pass left its split partials in tmp (RED_MAXCNT:
+// the maxima, then the counts; RED_MAXCNT_ARG: then the indices): S == 1 when there are none; C == 1 (rows): chunk s of line r
+// (kRowChunk elements from r * B + s * span) at tmp[r * S + s]; columns: split s (rows
+// [s * span, (s + 1) * span) of every line) at tmp[s * A * C + line].
+struct RedSplit {
+    int64_t S = 1, span = 0;
+};
 size_t reduce_abc_tmp_floats(int op, int64_t A, int64_t B, int64_t C);
 int reduce_abc(int op, int epi, const float* x, int64_t A, int64_t B, int64_t C, float* out,
-               float* out2, float div, float* tmp);
+               float* out2, float div, float* tmp, RedSplit* split = nullptr);
 // Sum over all n elements of the POW exponent-gradient term, accumulated into grad[0]; with
 // grad_x, the x gradient of every element is accumulated into grad_x in the same pass.
 int pow_exponent_grad(float* grad, const float* x, const float* exponent, const float* ug,

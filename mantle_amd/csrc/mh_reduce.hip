@@ -66,6 +66,28 @@ struct RMaxCnt {  // (line max, number of elements equal to it)
     }
 };
 
+// RMaxCnt with the element index of the maximum: the first pass of a column MAX backward.
+// Maxima and counts are RMaxCnt's (the same comparisons and sums); a tie keeps the lower index.
+// Where a split's count is 1, its index is the one element equal to its maximum, and the
+// routing pass adds there without reading x again (a count above 1 makes it read x).
+struct MCI {
+    float m;
+    uint32_t c, i;
+};
+struct RMaxCntArg {
+    using T = MCI;
+    __device__ static T init() { return MCI{-FLT_MAX, 0u, 0xffffffffu}; }
+    __device__ static T lift(float x) { return MCI{x, 1u, 0xffffffffu}; }
+    __device__ static T comb(T a, T b) {
+        if (a.m > b.m) return a;
+        if (b.m > a.m) return b;
+        return MCI{a.m, a.c + b.c, a.i < b.i ? a.i : b.i};
+    }
+    __device__ static T shfl(T v, int m) {
+        return MCI{__shfl_xor(v.m, m), (uint32_t)__shfl_xor((int)v.c, m), (uint32_t)__shfl_xor((int)v.i, m)};
+    }
+};
+
 // ---------------------------------------------------------------------------------------
 // loaders: get(i) -> R::T at element i; get4 for 16-byte aligned quads
 // ---------------------------------------------------------------------------------------
@@ -80,13 +102,44 @@ struct LdPlain {
     }
 };
 
-struct LdPairs {  // split partials of RMaxCnt
+struct LdArg {  // x, each element with its index (tensors of fewer than 2^32 elements)
+    const float* x;
+    __device__ void setup() {}
+    __device__ MCI get(int64_t i) const { return MCI{ld_nt(x + i), 1u, (uint32_t)i}; }
+    __device__ void get4(int64_t i, MCI* o) const {
+        const float4 q = ld_nt4(x + i, 0);
+        const uint32_t k = (uint32_t)i;
+        o[0] = MCI{q.x, 1u, k}; o[1] = MCI{q.y, 1u, k + 1}; o[2] = MCI{q.z, 1u, k + 2}; o[3] = MCI{q.w, 1u, k + 3};
+    }
+};
+
+// Split partials of RMaxCnt (LdPairs) and RMaxCntArg (LdPairsArg): the maxima at m, the counts
+// at c. The combines above the first level need no indices (only the first level's feed the
+// routing), so LdPairsArg leaves them at their initial value. get4 is called at quad-aligned
+// offsets only (counts of partials a multiple of 4 in 64-float-aligned scratch): two quad
+// loads.
+struct LdPairsArg {
+    const float* m;
+    const uint32_t* c;
+    __device__ void setup() {}
+    __device__ MCI get(int64_t k) const { return MCI{m[k], c[k], 0xffffffffu}; }
+    __device__ void get4(int64_t k, MCI* o) const {
+        const float4 a = *reinterpret_cast<const float4*>(m + k);
+        const uint4 b = *reinterpret_cast<const uint4*>(c + k);
+        o[0] = MCI{a.x, b.x, 0xffffffffu}; o[1] = MCI{a.y, b.y, 0xffffffffu};
+        o[2] = MCI{a.z, b.z, 0xffffffffu}; o[3] = MCI{a.w, b.w, 0xffffffffu};
+    }
+};
+
+struct LdPairs {
     const float* m;
     const uint32_t* c;
     __device__ void setup() {}
     __device__ MC get(int64_t i) const { return MC{m[i], c[i]}; }
     __device__ void get4(int64_t i, MC* o) const {
-        for (int j = 0; j < 4; ++j) o[j] = get(i + j);
+        const float4 a = *reinterpret_cast<const float4*>(m + i);
+        const uint4 b = *reinterpret_cast<const uint4*>(c + i);
+        o[0] = MC{a.x, b.x}; o[1] = MC{a.y, b.y}; o[2] = MC{a.z, b.z}; o[3] = MC{a.w, b.w};
     }
 };
 
@@ -232,11 +285,21 @@ __device__ __forceinline__ void epi_store(float* out, float* out2, int64_t o, MC
     out[o] = v.m;
     out2[o] = 1.0f / (float)v.c;  // MAX.backward: factor = 1 / count, basics.mojo:573, 609
 }
-// MC partials keep the counts in a second array right after the maxima.
+__device__ __forceinline__ void epi_store(float* out, float* out2, int64_t o, MCI v, int, float) {
+    out[o] = v.m;
+    out2[o] = 1.0f / (float)v.c;
+}
+// MC partials keep the counts in a second array right after the maxima, MCI partials the
+// indices in a third after the counts.
 __device__ __forceinline__ void part_store2(float* pm, int64_t npart, int64_t o, float v) { pm[o] = v; (void)npart; }
 __device__ __forceinline__ void part_store2(float* pm, int64_t npart, int64_t o, MC v) {
     pm[o] = v.m;
     reinterpret_cast<uint32_t*>(pm + npart)[o] = v.c;
+}
+__device__ __forceinline__ void part_store2(float* pm, int64_t npart, int64_t o, MCI v) {
+    pm[o] = v.m;
+    reinterpret_cast<uint32_t*>(pm + npart)[o] = v.c;
+    reinterpret_cast<uint32_t*>(pm + 2 * npart)[o] = v.i;
 }
 
 template <class R>
@@ -809,6 +872,162 @@ __global__ void __launch_bounds__(kRThreads)
     }
 }
 
+// MAX backward routing behind a split max-count reduction (basics.mojo:567-577, 597-613):
+// grad[i] = grad[i] + (x[i] == m ? fl(1/c) * ug : 0) for the line maximum m, each grad quad
+// stored only when its bits change. The reduction's first pass left each split's partial
+// maximum pm (a column's rows [s * rps, (s + 1) * rps), or a row's chunk s). A split holding
+// an element x[i] == m has pm == m: pm >= x[i] as the maximum of its elements, pm <= m as one
+// of the values m is the maximum of, and neither is NaN (RMaxCnt keeps NaN out of the
+// maximum, so x[i] == m excludes it too). A split with pm != m therefore holds no element of
+// its line's maximum: every term there is +0, and its x is not read (grad + 0 still turns -0
+// into +0, which the sparse store writes back). Where the partials also hold the split's count
+// and the index of its maximum (RMaxCntArg), a split with pm == m and count 1 holds exactly
+// one such element, at that index, and count 0 none; x is read again only in a split that
+// holds several.
+// Changed quads wait in registers (two of them) and are stored after the thread's loads: a
+// store issued between loads would hold every later wait for loaded data until the store
+// completes (vmcnt counts stores as well as loads), which cost the column route a third of
+// its time. A third change in one thread stores at once.
+struct PendingStores {
+    int64_t q0 = 0, q1 = 0;
+    float4 v0, v1;
+    int n = 0;
+    __device__ __forceinline__ void put(float* gr, int64_t q, float4 v) {
+        if (n == 0) {
+            q0 = q; v0 = v; n = 1;
+        } else if (n == 1) {
+            q1 = q; v1 = v; n = 2;
+        } else {
+            st_nt4(gr, q, v);
+        }
+    }
+    __device__ __forceinline__ void flush(float* gr) const {
+        if (n > 0) st_nt4(gr, q0, v0);
+        if (n > 1) st_nt4(gr, q1, v1);
+    }
+};
+// grad quad g plus add[j] where hit[j], else plus +0; queued when its bits change.
+__device__ __forceinline__ void route_quad(PendingStores& pd, float* gr, int64_t q, float4 g, const bool (&hit)[4],
+                                           const float (&add)[4]) {
+    const float4 n = make_float4(g.x + (hit[0] ? add[0] : 0.0f), g.y + (hit[1] ? add[1] : 0.0f),
+                                 g.z + (hit[2] ? add[2] : 0.0f), g.w + (hit[3] ? add[3] : 0.0f));
+    if (bits_differ4(g.x, g.y, g.z, g.w, n.x, n.y, n.z, n.w)) pd.put(gr, q, n);
+}
+__device__ __forceinline__ void route_quad_x(PendingStores& pd, float* gr, int64_t q, float4 g, float4 xv, bool need,
+                                             const float (&mv)[4], const float (&add)[4]) {
+    const bool hit[4] = {need && xv.x == mv[0], need && xv.y == mv[1], need && xv.z == mv[2], need && xv.w == mv[3]};
+    route_quad(pd, gr, q, g, hit, add);
+}
+
+// Columns (C % 4 == 0, 16-byte aligned grad and x): a thread per (column quad o, split s),
+// the layout of the reduction's column launchers; two rows in flight. SPLIT_X: splits on grid
+// x, column-quad blocks on grid y. ARG: pc / pi hold the splits' counts and indices. The
+// partials, m and f are 16-byte aligned scratch: one quad load each.
+template <bool SPLIT_X, bool ARG>
+__global__ void __launch_bounds__(kRThreads)
+    k_max_route_cols(float* __restrict__ grad, const float* __restrict__ x, const float* __restrict__ m,
+                     const float* __restrict__ f, const float* __restrict__ ug, const float* __restrict__ pm,
+                     const uint32_t* __restrict__ pc, const uint32_t* __restrict__ pi, int64_t A, int64_t B,
+                     int64_t C, int64_t rps) {
+    const int64_t AC = A * C;
+    const int64_t o = ((int64_t)(SPLIT_X ? blockIdx.y : blockIdx.x) * kRThreads + threadIdx.x) * 4;
+    if (o >= AC) return;
+    const int64_t s = SPLIT_X ? blockIdx.x : blockIdx.y;
+    const int64_t a = o / C, c = o - a * C;
+    const int64_t b0 = s * rps, b1 = b0 + rps < B ? b0 + rps : B;
+    const int64_t e0 = a * B * C + c;  // element of row 0, column c
+    const int64_t k = s * AC + o;      // this split's partials of columns o .. o + 3
+    const float4 m4 = *reinterpret_cast<const float4*>(m + o), f4 = *reinterpret_cast<const float4*>(f + o);
+    const float4 p4 = *reinterpret_cast<const float4*>(pm + k);
+    uint4 c4 = make_uint4(0u, 0u, 0u, 0u), i4 = make_uint4(0u, 0u, 0u, 0u);
+    if (ARG) {
+        c4 = *reinterpret_cast<const uint4*>(pc + k);
+        i4 = *reinterpret_cast<const uint4*>(pi + k);
+    }
+    const float u[4] = {ug[o], ug[o + 1], ug[o + 2], ug[o + 3]};
+    const float mv[4] = {m4.x, m4.y, m4.z, m4.w};
+    const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
+    const float fv[4] = {f4.x, f4.y, f4.z, f4.w};
+    const uint32_t cv[4] = {c4.x, c4.y, c4.z, c4.w}, iv[4] = {i4.x, i4.y, i4.z, i4.w};
+    // ARG: column j's single maximum in this split as an element offset from (row b0, column
+    // c + j), a multiple of C (x has fewer than 2^32 elements); else 0xffffffff, which no
+    // row's offset r * C reaches
+    const uint32_t eb = (uint32_t)(e0 + b0 * C);
+    float add[4];
+    uint32_t sel[4];
+    bool xread = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        add[j] = fv[j] * u[j];
+        const bool nj = pv[j] == mv[j];
+        if (ARG) {
+            xread = xread || (nj && cv[j] >= 2u);
+            sel[j] = nj && cv[j] == 1u ? iv[j] - (eb + (uint32_t)j) : 0xffffffffu;
+        } else {
+            xread = xread || nj;
+            sel[j] = 0xffffffffu;
+        }
+    }
+    const int64_t q0 = (e0 >> 2) + b0 * (C >> 2), qs = C >> 2;  // quad of row b0 + r: q0 + r * qs
+    const int nr = (int)(b1 - b0);
+    const uint32_t uc = (uint32_t)C;
+    // One loop for both ways (x compared, or the row offset against sel): with a loop per way
+    // in a branch that is uniform over few waves, the kernel took 61 us against 43 us here
+    // ([8192, 8192], axis 0).
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    PendingStores pd;
+    uint32_t rc = 0;  // r * C
+    int r = 0;
+    for (; r + 1 < nr; r += 2, rc += 2 * uc) {
+        const int64_t qa = q0 + r * qs, qb = qa + qs;
+        const float4 ga = ld_nt4(grad, qa), gb = ld_nt4(grad, qb);
+        const float4 xa = xread ? ld_nt4(x, qa) : z, xb = xread ? ld_nt4(x, qb) : z;
+        const uint32_t rd = rc + uc;
+        const bool ha[4] = {xread ? xa.x == mv[0] : rc == sel[0], xread ? xa.y == mv[1] : rc == sel[1],
+                            xread ? xa.z == mv[2] : rc == sel[2], xread ? xa.w == mv[3] : rc == sel[3]};
+        const bool hb[4] = {xread ? xb.x == mv[0] : rd == sel[0], xread ? xb.y == mv[1] : rd == sel[1],
+                            xread ? xb.z == mv[2] : rd == sel[2], xread ? xb.w == mv[3] : rd == sel[3]};
+        route_quad(pd, grad, qa, ga, ha, add);
+        route_quad(pd, grad, qb, gb, hb, add);
+    }
+    if (r < nr) {
+        const int64_t qa = q0 + r * qs;
+        const float4 ga = ld_nt4(grad, qa), xa = xread ? ld_nt4(x, qa) : z;
+        const bool ha[4] = {xread ? xa.x == mv[0] : rc == sel[0], xread ? xa.y == mv[1] : rc == sel[1],
+                            xread ? xa.z == mv[2] : rc == sel[2], xread ? xa.w == mv[3] : rc == sel[3]};
+        route_quad(pd, grad, qa, ga, ha, add);
+    }
+    pd.flush(grad);
+}
+
+// Rows (C == 1, B % 4 == 0, 16-byte aligned grad and x): a block per chunk vr = r * S + s of
+// kRowChunk elements (the reduction's row chunks), two quads per thread; whether the chunk
+// reads x is uniform over the block.
+__global__ void __launch_bounds__(kRThreads)
+    k_max_route_rows(float* __restrict__ grad, const float* __restrict__ x, const float* __restrict__ m,
+                     const float* __restrict__ f, const float* __restrict__ ug, const float* __restrict__ pm,
+                     int64_t S, int64_t B) {
+    const int64_t vr = blockIdx.x;
+    const int64_t r = vr / S, s = vr - r * S;
+    const int64_t rem = B - s * kRowChunk;
+    const int64_t nq = (rem < kRowChunk ? rem : kRowChunk) >> 2;
+    const int64_t q0 = (r * B + s * kRowChunk) >> 2;
+    const float mr = m[r];
+    const float ad = f[r] * ug[r];
+    const float mv[4] = {mr, mr, mr, mr}, add[4] = {ad, ad, ad, ad};
+    const bool need = pm[vr] == mr;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int t = threadIdx.x;
+    static_assert(kRowChunk == 8 * kRThreads, "two quads per thread cover a chunk");
+    const bool ha = t < nq, hb = t + kRThreads < nq;
+    const float4 ga = ha ? ld_nt4(grad, q0 + t) : z, gb = hb ? ld_nt4(grad, q0 + t + kRThreads) : z;
+    const float4 xa = ha && need ? ld_nt4(x, q0 + t) : z, xb = hb && need ? ld_nt4(x, q0 + t + kRThreads) : z;
+    PendingStores pd;
+    if (ha) route_quad_x(pd, grad, q0 + t, ga, xa, need, mv, add);
+    if (hb) route_quad_x(pd, grad, q0 + t + kRThreads, gb, xb, need, mv, add);
+    pd.flush(grad);
+}
+
 // ---------------------------------------------------------------------------------------
 // tstd: one pass over x, fp64 moments
 // ---------------------------------------------------------------------------------------
@@ -1143,7 +1362,7 @@ static ColSplit wide_split(int64_t A, int64_t B, int64_t C) {
 
 template <class R>
 static constexpr int part_words() {
-    return sizeof(typename R::T) == 4 ? 1 : 2;
+    return (int)(sizeof(typename R::T) / 4);
 }
 
 static inline size_t pad64(size_t v) { return (v + 63) & ~(size_t)63; }
@@ -1193,6 +1412,7 @@ static size_t tmp_floats_t(int64_t A, int64_t B, int64_t C, bool vec_ok) {
 
 size_t reduce_abc_tmp_floats(int op, int64_t A, int64_t B, int64_t C) {
     if (op == RED_MAXCNT) return tmp_floats_t<RMaxCnt>(A, B, C, true);
+    if (op == RED_MAXCNT_ARG) return tmp_floats_t<RMaxCntArg>(A, B, C, true);
     return tmp_floats_t<RSum>(A, B, C, true);
 }
 
@@ -1206,11 +1426,17 @@ struct PartLoader<RMaxCnt> {
     using type = LdPairs;
     static type make(float* p, int64_t n) { return LdPairs{p, reinterpret_cast<const uint32_t*>(p + n)}; }
 };
+template <>
+struct PartLoader<RMaxCntArg> {
+    using type = LdPairsArg;
+    static type make(float* p, int64_t n) { return LdPairsArg{p, reinterpret_cast<const uint32_t*>(p + n)}; }
+};
 
 // nosplit: the combine stage over column-split partials runs as a single pass (tmp unused).
 template <class R, class LD>
 static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C, float* out,
-                    float* out2, float div, float* tmp, bool nosplit = false, bool combine = false) {
+                    float* out2, float div, float* tmp, bool nosplit = false, bool combine = false,
+                    RedSplit* split = nullptr) {
     if (A * C == 0) return MH_OK;
     hipStream_t st = ctx().stream;
     if (C > 1 && B <= 64 && (epi == EPI_SEQ_ACCUM || epi == EPI_SEQ_ACCUM_NEG) && A * C < kMaxGridRows) {
@@ -1273,6 +1499,7 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
         }
         const int64_t L = S == 1 ? B : kRowChunk;
         const int64_t nv = A * S;
+        if (split && S > 1) *split = RedSplit{S, L};
         dim3 g((unsigned)nv), b(kRThreads);
         if (vec) hipLaunchKernelGGL((k_rows_block<R, LD, true>), g, b, 0, st, ld, S, B, L, out, out2, epi, div, tmp, nv);
         else hipLaunchKernelGGL((k_rows_block<R, LD, false>), g, b, 0, st, ld, S, B, L, out, out2, epi, div, tmp, nv);
@@ -1288,6 +1515,7 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
     if (!nosplit && use_wide_cols(C, vec_ok) && (A * C / 4 + kRThreads - 1) / kRThreads <= 65535) {
         ColSplit cs = wide_split(A, B, C);
         const int64_t items = A * C / 4;
+        if (split && cs.S > 1) *split = RedSplit{cs.S, cs.rps};
         dim3 g((unsigned)cs.S, (unsigned)((items + kRThreads - 1) / kRThreads)), b(kRThreads);
         hipLaunchKernelGGL((k_cols<R, LD, true, true>), g, b, 0, st, ld, A, B, C, cs.rps, cs.S, out, out2, epi, div,
                            tmp);
@@ -1307,6 +1535,7 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
             cs.S = 1;
             cs.rps = B;
         }
+        if (split && cs.S > 1) *split = RedSplit{cs.S, cs.rps};
         dim3 g((unsigned)(A * ns), (unsigned)cs.S), b(kRThreads);
         hipLaunchKernelGGL((k_cols_strip<R, LD>), g, b, 0, st, ld, A, B, C, ns, cs.rps, cs.S, out, out2, epi, div, tmp);
         if (cs.S > 1) {
@@ -1323,6 +1552,7 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
         cs.rps = B;
     }
     const int64_t items = A * C / (cs.vec ? 4 : 1);
+    if (split && cs.S > 1) *split = RedSplit{cs.S, cs.rps};
     dim3 g((unsigned)((items + kRThreads - 1) / kRThreads), (unsigned)cs.S), b(kRThreads);
     if (cs.vec) hipLaunchKernelGGL((k_cols<R, LD, true>), g, b, 0, st, ld, A, B, C, cs.rps, cs.S, out, out2, epi, div, tmp);
     else hipLaunchKernelGGL((k_cols<R, LD, false>), g, b, 0, st, ld, A, B, C, cs.rps, cs.S, out, out2, epi, div, tmp);
@@ -1336,13 +1566,20 @@ static int reduce_t(LD ld, bool vec_ok, int epi, int64_t A, int64_t B, int64_t C
 }
 
 int reduce_abc(int op, int epi, const float* x, int64_t A, int64_t B, int64_t C, float* out, float* out2,
-               float div, float* tmp) {
+               float div, float* tmp, RedSplit* split) {
     const bool al = al16(x);
     switch (op) {
-        case RED_SUM: return reduce_t<RSum, LdPlain<RSum>>(LdPlain<RSum>{x}, al, epi, A, B, C, out, out2, div, tmp);
-        case RED_MAX: return reduce_t<RMax, LdPlain<RMax>>(LdPlain<RMax>{x}, al, epi, A, B, C, out, out2, div, tmp);
+        case RED_SUM:
+            return reduce_t<RSum, LdPlain<RSum>>(LdPlain<RSum>{x}, al, epi, A, B, C, out, out2, div, tmp, false,
+                                                 false, split);
+        case RED_MAX:
+            return reduce_t<RMax, LdPlain<RMax>>(LdPlain<RMax>{x}, al, epi, A, B, C, out, out2, div, tmp, false,
+                                                 false, split);
+        case RED_MAXCNT_ARG:
+            return reduce_t<RMaxCntArg, LdArg>(LdArg{x}, al, epi, A, B, C, out, out2, div, tmp, false, false, split);
         default:
-            return reduce_t<RMaxCnt, LdPlain<RMaxCnt>>(LdPlain<RMaxCnt>{x}, al, epi, A, B, C, out, out2, div, tmp);
+            return reduce_t<RMaxCnt, LdPlain<RMaxCnt>>(LdPlain<RMaxCnt>{x}, al, epi, A, B, C, out, out2, div, tmp,
+                                                       false, false, split);
     }
 }
 
@@ -1869,6 +2106,45 @@ int mh_tstd(float* res, const float* x, const mh_shape* psx, int32_t axis) {
     return finish("mh_tstd");
 }
 
+}  // extern "C"
+
+// The routing pass of a MAX backward whose reduction left split partials (k_max_route_*;
+// arg: RED_MAXCNT_ARG partials): false where their layout does not fit those kernels (the
+// caller routes every element).
+static bool max_route_split(float* grad, const float* x, int64_t A, int64_t B, int64_t C, const float* m,
+                            const float* f, const float* ug, float* tmp, const RedSplit& sp, bool arg) {
+    if (sp.S <= 1 || !al16(x) || !al16(grad)) return false;
+    hipStream_t st = ctx().stream;
+    if (C == 1) {
+        const int64_t nv = A * sp.S;
+        if (arg || B % 4 != 0 || sp.span != kRowChunk || nv > 0x7fffffff) return false;
+        hipLaunchKernelGGL(k_max_route_rows, dim3((unsigned)nv), dim3(kRThreads), 0, st, grad, x, m, f, ug, tmp,
+                           sp.S, B);
+        return true;
+    }
+    if (C % 4 != 0 || sp.S > 65535) return false;
+    const int64_t np = sp.S * A * C;
+    const uint32_t* pc = reinterpret_cast<const uint32_t*>(tmp + np);
+    const uint32_t* pi = reinterpret_cast<const uint32_t*>(tmp + 2 * np);
+    const int64_t qb = (A * C / 4 + kRThreads - 1) / kRThreads;
+    const bool sx = qb <= 65535;
+    if (!sx && qb > 0x7fffffff) return false;
+    const dim3 g = sx ? dim3((unsigned)sp.S, (unsigned)qb) : dim3((unsigned)qb, (unsigned)sp.S), b(kRThreads);
+#define MH_RC(SX, AR) \
+    hipLaunchKernelGGL((k_max_route_cols<SX, AR>), g, b, 0, st, grad, x, m, f, ug, tmp, pc, pi, A, B, C, sp.span)
+    if (sx) {
+        if (arg) MH_RC(true, true);
+        else MH_RC(true, false);
+    } else {
+        if (arg) MH_RC(false, true);
+        else MH_RC(false, false);
+    }
+#undef MH_RC
+    return true;
+}
+
+extern "C" {
+
 int mh_reduce_bwd_accum(int op, float* grad, const float* x, const mh_shape* psx, const float* ug,
                         int32_t axis) {
     MH_TRACE_OP("mh_reduce_bwd_accum", op);
@@ -1930,13 +2206,18 @@ int mh_reduce_bwd_accum(int op, float* grad, const float* x, const mh_shape* psx
     } else {  // MAX, basics.mojo:536-615: line max and fl(1/count), then routing
         const int64_t nl = A * C;
         const size_t pad_nl = ((size_t)nl + 63) & ~(size_t)63;
-        const size_t t = reduce_abc_tmp_floats(RED_MAXCNT, A, B, C);
+        // columns: the split partials keep each split's index of its maximum (n < 2^32)
+        const bool arg = C > 1 && n < ((int64_t)1 << 32);
+        const int rop = arg ? RED_MAXCNT_ARG : RED_MAXCNT;
+        const size_t t = reduce_abc_tmp_floats(rop, A, B, C);
         float* base = nullptr;
         MH_TRY(scratch((2 * pad_nl + t + 64) * sizeof(float), reinterpret_cast<void**>(&base)));
         float* m = base;
         float* f = base + pad_nl;
-        MH_TRY(reduce_abc(RED_MAXCNT, EPI_STORE, x, A, B, C, m, f, 0.0f, base + 2 * pad_nl));
-        MH_TRY(map_max_route(grad, sx, x, sug, m, f, ug));
+        float* tmp = base + 2 * pad_nl;
+        RedSplit sp;
+        MH_TRY(reduce_abc(rop, EPI_STORE, x, A, B, C, m, f, 0.0f, tmp, &sp));
+        if (!max_route_split(grad, x, A, B, C, m, f, ug, tmp, sp, arg)) MH_TRY(map_max_route(grad, sx, x, sug, m, f, ug));
     }
     return finish("mh_reduce_bwd_accum");
 }

@@ -335,7 +335,11 @@ def test_reduce_fwd_bwd_parity(gpu, shape, axis):
 
 
 MAX_SPARSE_CASES = [((1024, 1024), 0), ((4099, 10), 1), ((300, 20), 1), ((64, 512), 1), ((9, 2052), 1),
-                    ((87, 73, 107), None), ((87, 73, 107), 1), ((4, 8, 1024), 0), ((2, 5000, 132), 1)]
+                    ((87, 73, 107), None), ((87, 73, 107), 1), ((4, 8, 1024), 0), ((2, 5000, 132), 1),
+                    # split routes: row chunks (all elements, a short last chunk), the strip and
+                    # thread-per-quad column splits, a wide split over three slabs
+                    ((1 << 20,), None), ((3, 12000), None), ((300, 256), 0), ((9000, 64), 0),
+                    ((3, 3000, 1024), 1)]
 
 
 @pytest.mark.parametrize("shape,axis", MAX_SPARSE_CASES, ids=[f"{s}-ax{a}" for s, a in MAX_SPARSE_CASES])
@@ -361,6 +365,48 @@ def test_max_backward_sparse_stores_keep_every_bit(gpu, shape, axis):
     assert_bitexact(got, ref, "MAX bwd")  # bits, so the sign of every zero too
     r3 = ref.reshape(-1)[::3]
     assert ((r3 == 0) & ~np.signbit(r3)).any(), "no -0 turned into +0: the case is not exercised"
+
+
+ROUTE_CASES = [((1024, 1024), 0), ((300, 256), 0), ((9000, 64), 0), ((3, 3000, 1024), 1), ((1 << 20,), None),
+               ((3, 12000), None), ((5, 70000), 1)]
+
+
+@pytest.mark.parametrize("shape,axis", ROUTE_CASES, ids=[f"{s}-ax{a}" for s, a in ROUTE_CASES])
+def test_max_backward_split_route_special_values(gpu, shape, axis):
+    """A MAX backward whose line maxima come from a split reduction reads x again only in the
+    splits whose partial maximum equals the line's. Lines here hold their maximum as +0 and -0
+    in far-apart splits (equal as floats: both route), -inf elements, only -inf (maximum
+    -FLT_MAX, count 0: nothing routes) and a maximum repeated across many splits; the
+    gradient holds -0 (turned into +0 in the splits that skip x too), +0 and NaN. Bit-exact
+    against the oracle; the forward maximum equal as floats (the sign of a maximum that is a
+    zero tie follows the order the maxima are combined in, the reference's SIMD lanes or the
+    GPU's splits: the routing is the same for either)."""
+    n = int(np.prod(shape))
+    ax = 0 if axis is None else axis
+    lead = () if axis is None else tuple(d for i, d in enumerate(shape) if i != ax)
+    B = n if axis is None else shape[ax]
+    L = synth.normal((n // B, B), 0, 1, 720)  # one line per row
+    L[0::4] = -np.abs(L[0::4]) - 1.0
+    L[0::4, 5::17] = -np.inf
+    L[0::4, B // 7] = 0.0
+    L[0::4, B - 3] = -0.0
+    if L.shape[0] > 1:
+        L[1::4] = -np.inf
+        L[2::4, ::97] = L[2::4].max(axis=1, keepdims=True) + np.float32(1.0)
+    if axis is None:
+        x = L.reshape(shape)
+    else:
+        x = np.ascontiguousarray(np.moveaxis(L.reshape(lead + (B,)), -1, ax))
+    red_shape = (1,) if axis is None else tuple(1 if i == ax else d for i, d in enumerate(shape))
+    ug = synth.normal(red_shape, 0, 1, 721)
+    g0 = synth.normal(shape, 0, 1, 722).reshape(-1)
+    g0[::3] = np.float32(-0.0)
+    g0[1::7] = np.float32(0.0)
+    g0[2::11] = np.float32(np.nan)
+    g0 = g0.reshape(shape)
+    np.testing.assert_array_equal(gpu.forward(OPS["MAX"], x, axis=axis), ORC.forward(OPS["MAX"], x, axis=axis))
+    got = gpu.backward(0, OPS["MAX"], ug, x, axis=axis, grad=g0)
+    assert_bitexact(got, ORC.backward(0, OPS["MAX"], ug, x, axis=axis, grad=g0), "MAX bwd")
 
 
 RANK8_A, RANK8_B = (2, 1, 3, 1, 2, 1, 2, 5), (1, 2, 1, 2, 1, 3, 1, 5)
