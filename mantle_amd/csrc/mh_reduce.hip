@@ -951,7 +951,8 @@ __global__ void __launch_bounds__(kRThreads)
     const uint32_t cv[4] = {c4.x, c4.y, c4.z, c4.w}, iv[4] = {i4.x, i4.y, i4.z, i4.w};
     // ARG: column j's single maximum in this split as an element offset from (row b0, column
     // c + j), a multiple of C (x has fewer than 2^32 elements); else 0xffffffff, which no
-    // row's offset r * C reaches
+    // row's offset r * C reaches (r * C < 2^32 with ARG; without it the 32-bit r * C may wrap,
+    // but stays a multiple of 4, as C is)
     const uint32_t eb = (uint32_t)(e0 + b0 * C);
     float add[4];
     uint32_t sel[4];
