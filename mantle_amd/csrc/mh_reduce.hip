@@ -302,6 +302,26 @@ __device__ __forceinline__ void part_store2(float* pm, int64_t npart, int64_t o,
     reinterpret_cast<uint32_t*>(pm + 2 * npart)[o] = v.i;
 }
 
+// RMaxCnt over lanes whose counts are below 16 (a first-level chunk: each lane combines at most
+// eight elements): the maximum by six float shuffles, the count as four ballots, one per count
+// bit, over the lanes at that maximum. The same count as wave_reduce<RMaxCnt> and a maximum
+// equal to its as a float (only the sign of a zero tie may differ), with half its shuffles:
+// the first pass of an all-element MAX backward took 49 us over 2^26 elements with the
+// pair-valued butterfly.
+__device__ __forceinline__ MC wave_reduce_mc_small(MC v) {
+    float m = v.m;
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1) {
+        const float o = __shfl_xor(m, k);
+        m = o > m ? o : m;
+    }
+    const uint32_t c = v.m == m ? v.c : 0u;
+    uint32_t tot = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) tot += (uint32_t)__popcll(__ballot((c >> b) & 1u)) << b;
+    return MC{m, tot};
+}
+
 template <class R>
 __device__ __forceinline__ typename R::T wave_reduce(typename R::T v) {
 #pragma unroll
@@ -736,7 +756,10 @@ __global__ void __launch_bounds__(kRThreads)
     } else {
         for (int64_t j = t; j < len; j += kRThreads) acc = R::comb(acc, ld.get(start + j));
     }
-    acc = wave_reduce<R>(acc);
+    if constexpr (std::is_same<R, RMaxCnt>::value && std::is_same<LD, LdPlain<RMaxCnt>>::value)
+        acc = wave_reduce_mc_small(acc);  // L <= kRowChunk: at most eight elements per lane
+    else
+        acc = wave_reduce<R>(acc);
     if (lane == 0) ws[w] = acc;
     __syncthreads();
     if (t == 0) {
