@@ -1146,16 +1146,27 @@ __global__ void __launch_bounds__(kRThreads)
     const double K = (double)kf;
     Mom m{0.0, 0.0};
     if (VEC) {
+        // four quads in flight; element j of every quad goes to accumulator chain j, and the
+        // chains are added in order (one chain had 16 dependent fp64 adds per pass of a
+        // 16384-element chunk: all-element tstd over 2^26 elements took 49.9 us)
         const int64_t nq = len >> 2;
         const float* xs = x + start;
-        for (int64_t q = t; q < nq; q += 2 * kRThreads) {
-            const vf4 a = ld_ntv(xs, q);
-            // a quad past the chunk holds K: x - K = 0 adds nothing to either moment
-            const vf4 b = q + kRThreads < nq ? ld_ntv(xs, q + kRThreads) : vf4{kf, kf, kf, kf};
+        Mom mc[4] = {Mom{0.0, 0.0}, Mom{0.0, 0.0}, Mom{0.0, 0.0}, Mom{0.0, 0.0}};
+        for (int64_t q = t; q < nq; q += 4 * kRThreads) {
+            vf4 v[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) mom_add(m, a[j], K);
+            for (int u = 0; u < 4; ++u)  // a quad past the chunk holds K: x - K = 0 adds nothing
+                v[u] = q + u * kRThreads < nq ? ld_ntv(xs, q + u * kRThreads) : vf4{kf, kf, kf, kf};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) mom_add(m, b[j], K);
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) mom_add(mc[j], v[u][j], K);
+        }
+        m = mc[0];
+#pragma unroll
+        for (int j = 1; j < 4; ++j) {
+            m.s1 = m.s1 + mc[j].s1;
+            m.s2 = m.s2 + mc[j].s2;
         }
     } else {
         for (int64_t j = t; j < len; j += kRThreads) mom_add(m, ld_nt(x + start + j), K);
@@ -1207,29 +1218,40 @@ __global__ void __launch_bounds__(kRThreads)
 #pragma unroll
         for (int j = 0; j < W; ++j) K[j] = (double)v0[j];
     }
-    Mom m[W];
+    // eight rows in flight; row u of each eight goes to accumulator chain u % 4 (the rest of the
+    // split to chain 0), and the chains are added in order at the end
+    constexpr int RU = 8, CH = 4;
+    Mom m[CH][W];
 #pragma unroll
-    for (int j = 0; j < W; ++j) m[j] = Mom{0.0, 0.0};
+    for (int h = 0; h < CH; ++h)
+#pragma unroll
+        for (int j = 0; j < W; ++j) m[h][j] = Mom{0.0, 0.0};
     int64_t b = b0;
-    for (; b + 3 < b1; b += 4) {
-        float v[4][W];
+    for (; b + RU - 1 < b1; b += RU) {
+        float v[RU][W];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) load(b + u, v[u]);
+        for (int u = 0; u < RU; ++u) load(b + u, v[u]);
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < RU; ++u)
 #pragma unroll
-            for (int j = 0; j < W; ++j) mom_add(m[j], v[u][j], K[j]);
+            for (int j = 0; j < W; ++j) mom_add(m[u % CH][j], v[u][j], K[j]);
     }
     for (; b < b1; ++b) {
         float v[W];
         load(b, v);
 #pragma unroll
-        for (int j = 0; j < W; ++j) mom_add(m[j], v[j], K[j]);
+        for (int j = 0; j < W; ++j) mom_add(m[0][j], v[j], K[j]);
     }
 #pragma unroll
     for (int j = 0; j < W; ++j) {
-        if (S == 1) res[o + j] = mom_std(m[j], B);
-        else part[s * AC + o + j] = m[j];
+        Mom t = m[0][j];
+#pragma unroll
+        for (int h = 1; h < CH; ++h) {
+            t.s1 = t.s1 + m[h][j].s1;
+            t.s2 = t.s2 + m[h][j].s2;
+        }
+        if (S == 1) res[o + j] = mom_std(t, B);
+        else part[s * AC + o + j] = t;
     }
 }
 
@@ -2104,15 +2126,17 @@ int mh_tstd(float* res, const float* x, const mh_shape* psx, int32_t axis) {
         if (S > 1) hipLaunchKernelGGL(k_tstd_mom_combine_rows, dim3((unsigned)A), b, 0, st, res, part, S, B);
         return finish("mh_tstd");
     }
-    // strided axis: a thread per column quad, about two blocks per CU, row splits of at least 32
-    // rows, 4 rows in flight (the fp64 accumulation runs best on these longer runs: 61.7 us at
-    // [8192, 8192] axis 0, 67.3 us with k_cols's 2 rows over 64-row splits)
+    // strided axis: a thread per column quad, about one block per CU, row splits of at least 64
+    // rows, eight rows in flight over four accumulator chains. Fewer, longer splits write and
+    // combine fewer fp64 partials: at [8192, 8192] axis 0 (a probe, moments + combine) 32 splits
+    // took 48.1 us against 52.6 us with 64 splits of four rows in flight, one chain; 128 and
+    // 256 splits took 57-60 us.
     const bool vec = al16(x) && C % 4 == 0;
     const int64_t W = vec ? 4 : 1;
     const int64_t items = A * C / W;
     const int64_t bx = (items + kRThreads - 1) / kRThreads;
-    int64_t S = (2 * (int64_t)ctx().num_cus + bx - 1) / bx;
-    int64_t maxS = B / 32;
+    int64_t S = ((int64_t)ctx().num_cus + bx - 1) / bx;
+    int64_t maxS = B / 64;
     if (maxS < 1) maxS = 1;
     if (S > maxS) S = maxS;
     if (S > 65535) S = 65535;
