@@ -942,11 +942,12 @@ __device__ __forceinline__ void route_quad_x(PendingStores& pd, float* gr, int64
     route_quad(pd, gr, q, g, hit, add);
 }
 
-// Columns (C % 4 == 0, 16-byte aligned grad and x): a thread per (column quad o, split s),
-// the layout of the reduction's column launchers; two rows in flight. SPLIT_X: splits on grid
-// x, column-quad blocks on grid y. ARG: pc / pi hold the splits' counts and indices. The
-// partials, m and f are 16-byte aligned scratch: one quad load each.
-template <bool SPLIT_X, bool ARG>
+// Columns (C % 4 == 0, 16-byte aligned grad and x, fewer than 2^32 elements): a thread per
+// (column quad o, split s), the layout of the reduction's column launchers; two rows in
+// flight. SPLIT_X: splits on grid x, column-quad blocks on grid y. pm / pc / pi hold the
+// splits' maxima, counts and indices (RMaxCntArg); they, m and f are 16-byte aligned scratch:
+// one quad load each.
+template <bool SPLIT_X>
 __global__ void __launch_bounds__(kRThreads)
     k_max_route_cols(float* __restrict__ grad, const float* __restrict__ x, const float* __restrict__ m,
                      const float* __restrict__ f, const float* __restrict__ ug, const float* __restrict__ pm,
@@ -962,20 +963,15 @@ __global__ void __launch_bounds__(kRThreads)
     const int64_t k = s * AC + o;      // this split's partials of columns o .. o + 3
     const float4 m4 = *reinterpret_cast<const float4*>(m + o), f4 = *reinterpret_cast<const float4*>(f + o);
     const float4 p4 = *reinterpret_cast<const float4*>(pm + k);
-    uint4 c4 = make_uint4(0u, 0u, 0u, 0u), i4 = make_uint4(0u, 0u, 0u, 0u);
-    if (ARG) {
-        c4 = *reinterpret_cast<const uint4*>(pc + k);
-        i4 = *reinterpret_cast<const uint4*>(pi + k);
-    }
+    const uint4 c4 = *reinterpret_cast<const uint4*>(pc + k), i4 = *reinterpret_cast<const uint4*>(pi + k);
     const float u[4] = {ug[o], ug[o + 1], ug[o + 2], ug[o + 3]};
     const float mv[4] = {m4.x, m4.y, m4.z, m4.w};
     const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
     const float fv[4] = {f4.x, f4.y, f4.z, f4.w};
     const uint32_t cv[4] = {c4.x, c4.y, c4.z, c4.w}, iv[4] = {i4.x, i4.y, i4.z, i4.w};
-    // ARG: column j's single maximum in this split as an element offset from (row b0, column
-    // c + j), a multiple of C (x has fewer than 2^32 elements); else 0xffffffff, which no
-    // row's offset r * C reaches (r * C < 2^32 with ARG; without it the 32-bit r * C may wrap,
-    // but stays a multiple of 4, as C is)
+    // column j's single maximum in this split as an element offset from (row b0, column c + j),
+    // a multiple of C (x has fewer than 2^32 elements); else 0xffffffff, which no row's offset
+    // r * C < 2^32 reaches
     const uint32_t eb = (uint32_t)(e0 + b0 * C);
     float add[4];
     uint32_t sel[4];
@@ -984,13 +980,8 @@ __global__ void __launch_bounds__(kRThreads)
     for (int j = 0; j < 4; ++j) {
         add[j] = fv[j] * u[j];
         const bool nj = pv[j] == mv[j];
-        if (ARG) {
-            xread = xread || (nj && cv[j] >= 2u);
-            sel[j] = nj && cv[j] == 1u ? iv[j] - (eb + (uint32_t)j) : 0xffffffffu;
-        } else {
-            xread = xread || nj;
-            sel[j] = 0xffffffffu;
-        }
+        xread = xread || (nj && cv[j] >= 2u);
+        sel[j] = nj && cv[j] == 1u ? iv[j] - (eb + (uint32_t)j) : 0xffffffffu;
     }
     const int64_t q0 = (e0 >> 2) + b0 * (C >> 2), qs = C >> 2;  // quad of row b0 + r: q0 + r * qs
     const int nr = (int)(b1 - b0);
@@ -2157,8 +2148,8 @@ int mh_tstd(float* res, const float* x, const mh_shape* psx, int32_t axis) {
 }  // extern "C"
 
 // The routing pass of a MAX backward whose reduction left split partials (k_max_route_*;
-// arg: RED_MAXCNT_ARG partials): false where their layout does not fit those kernels (the
-// caller routes every element).
+// arg: RED_MAXCNT_ARG partials, which the column route needs): false where their layout does
+// not fit those kernels (the caller routes every element).
 static bool max_route_split(float* grad, const float* x, int64_t A, int64_t B, int64_t C, const float* m,
                             const float* f, const float* ug, float* tmp, const RedSplit& sp, bool arg) {
     if (sp.S <= 1 || !al16(x) || !al16(grad)) return false;
@@ -2170,7 +2161,7 @@ static bool max_route_split(float* grad, const float* x, int64_t A, int64_t B, i
                            sp.S, B);
         return true;
     }
-    if (C % 4 != 0 || sp.S > 65535) return false;
+    if (!arg || C % 4 != 0 || sp.S > 65535) return false;
     const int64_t np = sp.S * A * C;
     const uint32_t* pc = reinterpret_cast<const uint32_t*>(tmp + np);
     const uint32_t* pi = reinterpret_cast<const uint32_t*>(tmp + 2 * np);
@@ -2178,16 +2169,10 @@ static bool max_route_split(float* grad, const float* x, int64_t A, int64_t B, i
     const bool sx = qb <= 65535;
     if (!sx && qb > 0x7fffffff) return false;
     const dim3 g = sx ? dim3((unsigned)sp.S, (unsigned)qb) : dim3((unsigned)qb, (unsigned)sp.S), b(kRThreads);
-#define MH_RC(SX, AR) \
-    hipLaunchKernelGGL((k_max_route_cols<SX, AR>), g, b, 0, st, grad, x, m, f, ug, tmp, pc, pi, A, B, C, sp.span)
-    if (sx) {
-        if (arg) MH_RC(true, true);
-        else MH_RC(true, false);
-    } else {
-        if (arg) MH_RC(false, true);
-        else MH_RC(false, false);
-    }
-#undef MH_RC
+    if (sx)
+        hipLaunchKernelGGL(k_max_route_cols<true>, g, b, 0, st, grad, x, m, f, ug, tmp, pc, pi, A, B, C, sp.span);
+    else
+        hipLaunchKernelGGL(k_max_route_cols<false>, g, b, 0, st, grad, x, m, f, ug, tmp, pc, pi, A, B, C, sp.span);
     return true;
 }
 

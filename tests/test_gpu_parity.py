@@ -376,7 +376,9 @@ def test_max_backward_split_route_special_values(gpu, shape, axis):
     """A MAX backward whose line maxima come from a split reduction reads x again only in the
     splits whose partial maximum equals the line's. Lines here hold their maximum as +0 and -0
     in far-apart splits (equal as floats: both route), -inf elements, only -inf (maximum
-    -FLT_MAX, count 0: nothing routes) and a maximum repeated across many splits; the
+    -FLT_MAX, count 0: nothing routes), a maximum repeated across many splits (one per split:
+    routed at the split's recorded index) and one on every third row (several per split:
+    routed by comparing x); the
     gradient holds -0 (turned into +0 in the splits that skip x too), +0 and NaN. Bit-exact
     against the oracle; the forward maximum equal as floats (the sign of a maximum that is a
     zero tie follows the order the maxima are combined in, the reference's SIMD lanes or the
@@ -393,6 +395,8 @@ def test_max_backward_split_route_special_values(gpu, shape, axis):
     if L.shape[0] > 1:
         L[1::4] = -np.inf
         L[2::4, ::97] = L[2::4].max(axis=1, keepdims=True) + np.float32(1.0)
+        # the maximum on every third row: several in every split, whose routing reads x
+        L[3::4, ::3] = L[3::4].max(axis=1, keepdims=True) + np.float32(1.0)
     if axis is None:
         x = L.reshape(shape)
     else:
