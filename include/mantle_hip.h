@@ -388,7 +388,7 @@ int mh_adam_step(float* param, const float* grad, float* m, float* v, int64_t n,
                  float beta2, float eps, int64_t iter);
 
 /* Adam.step over every trainable parameter of a model (the parallelize over parameters,
- * optim.mojo:140): arrays of ntensors device pointers and sizes, one launch per 64 tensors.
+ * optim.mojo:140): arrays of ntensors device pointers and sizes, one launch per 80 tensors.
  * Same arithmetic as mh_adam_step. */
 int mh_adam_step_multi(int64_t ntensors, float* const* params, const float* const* grads, float* const* m,
                        float* const* v, const int64_t* sizes, float lr, float beta1, float beta2, float eps,

@@ -10,10 +10,10 @@
 // 28 bytes per element: p, g, m, v read; p, m, v written.
 //
 // mh_adam_step updates one tensor; mh_adam_step_multi updates every parameter of a model
-// with one launch per 64 tensors (the reference parallelises over parameters,
+// with one launch per 80 tensors (the reference parallelises over parameters,
 // optim.mojo:140): threads walk the concatenated element quads of the launch's tensors and
 // find their tensor by a wave-uniform binary search in a table passed by value, so a model of
-// many small tensors costs a launch per 64 tensors, not one per tensor.
+// many small tensors costs a launch per 80 tensors, not one per tensor.
 #include <cmath>
 
 #include "mh_internal.h"
@@ -141,19 +141,25 @@ __global__ void __launch_bounds__(kOThreads)
     }
 }
 
+// 48 bytes: the first unit of the tensor in the launch's concatenated unit space is a multiple
+// of 64 (each tensor starts on a wave), so its low six bits carry the unit map: bits 0-1 sh,
+// bit 2 vec.
 struct AdamTensor {
     float* p;
     const float* g;
     float* m;
     float* v;
     int64_t n;
-    int64_t unit0;  // first unit of this tensor in the launch's concatenated unit space
-    UnitMap um;
+    int64_t u0m;
+    __host__ __device__ int64_t unit0() const { return u0m & ~int64_t(63); }
+    __host__ __device__ UnitMap um() const { return UnitMap{(int)(u0m & 3), (int)((u0m >> 2) & 1)}; }
 };
+static_assert(sizeof(AdamTensor) == 48, "table entry size");
 
-// Up to kAdamPerLaunch tensors travel by value in the kernel arguments (3 KB), so a launch
-// needs no device-side table.
-constexpr int kAdamPerLaunch = 64;
+// Up to kAdamPerLaunch tensors travel by value in the kernel arguments (3.8 KB of the 4 KB
+// they may take), so a launch needs no device-side table. (With 56-byte entries and 64 per
+// launch, 400 tensors of 1..2^18 elements took seven launches instead of five.)
+constexpr int kAdamPerLaunch = 80;
 struct AdamTable {
     AdamTensor t[kAdamPerLaunch];
     int32_t nt;
@@ -170,12 +176,13 @@ __global__ void __launch_bounds__(kOThreads) k_adam_multi(AdamTable tab, int64_t
         int lo = 0, hi = tab.nt - 1;  // the last tensor whose unit0 <= uw
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (tab.t[mid].unit0 <= uw) lo = mid;
+            if (tab.t[mid].unit0() <= uw) lo = mid;
             else hi = mid - 1;
         }
         const AdamTensor& t = tab.t[lo];
-        const int64_t k = uw - t.unit0 + lane;
-        if (k < adam_units(t.n, t.um.sh)) adam_unit_k(t.p, t.g, t.m, t.v, t.n, k, t.um, s);
+        const UnitMap um = t.um();
+        const int64_t k = uw - t.unit0() + lane;
+        if (k < adam_units(t.n, um.sh)) adam_unit_k(t.p, t.g, t.m, t.v, t.n, k, um, s);
     }
 }
 
@@ -246,9 +253,9 @@ int mh_adam_step_multi(int64_t ntensors, float* const* params, const float* cons
             t.m = m[i];
             t.v = v[i];
             t.n = sizes[i];
-            t.unit0 = units;
-            t.um = unit_map(t.p, t.g, t.m, t.v);
-            units += (adam_units(t.n, t.um.sh) + 63) & ~int64_t(63);  // next tensor starts on a wave
+            const UnitMap um = unit_map(t.p, t.g, t.m, t.v);
+            t.u0m = units | um.sh | (um.vec << 2);  // units: a multiple of 64
+            units += (adam_units(t.n, um.sh) + 63) & ~int64_t(63);  // next tensor starts on a wave
         }
         if (tab.nt > 0)
             hipLaunchKernelGGL(k_adam_multi, dim3(grid_units(units)), dim3(kOThreads), 0, ctx().stream, tab, units, s);

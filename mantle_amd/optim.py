@@ -4,7 +4,7 @@
 trainable parameters, get_trainable_parameters, optim.mojo:27-44) or (param, grad) ``Tensor``
 pairs, and keeps
 the momentum and rms tensors, zero-initialised, beside them. ``step()`` increments ``iter``
-and updates every parameter with one ``mh_adam_step_multi`` launch per 64 tensors;
+and updates every parameter with one ``mh_adam_step_multi`` launch per 80 tensors;
 ``zero_grad()`` zeroes the gradients (``Collection.set_zero``, collection.mojo:221-224).
 """
 from __future__ import annotations

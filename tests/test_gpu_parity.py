@@ -856,10 +856,10 @@ def test_adam_step_single(gpu, n):
 
 
 def test_adam_step_multi_and_optimizer(gpu):
-    """70 tensors (two launches of the 64-tensor table), sizes 0..5000 with ragged tails and one
+    """90 tensors (two launches of the 80-tensor table), sizes 0..5000 with ragged tails and one
     unaligned view, through mantle_amd.Adam (step counts iter, zero_grad clears)."""
     m = gpu.m
-    sizes = [0, 1, 2, 3, 4, 5, 7, 8, 33, 64, 100, 257, 1000, 4099, 5000] + [int(s) for s in synth.integers((55,), 1, 3000, 75)]
+    sizes = [0, 1, 2, 3, 4, 5, 7, 8, 33, 64, 100, 257, 1000, 4099, 5000] + [int(s) for s in synth.integers((75,), 1, 3000, 75)]
     params, grads, ps, owners = [], [], [], []
     for i, n in enumerate(sizes):
         p = synth.normal((max(n, 1),), 0, 1, 100 + i)[:n] if n else np.zeros(0, np.float32)
