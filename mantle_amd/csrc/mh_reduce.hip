@@ -2,20 +2,25 @@
 // backward tie routing and the POW exponent gradient.
 //
 // Every reduction is expressed on a view [A, B, C] reduced over B:
-//   C == 1, B <= 32 : 256 rows staged in LDS by coalesced float4 loads, one thread per
-//                     row (unaligned x: one thread per row straight from memory);
+//   C == 1, B <= 32 : 64 rows (a one-wavefront block) staged in LDS by coalesced float4
+//                     loads, one thread per row (unaligned x: one thread per row straight
+//                     from memory);
 //   C == 1, B < 2048: one wavefront (64 lanes) per row, 128-bit loads, butterfly shuffle;
 //   C == 1, B >= 2048: 2048-element chunks, one 4-wave block each (two quads per thread),
 //                     whose partials reduce again along the row the same way;
-//   C  > 1, C % 4 == 0 and >= 1024 columns: one thread per column quad, 128-row chunks;
-//   C  > 1, C % 4 == 0 and >= 128 columns: a block per (strip of 64 column quads, chunk of
-//                     rows), its four waves interleaving the rows, combined through LDS (also
-//                     the combine pass of the wide form);
+//   C  > 1, C % 4 == 0 and >= 1024 columns: one thread per column quad over a split of the
+//                     rows (about four blocks per CU; splits on grid x), the split partials
+//                     combined in one short launch (k_parts_comb);
+//   C  > 1, C % 4 == 0 and >= 128 columns: a block per (strip of 64 column quads, split of
+//                     rows), its four waves interleaving the rows, combined through LDS;
 //   C  > 1 otherwise  : one thread per output column (a quad of columns when C % 4 == 0);
-//   in both column forms the rows split across blocks when that is needed to fill the chip,
+//   in every column form the rows split across blocks when that is needed to fill the chip,
 //   and a second pass combines the split partials in fixed split order.
 // No atomics: each output's summation order is fixed by the launch shape, so a call repeated
 // on the same input returns the same bits.
+// MAX backward over axis 0 and all elements routes from the split partials its max-count
+// reduction leaves (k_max_route_*): x is read again only where a split holds a line maximum
+// it cannot place by its recorded index.
 #include <cfloat>
 #include <type_traits>
 
