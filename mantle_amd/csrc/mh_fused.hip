@@ -5,11 +5,14 @@
 // Forward: one pass reads x (and the small bias) and writes y = x + bias and r = relu(y):
 // 12 B per element instead of the 16 B of two separate ops.
 // Backward: with x viewed as [N, C, S] and the bias indexed by C alone (NCHW bias
-// [1, C, 1, 1], or any bias that is constant over a contiguous inner run S), one wavefront
-// per (plane, chunk) computes gy = g_y + relu'(y) * ug, accumulates it into grad_x (and g_y
-// when the caller keeps it), and writes the chunk's sum of gy; the last wave of each channel
-// adds that channel's partials into grad_bias in a fixed order, in the same launch. Shapes
-// outside that form run the op-by-op kernels.
+// [1, C, 1, 1], or any bias that is constant over a contiguous inner run S), every quad
+// computes gy = g_y + relu'(y) * ug and accumulates it into grad_x (and g_y when the caller
+// keeps it); grad_bias takes the per-channel sum of gy in a fixed order. Planes of at least
+// kBFlat quads run as one flat stream whose waves write their planes' partial sums, added per
+// channel by a short second launch (k_bias_relu_bwd_flat, k_bias_partials_comb); shorter
+// planes run a wavefront per (plane group, chunk), whose last arrival per channel adds the
+// channel's partials in the same launch (k_bias_relu_bwd_planes). Shapes outside that form run
+// the op-by-op kernels.
 #include "mh_internal.h"
 #include "mh_math.h"
 
