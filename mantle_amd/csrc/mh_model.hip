@@ -10,9 +10,16 @@
 // under MH_INIT_ASYNC). Inputs enter by copy into their slots, as Collection.__setitem__
 // does (collection.mojo:202-209); everything else stays on the device.
 //
-// Optional fusion (MH_MODEL_FUSE_BIAS_RELU): an ADD whose output feeds only the RELU node
-// right after it runs as the fused bias + RELU kernels. Every tensor and gradient slot holds
-// what the op-by-op execution writes there, so the fusion is not observable in results.
+// Optional fusion: an ADD whose output feeds only the RELU node right after it runs as the
+// fused bias + RELU kernels (MH_MODEL_FUSE_BIAS_RELU), and the node runs of nn.Softmax,
+// nn.LogSoftmax, CrossEntropyLoss and the Softmax -> LOG -> MUL -> MEAN head run as the
+// row-fused kernels (MH_MODEL_FUSE_ROWS). Every tensor and gradient slot holds what the
+// op-by-op execution writes there, so the fusion is not observable in results.
+// mh_model_capture records a pass (forward, backward, or zero_grad + forward + backward) as
+// one HIP graph that mh_model_replay launches. While a captured graph exists, a library
+// buffer that grows is retired rather than freed, so the addresses the graph holds stay
+// valid until the graph is released or the library shuts down (a replay after mh_shutdown is
+// refused).
 #include <new>
 #include <vector>
 
