@@ -52,6 +52,42 @@ BIN_SHAPES = [((37, 63, 107), (37, 63, 107)), ((37, 63, 107), (37, 63, 1)), ((37
               ((65, 4), (65, 1)), ((1001, 5), (1001, 1)), ((6, 2, 13), (6, 2, 1))]
 
 
+def _dim(rng, big):
+    """A dimension: often tiny (1-9, where the short-row and LDS forms apply), else 10-300 or,
+    for one axis of a case, up to `big` (row chunks, wide and strip column splits)."""
+    u = rng.random()
+    if u < 0.35:
+        return int(rng.integers(1, 10))
+    if u < 0.8:
+        return int(rng.integers(10, 301))
+    return int(rng.integers(301, big + 1))
+
+
+def _seeded_bin_shapes(count, seed):
+    """Broadcast pairs drawn with a fixed seed: an output of rank 1-5 and up to 2^18 elements,
+    each operand a copy with some axes set to 1 and, sometimes, leading axes dropped."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        r = int(rng.integers(1, 6))
+        shape = [_dim(rng, 3000) for _ in range(r)]
+        if int(np.prod(shape)) > (1 << 18):
+            continue
+        ops = []
+        for _ in range(2):
+            sh = [d if rng.random() < 0.6 else 1 for d in shape]
+            drop = int(rng.integers(0, r)) if rng.random() < 0.3 else 0
+            ops.append(tuple(sh[drop:]) or (1,))
+        if tuple(np.broadcast_shapes(*ops)) != tuple(shape) and rng.random() < 0.5:
+            continue  # keep most pairs at the full output shape
+        out.append((ops[0], ops[1]))
+    return out
+
+
+# seeded shapes beside the chosen ones: launch forms in combinations nobody picked by hand
+BIN_SHAPES += _seeded_bin_shapes(20, 20261202)
+
+
 def _binary_inputs(sa, sb, seed):
     a = synth.uniform(sa, -1, 1, seed)
     b = synth.uniform(sb, 0.5, 2, seed + 1)
@@ -308,6 +344,30 @@ RED_CASES = [((87, 73, 107), 0), ((87, 73, 107), 1), ((87, 73, 107), 2), ((87, 7
              # chunk-partial combines of 16386 (odd quads: the scalar pass) and 20000 partials, and
              # a wide column split whose last partial group is short
              ((2048 * 16385 + 4,), None), ((2048 * 20000,), None), ((3, 3000, 1024), 1)]
+
+
+def _seeded_red_cases(count, seed):
+    """Reduction cases drawn with a fixed seed: rank 1-4, up to 1.5 M elements, every axis and
+    all elements; a third of them strided over rows of 128-4096 columns in quads (the wide,
+    strip and per-quad column forms with their row splits)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        if len(out) % 3 == 2:
+            r = int(rng.integers(2, 4))
+            shape = tuple(_dim(rng, 600) for _ in range(r - 1)) + (4 * int(rng.integers(32, 1025)),)
+            axis = int(rng.integers(0, r - 1))
+        else:
+            r = int(rng.integers(1, 5))
+            shape = tuple(_dim(rng, 40000) for _ in range(r))
+            axis = int(rng.integers(-1, r))
+        if int(np.prod(shape)) > 1_500_000 or int(np.prod(shape)) < 2:
+            continue
+        out.append((shape, None if axis < 0 else axis))
+    return out
+
+
+RED_CASES += _seeded_red_cases(30, 20261203)
 
 
 @pytest.mark.parametrize("shape,axis", RED_CASES, ids=[f"{s}-ax{a}" for s, a in RED_CASES])
@@ -776,6 +836,23 @@ ROW_CASES = [(300, 1), (7, 2), (257, 3), (100, 10), (33, 31), (65, 32), (40, 33)
              (11, 66), (8, 100), (6, 128), (5, 130), (4, 257), (3, 1000), (2, 1024), (3, 1025), (2, 2044),
              (2, 2047), (1000, 10), (2000, 20), (1500, 48), (777, 47), (1200, 64)] + \
             [(259 + k, k) for k in (4, 5, 6, 7, 8, 9, 11, 12, 13, 14, 15, 16)]
+
+
+def _seeded_row_cases(count, seed):
+    """(rows, classes) drawn with a fixed seed over every row engine: 1-16 classes (the
+    pipelined kernels), 17-64 (the thread and multi-lane engines, quad rows or not) and
+    65-2047 (a wavefront per row), up to 600 K elements."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        lo, hi = [(1, 17), (17, 65), (65, 2048)][i % 3]
+        k = int(rng.integers(lo, hi))
+        rows = int(rng.integers(1, max(2, min(3000, 600_000 // k))))
+        out.append((rows, k))
+    return out
+
+
+ROW_CASES += _seeded_row_cases(12, 20261204)
 
 
 @pytest.mark.parametrize("rows,classes", ROW_CASES, ids=[f"{r}x{c}" for r, c in ROW_CASES])
