@@ -57,14 +57,19 @@ struct MC {
     float m;
     uint32_t c;
 };
-struct RMaxCnt {  // (line max, number of elements equal to it)
+// (line max, number of elements equal to it), from -FLT_MAX with count 0 (basics.mojo:551-577,
+// 597-613: c = #(x == m)). A NaN element is neither the maximum nor counted: the running
+// value never becomes NaN, so exactly one side of a combine can be NaN, and the other side is
+// kept. Every order of combining then gives the same maximum (as a float) and count.
+struct RMaxCnt {
     using T = MC;
     __device__ static T init() { return MC{-FLT_MAX, 0u}; }
     __device__ static T lift(float x) { return MC{x, 1u}; }
     __device__ static T comb(T a, T b) {
         if (a.m > b.m) return a;
         if (b.m > a.m) return b;
-        return MC{a.m, a.c + b.c};
+        if (a.m == b.m) return MC{a.m, a.c + b.c};
+        return a.m != a.m ? b : a;  // one side is a NaN element
     }
     __device__ static T shfl(T v, int m) {
         return MC{__shfl_xor(v.m, m), (uint32_t)__shfl_xor((int)v.c, m)};
@@ -86,7 +91,8 @@ struct RMaxCntArg {
     __device__ static T comb(T a, T b) {
         if (a.m > b.m) return a;
         if (b.m > a.m) return b;
-        return MCI{a.m, a.c + b.c, a.i < b.i ? a.i : b.i};
+        if (a.m == b.m) return MCI{a.m, a.c + b.c, a.i < b.i ? a.i : b.i};
+        return a.m != a.m ? b : a;  // one side is a NaN element
     }
     __device__ static T shfl(T v, int m) {
         return MCI{__shfl_xor(v.m, m), (uint32_t)__shfl_xor((int)v.c, m), (uint32_t)__shfl_xor((int)v.i, m)};

@@ -296,7 +296,7 @@ __global__ void __launch_bounds__(kSThreads)
                 } else if (v > mb) {
                     mb = v;
                     cntm = 1;
-                } else {
+                } else if (v == mb) {  // a NaN element is not counted
                     cntm += 1;
                 }
             }
@@ -592,7 +592,7 @@ __global__ void __launch_bounds__(kSThreads)
                     } else if (v > mb) {
                         mb = v;
                         cntm = 1;
-                    } else {
+                    } else if (v == mb) {  // a NaN element is not counted
                         cntm += 1;
                     }
                 }
@@ -833,7 +833,7 @@ __global__ void __launch_bounds__(kSThreads)
             } else if (v > mb) {
                 mb = v;
                 cntm = 1;
-            } else {
+            } else if (v == mb) {  // a NaN element is not counted
                 cntm += 1;
             }
         }
@@ -1111,7 +1111,7 @@ __global__ void __launch_bounds__(kSThreads)
                 } else if (v > a.m) {
                     a.m = v;
                     a.c = 1;
-                } else {
+                } else if (v == a.m) {  // a NaN element is not counted
                     a.c += 1;
                 }
             }

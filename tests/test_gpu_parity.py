@@ -473,6 +473,51 @@ def test_max_backward_split_route_special_values(gpu, shape, axis):
     assert_bitexact(got, ORC.backward(0, OPS["MAX"], ug, x, axis=axis, grad=g0), "MAX bwd")
 
 
+NAN_MAX_CASES = [((64, 10), 1), ((70, 33), 1), ((64, 1000), 1), ((3, 40000), 1), ((1 << 16,), None),
+                 ((1024, 1024), 0), ((300, 256), 0), ((9000, 64), 0), ((70, 3), 0), ((5, 6, 7), 1)]
+
+
+@pytest.mark.parametrize("shape,axis", NAN_MAX_CASES, ids=[f"{s}-ax{a}" for s, a in NAN_MAX_CASES])
+def test_max_backward_nan_elements_are_not_counted(gpu, shape, axis):
+    """MAX backward over lines holding NaN elements: the line maximum is the largest non-NaN
+    element (-FLT_MAX when there is none), the count the elements equal to it (c = #(x == m),
+    basics.mojo:551-577, 597-613; NaN equals nothing), so grad + (x == m ? fl(1/c) * ug : +0)
+    follows in float32. The reference's own maximum depends on where a NaN meets its SIMD
+    lanes (outside parity), so this pins the GPU's defined behaviour on every routing path:
+    short rows, register rows, row chunks, all elements, and the wide, strip, per-quad and
+    generic column forms."""
+    n = int(np.prod(shape))
+    ax = 0 if axis is None else axis
+    B = n if axis is None else shape[ax]
+    lead = () if axis is None else tuple(d for i, d in enumerate(shape) if i != ax)
+    L = synth.normal((n // B, B), 0, 1, 730)  # one line per row
+    L[:, 1::5] = np.nan
+    L[0::3] = np.where(np.arange(B) % 2 == 0, np.float32(np.nan), L[0::3])  # NaN-heavy lines
+    if L.shape[0] > 2:
+        L[2] = np.nan  # a line of NaN only: maximum -FLT_MAX, count 0, nothing routes
+    if axis is None:
+        x = L.reshape(shape)
+    else:
+        x = np.ascontiguousarray(np.moveaxis(L.reshape(lead + (B,)), -1, ax))
+    red_shape = (1,) if axis is None else tuple(1 if i == ax else d for i, d in enumerate(shape))
+    ug = synth.normal(red_shape, 0, 1, 731)
+    g0 = synth.normal(shape, 0, 1, 732)
+    got = gpu.backward(0, OPS["MAX"], ug, x, axis=axis, grad=g0)
+    # the expected gradient, line by line in float32
+    fmax = np.float32(np.finfo(np.float32).max)
+    m = np.maximum(np.where(np.isnan(L), -np.inf, L).max(axis=1), -fmax).astype(np.float32)
+    eq = L == m[:, None]
+    c = eq.sum(axis=1).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        f = (np.float32(1.0) / c).astype(np.float32)
+    U = ug.reshape(-1) if axis is None else np.moveaxis(ug, ax, -1).reshape(-1)
+    G = g0.reshape(1, -1) if axis is None else np.moveaxis(g0, ax, -1).reshape(-1, B)
+    add = (f * U).astype(np.float32)
+    E = (G + np.where(eq, add[:, None], np.float32(0.0))).astype(np.float32)
+    exp = E.reshape(shape) if axis is None else np.moveaxis(E.reshape(lead + (B,)), -1, ax)
+    assert_bitexact(got, np.ascontiguousarray(exp), "MAX bwd with NaN elements")
+
+
 RANK8_A, RANK8_B = (2, 1, 3, 1, 2, 1, 2, 5), (1, 2, 1, 2, 1, 3, 1, 5)
 
 
