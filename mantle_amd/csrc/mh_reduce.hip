@@ -636,7 +636,7 @@ __global__ void __launch_bounds__(kRThreads)
 
 // A pass over chunk partials (a row of at most kCombineMax elements per block, one block per
 // row): 1024 threads, each with all of its (up to eight) quads' loads in flight, so the row
-// takes one memory round trip; the sixteen wave results combine in wave order.
+// takes one memory round trip; the sixteen wave results combine by a fixed butterfly.
 constexpr int kCombThreads = 1024;
 template <class R, class LD, bool VEC>
 __global__ void __launch_bounds__(kCombThreads)
@@ -668,10 +668,13 @@ __global__ void __launch_bounds__(kCombThreads)
     acc = wave_reduce<R>(acc);
     if (lane == 0) ws[w] = acc;
     __syncthreads();
-    if (t == 0) {
-        T tot = ws[0];
-        for (int k = 1; k < kCombThreads / 64; ++k) tot = R::comb(tot, ws[k]);
-        epi_store(out, out2, r, tot, epi, div);
+    if (w == 0) {  // the sixteen wave results by a butterfly within lanes 0-15 (a serial fold of
+                   // max-count pairs took 2 us more)
+        static_assert(kCombThreads / 64 == 16, "sixteen waves");
+        T v = lane < 16 ? ws[lane] : R::init();
+#pragma unroll
+        for (int m = 8; m >= 1; m >>= 1) v = R::comb(v, R::shfl(v, m));
+        if (lane == 0) epi_store(out, out2, r, v, epi, div);
     }
 }
 
