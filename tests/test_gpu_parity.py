@@ -283,12 +283,15 @@ def test_pow_parity(gpu, e):
     assert_sum_close(got, ref, np.array([terms.sum()]), f"pow bwd exponent {e}", terms_abs=np.array([np.abs(terms).sum()]))
 
 
-@pytest.mark.parametrize("n", [1, 3, 4, 63, 64, 65, 2047, 2048, 2052, 4099, (1 << 18) + 4, (1 << 20) + 3])
+@pytest.mark.parametrize("n", [1, 3, 4, 63, 64, 65, 2047, 2048, 2052, 4099, (1 << 18) + 4, (1 << 20) + 3,
+                               (1 << 23) + 20])
 def test_pow_bwd_both_operands_fused(gpu, n):
     """mh_pow_bwd_accum2 (x's and the exponent's gradient in one pass) against the two
     mh_pow_bwd_accum calls bit for bit: the x gradient element by element, the exponent gradient
     through the same reduction kernels in the same order (every reduction shape the length
-    selects: LDS rows, one wavefront, block chunks with a combine). Bases include values where
+    selects: LDS rows, one wavefront, block chunks with a combine, and for aligned lengths of
+    2^16 whole quads or more the grid-stride kernel, one and several quads per thread with a
+    ragged last pass). Bases include values where
     x + 1e-12 is not x (0, 1e-13, a subnormal), a negative base, NaN and inf; exponents integral
     and fractional; x, ug and the gradients also as unaligned views. The x gradient also matches
     the oracle bit for bit and the exponent gradient the oracle's in the sum class."""
