@@ -334,6 +334,61 @@ def test_pow_bwd_both_operands_fused(gpu, n):
     assert_bitexact(fx.to_numpy(), sx.to_numpy(), "x grad alone")
 
 
+def _pow_band_edge_bases(e):
+    """Positive bases whose x^(e-1) or x^e lies at the edges of [FLT_MIN, 2e38] (the band in
+    which the one-pass POW backward takes x^e as x * (x + 1e-12)^(e-1) and that power's exp
+    without its clamp), near exp's clamp (e^+-88.376, about 2.4e38 and 4.2e-39) and beyond
+    it, each with its two float neighbours."""
+    a = np.float64(np.float32(e))
+    out = []
+    for target in (5e-39, 1.0e-38, 1.1754944e-38, 1.3e-38, 1.0e38, 1.99e38, 2.0e38, 2.01e38, 2.3e38, 2.45e38,
+                   3.3e38):
+        for y in (a - 1.0, a):
+            r = target ** (1.0 / y)
+            if 1e-37 < r < 3e38:  # a normal float base
+                v = np.float32(r)
+                out += [v, np.nextafter(v, np.float32(np.inf)), np.nextafter(v, np.float32(0))]
+    return np.array(out, np.float32)
+
+
+@pytest.mark.parametrize("e", [2.37, 1.5, -1.5, 3.9])
+def test_pow_bwd_band_edges(gpu, e):
+    """The one-pass POW backward (mh_pow_bwd_accum2, the one-wavefront kernel at 2^18
+    elements) at the edges of its shared-power band: the x gradient holds the oracle's bits at
+    every edge base (the unclamped exp is used only where its bits are exp's), and each base's
+    exponent-gradient term, alone in its call (a one-hot upstream gradient, every other base
+    1.0), is in the sum class against the oracle and bit-identical to the exponent-only call."""
+    m = gpu.m
+    pw = OPS["POW"]
+    n = 1 << 18
+    bases = _pow_band_edge_bases(e)
+    t2 = np.array([e], np.float32)
+    x = np.ones(n, np.float32)
+    x[:bases.size] = bases
+    ug = synth.normal((n,), 0, 1, 1400)
+    g0 = synth.normal((n,), 0, 1, 1401)
+    fx, fe = gpu.T(g0), gpu.T(np.zeros(1, np.float32))
+    m.backward_op_both(pw, gpu.T(ug), gpu.T(x), gpu.T(t2), fx, fe)
+    assert_bitexact(fx.to_numpy(), ORC.backward(0, pw, ug, x, t2, grad=g0), f"x grad at the band edges, e={e}")
+    te = gpu.T(t2)
+    for k, v in enumerate(bases):
+        xk = np.ones(n, np.float32)
+        xk[k] = v
+        uk = np.zeros(n, np.float32)
+        uk[k] = 1.0
+        tx, tu = gpu.T(xk), gpu.T(uk)
+        fx, fe = gpu.T(np.zeros(n, np.float32)), gpu.T(np.zeros(1, np.float32))
+        m.backward_op_both(pw, tu, tx, te, fx, fe)
+        sep = gpu.backward(1, pw, uk, xk, t2)
+        what = f"e={e} base {v!r}"
+        assert_bitexact(fe.to_numpy(), sep, f"fused vs exponent-only term, {what}")
+        ref = ORC.backward(1, pw, uk, xk, t2)
+        exact = np.float64(v) ** np.float64(t2[0]) * np.log(np.float64(v))
+        with np.errstate(invalid="ignore"):  # a term that overflows is inf on both sides
+            assert_sum_close(fe.to_numpy(), ref, np.array([exact]), f"exponent term, {what}",
+                             terms_abs=np.array([abs(exact)]))
+
+
 # ---------------------------------------------------------------------------------------
 # reductions
 # ---------------------------------------------------------------------------------------
