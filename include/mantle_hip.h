@@ -161,7 +161,10 @@ int mh_unary_bwd_accum(int op, float* grad, const float* x, const float* ug, int
 
 /* backward_op for POW (ops.mojo:408-463 with POW.backward, basics.mojo:329-378).
  * tensor_id 0: grad = grad + (a * powf(x + 1e-12, a - 1)) * ug, a = exponent[0].
- * tensor_id 1: grad[0] = grad[0] + sum(powf(x, a) * (isinf(log x) ? 0 : log x) * ug).
+ * tensor_id 1: grad[0] = grad[0] + sum(powf(x, a) * (isinf(log x) ? 0 : log x) * ug), a sum
+ * whose order differs from the reference's (rtol 1e-5); where x + 1e-12 rounds to x and
+ * powf(x + 1e-12, a - 1) and x times it are normal and below 2e38, a term takes powf(x, a) as
+ * that product (a few ulp from it), the power tensor_id 0 evaluates.
  * n is the element count of x and ug. */
 int mh_pow_bwd_accum(int tensor_id, float* grad, const float* x, const float* exponent,
                      const float* ug, int64_t n);
