@@ -3,8 +3,9 @@
  *
  * TEST INFRASTRUCTURE ONLY (the parity checker): only tests/, __graft_entry__.smoke() and
  * bench.py's cpu_baseline leg may load this library. See mantle_oracle.h for the pinning
- * status of each function; "PARITY UNPINNED" there applies to or_exp / or_log / or_powf at
- * the bit level and to the lane-combine shape of the sums.
+ * status of each function; "PARITY UNPINNED" there applies to or_exp / or_log at the bit
+ * level (and so to the exp/log bits inside or_powf, whose composition is pinned) and to the
+ * lane-combine shape of the sums.
  *
  * Built with -ffp-contract=off: every a*b+c below rounds twice unless written as fmaf.
  * Single-threaded by construction, like the reference's elementwise, broadcast,
@@ -124,10 +125,11 @@ float or_powi(float x, int64_t n) {
     return n < 0 ? 1.0f / res : res;
 }
 
-/* float SIMD ** SIMD (basics.mojo:353,373): Mojo stdlib _powf_scalar (believed): an
- * integral exponent goes through _powi, a negative base with a fractional exponent is NaN,
- * anything else is exp(y * log(x)) with the exp/log above. PARITY UNPINNED at the bit
- * level against Mojo. */
+/* float SIMD ** SIMD (basics.mojo:353,373): the Mojo stdlib's _powf_scalar
+ * (std/builtin/simd.mojo): an integral exponent goes through _powi, a negative base with a
+ * fractional exponent is NaN, anything else is exp(y * log(x)) with the exp/log above. The
+ * composition is pinned by test_powf_is_exp_of_y_times_log; the exp/log bits it inherits are
+ * PARITY UNPINNED against Mojo. */
 float or_powf(float x, float y) {
     if (y != y) return y;
     float yi = truncf(y);

@@ -16,9 +16,17 @@
  *   - closed-form single-IEEE-op functions (add/sub/mul/div, relu, max, broadcast index
  *     math, accumulate, tie routing): reference fixtures from the tests/mojo test files plus
  *     brute-force checks against numpy on small inputs;
- *   - or_exp / or_log / or_powf: reference special points plus an fp64 bound (<= 2 ulp
- *     over the config domains). Bit-level agreement with Mojo's stdlib exp/log/pow
- *     (mojo 1.0.0b3.dev2026061606, not installable here) is PARITY UNPINNED.
+ *   - or_exp / or_log: reference special points plus fp64 bounds over the config domains
+ *     (exp <= 2 ulp on [-30, 30], <= 6 ulp on [-88, 88]; log <= 2 ulp; the sigmoid built on
+ *     exp <= 3 ulp). Bit-level agreement with Mojo's stdlib exp/log (mojo
+ *     1.0.0b3.dev2026061606, not installable here) is PARITY UNPINNED;
+ *   - or_powf restates the stdlib's `_powf_scalar` (std/builtin/simd.mojo, the float
+ *     `SIMD ** SIMD` of basics.mojo:353,373). Its formula is pinned: wherever or_log and
+ *     or_exp are correctly rounded, or_powf has exactly the bits of RN(exp(fl32(y * RN(log x)))),
+ *     which a correctly rounded powf misses in 37-56 % of samples at config 2's exponents
+ *     (test_powf_is_exp_of_y_times_log). Its fp64 bound is <= 8 ulp (the product's rounding,
+ *     |y log x| * 2^-24 relative). What stays unpinned is only the exp/log bits it inherits;
+ *   - or_tanh: the cancellation formula is pinned the same way (test_tanh_is_the_exp_...);
  *   - lane-ordered sums (or_reduce_*): exact-integer fixtures plus an fp64 bound; the
  *     reduce_add lane-combine shape is PARITY UNPINNED at the bit level (rtol class).
  */

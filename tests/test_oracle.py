@@ -212,6 +212,46 @@ def test_powf_bound_and_rules():
     assert O.powf_scalar(-2.0, 3.0) == -8.0
 
 
+def _pow_composition_signature(powfn, x, y32):
+    """Share of eligible samples where powfn(x, y) has the bits of RN(exp(fl32(y * RN(log x)))),
+    and the share of them where that composition differs from the correctly rounded x^y.
+    Eligible: the oracle's log is correctly rounded at x and its exp at p = fl32(y * RN(log x)),
+    so the composition's value is fixed by fp64 numpy alone, not by the oracle's code."""
+    l_rn = np.log(x.astype(np.float64)).astype(np.float32)
+    p = (y32 * l_rn).astype(np.float32)  # one float32 rounding of the product
+    e_rn = _exp_rn(p)
+    ok = (O.elwise_transform(O.LOG, x) == l_rn) & (O.elwise_transform(O.EXP, p) == e_rn)
+    got = np.asarray(powfn(x, y32), np.float32)
+    same = (got[ok].view(np.uint32) == e_rn[ok].view(np.uint32)).mean()
+    pow_rn = (x.astype(np.float64) ** np.float64(y32)).astype(np.float32)
+    differs = (e_rn[ok] != pow_rn[ok]).mean()
+    return ok.mean(), same, differs
+
+
+def test_powf_is_exp_of_y_times_log():
+    """Float SIMD ** SIMD (basics.mojo:353 `** (a - 1)`, :373 `** a`) restated as the Mojo
+    stdlib's `_powf_scalar` (std/builtin/simd.mojo): an integral exponent through `_powi`, a
+    negative base with a fractional exponent NaN, otherwise `exp(y * log(x))` over the stdlib's
+    f32 exp and log. Where the oracle's log and exp are correctly rounded, its pow must have
+    exactly the bits of that composition evaluated in fp64 numpy; the composition differs from
+    a correctly rounded x^y (what a library powf returns) in a large share of those samples, so
+    a library powf in its place fails the check (the second loop shows it does)."""
+    rng = np.random.default_rng(21)
+    x = rng.uniform(0.1, 4, 30_000).astype(np.float32)
+    oracle_pow = lambda xs, y: [O.powf_scalar(v, y) for v in xs]  # noqa: E731
+    library_pow = lambda xs, y: (xs.astype(np.float64) ** np.float64(y)).astype(np.float32)  # noqa: E731
+    # config 2's exponent (the exponent gradient's `** a`), its `a - 1`, and a third point
+    for y in (2.4349, 1.4349, 2.9):
+        y32 = np.float32(y)
+        eligible, same, differs = _pow_composition_signature(oracle_pow, x, y32)
+        assert eligible > 0.7, (y, eligible)
+        assert same == 1.0, (y, same)
+        assert differs > 0.3, (y, differs)
+        # negative control: a correctly rounded pow misses the composition's bits
+        _, lib_same, _ = _pow_composition_signature(library_pow, x, y32)
+        assert lib_same < 0.7, (y, lib_same)
+
+
 # ---------------------------------------------------------------------------------------
 # reductions
 # ---------------------------------------------------------------------------------------
