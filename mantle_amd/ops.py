@@ -420,17 +420,13 @@ def softmax_log_mul_mean_forward(loss: Tensor, x: Tensor, target: Tensor) -> Non
     """The graph MAX -> SUB -> EXP -> SUM -> DIV -> LOG -> MUL(target) -> MEAN over the rows of
     x [rows, classes] in one pass (Softmax, mantle/nn/activations.mojo:74-87, then LOG, MUL,
     MEAN): loss[0] = mean(log(softmax(x)) * target)."""
-    rows, classes = x.shape().dims
-    if target.shape() != x.shape() or loss.num_elements() != 1:
-        raise _lib.MantleHipError(_lib.ERR_SHAPE, "target must match x and loss must hold one element")
+    rows, classes = _row_operands(x, same=(("target", target),), scalar=(("loss", loss),))
     _lib.call("mh_softmax_log_mul_mean_fwd", loss.ptr, x.ptr, target.ptr, rows, classes)
 
 
 def softmax_log_mul_mean_backward(grad_x: Tensor, x: Tensor, target: Tensor, ug: Tensor) -> None:
     """Backward of the same graph from the loss grad ug (shape (1)): grad_x += d loss / dx."""
-    rows, classes = x.shape().dims
-    if target.shape() != x.shape() or grad_x.shape() != x.shape() or ug.num_elements() != 1:
-        raise _lib.MantleHipError(_lib.ERR_SHAPE, "grad_x and target must match x; ug holds one element")
+    rows, classes = _row_operands(x, same=(("grad_x", grad_x), ("target", target)), scalar=(("ug", ug),))
     _lib.call("mh_softmax_log_mul_mean_bwd_accum", grad_x.ptr, x.ptr, target.ptr, ug.ptr, rows, classes)
 
 
@@ -439,37 +435,54 @@ def _rows_classes(t: Tensor):
     return (t.num_elements() // k if k else 0), k
 
 
+def _row_operands(x: Tensor, same=(), scalar=()):
+    """(rows, classes) of x over its last axis, after checking every tensor the fused row
+    kernels read or write beside x: those in `same` must have x's shape and those in `scalar`
+    one element. The C entry points take bare pointers and sizes, so a smaller tensor would
+    reach the kernel as an out-of-bounds access; the check runs before any launch."""
+    xs = x.shape()
+    for name, t in same:
+        if t is None or t.shape() != xs:
+            got = None if t is None else t.shape()
+            raise _lib.MantleHipError(_lib.ERR_SHAPE, f"{name} shape {got} differs from x shape {xs}")
+    for name, t in scalar:
+        if t is None or t.num_elements() != 1:
+            got = None if t is None else t.num_elements()
+            raise _lib.MantleHipError(_lib.ERR_SHAPE, f"{name} must hold one element (holds {got})")
+    return _rows_classes(x)
+
+
 def softmax_forward(out: Tensor, x: Tensor) -> None:
     """Softmax over the last axis (activations.mojo:74-87), one fused pass."""
-    r, k = _rows_classes(x)
+    r, k = _row_operands(x, same=(("out", out),))
     _lib.call("mh_softmax_fwd", out.ptr, x.ptr, r, k)
 
 
 def softmax_backward(grad_x: Tensor, x: Tensor, grad_out: Tensor) -> None:
     """grad_x += the five Softmax backward nodes' contribution from grad_out."""
-    r, k = _rows_classes(x)
+    r, k = _row_operands(x, same=(("grad_x", grad_x), ("grad_out", grad_out)))
     _lib.call("mh_softmax_bwd_accum", grad_x.ptr, x.ptr, grad_out.ptr, r, k)
 
 
 def logsoftmax_forward(out: Tensor, x: Tensor) -> None:
     """LogSoftmax over the last axis (activations.mojo:94-108), one fused pass."""
-    r, k = _rows_classes(x)
+    r, k = _row_operands(x, same=(("out", out),))
     _lib.call("mh_logsoftmax_fwd", out.ptr, x.ptr, r, k)
 
 
 def logsoftmax_backward(grad_x: Tensor, x: Tensor, grad_out: Tensor) -> None:
-    r, k = _rows_classes(x)
+    """grad_x += the six LogSoftmax backward nodes' contribution from grad_out."""
+    r, k = _row_operands(x, same=(("grad_x", grad_x), ("grad_out", grad_out)))
     _lib.call("mh_logsoftmax_bwd_accum", grad_x.ptr, x.ptr, grad_out.ptr, r, k)
 
 
 def cross_entropy_forward(loss: Tensor, x: Tensor, target: Tensor) -> None:
     """CrossEntropyLoss (loss.mojo:45-61) of x [rows, classes] against target, one fused pass."""
-    if x.shape() != target.shape():
-        raise _lib.MantleHipError(_lib.ERR_SHAPE, "x and target differ in shape")
-    r, k = _rows_classes(x)
+    r, k = _row_operands(x, same=(("target", target),), scalar=(("loss", loss),))
     _lib.call("mh_cross_entropy_fwd", loss.ptr, x.ptr, target.ptr, r, k)
 
 
 def cross_entropy_backward(grad_x: Tensor, x: Tensor, target: Tensor, ug: Tensor) -> None:
-    r, k = _rows_classes(x)
+    """grad_x += d loss / dx of CrossEntropyLoss from the loss grad ug (one element)."""
+    r, k = _row_operands(x, same=(("grad_x", grad_x), ("target", target)), scalar=(("ug", ug),))
     _lib.call("mh_cross_entropy_bwd_accum", grad_x.ptr, x.ptr, target.ptr, ug.ptr, r, k)

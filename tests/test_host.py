@@ -202,3 +202,65 @@ def test_graph_builder_rejects(build):
     x = g.input((5, 3))
     with pytest.raises(m.MantleHipError):
         build(m, g, x)
+
+
+class _HostTensor:
+    """A shape-only stand-in for mantle_amd.Tensor (no device memory): enough for the fused-row
+    wrappers' checks, which run before anything reaches the library."""
+
+    def __init__(self, *dims):
+        self._s = mantle_amd.TensorShape(*dims)
+        self.ptr = None
+
+    def shape(self):
+        return self._s
+
+    def num_elements(self):
+        return self._s.num_elements()
+
+    def rank(self):
+        return self._s.rank()
+
+
+FUSED_ROW_CALLS = [
+    ("softmax_forward", ("out", "x")),
+    ("softmax_backward", ("grad_x", "x", "grad_out")),
+    ("logsoftmax_forward", ("out", "x")),
+    ("logsoftmax_backward", ("grad_x", "x", "grad_out")),
+    ("cross_entropy_forward", ("loss", "x", "target")),
+    ("cross_entropy_backward", ("grad_x", "x", "target", "ug")),
+    ("softmax_log_mul_mean_forward", ("loss", "x", "target")),
+    ("softmax_log_mul_mean_backward", ("grad_x", "x", "target", "ug")),
+]
+
+
+@pytest.mark.parametrize("fn,args", FUSED_ROW_CALLS, ids=[c[0] for c in FUSED_ROW_CALLS])
+def test_fused_row_wrappers_check_shapes_before_any_launch(monkeypatch, fn, args):
+    """The fused row entry points take bare pointers and (rows, classes) from x: every other
+    tensor must be x's shape (or hold one element: a loss or its gradient), else the binding
+    raises MH_ERR_SHAPE before the library is called."""
+    calls = []
+    monkeypatch.setattr(_lib, "call", lambda name, *a: calls.append((name, a[-2:])))
+    f = getattr(mantle_amd.ops, fn)
+    x = (37, 33)
+
+    def make(bad=None, how=None):
+        out = []
+        for a in args:
+            scalar = a in ("loss", "ug")
+            dims = (1,) if scalar else x
+            if a == bad:
+                dims = (2,) if scalar else (how or (36, 33))
+            out.append(_HostTensor(*dims))
+        return out
+
+    f(*make())
+    assert calls and calls[-1][1] == (37, 33)
+    for a in args:
+        if a == "x":
+            continue
+        for how in ((36, 33), (37, 32), (37 * 33,)):
+            with pytest.raises(_lib.MantleHipError) as e:
+                f(*make(a, how))
+            assert e.value.code == _lib.ERR_SHAPE and a in str(e.value)
+    assert len(calls) == 1  # no mismatched call reached the library
