@@ -7,8 +7,9 @@ import numpy as np
 import pytest
 
 from mantle_amd import synth
-from util import (O, OPS, GpuEngine, Graph, OracleEngine, assert_bitexact, assert_sum_close, config5_nodes,
-                  cross_entropy_nodes, load_fixtures, logsoftmax_nodes, native_graph, softmax_nodes, spec_to_array)
+from util import (FMA, O, OPS, GpuEngine, Graph, Mag64Engine, OracleEngine, assert_bitexact, assert_order_close,
+                  assert_sum_close, config5_nodes, cross_entropy_nodes, load_fixtures, logsoftmax_nodes, native_graph,
+                  softmax_nodes, spec_to_array)
 
 pytestmark = pytest.mark.gpu
 ORC = OracleEngine()
@@ -150,9 +151,9 @@ def _every_op_reference(E, x, w):
     gh = E.backward(0, OPS["MAX"], gk, vh, axis=1, grad=gh)
     gf = E.backward(0, OPS["CLIP"], gh, vf, grad=z(vf), attrs={"min": -0.5, "max": 1.5})
     ge = E.backward(0, OPS["LEAKYRELU"], gf, ve, grad=z(ve), attrs={"negative_slope": 0.2})
-    gc = O.fma_bwd_accum(0, z(vc), ge, vc, vd)
-    gd = O.fma_bwd_accum(1, z(vd), ge, vc, vd)
-    gb = O.fma_bwd_accum(2, z(vb), ge, vc, vd)
+    gc = E.backward(0, FMA, ge, vc, vd, grad=z(vc))
+    gd = E.backward(1, FMA, ge, vc, vd, grad=z(vd))
+    gb = E.backward(2, FMA, ge, vc, vd, grad=z(vb))
     gc = E.backward(0, OPS["SIGMOID"], gd, vc, grad=gc)
     gb = E.backward(0, OPS["TANH"], gc, vb, grad=gb)
     ga = E.backward(0, OPS["ADD"], gb, va, x, grad=z(va))
@@ -169,8 +170,9 @@ def test_model_every_op(gpu, rows):
     a MUL, against the oracle op by op. With 20 rows the column SUM adds its 20 terms in element
     order on both sides (fewer than the oracle's 32 lanes), so every gradient is bit-exact and
     only the loss (an all-element MEAN) is in the rtol class. With 37 rows the oracle's column
-    sums run lane-striped: the slots are bit-exact against the GPU's own op-by-op calls and
-    within rtol 1e-4 of the oracle, which sets that tolerance through the DIV by the sums."""
+    sums run lane-striped: the slots are bit-exact against the GPU's own op-by-op calls and in
+    the fp64 sum class against the oracle (assert_order_close: the fp64 magnitude engine
+    carries the order of the column sums through the DIV and every gradient after it)."""
     m = gpu.m
     x = synth.normal((rows, 20), 0, 1, 1220)
     w = synth.normal((1, 20), 0, 1, 1221)
@@ -205,9 +207,9 @@ def test_model_every_op(gpu, rows):
         for k, v in og.items():
             assert_bitexact(slots[k].to_numpy(), v, f"grad {k} vs oracle")
         return
+    _, _, og64 = _every_op_reference(Mag64Engine(), x, w)
     for k, v in og.items():
-        got_k = slots[k].to_numpy()
-        np.testing.assert_allclose(got_k, v, rtol=1e-4, atol=1e-4 * float(np.abs(v).max()), err_msg=f"grad {k}")
+        assert_order_close(slots[k].to_numpy(), v, og64[k], f"grad {k} vs oracle")
     gl, _, gg = _every_op_reference(gpu, x, w)
     assert_bitexact(got, gl, "loss")
     for k, v in gg.items():
@@ -489,8 +491,9 @@ def _ce_graph(m, rows, classes, x_tr=True, extra=False):
 
 
 def _oracle_row_graph(build, xv, tv):
-    """(loss, grad_x, the loss's fp64 value and sum of |terms|) of a row graph on the oracle,
-    one forward_op / backward_op per node (util.Graph)."""
+    """(loss, grad_x, the loss's fp64 value and sum of |terms|, grad_x in fp64 with its
+    magnitudes) of a row graph on the oracle, one forward_op / backward_op per node
+    (util.Graph), and on the fp64 magnitude engine."""
     rows = xv.shape[0]
     if build == "head":
         nodes, vals0 = config5_nodes(), {"logits": xv, "onehot": tv}
@@ -505,20 +508,23 @@ def _oracle_row_graph(build, xv, tv):
     gr = Graph(nodes, [xname])
     v = gr.forward(ORC, vals0)
     gd = gr.backward(ORC, v)
+    f64 = Mag64Engine()
+    gx64 = gr.backward(f64, gr.forward(f64, vals0))[xname]
     terms = v[tname].astype(np.float64)
     ex, ab = terms.sum() * scale, np.abs(terms).sum() * abs(scale)
     if build == "ce_extra":
         sq = v["sq"].astype(np.float64)
         ex, ab = ex + sq.mean(), ab + np.abs(sq).mean()
-    return v[nodes[-1][3]], gd[xname], ex, ab
+    return v[nodes[-1][3]], gd[xname], ex, ab, gx64
 
 
 @pytest.mark.parametrize("rows,classes", [(4099, 10), (300, 130), (64, 1000), (7, 1)])
 def test_model_fused_rows_cross_entropy_and_head(gpu, rows, classes):
     """MH_MODEL_FUSE_ROWS: the cross-entropy group (and the config-5 head), fused and op by op,
     against the oracle: the loss in the sum class; grad_x bit-exact for rows shorter than the
-    oracle's 32 SIMD lanes (row sums in element order on both sides), else within rtol 1e-4 of
-    the oracle and bit-identical between the fused and op-by-op models."""
+    oracle's 32 SIMD lanes (row sums in element order on both sides), else in the fp64 sum
+    class against the oracle (assert_order_close) and bit-identical between the fused and
+    op-by-op models."""
     m = gpu.m
     xv = synth.normal((rows, classes), 0, 2, 1400)
     tv = synth.uniform((rows, classes), 0, 1, 1401)
@@ -539,14 +545,13 @@ def test_model_fused_rows_cross_entropy_and_head(gpu, rows, classes):
             results.append((loss, model.parameters.grads[x].to_numpy(), model.info()["fused_groups"]))
         (l0, g0, f0), (l1, g1, f1) = results
         assert f0 == 0 and f1 == 1, (build, f0, f1)
-        ol, og, ex, ab = _oracle_row_graph(build, xv, tv)
+        ol, og, ex, ab, gx64 = _oracle_row_graph(build, xv, tv)
         for lv, gv, label in ((l0, g0, "op by op"), (l1, g1, "fused")):
             assert_sum_close(lv, ol, np.array([ex]), f"{build} {label} loss", terms_abs=np.array([ab]))
             if classes < 32:
                 assert_bitexact(gv, og, f"{build} {label} grad_x vs oracle")
             else:
-                np.testing.assert_allclose(gv, og, rtol=1e-4, atol=1e-4 * float(np.abs(og).max()),
-                                           err_msg=f"{build} {label} grad_x vs oracle")
+                assert_order_close(gv, og, gx64, f"{build} {label} grad_x vs oracle")
         assert_bitexact(g1, g0, f"{build} grad_x fused vs op by op")
 
 
@@ -593,17 +598,22 @@ def test_model_fused_rows_softmax_inside_a_graph(gpu, classes):
     gd = ref.backward(ORC, v)
     th = v["th"].astype(np.float64)
     assert_sum_close(l1, v["loss"], np.array([th.sum()]), "loss vs oracle", terms_abs=np.array([np.abs(th).sum()]))
-    # grad w sums 513 terms ug * x; from 32 classes its terms (grad h) carry the rtol-1e-4
-    # difference of the row sums, so the sum is held to 1e-4 of its terms' magnitude
-    rgw = (gd["h"] * xv).astype(np.float64)
-    assert_sum_close(gw1, gd["w"], rgw.sum(axis=0, keepdims=True), "grad w vs oracle",
-                     terms_abs=np.abs(rgw).sum(axis=0, keepdims=True), rtol=1e-5 if classes < 32 else 1e-4)
-    for got, exp, what in ((s1, v["sm"], "softmax output"), (gx1, gd["x"], "grad x")):
+    # grad w sums 513 terms ug * x; from 32 classes its terms (grad h) also carry the order of
+    # the row sums: the fp64 magnitude engine bounds both
+    f64 = Mag64Engine()
+    v64 = ref.forward(f64, {"x": xv, "w": wv})
+    gd64 = ref.backward(f64, v64)
+    if classes < 32:
+        rgw = (gd["h"] * xv).astype(np.float64)
+        assert_sum_close(gw1, gd["w"], rgw.sum(axis=0, keepdims=True), "grad w vs oracle",
+                         terms_abs=np.abs(rgw).sum(axis=0, keepdims=True))
+    else:
+        assert_order_close(gw1, gd["w"], gd64["w"], "grad w vs oracle")
+    for got, exp, e64, what in ((s1, v["sm"], v64["sm"], "softmax output"), (gx1, gd["x"], gd64["x"], "grad x")):
         if classes < 32:
             assert_bitexact(got, exp, f"{what} vs oracle")
         else:
-            np.testing.assert_allclose(got, exp, rtol=1e-4, atol=1e-4 * float(np.abs(exp).max()),
-                                       err_msg=f"{what} vs oracle")
+            assert_order_close(got, exp, e64, f"{what} vs oracle")
 
 
 GRAPH_FIXTURES = [c for c in load_fixtures() if c["kind"] == "graph"]

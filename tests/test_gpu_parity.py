@@ -9,8 +9,8 @@ import numpy as np
 import pytest
 
 from mantle_amd import synth
-from util import (O, OPS, GpuEngine, Graph, OracleEngine, config5_nodes, assert_bitexact, assert_sum_close, assert_ulp,
-                  check_fixture, load_fixtures)
+from util import (O, OPS, GpuEngine, Graph, Mag64Engine, OracleEngine, config5_nodes, assert_bitexact,
+                  assert_order_close, assert_sum_close, assert_ulp, check_fixture, load_fixtures)
 
 pytestmark = pytest.mark.gpu
 
@@ -837,7 +837,9 @@ def _check_fused_head(gpu, logits, onehot, ugv):
     accumulated into a non-zero grad_x and from zero. Rows shorter than the oracle's 32 SIMD
     lanes sum in element order on every path, so the oracle is the reference; from 32 classes
     its row sums follow the lane order, so the bit-exact reference is the GPU op-by-op chain
-    and the oracle is met within the sum class."""
+    and the oracle is met within the sum class (the fp64 magnitude comparator); up to 64
+    classes that chain sums every row in element order and matches the oracle at nelts = 1
+    bit for bit."""
     m = gpu.m
     rows, classes = logits.shape
     g = Graph(config5_nodes(), ["logits"])
@@ -851,8 +853,17 @@ def _check_fused_head(gpu, logits, onehot, ugv):
         gr = g.backward(gpu, vr, seed)
         fin = np.isfinite(go["logits"])
         assert (np.isfinite(gr["logits"]) == fin).all()
-        np.testing.assert_allclose(gr["logits"][fin], go["logits"][fin], rtol=1e-4,
-                                   atol=1e-4 * float(np.abs(go["logits"][fin]).max(initial=0)))
+        f64 = Mag64Engine()
+        gx64 = g.backward(f64, g.forward(f64, {"logits": logits, "onehot": onehot}), seed)["logits"]
+        gx64 = type(gx64)(gx64.v[fin], gx64.M[fin])
+        assert_order_close(gr["logits"][fin], go["logits"][fin], gx64, "op-by-op grad vs oracle, reference order")
+        if classes <= 64:
+            O.set_nelts(1)
+            try:
+                g1 = g.backward(ORC, g.forward(ORC, {"logits": logits, "onehot": onehot}), seed)
+            finally:
+                O.set_nelts(32)
+            assert_bitexact(gr["logits"], g1["logits"], "op-by-op grad vs oracle, element order")
     tl, to = gpu.T(logits), gpu.T(onehot)
     loss = m.Tensor(m.TensorShape(1))
     m.softmax_log_mul_mean_forward(loss, tl, to)
@@ -998,6 +1009,71 @@ def test_fused_row_graphs(gpu, rows, classes):
     tg = gpu.T(g0)
     m.cross_entropy_backward(tg, tx, gpu.T(target), gpu.T(seed))
     assert_bitexact(tg.to_numpy(), gr["x"], "cross-entropy backward")
+
+
+ORACLE_ROW_CASES = [(513, 17), (300, 24), (1000, 31), (40, 33), (777, 47), (1200, 64), (500, 32)]
+
+
+@pytest.mark.parametrize("rows,classes", ORACLE_ROW_CASES, ids=[f"{r}x{c}" for r, c in ORACLE_ROW_CASES])
+def test_fused_rows_17_to_64_classes_against_the_oracle(gpu, rows, classes):
+    """The thread and multi-lane row engines (17-64 classes) through mh_softmax_*,
+    mh_logsoftmax_* and mh_cross_entropy_* against the oracle's op-by-op graphs
+    (activations.mojo:74-108, loss.mojo:45-61), ties injected, backward accumulated into a
+    non-zero grad_x:
+    - bit-exact against the oracle with nelts = 1, whose row sums run in element order, the
+      order these engines use: only the order of the sums separates them from the reference;
+    - against the reference's lane order (nelts = 32): bit-exact below 32 classes (both orders
+      are the element order there), else every element in the fp64 sum class
+      (assert_order_close with the fp64 magnitude engine);
+    - the cross-entropy loss (an all-element sum in the kernel's own order) in that class."""
+    from util import cross_entropy_nodes, logsoftmax_nodes, softmax_nodes
+    m = gpu.m
+    x = synth.normal((rows, classes), 0, 2, 1300)
+    synth.inject_ties(x, 1, 1301)
+    g0 = synth.normal((rows, classes), 0, 1, 1302)
+    gout = synth.normal((rows, classes), 0, 1, 1303)
+    target = synth.uniform((rows, classes), 0, 1, 1304)
+    cn = np.array([np.float32(-1.0 / rows)], np.float32)
+    seed = np.array([0.7], np.float32)
+    tx, tt = gpu.T(x), gpu.T(target)
+    f64 = Mag64Engine()
+
+    def graph(eng, nodes, vals, out, ug):
+        g = Graph(nodes, ["x"])
+        v = g.forward(eng, vals)
+        return v[out], g.backward(eng, v, seed=ug, init={"x": g0})["x"]
+
+    cases = []
+    for name, nodes, out, fwd, bwd in [
+            ("softmax", softmax_nodes("x", 1), "sm", m.softmax_forward, m.softmax_backward),
+            ("logsoftmax", logsoftmax_nodes("x", 1), "lsm", m.logsoftmax_forward, m.logsoftmax_backward)]:
+        res = m.Tensor(m.TensorShape(rows, classes))
+        fwd(res, tx)
+        tg = gpu.T(g0)
+        bwd(tg, tx, gpu.T(gout))
+        cases.append((name, nodes, out, {"x": x}, gout, res.to_numpy(), tg.to_numpy(), True))
+    loss = m.Tensor(m.TensorShape(1))
+    m.cross_entropy_forward(loss, tx, tt)
+    tg = gpu.T(g0)
+    m.cross_entropy_backward(tg, tx, tt, gpu.T(seed))
+    cases.append(("cross_entropy", cross_entropy_nodes("x", "target"), "loss", {"x": x, "target": target, "cN": cn},
+                  seed, loss.to_numpy(), tg.to_numpy(), False))
+    try:
+        for name, nodes, out, vals, ug, got_f, got_b, fwd_rows in cases:
+            O.set_nelts(1)
+            e1 = graph(ORC, nodes, vals, out, ug)
+            O.set_nelts(32)
+            e32 = graph(ORC, nodes, vals, out, ug)
+            ex = graph(f64, nodes, vals, out, ug)
+            if fwd_rows:
+                assert_bitexact(got_f, e1[0], f"{name} forward vs oracle, element order")
+            assert_bitexact(got_b, e1[1], f"{name} backward vs oracle, element order")
+            for got, ref, e, what in ((got_f, e32[0], ex[0], "forward"), (got_b, e32[1], ex[1], "backward")):
+                if classes < 32 and (fwd_rows or what == "backward"):
+                    assert_bitexact(got, ref, f"{name} {what} vs oracle, reference order")
+                assert_order_close(got, ref, e, f"{name} {what} vs oracle, reference order")
+    finally:
+        O.set_nelts(32)
 
 
 def test_fused_cross_entropy_matches_reference_fixtures(gpu):

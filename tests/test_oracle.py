@@ -6,8 +6,9 @@ import math
 import numpy as np
 import pytest
 
-from util import (O, OPS, OracleEngine, assert_bitexact, assert_sum_close, check_fixture,
-                  load_fixtures, spec_to_array, ulp_dist)
+from util import (O, OPS, Graph, Mag64Engine, OracleEngine, assert_bitexact, assert_order_close,
+                  assert_sum_close, check_fixture, cross_entropy_nodes, load_fixtures, logsoftmax_nodes,
+                  softmax_nodes, spec_to_array, ulp_dist)
 
 FIXTURES = load_fixtures()
 ENG = OracleEngine()
@@ -568,3 +569,61 @@ def test_threaded_axis_reduce_is_identical(shape, axis, nthreads):
     x = np.random.default_rng(13).standard_normal(shape).astype(np.float32)
     for op in (O.SUM, O.MEAN, O.MAX):
         assert_bitexact(O.reduce_axis_mt(op, x, axis, nthreads), O.forward_op(op, x, axis=axis), f"op {op}")
+
+
+# ---------------------------------------------------------------------------------------
+# row graphs: the summation order's effect, bounded by the fp64 magnitude comparator
+# ---------------------------------------------------------------------------------------
+ROW_ORDER_SHAPES = [(513, 17), (300, 24), (1000, 31), (40, 33), (777, 47), (1200, 64), (500, 32)]
+
+
+def _row_graph_cases(rows, k):
+    """(name, nodes, output, inputs, seed) of Softmax, LogSoftmax (activations.mojo:74-108) and
+    CrossEntropyLoss (loss.mojo:45-61) over [rows, k], ties injected, soft targets."""
+    from mantle_amd import synth
+    x = synth.normal((rows, k), 0, 2, 1300)
+    synth.inject_ties(x, 1, 1301)
+    gout = synth.normal((rows, k), 0, 1, 1303)
+    target = synth.uniform((rows, k), 0, 1, 1304)
+    cn = np.array([np.float32(-1.0 / rows)], np.float32)
+    return [("softmax", softmax_nodes("x", 1), "sm", {"x": x}, gout),
+            ("logsoftmax", logsoftmax_nodes("x", 1), "lsm", {"x": x}, gout),
+            ("cross_entropy", cross_entropy_nodes("x", "target"), "loss", {"x": x, "target": target, "cN": cn},
+             np.array([0.7], np.float32))]
+
+
+def _run_graph(eng, nodes, inputs, seed, g0, out):
+    g = Graph(nodes, ["x"])
+    v = g.forward(eng, inputs)
+    return v[out], g.backward(eng, v, seed=seed, init={"x": g0})["x"]
+
+
+@pytest.mark.parametrize("rows,k", ROW_ORDER_SHAPES, ids=[f"{r}x{c}" for r, c in ROW_ORDER_SHAPES])
+def test_row_graph_summation_orders_meet_in_the_sum_class(rows, k):
+    """The oracle's row graphs at nelts 1 (every row sum in element order, the order of the
+    GPU's row engines up to 64 classes) and at nelts 32 (the reference's AVX-512 lane order):
+    bit-identical below 32 classes, where both orders are the element order; from 32 classes
+    every output and gradient element meets the fp64 comparator (assert_order_close: no farther
+    from fp64 than the other order plus 2 ulp, or within 1e-5 of its first-order magnitude).
+    A result whose row sums drop one term must fail the same comparator."""
+    from mantle_amd import synth
+    g0 = synth.normal((rows, k), 0, 1, 1302)
+    f64 = Mag64Engine()
+    for name, nodes, out, inputs, seed in _row_graph_cases(rows, k):
+        O.set_nelts(1)
+        o1 = _run_graph(ENG, nodes, inputs, seed, g0, out)
+        O.set_nelts(32)
+        o32 = _run_graph(ENG, nodes, inputs, seed, g0, out)
+        ex = _run_graph(f64, nodes, inputs, seed, g0, out)
+        for got, ref, e, what in zip(o1, o32, ex, ("forward", "backward")):
+            if k < 32 and not (name == "cross_entropy" and what == "forward"):
+                assert_bitexact(got, ref, f"{name} {what}: element order below 32 lanes")
+            assert_order_close(got, ref, e, f"{name} {what}")
+    # negative control: a Softmax whose row sums miss their last term is far outside the class
+    x = _row_graph_cases(rows, k)[0][3]["x"]
+    O.set_nelts(32)
+    v = Graph(softmax_nodes("x", 1), ["x"]).forward(ENG, {"x": x})
+    short = O.forward_op(O.DIV, v["e"], v["s"] - v["e"][:, -1:])
+    with pytest.raises(AssertionError):
+        assert_order_close(short, v["sm"], Graph(softmax_nodes("x", 1), ["x"]).forward(f64, {"x": x})["sm"],
+                           "softmax with a dropped term")

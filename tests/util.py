@@ -104,6 +104,35 @@ def assert_sum_close(got, ref, exact64, what="", rtol=1e-5, terms_abs=None):
                              f"fp64 {ex.reshape(-1)[i]!r}")
 
 
+def _ulp32(v) -> np.ndarray:
+    return np.spacing(np.abs(np.asarray(v, np.float64)).astype(np.float32)).astype(np.float64)
+
+
+def assert_order_close(got, ref, exact, what="", rtol=1e-5):
+    """The sum class for values that depend on sums whose order differs (the GPU's fixed order
+    against the reference's lane-striped one). `exact` is an Mag64 value: the fp64 evaluation of
+    the same graph and, per element, the first-order magnitude M of everything a different
+    order of its sums can change. An element passes when it equals the reference, or is no
+    farther from fp64 than the reference is (plus 2 ulp), or lies within rtol * M of fp64 or of
+    the reference (the last covers values that both float32 evaluations share a larger error
+    in, such as subnormal intermediates)."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    ex = np.asarray(exact.v, dtype=np.float64).reshape(got.shape)
+    mag = np.asarray(exact.M, dtype=np.float64).reshape(got.shape)
+    assert got.shape == ref.shape, f"{what}: shape {got.shape} vs {ref.shape}"
+    with np.errstate(invalid="ignore"):
+        ok = (got == ref) | (np.isnan(got) & np.isnan(ref))
+        ok |= np.abs(got - ex) <= np.abs(ref - ex) + 2 * _ulp32(ex)
+        ok |= np.abs(got - ex) <= rtol * mag
+        ok |= np.abs(got - ref) <= rtol * mag
+    if not ok.all():
+        i = int(np.flatnonzero(~ok.reshape(-1))[0])
+        raise AssertionError(f"{what}: {int((~ok).sum())} of {ok.size} out of the sum class; first at {i}: "
+                             f"got {got.reshape(-1)[i]!r} ref {ref.reshape(-1)[i]!r} fp64 {ex.reshape(-1)[i]!r} "
+                             f"M {mag.reshape(-1)[i]!r}")
+
+
 def assert_almost(got, ref, what="", rtol=1e-5, atol=1e-5):
     """testing_utils.mojo:16-27 'almost': rtol = atol = 1e-5 per element."""
     got = np.asarray(got, dtype=np.float64)
@@ -147,6 +176,199 @@ class OracleEngine:
 
     def tstd(self, t1, axis=None):
         return O.tstd(t1, axis)
+
+
+
+class Mag64:
+    """A value of the fp64 magnitude engine: v, the fp64 evaluation, and M, the first-order
+    magnitude of what the order of sums can change in it (Sum |terms| through every sum,
+    carried through each op by its derivative, plus |v| for the op's own rounding). Arrays
+    compare and reshape through `v`, so the graph executor handles these like numpy arrays."""
+    __slots__ = ("v", "M")
+
+    def __init__(self, v, M=None):
+        self.v = np.asarray(v, np.float64)
+        self.M = np.zeros(self.v.shape) if M is None else np.broadcast_to(np.asarray(M, np.float64), self.v.shape)
+
+    @property
+    def shape(self):
+        return self.v.shape
+
+    def __array__(self, dtype=None, copy=None):
+        return self.v if dtype is None else self.v.astype(dtype)
+
+
+def _mag(a):
+    if a is None or isinstance(a, Mag64):
+        return a
+    return Mag64(np.asarray(a, np.float64))
+
+
+def _pm(*factors):
+    """Product of the factors' magnitudes, with 0 * inf = 0: a term whose derivative vanishes
+    (a clamped exp, a relu below zero) carries nothing, even from an infinite operand."""
+    out = np.ones(())
+    zero = np.zeros((), bool)
+    for f in factors:
+        f = np.abs(np.asarray(f, np.float64))
+        zero = zero | (f == 0)
+        with np.errstate(invalid="ignore", over="ignore"):
+            out = out * f
+    return np.where(zero, 0.0, out)
+
+
+_FLT_MIN = float(np.finfo(np.float32).tiny)
+
+
+def _own(v):
+    """The magnitude of one float32 rounding of v: |v|, or FLT_MIN for a subnormal result
+    (its rounding error is absolute, 2^-150, not relative)."""
+    return np.maximum(np.abs(v), _FLT_MIN)
+
+
+def _unbroadcast_mag(v, M, shape):
+    """Sums v (and M + |v|, a sum's own magnitude) over the axes that broadcast `shape` to v's."""
+    while v.ndim > len(shape):
+        M, v = (M + np.abs(v)).sum(axis=0), v.sum(axis=0)
+    for ax, d in enumerate(shape):
+        if d == 1 and v.shape[ax] != 1:
+            M, v = (M + np.abs(v)).sum(axis=ax, keepdims=True), v.sum(axis=ax, keepdims=True)
+    return v, M
+
+
+_EXP_LO, _EXP_HI = float(np.float32(-88.3762626647949)), float(np.float32(88.3762626647950))
+
+
+class Mag64Engine:
+    """The path's ops in fp64 with first-order magnitudes (see Mag64), behind the engines'
+    forward / backward interface. Each value is the reference expression in exact arithmetic
+    (exp clamps its argument to +-88.376 as the reference's exp does, POW truncates its
+    exponent as POW.forward does, MAX splits ties as fl(1/c) * ug with the same count, CLIP and
+    LEAKYRELU keep the oracle's boundary rules); M bounds, to first order, how far two float32
+    evaluations that differ only in the order of their sums can move apart (in units of the
+    relative rounding error)."""
+    name = "fp64"
+
+    @staticmethod
+    def _unary(op, a, attrs):
+        """(value, its derivative, the factor the reference's backward multiplies ug by, that
+        factor's derivative) of a unary op at a. The factor is the derivative except for exp
+        beyond its clamp, where the reference's backward still multiplies by E(x)."""
+        if op == OPS["EXP"]:
+            e = np.exp(np.clip(a, _EXP_LO, _EXP_HI))
+            d = np.where((a >= _EXP_LO) & (a <= _EXP_HI), e, 0.0)  # flat beyond the clamp
+            return e, d, e, d
+        if op == OPS["LOG"]:
+            with np.errstate(divide="ignore", invalid="ignore"):
+                return np.log(a), 1 / a, 1 / a, -1 / (a * a)
+        if op == OPS["TANH"]:
+            t = np.tanh(a)
+            d = 1 - t * t
+            return t, d, d, -2 * t * d
+        if op == OPS["SIGMOID"]:
+            s = 1 / (1 + np.exp(-a))
+            d = s * (1 - s)
+            return s, d, d, d * (1 - 2 * s)
+        zero = np.zeros(a.shape)
+        if op == OPS["RELU"]:
+            d = (a > 0).astype(np.float64)
+            return np.where(a > 0, a, 0.0), d, d, zero
+        if op == LEAKYRELU:
+            d = np.where(a > 0, 1.0, float(np.float32(attrs["negative_slope"])))
+            return a * d, d, d, zero
+        if op == CLIP:
+            lo, hi = _clip_bounds(attrs)
+            d = ((a >= lo) & (a <= hi)).astype(np.float64)
+            return np.clip(a, lo, hi), d, d, zero
+        raise AssertionError(f"fp64 engine: op {op}")
+
+    def forward(self, op, t1, t2=None, axis=None, attrs=None, t3=None):
+        A, B = _mag(t1), _mag(t2)
+        a, Ma = A.v, A.M
+        if op in REDUCE:
+            if op == OPS["MAX"]:
+                if axis is None:
+                    return Mag64([a.max()], [Ma.max()])
+                return Mag64(a.max(axis=axis, keepdims=True), Ma.max(axis=axis, keepdims=True))
+            n = a.size if axis is None else a.shape[axis]
+            sc = 1.0 / n if op == OPS["MEAN"] else 1.0
+            if axis is None:
+                return Mag64([a.sum() * sc], [(Ma + np.abs(a)).sum() * sc])
+            return Mag64(a.sum(axis=axis, keepdims=True) * sc, (Ma + np.abs(a)).sum(axis=axis, keepdims=True) * sc)
+        with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+            if op == FMA:
+                C = _mag(t3)
+                b, Mb = B.v, B.M
+                v = a * b + C.v
+                return Mag64(v, _pm(Ma, b) + _pm(a, Mb) + C.M + _own(v))
+            if op == OPS["POW"]:
+                p = float(np.trunc(B.v.reshape(-1)[0]))
+                v = a ** p
+                return Mag64(v, (_pm(p * a ** (p - 1), Ma) if p else 0.0) + _own(v))
+            if op in BINARY:
+                b, Mb = B.v, B.M
+                if op == OPS["ADD"]:
+                    v, M = a + b, Ma + Mb
+                elif op == OPS["SUB"]:
+                    v, M = a - b, Ma + Mb
+                elif op == OPS["MUL"]:
+                    v, M = a * b, _pm(Ma, b) + _pm(a, Mb)
+                else:
+                    v, M = a / b, _pm(Ma, 1 / b) + _pm(a, Mb, 1 / (b * b))
+                return Mag64(v, M + _own(v))
+            v, d1, _, _ = self._unary(op, a, attrs)
+            return Mag64(v, _pm(d1, Ma) + _own(v))
+
+    def backward(self, tensor_id, op, ug, t1, t2=None, axis=None, grad=None, attrs=None):
+        U, A, B = _mag(ug), _mag(t1), _mag(t2)
+        u, Mu, a, Ma = U.v, U.M, A.v, A.M
+        tshape = a.shape if tensor_id != 1 or B is None else B.v.shape
+        with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+            if op in REDUCE:
+                n = a.size if axis is None else a.shape[axis]
+                uu, MM = (u, Mu) if axis is not None else (u.reshape(-1)[0], Mu.reshape(-1)[0])
+                if op == OPS["MAX"]:
+                    m = a.max(axis=axis, keepdims=axis is not None)
+                    eq = a == m
+                    c = eq.sum(axis=axis, keepdims=axis is not None)
+                    rg = np.where(eq, uu / c, 0.0)
+                    M = np.where(eq, MM / c, 0.0) + _own(rg)
+                else:
+                    sc = 1.0 / n if op == OPS["MEAN"] else 1.0
+                    rg = np.broadcast_to(uu * sc, a.shape)
+                    M = np.broadcast_to(MM * sc, a.shape)
+            elif op in BINARY or op == FMA:
+                b, Mb = B.v, B.M
+                if op == OPS["ADD"] or (op == FMA and tensor_id == 2):
+                    rg, M = u, Mu
+                elif op == OPS["SUB"]:
+                    rg, M = (u, Mu) if tensor_id == 0 else (-u, Mu)
+                elif op in (OPS["MUL"], FMA):
+                    o, Mo = (b, Mb) if tensor_id == 0 else (a, Ma)
+                    rg = u * o
+                    M = _pm(Mu, o) + _pm(u, Mo) + _own(rg)
+                elif tensor_id == 0:
+                    rg = u / b
+                    M = _pm(Mu, 1 / b) + _pm(u, Mb, 1 / (b * b)) + _own(rg)
+                else:
+                    rg = u * (-a / (b * b))
+                    M = _pm(Mu, a, 1 / (b * b)) + _pm(u, Ma, 1 / (b * b)) + 2 * _pm(u, a, Mb, 1 / (b * b * b)) \
+                        + _own(rg)
+            elif op == OPS["POW"]:
+                if tensor_id != 0:
+                    raise AssertionError("fp64 engine: POW exponent gradient")
+                p = float(B.v.reshape(-1)[0])
+                d1, d2 = p * a ** (p - 1), p * (p - 1) * a ** (p - 2)
+                rg = u * d1
+                M = _pm(Mu, d1) + _pm(u, d2, Ma) + _own(rg)
+            else:
+                _, _, f, df = self._unary(op, a, attrs)
+                rg = u * f
+                M = _pm(Mu, f) + _pm(u, df, Ma) + _own(rg)
+            rg, M = _unbroadcast_mag(np.asarray(rg, np.float64), np.asarray(M, np.float64), tshape)
+            G = _mag(np.zeros(tshape) if grad is None else grad)
+            v = G.v + rg
+            return Mag64(v, G.M + M + _own(v))
 
 
 # MANTLE_TEST_ASYNC=1 runs the GPU tests with the library in MH_INIT_ASYNC mode (no stream
