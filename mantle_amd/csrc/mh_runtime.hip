@@ -167,14 +167,18 @@ int graph_release(uint64_t epoch) {
 
 static int grow(void** buf, size_t* have, size_t bytes, void** out) {
     if (bytes > *have) {
+        size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+        // While a captured graph exists, the replaced buffer is retired, not freed, until the
+        // last graph goes: growing at least twofold then keeps every retired buffer together
+        // smaller than the live one, whatever sequence of sizes the eager calls ask for.
+        if (ctx().graphs_live > 0 && want < 2 * *have) want = 2 * *have;
+        want = (want + 255) & ~(size_t)255;
         if (*buf) {
             void* old = *buf;
             *buf = nullptr;
             *have = 0;
             MH_TRY(drop_buffer(old));
         }
-        size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-        want = (want + 255) & ~(size_t)255;
         MH_HIP(hipMalloc(buf, want));
         *have = want;
     }
@@ -191,6 +195,7 @@ int tickets(int64_t n, uint32_t** out) {
     Context& c = ctx();
     if (n > c.ntickets) {
         int64_t want = n < 65536 ? 65536 : n;
+        if (c.graphs_live > 0 && want < 2 * c.ntickets) want = 2 * c.ntickets;  // as in grow()
         if (c.tickets) {
             void* old = c.tickets;
             c.tickets = nullptr;
@@ -428,18 +433,25 @@ __global__ void __launch_bounds__(256) k_rand(float* __restrict__ t, int64_t n, 
     }
 }
 
+// One-wavefront workgroups, one quad (or, unaligned, one element) per thread; k_fill and
+// k_fill_scalar loop over the grid beyond what one dispatch holds.
+LaunchShape fill_launch(int64_t n, bool aligned) {
+    return LaunchShape{aligned ? 0 : 1, 64, grid_blocks(aligned ? (n >> 2) : n, 64)};
+}
+
+// One-wavefront workgroups, one quad per thread; k_copy loops over the grid beyond that.
+LaunchShape copy_launch(int64_t nquads) { return LaunchShape{0, 64, grid_blocks(nquads, 64)}; }
+
 static int launch_fill(float* t, float v, int64_t n) {
     if (n == 0) return MH_OK;
     if (!t) return fail(MH_ERR_NULL, "fill: null tensor");
     MH_TRY(require_init());
-    int64_t work = ((reinterpret_cast<uintptr_t>(t) & 15) == 0) ? (n >> 2) : n;
-    int64_t blocks = (work + 63) / 64;  // one-wavefront workgroups, one quad per thread
-    if (blocks < 1) blocks = 1;
-    if (blocks > 0x7fffffff) blocks = 0x7fffffff;
-    if ((reinterpret_cast<uintptr_t>(t) & 15) == 0)
-        hipLaunchKernelGGL(k_fill, dim3((unsigned)blocks), dim3(64), 0, ctx().stream, t, v, n);
+    const bool al = (reinterpret_cast<uintptr_t>(t) & 15) == 0;
+    const LaunchShape ls = fill_launch(n, al);
+    if (al)
+        hipLaunchKernelGGL(k_fill, dim3((unsigned)ls.blocks), dim3(ls.threads), 0, ctx().stream, t, v, n);
     else
-        hipLaunchKernelGGL(k_fill_scalar, dim3((unsigned)blocks), dim3(64), 0, ctx().stream, t, v, n);
+        hipLaunchKernelGGL(k_fill_scalar, dim3((unsigned)ls.blocks), dim3(ls.threads), 0, ctx().stream, t, v, n);
     return finish("fill");
 }
 
@@ -583,10 +595,9 @@ int mh_memcpy_d2d(void* dst, const void* src, size_t bytes) {
     if (!dst || !src) return fail(MH_ERR_NULL, "mh_memcpy_d2d: null pointer");
     MH_TRY(require_init());
     if (((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) | bytes) & 15) == 0) {
-        int64_t nq = (int64_t)(bytes >> 4);
-        int64_t blocks = (nq + 63) / 64;  // one-wavefront workgroups, one quad per thread (the
-        if (blocks > 0x7fffffff) blocks = 0x7fffffff;  // stride loop covers > 2^31 blocks)
-        hipLaunchKernelGGL(k_copy, dim3((unsigned)blocks), dim3(64), 0, ctx().stream,
+        const int64_t nq = (int64_t)(bytes >> 4);
+        const LaunchShape ls = copy_launch(nq);
+        hipLaunchKernelGGL(k_copy, dim3((unsigned)ls.blocks), dim3(ls.threads), 0, ctx().stream,
                            reinterpret_cast<float4*>(dst), reinterpret_cast<const float4*>(src), nq);
     } else {
         MH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx().stream));
@@ -690,6 +701,25 @@ int mh_plan_unbroadcast(const mh_shape* psgrad, const mh_shape* psrg, mh_reduce_
     MH_TRY(check_shape(sgrad, "grad"));
     MH_TRY(check_shape(srg, "rg"));
     return plan_unbroadcast(sgrad, srg, out);
+}
+
+int mh_plan_launch(int32_t what, int64_t n, mh_launch_info* out) {
+    if (!out) return fail(MH_ERR_NULL, "mh_plan_launch: null");
+    if (n < 0) return fail(MH_ERR_INVALID, "mh_plan_launch: negative count");
+    LaunchShape ls;
+    switch (what) {
+        case MH_LAUNCH_FILL: ls = fill_launch(n, true); break;
+        case MH_LAUNCH_FILL_UNALIGNED: ls = fill_launch(n, false); break;
+        case MH_LAUNCH_COPY: ls = copy_launch(n >> 2); break;
+        case MH_LAUNCH_SAME_SHAPE: ls = elw_same_launch(n); break;
+        case MH_LAUNCH_ADAM: ls = adam_launch(n, true); break;
+        case MH_LAUNCH_ADAM_UNALIGNED: ls = adam_launch(n, false); break;
+        default: return fail(MH_ERR_INVALID, "mh_plan_launch: unknown launch %d", what);
+    }
+    out->kernel = ls.kernel;
+    out->threads = ls.threads;
+    out->blocks = ls.blocks;
+    return MH_OK;
 }
 
 }  // extern "C"

@@ -283,3 +283,64 @@ def test_trace_ranges_leave_results_unchanged():
     for x, y, z in zip(plain, traced, again):
         assert (x.view(np.uint32) == y.view(np.uint32)).all()
         assert (x.view(np.uint32) == z.view(np.uint32)).all()
+
+
+def _device_free_bytes():
+    import ctypes
+    hip = ctypes.CDLL("/opt/rocm/lib/libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipDeviceSynchronize() == 0
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def test_scratch_grows_geometrically_under_a_live_graph():
+    """While a captured graph exists, library scratch that grows is retired, not freed (the graph
+    may still read it), until the last graph is released. Growth then at least doubles the
+    buffer, so eager calls whose partials creep upward (axis-0 SUMs of [B, 8192] for B = 512 ...
+    4096: 1 ... 8 MiB of partials in 0.5 MiB steps) retire buffers that together stay below the
+    live one: the device's free memory drops by at most twice the largest growth in all, and
+    releasing the graph gives the retired buffers back. Every sum stays right."""
+    from util import config5_nodes, native_graph
+    eng = GpuEngine()
+    m = eng.m
+    L = m.lib()
+    m._lib.call("mh_shutdown")
+    m.init(0, asynchronous=TEST_ASYNC)
+    rows = 1025
+    onehot = np.zeros((rows, 10), np.float32)
+    onehot[np.arange(rows), synth.integers((rows,), 0, 10, 1620)] = 1
+    values = {"logits": synth.normal((rows, 10), 0, 2, 1621), "onehot": onehot}
+    g, syms, inputs = native_graph(m, config5_nodes(), values, ["logits"])
+    g.loss(syms["loss"])
+    model = m.Model(g)
+    model.parameters.tensors[syms["onehot"]] = onehot
+    model.parameters.tensors[syms["logits"]] = values["logits"]
+    model.capture("forward")
+    big_np = synth.normal((4096, 8192), 0, 1, 1622)
+    big = eng.T(big_np)
+    col = m.Tensor(m.TensorShape(1, 8192))
+    free0 = _device_free_bytes()
+    prev, drops = free0, []
+    for b in range(512, 4097, 256):
+        m._lib.check(L.mh_reduce_fwd(8, col.ptr, big.ptr, m.TensorShape(b, 8192).c(), 0), f"axis-0 SUM of [{b}, 8192]")
+        f = _device_free_bytes()
+        if prev - f > 0:
+            drops.append(prev - f)
+        prev = min(prev, f)
+        if b in (512, 2048, 4096):
+            ref = big_np[:b].astype(np.float64)
+            np.testing.assert_allclose(col.to_numpy()[0], ref.sum(axis=0), rtol=1e-5,
+                                       atol=1e-5 * float(np.abs(ref).sum(axis=0).max()))
+    total = free0 - prev
+    print(f"\n[growth] {len(drops)} growths {[d >> 20 for d in drops]} MiB, {total >> 20} MiB held", flush=True)
+    assert len(drops) >= 2, drops
+    assert total <= 2 * max(drops) + (2 << 20), (drops, total)
+    lb = model.replay("forward").to_numpy()  # the graph still reads the buffers it was captured with
+    la = model.forward(values["logits"], onehot).to_numpy()
+    assert (lb.view(np.uint32) == la.view(np.uint32)).all()
+    del model
+    import gc
+    gc.collect()
+    back = _device_free_bytes() - prev
+    assert back >= total - max(drops) - (2 << 20), (back, total, drops)
