@@ -433,6 +433,26 @@ typedef struct {
 } mh_reduce_plan_info;
 int mh_plan_unbroadcast(const mh_shape* sgrad, const mh_shape* srg, mh_reduce_plan_info* out);
 
+/* The 1-D launch an element-streaming entry point makes over n elements (host-only): `what`
+ * names it, and *out gets the kernel form (Adam: 0 the one-quad-per-thread k_adam_al, 1 the
+ * grid-stride k_adam; 0 elsewhere), the workgroup size and the number of workgroups. Every
+ * grid stays below the 2^32 work-items of one dispatch; the kernels loop over the grid for the
+ * rest (k_adam_al, which does not, only takes tensors its grid covers). */
+enum {
+    MH_LAUNCH_FILL = 0,            /* mh_fill / mh_zero, 16-byte-aligned tensor */
+    MH_LAUNCH_FILL_UNALIGNED = 1,  /* mh_fill / mh_zero, other tensors */
+    MH_LAUNCH_COPY = 2,            /* mh_memcpy_d2d of n floats, 16-byte aligned */
+    MH_LAUNCH_SAME_SHAPE = 3,      /* same-shape elementwise forward / backward, aligned */
+    MH_LAUNCH_ADAM = 4,            /* mh_adam_step, all four tensors 16-byte aligned */
+    MH_LAUNCH_ADAM_UNALIGNED = 5   /* mh_adam_step, other tensors */
+};
+typedef struct {
+    int32_t kernel;
+    int32_t threads;
+    int64_t blocks;
+} mh_launch_info;
+int mh_plan_launch(int32_t what, int64_t n, mh_launch_info* out);
+
 #ifdef __cplusplus
 }
 #endif

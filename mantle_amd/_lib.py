@@ -41,6 +41,13 @@ class mh_reduce_plan_info(ctypes.Structure):
                 ("b", ctypes.c_int64 * MAX_RANK), ("c", ctypes.c_int64 * MAX_RANK)]
 
 
+class mh_launch_info(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_int32), ("threads", ctypes.c_int32), ("blocks", ctypes.c_int64)]
+
+
+LAUNCH_FILL, LAUNCH_FILL_UNALIGNED, LAUNCH_COPY, LAUNCH_SAME_SHAPE, LAUNCH_ADAM, LAUNCH_ADAM_UNALIGNED = range(6)
+
+
 class mh_attrs(ctypes.Structure):
     """AttributeVector entries of the ops on this path (mantle/autograd/attributes.mojo)."""
     _fields_ = [("flags", ctypes.c_int32), ("axis", ctypes.c_int32), ("negative_slope", ctypes.c_float),
@@ -154,6 +161,7 @@ SIGNATURES = {
     "mh_model_info": [_VP, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_int32)],
     "mh_plan_binary": [_S, _S, _S, ctypes.POINTER(mh_plan_info)],
     "mh_plan_unbroadcast": [_S, _S, ctypes.POINTER(mh_reduce_plan_info)],
+    "mh_plan_launch": [ctypes.c_int32, _I64, ctypes.POINTER(mh_launch_info)],
 }
 _RESTYPE = {"mh_last_error": ctypes.c_char_p, "mh_status_string": ctypes.c_char_p}
 

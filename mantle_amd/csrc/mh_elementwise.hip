@@ -622,12 +622,12 @@ __global__ void __launch_bounds__(kThreads)
 // ---------------------------------------------------------------------------------------
 static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-static inline unsigned grid_for(int64_t items, int64_t per_block) {
-    int64_t b = (items + per_block - 1) / per_block;
-    if (b < 1) b = 1;
-    if (b > 0x7fffffff) b = 0x7fffffff;
-    return (unsigned)b;
-}
+// Every kernel launched over grid_for(items) loops over its grid: items beyond what one
+// dispatch holds take further iterations.
+static inline unsigned grid_for(int64_t items, int per_block) { return (unsigned)grid_blocks(items, per_block); }
+
+// The same-shape engine's launch (k_same4, k_bwd2_same4): a thread per quad.
+LaunchShape elw_same_launch(int64_t n) { return LaunchShape{0, kThreads, grid_blocks(n >> 2, kThreads)}; }
 
 // Runs F over the plan: out (shape = plan output) = F(inputs), or out += F(inputs).
 template <class F, int NIN, bool ACCUM>

@@ -345,10 +345,7 @@ int mh_bias_relu_fwd(float* y, float* r, const float* x, const mh_shape* psx, co
     }
     const bool big = n >= ((int64_t)1 << 31);
     const bool inner4 = pl.vec_ok && al16f(bias);
-    int64_t blocks = ((n >> 2) + kFFwdThreads - 1) / kFFwdThreads;
-    if (blocks < 1) blocks = 1;
-    if (blocks > 0x7fffffff) blocks = 0x7fffffff;
-    dim3 g((unsigned)blocks), b(kFFwdThreads);
+    dim3 g((unsigned)grid_blocks(n >> 2, kFFwdThreads)), b(kFFwdThreads);  // both kernels loop over the grid
     hipStream_t st = ctx().stream;
     int64_t N = 0, C = 0, S = 0;
     if (!big && pl.kind[1] != IN_FULL && plane_form(pl, &N, &C, &S) && S % 4 == 0) {

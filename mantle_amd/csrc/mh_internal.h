@@ -105,6 +105,29 @@ int require_init();
 // End of an entry point: checks the launch and synchronises unless MH_INIT_ASYNC.
 int finish(const char* what);
 // Library scratch of at least `bytes` (synchronises before growing).
+// A dispatch holds fewer than 2^32 work-items per grid dimension (the AQL packet's grid size
+// is 32-bit), so a 1-D launch of `per_block`-thread workgroups has at most this many.
+constexpr int64_t kMaxDispatchItems = ((int64_t)1 << 32) - 1;
+constexpr int64_t max_grid_blocks(int per_block) { return kMaxDispatchItems / per_block; }
+// Workgroups to give each of `items` a thread, clamped to what one dispatch holds; the
+// kernels launched this way loop over the grid for what lies beyond.
+inline int64_t grid_blocks(int64_t items, int per_block) {
+    int64_t b = (items + per_block - 1) / per_block;
+    if (b < 1) b = 1;
+    return b > max_grid_blocks(per_block) ? max_grid_blocks(per_block) : b;
+}
+
+// Launch shapes of the element-streaming entry points (what mh_plan_launch reports).
+struct LaunchShape {
+    int32_t kernel;   // entry-point specific form (Adam: 0 k_adam_al, 1 k_adam)
+    int32_t threads;  // per workgroup
+    int64_t blocks;
+};
+LaunchShape fill_launch(int64_t n, bool aligned);
+LaunchShape copy_launch(int64_t nquads);
+LaunchShape elw_same_launch(int64_t n);
+LaunchShape adam_launch(int64_t n, bool aligned);
+
 int scratch(size_t bytes, void** out);
 // A second library buffer for intermediates that live across calls using scratch().
 int stage(size_t bytes, void** out);

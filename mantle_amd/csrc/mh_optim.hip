@@ -186,12 +186,19 @@ __global__ void __launch_bounds__(kOThreads) k_adam_multi(AdamTable tab, int64_t
     }
 }
 
-static inline unsigned grid_units(int64_t units) {
-    int64_t b = (units + kOThreads - 1) / kOThreads;
-    if (b < 1) b = 1;
-    if (b > 0x7fffffff) b = 0x7fffffff;
-    return (unsigned)b;
+static inline unsigned grid_units(int64_t units) { return (unsigned)grid_blocks(units, kOThreads); }
+
+// k_adam_al gives every quad, and the tail after the last one, a thread of its own with no
+// loop, so it takes the aligned tensors whose quads fit one dispatch; every other tensor goes
+// through k_adam, which loops over its grid.
+static LaunchShape adam_shape(int64_t n, UnitMap um) {
+    const int64_t al_items = (n >> 2) + 1;
+    if (um.vec && um.sh == 0 && al_items <= max_grid_blocks(kOThreads) * kOThreads)
+        return LaunchShape{0, kOThreads, grid_blocks(al_items, kOThreads)};
+    return LaunchShape{1, kOThreads, grid_blocks(adam_units(n, um.sh), kOThreads)};
 }
+
+LaunchShape adam_launch(int64_t n, bool aligned) { return adam_shape(n, UnitMap{0, aligned ? 1 : 0}); }
 
 static int check_hyper(const char* what, float lr, float b1, float b2, float eps, int64_t iter) {
     if (iter < 1) return fail(MH_ERR_INVALID, "%s: iter %lld (Adam.step counts from 1)", what, (long long)iter);
@@ -216,12 +223,13 @@ int mh_adam_step(float* param, const float* grad, float* m, float* v, int64_t n,
     MH_TRY(require_init());
     const AdamScal s = adam_scalars(lr, beta1, beta2, eps, iter);
     const UnitMap um = unit_map(param, grad, m, v);
-    if (um.vec && um.sh == 0)
-        hipLaunchKernelGGL(k_adam_al, dim3(grid_units((n >> 2) + 1)), dim3(kOThreads), 0, ctx().stream, param, grad,
-                           m, v, n, s);
+    const LaunchShape ls = adam_shape(n, um);
+    if (ls.kernel == 0)
+        hipLaunchKernelGGL(k_adam_al, dim3((unsigned)ls.blocks), dim3(ls.threads), 0, ctx().stream, param, grad, m, v,
+                           n, s);
     else
-        hipLaunchKernelGGL(k_adam, dim3(grid_units(adam_units(n, um.sh))), dim3(kOThreads), 0, ctx().stream, param,
-                           grad, m, v, n, um, s);
+        hipLaunchKernelGGL(k_adam, dim3((unsigned)ls.blocks), dim3(ls.threads), 0, ctx().stream, param, grad, m, v, n,
+                           um, s);
     return finish("mh_adam_step");
 }
 

@@ -264,3 +264,30 @@ def test_fused_row_wrappers_check_shapes_before_any_launch(monkeypatch, fn, args
                 f(*make(a, how))
             assert e.value.code == _lib.ERR_SHAPE and a in str(e.value)
     assert len(calls) == 1  # no mismatched call reached the library
+
+
+@pytest.mark.parametrize("what", range(6))
+def test_launch_grids_fit_one_dispatch(what):
+    """Every element-streaming launch stays below the 2^32 work-items of one dispatch, up to
+    tensors of 2^40 elements (no 64 GiB device run needed to see it), and covers the tensor in
+    one pass wherever that fits (the kernels loop over the grid beyond)."""
+    L = _lib.lib()
+    info = _lib.mh_launch_info()
+    per_thread = {_lib.LAUNCH_FILL_UNALIGNED: 1}.get(what, 4)
+    for n in (1, 1000, 1 << 28, (1 << 34) - 4, 1 << 34, (1 << 34) + 5, 1 << 36, 1 << 40):
+        assert L.mh_plan_launch(what, n, ctypes.byref(info)) == 0, L.mh_last_error()
+        items = info.blocks * info.threads
+        assert 1 <= info.blocks and items < (1 << 32), (what, n, info.blocks, info.threads)
+        need = (n + per_thread - 1) // per_thread
+        if need < (1 << 32) - info.threads:
+            assert items >= need, (what, n, items, need)  # one pass covers the tensor
+        if what == _lib.LAUNCH_ADAM:
+            # k_adam_al has no stride loop: it takes only tensors whose quads and tail its grid covers
+            fits = (n >> 2) + 1 <= ((1 << 32) - 1) // info.threads * info.threads
+            assert info.kernel == (0 if fits else 1), (n, info.kernel)
+            if info.kernel == 0:
+                assert items >= (n >> 2) + 1
+        elif what == _lib.LAUNCH_ADAM_UNALIGNED:
+            assert info.kernel == 1
+    assert L.mh_plan_launch(6, 10, ctypes.byref(info)) == _lib.ERR_INVALID
+    assert L.mh_plan_launch(0, -1, ctypes.byref(info)) == _lib.ERR_INVALID
