@@ -1,9 +1,11 @@
 """mh_reduce_fwd_noalloc (the no-allocation form of mh_reduce_fwd, for callers that cannot
 allocate device memory) against mh_reduce_fwd through the C ABI: the same kernels, so the same
 bits, on two calls in a row with the second smaller, for SUM / MEAN / MAX over axis 0, the last
-axis and all elements. The no-allocation calls run first, and the device's free memory does not
-drop across them (mh_reduce_fwd would allocate 8 MiB of partials for the first shape in a
-fresh library); a small call before them has the runtime load the kernels' code object."""
+axis and all elements. The library is shut down and initialised again first, so it holds no
+scratch buffer; the no-allocation calls then run, and the device's free memory does not drop
+across them. A small call before them has the runtime load the kernels' code object. As a
+positive control, mh_reduce_fwd over axis 0 of [8192, 8192] right after them must allocate
+its 8 MiB of partials, and the same probe must see that drop."""
 from __future__ import annotations
 
 import ctypes
@@ -12,7 +14,7 @@ import numpy as np
 import pytest
 
 from mantle_amd import synth
-from util import GpuEngine
+from util import TEST_ASYNC, GpuEngine
 
 pytestmark = pytest.mark.gpu
 
@@ -40,15 +42,18 @@ def test_noalloc_matches_reduce_fwd(axis_kind):
     cases = [(big, (8192, 8192)), (small, (777, 300))]  # the second call is smaller
     axis = {"axis0": 0, "last": 1, "all": -1}[axis_kind]
     outs = {}
-    f0 = _free_bytes()
     for op in (8, 9, 10):  # SUM, MEAN, MAX
         for k, (t, shape) in enumerate(cases):
             rshape = (1,) if axis < 0 else tuple(1 if i == axis else d for i, d in enumerate(shape))
             r = m.Tensor(m.TensorShape(*rshape))
             outs[(op, k)] = r
+    warm = m.Tensor(m.TensorShape(1))
+    # an empty library: earlier calls in this process may have grown its scratch, which
+    # mh_shutdown frees (device tensors stay valid across it)
+    m._lib.call("mh_shutdown")
+    m.init(0, asynchronous=TEST_ASYNC)
     # one small call first: the HIP runtime loads a module's code object on the first launch of
     # one of its kernels, which takes device memory once per process (not the entry point's)
-    warm = m.Tensor(m.TensorShape(1))
     m._lib.check(L.mh_reduce_fwd_noalloc(8, warm.ptr, small.ptr, m.TensorShape(777 * 300).c(), -1), "warm-up")
     f1 = _free_bytes()  # result tensors allocated above, outside the measured span
     for op in (8, 9, 10):
@@ -57,13 +62,18 @@ def test_noalloc_matches_reduce_fwd(axis_kind):
                          f"noalloc op {op} call {k}")
     f2 = _free_bytes()
     assert f1 - f2 < (1 << 20), f"free memory dropped by {f1 - f2} bytes across the no-allocation calls"
+    # positive control: the allocating form grows the (empty) library scratch by its partials
+    col = m.Tensor(m.TensorShape(1, 8192))
+    f3 = _free_bytes()
+    m._lib.check(L.mh_reduce_fwd(8, col.ptr, big.ptr, m.TensorShape(8192, 8192).c(), 0), "reduce_fwd axis 0")
+    f4 = _free_bytes()
+    assert f3 - f4 >= (4 << 20), f"mh_reduce_fwd's partials were not seen: free memory dropped by {f3 - f4} bytes"
     for op in (8, 9, 10):
         for k, (t, shape) in enumerate(cases):
             got = outs[(op, k)].to_numpy()
             ref = m.Tensor(outs[(op, k)].shape())
             m._lib.check(L.mh_reduce_fwd(op, ref.ptr, t.ptr, m.TensorShape(*shape).c(), axis), "reduce_fwd")
             assert (got.view(np.uint32) == ref.to_numpy().view(np.uint32)).all(), (axis_kind, op, k)
-    assert f0 >= f1
 
 
 def test_noalloc_rejects_partials_beyond_its_scratch():
