@@ -995,6 +995,59 @@ def cpu_baseline(n_sample: int, reps: int, expo: float):
     return out
 
 
+def _fracs(d, strip=""):
+    return {k.replace(strip, ""): v["frac"] for k, v in d.items() if isinstance(v, dict) and "frac" in v}
+
+
+def _lowest(fr):
+    k = min(fr, key=fr.get)
+    return [k, fr[k]]
+
+
+def summary(out):
+    """A compact digest of every config, written as the JSON line's last key so that a reader
+    who keeps only the end of the line still sees all of them: each op family's streamed
+    fraction of peak, the lowest family and the total per config, the copy ceiling at that
+    tensor size, and the CPU baseline figure (GB/s, same byte accounting)."""
+    s = {}
+    cpu = out.get("cpu_baseline") or {}
+    cpu_cfg = cpu.get("configs", {})
+    if out.get("ops"):
+        fr = _fracs(out["ops"])
+        s["c2"] = {"step": out["config"]["frac_of_peak"], "lowest": _lowest(fr), "highest": [max(fr, key=fr.get),
+                   max(fr.values())], "cpu_GB/s": cpu.get("value")}
+    w = out.get("workloads", {})
+    copy = w.get("copy", {})
+    if "c3" in w:
+        c3 = w["c3"]
+        fr = _fracs(c3["op_by_op"])
+        s["c3"] = {"op_by_op": fr, "op_by_op_total": c3["op_by_op_total"]["frac"],
+                   "fused": _fracs(c3["fused"]), "fused_total": c3["fused_total"]["frac"],
+                   "lowest": _lowest({**fr, **_fracs(c3["fused"])}),
+                   "copy_ceiling": copy.get("copy_c3_tensor", {}).get("frac"),
+                   "cpu_GB/s": cpu_cfg.get("c3", {}).get("value")}
+    if "c4" in w:
+        c4 = w["c4"]
+        fr = {k.replace("8192x8192.", "").replace("64x512x1024.", "3d."): v for k, v in _fracs(c4["ops"]).items()}
+        s["c4"] = {"ops": fr, "fwd_total": c4["fwd_total"]["frac"], "bwd_total": c4["bwd_total"]["frac"],
+                   "lowest": _lowest(fr), "cpu_GB/s": cpu_cfg.get("c4", {}).get("value")}
+    if "c5" in w:
+        c5 = w["c5"]
+        fr = {**_fracs(c5["fwd"]), **_fracs(c5["bwd"])}
+        s["c5"] = {"op_by_op": fr, "fwd_total": c5["fwd_total"]["frac"], "bwd_total": c5["bwd_total"]["frac"],
+                   "fused": _fracs(c5["fused"]), "fused_total": c5["fused_total"]["frac"],
+                   "model_total": c5.get("model_total", {}).get("frac"),
+                   "lowest": _lowest(fr), "copy_ceiling": copy.get("copy_c5_tensor", {}).get("frac"),
+                   "cpu_GB/s": cpu_cfg.get("c5", {}).get("value")}
+    extra = {}
+    for name in ("adam", "adj", "rows"):
+        if name in w:
+            extra.update({(k if k.startswith(name) else f"{name}.{k}"): v for k, v in _fracs(w[name]).items()})
+    if extra:
+        s["next_rows"] = extra
+    return s
+
+
 # ---------------------------------------------------------------------------------------
 # rocprofv3 summaries
 # ---------------------------------------------------------------------------------------
@@ -1383,6 +1436,7 @@ def main():
     elif rank == 0:
         out["cpu_baseline"] = None
     if rank == 0:
+        out["summary"] = summary(out)  # last: the end of the line holds every config
         print(json.dumps(out), flush=True)
 
 
