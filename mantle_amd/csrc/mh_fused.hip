@@ -214,15 +214,20 @@ __global__ void __launch_bounds__(kFThreads)
 //   rg = (y > 0 ? 1 : 0) * ug;  g = g_y + rg (0 + rg without g_y);  grad_x = grad_x + g
 // (RELU backward_op, then ADD backward_op operand 0) and adds its quad's g in order. A wave
 // covers 64 consecutive quads, so at most two planes (a plane has >= 64 quads): the wave sums
-// the lanes of its first plane into part[2 w] and those of the next plane into part[2 w + 1]
-// (+0 when there is none), each with an xor butterfly. k_bias_partials_comb then adds every
-// plane's wave partials into grad_bias in a fixed order.
+// the lanes of its first plane and those of the next plane, each with an xor butterfly. With
+// SLOTS, planes span at most kPlaneSlots waves and the partials go to a slot table [C][N][8]:
+// the first plane's partial to slot (wave - the plane's first wave), the next plane's to its
+// slot 0 (this wave is that plane's first). Without SLOTS they go to part[2 w] and
+// part[2 w + 1] (+0 when there is no next plane). k_bias_partials_comb (or _comb8 for the slot
+// table) then adds every plane's wave partials into grad_bias in a fixed order.
 constexpr int kBFlat = 64;
+constexpr int kPlaneSlots = 8;  // a plane of Sq quads spans at most (Sq + 126) / 64 waves
 
-template <bool HAS_GY, bool HAS_GX, bool HAS_PART>
+template <bool HAS_GY, bool HAS_GX, bool HAS_PART, bool SLOTS>
 __global__ void __launch_bounds__(kBFlat)
     k_bias_relu_bwd_flat(float* __restrict__ gy, float* __restrict__ gx, const float* __restrict__ y,
-                         const float* __restrict__ ug, int64_t nq, uint32_t Sq, FastDiv fsq, float* part) {
+                         const float* __restrict__ ug, int64_t nq, uint32_t Sq, FastDiv fsq, float* part,
+                         uint32_t N, uint32_t C, FastDiv fc) {
     const int lane = threadIdx.x;
     const int64_t q = (int64_t)blockIdx.x * kBFlat + lane;
     float sum = 0.0f;
@@ -254,8 +259,20 @@ __global__ void __launch_bounds__(kBFlat)
             s1 = s1 + __shfl_xor(s1, m);
         }
         if (lane == 0) {
-            part[2 * (int64_t)blockIdx.x] = s0;
-            part[2 * (int64_t)blockIdx.x + 1] = s1;
+            if (SLOTS) {
+                const uint32_t w = blockIdx.x;
+                const uint32_t n0 = fdiv(first, fc), c0 = first - n0 * C;
+                const uint32_t k0 = w - (uint32_t)(((uint64_t)first * Sq) / kBFlat);  // first plane's slot
+                part[((size_t)c0 * N + n0) * kPlaneSlots + k0] = s0;
+                const uint32_t next = first + 1;
+                if ((uint64_t)next * Sq < (uint64_t)(w + 1) * kBFlat && (uint64_t)next * Sq < (uint64_t)nq) {
+                    const uint32_t n1 = fdiv(next, fc), c1 = next - n1 * C;
+                    part[((size_t)c1 * N + n1) * kPlaneSlots] = s1;
+                }
+            } else {
+                part[2 * (int64_t)blockIdx.x] = s0;
+                part[2 * (int64_t)blockIdx.x + 1] = s1;
+            }
         }
     }
 }
@@ -275,18 +292,51 @@ __global__ void __launch_bounds__(256)
     float acc = 0.0f;
     for (int64_t n = threadIdx.x; n < N; n += 256) {
         const int64_t p = n * C + c;
-        const int64_t w0 = (p * Sq) / kBFlat, w1 = ((p + 1) * Sq - 1) / kBFlat;
+        const int64_t q0 = p * Sq;  // the plane's first quad; its waves are w0 .. w1
+        const int64_t w0 = q0 / kBFlat, w1 = (q0 + Sq - 1) / kBFlat;
+        // slot 0 where the wave begins inside the plane (w * 64 >= q0), else slot 1: the wave
+        // began in the plane before (only w0 can); no integer division on the load path
+        // every load issued before any add: a slot past w1 reloads w1's (in bounds) and adds 0
         float v[kCombPlaneWaves];
 #pragma unroll
         for (int k = 0; k < kCombPlaneWaves; ++k) {
-            const int64_t w = w0 + k;
-            // slot 0 when the plane is the wave's first, else the wave began in the plane before
-            v[k] = w <= w1 ? part[2 * w + ((w * kBFlat) / Sq == p ? 0 : 1)] : 0.0f;
+            const int64_t w = w0 + k <= w1 ? w0 + k : w1;
+            v[k] = part[2 * w + (w * kBFlat >= q0 ? 0 : 1)];
         }
+        __builtin_amdgcn_sched_barrier(0);  // keep the adds (and their waits) after every load
         float sp = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kCombPlaneWaves; ++k) sp = sp + v[k];
-        for (int64_t w = w0 + kCombPlaneWaves; w <= w1; ++w) sp = sp + part[2 * w + ((w * kBFlat) / Sq == p ? 0 : 1)];
+        for (int k = 0; k < kCombPlaneWaves; ++k) sp = sp + (w0 + k <= w1 ? v[k] : 0.0f);
+        for (int64_t w = w0 + kCombPlaneWaves; w <= w1; ++w) sp = sp + part[2 * w + (w * kBFlat >= q0 ? 0 : 1)];
+        acc = acc + sp;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
+    if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) grad_bias[c] = grad_bias[c] + (((ws[0] + ws[1]) + ws[2]) + ws[3]);
+}
+
+// The same sums over the slot table [C][N][kPlaneSlots] that k_bias_relu_bwd_flat<.., SLOTS>
+// writes: thread t reads plane (n = t, c)'s slots with two 16-byte loads (contiguous across the
+// workgroup) and adds its cnt wave partials in wave order, then +0 for each unused slot, which
+// is the order and the bits of k_bias_partials_comb.
+__global__ void __launch_bounds__(256)
+    k_bias_partials_comb8(float* __restrict__ grad_bias, const float* __restrict__ part, int64_t N, int64_t C,
+                          int64_t Sq) {
+    static_assert(kPlaneSlots == 8, "two quads per plane");
+    __shared__ float ws[4];
+    const int64_t c = blockIdx.x;
+    float acc = 0.0f;
+    for (int64_t n = threadIdx.x; n < N; n += 256) {
+        const vf4* src = reinterpret_cast<const vf4*>(part + (c * N + n) * kPlaneSlots);
+        const vf4 a = src[0], b = src[1];
+        const int64_t q0 = (n * C + c) * Sq;
+        const int64_t cnt = (q0 + Sq - 1) / kBFlat - q0 / kBFlat + 1;  // waves of the plane
+        const float v[kPlaneSlots] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        float sp = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kPlaneSlots; ++k) sp = sp + (k < cnt ? v[k] : 0.0f);
         acc = acc + sp;
     }
 #pragma unroll
@@ -398,12 +448,21 @@ int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const fl
         const int64_t nw = (nqf + kBFlat - 1) / kBFlat;
         float* part = nullptr;
         const bool has_part = grad_bias != nullptr;
-        if (has_part) MH_TRY(scratch(((size_t)(2 * nw) + 64) * sizeof(float), reinterpret_cast<void**>(&part)));
+        const bool slots = (Sq + 2 * kBFlat - 2) / kBFlat <= kPlaneSlots;  // every plane within 8 waves
+        const size_t part_floats = slots ? (size_t)(N * C) * kPlaneSlots : (size_t)(2 * nw);
+        if (has_part) MH_TRY(scratch((part_floats + 64) * sizeof(float), reinterpret_cast<void**>(&part)));
         hipStream_t st = ctx().stream;
         dim3 g((unsigned)nw), b(kBFlat);
-        const FastDiv fsq = make_fastdiv((uint32_t)Sq);
-#define MH_BRF(GY, GX, PT) \
-    hipLaunchKernelGGL((k_bias_relu_bwd_flat<GY, GX, PT>), g, b, 0, st, g_y, grad_x, y, ug, nqf, (uint32_t)Sq, fsq, part)
+        const FastDiv fsq = make_fastdiv((uint32_t)Sq), fc = make_fastdiv((uint32_t)C);
+#define MH_BRF(GY, GX, PT)                                                                                      \
+    do {                                                                                                        \
+        if (slots)                                                                                              \
+            hipLaunchKernelGGL((k_bias_relu_bwd_flat<GY, GX, PT, true>), g, b, 0, st, g_y, grad_x, y, ug, nqf,  \
+                               (uint32_t)Sq, fsq, part, (uint32_t)N, (uint32_t)C, fc);                          \
+        else                                                                                                    \
+            hipLaunchKernelGGL((k_bias_relu_bwd_flat<GY, GX, PT, false>), g, b, 0, st, g_y, grad_x, y, ug, nqf, \
+                               (uint32_t)Sq, fsq, part, (uint32_t)N, (uint32_t)C, fc);                          \
+    } while (0)
         const int sel = (g_y ? 4 : 0) | (grad_x ? 2 : 0) | (has_part ? 1 : 0);
         switch (sel) {
             case 0: return MH_OK;  // nothing to produce
@@ -416,7 +475,10 @@ int mh_bias_relu_bwd_accum(float* g_y, float* grad_x, float* grad_bias, const fl
             default: MH_BRF(true, true, true); break;
         }
 #undef MH_BRF
-        if (has_part) hipLaunchKernelGGL(k_bias_partials_comb, dim3((unsigned)C), dim3(256), 0, st, grad_bias, part, N, C, Sq);
+        if (has_part && slots)
+            hipLaunchKernelGGL(k_bias_partials_comb8, dim3((unsigned)C), dim3(256), 0, st, grad_bias, part, N, C, Sq);
+        else if (has_part)
+            hipLaunchKernelGGL(k_bias_partials_comb, dim3((unsigned)C), dim3(256), 0, st, grad_bias, part, N, C, Sq);
         return finish("mh_bias_relu_bwd_accum");
     }
     if (planes && nblocks <= 0x7fffffff) {
