@@ -696,8 +696,10 @@ def run_rows(L, reps):
 def run_graph(L, reps, steps=200):
     """One training step (zero_grad, forward, backward) of a model through the native executor,
     eager against the replay of the step captured as one HIP graph (MH_PASS_STEP): config 1's
-    ADD(bias) -> RELU graph with a MEAN loss (the launch-bound case) and config 5's head chain. Wall time per step on the host (inputs copied
-    from device buffers into their slots every step), one synchronisation per `steps` steps."""
+    ADD(bias) -> RELU graph with a MEAN loss (the launch-bound case), a deep chain of 24
+    MUL -> ADD -> RELU layers over [32, 32] and config 5's head chain. Wall time per step on the
+    host (inputs copied from device buffers into their slots every step), one synchronisation per
+    `steps` steps."""
     import time
     import mantle_amd as mm
     from mantle_amd import synth
@@ -722,7 +724,18 @@ def run_graph(L, reps, steps=200):
         onehot[np.arange(rows), synth.integers((rows,), 0, 10, 54)] = 1
         return g, [synth.normal((rows, 10), 0, 2, 53), onehot]
 
-    for name, make, n in (("c1", c1, steps), ("c5", c5, max(steps // 10, 10))):
+    def deep():  # a deep chain of small tensors: 24 layers of MUL(w) -> ADD(b) -> RELU over [32, 32]
+        g = mm.Graph()
+        x = g.input((32, 32), trainable=True)
+        h = x
+        for i in range(24):
+            w = g.param((1, 32), init=synth.normal((1, 32), 1, 0.1, 60 + 2 * i))
+            b = g.param((1, 32), init=synth.normal((1, 32), 0, 0.1, 61 + 2 * i))
+            h = g.op(mm.OP.RELU, g.op(mm.OP.ADD, g.op(mm.OP.MUL, h, w), b))
+        g.loss(g.op(mm.OP.MEAN, h))
+        return g, [synth.normal((32, 32), 0, 1, 59)]
+
+    for name, make, n in (("c1", c1, steps), ("deep", deep, steps), ("c5", c5, max(steps // 10, 10))):
         g, inputs = make()
         res = {}
         for mode in ("eager", "graph"):

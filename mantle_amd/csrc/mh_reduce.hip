@@ -1359,36 +1359,35 @@ __global__ void __launch_bounds__(kRThreads)
     }
 }
 
-// Combines of the split partials, in split order. Rows: one block per row, S partials
-// contiguous (thread-strided, then the waves' butterflies and the four waves in order).
-// Columns: partials at stride nlines, a block per 16 lines (below).
-__global__ void __launch_bounds__(kRThreads)
+// Combines of the split partials, in split order. Rows: one 1024-thread block per row, S
+// partials contiguous: thread t adds partials t, t + 1024, ... (four in flight, so a row of
+// up to kMomMaxSplit partials waits on memory once), then the waves' butterflies and the 16
+// waves in order. Columns: partials at stride nlines, a block per 16 lines (below).
+constexpr int kMomCombThreads = 1024;
+static_assert(kMomMaxSplit <= 4 * kMomCombThreads, "one round of loads per thread");
+
+__global__ void __launch_bounds__(kMomCombThreads)
     k_tstd_mom_combine_rows(float* __restrict__ res, const Mom* __restrict__ part, int64_t S, int64_t B) {
-    __shared__ Mom ws[4];
+    __shared__ Mom ws[kMomCombThreads / 64];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const Mom* p = part + (int64_t)blockIdx.x * S;
     Mom m{0.0, 0.0};
-    int64_t i = t;
-    for (; i + 3 * kRThreads < S; i += 4 * kRThreads) {  // four partials in flight, added in order
+    for (int64_t i = t; i < S; i += 4 * kMomCombThreads) {  // four partials in flight, added in order
         Mom q[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) q[u] = p[i + u * kRThreads];
+        for (int u = 0; u < 4; ++u) q[u] = i + u * kMomCombThreads < S ? p[i + u * kMomCombThreads] : Mom{0.0, 0.0};
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             m.s1 = m.s1 + q[u].s1;
             m.s2 = m.s2 + q[u].s2;
         }
     }
-    for (; i < S; i += kRThreads) {
-        m.s1 = m.s1 + p[i].s1;
-        m.s2 = m.s2 + p[i].s2;
-    }
     m = mom_wave(m);
     if (lane == 0) ws[w] = m;
     __syncthreads();
     if (t == 0) {
         Mom tot = ws[0];
-        for (int k = 1; k < 4; ++k) {
+        for (int k = 1; k < kMomCombThreads / 64; ++k) {
             tot.s1 = tot.s1 + ws[k].s1;
             tot.s2 = tot.s2 + ws[k].s2;
         }
@@ -2288,7 +2287,8 @@ int mh_tstd(float* res, const float* x, const mh_shape* psx, int32_t axis) {
         dim3 g((unsigned)(A * S)), b(kRThreads);
         if (vec) hipLaunchKernelGGL(k_tstd_mom_rows<true>, g, b, 0, st, res, x, B, L, S, part);
         else hipLaunchKernelGGL(k_tstd_mom_rows<false>, g, b, 0, st, res, x, B, L, S, part);
-        if (S > 1) hipLaunchKernelGGL(k_tstd_mom_combine_rows, dim3((unsigned)A), b, 0, st, res, part, S, B);
+        if (S > 1)
+            hipLaunchKernelGGL(k_tstd_mom_combine_rows, dim3((unsigned)A), dim3(kMomCombThreads), 0, st, res, part, S, B);
         return finish("mh_tstd");
     }
     // strided axis: a thread per column quad, about one block per CU, row splits of at least 64
