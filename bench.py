@@ -1130,10 +1130,10 @@ _N3, _N4, _N5 = 6422528, 1 << 26, 10485760
 WL_KERNELS = [
     ("c3 bias_relu.fwd (fused)", "mh::k_bias_relu_fwd_planes", 1605632, 12 * _N3 + 128, ""),
     ("c3 ADD.fwd", "void mh::k_planebc4<mh::FBin<0>, 2, false>", 1605632, 8 * _N3 + 128, ""),
-    ("c3 bias_relu.bwd (fused), stream", "void mh::k_bias_relu_bwd_flat<false, true, true>", 1605632, 16 * _N3,
-     "grad_x read and written; two bias partials per wave"),
-    ("c3 bias_relu.bwd (fused), combine", "mh::k_bias_partials_comb", 8192, 8 * (_N3 // 256) + 256,
-     "the wave partials (two per 64 quads) read, 32 bias values updated"),
+    ("c3 bias_relu.bwd (fused), stream", "void mh::k_bias_relu_bwd_flat<false, true, true, true>", 1605632, 16 * _N3,
+     "grad_x read and written; a wave's plane partials into the slot table"),
+    ("c3 bias_relu.bwd (fused), combine", "mh::k_bias_partials_comb8", 8192, 4 * 8 * (_N3 // 784) + 256,
+     "the slot table (8 slots per plane) read, 32 bias values updated"),
     ("c3 ADD.bwd_bias", "void mh::k_unb_planes<false>", 131072, 4 * _N3 + 256, "one launch, arrival tickets"),
     ("c4 [8192,8192] axis 0 MAX.fwd", "void mh::k_cols<mh::RMax, mh::LdPlain<mh::RMax>, true, true>", 262144,
      4 * _N4, "first of two launches (split partials)"),
@@ -1164,8 +1164,8 @@ WL_KERNELS = [
 WL_STATS = [("c3", "op_by_op", "ADD.bwd_bias", "void mh::k_unb_planes<false>"),
             ("c3", "fused", "bias_relu.fwd", "mh::k_bias_relu_fwd_planes"),
             ("c3", "op_by_op", "ADD.fwd", "void mh::k_planebc4<mh::FBin<0>, 2, false>"),
-            ("c3", "fused", "bias_relu.bwd", ("void mh::k_bias_relu_bwd_flat<false, true, true>",
-                                              "mh::k_bias_partials_comb")),
+            ("c3", "fused", "bias_relu.bwd", ("void mh::k_bias_relu_bwd_flat<false, true, true, true>",
+                                              "mh::k_bias_partials_comb8")),
             ("c4", "ops", "8192x8192.ax1.MAX.bwd", "void mh::k_max_bwd_rowreg<4, 8>"),
             ("c5", "fused", "fused.fwd", "void mh::k_rowp_fwd<0, 10>"),
             ("c5", "fused", "fused.bwd", "void mh::k_rowp_bwd<0, 10>"),
