@@ -763,7 +763,10 @@ def test_fused_bias_relu_matches_op_by_op(gpu):
 FUSED_SHAPES = [((8, 32, 28, 28), (1, 32, 1, 1)), ((2, 3, 64), (3, 1)), ((5, 300), (5, 1)), ((4, 6, 96), (1,)),
                 ((3, 7, 10), (1, 7, 1)), ((64, 40), (1, 40)), ((2, 3, 4, 80), (1, 3, 4, 1)), ((3, 2, 20000), (1, 2, 1)),
                 ((100, 3, 64), (1, 3, 1)), ((33, 2, 5000), (1, 2, 1)), ((7, 5, 260), (1, 5, 1)),
-                ((3, 4, 256), (1, 4, 1))]
+                ((3, 4, 256), (1, 4, 1)),
+                # planes of 449 quads: the slot table's bound, planes starting at every offset of a
+                # wave, so some span all eight slots; 450 quads: the two-slots-per-wave layout
+                ((22, 3, 1796), (1, 3, 1)), ((5, 3, 1800), (1, 3, 1))]
 
 
 @pytest.mark.parametrize("sx,sb", FUSED_SHAPES, ids=[f"{a}+{b}" for a, b in FUSED_SHAPES])
