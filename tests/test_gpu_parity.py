@@ -1015,6 +1015,8 @@ def test_fused_row_graphs(gpu, rows, classes):
 
 
 ORACLE_ROW_CASES = [(513, 17), (300, 24), (1000, 31), (40, 33), (777, 47), (1200, 64), (500, 32)]
+_rng_oracle_rows = np.random.default_rng(20261202)
+ORACLE_ROW_CASES += [(int(_rng_oracle_rows.integers(1, 1500)), int(_rng_oracle_rows.integers(17, 65))) for _ in range(6)]
 
 
 @pytest.mark.parametrize("rows,classes", ORACLE_ROW_CASES, ids=[f"{r}x{c}" for r, c in ORACLE_ROW_CASES])
