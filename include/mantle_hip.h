@@ -435,11 +435,13 @@ typedef struct {
 } mh_reduce_plan_info;
 int mh_plan_unbroadcast(const mh_shape* sgrad, const mh_shape* srg, mh_reduce_plan_info* out);
 
-/* The 1-D launch an element-streaming entry point makes over n elements (host-only): `what`
+/* The 1-D launches an element-streaming entry point makes over n elements (host-only): `what`
  * names it, and *out gets the kernel form (Adam: 0 the one-quad-per-thread k_adam_al, 1 the
- * grid-stride k_adam; 0 elsewhere), the workgroup size and the number of workgroups. Every
- * grid stays below the 2^32 work-items of one dispatch; the kernels loop over the grid for the
- * rest (k_adam_al, which does not, only takes tensors its grid covers). */
+ * grid-stride k_adam; 0 elsewhere), the workgroup size, the number of workgroups of a launch
+ * and the number of launches. Every grid stays below the 2^32 work-items of one dispatch: the
+ * one-quad-per-thread kernels (fill, copy, same-shape ops) cover at most 2^31 quads per launch
+ * and longer tensors take several launches; the unaligned fill and k_adam loop over their grid
+ * (k_adam_al, which does not, only takes tensors its grid covers). */
 enum {
     MH_LAUNCH_FILL = 0,            /* mh_fill / mh_zero, 16-byte-aligned tensor */
     MH_LAUNCH_FILL_UNALIGNED = 1,  /* mh_fill / mh_zero, other tensors */
@@ -452,6 +454,7 @@ typedef struct {
     int32_t kernel;
     int32_t threads;
     int64_t blocks;
+    int64_t launches;
 } mh_launch_info;
 int mh_plan_launch(int32_t what, int64_t n, mh_launch_info* out);
 

@@ -42,7 +42,8 @@ class mh_reduce_plan_info(ctypes.Structure):
 
 
 class mh_launch_info(ctypes.Structure):
-    _fields_ = [("kernel", ctypes.c_int32), ("threads", ctypes.c_int32), ("blocks", ctypes.c_int64)]
+    _fields_ = [("kernel", ctypes.c_int32), ("threads", ctypes.c_int32), ("blocks", ctypes.c_int64),
+                ("launches", ctypes.c_int64)]
 
 
 LAUNCH_FILL, LAUNCH_FILL_UNALIGNED, LAUNCH_COPY, LAUNCH_SAME_SHAPE, LAUNCH_ADAM, LAUNCH_ADAM_UNALIGNED = range(6)

@@ -208,9 +208,10 @@ struct FFmaRg {  // FMA.backward, basics.mojo:804-817: id 0 ug * t2, id 1 ug * t
 // ---------------------------------------------------------------------------------------
 
 // Same-shape engine: all inputs FULL or SCALAR (bit k of smask). One quad (16 B per
-// stream) per thread per iteration: on gfx950 this streams faster than several quads per
-// thread (fewer bytes in flight per wave, more waves resident). The launch covers every quad
-// in one iteration up to 2^31 blocks; the stride loop only matters beyond that.
+// stream) per thread, and no loop: on gfx950 this streams faster than several quads per
+// thread (fewer bytes in flight per wave, more waves resident), and at config-5 sizes a grid
+// loop that ran once still cost about 6 %. A launch covers at most kMaxLaunchQuads quads
+// (the launcher splits longer tensors); block 0's first thread takes the n % 4 tail.
 template <class F, int NIN, bool ACCUM>
 __global__ void __launch_bounds__(kThreads)
     k_same4(float* __restrict__ out, InPtrs<NIN> in, int smask, int64_t n, DevScal ds, F f) {
@@ -219,8 +220,8 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int k = 0; k < NIN; ++k) sv[k] = ((smask >> k) & 1) ? in.p[k][0] : 0.0f;
     const int64_t nq = n >> 2;
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
+    const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (q < nq) {
         float4 iv[NIN > 0 ? NIN : 1];
         float4 ov;
 #pragma unroll
@@ -236,8 +237,8 @@ __global__ void __launch_bounds__(kThreads)
             r[j] = f(v);
             if (ACCUM) r[j] = comp(ov, j) + r[j];
         }
-        if (ACCUM && kSparseAccum<F> && !bits_differ4(ov.x, ov.y, ov.z, ov.w, r[0], r[1], r[2], r[3])) continue;
-        st_nt4(out, q, make_float4(r[0], r[1], r[2], r[3]));
+        if (!(ACCUM && kSparseAccum<F>) || bits_differ4(ov.x, ov.y, ov.z, ov.w, r[0], r[1], r[2], r[3]))
+            st_nt4(out, q, make_float4(r[0], r[1], r[2], r[3]));
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         for (int64_t i = nq << 2; i < n; ++i) {
@@ -287,8 +288,8 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int k = 0; k < NIN; ++k) sv[k] = ((kinds >> (2 * k)) & 3) == IN_SCALAR ? in.p[k][0] : 0.0f;
     const int64_t nq = n >> 2;
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
+    const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (q < nq) {
         const uint32_t e0 = (uint32_t)(q << 2);
         const uint32_t r0 = fdiv(e0, fk);
         const uint32_t c0 = e0 - r0 * K;
@@ -320,8 +321,8 @@ __global__ void __launch_bounds__(kThreads)
             const float fv = f(v[j]);
             r[j] = ACCUM ? o[j] + fv : fv;
         }
-        if (ACCUM && kSparseAccum<F> && !bits_differ4(o[0], o[1], o[2], o[3], r[0], r[1], r[2], r[3])) continue;
-        st_ntv(out, q, r);
+        if (!(ACCUM && kSparseAccum<F>) || bits_differ4(o[0], o[1], o[2], o[3], r[0], r[1], r[2], r[3]))
+            st_ntv(out, q, r);
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         for (int64_t i = nq << 2; i < n; ++i) {
@@ -352,8 +353,8 @@ __global__ void __launch_bounds__(kThreads)
     float sv[NA];
 #pragma unroll
     for (int k = 0; k < NIN; ++k) sv[k] = ((kinds >> (2 * k)) & 3) == IN_SCALAR ? in.p[k][0] : 0.0f;
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
+    const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (q < nq) {
         const uint32_t cq = (uint32_t)q - fdiv((uint32_t)q, fcq) * Cq;
         vf4 t[NA];
 #pragma unroll
@@ -374,8 +375,8 @@ __global__ void __launch_bounds__(kThreads)
             const float fv = f(v);
             r[j] = ACCUM ? o[j] + fv : fv;
         }
-        if (ACCUM && kSparseAccum<F> && !bits_differ4(o[0], o[1], o[2], o[3], r[0], r[1], r[2], r[3])) continue;
-        st_ntv(out, q, r);
+        if (!(ACCUM && kSparseAccum<F>) || bits_differ4(o[0], o[1], o[2], o[3], r[0], r[1], r[2], r[3]))
+            st_ntv(out, q, r);
     }
 }
 
@@ -392,8 +393,8 @@ __global__ void __launch_bounds__(kThreads)
     float sv[NA];
 #pragma unroll
     for (int k = 0; k < NIN; ++k) sv[k] = ((kinds >> (2 * k)) & 3) == IN_SCALAR ? in.p[k][0] : 0.0f;
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
+    const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (q < nq) {
         const uint32_t p = fdiv((uint32_t)q, fsq);
         const uint32_t c = p - fdiv(p, fc) * C;
         vf4 t[NA];
@@ -418,8 +419,8 @@ __global__ void __launch_bounds__(kThreads)
             const float fv = f(v);
             r[j] = ACCUM ? o[j] + fv : fv;
         }
-        if (ACCUM && kSparseAccum<F> && !bits_differ4(o[0], o[1], o[2], o[3], r[0], r[1], r[2], r[3])) continue;
-        st_ntv(out, q, r);
+        if (!(ACCUM && kSparseAccum<F>) || bits_differ4(o[0], o[1], o[2], o[3], r[0], r[1], r[2], r[3]))
+            st_ntv(out, q, r);
     }
 }
 
@@ -562,8 +563,8 @@ __global__ void __launch_bounds__(kThreads)
 }
 
 // Fused two-operand backward of a same-shape binary op (both backward_op calls of
-// ops.mojo:408-463 with equal shapes): g1 = g1 + rg0, g2 = g2 + rg1. One quad per thread per
-// iteration, as k_same4. ALIAS: both operands are one symbol (x * x, x + x), so both calls
+// ops.mojo:408-463 with equal shapes): g1 = g1 + rg0, g2 = g2 + rg1. One quad per thread, no
+// loop, as k_same4. ALIAS: both operands are one symbol (x * x, x + x), so both calls
 // accumulate into one gradient, id 0 first (model.mojo:233-270): g1 = (g1 + rg0) + rg1, and
 // g2 is not used.
 template <int OP, bool ALIAS = false>
@@ -572,10 +573,10 @@ __global__ void __launch_bounds__(kThreads)
                  const float* __restrict__ a, const float* __restrict__ b, int64_t n) {
     constexpr bool NEED_AB = (OP == MH_MUL || OP == MH_DIV);
     const int64_t nq = n >> 2;
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
     FBinRg<OP, 0, false> f0;
     FBinRg<OP, 1, false> f1;
-    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
+    const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (q < nq) {
         const float4 vu = ld_nt4(ug, q);
         float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vb = va;
         if (NEED_AB) {
@@ -622,12 +623,17 @@ __global__ void __launch_bounds__(kThreads)
 // ---------------------------------------------------------------------------------------
 static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Every kernel launched over grid_for(items) loops over its grid: items beyond what one
-// dispatch holds take further iterations.
+// Workgroups of a launch of one thread per item. The one-quad-per-thread kernels get at most
+// kMaxLaunchQuads items per launch (every launch site splits longer tensors); k_bcast4 and
+// k_same1, which loop over their grid, take the clamped grid whatever the count.
 static inline unsigned grid_for(int64_t items, int per_block) { return (unsigned)grid_blocks(items, per_block); }
 
-// The same-shape engine's launch (k_same4, k_bwd2_same4): a thread per quad.
-LaunchShape elw_same_launch(int64_t n) { return LaunchShape{0, kThreads, grid_blocks(n >> 2, kThreads)}; }
+// The same-shape engine's launch (k_same4, k_bwd2_same4): a thread per quad, in launches of at
+// most kMaxLaunchQuads quads.
+LaunchShape elw_same_launch(int64_t n) {
+    const int64_t nq = n >> 2;
+    return LaunchShape{0, kThreads, grid_blocks(nq < kMaxLaunchQuads ? nq : kMaxLaunchQuads, kThreads), launch_count(nq)};
+}
 
 // Runs F over the plan: out (shape = plan output) = F(inputs), or out += F(inputs).
 template <class F, int NIN, bool ACCUM>
@@ -643,9 +649,15 @@ static int run_map(float* out, const ElwPlan& pl, const float* const* ptrs, cons
         int smask = 0;
         for (int k = 0; k < NIN; ++k)
             if (pl.kind[k] == IN_SCALAR) smask |= 1 << k;
-        if (al) {
-            hipLaunchKernelGGL((k_same4<F, NIN, ACCUM>), dim3(grid_for(pl.n >> 2, kThreads)),
-                               dim3(kThreads), 0, st, out, in, smask, pl.n, ds, f);
+        if (al) {  // a thread per quad; past kMaxLaunchQuads quads, several launches
+            for (int64_t off = 0; off < pl.n; off += 4 * kMaxLaunchQuads) {
+                const int64_t cnt = pl.n - off < 4 * kMaxLaunchQuads ? pl.n - off : 4 * kMaxLaunchQuads;
+                InPtrs<NIN> part = in;
+                for (int k = 0; k < NIN; ++k)
+                    if (!((smask >> k) & 1)) part.p[k] += off;
+                hipLaunchKernelGGL((k_same4<F, NIN, ACCUM>), dim3(grid_for(cnt >> 2, kThreads)), dim3(kThreads), 0,
+                                   st, out + off, part, smask, cnt, ds, f);
+            }
         } else {
             int64_t b = (pl.n + kThreads - 1) / kThreads;
             if (b > 65536) b = 65536;
@@ -1072,23 +1084,31 @@ int mh_binary_bwd_accum2(int op, float* grad1, float* grad2, const float* ug, co
     const bool need_ab = op == MH_MUL || op == MH_DIV;
     if (!ug || (need_ab && (!t1 || !t2))) return fail(MH_ERR_NULL, "mh_binary_bwd_accum2: null tensor");
     MH_TRY(require_init());
-    const int64_t n = nel;
-    dim3 g(grid_for(n >> 2, kThreads)), b(kThreads);
     hipStream_t st = ctx().stream;
-    if (alias) {  // g2 is not read: pass a null pointer so no access can go through it
-        switch (op) {
-            case MH_ADD: hipLaunchKernelGGL((k_bwd2_same4<MH_ADD, true>), g, b, 0, st, grad1, nullptr, ug, t1, t2, n); break;
-            case MH_SUB: hipLaunchKernelGGL((k_bwd2_same4<MH_SUB, true>), g, b, 0, st, grad1, nullptr, ug, t1, t2, n); break;
-            case MH_MUL: hipLaunchKernelGGL((k_bwd2_same4<MH_MUL, true>), g, b, 0, st, grad1, nullptr, ug, t1, t2, n); break;
-            default: hipLaunchKernelGGL((k_bwd2_same4<MH_DIV, true>), g, b, 0, st, grad1, nullptr, ug, t1, t2, n); break;
+    // a thread per quad; past kMaxLaunchQuads quads, several launches over offset pointers
+    for (int64_t off = 0; off < nel; off += 4 * kMaxLaunchQuads) {
+        const int64_t n = nel - off < 4 * kMaxLaunchQuads ? nel - off : 4 * kMaxLaunchQuads;
+        dim3 g(grid_for(n >> 2, kThreads)), b(kThreads);
+        float* g1 = grad1 + off;
+        const float* u = ug + off;
+        const float* a = t1 ? t1 + off : nullptr;  // ADD and SUB do not read the operands
+        const float* c = t2 ? t2 + off : nullptr;
+        if (alias) {  // g2 is not read: pass a null pointer so no access can go through it
+            switch (op) {
+                case MH_ADD: hipLaunchKernelGGL((k_bwd2_same4<MH_ADD, true>), g, b, 0, st, g1, nullptr, u, a, c, n); break;
+                case MH_SUB: hipLaunchKernelGGL((k_bwd2_same4<MH_SUB, true>), g, b, 0, st, g1, nullptr, u, a, c, n); break;
+                case MH_MUL: hipLaunchKernelGGL((k_bwd2_same4<MH_MUL, true>), g, b, 0, st, g1, nullptr, u, a, c, n); break;
+                default: hipLaunchKernelGGL((k_bwd2_same4<MH_DIV, true>), g, b, 0, st, g1, nullptr, u, a, c, n); break;
+            }
+            continue;
         }
-        return finish("mh_binary_bwd_accum2");
-    }
-    switch (op) {
-        case MH_ADD: hipLaunchKernelGGL(k_bwd2_same4<MH_ADD>, g, b, 0, st, grad1, grad2, ug, t1, t2, n); break;
-        case MH_SUB: hipLaunchKernelGGL(k_bwd2_same4<MH_SUB>, g, b, 0, st, grad1, grad2, ug, t1, t2, n); break;
-        case MH_MUL: hipLaunchKernelGGL(k_bwd2_same4<MH_MUL>, g, b, 0, st, grad1, grad2, ug, t1, t2, n); break;
-        default: hipLaunchKernelGGL(k_bwd2_same4<MH_DIV>, g, b, 0, st, grad1, grad2, ug, t1, t2, n); break;
+        float* g2 = grad2 + off;
+        switch (op) {
+            case MH_ADD: hipLaunchKernelGGL(k_bwd2_same4<MH_ADD>, g, b, 0, st, g1, g2, u, a, c, n); break;
+            case MH_SUB: hipLaunchKernelGGL(k_bwd2_same4<MH_SUB>, g, b, 0, st, g1, g2, u, a, c, n); break;
+            case MH_MUL: hipLaunchKernelGGL(k_bwd2_same4<MH_MUL>, g, b, 0, st, g1, g2, u, a, c, n); break;
+            default: hipLaunchKernelGGL(k_bwd2_same4<MH_DIV>, g, b, 0, st, g1, g2, u, a, c, n); break;
+        }
     }
     return finish("mh_binary_bwd_accum2");
 }

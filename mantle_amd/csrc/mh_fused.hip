@@ -94,12 +94,12 @@ __global__ void __launch_bounds__(kFFwdThreads)
 
 // Forward over [N, C, S] planes (S % 4 == 0, fewer than 2^31 elements; the bias indexed by C,
 // or a scalar with C == 1): one quad per thread in flat order, its channel
-// (q / (S / 4)) mod C from two fast divisions.
+// (q / (S / 4)) mod C from two fast divisions. No grid loop: one launch covers the tensor.
 __global__ void __launch_bounds__(kFFwdThreads)
     k_bias_relu_fwd_planes(float* __restrict__ y, float* __restrict__ r, const float* __restrict__ x,
                            const float* __restrict__ bias, int64_t nq, uint32_t C, FastDiv fsq, FastDiv fc) {
-    const int64_t stride = (int64_t)gridDim.x * kFFwdThreads;
-    for (int64_t q = (int64_t)blockIdx.x * kFFwdThreads + threadIdx.x; q < nq; q += stride) {
+    const int64_t q = (int64_t)blockIdx.x * kFFwdThreads + threadIdx.x;
+    if (q < nq) {
         const uint32_t p = fdiv((uint32_t)q, fsq);
         const float bv = bias[p - fdiv(p, fc) * C];
         const vf4 xv = ld_ntv(x, q);
@@ -395,7 +395,9 @@ int mh_bias_relu_fwd(float* y, float* r, const float* x, const mh_shape* psx, co
     }
     const bool big = n >= ((int64_t)1 << 31);
     const bool inner4 = pl.vec_ok && al16f(bias);
-    dim3 g((unsigned)grid_blocks(n >> 2, kFFwdThreads)), b(kFFwdThreads);  // both kernels loop over the grid
+    // the plane kernel (below 2^31 elements) covers every quad with this grid; k_bias_relu_fwd4
+    // loops over it beyond one dispatch
+    dim3 g((unsigned)grid_blocks(n >> 2, kFFwdThreads)), b(kFFwdThreads);
     hipStream_t st = ctx().stream;
     int64_t N = 0, C = 0, S = 0;
     if (!big && pl.kind[1] != IN_FULL && plane_form(pl, &N, &C, &S) && S % 4 == 0) {

@@ -117,11 +117,18 @@ inline int64_t grid_blocks(int64_t items, int per_block) {
     return b > max_grid_blocks(per_block) ? max_grid_blocks(per_block) : b;
 }
 
+// The one-quad-per-thread kernels (no grid loop: at config-5 sizes a loop that runs once
+// still cost 6 % of a row-broadcast op) cover at most this many quads per launch; a longer
+// tensor runs as several launches over offset pointers.
+constexpr int64_t kMaxLaunchQuads = (int64_t)1 << 31;
+inline int64_t launch_count(int64_t nq) { return nq <= kMaxLaunchQuads ? 1 : (nq + kMaxLaunchQuads - 1) / kMaxLaunchQuads; }
+
 // Launch shapes of the element-streaming entry points (what mh_plan_launch reports).
 struct LaunchShape {
-    int32_t kernel;   // entry-point specific form (Adam: 0 k_adam_al, 1 k_adam)
-    int32_t threads;  // per workgroup
-    int64_t blocks;
+    int32_t kernel;    // entry-point specific form (Adam: 0 k_adam_al, 1 k_adam)
+    int32_t threads;   // per workgroup
+    int64_t blocks;    // workgroups of the (first) launch
+    int64_t launches;  // launches over the tensor
 };
 LaunchShape fill_launch(int64_t n, bool aligned);
 LaunchShape copy_launch(int64_t nquads);

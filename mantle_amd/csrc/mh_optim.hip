@@ -194,8 +194,8 @@ static inline unsigned grid_units(int64_t units) { return (unsigned)grid_blocks(
 static LaunchShape adam_shape(int64_t n, UnitMap um) {
     const int64_t al_items = (n >> 2) + 1;
     if (um.vec && um.sh == 0 && al_items <= max_grid_blocks(kOThreads) * kOThreads)
-        return LaunchShape{0, kOThreads, grid_blocks(al_items, kOThreads)};
-    return LaunchShape{1, kOThreads, grid_blocks(adam_units(n, um.sh), kOThreads)};
+        return LaunchShape{0, kOThreads, grid_blocks(al_items, kOThreads), 1};
+    return LaunchShape{1, kOThreads, grid_blocks(adam_units(n, um.sh), kOThreads), 1};
 }
 
 LaunchShape adam_launch(int64_t n, bool aligned) { return adam_shape(n, UnitMap{0, aligned ? 1 : 0}); }

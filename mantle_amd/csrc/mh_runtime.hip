@@ -386,12 +386,13 @@ int build_elw_plan(const mh_shape& out, int nin, const mh_shape* in, ElwPlan* pl
 // ---------------------------------------------------------------------------------------
 // fill kernel (also used for zeroing: a kernel, so it can live inside captured graphs)
 // ---------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) k_fill(float* __restrict__ t, float v, int64_t n) {
+// A thread per quad, no grid loop (a launch covers at most kMaxLaunchQuads quads); the first
+// thread also writes the n % 4 tail.
+__global__ void __launch_bounds__(64) k_fill(float* __restrict__ t, float v, int64_t n) {
     const int64_t nq = n >> 2;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    for (int64_t q = i; q < nq; q += stride) st_nt4(t, q, make_float4(v, v, v, v));
-    if (i == 0)
+    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q < nq) st_nt4(t, q, make_float4(v, v, v, v));
+    if (q == 0)
         for (int64_t j = nq << 2; j < n; ++j) t[j] = v;
 }
 
@@ -400,10 +401,9 @@ __global__ void __launch_bounds__(256) k_fill_scalar(float* __restrict__ t, floa
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) t[i] = v;
 }
 
-__global__ void __launch_bounds__(256) k_copy(float4* __restrict__ dst, const float4* __restrict__ src, int64_t nq) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < nq; q += stride)
-        st_ntv(reinterpret_cast<float*>(dst), q, ld_ntv(reinterpret_cast<const float*>(src), q));
+__global__ void __launch_bounds__(64) k_copy(float4* __restrict__ dst, const float4* __restrict__ src, int64_t nq) {
+    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q < nq) st_ntv(reinterpret_cast<float*>(dst), q, ld_ntv(reinterpret_cast<const float*>(src), q));
 }
 
 // Counter-based SplitMix64 (Steele, Lea & Flood, "Fast splittable pseudorandom number
@@ -433,25 +433,35 @@ __global__ void __launch_bounds__(256) k_rand(float* __restrict__ t, int64_t n, 
     }
 }
 
-// One-wavefront workgroups, one quad (or, unaligned, one element) per thread; k_fill and
-// k_fill_scalar loop over the grid beyond what one dispatch holds.
+// One-wavefront workgroups. Aligned: one quad per thread, at most kMaxLaunchQuads quads per
+// launch. Unaligned (k_fill_scalar): one element per thread, a grid loop beyond one dispatch.
 LaunchShape fill_launch(int64_t n, bool aligned) {
-    return LaunchShape{aligned ? 0 : 1, 64, grid_blocks(aligned ? (n >> 2) : n, 64)};
+    if (!aligned) return LaunchShape{1, 64, grid_blocks(n, 64), 1};
+    const int64_t nq = n >> 2;
+    return LaunchShape{0, 64, grid_blocks(nq < kMaxLaunchQuads ? nq : kMaxLaunchQuads, 64), launch_count(nq)};
 }
 
-// One-wavefront workgroups, one quad per thread; k_copy loops over the grid beyond that.
-LaunchShape copy_launch(int64_t nquads) { return LaunchShape{0, 64, grid_blocks(nquads, 64)}; }
+// One-wavefront workgroups, one quad per thread, at most kMaxLaunchQuads quads per launch.
+LaunchShape copy_launch(int64_t nquads) {
+    return LaunchShape{0, 64, grid_blocks(nquads < kMaxLaunchQuads ? nquads : kMaxLaunchQuads, 64),
+                       launch_count(nquads)};
+}
 
 static int launch_fill(float* t, float v, int64_t n) {
     if (n == 0) return MH_OK;
     if (!t) return fail(MH_ERR_NULL, "fill: null tensor");
     MH_TRY(require_init());
     const bool al = (reinterpret_cast<uintptr_t>(t) & 15) == 0;
-    const LaunchShape ls = fill_launch(n, al);
-    if (al)
-        hipLaunchKernelGGL(k_fill, dim3((unsigned)ls.blocks), dim3(ls.threads), 0, ctx().stream, t, v, n);
-    else
+    if (al) {
+        for (int64_t off = 0; off < n; off += 4 * kMaxLaunchQuads) {
+            const int64_t cnt = n - off < 4 * kMaxLaunchQuads ? n - off : 4 * kMaxLaunchQuads;
+            const LaunchShape ls = fill_launch(cnt, true);
+            hipLaunchKernelGGL(k_fill, dim3((unsigned)ls.blocks), dim3(ls.threads), 0, ctx().stream, t + off, v, cnt);
+        }
+    } else {
+        const LaunchShape ls = fill_launch(n, false);
         hipLaunchKernelGGL(k_fill_scalar, dim3((unsigned)ls.blocks), dim3(ls.threads), 0, ctx().stream, t, v, n);
+    }
     return finish("fill");
 }
 
@@ -595,10 +605,13 @@ int mh_memcpy_d2d(void* dst, const void* src, size_t bytes) {
     if (!dst || !src) return fail(MH_ERR_NULL, "mh_memcpy_d2d: null pointer");
     MH_TRY(require_init());
     if (((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) | bytes) & 15) == 0) {
-        const int64_t nq = (int64_t)(bytes >> 4);
-        const LaunchShape ls = copy_launch(nq);
-        hipLaunchKernelGGL(k_copy, dim3((unsigned)ls.blocks), dim3(ls.threads), 0, ctx().stream,
-                           reinterpret_cast<float4*>(dst), reinterpret_cast<const float4*>(src), nq);
+        const int64_t nq_all = (int64_t)(bytes >> 4);
+        for (int64_t off = 0; off < nq_all; off += kMaxLaunchQuads) {
+            const int64_t nq = nq_all - off < kMaxLaunchQuads ? nq_all - off : kMaxLaunchQuads;
+            const LaunchShape ls = copy_launch(nq);
+            hipLaunchKernelGGL(k_copy, dim3((unsigned)ls.blocks), dim3(ls.threads), 0, ctx().stream,
+                               reinterpret_cast<float4*>(dst) + off, reinterpret_cast<const float4*>(src) + off, nq);
+        }
     } else {
         MH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx().stream));
     }
@@ -719,6 +732,7 @@ int mh_plan_launch(int32_t what, int64_t n, mh_launch_info* out) {
     out->kernel = ls.kernel;
     out->threads = ls.threads;
     out->blocks = ls.blocks;
+    out->launches = ls.launches;
     return MH_OK;
 }
 

@@ -274,12 +274,20 @@ def test_launch_grids_fit_one_dispatch(what):
     L = _lib.lib()
     info = _lib.mh_launch_info()
     per_thread = {_lib.LAUNCH_FILL_UNALIGNED: 1}.get(what, 4)
-    for n in (1, 1000, 1 << 28, (1 << 34) - 4, 1 << 34, (1 << 34) + 5, 1 << 36, 1 << 40):
+    for n in (1, 1000, 1 << 28, (1 << 33) - 4, 1 << 33, (1 << 33) + 8, (1 << 34) - 4, 1 << 34, (1 << 34) + 5,
+              1 << 36, 1 << 40):
         assert L.mh_plan_launch(what, n, ctypes.byref(info)) == 0, L.mh_last_error()
         items = info.blocks * info.threads
         assert 1 <= info.blocks and items < (1 << 32), (what, n, info.blocks, info.threads)
+        assert info.launches >= 1
         need = (n + per_thread - 1) // per_thread
-        if need < (1 << 32) - info.threads:
+        if what in (_lib.LAUNCH_FILL, _lib.LAUNCH_COPY, _lib.LAUNCH_SAME_SHAPE):
+            # a thread per quad with no grid loop: at most 2^31 quads per launch, the launches
+            # together covering the tensor
+            nq = n // 4
+            assert info.launches == max(1, -(-nq // (1 << 31))), (what, n, info.launches)
+            assert items >= min(nq, 1 << 31) and items * info.launches >= nq, (what, n, items)
+        elif need < (1 << 32) - info.threads:
             assert items >= need, (what, n, items, need)  # one pass covers the tensor
         if what == _lib.LAUNCH_ADAM:
             # k_adam_al has no stride loop: it takes only tensors whose quads and tail its grid covers
