@@ -298,7 +298,8 @@ __global__ void __launch_bounds__(kThreads)
         float v[4][NA];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
-            const int kind = (kinds >> (2 * k)) & 3;
+            // a lone operand is the broadcast one: these engines run only on plans with one
+            const int kind = NIN == 1 ? (int)IN_BCAST : (kinds >> (2 * k)) & 3;
             if (kind == IN_SCALAR) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) v[j][k] = sv[k];
@@ -359,7 +360,8 @@ __global__ void __launch_bounds__(kThreads)
         vf4 t[NA];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
-            const int kind = (kinds >> (2 * k)) & 3;
+            // a lone operand is the broadcast one: these engines run only on plans with one
+            const int kind = NIN == 1 ? (int)IN_BCAST : (kinds >> (2 * k)) & 3;
             if (kind == IN_FULL) t[k] = ld_ntv(in.p[k], q);
             else if (kind == IN_BCAST) t[k] = reinterpret_cast<const vf4*>(in.p[k])[cq];
             else t[k] = vf4{sv[k], sv[k], sv[k], sv[k]};
@@ -400,7 +402,8 @@ __global__ void __launch_bounds__(kThreads)
         vf4 t[NA];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
-            const int kind = (kinds >> (2 * k)) & 3;
+            // a lone operand is the broadcast one: these engines run only on plans with one
+            const int kind = NIN == 1 ? (int)IN_BCAST : (kinds >> (2 * k)) & 3;
             if (kind == IN_FULL) {
                 t[k] = ld_ntv(in.p[k], q);
             } else {
