@@ -269,6 +269,14 @@ __global__ void __launch_bounds__(kThreads)
     }
 }
 
+// Kind of operand k in the row/column/plane engines, from two bits per operand in kinds. A
+// lone operand is the broadcast one (these engines run only on plans with one), which makes
+// its kind a compile-time constant: no scalar load or kind test at wave start.
+template <int NIN>
+__device__ __forceinline__ int bc_kind(int kinds, int k) {
+    return NIN == 1 ? (int)IN_BCAST : (kinds >> (2 * k)) & 3;
+}
+
 // Row-broadcast engine: output [rows, K] with K >= 4 and fewer than 2^31 elements, every
 // IN_BCAST operand a contiguous per-row vector ([rows, 1], as a row max or row sum is), the
 // output and FULL operands 16-byte aligned. One quad per thread: the quad's first row comes
@@ -286,7 +294,7 @@ __global__ void __launch_bounds__(kThreads)
     f.setup(ds);
     float sv[NA];
 #pragma unroll
-    for (int k = 0; k < NIN; ++k) sv[k] = ((kinds >> (2 * k)) & 3) == IN_SCALAR ? in.p[k][0] : 0.0f;
+    for (int k = 0; k < NIN; ++k) sv[k] = bc_kind<NIN>(kinds, k) == IN_SCALAR ? in.p[k][0] : 0.0f;
     const int64_t nq = n >> 2;
     const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (q < nq) {
@@ -298,8 +306,7 @@ __global__ void __launch_bounds__(kThreads)
         float v[4][NA];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
-            // a lone operand is the broadcast one: these engines run only on plans with one
-            const int kind = NIN == 1 ? (int)IN_BCAST : (kinds >> (2 * k)) & 3;
+            const int kind = bc_kind<NIN>(kinds, k);
             if (kind == IN_SCALAR) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) v[j][k] = sv[k];
@@ -331,7 +338,7 @@ __global__ void __launch_bounds__(kThreads)
             float v[NA];
 #pragma unroll
             for (int k = 0; k < NIN; ++k) {
-                const int kind = (kinds >> (2 * k)) & 3;
+                const int kind = bc_kind<NIN>(kinds, k);
                 v[k] = kind == IN_SCALAR ? sv[k] : (kind == IN_FULL ? in.p[k][i] : in.p[k][row]);
             }
             const float fv = f(v);
@@ -353,15 +360,14 @@ __global__ void __launch_bounds__(kThreads)
     f.setup(ds);
     float sv[NA];
 #pragma unroll
-    for (int k = 0; k < NIN; ++k) sv[k] = ((kinds >> (2 * k)) & 3) == IN_SCALAR ? in.p[k][0] : 0.0f;
+    for (int k = 0; k < NIN; ++k) sv[k] = bc_kind<NIN>(kinds, k) == IN_SCALAR ? in.p[k][0] : 0.0f;
     const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (q < nq) {
         const uint32_t cq = (uint32_t)q - fdiv((uint32_t)q, fcq) * Cq;
         vf4 t[NA];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
-            // a lone operand is the broadcast one: these engines run only on plans with one
-            const int kind = NIN == 1 ? (int)IN_BCAST : (kinds >> (2 * k)) & 3;
+            const int kind = bc_kind<NIN>(kinds, k);
             if (kind == IN_FULL) t[k] = ld_ntv(in.p[k], q);
             else if (kind == IN_BCAST) t[k] = reinterpret_cast<const vf4*>(in.p[k])[cq];
             else t[k] = vf4{sv[k], sv[k], sv[k], sv[k]};
@@ -394,7 +400,7 @@ __global__ void __launch_bounds__(kThreads)
     f.setup(ds);
     float sv[NA];
 #pragma unroll
-    for (int k = 0; k < NIN; ++k) sv[k] = ((kinds >> (2 * k)) & 3) == IN_SCALAR ? in.p[k][0] : 0.0f;
+    for (int k = 0; k < NIN; ++k) sv[k] = bc_kind<NIN>(kinds, k) == IN_SCALAR ? in.p[k][0] : 0.0f;
     const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (q < nq) {
         const uint32_t p = fdiv((uint32_t)q, fsq);
@@ -402,8 +408,7 @@ __global__ void __launch_bounds__(kThreads)
         vf4 t[NA];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
-            // a lone operand is the broadcast one: these engines run only on plans with one
-            const int kind = NIN == 1 ? (int)IN_BCAST : (kinds >> (2 * k)) & 3;
+            const int kind = bc_kind<NIN>(kinds, k);
             if (kind == IN_FULL) {
                 t[k] = ld_ntv(in.p[k], q);
             } else {

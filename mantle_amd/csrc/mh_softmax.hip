@@ -196,6 +196,43 @@ __device__ __forceinline__ float smlm_bwd_row(float (&pre)[KM], const float* xr,
     return acc;
 }
 
+// One row of a row graph's forward from LDS (x row xrow, target row trow, K elements, K <= KM):
+// MAX, SUB, EXP, SUM over the row, then the loss graphs add the row's terms to rowsum (and
+// return it) and Softmax / LogSoftmax overwrite the x row with the output row.
+template <int V, int KM>
+__device__ __forceinline__ float row_fwd(float* xrow, const float* trow, float rowsum, int K) {
+    float xr[KM], e[KM];
+#pragma unroll
+    for (int j = 0; j < KM; ++j) xr[j] = j < K ? xrow[j] : 0.0f;
+    float m = -FLT_MAX;  // MAX.forward: max_simd from min_finite, element order
+#pragma unroll
+    for (int j = 0; j < KM; ++j)
+        if (j < K) m = max_simd(m, xr[j]);
+    float s = 0.0f;  // SUB, EXP, SUM.forward
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+        if (j < K) {
+            e[j] = mexp(xr[j] - m);
+            s = s + e[j];
+        }
+    }
+    const float ls = (V == G_CE || V == G_LOGSOFTMAX) ? mlog(s) : 0.0f;  // LOG.forward of the sum
+    if constexpr (V == G_SMLM) rowsum = smlm_fwd_row<KM>(rowsum, xrow, trow, e, m, s, K);
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+        if (V != G_SMLM && j < K) {
+            if constexpr (V == G_CE) {
+                rowsum = rowsum + trow[j] * ((xr[j] - m) - ls);  // SUB(xm, ls), MUL(target, .)
+            } else if constexpr (V == G_SOFTMAX) {
+                xrow[j] = e[j] / s;  // DIV.forward
+            } else {
+                xrow[j] = (xr[j] - m) - ls;  // SUB(xm, ls).forward
+            }
+        }
+    }
+    return rowsum;
+}
+
 // ---------------------------------------------------------------------------------------
 // thread engine: rows of at most KM (<= 64) elements, element-order row sums
 // ---------------------------------------------------------------------------------------
@@ -218,37 +255,7 @@ __global__ void __launch_bounds__(kSThreads)
     __syncthreads();
     float rowsum = 0.0f;
     const int t = threadIdx.x;
-    if (t < nr) {
-        float xr[KM], e[KM];
-#pragma unroll
-        for (int j = 0; j < KM; ++j) xr[j] = j < K ? xs[t * K + j] : 0.0f;
-        float m = -FLT_MAX;  // MAX.forward: max_simd from min_finite, element order
-#pragma unroll
-        for (int j = 0; j < KM; ++j)
-            if (j < K) m = max_simd(m, xr[j]);
-        float s = 0.0f;  // SUB, EXP, SUM.forward
-#pragma unroll
-        for (int j = 0; j < KM; ++j) {
-            if (j < K) {
-                e[j] = mexp(xr[j] - m);
-                s = s + e[j];
-            }
-        }
-        const float ls = (V == G_CE || V == G_LOGSOFTMAX) ? mlog(s) : 0.0f;  // LOG.forward of the sum
-        if constexpr (V == G_SMLM) rowsum = smlm_fwd_row<KM>(rowsum, xs + t * K, ts + t * K, e, m, s, K);
-#pragma unroll
-        for (int j = 0; j < KM; ++j) {
-            if (V != G_SMLM && j < K) {
-                if constexpr (V == G_CE) {
-                    rowsum = rowsum + ts[t * K + j] * ((xr[j] - m) - ls);  // SUB(xm, ls), MUL(target, .)
-                } else if constexpr (V == G_SOFTMAX) {
-                    xs[t * K + j] = e[j] / s;  // DIV.forward
-                } else {
-                    xs[t * K + j] = (xr[j] - m) - ls;  // SUB(xm, ls).forward
-                }
-            }
-        }
-    }
+    if (t < nr) rowsum = row_fwd<V, KM>(xs + t * K, ts + t * K, rowsum, K);
     if constexpr (LOSS) {
         const float tot = block_sum(rowsum, ws);
         if (t == 0) part[blockIdx.x] = tot;
@@ -496,33 +503,7 @@ __global__ void __launch_bounds__(kSThreads)
             tile_load(rx, x, n0 * K, ncnt);
             if (LOSS) tile_load(rt, tg, n0 * K, ncnt);
         }
-        if (t < nr) {
-            float xr[KM], e[KM];
-#pragma unroll
-            for (int j = 0; j < KM; ++j) xr[j] = j < K ? xs[t * K + j] : 0.0f;
-            float m = -FLT_MAX;
-#pragma unroll
-            for (int j = 0; j < KM; ++j)
-                if (j < K) m = max_simd(m, xr[j]);
-            float s = 0.0f;
-#pragma unroll
-            for (int j = 0; j < KM; ++j) {
-                if (j < K) {
-                    e[j] = mexp(xr[j] - m);
-                    s = s + e[j];
-                }
-            }
-            const float ls = (V == G_CE || V == G_LOGSOFTMAX) ? mlog(s) : 0.0f;
-            if constexpr (V == G_SMLM) rowsum = smlm_fwd_row<KM>(rowsum, xs + t * K, ts + t * K, e, m, s, K);
-#pragma unroll
-            for (int j = 0; j < KM; ++j) {
-                if (V != G_SMLM && j < K) {
-                    if constexpr (V == G_CE) rowsum = rowsum + ts[t * K + j] * ((xr[j] - m) - ls);
-                    else if constexpr (V == G_SOFTMAX) xs[t * K + j] = e[j] / s;
-                    else xs[t * K + j] = (xr[j] - m) - ls;
-                }
-            }
-        }
+        if (t < nr) rowsum = row_fwd<V, KM>(xs + t * K, ts + t * K, rowsum, K);
         __syncthreads();
         if (!LOSS) {
             unstage_tile(out, xs, r0 * K, cnt, true);
@@ -536,6 +517,107 @@ __global__ void __launch_bounds__(kSThreads)
         } else if (t < 64) {
             loss_tail<V>(tot, part, tickets, loss, lscale);
         }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// one-shot loss engine: loss graphs over rows of at most 16 classes, aligned operands
+// ---------------------------------------------------------------------------------------
+// A one-wavefront block takes 64 rows and issues every load of its x and target tiles
+// (ceil(K / 4) float4 per thread per operand, the 64 * K % 4 tail floats on threads 0..2)
+// before it uses any; the tiles go through LDS, thread t computes row t exactly as the thread
+// and pipelined engines do, and the wavefront's butterfly sum of its row sums is the block's
+// partial, which k_loss_comb then sums. Many small blocks keep more waves resident than the
+// persistent kernel's 256-thread blocks (5 KB of LDS each at 10 classes), so the loads of
+// some waves overlap the exp work of others without a prefetch pipeline: at config 5 the pass
+// reads its 84 MB in 15.3 us against 16.7 us for the persistent form.
+constexpr int kORows = 64;
+
+template <int V, int K>
+__global__ void __launch_bounds__(kORows)
+    k_rowo_fwd(const float* __restrict__ x, const float* __restrict__ tg, int64_t rows, float* __restrict__ part) {
+    static_assert(V == G_SMLM || V == G_CE, "the one-shot engine runs the loss graphs");
+    constexpr int QPT = (K + 3) / 4;  // 16 K quads per tile over 64 threads
+    __shared__ vf4 xs4[kORows * K / 4 + 1], ts4[kORows * K / 4 + 1];
+    float* xs = reinterpret_cast<float*>(xs4);
+    float* ts = reinterpret_cast<float*>(ts4);
+    const int t = threadIdx.x;
+    const int64_t r0 = (int64_t)blockIdx.x * kORows;
+    const int nr = (int)((rows - r0) < kORows ? (rows - r0) : kORows);
+    const int cnt = nr * K, nq = cnt >> 2;
+    const float* xb = x + r0 * K;  // 16-byte aligned: r0 * K is a multiple of 64
+    const float* tb = tg + r0 * K;
+    vf4 qx[QPT], qt[QPT];
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+        if (t + kORows * u < nq) {
+            qx[u] = ld_ntv(xb, t + kORows * u);
+            qt[u] = ld_ntv(tb, t + kORows * u);
+        }
+    }
+    const int tl = (nq << 2) + t;
+    float tx = 0.0f, tt = 0.0f;
+    if (tl < cnt) {
+        tx = ld_nt(xb + tl);
+        tt = ld_nt(tb + tl);
+    }
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+        if (t + kORows * u < nq) {
+            xs4[t + kORows * u] = qx[u];
+            ts4[t + kORows * u] = qt[u];
+        }
+    }
+    if (tl < cnt) {
+        xs[tl] = tx;
+        ts[tl] = tt;
+    }
+    __syncthreads();
+    float rowsum = 0.0f;
+    if (t < nr) rowsum = row_fwd<V, K>(xs + t * K, ts + t * K, rowsum, K);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) rowsum = rowsum + __shfl_xor(rowsum, m);
+    if (t == 0) part[blockIdx.x] = rowsum;
+}
+
+// A loss's all-element sum over np block partials (16-byte aligned) in one 1024-thread block:
+// thread t adds the partials' float4 quads t, t + 1024, ... in order, four loads in flight per
+// round, each quad summed left to right, then the np % 4 tail (threads 0..2); an xor butterfly
+// per wavefront and the sixteen wavefront sums in order finish it. The loss is the sum / lscale
+// (MEAN, lscale = f32(N)) or the sum * lscale (cross entropy, lscale = its scale). One launch
+// with every load of a round in flight: at config 5 (16384 partials) 2.4 us after the pass,
+// against 3.2 us for two rounds of scalar loads. Used up to kLossCombMax partials; above that
+// the library's multi-block all-element reduction is faster.
+constexpr int kLCThreads = 1024;
+constexpr int64_t kLossCombMax = 4 * 4 * kLCThreads;
+
+template <int V>
+__global__ void __launch_bounds__(kLCThreads)
+    k_loss_comb(const float* __restrict__ part, int64_t np, float* __restrict__ loss, float lscale) {
+    __shared__ float ws[kLCThreads / 64];
+    const int t = threadIdx.x;
+    const int64_t nq = np >> 2;
+    const vf4* p4 = reinterpret_cast<const vf4*>(part);
+    float a = 0.0f;
+    for (int64_t b = 0; b < nq; b += 4 * kLCThreads) {
+        vf4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t i = b + t + (int64_t)u * kLCThreads;
+            v[u] = i < nq ? p4[i] : vf4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a = a + (((v[u][0] + v[u][1]) + v[u][2]) + v[u][3]);
+    }
+    if (t < (int)(np & 3)) a = a + part[(nq << 2) + t];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) a = a + __shfl_xor(a, m);
+    if ((t & 63) == 0) ws[t >> 6] = a;
+    __syncthreads();
+    if (t == 0) {
+        float w = ws[0];
+        for (int k = 1; k < kLCThreads / 64; ++k) w = w + ws[k];
+        loss[0] = V == G_SMLM ? w / lscale : w * lscale;
     }
 }
 
@@ -1216,14 +1298,31 @@ static int check_rows(const char* what, int64_t rows, int64_t classes) {
     return MH_OK;
 }
 
-// Loss graphs on the pipelined path finish the sum in the kernel when `loss` is given (and
-// set *done); otherwise they leave block partials in `part`.
+// Loss graphs over aligned rows of up to 16 classes run the one-shot engine and leave block
+// partials in `part`. On the pipelined path (rows beyond one launch of the one-shot engine)
+// they finish the sum in the kernel when `loss` is given (and set *done); every other engine
+// leaves block partials.
 template <int V>
 static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows, int K, float* part,
                       int64_t* nblocks_out, float* loss = nullptr, float lscale = 0.0f, bool* done = nullptr) {
     hipStream_t st = ctx().stream;
     constexpr bool LOSS = V == G_SMLM || V == G_CE;
     const bool al = al16s(x) && (!LOSS || al16s(tg)) && (LOSS || al16s(out));
+    if constexpr (LOSS) {  // one-shot blocks of 64 rows; the caller sums the partials
+        const int64_t nb = (rows + kORows - 1) / kORows;
+        if (K <= 16 && al && nb <= max_grid_blocks(kORows)) {
+            *nblocks_out = nb;
+            dim3 g((unsigned)nb), b(kORows);
+            switch (K) {
+#define MH_K(KK) \
+    case KK: hipLaunchKernelGGL((k_rowo_fwd<V, KK>), g, b, 0, st, x, tg, rows, part); break;
+                MH_ROWP_CLASSES(MH_K)
+#undef MH_K
+                default: return fail(MH_ERR_INVALID, "row kernel: %d classes", K);
+            }
+            return MH_OK;
+        }
+    }
     if (K <= 16 && al) {  // persistent, pipelined
         const void* kern = nullptr;
         switch (K) {
@@ -1412,6 +1511,10 @@ static int loss_fwd(const char* what, float* loss, const float* x, const float* 
     const float lscale = V == G_SMLM ? (float)n : ce;
     MH_TRY(launch_fwd<V>(x, tg, nullptr, rows, (int)K, part, &nb, loss, lscale, &done));
     if (done) return finish(what);
+    if (nb <= kLossCombMax) {  // MEAN.forward: / f32(N); cross entropy: SUM, then MUL(., f32(-1 / f64(rows)))
+        hipLaunchKernelGGL((k_loss_comb<V>), dim3(1), dim3(kLCThreads), 0, ctx().stream, part, nb, loss, lscale);
+        return finish(what);
+    }
     if (V == G_SMLM)  // MEAN.forward: the sum of every element / f32(N)
         MH_TRY(reduce_abc(RED_SUM, EPI_MEAN, part, 1, nb, 1, loss, nullptr, (float)n, part + np));
     else  // SUM.forward, then MUL(., f32(-1 / f64(rows))) (loss.mojo:58-59)
