@@ -621,6 +621,80 @@ __global__ void __launch_bounds__(kLCThreads)
     }
 }
 
+// One row of a row graph's backward from LDS (x row xrow, upstream row urow: the target of a
+// loss graph, the output's gradient otherwise; K elements, K <= KM). Returns the row in xr,
+// pre[j] = every node's gradient term of element j up to SUB(x, max) in node order, and the MAX
+// node's route: sg goes to the elements equal to the row max mb (NaN elements never). The
+// caller adds (grad + pre[j]) + (xr[j] == mb ? sg : 0). The head graph overwrites urow.
+template <int V, int KM>
+__device__ __forceinline__ void row_bwd(float (&xr)[KM], float (&pre)[KM], float& mb, float& sg, const float* xrow,
+                                        float* urow, float gconst, bool skip_ok, int K) {
+    float e[KM];
+#pragma unroll
+    for (int j = 0; j < KM; ++j) xr[j] = j < K ? xrow[j] : 0.0f;
+    float m = -FLT_MAX;
+    mb = -FLT_MAX;
+    uint32_t cntm = 0;
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+        if (j < K) {
+            const float v = xr[j];
+            m = max_simd(m, v);
+            if (mb > v) {
+            } else if (v > mb) {
+                mb = v;
+                cntm = 1;
+            } else if (v == mb) {  // a NaN element is not counted
+                cntm += 1;
+            }
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+        if (j < K) {
+            e[j] = mexp(xr[j] - m);
+            s = s + e[j];
+        }
+    }
+    float acc = 0.0f, gS;
+    if constexpr (V == G_SMLM) {
+        gS = 0.0f + smlm_bwd_row<KM>(pre, xrow, urow, e, m, s, gconst, skip_ok, K);
+    } else if constexpr (from_softmax<V>()) {
+        const float s2 = s * s;
+#pragma unroll
+        for (int j = 0; j < KM; ++j) {
+            if (j < K) {
+                const float gsm = upstream<V>(urow[j], e[j], s, gconst);
+                pre[j] = 0.0f + gsm / s;
+                acc = acc + ((-e[j]) / s2) * gsm;
+            }
+        }
+        gS = 0.0f + acc;
+    } else {
+#pragma unroll
+        for (int j = 0; j < KM; ++j) {
+            if (j < K) {
+                const float glsm = upstream<V>(urow[j], e[j], s, gconst);
+                pre[j] = 0.0f + glsm;
+                acc = acc + glsm;
+            }
+        }
+        gS = 0.0f + (0.0f + (-acc)) / s;
+    }
+    const float rgs = K == 1 ? (1.0f * gS) * gS : 1.0f * gS;
+    float acc2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+        if (j < K) {
+            if constexpr (from_softmax<V>()) pre[j] = 0.0f + e[j] * (pre[j] + rgs);
+            else pre[j] = pre[j] + e[j] * (0.0f + rgs);
+            acc2 = acc2 + pre[j];
+        }
+    }
+    sg = (1.0f / (float)cntm) * (0.0f + (-acc2));
+}
+
 template <int V, int KM>
 __global__ void __launch_bounds__(kSThreads)
     k_rowp_bwd(float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ up,
@@ -660,69 +734,8 @@ __global__ void __launch_bounds__(kSThreads)
             tile_load(rg, g, n0 * K, ncnt);
         }
         if (t < nr) {
-            float xr[KM], e[KM], pre[KM];
-#pragma unroll
-            for (int j = 0; j < KM; ++j) xr[j] = j < K ? xs[t * K + j] : 0.0f;
-            float m = -FLT_MAX, mb = -FLT_MAX;
-            uint32_t cntm = 0;
-#pragma unroll
-            for (int j = 0; j < KM; ++j) {
-                if (j < K) {
-                    const float v = xr[j];
-                    m = max_simd(m, v);
-                    if (mb > v) {
-                    } else if (v > mb) {
-                        mb = v;
-                        cntm = 1;
-                    } else if (v == mb) {  // a NaN element is not counted
-                        cntm += 1;
-                    }
-                }
-            }
-            float s = 0.0f;
-#pragma unroll
-            for (int j = 0; j < KM; ++j) {
-                if (j < K) {
-                    e[j] = mexp(xr[j] - m);
-                    s = s + e[j];
-                }
-            }
-            float acc = 0.0f, gS;
-            if constexpr (V == G_SMLM) {
-                gS = 0.0f + smlm_bwd_row<KM>(pre, xs + t * K, us + t * K, e, m, s, gconst, skip_ok, K);
-            } else if constexpr (from_softmax<V>()) {
-                const float s2 = s * s;
-#pragma unroll
-                for (int j = 0; j < KM; ++j) {
-                    if (j < K) {
-                        const float gsm = upstream<V>(us[t * K + j], e[j], s, gconst);
-                        pre[j] = 0.0f + gsm / s;
-                        acc = acc + ((-e[j]) / s2) * gsm;
-                    }
-                }
-                gS = 0.0f + acc;
-            } else {
-#pragma unroll
-                for (int j = 0; j < KM; ++j) {
-                    if (j < K) {
-                        const float glsm = upstream<V>(us[t * K + j], e[j], s, gconst);
-                        pre[j] = 0.0f + glsm;
-                        acc = acc + glsm;
-                    }
-                }
-                gS = 0.0f + (0.0f + (-acc)) / s;
-            }
-            const float rgs = K == 1 ? (1.0f * gS) * gS : 1.0f * gS;
-            float acc2 = 0.0f;
-#pragma unroll
-            for (int j = 0; j < KM; ++j) {
-                if (j < K) {
-                    if constexpr (from_softmax<V>()) pre[j] = 0.0f + e[j] * (pre[j] + rgs);
-                    else pre[j] = pre[j] + e[j] * (0.0f + rgs);
-                    acc2 = acc2 + pre[j];
-                }
-            }
-            const float sg = (1.0f / (float)cntm) * (0.0f + (-acc2));
+            float xr[KM], pre[KM], mb, sg;
+            row_bwd<V, KM>(xr, pre, mb, sg, xs + t * K, us + t * K, gconst, skip_ok, K);
 #pragma unroll
             for (int j = 0; j < KM; ++j) {
                 if (j < K) {
@@ -736,6 +749,80 @@ __global__ void __launch_bounds__(kSThreads)
         __syncthreads();
     }
 }
+
+// One-shot backward of the loss graphs over rows of at most 16 classes, aligned operands: a
+// one-wavefront block takes 64 rows and issues every load of its x, target and grad_x tiles
+// first. The grad_x quads stay in registers; x and the target go through LDS, where thread t
+// computes row t as the pipelined kernel does and writes pre over its x row and the MAX route
+// over its target row. Each thread then stores its grad_x quads as (g + pre) + route, the
+// pipelined kernel's sums: two LDS tiles instead of three (5 KB per wavefront at 10 classes).
+template <int V, int K>
+__global__ void __launch_bounds__(kORows)
+    k_rowo_bwd(float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ up,
+               const float* __restrict__ ug, int64_t rows, float c) {
+    static_assert(V == G_SMLM || V == G_CE, "the one-shot engine runs the loss graphs");
+    constexpr int QPT = (K + 3) / 4;
+    __shared__ vf4 xs4[kORows * K / 4 + 1], us4[kORows * K / 4 + 1];
+    float* xs = reinterpret_cast<float*>(xs4);
+    float* us = reinterpret_cast<float*>(us4);
+    const int t = threadIdx.x;
+    const int64_t r0 = (int64_t)blockIdx.x * kORows;
+    const int nr = (int)((rows - r0) < kORows ? (rows - r0) : kORows);
+    const int cnt = nr * K, nq = cnt >> 2;
+    const int64_t base = r0 * K;  // a multiple of 64: 16-byte aligned
+    const float gconst = V == G_SMLM ? 0.0f + c * ug[0] : 0.0f + 1.0f * (0.0f + ug[0] * c);
+    const bool skip_ok = gconst - gconst == 0.0f;  // g_t finite (the head graph's zero-target shortcut)
+    vf4 qx[QPT], qu[QPT], qg[QPT];
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+        if (t + kORows * u < nq) {
+            qx[u] = ld_ntv(x + base, t + kORows * u);
+            qu[u] = ld_ntv(up + base, t + kORows * u);
+            qg[u] = ld_ntv(g + base, t + kORows * u);
+        }
+    }
+    const int tl = (nq << 2) + t;
+    float tx = 0.0f, tu = 0.0f, tg = 0.0f;
+    if (tl < cnt) {
+        tx = ld_nt(x + base + tl);
+        tu = ld_nt(up + base + tl);
+        tg = ld_nt(g + base + tl);
+    }
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+        if (t + kORows * u < nq) {
+            xs4[t + kORows * u] = qx[u];
+            us4[t + kORows * u] = qu[u];
+        }
+    }
+    if (tl < cnt) {
+        xs[tl] = tx;
+        us[tl] = tu;
+    }
+    __syncthreads();
+    if (t < nr) {
+        float xr[K], pre[K], mb, sg;
+        row_bwd<V, K>(xr, pre, mb, sg, xs + t * K, us + t * K, gconst, skip_ok, K);
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            xs[t * K + j] = pre[j];
+            us[t * K + j] = xr[j] == mb ? sg : 0.0f;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+        if (t + kORows * u < nq) {
+            const vf4 p = xs4[t + kORows * u], r = us4[t + kORows * u];
+            vf4 o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = (qg[u][j] + p[j]) + r[j];
+            st_ntv(g + base, t + kORows * u, o);
+        }
+    }
+    if (tl < cnt) st_nt(g + base + tl, (tg + xs[tl]) + us[tl]);
+}
+
 
 // ---------------------------------------------------------------------------------------
 // wavefront engine: 64 < classes <= 2047, one wavefront per row, k_rows_wave's order
@@ -1411,6 +1498,20 @@ template <int V>
 static int launch_bwd(float* gx, const float* x, const float* up, const float* ug, int64_t rows, int K, float c) {
     hipStream_t st = ctx().stream;
     const bool al = al16s(x) && al16s(up) && al16s(gx);
+    if constexpr (V == G_SMLM || V == G_CE) {  // one-shot blocks of 64 rows
+        const int64_t nb = (rows + kORows - 1) / kORows;
+        if (K <= 16 && al && nb <= max_grid_blocks(kORows)) {
+            dim3 g((unsigned)nb), b(kORows);
+            switch (K) {
+#define MH_K(KK) \
+    case KK: hipLaunchKernelGGL((k_rowo_bwd<V, KK>), g, b, 0, st, gx, x, up, ug, rows, c); break;
+                MH_ROWP_CLASSES(MH_K)
+#undef MH_K
+                default: return fail(MH_ERR_INVALID, "row kernel: %d classes", K);
+            }
+            return MH_OK;
+        }
+    }
     if (K <= 16 && al) {  // persistent, pipelined
         const void* kern = nullptr;
         switch (K) {
