@@ -1153,8 +1153,9 @@ WL_KERNELS = [
      8 * _N5 + 12 * (_N5 // 10), "the rg terms computed in the loader, added into the gradient in row order"),
     ("c5 MAX.bwd (rows of 10)", "void mh::k_max_bwd_rows<16>", 1048576, 12 * _N5 + 8 * (_N5 // 10),
      "stores only quads holding a row maximum (most quads, at 10 classes)"),
-    ("c5 fused head forward", "void mh::k_rowp_fwd<0, 10>", 262144, 8 * _N5, "logits and targets read once"),
-    ("c5 fused head backward", "void mh::k_rowp_bwd<0, 10>", 196608, 16 * _N5, ""),
+    ("c5 fused head forward", "void mh::k_rowo_fwd<0, 10>", 1048576, 8 * _N5,
+     "logits and targets read once; 64 KB of block partials written for k_loss_comb<0>"),
+    ("c5 fused head backward", "void mh::k_rowo_bwd<0, 10>", 1048576, 16 * _N5, ""),
     ("CrossEntropy [32768,1000] backward", "void mh::k_roww_bwd<1, true, 16>", 2097152, 16 * 32768000, ""),
 ]
 
@@ -1167,8 +1168,8 @@ WL_STATS = [("c3", "op_by_op", "ADD.bwd_bias", "void mh::k_unb_planes<false>"),
             ("c3", "fused", "bias_relu.bwd", ("void mh::k_bias_relu_bwd_flat<false, true, true, true>",
                                               "mh::k_bias_partials_comb8")),
             ("c4", "ops", "8192x8192.ax1.MAX.bwd", "void mh::k_max_bwd_rowreg<4, 8>"),
-            ("c5", "fused", "fused.fwd", "void mh::k_rowp_fwd<0, 10>"),
-            ("c5", "fused", "fused.bwd", "void mh::k_rowp_bwd<0, 10>"),
+            ("c5", "fused", "fused.fwd", ("void mh::k_rowo_fwd<0, 10>", "void mh::k_loss_comb<0>")),
+            ("c5", "fused", "fused.bwd", "void mh::k_rowo_bwd<0, 10>"),
             ("c5", "fwd", "SUB.fwd", "void mh::k_rowbc4<mh::FBin<1>, 2, false>"),
             ("c5", "fwd", "DIV.fwd", "void mh::k_rowbc4<mh::FBin<3>, 2, false>"),
             ("c5", "bwd", "DIV.bwd1", "void mh::k_rows_binrg<3, 1, false, 16>")]
@@ -1266,8 +1267,8 @@ def traffic_summary_md(commands):
 
 
 VALU_KERNELS = [  # (label, kernel-name prefix, elements per dispatch)
-    ("c5 fused head forward [2^20, 10]", "void mh::k_rowp_fwd<0, 10>", _N5),
-    ("c5 fused head backward [2^20, 10]", "void mh::k_rowp_bwd<0, 10>", _N5),
+    ("c5 fused head forward [2^20, 10]", "void mh::k_rowo_fwd<0, 10>", _N5),
+    ("c5 fused head backward [2^20, 10]", "void mh::k_rowo_bwd<0, 10>", _N5),
     ("c2 POW backward, x and exponent gradients (2^28)", "mh::k_pow_grad_quads(", 1 << 28),
     ("c2 TANH backward (2^28)", "void mh::k_same4<mh::FUnBwd<15>, 2, true>", 1 << 28),
     ("c2 MUL backward, both operands (2^28)", "void mh::k_bwd2_same4<2, false>", 1 << 28),

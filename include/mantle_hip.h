@@ -360,7 +360,7 @@ int mh_model_zero_grad(mh_model* m);
  * the gradient arena zeroed (mh_model_zero_grad), then the forward and backward passes. A graph
  * launch costs the host about as much as launching a handful of kernels, so a step replays
  * fastest as one MH_PASS_STEP graph: for a deep chain of small tensors (24 MUL/ADD/RELU layers
- * over [32, 32]) about twice as fast as the eager step, whose host launches bound it; a short
+ * over [32, 32]) 1.5-2 times as fast as the eager step, whose host launches bound it; a short
  * step or one over large tensors runs as fast eagerly. The graph holds kernel launches only
  * (no memset or host-copy nodes). Capturing again replaces the graph. A captured graph keeps
  * the library buffers it was recorded with (a library buffer that grows while any graph exists

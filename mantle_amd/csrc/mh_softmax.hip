@@ -432,7 +432,8 @@ __device__ __forceinline__ void loss_tail(float tot, float* part, uint32_t* tick
 // float4 per thread per operand); rows are computed exactly as in k_rowt_fwd / k_rowt_bwd.
 // Each class count 1..16 has its own kernel (KM = K at compile time: every loop over a row
 // unrolled without per-class guards), 5-6 % faster at 10 classes than one kernel for all
-// counts up to 16.
+// counts up to 16. Softmax and LogSoftmax run here; the loss graphs run the one-shot engine
+// below (faster at config 5 both ways) unless their rows exceed one launch of it.
 constexpr int kPQ = 4;  // float4 per thread per operand tile (q0..q3 below)
 
 // Four float4 of one operand tile per thread, as named registers (an array here ends up in
