@@ -1014,6 +1014,51 @@ def test_fused_row_graphs(gpu, rows, classes):
     assert_bitexact(tg.to_numpy(), gr["x"], "cross-entropy backward")
 
 
+# Row counts whose one-shot loss partials (one per 64 rows) the one-block combine sums in three
+# rounds with a partial count that is not a multiple of four (2999999 rows: 46875 partials), in
+# exactly its largest count (64 * 65536 rows), and one past it, where the multi-block
+# all-element reduction takes the partials instead.
+LOSS_PARTIAL_CASES = [(2_999_999, 2), (64 * 65536, 3), (64 * 65536 + 1, 2)]
+
+
+@pytest.mark.parametrize("rows,classes", LOSS_PARTIAL_CASES, ids=[f"{r}x{c}" for r, c in LOSS_PARTIAL_CASES])
+def test_fused_loss_sums_over_many_block_partials(gpu, rows, classes):
+    """The config-5 head and CrossEntropyLoss losses at row counts that take every way the
+    block partials of the loss engines are summed, against the op-by-op graphs on the GPU
+    (whose per-element terms are the oracle's bits) in the sum class; the cross-entropy
+    backward at the same size bit-identical to the op-by-op graph."""
+    from util import cross_entropy_nodes
+    m = gpu.m
+    print(f"\n[loss partials] rows {rows} classes {classes}", flush=True)
+    x = synth.normal((rows, classes), 0, 2, 1400)
+    cls = synth.integers((rows,), 0, classes, 1401)
+    onehot = np.zeros((rows, classes), np.float32)
+    onehot[np.arange(rows), cls] = 1.0
+    tx = gpu.T(x)
+    g = Graph(config5_nodes(), ["logits"])
+    v = g.forward(gpu, {"logits": x, "onehot": onehot})
+    loss = m.Tensor(m.TensorShape(1))
+    m.softmax_log_mul_mean_forward(loss, tx, gpu.T(onehot))
+    t64 = v["t"].astype(np.float64)
+    assert_sum_close(loss.to_numpy(), v["loss"], np.array([t64.mean()]), "head loss",
+                     terms_abs=np.array([np.abs(t64).mean()]))
+    target = synth.uniform((rows, classes), 0, 1, 1402)
+    cn = np.array([np.float32(-1.0 / rows)], np.float32)
+    g = Graph(cross_entropy_nodes("x", "target"), ["x"])
+    v = g.forward(gpu, {"x": x, "target": target, "cN": cn})
+    ttg = gpu.T(target)
+    m.cross_entropy_forward(loss, tx, ttg)
+    tl64 = v["tl"].astype(np.float64)
+    assert_sum_close(loss.to_numpy(), v["loss"], np.array([tl64.sum() * float(cn[0])]), "cross-entropy loss",
+                     terms_abs=np.array([np.abs(tl64).sum() * abs(float(cn[0]))]))
+    seed = np.array([0.7], np.float32)
+    g0 = synth.normal((rows, classes), 0, 1, 1403)
+    gr = g.backward(gpu, v, seed=seed, init={"x": g0})
+    tg = gpu.T(g0)
+    m.cross_entropy_backward(tg, tx, ttg, gpu.T(seed))
+    assert_bitexact(tg.to_numpy(), gr["x"], "cross-entropy backward")
+
+
 ORACLE_ROW_CASES = [(513, 17), (300, 24), (1000, 31), (40, 33), (777, 47), (1200, 64), (500, 32)]
 _rng_oracle_rows = np.random.default_rng(20261202)
 ORACLE_ROW_CASES += [(int(_rng_oracle_rows.integers(1, 1500)), int(_rng_oracle_rows.integers(17, 65))) for _ in range(6)]
