@@ -656,8 +656,8 @@ def run_adj(L, reps):
 
 
 def run_rows(L, reps):
-    """Row-fused graphs: CrossEntropyLoss over [2^20, 10] and [32768, 1000]; Softmax and
-    LogSoftmax over [32768, 1000]. Bytes: loss forward 8 B/elem (x, target), loss backward
+    """Row-fused graphs: CrossEntropyLoss, Softmax and LogSoftmax over [2^20, 10] and
+    [32768, 1000]. Bytes: loss forward 8 B/elem (x, target), loss backward
     16 (x, target, grad_x read and written), Softmax / LogSoftmax forward 8 (x, out) and
     backward 16 (x, grad_out, grad_x read and written)."""
     d = Dev(L)
@@ -678,12 +678,11 @@ def run_rows(L, reps):
                     P[f"loss{tag}"], P[f"x{tag}"], P[f"t{tag}"], r, k), 8 * n + 4),
                 (f"cross_entropy.bwd.{tag}", lambda P, tag=tag, r=rows, k=k: L.mh_cross_entropy_bwd_accum(
                     P[f"g{tag}"], P[f"x{tag}"], P[f"t{tag}"], P[f"ug{tag}"], r, k), 16 * n + 4)]
-        if k == 1000:
-            for nm, f, b in (("softmax", L.mh_softmax_fwd, L.mh_softmax_bwd_accum),
-                             ("logsoftmax", L.mh_logsoftmax_fwd, L.mh_logsoftmax_bwd_accum)):
-                ops += [(f"{nm}.fwd.{tag}", lambda P, tag=tag, r=rows, k=k, f=f: f(P[f"o{tag}"], P[f"x{tag}"], r, k), 8 * n),
-                        (f"{nm}.bwd.{tag}", lambda P, tag=tag, r=rows, k=k, b=b: b(P[f"g{tag}"], P[f"x{tag}"], P[f"t{tag}"],
-                                                                              r, k), 16 * n)]
+        for nm, f, b in (("softmax", L.mh_softmax_fwd, L.mh_softmax_bwd_accum),
+                         ("logsoftmax", L.mh_logsoftmax_fwd, L.mh_logsoftmax_bwd_accum)):
+            ops += [(f"{nm}.fwd.{tag}", lambda P, tag=tag, r=rows, k=k, f=f: f(P[f"o{tag}"], P[f"x{tag}"], r, k), 8 * n),
+                    (f"{nm}.bwd.{tag}", lambda P, tag=tag, r=rows, k=k, b=b: b(P[f"g{tag}"], P[f"x{tag}"], P[f"t{tag}"],
+                                                                          r, k), 16 * n)]
     chk(L, L.mh_sync(), "sync")
     for label, fn, _ in ops:  # real outputs and gradients in the copied sets
         chk(L, fn(d.ptrs), label)

@@ -370,61 +370,8 @@ __global__ void __launch_bounds__(kSThreads)
 }
 
 // ---------------------------------------------------------------------------------------
-// in-kernel end of a loss's all-element sum (grids of at most 64 * 32 blocks)
-// ---------------------------------------------------------------------------------------
-// Block b publishes its partial with an agent-scope store, waits for it to complete, and
-// takes a ticket on the counter of its group of 32 blocks; the group's last arrival sums the
-// group's partials (lane i loads partial i, an xor butterfly adds them), publishes the group
-// sum the same way and takes a ticket on the top counter, whose last arrival sums the group
-// sums and writes the loss (MEAN: / f32(N); cross entropy: * f32(-1 / rows)). Every sum runs
-// in an order fixed by block indices alone, so the loss does not depend on which block ends
-// last, and every counter is back at zero when the kernel ends. Counters sit one per 128-byte
-// line; called by the 64 lanes of the block's first wavefront.
-constexpr int kTailGroup = 32;
-constexpr int64_t kTailStride = 32;
-constexpr int64_t kTailMaxBlocks = 64 * kTailGroup;
-
-template <int V>
-__device__ __forceinline__ void loss_tail(float tot, float* part, uint32_t* tickets, float* loss, float lscale) {
-    const int lane = threadIdx.x & 63;
-    const int b = blockIdx.x, nparts = gridDim.x;
-    const int grp = b / kTailGroup, g0 = grp * kTailGroup;
-    const int members = (nparts - g0) < kTailGroup ? (nparts - g0) : kTailGroup;
-    const int ngroups = (nparts + kTailGroup - 1) / kTailGroup;
-    uint32_t tk = 0;
-    if (lane == 0) {
-        __hip_atomic_store(&part[b], tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);
-        tk = __hip_atomic_fetch_add(&tickets[(1 + grp) * kTailStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    tk = __shfl(tk, 0);
-    if (tk != (uint32_t)(members - 1)) return;  // uniform across the wavefront
-    // acquire on the group's last arriver: the members' partials are visible below
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    float v = lane < members ? __hip_atomic_load(&part[g0 + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
-#pragma unroll
-    for (int mm = 32; mm >= 1; mm >>= 1) v = v + __shfl_xor(v, mm);
-    if (lane == 0) {
-        __hip_atomic_store(&tickets[(1 + grp) * kTailStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&part[nparts + grp], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);
-        tk = __hip_atomic_fetch_add(&tickets[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    tk = __shfl(tk, 0);
-    if (tk != (uint32_t)(ngroups - 1)) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the group sums are visible below
-    float w = lane < ngroups ? __hip_atomic_load(&part[nparts + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                             : 0.0f;
-#pragma unroll
-    for (int mm = 32; mm >= 1; mm >>= 1) w = w + __shfl_xor(w, mm);
-    if (lane == 0) {
-        __hip_atomic_store(&tickets[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        loss[0] = V == G_SMLM ? w / lscale : w * lscale;
-    }
-}
-
-// ---------------------------------------------------------------------------------------
-// pipelined thread engine: rows of at most 16 classes, 16-byte aligned operands
+// pipelined thread engine: Softmax / LogSoftmax forward over rows of at most 16 classes,
+// 16-byte aligned operands
 // ---------------------------------------------------------------------------------------
 // A persistent grid walks 256-row tiles; while a block computes tile i from LDS, the loads of
 // its next tile are already in flight into registers, so the chip never alternates between
@@ -432,8 +379,9 @@ __device__ __forceinline__ void loss_tail(float tot, float* part, uint32_t* tick
 // float4 per thread per operand); rows are computed exactly as in k_rowt_fwd / k_rowt_bwd.
 // Each class count 1..16 has its own kernel (KM = K at compile time: every loop over a row
 // unrolled without per-class guards), 5-6 % faster at 10 classes than one kernel for all
-// counts up to 16. Softmax and LogSoftmax run here; the loss graphs run the one-shot engine
-// below (faster at config 5 both ways) unless their rows exceed one launch of it.
+// counts up to 16. Only the Softmax and LogSoftmax forward run here: at [2^20, 10] it took
+// 16.0-18.8 us against 16.2-20.3 us for the one-shot engine (which writes each 64-row block's
+// output as its last step), box to box; the loss graphs and every backward run one-shot.
 constexpr int kPQ = 4;  // float4 per thread per operand tile (q0..q3 below)
 
 // Four float4 of one operand tile per thread, as named registers (an array here ends up in
@@ -471,73 +419,58 @@ __device__ __forceinline__ void tile_to_lds(float* dst, const TileRegs& r, int c
 
 template <int V, int KM>
 __global__ void __launch_bounds__(kSThreads)
-    k_rowp_fwd(const float* __restrict__ x, const float* __restrict__ tg, float* __restrict__ out, int64_t rows,
-               float* __restrict__ part, uint32_t* tickets, float* loss, float lscale) {
+    k_rowp_fwd(const float* __restrict__ x, float* __restrict__ out, int64_t rows) {
+    static_assert(V == G_SOFTMAX || V == G_LOGSOFTMAX, "the pipelined engine runs the output-writing graphs");
     constexpr int K = KM;  // compiled for the exact class count
-    __shared__ float4 xs4[kPQ * kSThreads], ts4[kPQ * kSThreads];
-    __shared__ float ws[4];
-    constexpr bool LOSS = V == G_SMLM || V == G_CE;
+    __shared__ float4 xs4[kPQ * kSThreads];
     float* xs = reinterpret_cast<float*>(xs4);
-    float* ts = reinterpret_cast<float*>(ts4);
     const int64_t ntiles = (rows + kSThreads - 1) / kSThreads;
     const int t = threadIdx.x;
-    TileRegs rx{}, rt{};
-    float rowsum = 0.0f;
+    TileRegs rx{};
     int64_t tile = blockIdx.x;
     if (tile < ntiles) {
         const int64_t r0 = tile * kSThreads;
         const int cnt = (int)(((rows - r0) < kSThreads ? (rows - r0) : kSThreads) * K);
         tile_load(rx, x, r0 * K, cnt);
-        if (LOSS) tile_load(rt, tg, r0 * K, cnt);
     }
     for (; tile < ntiles; tile += gridDim.x) {
         const int64_t r0 = tile * kSThreads;
         const int nr = (int)((rows - r0) < kSThreads ? (rows - r0) : kSThreads);
         const int cnt = nr * K;
         tile_to_lds(xs, rx, cnt);
-        if (LOSS) tile_to_lds(ts, rt, cnt);
         __syncthreads();
         const int64_t nxt = tile + gridDim.x;  // the next tile's loads overlap this tile's work
         if (nxt < ntiles) {
             const int64_t n0 = nxt * kSThreads;
             const int ncnt = (int)(((rows - n0) < kSThreads ? (rows - n0) : kSThreads) * K);
             tile_load(rx, x, n0 * K, ncnt);
-            if (LOSS) tile_load(rt, tg, n0 * K, ncnt);
         }
-        if (t < nr) rowsum = row_fwd<V, KM>(xs + t * K, ts + t * K, rowsum, K);
+        if (t < nr) row_fwd<V, KM>(xs + t * K, xs + t * K, 0.0f, K);  // no target: unread
         __syncthreads();
-        if (!LOSS) {
-            unstage_tile(out, xs, r0 * K, cnt, true);
-            __syncthreads();
-        }
-    }
-    if constexpr (LOSS) {
-        const float tot = block_sum(rowsum, ws);
-        if (tickets == nullptr) {  // the host reduces the partials
-            if (t == 0) part[blockIdx.x] = tot;
-        } else if (t < 64) {
-            loss_tail<V>(tot, part, tickets, loss, lscale);
-        }
+        unstage_tile(out, xs, r0 * K, cnt, true);
+        __syncthreads();
     }
 }
 
 // ---------------------------------------------------------------------------------------
-// one-shot loss engine: loss graphs over rows of at most 16 classes, aligned operands
+// one-shot engine: rows of at most 16 classes, aligned operands
 // ---------------------------------------------------------------------------------------
-// A one-wavefront block takes 64 rows and issues every load of its x and target tiles
-// (ceil(K / 4) float4 per thread per operand, the 64 * K % 4 tail floats on threads 0..2)
-// before it uses any; the tiles go through LDS, thread t computes row t exactly as the thread
-// and pipelined engines do, and the wavefront's butterfly sum of its row sums is the block's
-// partial, which k_loss_comb then sums. Many small blocks keep more waves resident than the
-// persistent kernel's 256-thread blocks (5 KB of LDS each at 10 classes), so the loads of
-// some waves overlap the exp work of others without a prefetch pipeline: at config 5 the pass
-// reads its 84 MB in 15.3 us against 16.7 us for the persistent form.
+// A one-wavefront block takes 64 rows and issues every load of its tiles (ceil(K / 4) float4
+// per thread per operand, the 64 * K % 4 tail floats on threads 0..2) before it uses any; the
+// tiles go through LDS and thread t computes row t (row_fwd, the op-by-op chain's expressions
+// and element-order sums). The forward runs the loss graphs: a block's partial is the
+// wavefront's butterfly sum of its row sums, which k_loss_comb then sums. The backward runs
+// every graph. Each class count 1..16 has its own kernel (every loop over a row unrolled
+// without per-class guards). Many small blocks (5 KB of LDS each at 10 classes)
+// keep the CU full of waves, so the loads of some overlap the exp work of others: at config 5
+// the pass reads its 84 MB in 15.3 us, against 16.7 us for a persistent grid of 256-thread
+// blocks that prefetched each next 256-row tile into registers while computing the current one.
 constexpr int kORows = 64;
 
 template <int V, int K>
 __global__ void __launch_bounds__(kORows)
     k_rowo_fwd(const float* __restrict__ x, const float* __restrict__ tg, int64_t rows, float* __restrict__ part) {
-    static_assert(V == G_SMLM || V == G_CE, "the one-shot engine runs the loss graphs");
+    static_assert(V == G_SMLM || V == G_CE, "the one-shot forward runs the loss graphs");
     constexpr int QPT = (K + 3) / 4;  // 16 K quads per tile over 64 threads
     __shared__ vf4 xs4[kORows * K / 4 + 1], ts4[kORows * K / 4 + 1];
     float* xs = reinterpret_cast<float*>(xs4);
@@ -546,21 +479,20 @@ __global__ void __launch_bounds__(kORows)
     const int64_t r0 = (int64_t)blockIdx.x * kORows;
     const int nr = (int)((rows - r0) < kORows ? (rows - r0) : kORows);
     const int cnt = nr * K, nq = cnt >> 2;
-    const float* xb = x + r0 * K;  // 16-byte aligned: r0 * K is a multiple of 64
-    const float* tb = tg + r0 * K;
+    const int64_t base = r0 * K;  // a multiple of 64: 16-byte aligned
     vf4 qx[QPT], qt[QPT];
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
         if (t + kORows * u < nq) {
-            qx[u] = ld_ntv(xb, t + kORows * u);
-            qt[u] = ld_ntv(tb, t + kORows * u);
+            qx[u] = ld_ntv(x + base, t + kORows * u);
+            qt[u] = ld_ntv(tg + base, t + kORows * u);
         }
     }
     const int tl = (nq << 2) + t;
     float tx = 0.0f, tt = 0.0f;
     if (tl < cnt) {
-        tx = ld_nt(xb + tl);
-        tt = ld_nt(tb + tl);
+        tx = ld_nt(x + base + tl);
+        tt = ld_nt(tg + base + tl);
     }
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
@@ -696,72 +628,18 @@ __device__ __forceinline__ void row_bwd(float (&xr)[KM], float (&pre)[KM], float
     sg = (1.0f / (float)cntm) * (0.0f + (-acc2));
 }
 
-template <int V, int KM>
-__global__ void __launch_bounds__(kSThreads)
-    k_rowp_bwd(float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ up,
-               const float* __restrict__ ug, int64_t rows, float c) {
-    constexpr int K = KM;  // compiled for the exact class count
-    __shared__ float4 xs4[kPQ * kSThreads], us4[kPQ * kSThreads], gs4[kPQ * kSThreads];
-    float* xs = reinterpret_cast<float*>(xs4);
-    float* us = reinterpret_cast<float*>(us4);
-    float* gs = reinterpret_cast<float*>(gs4);
-    const int64_t ntiles = (rows + kSThreads - 1) / kSThreads;
-    const int t = threadIdx.x;
-    const float gconst = V == G_SMLM ? 0.0f + c * ug[0] : V == G_CE ? 0.0f + 1.0f * (0.0f + ug[0] * c) : 0.0f;
-    const bool skip_ok = gconst - gconst == 0.0f;  // g_t finite (the head graph's zero-target shortcut)
-    TileRegs rx{}, ru{}, rg{};
-    int64_t tile = blockIdx.x;
-    if (tile < ntiles) {
-        const int64_t r0 = tile * kSThreads;
-        const int cnt = (int)(((rows - r0) < kSThreads ? (rows - r0) : kSThreads) * K);
-        tile_load(rx, x, r0 * K, cnt);
-        tile_load(ru, up, r0 * K, cnt);
-        tile_load(rg, g, r0 * K, cnt);
-    }
-    for (; tile < ntiles; tile += gridDim.x) {
-        const int64_t r0 = tile * kSThreads;
-        const int nr = (int)((rows - r0) < kSThreads ? (rows - r0) : kSThreads);
-        const int cnt = nr * K;
-        tile_to_lds(xs, rx, cnt);
-        tile_to_lds(us, ru, cnt);
-        tile_to_lds(gs, rg, cnt);
-        __syncthreads();
-        const int64_t nxt = tile + gridDim.x;
-        if (nxt < ntiles) {
-            const int64_t n0 = nxt * kSThreads;
-            const int ncnt = (int)(((rows - n0) < kSThreads ? (rows - n0) : kSThreads) * K);
-            tile_load(rx, x, n0 * K, ncnt);
-            tile_load(ru, up, n0 * K, ncnt);
-            tile_load(rg, g, n0 * K, ncnt);
-        }
-        if (t < nr) {
-            float xr[KM], pre[KM], mb, sg;
-            row_bwd<V, KM>(xr, pre, mb, sg, xs + t * K, us + t * K, gconst, skip_ok, K);
-#pragma unroll
-            for (int j = 0; j < KM; ++j) {
-                if (j < K) {
-                    const float a = gs[t * K + j] + pre[j];
-                    gs[t * K + j] = a + (xr[j] == mb ? sg : 0.0f);
-                }
-            }
-        }
-        __syncthreads();
-        unstage_tile(g, gs, r0 * K, cnt, true);
-        __syncthreads();
-    }
-}
-
-// One-shot backward of the loss graphs over rows of at most 16 classes, aligned operands: a
-// one-wavefront block takes 64 rows and issues every load of its x, target and grad_x tiles
-// first. The grad_x quads stay in registers; x and the target go through LDS, where thread t
-// computes row t as the pipelined kernel does and writes pre over its x row and the MAX route
-// over its target row. Each thread then stores its grad_x quads as (g + pre) + route, the
-// pipelined kernel's sums: two LDS tiles instead of three (5 KB per wavefront at 10 classes).
+// One-shot backward over rows of at most 16 classes, aligned operands: a one-wavefront block
+// takes 64 rows and issues every load of its x, upstream (a loss graph's target, else the
+// output's gradient) and grad_x tiles first. The grad_x quads stay in registers; x and the
+// upstream tile go through LDS, where thread t computes row t (row_bwd) and writes pre over its
+// x row and the MAX route over its upstream row. Each thread then stores its grad_x quads as
+// (g + pre) + route, the op-by-op chain's sums in its order. Two tiles in LDS (5 KB per
+// wavefront at 10 classes): 29.9 us at config 5 against 31.3 us for the persistent grid, which
+// staged grad_x as a third tile and so fitted three 256-thread blocks per CU.
 template <int V, int K>
 __global__ void __launch_bounds__(kORows)
     k_rowo_bwd(float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ up,
                const float* __restrict__ ug, int64_t rows, float c) {
-    static_assert(V == G_SMLM || V == G_CE, "the one-shot engine runs the loss graphs");
     constexpr int QPT = (K + 3) / 4;
     __shared__ vf4 xs4[kORows * K / 4 + 1], us4[kORows * K / 4 + 1];
     float* xs = reinterpret_cast<float*>(xs4);
@@ -771,7 +649,7 @@ __global__ void __launch_bounds__(kORows)
     const int nr = (int)((rows - r0) < kORows ? (rows - r0) : kORows);
     const int cnt = nr * K, nq = cnt >> 2;
     const int64_t base = r0 * K;  // a multiple of 64: 16-byte aligned
-    const float gconst = V == G_SMLM ? 0.0f + c * ug[0] : 0.0f + 1.0f * (0.0f + ug[0] * c);
+    const float gconst = V == G_SMLM ? 0.0f + c * ug[0] : V == G_CE ? 0.0f + 1.0f * (0.0f + ug[0] * c) : 0.0f;
     const bool skip_ok = gconst - gconst == 0.0f;  // g_t finite (the head graph's zero-target shortcut)
     vf4 qx[QPT], qu[QPT], qg[QPT];
 #pragma unroll
@@ -1360,8 +1238,8 @@ __global__ void __launch_bounds__(kSThreads)
 // ---------------------------------------------------------------------------------------
 static inline bool al16s(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// The class counts with a persistent row kernel of their own.
-#define MH_ROWP_CLASSES(X) \
+// The class counts with row kernels of their own (one-shot and pipelined).
+#define MH_ROW16_CLASSES(X) \
     X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11) X(12) X(13) X(14) X(15) X(16)
 
 // Blocks of a persistent kernel: as many as can be resident at once (queried once per
@@ -1386,57 +1264,58 @@ static int check_rows(const char* what, int64_t rows, int64_t classes) {
     return MH_OK;
 }
 
-// Loss graphs over aligned rows of up to 16 classes run the one-shot engine and leave block
-// partials in `part`. On the pipelined path (rows beyond one launch of the one-shot engine)
-// they finish the sum in the kernel when `loss` is given (and set *done); every other engine
-// leaves block partials.
+// Loss graphs leave one partial per block in `part` (the caller sums them); Softmax and
+// LogSoftmax write `out`. Over rows of up to 16 classes with aligned operands, Softmax and
+// LogSoftmax run the pipelined engine and the loss graphs the one-shot engine, in several
+// launches (each over its own rows and partials) past one dispatch.
 template <int V>
 static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows, int K, float* part,
-                      int64_t* nblocks_out, float* loss = nullptr, float lscale = 0.0f, bool* done = nullptr) {
+                      int64_t* nblocks_out) {
     hipStream_t st = ctx().stream;
     constexpr bool LOSS = V == G_SMLM || V == G_CE;
     const bool al = al16s(x) && (!LOSS || al16s(tg)) && (LOSS || al16s(out));
-    if constexpr (LOSS) {  // one-shot blocks of 64 rows; the caller sums the partials
-        const int64_t nb = (rows + kORows - 1) / kORows;
-        if (K <= 16 && al && nb <= max_grid_blocks(kORows)) {
-            *nblocks_out = nb;
-            dim3 g((unsigned)nb), b(kORows);
+    if constexpr (!LOSS) {
+        if (K <= 16 && al) {  // persistent, pipelined
+            const void* kern = nullptr;
             switch (K) {
 #define MH_K(KK) \
-    case KK: hipLaunchKernelGGL((k_rowo_fwd<V, KK>), g, b, 0, st, x, tg, rows, part); break;
-                MH_ROWP_CLASSES(MH_K)
+    case KK: kern = reinterpret_cast<const void*>(&k_rowp_fwd<V, KK>); break;
+                MH_ROW16_CLASSES(MH_K)
 #undef MH_K
                 default: return fail(MH_ERR_INVALID, "row kernel: %d classes", K);
             }
+            const int64_t ntiles = (rows + kSThreads - 1) / kSThreads;
+            const int64_t pg = pipe_grid(kern);
+            const int64_t nb = ntiles < pg ? ntiles : pg;
+            *nblocks_out = nb;
+            dim3 g((unsigned)nb), b(kSThreads);
+            switch (K) {
+#define MH_K(KK) \
+    case KK: hipLaunchKernelGGL((k_rowp_fwd<V, KK>), g, b, 0, st, x, out, rows); break;
+                MH_ROW16_CLASSES(MH_K)
+#undef MH_K
+            }
             return MH_OK;
         }
-    }
-    if (K <= 16 && al) {  // persistent, pipelined
-        const void* kern = nullptr;
-        switch (K) {
+    } else {
+        if (K <= 16 && al) {  // one-shot blocks of 64 rows
+            const int64_t nb = (rows + kORows - 1) / kORows;
+            *nblocks_out = nb;
+            for (int64_t b0 = 0; b0 < nb; b0 += max_grid_blocks(kORows)) {
+                const int64_t cnt = nb - b0 < max_grid_blocks(kORows) ? nb - b0 : max_grid_blocks(kORows);
+                const int64_t r0 = b0 * kORows, off = r0 * K;  // 16-byte aligned: r0 is a multiple of 64
+                const int64_t nr = rows - r0 < cnt * kORows ? rows - r0 : cnt * kORows;
+                dim3 g((unsigned)cnt), b(kORows);
+                switch (K) {
 #define MH_K(KK) \
-    case KK: kern = reinterpret_cast<const void*>(&k_rowp_fwd<V, KK>); break;
-            MH_ROWP_CLASSES(MH_K)
+    case KK: hipLaunchKernelGGL((k_rowo_fwd<V, KK>), g, b, 0, st, x + off, tg + off, nr, part + b0); break;
+                    MH_ROW16_CLASSES(MH_K)
 #undef MH_K
-            default: return fail(MH_ERR_INVALID, "row kernel: %d classes", K);
+                    default: return fail(MH_ERR_INVALID, "row kernel: %d classes", K);
+                }
+            }
+            return MH_OK;
         }
-        const int64_t ntiles = (rows + kSThreads - 1) / kSThreads;
-        const int64_t pg = pipe_grid(kern);
-        const int64_t nb = ntiles < pg ? ntiles : pg;
-        *nblocks_out = nb;
-        uint32_t* tk = nullptr;
-        if (LOSS && loss && nb <= kTailMaxBlocks) {
-            MH_TRY(tickets((1 + nb / kTailGroup + 1) * kTailStride, &tk));
-            if (done) *done = true;
-        }
-        dim3 g((unsigned)nb), b(kSThreads);
-        switch (K) {
-#define MH_K(KK) \
-    case KK: hipLaunchKernelGGL((k_rowp_fwd<V, KK>), g, b, 0, st, x, tg, out, rows, part, tk, loss, lscale); break;
-            MH_ROWP_CLASSES(MH_K)
-#undef MH_K
-        }
-        return MH_OK;
     }
     // multi-lane engine, aligned operands, over 8M elements: rows of whole 16-byte quads for
     // 17-64 classes (Softmax 30-32 us against 25-52 us in the thread engine, CrossEntropy faster
@@ -1499,38 +1378,20 @@ template <int V>
 static int launch_bwd(float* gx, const float* x, const float* up, const float* ug, int64_t rows, int K, float c) {
     hipStream_t st = ctx().stream;
     const bool al = al16s(x) && al16s(up) && al16s(gx);
-    if constexpr (V == G_SMLM || V == G_CE) {  // one-shot blocks of 64 rows
+    if (K <= 16 && al) {  // one-shot blocks of 64 rows, several launches past one dispatch
         const int64_t nb = (rows + kORows - 1) / kORows;
-        if (K <= 16 && al && nb <= max_grid_blocks(kORows)) {
-            dim3 g((unsigned)nb), b(kORows);
+        for (int64_t b0 = 0; b0 < nb; b0 += max_grid_blocks(kORows)) {
+            const int64_t cnt = nb - b0 < max_grid_blocks(kORows) ? nb - b0 : max_grid_blocks(kORows);
+            const int64_t r0 = b0 * kORows, off = r0 * K;
+            const int64_t nr = rows - r0 < cnt * kORows ? rows - r0 : cnt * kORows;
+            dim3 g((unsigned)cnt), b(kORows);
             switch (K) {
 #define MH_K(KK) \
-    case KK: hipLaunchKernelGGL((k_rowo_bwd<V, KK>), g, b, 0, st, gx, x, up, ug, rows, c); break;
-                MH_ROWP_CLASSES(MH_K)
+    case KK: hipLaunchKernelGGL((k_rowo_bwd<V, KK>), g, b, 0, st, gx + off, x + off, up + off, ug, nr, c); break;
+                MH_ROW16_CLASSES(MH_K)
 #undef MH_K
                 default: return fail(MH_ERR_INVALID, "row kernel: %d classes", K);
             }
-            return MH_OK;
-        }
-    }
-    if (K <= 16 && al) {  // persistent, pipelined
-        const void* kern = nullptr;
-        switch (K) {
-#define MH_K(KK) \
-    case KK: kern = reinterpret_cast<const void*>(&k_rowp_bwd<V, KK>); break;
-            MH_ROWP_CLASSES(MH_K)
-#undef MH_K
-            default: return fail(MH_ERR_INVALID, "row kernel: %d classes", K);
-        }
-        const int64_t ntiles = (rows + kSThreads - 1) / kSThreads;
-        const int64_t pg = pipe_grid(kern);
-        const int64_t nb = ntiles < pg ? ntiles : pg;
-        dim3 g((unsigned)nb), b(kSThreads);
-        switch (K) {
-#define MH_K(KK) \
-    case KK: hipLaunchKernelGGL((k_rowp_bwd<V, KK>), g, b, 0, st, gx, x, up, ug, rows, c); break;
-            MH_ROWP_CLASSES(MH_K)
-#undef MH_K
         }
         return MH_OK;
     }
@@ -1609,10 +1470,8 @@ static int loss_fwd(const char* what, float* loss, const float* x, const float* 
     float* part = nullptr;
     MH_TRY(scratch((np + t + 64) * sizeof(float), reinterpret_cast<void**>(&part)));
     int64_t nb = 0;
-    bool done = false;
     const float lscale = V == G_SMLM ? (float)n : ce;
-    MH_TRY(launch_fwd<V>(x, tg, nullptr, rows, (int)K, part, &nb, loss, lscale, &done));
-    if (done) return finish(what);
+    MH_TRY(launch_fwd<V>(x, tg, nullptr, rows, (int)K, part, &nb));
     if (nb <= kLossCombMax) {  // MEAN.forward: / f32(N); cross entropy: SUM, then MUL(., f32(-1 / f64(rows)))
         hipLaunchKernelGGL((k_loss_comb<V>), dim3(1), dim3(kLCThreads), 0, ctx().stream, part, nb, loss, lscale);
         return finish(what);
