@@ -441,14 +441,17 @@ int mh_plan_unbroadcast(const mh_shape* sgrad, const mh_shape* srg, mh_reduce_pl
  * and the number of launches. Every grid stays below the 2^32 work-items of one dispatch: the
  * one-quad-per-thread kernels (fill, copy, same-shape ops) cover at most 2^31 quads per launch
  * and longer tensors take several launches; the unaligned fill and k_adam loop over their grid
- * (k_adam_al, which does not, only takes tensors its grid covers). */
+ * (k_adam_al, which does not, only takes tensors its grid covers). MH_LAUNCH_ROWS16 counts rows,
+ * not elements: the row-fused losses' forward and every row-fused backward over rows of at most
+ * 16 classes run 64-row workgroups, several launches past one dispatch (none for zero rows). */
 enum {
     MH_LAUNCH_FILL = 0,            /* mh_fill / mh_zero, 16-byte-aligned tensor */
     MH_LAUNCH_FILL_UNALIGNED = 1,  /* mh_fill / mh_zero, other tensors */
     MH_LAUNCH_COPY = 2,            /* mh_memcpy_d2d of n floats, 16-byte aligned */
     MH_LAUNCH_SAME_SHAPE = 3,      /* same-shape elementwise forward / backward, aligned */
     MH_LAUNCH_ADAM = 4,            /* mh_adam_step, all four tensors 16-byte aligned */
-    MH_LAUNCH_ADAM_UNALIGNED = 5   /* mh_adam_step, other tensors */
+    MH_LAUNCH_ADAM_UNALIGNED = 5,  /* mh_adam_step, other tensors */
+    MH_LAUNCH_ROWS16 = 6           /* row-fused one-shot kernels over n rows of <= 16 classes, aligned */
 };
 typedef struct {
     int32_t kernel;

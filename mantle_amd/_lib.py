@@ -46,7 +46,8 @@ class mh_launch_info(ctypes.Structure):
                 ("launches", ctypes.c_int64)]
 
 
-LAUNCH_FILL, LAUNCH_FILL_UNALIGNED, LAUNCH_COPY, LAUNCH_SAME_SHAPE, LAUNCH_ADAM, LAUNCH_ADAM_UNALIGNED = range(6)
+(LAUNCH_FILL, LAUNCH_FILL_UNALIGNED, LAUNCH_COPY, LAUNCH_SAME_SHAPE, LAUNCH_ADAM, LAUNCH_ADAM_UNALIGNED,
+ LAUNCH_ROWS16) = range(7)
 
 
 class mh_attrs(ctypes.Structure):

@@ -134,6 +134,7 @@ LaunchShape fill_launch(int64_t n, bool aligned);
 LaunchShape copy_launch(int64_t nquads);
 LaunchShape elw_same_launch(int64_t n);
 LaunchShape adam_launch(int64_t n, bool aligned);
+LaunchShape row16_launch(int64_t rows);
 
 int scratch(size_t bytes, void** out);
 // A second library buffer for intermediates that live across calls using scratch().

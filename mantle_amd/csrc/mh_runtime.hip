@@ -727,6 +727,7 @@ int mh_plan_launch(int32_t what, int64_t n, mh_launch_info* out) {
         case MH_LAUNCH_SAME_SHAPE: ls = elw_same_launch(n); break;
         case MH_LAUNCH_ADAM: ls = adam_launch(n, true); break;
         case MH_LAUNCH_ADAM_UNALIGNED: ls = adam_launch(n, false); break;
+        case MH_LAUNCH_ROWS16: ls = row16_launch(n); break;
         default: return fail(MH_ERR_INVALID, "mh_plan_launch: unknown launch %d", what);
     }
     out->kernel = ls.kernel;

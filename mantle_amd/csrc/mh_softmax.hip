@@ -466,6 +466,7 @@ __global__ void __launch_bounds__(kSThreads)
 // the pass reads its 84 MB in 15.3 us, against 16.7 us for a persistent grid of 256-thread
 // blocks that prefetched each next 256-row tile into registers while computing the current one.
 constexpr int kORows = 64;
+constexpr int64_t kOMaxBlocks = max_grid_blocks(kORows);  // blocks of one launch
 
 template <int V, int K>
 __global__ void __launch_bounds__(kORows)
@@ -1255,6 +1256,13 @@ static int64_t pipe_grid(const void* kernel) {
     return (int64_t)it->second * ctx().num_cus;
 }
 
+// The one-shot engine's launches over `rows` rows (what mh_plan_launch reports): blocks of 64
+// rows, at most kOMaxBlocks per launch, each launch over the next run of rows.
+LaunchShape row16_launch(int64_t rows) {
+    const int64_t nb = (rows + kORows - 1) / kORows;
+    return LaunchShape{0, kORows, nb < kOMaxBlocks ? nb : kOMaxBlocks, (nb + kOMaxBlocks - 1) / kOMaxBlocks};
+}
+
 static int check_rows(const char* what, int64_t rows, int64_t classes) {
     if (rows < 0 || classes < 0) return fail(MH_ERR_INVALID, "%s: negative size", what);
     if (classes > kSWaveMax)
@@ -1301,8 +1309,8 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
         if (K <= 16 && al) {  // one-shot blocks of 64 rows
             const int64_t nb = (rows + kORows - 1) / kORows;
             *nblocks_out = nb;
-            for (int64_t b0 = 0; b0 < nb; b0 += max_grid_blocks(kORows)) {
-                const int64_t cnt = nb - b0 < max_grid_blocks(kORows) ? nb - b0 : max_grid_blocks(kORows);
+            for (int64_t b0 = 0; b0 < nb; b0 += kOMaxBlocks) {
+                const int64_t cnt = nb - b0 < kOMaxBlocks ? nb - b0 : kOMaxBlocks;
                 const int64_t r0 = b0 * kORows, off = r0 * K;  // 16-byte aligned: r0 is a multiple of 64
                 const int64_t nr = rows - r0 < cnt * kORows ? rows - r0 : cnt * kORows;
                 dim3 g((unsigned)cnt), b(kORows);
@@ -1380,8 +1388,8 @@ static int launch_bwd(float* gx, const float* x, const float* up, const float* u
     const bool al = al16s(x) && al16s(up) && al16s(gx);
     if (K <= 16 && al) {  // one-shot blocks of 64 rows, several launches past one dispatch
         const int64_t nb = (rows + kORows - 1) / kORows;
-        for (int64_t b0 = 0; b0 < nb; b0 += max_grid_blocks(kORows)) {
-            const int64_t cnt = nb - b0 < max_grid_blocks(kORows) ? nb - b0 : max_grid_blocks(kORows);
+        for (int64_t b0 = 0; b0 < nb; b0 += kOMaxBlocks) {
+            const int64_t cnt = nb - b0 < kOMaxBlocks ? nb - b0 : kOMaxBlocks;
             const int64_t r0 = b0 * kORows, off = r0 * K;
             const int64_t nr = rows - r0 < cnt * kORows ? rows - r0 : cnt * kORows;
             dim3 g((unsigned)cnt), b(kORows);

@@ -297,5 +297,23 @@ def test_launch_grids_fit_one_dispatch(what):
                 assert items >= (n >> 2) + 1
         elif what == _lib.LAUNCH_ADAM_UNALIGNED:
             assert info.kernel == 1
-    assert L.mh_plan_launch(6, 10, ctypes.byref(info)) == _lib.ERR_INVALID
+    assert L.mh_plan_launch(7, 10, ctypes.byref(info)) == _lib.ERR_INVALID
+
+
+def test_row_engine_launches_split_rows_past_one_dispatch():
+    """The row-fused one-shot kernels (64-row workgroups of one wavefront) stay below the 2^32
+    work-items of one dispatch and cover every row, in consecutive launches whose row runs
+    start at multiples of 64 rows (so each launch's operands stay 16-byte aligned), up to
+    2^40 rows; zero rows make no launch."""
+    L = _lib.lib()
+    info = _lib.mh_launch_info()
+    assert L.mh_plan_launch(_lib.LAUNCH_ROWS16, 0, ctypes.byref(info)) == 0
+    assert info.launches == 0
+    for rows in (1, 63, 64, 65, 1 << 20, (1 << 32) - 64, (1 << 32) - 1, 1 << 32, (1 << 32) + 1, 1 << 36, 1 << 40):
+        assert L.mh_plan_launch(_lib.LAUNCH_ROWS16, rows, ctypes.byref(info)) == 0, L.mh_last_error()
+        assert info.threads == 64 and 1 <= info.blocks and info.blocks * 64 < (1 << 32), (rows, info.blocks)
+        nb = -(-rows // 64)
+        assert info.launches == -(-nb // info.blocks), (rows, info.launches)
+        assert info.blocks == min(nb, ((1 << 32) - 1) // 64), (rows, info.blocks)
+        assert info.blocks * 64 * info.launches >= rows > info.blocks * 64 * (info.launches - 1), rows
     assert L.mh_plan_launch(0, -1, ctypes.byref(info)) == _lib.ERR_INVALID
