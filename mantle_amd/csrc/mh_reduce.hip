@@ -1359,12 +1359,16 @@ __global__ void __launch_bounds__(kRThreads)
     }
 }
 
-// Combines of the split partials, in split order. Rows: one 1024-thread block per row, S
-// partials contiguous: thread t adds partials t, t + 1024, ... (four in flight, so a row of
-// up to kMomMaxSplit partials waits on memory once), then the waves' butterflies and the 16
-// waves in order. Columns: partials at stride nlines, a block per 16 lines (below).
-constexpr int kMomCombThreads = 1024;
-static_assert(kMomMaxSplit <= 4 * kMomCombThreads, "one round of loads per thread");
+// Combines of the split partials, in split order. Rows: one 256-thread block per row, S
+// partials contiguous: thread t adds partials t, t + 256, ... (sixteen in flight, so a row of
+// up to kMomMaxSplit partials waits on memory once), then the waves' butterflies and the four
+// waves in order. Fewer, fuller threads shorten the serial end (butterflies of fp64 values,
+// the waves' sums, the division and square root): after the moment pass over [8192, 8192]
+// this ended 0.6-1.4 us sooner than 1024 threads with four partials each. Columns: partials at
+// stride nlines, a block per 16 lines (below).
+constexpr int kMomCombThreads = 256;
+constexpr int kMomCombLoads = 16;
+static_assert(kMomMaxSplit <= kMomCombLoads * kMomCombThreads, "one round of loads per thread");
 
 __global__ void __launch_bounds__(kMomCombThreads)
     k_tstd_mom_combine_rows(float* __restrict__ res, const Mom* __restrict__ part, int64_t S, int64_t B) {
@@ -1372,12 +1376,13 @@ __global__ void __launch_bounds__(kMomCombThreads)
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const Mom* p = part + (int64_t)blockIdx.x * S;
     Mom m{0.0, 0.0};
-    for (int64_t i = t; i < S; i += 4 * kMomCombThreads) {  // four partials in flight, added in order
-        Mom q[4];
+    for (int64_t i = t; i < S; i += kMomCombLoads * kMomCombThreads) {  // partials in flight, added in order
+        Mom q[kMomCombLoads];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) q[u] = i + u * kMomCombThreads < S ? p[i + u * kMomCombThreads] : Mom{0.0, 0.0};
+        for (int u = 0; u < kMomCombLoads; ++u)
+            q[u] = i + u * kMomCombThreads < S ? p[i + u * kMomCombThreads] : Mom{0.0, 0.0};
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kMomCombLoads; ++u) {
             m.s1 = m.s1 + q[u].s1;
             m.s2 = m.s2 + q[u].s2;
         }
