@@ -1014,6 +1014,83 @@ def test_fused_row_graphs(gpu, rows, classes):
     assert_bitexact(tg.to_numpy(), gr["x"], "cross-entropy backward")
 
 
+SPECIAL_ROW_CASES = [(64, 1), (131, 3), (200, 10), (129, 16), (70, 20), (65, 33), (40, 100)]
+
+
+def _special_rows(rows, classes, nonfinite):
+    """Logits with signed zeros, magnitudes near the float limit, subnormals and exact ties
+    (and with `nonfinite`, NaN and infinities), plus whole rows of one value."""
+    x = synth.normal((rows, classes), 0, 2, 1500)
+    if classes > 1:
+        synth.inject_ties(x, 1, 1501)
+    u = synth.uniform((rows, classes), 0, 1, 1502)
+    x[u < 0.05] = np.float32(-0.0)
+    x[(u >= 0.05) & (u < 0.08)] = np.float32(0.0)
+    x[(u >= 0.08) & (u < 0.10)] = np.float32(3.0e38)
+    x[(u >= 0.10) & (u < 0.12)] = np.float32(-3.0e38)
+    x[(u >= 0.12) & (u < 0.14)] = np.float32(1.0e-40)
+    x[1] = np.float32(-3.0e38)
+    x[2] = np.float32(-0.0)
+    if nonfinite:
+        x[(u >= 0.14) & (u < 0.16)] = np.float32(np.nan)
+        x[(u >= 0.16) & (u < 0.18)] = np.float32(np.inf)
+        x[(u >= 0.18) & (u < 0.20)] = np.float32(-np.inf)
+        x[3] = np.float32(-np.inf)
+        x[4] = np.float32(np.inf)
+    return x
+
+
+@pytest.mark.parametrize("rows,classes", SPECIAL_ROW_CASES, ids=[f"{r}x{c}" for r, c in SPECIAL_ROW_CASES])
+@pytest.mark.parametrize("nonfinite", [False, True], ids=["finite", "nonfinite"])
+def test_fused_row_graphs_special_values(gpu, rows, classes, nonfinite):
+    """Softmax, LogSoftmax and CrossEntropyLoss fused against the op-by-op graphs on the GPU
+    at row lengths of every engine (one-shot and pipelined up to 16 classes, thread and
+    multi-lane up to 64, wavefront beyond), on logits with signed zeros, near-limit
+    magnitudes, subnormals, ties and whole rows of one value, and (nonfinite) NaN and
+    infinities: outputs and gradients bit-identical (NaN matching NaN), the loss in the sum
+    class or non-finite where the graph's is."""
+    from util import cross_entropy_nodes, logsoftmax_nodes, softmax_nodes
+    m = gpu.m
+    print(f"\n[special rows] {rows}x{classes} nonfinite={nonfinite}", flush=True)
+    x = _special_rows(rows, classes, nonfinite)
+    g0 = synth.normal((rows, classes), 0, 1, 1503)
+    gout = synth.normal((rows, classes), 0, 1, 1504)
+    gout[0] = np.float32(-0.0)
+    tx = gpu.T(x)
+    for name, nodes, out_name, fwd, bwd in [
+            ("softmax", softmax_nodes("x", 1), "sm", m.softmax_forward, m.softmax_backward),
+            ("logsoftmax", logsoftmax_nodes("x", 1), "lsm", m.logsoftmax_forward, m.logsoftmax_backward)]:
+        g = Graph(nodes, ["x"])
+        v = g.forward(gpu, {"x": x})
+        out = m.Tensor(m.TensorShape(rows, classes))
+        fwd(out, tx)
+        assert_bitexact(out.to_numpy(), v[out_name], f"{name} forward")
+        gr = g.backward(gpu, v, seed=gout, init={"x": g0})
+        tg = gpu.T(g0)
+        bwd(tg, tx, gpu.T(gout))
+        assert_bitexact(tg.to_numpy(), gr["x"], f"{name} backward")
+    target = synth.uniform((rows, classes), 0, 1, 1505)
+    target[0] = np.float32(0.0)
+    cn = np.array([np.float32(-1.0 / rows)], np.float32)
+    g = Graph(cross_entropy_nodes("x", "target"), ["x"])
+    v = g.forward(gpu, {"x": x, "target": target, "cN": cn})
+    loss = m.Tensor(m.TensorShape(1))
+    ttg = gpu.T(target)
+    m.cross_entropy_forward(loss, tx, ttg)
+    got, ref = loss.to_numpy(), v["loss"]
+    if np.isfinite(ref).all():
+        tl64 = v["tl"].astype(np.float64)
+        assert_sum_close(got, ref, np.array([tl64.sum() * float(cn[0])]), "cross-entropy loss",
+                         terms_abs=np.array([np.abs(tl64).sum() * abs(float(cn[0]))]))
+    else:
+        assert (np.isnan(got) == np.isnan(ref)).all() and (np.isinf(got) == np.isinf(ref)).all(), (got, ref)
+    seed = np.array([0.7], np.float32)
+    gr = g.backward(gpu, v, seed=seed, init={"x": g0})
+    tg = gpu.T(g0)
+    m.cross_entropy_backward(tg, tx, ttg, gpu.T(seed))
+    assert_bitexact(tg.to_numpy(), gr["x"], "cross-entropy backward")
+
+
 # Row counts whose one-shot loss partials (one per 64 rows) the one-block combine sums in three
 # rounds with a partial count that is not a multiple of four (2999999 rows: 46875 partials), in
 # exactly its largest count (64 * 65536 rows), and one past it, where the multi-block
