@@ -801,6 +801,62 @@ def test_fused_bias_relu_shapes(gpu, sx, sb, keep_gy):
                      terms_abs=mag)
 
 
+FUSED_SPECIAL_SHAPES = [((8, 32, 28, 28), (1, 32, 1, 1)), ((22, 3, 1796), (1, 3, 1)), ((3, 7, 10), (1, 7, 1)),
+                        ((64, 40), (1, 40))]
+
+
+@pytest.mark.parametrize("sx,sb", FUSED_SPECIAL_SHAPES, ids=[f"{a}+{b}" for a, b in FUSED_SPECIAL_SHAPES])
+@pytest.mark.parametrize("nonfinite", [False, True], ids=["finite", "nonfinite"])
+def test_fused_bias_relu_special_values(gpu, sx, sb, nonfinite):
+    """mh_bias_relu_fwd / _bwd_accum against the op-by-op oracle where y = x + bias is a signed
+    zero (RELU's gradient at -0 and +0), near the float limit, subnormal, and (nonfinite) NaN
+    or infinite, with such values in the upstream gradient too: y, r, grad_y and grad_x
+    bit-identical (NaN matching NaN); the bias gradient in the sum class, or NaN / infinite
+    exactly where the oracle's is."""
+    m = gpu.m
+    print(f"\n[fused bias relu special] {sx}+{sb} nonfinite={nonfinite}", flush=True)
+    x = synth.normal(sx, 0, 1, 41)
+    bias = synth.normal(sb, 0, 0.1, 42)
+    bias.reshape(-1)[0] = np.float32(-0.0)
+    ug = synth.normal(sx, 0, 1, 43)
+    u = synth.uniform(sx, 0, 1, 44)
+    x[u < 0.04] = np.float32(-0.0)
+    x[(u >= 0.04) & (u < 0.08)] = np.float32(0.0)
+    x[(u >= 0.08) & (u < 0.09)] = np.float32(3.0e38)
+    x[(u >= 0.09) & (u < 0.10)] = np.float32(-3.0e38)
+    x[(u >= 0.10) & (u < 0.11)] = np.float32(1.0e-40)
+    ug[(u >= 0.11) & (u < 0.13)] = np.float32(-0.0)
+    ug[(u >= 0.13) & (u < 0.14)] = np.float32(2.0e38)
+    if nonfinite:
+        x[(u >= 0.14) & (u < 0.15)] = np.float32(np.nan)
+        x[(u >= 0.15) & (u < 0.16)] = np.float32(np.inf)
+        x[(u >= 0.16) & (u < 0.17)] = np.float32(-np.inf)
+        ug[(u >= 0.17) & (u < 0.18)] = np.float32(np.nan)
+        ug[(u >= 0.18) & (u < 0.19)] = np.float32(np.inf)
+    gy0, gx0, gb0 = synth.normal(sx, 0, 1, 45), synth.normal(sx, 0, 1, 46), synth.normal(sb, 0, 1, 47)
+    tx, tb, tu = gpu.T(x), gpu.T(bias), gpu.T(ug)
+    y, r = m.Tensor(tx.shape()), m.Tensor(tx.shape())
+    S = m._lib
+    S.call("mh_bias_relu_fwd", y.ptr, r.ptr, tx.ptr, tx.shape().c(), tb.ptr, tb.shape().c())
+    y_ref = ORC.forward(OPS["ADD"], x, bias)
+    assert_bitexact(y.to_numpy(), y_ref, "y")
+    assert_bitexact(r.to_numpy(), ORC.forward(OPS["RELU"], y_ref), "r")
+    tgy, tgx, tgb = gpu.T(gy0), gpu.T(gx0), gpu.T(gb0)
+    S.call("mh_bias_relu_bwd_accum", tgy.ptr, tgx.ptr, tgb.ptr, y.ptr, tu.ptr, tx.shape().c(), tb.shape().c())
+    gy = ORC.backward(0, OPS["RELU"], ug, y_ref, grad=gy0)
+    assert_bitexact(tgy.to_numpy(), gy, "fused grad y")
+    assert_bitexact(tgx.to_numpy(), ORC.backward(0, OPS["ADD"], gy, x, bias, grad=gx0), "fused grad x")
+    ref = ORC.backward(1, OPS["ADD"], gy, x, bias, grad=gb0)
+    got = tgb.to_numpy()
+    fin = np.isfinite(ref)
+    assert (np.isnan(got) == np.isnan(ref)).all() and (np.isinf(got) == np.isinf(ref)).all(), "bias grad non-finite"
+    red = tuple(i for i in range(len(sx)) if i < len(sx) - len(sb) or sb[i - (len(sx) - len(sb))] == 1)
+    gyd = gy.astype(np.float64)
+    ex = gyd.sum(axis=red).reshape(sb) + gb0.astype(np.float64)
+    mag = np.abs(gyd).sum(axis=red).reshape(sb) + np.abs(gb0)
+    assert_sum_close(got[fin], ref[fin], ex[fin], "fused grad bias", terms_abs=mag[fin])
+
+
 def config5_inputs(n, seed=0):
     logits = synth.normal((n, 10), 0, 2, 31 + seed)
     cls = synth.integers((n,), 0, 10, 32 + seed)
