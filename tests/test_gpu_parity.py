@@ -156,6 +156,40 @@ def test_binary_bwd_both_operands_fused(gpu, op):
     assert_bitexact(tg2.to_numpy(), ORC.backward(1, op, ug, a, b, grad=g2), "fused id1")
 
 
+_SPECIAL32 = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1e-45, -1e-40, 1.17549435e-38, 1.0, -1.0, 0.5, 2.0,
+                       3.4e38, -3.4e38, 1e20, -1e-20, 3.0, -7.0], np.float32)
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3], ids=["ADD", "SUB", "MUL", "DIV"])
+def test_binary_special_values_bitexact(gpu, op):
+    """Every pair of special operands (NaN, infinities, signed zeros, subnormals, values near
+    the float limit, and ordinary ones), same shape and with each operand a scalar: the
+    forward, each operand's gradient and the fused two-gradient pass bit-identical to the
+    oracle (NaN matching NaN), accumulated into gradients that hold special values too."""
+    m = gpu.m
+    s = _SPECIAL32
+    a = np.repeat(s, s.size).astype(np.float32)
+    b = np.tile(s, s.size).astype(np.float32)
+    n = a.size
+    ug = np.tile(np.array([1.0, -0.0, np.nan, 2.5e38, -3.0, 1e-42], np.float32), -(-n // 6))[:n].copy()
+    g1 = np.tile(np.array([0.0, -0.0, 1.0, np.inf, -2.0], np.float32), -(-n // 5))[:n].copy()
+    g2 = np.tile(np.array([-0.0, 3.0, np.nan, 0.0, -1e38, 7.0, 1e-44], np.float32), -(-n // 7))[:n].copy()
+    assert_bitexact(gpu.forward(op, a, b), ORC.forward(op, a, b), f"fwd op{op}")
+    for k, g0 in ((0, g1), (1, g2)):
+        assert_bitexact(gpu.backward(k, op, ug, a, b, grad=g0), ORC.backward(k, op, ug, a, b, grad=g0),
+                        f"bwd op{op} id{k}")
+    ta, tb, tu, tg1, tg2 = (gpu.T(v) for v in (a, b, ug, g1, g2))
+    m.backward_op_both(op, tu, ta, tb, tg1, tg2)
+    assert_bitexact(tg1.to_numpy(), ORC.backward(0, op, ug, a, b, grad=g1), f"fused op{op} id0")
+    assert_bitexact(tg2.to_numpy(), ORC.backward(1, op, ug, a, b, grad=g2), f"fused op{op} id1")
+    for sv in (np.float32(-0.0), np.float32(np.inf), np.float32(np.nan), np.float32(1e-40)):
+        sc = np.array([sv], np.float32)
+        assert_bitexact(gpu.forward(op, a, sc), ORC.forward(op, a, sc), f"fwd op{op} tensor-scalar {sv}")
+        assert_bitexact(gpu.forward(op, sc, b), ORC.forward(op, sc, b), f"fwd op{op} scalar-tensor {sv}")
+        assert_bitexact(gpu.backward(0, op, ug, a, sc, grad=g1), ORC.backward(0, op, ug, a, sc, grad=g1),
+                        f"bwd op{op} id0 tensor-scalar {sv}")
+
+
 @pytest.mark.parametrize("n", [(1 << 16) + 3, 5, 4096])
 @pytest.mark.parametrize("op", [0, 1, 2, 3], ids=["ADD", "SUB", "MUL", "DIV"])
 def test_binary_bwd_both_operands_one_symbol(gpu, op, n):
