@@ -273,6 +273,27 @@ def test_device_math_matches_oracle_bitwise(gpu, name):
     assert_bitexact(gpu.forward(OPS[name], x), ORC.forward(OPS[name], x), f"{name} special inputs")
 
 
+@pytest.mark.parametrize("name", ["EXP", "LOG", "SIGMOID", "TANH", "RELU"])
+def test_unary_backward_special_values_bitexact(gpu, name):
+    """The unary backward passes on the same special arguments, with NaN, infinite, signed-zero
+    and subnormal values in the upstream gradient and in the gradient they accumulate into:
+    bit-identical to the oracle (NaN matching NaN)."""
+    x = _special_inputs(960 + OPS[name])
+    n = x.size
+    ug = synth.normal((n,), 0, 1, 961)
+    ug[::7] = np.float32(-0.0)
+    ug[1::11] = np.float32(np.nan)
+    ug[2::13] = np.float32(np.inf)
+    ug[3::17] = np.float32(1e-42)
+    ug[4::19] = np.float32(-3.0e38)
+    g0 = synth.normal((n,), 0, 1, 962)
+    g0[::5] = np.float32(-0.0)
+    g0[1::9] = np.float32(-np.inf)
+    g0[2::23] = np.float32(np.nan)
+    assert_bitexact(gpu.backward(0, OPS[name], ug, x, grad=g0), ORC.backward(0, OPS[name], ug, x, grad=g0),
+                    f"{name} backward, special values")
+
+
 def test_device_pow_matches_oracle_bitwise(gpu):
     x = np.abs(_special_inputs(950))
     ug = synth.normal(x.shape, 0, 1, 951)
