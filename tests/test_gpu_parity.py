@@ -507,6 +507,67 @@ def test_reduce_fwd_bwd_parity(gpu, shape, axis):
         assert_bitexact(got, ORC.backward(0, OPS[name], ug, x, axis=axis, grad=g0), f"{name} bwd")
 
 
+SUM_SPECIAL_CASES = [((4099, 10), 1), ((300, 257), 0), ((64, 5000), 1), ((37, 63, 107), 1), ((9000, 64), 0),
+                     (((1 << 20) + 3,), None), ((3, 12000), None)]
+
+
+@pytest.mark.parametrize("shape,axis", SUM_SPECIAL_CASES, ids=[f"{s}-ax{a}" for s, a in SUM_SPECIAL_CASES])
+def test_sum_mean_special_values(gpu, shape, axis):
+    """SUM and MEAN over lines holding +inf, both infinities, NaN, only -0 (which sum to +0, as
+    a sum from +0 does), only positive values near the float limit (which overflow in any
+    order), signed zeros and subnormals: a line's result is NaN / +-inf exactly where the
+    oracle's is, +0 bit for bit on the -0 lines, and in the sum class elsewhere; the backward
+    passes (a scaled broadcast of an upstream gradient holding special values) bit-identical."""
+    x = synth.normal(shape, 0, 1, 760)
+    lines = np.moveaxis(x, axis, -1) if axis is not None else x.reshape(1, -1)
+    flat = lines.reshape(-1, lines.shape[-1])  # a view for contiguous moves, else a copy
+    L = flat.shape[0]
+    special = [(0, "inf"), (1, "both"), (2, "nan"), (3, "negzero"), (4, "huge")] if L >= 5 else [(0, "nan")]
+    for li, kind in special:
+        row = flat[li]
+        if kind == "inf":
+            row[row.size // 3] = np.inf
+        elif kind == "both":
+            row[0], row[-1] = np.inf, -np.inf
+        elif kind == "nan":
+            row[row.size // 2] = np.nan
+        elif kind == "negzero":
+            row[:] = np.float32(-0.0)
+        else:
+            row[:] = np.abs(row) + np.float32(1.0)
+            row[: max(2, row.size // 4)] = np.float32(3.0e38)
+    if L > 6:
+        flat[5, ::3] = np.float32(-0.0)
+        flat[6, 1::4] = np.float32(1e-41)
+    if not np.shares_memory(flat, x):
+        lines[...] = flat.reshape(lines.shape)  # lines is a view of x
+    red_shape = (1,) if axis is None else tuple(1 if i == axis else d for i, d in enumerate(shape))
+    d = x.size if axis is None else shape[axis]
+    for name in ("SUM", "MEAN"):
+        got = gpu.forward(OPS[name], x, axis=axis)
+        ref = ORC.forward(OPS[name], x, axis=axis)
+        assert (np.isnan(got) == np.isnan(ref)).all(), f"{name}: NaN lines"
+        assert (np.isinf(got) == np.isinf(ref)).all() and (np.sign(got[np.isinf(got)]) == np.sign(ref[np.isinf(ref)])).all(), \
+            f"{name}: infinite lines"
+        fin = np.isfinite(ref)
+        if L >= 5:  # line 3 holds only -0: the sum from +0 is +0
+            assert_bitexact(got.reshape(-1)[3:4], ref.reshape(-1)[3:4], f"{name}: a line of -0")
+            assert ref.reshape(-1)[3].tobytes() == np.float32(0.0).tobytes()
+        x64 = np.where(np.isfinite(x), x, 0).astype(np.float64)
+        kd = dict(axis=axis, keepdims=True) if axis is not None else {}
+        ex = x64.sum(**kd).reshape(red_shape) / (d if name == "MEAN" else 1)
+        mag = np.abs(x64).sum(**kd).reshape(red_shape) / (d if name == "MEAN" else 1)
+        assert_sum_close(got[fin], ref[fin], ex[fin], name, terms_abs=mag[fin])
+        ug = synth.normal(red_shape, 0, 1, 761)
+        ug.reshape(-1)[0] = np.float32(-0.0)
+        if ug.size > 2:
+            ug.reshape(-1)[1], ug.reshape(-1)[2] = np.float32(np.inf), np.float32(np.nan)
+        g0 = synth.normal(shape, 0, 1, 762)
+        g0.reshape(-1)[::97] = np.float32(-0.0)
+        got = gpu.backward(0, OPS[name], ug, x, axis=axis, grad=g0)
+        assert_bitexact(got, ORC.backward(0, OPS[name], ug, x, axis=axis, grad=g0), f"{name} bwd")
+
+
 MAX_SPARSE_CASES = [((1024, 1024), 0), ((4099, 10), 1), ((300, 20), 1), ((64, 512), 1), ((9, 2052), 1),
                     ((87, 73, 107), None), ((87, 73, 107), 1), ((4, 8, 1024), 0), ((2, 5000, 132), 1),
                     # split routes: row chunks (all elements, a short last chunk), the strip and
