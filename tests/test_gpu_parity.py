@@ -190,6 +190,56 @@ def test_binary_special_values_bitexact(gpu, op):
                         f"bwd op{op} id0 tensor-scalar {sv}")
 
 
+# the broadcast engines: per-row and per-column operands, a per-channel NCHW operand, and a
+# general broadcast (both operands broadcast)
+BCAST_SPECIAL = [((18, 20), (18, 1)), ((20, 18), (1, 18)), ((2, 18, 20), (1, 18, 1)), ((18, 1, 20), (1, 3, 20))]
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3], ids=["ADD", "SUB", "MUL", "DIV"])
+@pytest.mark.parametrize("sa,sb", BCAST_SPECIAL, ids=[f"{a}x{b}" for a, b in BCAST_SPECIAL])
+def test_broadcast_special_values(gpu, op, sa, sb):
+    """Special operands (NaN, infinities, signed zeros, subnormals, near-limit values) through
+    the row, column, plane and general broadcast engines, in both operand orders: the forward
+    and the full-shape operand's gradient bit for bit against the oracle; the broadcast
+    operand's gradient (a sum over the broadcast axes) NaN / +-inf exactly where the oracle's
+    is and in the sum class elsewhere."""
+    s = _SPECIAL32
+    for x_shape, y_shape in ((sa, sb), (sb, sa)):
+        a = np.resize(s, int(np.prod(x_shape))).reshape(x_shape).astype(np.float32)
+        b = np.resize(s[::-1], int(np.prod(y_shape))).reshape(y_shape).astype(np.float32)
+        assert_bitexact(gpu.forward(op, a, b), ORC.forward(op, a, b), f"fwd op{op} {x_shape}x{y_shape}")
+        out_shape = np.broadcast_shapes(x_shape, y_shape)
+        ug = synth.normal(out_shape, 0, 1, 790 + op)
+        ug.reshape(-1)[::11] = np.float32(-0.0)
+        for k, shape in ((0, x_shape), (1, y_shape)):
+            g0 = synth.normal(shape, 0, 1, 795 + k)
+            got = gpu.backward(k, op, ug, a, b, grad=g0)
+            ref = ORC.backward(k, op, ug, a, b, grad=g0)
+            what = f"bwd op{op} id{k} {x_shape}x{y_shape}"
+            if tuple(shape) == tuple(out_shape):
+                assert_bitexact(got, ref, what)
+                continue
+            A, B, U = (v.astype(np.float64) for v in np.broadcast_arrays(a, b, ug))
+            with np.errstate(all="ignore"):
+                rg = {0: U, 1: (U if k == 0 else -U), 2: (U * B if k == 0 else U * A),
+                      3: (U / B if k == 0 else -A / (B * B) * U)}[op]
+            red = tuple(i for i in range(len(out_shape)) if i >= len(out_shape) - len(shape) and
+                        shape[i - (len(out_shape) - len(shape))] == 1 and out_shape[i] != 1) + \
+                tuple(range(len(out_shape) - len(shape)))
+            rgf = np.where(np.isfinite(rg), rg, 0.0)
+            ex = rgf.sum(axis=red, keepdims=True).reshape(shape) + g0.astype(np.float64)
+            mag = np.abs(rgf).sum(axis=red, keepdims=True).reshape(shape) + np.abs(g0)
+            # where the finite terms' magnitudes stay below the float limit no partial sum can
+            # overflow, so whether a sum is NaN or infinite does not depend on its order
+            safe = mag < 1e38
+            assert (np.isnan(got) == np.isnan(ref))[safe].all(), what
+            assert (np.isinf(got) == np.isinf(ref))[safe].all(), what
+            inf = np.isinf(ref) & safe
+            assert (np.sign(got[inf]) == np.sign(ref[inf])).all(), what
+            fin = np.isfinite(ref) & safe
+            assert_sum_close(got[fin], ref[fin], ex[fin], what, terms_abs=mag[fin])
+
+
 @pytest.mark.parametrize("n", [(1 << 16) + 3, 5, 4096])
 @pytest.mark.parametrize("op", [0, 1, 2, 3], ids=["ADD", "SUB", "MUL", "DIV"])
 def test_binary_bwd_both_operands_one_symbol(gpu, op, n):
