@@ -461,10 +461,10 @@ __global__ void __launch_bounds__(kSThreads)
 // and element-order sums). The forward runs the loss graphs: a block's partial is the
 // wavefront's butterfly sum of its row sums, which k_loss_comb then sums. The backward runs
 // every graph. Each class count 1..16 has its own kernel (every loop over a row unrolled
-// without per-class guards). Many small blocks (5 KB of LDS each at 10 classes)
-// keep the CU full of waves, so the loads of some overlap the exp work of others: at config 5
-// the pass reads its 84 MB in 15.3 us, against 16.7 us for a persistent grid of 256-thread
-// blocks that prefetched each next 256-row tile into registers while computing the current one.
+// without per-class guards). Many small blocks (5 KB of LDS each at 10 classes) keep the CU
+// full of waves, so the loads of some overlap the exp work of others: at config 5 the pass
+// reads its 84 MB in 15.3 us, against 16.7 us for a persistent grid of 256-thread blocks that
+// prefetched each next 256-row tile into registers while computing the current one.
 constexpr int kORows = 64;
 constexpr int64_t kOMaxBlocks = max_grid_blocks(kORows);  // blocks of one launch
 
@@ -520,8 +520,8 @@ __global__ void __launch_bounds__(kORows)
 // per wavefront and the sixteen wavefront sums in order finish it. The loss is the sum / lscale
 // (MEAN, lscale = f32(N)) or the sum * lscale (cross entropy, lscale = its scale). One launch
 // with every load of a round in flight: at config 5 (16384 partials) 2.4 us after the pass,
-// against 3.2 us for two rounds of scalar loads. Used up to kLossCombMax partials; above that
-// the library's multi-block all-element reduction is faster.
+// against 2.8-3.3 us for two rounds of scalar loads. It takes up to kLossCombMax partials (four
+// rounds); more go through the library's multi-block all-element reduction.
 constexpr int kLCThreads = 1024;
 constexpr int64_t kLossCombMax = 4 * 4 * kLCThreads;
 
