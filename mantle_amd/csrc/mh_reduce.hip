@@ -65,11 +65,14 @@ struct RMaxCnt {
     using T = MC;
     __device__ static T init() { return MC{-FLT_MAX, 0u}; }
     __device__ static T lift(float x) { return MC{x, 1u}; }
+    // the larger side wins; equal maxima add their counts; against a NaN element the other
+    // side wins. Written as selects over comparisons joined without short-circuits: early
+    // returns (or || and &&) compiled to a branch per comparison, with an exec-mask save and
+    // restore around each element of a line.
     __device__ static T comb(T a, T b) {
-        if (a.m > b.m) return a;
-        if (b.m > a.m) return b;
-        if (a.m == b.m) return MC{a.m, a.c + b.c};
-        return a.m != a.m ? b : a;  // one side is a NaN element
+        const bool eq = a.m == b.m;
+        const bool take_b = (b.m > a.m) | (!(a.m > b.m) & !eq & (a.m != a.m));
+        return MC{take_b ? b.m : a.m, eq ? a.c + b.c : (take_b ? b.c : a.c)};
     }
     __device__ static T shfl(T v, int m) {
         return MC{__shfl_xor(v.m, m), (uint32_t)__shfl_xor((int)v.c, m)};
@@ -88,11 +91,11 @@ struct RMaxCntArg {
     using T = MCI;
     __device__ static T init() { return MCI{-FLT_MAX, 0u, 0xffffffffu}; }
     __device__ static T lift(float x) { return MCI{x, 1u, 0xffffffffu}; }
-    __device__ static T comb(T a, T b) {
-        if (a.m > b.m) return a;
-        if (b.m > a.m) return b;
-        if (a.m == b.m) return MCI{a.m, a.c + b.c, a.i < b.i ? a.i : b.i};
-        return a.m != a.m ? b : a;  // one side is a NaN element
+    __device__ static T comb(T a, T b) {  // RMaxCnt's selects, the lower index on a tie
+        const bool eq = a.m == b.m;
+        const bool take_b = (b.m > a.m) | (!(a.m > b.m) & !eq & (a.m != a.m));
+        return MCI{take_b ? b.m : a.m, eq ? a.c + b.c : (take_b ? b.c : a.c),
+                   eq ? (a.i < b.i ? a.i : b.i) : (take_b ? b.i : a.i)};
     }
     __device__ static T shfl(T v, int m) {
         return MCI{__shfl_xor(v.m, m), (uint32_t)__shfl_xor((int)v.c, m), (uint32_t)__shfl_xor((int)v.i, m)};
