@@ -66,6 +66,24 @@ constexpr bool from_softmax() {
 
 __device__ __forceinline__ float max_simd(float a, float b) { return a > b ? a : b; }
 
+// One element v into a row's running (maximum, count) from (-FLT_MAX, 0): a larger v starts
+// a new count, an equal one adds to it, a smaller one or a NaN changes nothing. Selects over
+// the comparisons: the if / else-if chain this replaces compiled to a branch per element.
+__device__ __forceinline__ void max_count_add(float& mb, uint32_t& cnt, float v) {
+    const bool gt = v > mb, eq = v == mb;
+    cnt = gt ? 1u : (eq ? cnt + 1u : cnt);
+    mb = gt ? v : mb;
+}
+
+// Two (maximum, count) pairs whose maxima are not NaN: the larger maximum with its count,
+// equal maxima with both counts.
+__device__ __forceinline__ void max_count_merge(float& mb, uint32_t& cnt, float om, uint32_t oc) {
+    const bool gt = om > mb, eq = om == mb;
+    cnt = gt ? oc : (eq ? cnt + oc : cnt);
+    mb = gt ? om : mb;
+}
+
+
 // Rows per block of the thread engine: 256, halved until `tiles` tiles of rb * K floats fit.
 static inline int rows_per_block(int tiles, int64_t K) {
     int rb = kSThreads;
@@ -299,13 +317,7 @@ __global__ void __launch_bounds__(kSThreads)
             if (j < K) {
                 const float v = xr[j];
                 m = max_simd(m, v);
-                if (mb > v) {
-                } else if (v > mb) {
-                    mb = v;
-                    cntm = 1;
-                } else if (v == mb) {  // a NaN element is not counted
-                    cntm += 1;
-                }
+                max_count_add(mb, cntm, v);  // a NaN element is not counted
             }
         }
         float s = 0.0f;
@@ -574,13 +586,7 @@ __device__ __forceinline__ void row_bwd(float (&xr)[KM], float (&pre)[KM], float
         if (j < K) {
             const float v = xr[j];
             m = max_simd(m, v);
-            if (mb > v) {
-            } else if (v > mb) {
-                mb = v;
-                cntm = 1;
-            } else if (v == mb) {  // a NaN element is not counted
-                cntm += 1;
-            }
+            max_count_add(mb, cntm, v);  // a NaN element is not counted
         }
     }
     float s = 0.0f;
@@ -878,26 +884,14 @@ __global__ void __launch_bounds__(kSThreads)
     for (int i = 0; i < NE; ++i) {
         if (slot_elem<VEC>(lane, i) < K) {
             const float v = xv[i];
-            if (mb > v) {
-            } else if (v > mb) {
-                mb = v;
-                cntm = 1;
-            } else if (v == mb) {  // a NaN element is not counted
-                cntm += 1;
-            }
+            max_count_add(mb, cntm, v);  // a NaN element is not counted
         }
     }
 #pragma unroll
     for (int mm = 32; mm >= 1; mm >>= 1) {
         const float om = __shfl_xor(mb, mm);
         const uint32_t oc = (uint32_t)__shfl_xor((int)cntm, mm);
-        if (mb > om) {
-        } else if (om > mb) {
-            mb = om;
-            cntm = oc;
-        } else {
-            cntm += oc;
-        }
+        max_count_merge(mb, cntm, om, oc);
     }
     load_row<VEC, NE>(tmp, up + base, lane, K, al);
     const float gconst = V == G_SMLM ? 0.0f + c * ug[0] : V == G_CE ? 0.0f + 1.0f * (0.0f + ug[0] * c) : 0.0f;
@@ -1155,14 +1149,7 @@ __global__ void __launch_bounds__(kSThreads)
 #pragma unroll
         for (int j = 0; j < kMNE; ++j) {
             if (j < cnt) {
-                const float v = xv[j];
-                if (a.m > v) {
-                } else if (v > a.m) {
-                    a.m = v;
-                    a.c = 1;
-                } else if (v == a.m) {  // a NaN element is not counted
-                    a.c += 1;
-                }
+                max_count_add(a.m, a.c, xv[j]);  // a NaN element is not counted
             }
         }
         return a;
