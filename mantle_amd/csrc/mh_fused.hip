@@ -196,13 +196,15 @@ __global__ void __launch_bounds__(kFThreads)
             // acquire: the other waves' partials (stored before their tickets) are visible
             // to the loads below; one cache invalidate, on the last arriver only
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            const float gb =  // in flight with the partials (a vector load, not a scalar one waited for first)
+                lane == 0 ? __hip_atomic_load(&grad_bias[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
             float s = 0.0f;
             for (int64_t i = lane; i < nper; i += 64)
                 s = s + __hip_atomic_load(&part[i * C + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
             for (int m = 32; m >= 1; m >>= 1) s = s + __shfl_xor(s, m);
             if (lane == 0) {
-                grad_bias[c] = grad_bias[c] + s;
+                grad_bias[c] = gb + s;
                 __hip_atomic_store(&tickets[c * kTicketStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
@@ -289,6 +291,10 @@ __global__ void __launch_bounds__(256)
                          int64_t Sq) {
     __shared__ float ws[4];
     const int64_t c = blockIdx.x;
+    // grad_bias[c] is loaded with the partials, not after them (a vector load: a scalar one
+    // would be waited for before the partials' loads issue)
+    const float gb =
+        threadIdx.x == 0 ? __hip_atomic_load(&grad_bias[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
     float acc = 0.0f;
     for (int64_t n = threadIdx.x; n < N; n += 256) {
         const int64_t p = n * C + c;
@@ -314,7 +320,7 @@ __global__ void __launch_bounds__(256)
     for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
     if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = acc;
     __syncthreads();
-    if (threadIdx.x == 0) grad_bias[c] = grad_bias[c] + (((ws[0] + ws[1]) + ws[2]) + ws[3]);
+    if (threadIdx.x == 0) grad_bias[c] = gb + (((ws[0] + ws[1]) + ws[2]) + ws[3]);
 }
 
 // The same sums over the slot table [C][N][kPlaneSlots] that k_bias_relu_bwd_flat<.., SLOTS>
@@ -327,6 +333,10 @@ __global__ void __launch_bounds__(256)
     static_assert(kPlaneSlots == 8, "two quads per plane");
     __shared__ float ws[4];
     const int64_t c = blockIdx.x;
+    // grad_bias[c] is loaded with the partials, not after them (a vector load: a scalar one
+    // would be waited for before the partials' loads issue)
+    const float gb =
+        threadIdx.x == 0 ? __hip_atomic_load(&grad_bias[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
     float acc = 0.0f;
     for (int64_t n = threadIdx.x; n < N; n += 256) {
         const vf4* src = reinterpret_cast<const vf4*>(part + (c * N + n) * kPlaneSlots);
@@ -343,7 +353,7 @@ __global__ void __launch_bounds__(256)
     for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
     if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = acc;
     __syncthreads();
-    if (threadIdx.x == 0) grad_bias[c] = grad_bias[c] + (((ws[0] + ws[1]) + ws[2]) + ws[3]);
+    if (threadIdx.x == 0) grad_bias[c] = gb + (((ws[0] + ws[1]) + ws[2]) + ws[3]);
 }
 
 // [N, C, S] form of x with the bias indexed by C alone, from the collapsed plan of

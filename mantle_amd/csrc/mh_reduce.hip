@@ -1874,13 +1874,15 @@ __global__ void __launch_bounds__(kRThreads)
     // acquire on the last arriver only: the partials stored before the other tickets are
     // visible to the loads below
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // grad[c] is loaded with the partials (one memory round trip for both, not two in a row)
+    const float g0 = lane == 0 ? __hip_atomic_load(&grad[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
     float s = 0.0f;
     for (int64_t i = lane; i < nper; i += 64)
         s = s + __hip_atomic_load(&part[i * C + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) s = s + __shfl_xor(s, m);
     if (lane == 0) {
-        grad[c] = NEG ? grad[c] + (-s) : grad[c] + s;
+        grad[c] = NEG ? g0 + (-s) : g0 + s;
         __hip_atomic_store(&tickets[c * kPlanesTicketStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
