@@ -1209,14 +1209,20 @@ __global__ void __launch_bounds__(kRThreads)
     constexpr int NT = 64 * WPR;
     const int64_t Bq = B >> 2;
     const float* xr = x + row * B;
-    const float kf = x[row * B];
-    const double K = (double)kf;
-    vf4 v[NQ];  // a quad past the row holds K: x - K = 0 adds nothing to either moment
+    // the row's quads load before K is needed (a quad past the row loads the last quad, then
+    // holds K: x - K = 0 adds nothing to either moment), so K's load is not waited for first
+    vf4 v[NQ];
 #pragma unroll
     for (int k = 0; k < NQ; ++k) {
         const int64_t qi = tr + (int64_t)k * NT;
-        v[k] = qi < Bq ? ld_ntv(xr, qi) : vf4{kf, kf, kf, kf};
+        v[k] = ld_ntv(xr, qi < Bq ? qi : Bq - 1);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    const float kf = xr[0];
+    const double K = (double)kf;
+#pragma unroll
+    for (int k = 0; k < NQ; ++k)
+        if (tr + (int64_t)k * NT >= Bq) v[k] = vf4{kf, kf, kf, kf};
     Mom m{0.0, 0.0};
 #pragma unroll
     for (int k = 0; k < NQ; ++k)
@@ -1249,8 +1255,6 @@ __global__ void __launch_bounds__(kRThreads)
     const int64_t start = r * B + s * L;
     const int64_t rem = B - s * L;
     const int64_t len = rem < L ? rem : L;
-    const float kf = x[r * B];
-    const double K = (double)kf;
     Mom m{0.0, 0.0};
     if (VEC) {
         // four quads in flight; element j of every quad goes to accumulator chain j, and the
@@ -1258,12 +1262,25 @@ __global__ void __launch_bounds__(kRThreads)
         // 16384-element chunk: all-element tstd over 2^26 elements took 49.9 us)
         const int64_t nq = len >> 2;
         const float* xs = x + start;
+        // K (the row's first element) as a vector load, which the first quads' loads follow
+        // without waiting for it: a scalar load here was waited for before any of them issued
+        const float kf = __hip_atomic_load(x + r * B, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         Mom mc[4] = {Mom{0.0, 0.0}, Mom{0.0, 0.0}, Mom{0.0, 0.0}, Mom{0.0, 0.0}};
         for (int64_t q = t; q < nq; q += 4 * kRThreads) {
+            // a quad past the chunk loads the chunk's last quad, then holds K: x - K = 0 adds
+            // nothing to either moment
             vf4 v[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u)  // a quad past the chunk holds K: x - K = 0 adds nothing
-                v[u] = q + u * kRThreads < nq ? ld_ntv(xs, q + u * kRThreads) : vf4{kf, kf, kf, kf};
+            for (int u = 0; u < 4; ++u) {
+                const int64_t qi = q + u * kRThreads;
+                v[u] = ld_ntv(xs, qi < nq ? qi : nq - 1);
+            }
+            float kq = kf;
+            asm volatile("" : "+v"(kq) : : "memory");  // K's wait and conversion after the loads above
+            const double K = (double)kq;
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (q + u * kRThreads >= nq) v[u] = vf4{kq, kq, kq, kq};
 #pragma unroll
             for (int u = 0; u < 4; ++u)
 #pragma unroll
@@ -1276,6 +1293,7 @@ __global__ void __launch_bounds__(kRThreads)
             m.s2 = m.s2 + mc[j].s2;
         }
     } else {
+        const double K = (double)x[r * B];
         for (int64_t j = t; j < len; j += kRThreads) mom_add(m, ld_nt(x + start + j), K);
     }
     m = mom_wave(m);
@@ -1293,19 +1311,20 @@ __global__ void __launch_bounds__(kRThreads)
 }
 
 // Strided axis over [A, B, C]: thread = a quad (VEC) or one element of the [A, C] output,
-// rows [s * rps, min((s + 1) * rps, B)) of split s = blockIdx.y in order, 4 rows in flight;
-// K is the line's element at row 0. S == 1 writes the result, S > 1 partials at
-// s * (A * C) + o.
-template <bool VEC>
+// rows [s * rps, min((s + 1) * rps, B)) of split s in order; K is the line's element at row
+// 0. S == 1 writes the result, S > 1 partials at s * (A * C) + o. SPLIT_X puts the splits on
+// grid x (the column blocks on y), so the round-robin dispatch spreads each column block's
+// splits over the eight XCDs instead of giving each XCD one column block of every row.
+template <bool VEC, bool SPLIT_X>
 __global__ void __launch_bounds__(kRThreads)
     k_tstd_mom_cols(float* __restrict__ res, const float* __restrict__ x, int64_t A, int64_t B, int64_t C,
                     int64_t rps, int64_t S, Mom* __restrict__ part) {
     constexpr int W = VEC ? 4 : 1;
     const int64_t AC = A * C;
-    const int64_t o = ((int64_t)blockIdx.x * kRThreads + threadIdx.x) * W;
+    const int64_t o = ((int64_t)(SPLIT_X ? blockIdx.y : blockIdx.x) * kRThreads + threadIdx.x) * W;
     if (o >= AC) return;
     const int64_t a = o / C, c = o - a * C;
-    const int64_t s = blockIdx.y;
+    const int64_t s = SPLIT_X ? blockIdx.x : blockIdx.y;
     const int64_t b0 = s * rps;
     const int64_t b1 = b0 + rps < B ? b0 + rps : B;
     const int64_t base = a * B * C + c;
@@ -1318,31 +1337,54 @@ __global__ void __launch_bounds__(kRThreads)
             v[0] = ld_nt(x + base + b * C);
         }
     };
-    double K[W];
-    {
-        float v0[W];
-        load(0, v0);
-#pragma unroll
-        for (int j = 0; j < W; ++j) K[j] = (double)v0[j];
-    }
-    // eight rows in flight; row u of each eight goes to accumulator chain u % 4 (the rest of the
-    // split to chain 0), and the chains are added in order at the end
+    // eight rows in flight, the next eight loaded before the current eight are added (about
+    // one wave per SIMD runs this kernel, so no other wave's loads cover its fp64 work); row u
+    // of each eight goes to accumulator chain u % 4 (the rest of the split to chain 0), and the
+    // chains are added in order at the end. K (the line's row 0) loads with the first eight
+    // rows (rows past the split reload its last row), not before them.
     constexpr int RU = 8, CH = 4;
     Mom m[CH][W];
 #pragma unroll
     for (int h = 0; h < CH; ++h)
 #pragma unroll
         for (int j = 0; j < W; ++j) m[h][j] = Mom{0.0, 0.0};
-    int64_t b = b0;
-    for (; b + RU - 1 < b1; b += RU) {
-        float v[RU][W];
+    float k0[W], v[RU][W];
+    load(0, k0);
 #pragma unroll
-        for (int u = 0; u < RU; ++u) load(b + u, v[u]);
+    for (int u = 0; u < RU; ++u) load(b0 + u < b1 ? b0 + u : b1 - 1, v[u]);
+    double K[W];
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+        asm volatile("" : "+v"(k0[j]) : : "memory");  // K's wait and conversion after the loads above
+        K[j] = (double)k0[j];
+    }
+#pragma unroll
+    for (int u = 0; u < RU; ++u)  // rows past a short split hold K: x - K = 0 adds nothing
+        if (b0 + u >= b1)
+#pragma unroll
+            for (int j = 0; j < W; ++j) v[u][j] = k0[j];
+    auto add_rows = [&](const float (&r)[RU][W]) {
 #pragma unroll
         for (int u = 0; u < RU; ++u)
 #pragma unroll
-            for (int j = 0; j < W; ++j) mom_add(m[u % CH][j], v[u][j], K[j]);
+            for (int j = 0; j < W; ++j) mom_add(m[u % CH][j], r[u][j], K[j]);
+    };
+    // every pass of the loop issues its loads unconditionally, so the waits before the adds
+    // cover the older eight rows only
+    int64_t b = b0;
+    for (; b + 2 * RU - 1 < b1; b += RU) {
+        float w[RU][W];
+#pragma unroll
+        for (int u = 0; u < RU; ++u) load(b + RU + u, w[u]);
+        __builtin_amdgcn_sched_barrier(0);  // the next rows' loads stay ahead of the adds
+        add_rows(v);
+#pragma unroll
+        for (int u = 0; u < RU; ++u)
+#pragma unroll
+            for (int j = 0; j < W; ++j) v[u][j] = w[u][j];
     }
+    add_rows(v);
+    b += RU;
     for (; b < b1; ++b) {
         float v[W];
         load(b, v);
@@ -2305,7 +2347,9 @@ int mh_tstd(float* res, const float* x, const mh_shape* psx, int32_t axis) {
     // rows, eight rows in flight over four accumulator chains. Fewer, longer splits write and
     // combine fewer fp64 partials: at [8192, 8192] axis 0 (a probe, moments + combine) 32 splits
     // took 48.1 us against 52.6 us with 64 splits of four rows in flight, one chain; 128 and
-    // 256 splits took 57-60 us.
+    // 256 splits took 57-60 us. In the bench (moments + combine, streamed) the splits on grid x
+    // took 47.2 us against 48.9 us on y; 16 rows in flight 49.4 us, two blocks per CU 59.4 us.
+    // With S > 1 there are fewer column blocks than CUs, well inside grid y's limit.
     const bool vec = al16(x) && C % 4 == 0;
     const int64_t W = vec ? 4 : 1;
     const int64_t items = A * C / W;
@@ -2320,9 +2364,16 @@ int mh_tstd(float* res, const float* x, const mh_shape* psx, int32_t axis) {
     S = (B + rps - 1) / rps;
     Mom* part = nullptr;
     if (S > 1) MH_TRY(scratch((size_t)(S * A * C) * sizeof(Mom), reinterpret_cast<void**>(&part)));
-    dim3 g((unsigned)bx, (unsigned)S), b(kRThreads);
-    if (vec) hipLaunchKernelGGL(k_tstd_mom_cols<true>, g, b, 0, st, res, x, A, B, C, rps, S, part);
-    else hipLaunchKernelGGL(k_tstd_mom_cols<false>, g, b, 0, st, res, x, A, B, C, rps, S, part);
+    const dim3 b(kRThreads);
+    if (S > 1) {
+        const dim3 g((unsigned)S, (unsigned)bx);
+        if (vec) hipLaunchKernelGGL((k_tstd_mom_cols<true, true>), g, b, 0, st, res, x, A, B, C, rps, S, part);
+        else hipLaunchKernelGGL((k_tstd_mom_cols<false, true>), g, b, 0, st, res, x, A, B, C, rps, S, part);
+    } else {
+        const dim3 g((unsigned)bx);
+        if (vec) hipLaunchKernelGGL((k_tstd_mom_cols<true, false>), g, b, 0, st, res, x, A, B, C, rps, S, part);
+        else hipLaunchKernelGGL((k_tstd_mom_cols<false, false>), g, b, 0, st, res, x, A, B, C, rps, S, part);
+    }
     if (S > 1)
         hipLaunchKernelGGL(k_tstd_mom_combine_cols, dim3((unsigned)((A * C + 15) / 16)), b, 0, st,
                            res, part, A * C, S, B);

@@ -1590,7 +1590,10 @@ TSTD_CASES = [((87, 73, 107), 0), ((87, 73, 107), 1), ((87, 73, 107), 2), ((87, 
               ((3, 4, 5), 1), ((1,), None), ((5,), 0), ((2, 70000), 1), ((70000, 3), 0), ((1 << 22,), None),
               ((1000, 20), 1), ((513, 32), 1), ((40, 33), 1), ((3, 4100), 1), ((300, 256), 0),
               ((33, 512, 128), 1), ((9000, 64), 0), ((5, 1, 7), 1), ((7, 4), 1), ((9, 8), 1), ((6, 4096), 1),
-              ((5, 16384), 1), ((3, 12000), 1), ((2, 3, 16388), 2)]
+              ((5, 16384), 1), ((3, 12000), 1), ((2, 3, 16388), 2),
+              # strided splits of 65 rows whose last split is shorter than one group of eight
+              # rows (5 / 10 rows), column quads and single columns
+              ((16385, 4), 0), ((16385, 3), 0), ((16390, 8), 0)]
 
 
 @pytest.mark.parametrize("shape,axis", TSTD_CASES, ids=[f"{s}-ax{a}" for s, a in TSTD_CASES])
@@ -1605,7 +1608,7 @@ def test_tstd_parity(gpu, shape, axis):
 
 
 TSTD_OFFSET_CASES = [((1000, 256), 0), ((1000, 256), 1), ((1000, 256), None), ((37, 63, 107), 1),
-                     ((3, 40000), 1), ((2, 3, 20002), 2)]
+                     ((3, 40000), 1), ((2, 3, 20002), 2), ((16385, 4), 0)]
 
 
 @pytest.mark.parametrize("shape,axis", TSTD_OFFSET_CASES, ids=[f"{s}-ax{a}" for s, a in TSTD_OFFSET_CASES])
