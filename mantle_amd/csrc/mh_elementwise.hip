@@ -215,19 +215,24 @@ struct FFmaRg {  // FMA.backward, basics.mojo:804-817: id 0 ug * t2, id 1 ug * t
 template <class F, int NIN, bool ACCUM>
 __global__ void __launch_bounds__(kThreads)
     k_same4(float* __restrict__ out, InPtrs<NIN> in, int smask, int64_t n, DevScal ds, F f) {
-    f.setup(ds);
-    float sv[NIN > 0 ? NIN : 1];
-#pragma unroll
-    for (int k = 0; k < NIN; ++k) sv[k] = ((smask >> k) & 1) ? in.p[k][0] : 0.0f;
     const int64_t nq = n >> 2;
     const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    float4 iv[NIN > 0 ? NIN : 1];
+    float4 ov;
     if (q < nq) {
-        float4 iv[NIN > 0 ? NIN : 1];
-        float4 ov;
 #pragma unroll
         for (int k = 0; k < NIN; ++k)
             if (!((smask >> k) & 1)) iv[k] = ld_nt4(in.p[k], q);
         if (ACCUM) ov = ld_nt4(out, q);
+    }
+    // device scalars (the functor's, scalar operands) after the quads' loads: read first, the
+    // wave waited for them before its quads' loads went out
+    __builtin_amdgcn_sched_barrier(0);
+    f.setup(ds);
+    float sv[NIN > 0 ? NIN : 1];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) sv[k] = ((smask >> k) & 1) ? in.p[k][0] : 0.0f;
+    if (q < nq) {
         float r[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {

@@ -2151,42 +2151,57 @@ int unbroadcast_binrg(int op, int id, bool divs, float* grad, const mh_shape& sg
 constexpr int kPowThreads = 64;
 constexpr int kPowQuads = 2;
 constexpr int64_t kPowStreamMinQuads = 1 << 16;
-template <bool FRAC, bool GX>
-__device__ __forceinline__ void pow_block_quads(const LdPowGrad& ld, int64_t nq, float (&acc)[4]) {
-    const int64_t base = (int64_t)blockIdx.x * (kPowThreads * kPowQuads) + threadIdx.x;
-    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+struct PowQuads {
     float4 xs[kPowQuads], us[kPowQuads], gs[kPowQuads];
+};
+
+// every quad's loads (a quad past the end reloads the last quad, unused)
+template <bool GX>
+__device__ __forceinline__ void pow_load_quads(const LdPowGrad& ld, int64_t nq, PowQuads& t) {
+    const int64_t base = (int64_t)blockIdx.x * (kPowThreads * kPowQuads) + threadIdx.x;
 #pragma unroll
     for (int k = 0; k < kPowQuads; ++k) {
         const int64_t q = base + k * kPowThreads;
-        const int64_t qc = q < nq ? q : nq - 1;  // past the end: the last quad again (unused)
-        xs[k] = ld_nt4(ld.x, qc);
-        us[k] = ld_nt4(ld.ug, qc);
-        gs[k] = GX ? ld_nt4(ld.gx, qc) : zero;
+        const int64_t qc = q < nq ? q : nq - 1;
+        t.xs[k] = ld_nt4(ld.x, qc);
+        t.us[k] = ld_nt4(ld.ug, qc);
+        t.gs[k] = GX ? ld_nt4(ld.gx, qc) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+}
+
+template <bool FRAC, bool GX>
+__device__ __forceinline__ void pow_block_quads(const LdPowGrad& ld, int64_t nq, PowQuads& t, float (&acc)[4]) {
+    const int64_t base = (int64_t)blockIdx.x * (kPowThreads * kPowQuads) + threadIdx.x;
 #pragma unroll
     for (int k = 0; k < kPowQuads; ++k) {
         const int64_t q = base + k * kPowThreads;
         if (q < nq) {
-            acc[0] = acc[0] + ld.elem<FRAC, GX>(xs[k].x, us[k].x, gs[k].x);
-            acc[1] = acc[1] + ld.elem<FRAC, GX>(xs[k].y, us[k].y, gs[k].y);
-            acc[2] = acc[2] + ld.elem<FRAC, GX>(xs[k].z, us[k].z, gs[k].z);
-            acc[3] = acc[3] + ld.elem<FRAC, GX>(xs[k].w, us[k].w, gs[k].w);
-            if constexpr (GX) st_nt4(ld.gx, q, gs[k]);
+            acc[0] = acc[0] + ld.elem<FRAC, GX>(t.xs[k].x, t.us[k].x, t.gs[k].x);
+            acc[1] = acc[1] + ld.elem<FRAC, GX>(t.xs[k].y, t.us[k].y, t.gs[k].y);
+            acc[2] = acc[2] + ld.elem<FRAC, GX>(t.xs[k].z, t.us[k].z, t.gs[k].z);
+            acc[3] = acc[3] + ld.elem<FRAC, GX>(t.xs[k].w, t.us[k].w, t.gs[k].w);
+            if constexpr (GX) st_nt4(ld.gx, q, t.gs[k]);
         }
     }
 }
 
+// The quads' loads go out before the exponent is read (setup): read first, every wave waited
+// for that scalar load before its quads' loads issued.
 __global__ void __launch_bounds__(kPowThreads) k_pow_grad_quads(LdPowGrad ld, int64_t nq, float* part) {
-    ld.setup();
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    PowQuads t;
     if (ld.gx) {
-        if (ld.frac) pow_block_quads<true, true>(ld, nq, acc);
-        else pow_block_quads<false, true>(ld, nq, acc);
-    } else if (ld.frac) {
-        pow_block_quads<true, false>(ld, nq, acc);
+        pow_load_quads<true>(ld, nq, t);
+        __builtin_amdgcn_sched_barrier(0);
+        ld.setup();
+        if (ld.frac) pow_block_quads<true, true>(ld, nq, t, acc);
+        else pow_block_quads<false, true>(ld, nq, t, acc);
     } else {
-        pow_block_quads<false, false>(ld, nq, acc);
+        pow_load_quads<false>(ld, nq, t);
+        __builtin_amdgcn_sched_barrier(0);
+        ld.setup();
+        if (ld.frac) pow_block_quads<true, false>(ld, nq, t, acc);
+        else pow_block_quads<false, false>(ld, nq, t, acc);
     }
     const float a = wave_reduce<RSum>((acc[0] + acc[1]) + (acc[2] + acc[3]));
     if (threadIdx.x == 0) part[blockIdx.x] = a;
