@@ -656,8 +656,6 @@ __global__ void __launch_bounds__(kORows)
     const int nr = (int)((rows - r0) < kORows ? (rows - r0) : kORows);
     const int cnt = nr * K, nq = cnt >> 2;
     const int64_t base = r0 * K;  // a multiple of 64: 16-byte aligned
-    const float gconst = V == G_SMLM ? 0.0f + c * ug[0] : V == G_CE ? 0.0f + 1.0f * (0.0f + ug[0] * c) : 0.0f;
-    const bool skip_ok = gconst - gconst == 0.0f;  // g_t finite (the head graph's zero-target shortcut)
     vf4 qx[QPT], qu[QPT], qg[QPT];
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
@@ -674,6 +672,12 @@ __global__ void __launch_bounds__(kORows)
         tu = ld_nt(up + base + tl);
         tg = ld_nt(g + base + tl);
     }
+    // the loss's upstream gradient as a vector load behind the tiles' loads: as a scalar load
+    // at its first use it cost every block a memory round trip after its barrier
+    float u0 = 0.0f;
+    if constexpr (V == G_SMLM || V == G_CE) u0 = __hip_atomic_load(ug, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float gconst = V == G_SMLM ? 0.0f + c * u0 : V == G_CE ? 0.0f + 1.0f * (0.0f + u0 * c) : 0.0f;
+    const bool skip_ok = gconst - gconst == 0.0f;  // g_t finite (the head graph's zero-target shortcut)
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
         if (t + kORows * u < nq) {
