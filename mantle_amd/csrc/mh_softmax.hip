@@ -995,34 +995,65 @@ __device__ __forceinline__ float shifted(const float* w, int j, int s) {
     return s == 0 ? w[j] : s == 1 ? w[j + 1] : s == 2 ? w[j + 2] : w[j + 3];
 }
 
+// A chunk's loads in two steps, so that a kernel issues every tensor's quad loads before it
+// waits for any: chunk_issue loads every quad unconditionally (a quad the chunk does not need
+// loads one that is sure to exist: the chunk's first, or the tensor's last whole quad; n >= 17
+// here), chunk_finish keeps the needed ones by selects and, for a chunk that reaches the
+// tensor's last, partial quad, loads its elements one by one. Loads under per-quad branches
+// made the compiler copy the registers at each join, and each copy waited for the loads
+// before it: one memory round trip per quad.
+struct ChunkQuads {
+    vf4 t[kMNE / 4 + 1];
+};
+
 template <bool VEC>
-__device__ __forceinline__ void load_chunk(float (&v)[kMNE], const float* __restrict__ base, int64_t off, int cnt,
-                                           int64_t n) {
-    if constexpr (VEC) {  // off and cnt multiples of 4
-        const float* p = base + off;
+__device__ __forceinline__ void chunk_issue(ChunkQuads& c, const float* __restrict__ base, int64_t off, int cnt,
+                                            int64_t n) {
+    if constexpr (VEC) {  // off and cnt multiples of 4; a lane with no chunk has off = 0
+        const vf4* p = reinterpret_cast<const vf4*>(base + off);
 #pragma unroll
-        for (int q = 0; q < kMNE / 4; ++q) {
-            if (4 * q < cnt) {
-                const vf4 t = reinterpret_cast<const vf4*>(p)[q];
-                v[4 * q] = t[0]; v[4 * q + 1] = t[1]; v[4 * q + 2] = t[2]; v[4 * q + 3] = t[3];
-            } else {
-                v[4 * q] = v[4 * q + 1] = v[4 * q + 2] = v[4 * q + 3] = 0.0f;
-            }
+        for (int q = 0; q < kMNE / 4; ++q) c.t[q] = p[4 * q < cnt ? q : 0];
+    } else {
+        const int64_t a0 = off & ~(int64_t)3;
+        const int64_t last = off + cnt;       // one past the chunk
+        const int64_t nq4 = n & ~(int64_t)3;  // the tensor's elements in whole quads
+#pragma unroll
+        for (int q = 0; q < kMNE / 4 + 1; ++q) {
+            const int64_t e = a0 + 4 * q;
+            c.t[q] = *reinterpret_cast<const vf4*>(base + (e < last && e < nq4 ? e : nq4 - 4));
         }
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void chunk_finish(float (&v)[kMNE], const ChunkQuads& c, const float* __restrict__ base,
+                                             int64_t off, int cnt, int64_t n) {
+    if constexpr (VEC) {
+#pragma unroll
+        for (int q = 0; q < kMNE / 4; ++q)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[4 * q + i] = 4 * q < cnt ? c.t[q][i] : 0.0f;
     } else {
         const int64_t a0 = off & ~(int64_t)3;
         const int s = (int)(off - a0);
-        const int64_t last = off + cnt;  // one past the chunk
+        const int64_t last = off + cnt;
+        const int64_t nq4 = n & ~(int64_t)3;
         float w[kMNE + 4];
 #pragma unroll
         for (int q = 0; q < kMNE / 4 + 1; ++q) {
             const int64_t e = a0 + 4 * q;
-            if (e < last && e + 3 < n) {
-                const vf4 t = *reinterpret_cast<const vf4*>(base + e);
-                w[4 * q] = t[0]; w[4 * q + 1] = t[1]; w[4 * q + 2] = t[2]; w[4 * q + 3] = t[3];
-            } else {
+            const bool in = e < last && e < nq4;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) w[4 * q + i] = e < last && e + i < n ? base[e + i] : 0.0f;
+            for (int i = 0; i < 4; ++i) w[4 * q + i] = in ? c.t[q][i] : 0.0f;
+        }
+        if (last > nq4) {  // the tensor's last, partial quad
+#pragma unroll
+            for (int q = 0; q < kMNE / 4 + 1; ++q) {
+                const int64_t e = a0 + 4 * q;
+                if (e == nq4)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (e + i < n) w[4 * q + i] = base[e + i];
             }
         }
 #pragma unroll
@@ -1089,8 +1120,12 @@ __global__ void __launch_bounds__(kSThreads)
     float xv[kMNE], tv[kMNE], e[kMNE];
     const int cnt = L.live ? L.cnt : 0;
     const int64_t n = rows * (int64_t)K;
-    load_chunk<VEC>(xv, x, L.live ? off : 0, cnt, n);
-    if constexpr (LOSS) load_chunk<VEC>(tv, tg, L.live ? off : 0, cnt, n);
+    const int64_t o = L.live ? off : 0;
+    ChunkQuads cx, ct;
+    chunk_issue<VEC>(cx, x, o, cnt, n);
+    if constexpr (LOSS) chunk_issue<VEC>(ct, tg, o, cnt, n);
+    chunk_finish<VEC>(xv, cx, x, o, cnt, n);
+    if constexpr (LOSS) chunk_finish<VEC>(tv, ct, tg, o, cnt, n);
     // MAX.forward: max_simd from min_finite, element order
     const float m = row_chain<P>(L, -FLT_MAX, [&](float a) {
 #pragma unroll
@@ -1138,9 +1173,14 @@ __global__ void __launch_bounds__(kSThreads)
     const int cnt = L.live ? L.cnt : 0;
     float xv[kMNE], uv[kMNE], gv[kMNE], e[kMNE];
     const int64_t n = rows * (int64_t)K;
-    load_chunk<VEC>(xv, x, L.live ? off : 0, cnt, n);
-    load_chunk<VEC>(uv, up, L.live ? off : 0, cnt, n);
-    load_chunk<VEC>(gv, g, L.live ? off : 0, cnt, n);
+    const int64_t o = L.live ? off : 0;
+    ChunkQuads cx, cu, cg;
+    chunk_issue<VEC>(cx, x, o, cnt, n);
+    chunk_issue<VEC>(cu, up, o, cnt, n);
+    chunk_issue<VEC>(cg, g, o, cnt, n);
+    chunk_finish<VEC>(xv, cx, x, o, cnt, n);
+    chunk_finish<VEC>(uv, cu, up, o, cnt, n);
+    chunk_finish<VEC>(gv, cg, g, o, cnt, n);
     // the forward row max (MAX.forward) and, as MAX.backward recomputes it, the max with its
     // count (an element neither above nor below the running max adds to the count)
     const float m = row_chain<P>(L, -FLT_MAX, [&](float a) {
@@ -1316,11 +1356,11 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
             return MH_OK;
         }
     }
-    // multi-lane engine, aligned operands, over 8M elements: rows of whole 16-byte quads for
-    // 17-64 classes (Softmax 30-32 us against 25-52 us in the thread engine, CrossEntropy faster
-    // at every such count) and loss rows of more than 24 classes (shifted quad loads: 37-41 us
-    // against 46-49 us). Softmax rows that are not whole quads (shifted loads: 39-44 us) and
-    // losses of 17-24 classes stay on the thread engine (25-32 us).
+    // multi-lane engine, aligned operands: rows of whole 16-byte quads for 17-64 classes and
+    // loss rows of more than 24 classes. Streamed over 8M elements, Softmax rows that are not
+    // whole quads run 15-19 us in the thread engine (32 us at 63 classes) against 30-31 us
+    // here, and losses of 17-23 classes 22-28 us there against 23-28 us here, so those stay on
+    // the thread engine.
     if (K > 16 && K <= 4 * kMNE && al && (K % 4 == 0 || (LOSS && K > 24))) {
         const int P = (K + kMNE - 1) / kMNE;
         const int64_t rpb = (int64_t)(kSThreads / 64) * (64 / P);
@@ -1394,10 +1434,10 @@ static int launch_bwd(float* gx, const float* x, const float* up, const float* u
         }
         return MH_OK;
     }
-    // multi-lane engine, aligned operands: rows of whole quads (over 8M elements 41-51 us for
-    // 20-64 classes, against 62-149 us in the thread engine) and other rows of more than 24
-    // classes (shifted quad loads: 61-76 us against 69-149); at 17 classes the thread engine
-    // is faster (53 against 90 us)
+    // multi-lane engine, aligned operands: rows of whole quads and other rows of more than 24
+    // classes. Streamed over 8M elements, rows of 17-23 classes that are not whole quads run
+    // 41-56 us in the thread engine against 47-63 us here (about equal at 21), so they stay
+    // there.
     if (K > 16 && K <= 4 * kMNE && al && (K % 4 == 0 || K > 24)) {
         const int P = (K + kMNE - 1) / kMNE;
         const int64_t rpb = (int64_t)(kSThreads / 64) * (64 / P);
