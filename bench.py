@@ -1159,7 +1159,7 @@ WL_KERNELS = [
      "one pass; stores only quads holding a line maximum"),
     ("c5 SUB.fwd [N,10] - [N,1]", "void mh::k_rowbc4<mh::FBin<1>, 2, false>", 2621440, 8 * _N5 + 4 * (_N5 // 10), ""),
     ("c5 DIV.bwd0", "void mh::k_rowbc4<mh::FBinRg<3, 0, false>, 2, true>", 2621440, 12 * _N5 + 4 * (_N5 // 10), ""),
-    ("c5 DIV.bwd1 (un-broadcast into [N,1])", "void mh::k_rows_binrg<3, 1, false, 16>", 1048576,
+    ("c5 DIV.bwd1 (un-broadcast into [N,1])", "void mh::k_rows_binrg<3, 1, false, 16, true>", 1048576,
      8 * _N5 + 12 * (_N5 // 10), "the rg terms computed in the loader, added into the gradient in row order"),
     ("c5 MAX.bwd (rows of 10)", "void mh::k_max_bwd_rows<16>", 1048576, 12 * _N5 + 8 * (_N5 // 10),
      "stores only quads holding a row maximum (most quads, at 10 classes)"),
@@ -1182,7 +1182,7 @@ WL_STATS = [("c3", "op_by_op", "ADD.bwd_bias", "void mh::k_unb_planes<false>"),
             ("c5", "fused", "fused.bwd", "void mh::k_rowo_bwd<0, 10>"),
             ("c5", "fwd", "SUB.fwd", "void mh::k_rowbc4<mh::FBin<1>, 2, false>"),
             ("c5", "fwd", "DIV.fwd", "void mh::k_rowbc4<mh::FBin<3>, 2, false>"),
-            ("c5", "bwd", "DIV.bwd1", "void mh::k_rows_binrg<3, 1, false, 16>")]
+            ("c5", "bwd", "DIV.bwd1", "void mh::k_rows_binrg<3, 1, false, 16, true>")]
 
 
 def stats_summary(stats_csv, command, bench_json=None):

@@ -278,8 +278,11 @@ struct LdPowGrad {
 // a scalar t2). `a` is the full-shape operand; `t2` of DIV's operand 1 has the grad's shape
 // and is read at the element's output line (i / (B*C)) * C + i % C. get4 takes a quad in
 // one row (C == 1) or over four consecutive lines (C % 4 == 0), with 16-byte loads when
-// `al`, else four scalar loads, so the reduction runs in the same order either way.
-template <int OP, int ID, bool DIVS, bool BIG>
+// `al`, else four scalar loads, so the reduction runs in the same order either way. COL1
+// (DIV's operand 1 only): C == 1, known when the kernel is compiled, so the divisor's load has
+// one form (under a branch between the two, the compiler waited at the join for every load
+// issued before it, and a thread's rows in flight went out one after another).
+template <int OP, int ID, bool DIVS, bool BIG, bool COL1 = false>
 struct LdBinRg {
     const float* ug;
     const float* a;
@@ -325,7 +328,7 @@ struct LdBinRg {
         float4 d = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if constexpr (OP == MH_DIV && ID == 1 && !DIVS) {
             const int64_t l = line(i);
-            if (C == 1) d = make_float4(t2[l], t2[l], t2[l], t2[l]);
+            if constexpr (COL1) d = make_float4(t2[l], t2[l], t2[l], t2[l]);
             else d = make_float4(t2[l], t2[l + 1], t2[l + 2], t2[l + 3]);
         }
         o[0] = term(u.x, v.x, d.x);
@@ -2020,9 +2023,9 @@ int unbroadcast_accum_scratch(float* grad, const mh_shape& sgrad, const float* r
 // gradient (EPI_SEQ_ACCUM), with DIV's divisor read once per row: the terms and order of the
 // generic loader path (k_rows_lds_ld over LdBinRg), so the same bits, without a row lookup
 // per element. ug and the operand 16-byte aligned.
-template <int OP, int ID, bool DIVS, int BMAX>
+template <int OP, int ID, bool DIVS, int BMAX, bool COL1>
 __global__ void __launch_bounds__(kLdsRows)
-    k_rows_binrg(LdBinRg<OP, ID, DIVS, false> ld, float* __restrict__ grad, int64_t nrows, int B) {
+    k_rows_binrg(LdBinRg<OP, ID, DIVS, false, COL1> ld, float* __restrict__ grad, int64_t nrows, int B) {
     constexpr int QPT = BMAX / 4;  // quads per thread per operand: rows * B / 4 <= kLdsRows * QPT
     __shared__ float4 us4[kLdsRows * BMAX / 4], as4[kLdsRows * BMAX / 4];
     float* us = reinterpret_cast<float*>(us4);
@@ -2068,10 +2071,11 @@ __global__ void __launch_bounds__(kLdsRows)
     }
 }
 
-template <int OP, int ID, bool DIVS, bool BIG>
+template <int OP, int ID, bool DIVS, bool BIG, bool COL1>
 static int binrg_reduce(float* grad, const float* ug, const float* a, const float* t2, int64_t A, int64_t B,
                         int64_t C, bool al, float* tmp) {
-    LdBinRg<OP, ID, DIVS, BIG> ld{};
+    constexpr bool DV = OP == MH_DIV && ID == 1 && !DIVS;
+    LdBinRg<OP, ID, DIVS, BIG, COL1> ld{};
     ld.ug = ug;
     ld.a = a;
     ld.t2 = t2;
@@ -2082,28 +2086,39 @@ static int binrg_reduce(float* grad, const float* ug, const float* a, const floa
         ld.fc = make_fastdiv((uint32_t)C);
     }
     ld.al = al;
-    if constexpr (!BIG) {
+    if constexpr (!BIG && (COL1 || !DV)) {
         if (C == 1 && B <= 32 && al && A < kMaxGridRows) {  // short rows, staged as quads
             const unsigned blocks = (unsigned)((A + kLdsRows - 1) / kLdsRows);
             if (B <= 16)
-                hipLaunchKernelGGL((k_rows_binrg<OP, ID, DIVS, 16>), dim3(blocks), dim3(kLdsRows), 0, ctx().stream,
-                                   ld, grad, A, (int)B);
+                hipLaunchKernelGGL((k_rows_binrg<OP, ID, DIVS, 16, COL1>), dim3(blocks), dim3(kLdsRows), 0,
+                                   ctx().stream, ld, grad, A, (int)B);
             else
-                hipLaunchKernelGGL((k_rows_binrg<OP, ID, DIVS, 32>), dim3(blocks), dim3(kLdsRows), 0, ctx().stream,
-                                   ld, grad, A, (int)B);
+                hipLaunchKernelGGL((k_rows_binrg<OP, ID, DIVS, 32, COL1>), dim3(blocks), dim3(kLdsRows), 0,
+                                   ctx().stream, ld, grad, A, (int)B);
             return MH_OK;
         }
     }
     // vec_ok: the loader reads quads at any alignment, so the kernels (and the summation
     // order) are those of a materialised, aligned rg
-    return reduce_t<RSum, LdBinRg<OP, ID, DIVS, BIG>>(ld, true, EPI_SEQ_ACCUM, A, B, C, grad, nullptr, 0.0f, tmp);
+    return reduce_t<RSum, LdBinRg<OP, ID, DIVS, BIG, COL1>>(ld, true, EPI_SEQ_ACCUM, A, B, C, grad, nullptr, 0.0f,
+                                                            tmp);
+}
+
+// COL1 only for DIV's operand 1, whose loader reads the divisor (C == 1: one per row)
+template <int OP, int ID, bool DIVS, bool BIG>
+static int binrg_reduce_c(float* grad, const float* ug, const float* a, const float* t2, int64_t A, int64_t B,
+                          int64_t C, bool al, float* tmp) {
+    if constexpr (OP == MH_DIV && ID == 1 && !DIVS) {
+        if (C == 1) return binrg_reduce<OP, ID, DIVS, BIG, true>(grad, ug, a, t2, A, B, C, al, tmp);
+    }
+    return binrg_reduce<OP, ID, DIVS, BIG, false>(grad, ug, a, t2, A, B, C, al, tmp);
 }
 
 template <int OP, int ID, bool DIVS>
 static int binrg_reduce_n(float* grad, const float* ug, const float* a, const float* t2, int64_t A, int64_t B,
                           int64_t C, bool al, float* tmp) {
-    if (A * B * C < ((int64_t)1 << 32)) return binrg_reduce<OP, ID, DIVS, false>(grad, ug, a, t2, A, B, C, al, tmp);
-    return binrg_reduce<OP, ID, DIVS, true>(grad, ug, a, t2, A, B, C, al, tmp);
+    if (A * B * C < ((int64_t)1 << 32)) return binrg_reduce_c<OP, ID, DIVS, false>(grad, ug, a, t2, A, B, C, al, tmp);
+    return binrg_reduce_c<OP, ID, DIVS, true>(grad, ug, a, t2, A, B, C, al, tmp);
 }
 
 int unbroadcast_binrg(int op, int id, bool divs, float* grad, const mh_shape& sgrad, const float* ug,
