@@ -478,6 +478,16 @@ __global__ void __launch_bounds__(kSThreads)
 // reads its 84 MB in 15.3 us, against 16.7 us for a persistent grid of 256-thread blocks that
 // prefetched each next 256-row tile into registers while computing the current one.
 constexpr int kORows = 64;
+
+// A tile quad's index for the one-shot kernels' loads. With K >= 4 every block holds at least
+// one whole quad (nq >= 1), so a quad past the tile reloads the tile's last one and the loads
+// need no branch (under a branch the compiler zeroed every tile register first: about three
+// VALU instructions per element); smaller K keeps the guarded load.
+template <int K>
+__device__ __forceinline__ int tile_quad(int q, int nq) {
+    if constexpr (K >= 4) return q < nq ? q : nq - 1;
+    return q;
+}
 constexpr int64_t kOMaxBlocks = max_grid_blocks(kORows);  // blocks of one launch
 
 template <int V, int K>
@@ -496,9 +506,10 @@ __global__ void __launch_bounds__(kORows)
     vf4 qx[QPT], qt[QPT];
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
-        if (t + kORows * u < nq) {
-            qx[u] = ld_ntv(x + base, t + kORows * u);
-            qt[u] = ld_ntv(tg + base, t + kORows * u);
+        const int qi = tile_quad<K>(t + kORows * u, nq);
+        if (K >= 4 || t + kORows * u < nq) {
+            qx[u] = ld_ntv(x + base, qi);
+            qt[u] = ld_ntv(tg + base, qi);
         }
     }
     const int tl = (nq << 2) + t;
@@ -659,10 +670,11 @@ __global__ void __launch_bounds__(kORows)
     vf4 qx[QPT], qu[QPT], qg[QPT];
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
-        if (t + kORows * u < nq) {
-            qx[u] = ld_ntv(x + base, t + kORows * u);
-            qu[u] = ld_ntv(up + base, t + kORows * u);
-            qg[u] = ld_ntv(g + base, t + kORows * u);
+        const int qi = tile_quad<K>(t + kORows * u, nq);
+        if (K >= 4 || t + kORows * u < nq) {
+            qx[u] = ld_ntv(x + base, qi);
+            qu[u] = ld_ntv(up + base, qi);
+            qg[u] = ld_ntv(g + base, qi);
         }
     }
     const int tl = (nq << 2) + t;
