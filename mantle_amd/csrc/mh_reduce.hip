@@ -537,13 +537,15 @@ __global__ void __launch_bounds__(kLdsRows)
     const int cnt = (int)(rows * B);
     const int nq = cnt >> 2;
     float* gb = grad + base;
+    // a quad past the tile reloads the tile's last one (the loads need no per-lane guard, under
+    // which the compiler zeroed the registers first); a tile of no whole quad loads none
     float4 xq[QPT], gq[QPT];
+    if (nq > 0) {
 #pragma unroll
-    for (int u = 0; u < QPT; ++u) {
-        const int i = t + u * kLdsRows;
-        if (i < nq) {
-            xq[u] = ld_nt4(x + base, i);
-            gq[u] = ld_nt4(gb, i);
+        for (int u = 0; u < QPT; ++u) {
+            const int i = t + u * kLdsRows;
+            xq[u] = ld_nt4(x + base, i < nq ? i : nq - 1);
+            gq[u] = ld_nt4(gb, i < nq ? i : nq - 1);
         }
     }
     const float ugt = t < rows ? ug[r0 + t] : 0.0f;
