@@ -276,10 +276,23 @@ __global__ void __launch_bounds__(kThreads)
 
 // Kind of operand k in the row/column/plane engines, from two bits per operand in kinds. A
 // lone operand is the broadcast one (these engines run only on plans with one), which makes
-// its kind a compile-time constant: no scalar load or kind test at wave start.
-template <int NIN>
+// its kind a compile-time constant: no scalar load or kind test at wave start. KS >= 0 fixes
+// the kinds of two operands at compile time (a full operand and a broadcast one, in either
+// order: KS_FB, KS_BF); with kinds known only at run time, each operand's loads sit in a branch
+// on its kind, and the compiler waits at the branch's end for the loads issued so far, so a
+// broadcast operand ahead of a full one cost a second memory round trip.
+constexpr int KS_RUN = -1;
+constexpr int KS_FB = IN_FULL | (IN_BCAST << 2);
+constexpr int KS_BF = IN_BCAST | (IN_FULL << 2);
+template <int NIN, int KS = KS_RUN>
 __device__ __forceinline__ int bc_kind(int kinds, int k) {
-    return NIN == 1 ? (int)IN_BCAST : (kinds >> (2 * k)) & 3;
+    if constexpr (NIN == 1) return (int)IN_BCAST;
+    return ((KS >= 0 ? KS : kinds) >> (2 * k)) & 3;
+}
+
+// KS for a launch: the compile-time form for two operands of those kinds
+static inline int bc_static_kinds(int nin, int kinds) {
+    return nin == 2 && (kinds == KS_FB || kinds == KS_BF) ? kinds : KS_RUN;
 }
 
 // Row-broadcast engine: output [rows, K] with K >= 4 and fewer than 2^31 elements, every
@@ -291,7 +304,7 @@ __device__ __forceinline__ int bc_kind(int kinds, int k) {
 // so the two loads are in flight together: loading the second under a branch made every
 // quad wait for the first before issuing it. kinds holds two bits of InKind per operand.
 // Element values are the same single operations as every engine.
-template <class F, int NIN, bool ACCUM>
+template <class F, int NIN, bool ACCUM, int KS = KS_RUN>
 __global__ void __launch_bounds__(kThreads)
     k_rowbc4(float* __restrict__ out, InPtrs<NIN> in, int kinds, int64_t n, uint32_t K, uint32_t last_row,
              FastDiv fk, DevScal ds, F f) {
@@ -299,7 +312,7 @@ __global__ void __launch_bounds__(kThreads)
     f.setup(ds);
     float sv[NA];
 #pragma unroll
-    for (int k = 0; k < NIN; ++k) sv[k] = bc_kind<NIN>(kinds, k) == IN_SCALAR ? in.p[k][0] : 0.0f;
+    for (int k = 0; k < NIN; ++k) sv[k] = bc_kind<NIN, KS>(kinds, k) == IN_SCALAR ? in.p[k][0] : 0.0f;
     const int64_t nq = n >> 2;
     const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (q < nq) {
@@ -311,7 +324,7 @@ __global__ void __launch_bounds__(kThreads)
         float v[4][NA];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
-            const int kind = bc_kind<NIN>(kinds, k);
+            const int kind = bc_kind<NIN, KS>(kinds, k);
             if (kind == IN_SCALAR) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) v[j][k] = sv[k];
@@ -343,7 +356,7 @@ __global__ void __launch_bounds__(kThreads)
             float v[NA];
 #pragma unroll
             for (int k = 0; k < NIN; ++k) {
-                const int kind = bc_kind<NIN>(kinds, k);
+                const int kind = bc_kind<NIN, KS>(kinds, k);
                 v[k] = kind == IN_SCALAR ? sv[k] : (kind == IN_FULL ? in.p[k][i] : in.p[k][row]);
             }
             const float fv = f(v);
@@ -357,7 +370,7 @@ __global__ void __launch_bounds__(kThreads)
 // is), all operands and the output 16-byte aligned. One quad per thread in flat order (one
 // sequential stream, as for same-shape operands); the quad's column quad is q mod C/4 (one
 // fast division), whose operand quads are small enough to stay in L2.
-template <class F, int NIN, bool ACCUM>
+template <class F, int NIN, bool ACCUM, int KS = KS_RUN>
 __global__ void __launch_bounds__(kThreads)
     k_colbc4(float* __restrict__ out, InPtrs<NIN> in, int kinds, int64_t nq, uint32_t Cq, FastDiv fcq, DevScal ds,
              F f) {
@@ -365,14 +378,14 @@ __global__ void __launch_bounds__(kThreads)
     f.setup(ds);
     float sv[NA];
 #pragma unroll
-    for (int k = 0; k < NIN; ++k) sv[k] = bc_kind<NIN>(kinds, k) == IN_SCALAR ? in.p[k][0] : 0.0f;
+    for (int k = 0; k < NIN; ++k) sv[k] = bc_kind<NIN, KS>(kinds, k) == IN_SCALAR ? in.p[k][0] : 0.0f;
     const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (q < nq) {
         const uint32_t cq = (uint32_t)q - fdiv((uint32_t)q, fcq) * Cq;
         vf4 t[NA];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
-            const int kind = bc_kind<NIN>(kinds, k);
+            const int kind = bc_kind<NIN, KS>(kinds, k);
             if (kind == IN_FULL) t[k] = ld_ntv(in.p[k], q);
             else if (kind == IN_BCAST) t[k] = reinterpret_cast<const vf4*>(in.p[k])[cq];
             else t[k] = vf4{sv[k], sv[k], sv[k], sv[k]};
@@ -397,7 +410,7 @@ __global__ void __launch_bounds__(kThreads)
 // every IN_BCAST operand a per-channel vector ([1, C, 1], as an NCHW bias is), the output and
 // FULL operands 16-byte aligned. One quad per thread in flat order; a quad lies in one plane
 // (S % 4 == 0), whose channel is (q / (S / 4)) mod C (two fast divisions).
-template <class F, int NIN, bool ACCUM>
+template <class F, int NIN, bool ACCUM, int KS = KS_RUN>
 __global__ void __launch_bounds__(kThreads)
     k_planebc4(float* __restrict__ out, InPtrs<NIN> in, int kinds, int64_t nq, uint32_t C, FastDiv fsq, FastDiv fc,
                DevScal ds, F f) {
@@ -405,7 +418,7 @@ __global__ void __launch_bounds__(kThreads)
     f.setup(ds);
     float sv[NA];
 #pragma unroll
-    for (int k = 0; k < NIN; ++k) sv[k] = bc_kind<NIN>(kinds, k) == IN_SCALAR ? in.p[k][0] : 0.0f;
+    for (int k = 0; k < NIN; ++k) sv[k] = bc_kind<NIN, KS>(kinds, k) == IN_SCALAR ? in.p[k][0] : 0.0f;
     const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (q < nq) {
         const uint32_t p = fdiv((uint32_t)q, fsq);
@@ -413,7 +426,7 @@ __global__ void __launch_bounds__(kThreads)
         vf4 t[NA];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
-            const int kind = bc_kind<NIN>(kinds, k);
+            const int kind = bc_kind<NIN, KS>(kinds, k);
             if (kind == IN_FULL) {
                 t[k] = ld_ntv(in.p[k], q);
             } else {
@@ -694,8 +707,22 @@ static int run_map(float* out, const ElwPlan& pl, const float* const* ptrs, cons
         if (rowform) {
             const uint32_t K = (uint32_t)pl.dims[1];
             const uint32_t last_row = (uint32_t)(pl.n / K) - 1;  // pl.n > 0: empty tensors return earlier
+            const FastDiv fk = make_fastdiv(K);
+            if constexpr (NIN == 2) {  // a full and a broadcast operand: kinds fixed at compile time
+                const int ks = bc_static_kinds(NIN, kinds);
+                if (ks == KS_FB) {
+                    hipLaunchKernelGGL((k_rowbc4<F, NIN, ACCUM, KS_FB>), g, b, 0, st, out, in, kinds, pl.n, K,
+                                       last_row, fk, ds, f);
+                    return MH_OK;
+                }
+                if (ks == KS_BF) {
+                    hipLaunchKernelGGL((k_rowbc4<F, NIN, ACCUM, KS_BF>), g, b, 0, st, out, in, kinds, pl.n, K,
+                                       last_row, fk, ds, f);
+                    return MH_OK;
+                }
+            }
             hipLaunchKernelGGL((k_rowbc4<F, NIN, ACCUM>), g, b, 0, st, out, in, kinds, pl.n, K, last_row,
-                               make_fastdiv(K), ds, f);
+                               fk, ds, f);
             return MH_OK;
         }
         // [rows, C] with per-column operands ([1, C]), C % 4 == 0
@@ -708,14 +735,42 @@ static int run_map(float* out, const ElwPlan& pl, const float* const* ptrs, cons
             if (pl.kind[k] == IN_BCAST && !(pl.st[k][0] == 0 && pl.st[k][1] == 1 && pl.st[k][2] == 0)) planeform = false;
         if (planeform) {
             const uint32_t C = (uint32_t)pl.dims[1], Sq = (uint32_t)(pl.dims[2] / 4);
-            hipLaunchKernelGGL((k_planebc4<F, NIN, ACCUM>), g, b, 0, st, out, in, kinds, pl.n >> 2, C,
-                               make_fastdiv(Sq), make_fastdiv(C), ds, f);
+            const FastDiv fsq = make_fastdiv(Sq), fc = make_fastdiv(C);
+            if constexpr (NIN == 2) {  // a full and a broadcast operand: kinds fixed at compile time
+                const int ks = bc_static_kinds(NIN, kinds);
+                if (ks == KS_FB) {
+                    hipLaunchKernelGGL((k_planebc4<F, NIN, ACCUM, KS_FB>), g, b, 0, st, out, in, kinds, pl.n >> 2, C,
+                                       fsq, fc, ds, f);
+                    return MH_OK;
+                }
+                if (ks == KS_BF) {
+                    hipLaunchKernelGGL((k_planebc4<F, NIN, ACCUM, KS_BF>), g, b, 0, st, out, in, kinds, pl.n >> 2, C,
+                                       fsq, fc, ds, f);
+                    return MH_OK;
+                }
+            }
+            hipLaunchKernelGGL((k_planebc4<F, NIN, ACCUM>), g, b, 0, st, out, in, kinds, pl.n >> 2, C, fsq,
+                               fc, ds, f);
             return MH_OK;
         }
         if (colform) {
             const uint32_t Cq = (uint32_t)(pl.dims[1] / 4);
-            hipLaunchKernelGGL((k_colbc4<F, NIN, ACCUM>), g, b, 0, st, out, in, kinds, pl.n >> 2, Cq, make_fastdiv(Cq),
-                               ds, f);
+            const FastDiv fcq = make_fastdiv(Cq);
+            if constexpr (NIN == 2) {  // a full and a broadcast operand: kinds fixed at compile time
+                const int ks = bc_static_kinds(NIN, kinds);
+                if (ks == KS_FB) {
+                    hipLaunchKernelGGL((k_colbc4<F, NIN, ACCUM, KS_FB>), g, b, 0, st, out, in, kinds, pl.n >> 2, Cq,
+                                       fcq, ds, f);
+                    return MH_OK;
+                }
+                if (ks == KS_BF) {
+                    hipLaunchKernelGGL((k_colbc4<F, NIN, ACCUM, KS_BF>), g, b, 0, st, out, in, kinds, pl.n >> 2, Cq,
+                                       fcq, ds, f);
+                    return MH_OK;
+                }
+            }
+            hipLaunchKernelGGL((k_colbc4<F, NIN, ACCUM>), g, b, 0, st, out, in, kinds, pl.n >> 2, Cq, fcq, ds,
+                               f);
             return MH_OK;
         }
         const bool inner4 = pl.vec_ok && al_b;
