@@ -1368,12 +1368,16 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
             return MH_OK;
         }
     }
-    // multi-lane engine, aligned operands: rows of whole 16-byte quads for 17-64 classes and
-    // loss rows of more than 24 classes. Streamed over 8M elements, Softmax rows that are not
-    // whole quads run 15-19 us in the thread engine (32 us at 63 classes) against 30-31 us
-    // here, and losses of 17-23 classes 22-28 us there against 23-28 us here, so those stay on
-    // the thread engine.
-    if (K > 16 && K <= 4 * kMNE && al && (K % 4 == 0 || (LOSS && K > 24))) {
+    // multi-lane engine, aligned operands: loss rows of whole 16-byte quads or of more than 24
+    // classes, and Softmax / LogSoftmax rows of whole quads where the thread engine's tile
+    // reads collide in LDS (a row stride that is a multiple of 8 floats, from 32 classes) or
+    // its 64-element registers cost occupancy (above 52). Streamed over 8M elements, Softmax
+    // quad rows run 14.5-19 us in the thread engine at 20-28, 36, 44 and 52 classes against
+    // 19.6-20.7 us here, but 21-41 us there at 32, 40, 48 and 56-64 against 20.4-20.9 us here;
+    // rows that are not whole quads run 15-19 us there (32 us at 63 classes) against 30-31 us
+    // here; losses of 17-23 classes 22-28 us there against 23-28 us here.
+    const bool rowm_map = K % 4 == 0 && K >= 32 && (K % 8 == 0 || K > 52);
+    if (K > 16 && K <= 4 * kMNE && al && (LOSS ? (K % 4 == 0 || K > 24) : rowm_map)) {
         const int P = (K + kMNE - 1) / kMNE;
         const int64_t rpb = (int64_t)(kSThreads / 64) * (64 / P);
         const int64_t nb = (rows + rpb - 1) / rpb;
