@@ -295,6 +295,13 @@ static inline int bc_static_kinds(int nin, int kinds) {
     return nin == 2 && (kinds == KS_FB || kinds == KS_BF) ? kinds : KS_RUN;
 }
 
+// The general engine's kind of operand k: from the plan, or fixed by KS
+template <int NIN, int KS>
+__device__ __forceinline__ int bc_kind_pl(const ElwPlan& pl, int k) {
+    if constexpr (KS >= 0) return (KS >> (2 * k)) & 3;
+    return pl.kind[k];
+}
+
 // Row-broadcast engine: output [rows, K] with K >= 4 and fewer than 2^31 elements, every
 // IN_BCAST operand a contiguous per-row vector ([rows, 1], as a row max or row sum is), the
 // output and FULL operands 16-byte aligned. One quad per thread: the quad's first row comes
@@ -459,7 +466,7 @@ __global__ void __launch_bounds__(kThreads)
 // the next one, whose offsets follow by addition while the next-outer coordinate does not
 // wrap (a full decode per element only for rows shorter than 4 or at such a wrap); an
 // operand constant along the inner dim is read once per row touched.
-template <class F, int NIN, bool ACCUM, bool INNER4, bool BIG, int MAXR>
+template <class F, int NIN, bool ACCUM, bool INNER4, bool BIG, int MAXR, int KS = KS_RUN>
 __global__ void __launch_bounds__(kThreads)
     k_bcast4(float* __restrict__ out, InPtrs<NIN> in, ElwPlan pl, DevScal ds, F f) {
     constexpr int NA = NIN > 0 ? NIN : 1;
@@ -467,7 +474,7 @@ __global__ void __launch_bounds__(kThreads)
     f.setup(ds);
     float sv[NA];
 #pragma unroll
-    for (int k = 0; k < NIN; ++k) sv[k] = pl.kind[k] == IN_SCALAR ? in.p[k][0] : 0.0f;
+    for (int k = 0; k < NIN; ++k) sv[k] = bc_kind_pl<NIN, KS>(pl, k) == IN_SCALAR ? in.p[k][0] : 0.0f;
     const int inner = pl.rank - 1;
     const int64_t dinner = pl.dims[inner];
     const int64_t douter = inner > 0 ? pl.dims[inner - 1] : 1;
@@ -492,12 +499,16 @@ __global__ void __launch_bounds__(kThreads)
                 slow = true;
             }
         }
+        // with the kinds fixed (KS), broadcast operands go first: their loads sit under run-time
+        // branches on the stride, whose joins wait for the loads issued before them, so a full
+        // operand loaded ahead would be waited for there (two memory round trips per quad)
 #pragma unroll
-        for (int k = 0; k < NIN; ++k) {
-            if (pl.kind[k] == IN_SCALAR) {
+        for (int kk = 0; kk < NIN; ++kk) {
+            const int k = KS == KS_FB ? NIN - 1 - kk : kk;
+            if (bc_kind_pl<NIN, KS>(pl, k) == IN_SCALAR) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) v[j][k] = sv[k];
-            } else if (pl.kind[k] == IN_FULL) {
+            } else if (bc_kind_pl<NIN, KS>(pl, k) == IN_FULL) {
                 const float4 t = ld_nt4(in.p[k], q);
                 v[0][k] = t.x; v[1][k] = t.y; v[2][k] = t.z; v[3][k] = t.w;
             } else if (INNER4) {
@@ -536,7 +547,7 @@ __global__ void __launch_bounds__(kThreads)
                 }
 #pragma unroll
                 for (int k = 0; k < NIN; ++k)
-                    if (pl.kind[k] == IN_BCAST) v[j][k] = in.p[k][oj[k]];
+                    if (bc_kind_pl<NIN, KS>(pl, k) == IN_BCAST) v[j][k] = in.p[k][oj[k]];
             }
         }
         const float4 o = ACCUM ? ld_nt4(out, q) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -557,7 +568,7 @@ __global__ void __launch_bounds__(kThreads)
             float v1[NA];
 #pragma unroll
             for (int k = 0; k < NIN; ++k)
-                v1[k] = pl.kind[k] == IN_SCALAR ? sv[k] : (pl.kind[k] == IN_FULL ? in.p[k][i] : in.p[k][off1[k]]);
+                v1[k] = bc_kind_pl<NIN, KS>(pl, k) == IN_SCALAR ? sv[k] : (bc_kind_pl<NIN, KS>(pl, k) == IN_FULL ? in.p[k][i] : in.p[k][off1[k]]);
             const float r1 = f(v1);
             out[i] = ACCUM ? out[i] + r1 : r1;
         }
@@ -778,6 +789,23 @@ static int run_map(float* out, const ElwPlan& pl, const float* const* ptrs, cons
             if (inner4) hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, true, true, MH_MAX_RANK>), g, b, 0, st, out, in, pl, ds, f);
             else hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, false, true, MH_MAX_RANK>), g, b, 0, st, out, in, pl, ds, f);
         } else if (pl.rank <= 3) {
+            if constexpr (NIN == 2) {  // a full and a broadcast operand: kinds fixed at compile time
+                const int ks = bc_static_kinds(NIN, kinds);
+                if (ks == KS_FB) {
+                    if (inner4) hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, true, false, 3, KS_FB>), g, b, 0, st, out,
+                                                   in, pl, ds, f);
+                    else hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, false, false, 3, KS_FB>), g, b, 0, st, out, in,
+                                            pl, ds, f);
+                    return MH_OK;
+                }
+                if (ks == KS_BF) {
+                    if (inner4) hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, true, false, 3, KS_BF>), g, b, 0, st, out,
+                                                   in, pl, ds, f);
+                    else hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, false, false, 3, KS_BF>), g, b, 0, st, out, in,
+                                            pl, ds, f);
+                    return MH_OK;
+                }
+            }
             if (inner4) hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, true, false, 3>), g, b, 0, st, out, in, pl, ds, f);
             else hipLaunchKernelGGL((k_bcast4<F, NIN, ACCUM, false, false, 3>), g, b, 0, st, out, in, pl, ds, f);
         } else {
