@@ -1139,7 +1139,7 @@ C2_KERNEL = {"ADD.bwd": "void mh::k_bwd2_same4<0, false>", "SUB.bwd": "void mh::
 _N3, _N4, _N5 = 6422528, 1 << 26, 10485760
 WL_KERNELS = [
     ("c3 bias_relu.fwd (fused)", "mh::k_bias_relu_fwd_planes", 1605632, 12 * _N3 + 128, ""),
-    ("c3 ADD.fwd", "void mh::k_planebc4<mh::FBin<0>, 2, false>", 1605632, 8 * _N3 + 128, ""),
+    ("c3 ADD.fwd", "void mh::k_planebc4<mh::FBin<0>, 2, false, 8>", 1605632, 8 * _N3 + 128, ""),
     ("c3 bias_relu.bwd (fused), stream", "void mh::k_bias_relu_bwd_flat<false, true, true, true>", 1605632, 16 * _N3,
      "grad_x read and written; a wave's plane partials into the slot table"),
     ("c3 bias_relu.bwd (fused), combine", "mh::k_bias_partials_comb8", 8192, 4 * 8 * (_N3 // 784) + 256,
@@ -1147,18 +1147,18 @@ WL_KERNELS = [
     ("c3 ADD.bwd_bias", "void mh::k_unb_planes<false>", 131072, 4 * _N3 + 256, "one launch, arrival tickets"),
     ("c4 [8192,8192] axis 0 MAX.fwd", "void mh::k_cols<mh::RMax, mh::LdPlain<mh::RMax>, true, true>", 262144,
      4 * _N4, "first of two launches (split partials)"),
-    ("c4 [8192,8192] axis 0 MAX.bwd, route", "void mh::k_max_route_cols<true, true>", 262144, 4 * _N4,
+    ("c4 [8192,8192] axis 0 MAX.bwd, route", "void mh::k_max_route_cols<true>", 262144, 4 * _N4,
      "grad read; x read again only in splits holding several maxima of a column; stores only quads "
      "holding a maximum"),
-    ("c4 [8192,8192] axis 0 SUM.bwd", "void mh::k_colbc4<mh::FScaleBcast<false>, 1, true>", 16777216, 8 * _N4, ""),
+    ("c4 [8192,8192] axis 0 SUM.bwd", "void mh::k_colbc4<mh::FScaleBcast<false>, 1, true, -1>", 16777216, 8 * _N4, ""),
     ("c4 [8192,8192] axis 1 MAX.bwd", "void mh::k_max_bwd_rowreg<4, 8>", 2097152, 12 * _N4,
      "one pass; stores only quads holding a line maximum"),
     ("c4 [8192,8192] all MAX.bwd, route", "mh::k_max_route_rows", 8388608, 4 * _N4,
      "grad read; x read again only in the chunk holding the maximum; stores only quads holding it"),
     ("c4 [64,512,1024] axis 2 MAX.bwd", "void mh::k_max_bwd_rowreg<1, 4>", 2097152, 12 * (1 << 25),
      "one pass; stores only quads holding a line maximum"),
-    ("c5 SUB.fwd [N,10] - [N,1]", "void mh::k_rowbc4<mh::FBin<1>, 2, false>", 2621440, 8 * _N5 + 4 * (_N5 // 10), ""),
-    ("c5 DIV.bwd0", "void mh::k_rowbc4<mh::FBinRg<3, 0, false>, 2, true>", 2621440, 12 * _N5 + 4 * (_N5 // 10), ""),
+    ("c5 SUB.fwd [N,10] - [N,1]", "void mh::k_rowbc4<mh::FBin<1>, 2, false, 8>", 2621440, 8 * _N5 + 4 * (_N5 // 10), ""),
+    ("c5 DIV.bwd0", "void mh::k_rowbc4<mh::FBinRg<3, 0, false>, 2, true, 8>", 2621440, 12 * _N5 + 4 * (_N5 // 10), ""),
     ("c5 DIV.bwd1 (un-broadcast into [N,1])", "void mh::k_rows_binrg<3, 1, false, 16, true>", 1048576,
      8 * _N5 + 12 * (_N5 // 10), "the rg terms computed in the loader, added into the gradient in row order"),
     ("c5 MAX.bwd (rows of 10)", "void mh::k_max_bwd_rows<16>", 1048576, 12 * _N5 + 8 * (_N5 // 10),
@@ -1174,14 +1174,14 @@ WL_KERNELS = [
 # rocprofv3 duration the stats summary sets beside the bench's figures
 WL_STATS = [("c3", "op_by_op", "ADD.bwd_bias", "void mh::k_unb_planes<false>"),
             ("c3", "fused", "bias_relu.fwd", "mh::k_bias_relu_fwd_planes"),
-            ("c3", "op_by_op", "ADD.fwd", "void mh::k_planebc4<mh::FBin<0>, 2, false>"),
+            ("c3", "op_by_op", "ADD.fwd", "void mh::k_planebc4<mh::FBin<0>, 2, false, 8>"),
             ("c3", "fused", "bias_relu.bwd", ("void mh::k_bias_relu_bwd_flat<false, true, true, true>",
                                               "mh::k_bias_partials_comb8")),
             ("c4", "ops", "8192x8192.ax1.MAX.bwd", "void mh::k_max_bwd_rowreg<4, 8>"),
             ("c5", "fused", "fused.fwd", ("void mh::k_rowo_fwd<0, 10>", "void mh::k_loss_comb<0>")),
             ("c5", "fused", "fused.bwd", "void mh::k_rowo_bwd<0, 10>"),
-            ("c5", "fwd", "SUB.fwd", "void mh::k_rowbc4<mh::FBin<1>, 2, false>"),
-            ("c5", "fwd", "DIV.fwd", "void mh::k_rowbc4<mh::FBin<3>, 2, false>"),
+            ("c5", "fwd", "SUB.fwd", "void mh::k_rowbc4<mh::FBin<1>, 2, false, 8>"),
+            ("c5", "fwd", "DIV.fwd", "void mh::k_rowbc4<mh::FBin<3>, 2, false, 8>"),
             ("c5", "bwd", "DIV.bwd1", "void mh::k_rows_binrg<3, 1, false, 16, true>")]
 
 
