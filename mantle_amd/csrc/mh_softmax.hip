@@ -543,8 +543,9 @@ __global__ void __launch_bounds__(kORows)
 // per wavefront and the sixteen wavefront sums in order finish it. The loss is the sum / lscale
 // (MEAN, lscale = f32(N)) or the sum * lscale (cross entropy, lscale = its scale). One launch
 // with every load of a round in flight: at config 5 (16384 partials) 2.4 us after the pass,
-// against 2.8-3.3 us for two rounds of scalar loads. It takes up to kLossCombMax partials (four
-// rounds); more go through the library's multi-block all-element reduction.
+// against 2.8-3.3 us for two rounds of scalar loads (256 threads of sixteen loads each measured
+// the same). It takes up to kLossCombMax partials (four rounds); more go through the library's
+// multi-block all-element reduction.
 constexpr int kLCThreads = 1024;
 constexpr int64_t kLossCombMax = 4 * 4 * kLCThreads;
 
