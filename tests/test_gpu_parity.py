@@ -49,7 +49,11 @@ BIN_SHAPES = [((37, 63, 107), (37, 63, 107)), ((37, 63, 107), (37, 63, 1)), ((37
               ((4, 32, 7, 7), (1, 32, 1, 1)), ((4099, 10), (4099, 1)), ((8, 1, 5), (1, 6, 1)),
               ((3,), (3,)), ((1,), (1,)), ((7, 5), (5,)), ((2, 1, 3, 1, 5), (1, 4, 3, 6, 1)),
               ((5, 3), (5, 1)), ((7, 2), (1, 2)), ((9, 1, 3), (9, 4, 1)), ((1023, 6), (1023, 1)),
-              ((65, 4), (65, 1)), ((1001, 5), (1001, 1)), ((6, 2, 13), (6, 2, 1))]
+              ((65, 4), (65, 1)), ((1001, 5), (1001, 1)), ((6, 2, 13), (6, 2, 1)),
+              # a full and a broadcast operand in both orders through the column, plane and
+              # general engines (their compile-time kind pairs)
+              ((1, 32), (32, 32)), ((4, 32, 8, 8), (1, 32, 1, 1)), ((1, 32, 1, 1), (4, 32, 8, 8)),
+              ((6, 5, 16), (6, 1, 16)), ((6, 1, 16), (6, 5, 16)), ((1, 5, 16), (6, 5, 16))]
 
 
 def _dim(rng, big):
