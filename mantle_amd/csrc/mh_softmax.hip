@@ -135,6 +135,45 @@ __device__ __forceinline__ void unstage_tile(float* __restrict__ dst, const floa
     for (int i = done + t; i < cnt; i += kSThreads) st_nt(dst + base + i, src[i]);
 }
 
+// The same with each row of K floats at a stride of K + 1 in LDS (K a multiple of 4, so no quad
+// straddles two rows; fk divides by K): the thread engine reads row t at t * (K + 1), and with K
+// a multiple of 8 the rows at stride K put a wavefront's reads on a few LDS banks (at 32
+// classes all on one).
+__device__ __forceinline__ void stage_tile_pad(float* dst, const float* __restrict__ src, int64_t base, int cnt,
+                                               FastDiv fk) {
+    const int t = threadIdx.x;
+    const int nq = cnt >> 2;
+    int i = t;
+    for (; i + 3 * kSThreads < nq; i += 4 * kSThreads) {
+        float4 q[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) q[u] = ld_nt4(src + base, i + u * kSThreads);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t e = 4u * (uint32_t)(i + u * kSThreads);
+            float* d = dst + e + fdiv(e, fk);
+            d[0] = q[u].x; d[1] = q[u].y; d[2] = q[u].z; d[3] = q[u].w;
+        }
+    }
+    for (; i < nq; i += kSThreads) {
+        const float4 q = ld_nt4(src + base, i);
+        const uint32_t e = 4u * (uint32_t)i;
+        float* d = dst + e + fdiv(e, fk);
+        d[0] = q.x; d[1] = q.y; d[2] = q.z; d[3] = q.w;
+    }
+}
+
+__device__ __forceinline__ void unstage_tile_pad(float* __restrict__ dst, const float* src, int64_t base, int cnt,
+                                                 FastDiv fk) {
+    const int t = threadIdx.x;
+    const int nq = cnt >> 2;
+    for (int i = t; i < nq; i += kSThreads) {
+        const uint32_t e = 4u * (uint32_t)i;
+        const float* s4 = src + e + fdiv(e, fk);
+        st_nt4(dst + base, i, make_float4(s4[0], s4[1], s4[2], s4[3]));
+    }
+}
+
 __device__ __forceinline__ float block_sum(float v, float* ws) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m);
@@ -259,27 +298,35 @@ __device__ __forceinline__ float row_fwd(float* xrow, const float* trow, float r
 template <int V, int KM>
 __global__ void __launch_bounds__(kSThreads)
     k_rowt_fwd(const float* __restrict__ x, const float* __restrict__ tg, float* __restrict__ out, int64_t rows,
-               int K, int rb, bool al, float* __restrict__ part) {
+               int K, int rb, bool al, float* __restrict__ part, int Kp, FastDiv fk) {
+    // Kp: the LDS row stride, K or (padded, aligned operands, K a multiple of 8) K + 1
     extern __shared__ float4 smem4[];
     __shared__ float ws[4];
     constexpr bool LOSS = V == G_SMLM || V == G_CE;
+    const bool pad = Kp != K;
     float* xs = reinterpret_cast<float*>(smem4);
-    float* ts = xs + rb * K;
+    float* ts = xs + rb * Kp;
     const int64_t r0 = (int64_t)blockIdx.x * rb;
     const int nr = (int)((rows - r0) < rb ? (rows - r0) : rb);
     const int64_t base = r0 * K;
-    stage_tile(xs, x, base, nr * K, al);
-    if (LOSS) stage_tile(ts, tg, base, nr * K, al);
+    if (pad) {
+        stage_tile_pad(xs, x, base, nr * K, fk);
+        if (LOSS) stage_tile_pad(ts, tg, base, nr * K, fk);
+    } else {
+        stage_tile(xs, x, base, nr * K, al);
+        if (LOSS) stage_tile(ts, tg, base, nr * K, al);
+    }
     __syncthreads();
     float rowsum = 0.0f;
     const int t = threadIdx.x;
-    if (t < nr) rowsum = row_fwd<V, KM>(xs + t * K, ts + t * K, rowsum, K);
+    if (t < nr) rowsum = row_fwd<V, KM>(xs + t * Kp, ts + t * Kp, rowsum, K);
     if constexpr (LOSS) {
         const float tot = block_sum(rowsum, ws);
         if (t == 0) part[blockIdx.x] = tot;
     } else {
         __syncthreads();
-        unstage_tile(out, xs, base, nr * K, al);
+        if (pad) unstage_tile_pad(out, xs, base, nr * K, fk);
+        else unstage_tile(out, xs, base, nr * K, al);
     }
 }
 
@@ -1370,14 +1417,15 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
         }
     }
     // multi-lane engine, aligned operands: loss rows of whole 16-byte quads or of more than 24
-    // classes, and Softmax / LogSoftmax rows of whole quads where the thread engine's tile
-    // reads collide in LDS (a row stride that is a multiple of 8 floats, from 32 classes) or
-    // its 64-element registers cost occupancy (above 52). Streamed over 8M elements, Softmax
-    // quad rows run 14.5-19 us in the thread engine at 20-28, 36, 44 and 52 classes against
-    // 19.6-20.7 us here, but 21-41 us there at 32, 40, 48 and 56-64 against 20.4-20.9 us here;
-    // rows that are not whole quads run 15-19 us there (32 us at 63 classes) against 30-31 us
-    // here; losses of 17-23 classes 22-28 us there against 23-28 us here.
-    const bool rowm_map = K % 4 == 0 && K >= 32 && (K % 8 == 0 || K > 52);
+    // classes, and Softmax / LogSoftmax rows of whole quads of 40, 48 or more than 52 classes.
+    // Streamed over 8M elements, Softmax quad rows run 14.1-19 us in the thread engine at 20-36,
+    // 44 and 52 classes (32 with its rows padded in LDS: 14.5 against 36 us unpadded) against
+    // 19.6-20.7 us here; at 40-64 classes the thread engine's LDS tiles (and, above 32, its
+    // 64-element registers) hold a CU to two or three blocks, and how its blocks fall into
+    // rounds decides (18-31 us against 20.6-21.0 us here). Rows that are not whole quads run
+    // 15-19 us there (32 us at 63 classes) against 30-31 us here; losses of 17-23 classes
+    // 22-28 us there against 23-28 us here.
+    const bool rowm_map = K % 4 == 0 && K > 32 && (K % 8 == 0 || K > 52);
     if (K > 16 && K <= 4 * kMNE && al && (LOSS ? (K % 4 == 0 || K > 24) : rowm_map)) {
         const int P = (K + kMNE - 1) / kMNE;
         const int64_t rpb = (int64_t)(kSThreads / 64) * (64 / P);
@@ -1400,13 +1448,17 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
         return MH_OK;
     }
     if (K <= kSThreadMax) {
-        const int rb = rows_per_block(LOSS ? 2 : 1, K);
+        // rows of a multiple of 8 floats at a stride of K + 1 in LDS (aligned operands)
+        const int Kp = al && K % 8 == 0 ? K + 1 : K;
+        const int rb = rows_per_block(LOSS ? 2 : 1, Kp);
         const int64_t nb = (rows + rb - 1) / rb;
         if (nb > 0x7fffffff) return fail(MH_ERR_OVERFLOW, "too many rows");
         *nblocks_out = nb;
-        const size_t lds = (LOSS ? 2 : 1) * (size_t)rb * (size_t)K * sizeof(float);
+        const size_t lds = (LOSS ? 2 : 1) * (size_t)rb * (size_t)Kp * sizeof(float);
+        const FastDiv fk = make_fastdiv((uint32_t)K);
         dim3 g((unsigned)nb), b(kSThreads);
-#define MH_RT(KM) hipLaunchKernelGGL((k_rowt_fwd<V, KM>), g, b, lds, st, x, tg, out, rows, K, rb, al, part)
+#define MH_RT(KM) \
+    hipLaunchKernelGGL((k_rowt_fwd<V, KM>), g, b, lds, st, x, tg, out, rows, K, rb, al, part, Kp, fk)
         if (K <= 8) MH_RT(8);
         else if (K <= 16) MH_RT(16);
         else if (K <= 32) MH_RT(32);
