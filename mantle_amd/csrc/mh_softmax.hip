@@ -535,6 +535,38 @@ __device__ __forceinline__ int tile_quad(int q, int nq) {
     if constexpr (K >= 4) return q < nq ? q : nq - 1;
     return q;
 }
+
+// The one-shot tiles' LDS row stride: K, or K + 1 for 24 and 32 classes (at stride K the
+// wavefront's row reads t * K + j fall on a few banks, at 32 classes on one). Quads go in and
+// out as float4 at stride K; at stride K + 1 (K a multiple of 4, so a quad never straddles two
+// rows) element e sits at e + e / K. At 8 and 16 classes the padded tiles measured no faster
+// (the CrossEntropy forward 0.3-0.7 us slower over 8M elements).
+template <int K>
+constexpr int tile_stride() {
+    return K % 8 == 0 && K > 16 ? K + 1 : K;
+}
+template <int K>
+__device__ __forceinline__ int tile_el(int e) {
+    return tile_stride<K>() == K ? e : e + e / K;
+}
+template <int K>
+__device__ __forceinline__ void tile_put(float* s, int qi, const vf4& q) {
+    if constexpr (tile_stride<K>() == K) {
+        reinterpret_cast<vf4*>(s)[qi] = q;
+    } else {
+        float* d = s + tile_el<K>(4 * qi);
+        d[0] = q[0]; d[1] = q[1]; d[2] = q[2]; d[3] = q[3];
+    }
+}
+template <int K>
+__device__ __forceinline__ vf4 tile_get(const float* s, int qi) {
+    if constexpr (tile_stride<K>() == K) {
+        return reinterpret_cast<const vf4*>(s)[qi];
+    } else {
+        const float* d = s + tile_el<K>(4 * qi);
+        return vf4{d[0], d[1], d[2], d[3]};
+    }
+}
 constexpr int64_t kOMaxBlocks = max_grid_blocks(kORows);  // blocks of one launch
 
 template <int V, int K>
@@ -542,7 +574,8 @@ __global__ void __launch_bounds__(kORows)
     k_rowo_fwd(const float* __restrict__ x, const float* __restrict__ tg, int64_t rows, float* __restrict__ part) {
     static_assert(V == G_SMLM || V == G_CE, "the one-shot forward runs the loss graphs");
     constexpr int QPT = (K + 3) / 4;  // 16 K quads per tile over 64 threads
-    __shared__ vf4 xs4[kORows * K / 4 + 1], ts4[kORows * K / 4 + 1];
+    constexpr int KP = tile_stride<K>();
+    __shared__ vf4 xs4[(kORows * KP + 3) / 4 + 1], ts4[(kORows * KP + 3) / 4 + 1];
     float* xs = reinterpret_cast<float*>(xs4);
     float* ts = reinterpret_cast<float*>(ts4);
     const int t = threadIdx.x;
@@ -568,17 +601,17 @@ __global__ void __launch_bounds__(kORows)
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
         if (t + kORows * u < nq) {
-            xs4[t + kORows * u] = qx[u];
-            ts4[t + kORows * u] = qt[u];
+            tile_put<K>(xs, t + kORows * u, qx[u]);
+            tile_put<K>(ts, t + kORows * u, qt[u]);
         }
     }
     if (tl < cnt) {
-        xs[tl] = tx;
-        ts[tl] = tt;
+        xs[tile_el<K>(tl)] = tx;
+        ts[tile_el<K>(tl)] = tt;
     }
     __syncthreads();
     float rowsum = 0.0f;
-    if (t < nr) rowsum = row_fwd<V, K>(xs + t * K, ts + t * K, rowsum, K);
+    if (t < nr) rowsum = row_fwd<V, K>(xs + t * KP, ts + t * KP, rowsum, K);
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) rowsum = rowsum + __shfl_xor(rowsum, m);
     if (t == 0) part[blockIdx.x] = rowsum;
@@ -707,7 +740,8 @@ __global__ void __launch_bounds__(kORows)
     k_rowo_bwd(float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ up,
                const float* __restrict__ ug, int64_t rows, float c) {
     constexpr int QPT = (K + 3) / 4;
-    __shared__ vf4 xs4[kORows * K / 4 + 1], us4[kORows * K / 4 + 1];
+    constexpr int KP = tile_stride<K>();
+    __shared__ vf4 xs4[(kORows * KP + 3) / 4 + 1], us4[(kORows * KP + 3) / 4 + 1];
     float* xs = reinterpret_cast<float*>(xs4);
     float* us = reinterpret_cast<float*>(us4);
     const int t = threadIdx.x;
@@ -741,36 +775,36 @@ __global__ void __launch_bounds__(kORows)
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
         if (t + kORows * u < nq) {
-            xs4[t + kORows * u] = qx[u];
-            us4[t + kORows * u] = qu[u];
+            tile_put<K>(xs, t + kORows * u, qx[u]);
+            tile_put<K>(us, t + kORows * u, qu[u]);
         }
     }
     if (tl < cnt) {
-        xs[tl] = tx;
-        us[tl] = tu;
+        xs[tile_el<K>(tl)] = tx;
+        us[tile_el<K>(tl)] = tu;
     }
     __syncthreads();
     if (t < nr) {
         float xr[K], pre[K], mb, sg;
-        row_bwd<V, K>(xr, pre, mb, sg, xs + t * K, us + t * K, gconst, skip_ok, K);
+        row_bwd<V, K>(xr, pre, mb, sg, xs + t * KP, us + t * KP, gconst, skip_ok, K);
 #pragma unroll
         for (int j = 0; j < K; ++j) {
-            xs[t * K + j] = pre[j];
-            us[t * K + j] = xr[j] == mb ? sg : 0.0f;
+            xs[t * KP + j] = pre[j];
+            us[t * KP + j] = xr[j] == mb ? sg : 0.0f;
         }
     }
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
         if (t + kORows * u < nq) {
-            const vf4 p = xs4[t + kORows * u], r = us4[t + kORows * u];
+            const vf4 p = tile_get<K>(xs, t + kORows * u), r = tile_get<K>(us, t + kORows * u);
             vf4 o;
 #pragma unroll
             for (int j = 0; j < 4; ++j) o[j] = (qg[u][j] + p[j]) + r[j];
             st_ntv(g + base, t + kORows * u, o);
         }
     }
-    if (tl < cnt) st_nt(g + base + tl, (tg + xs[tl]) + us[tl]);
+    if (tl < cnt) st_nt(g + base + tl, (tg + xs[tile_el<K>(tl)]) + us[tile_el<K>(tl)]);
 }
 
 
@@ -1333,6 +1367,9 @@ static inline bool al16s(const void* p) { return (reinterpret_cast<uintptr_t>(p)
 // The class counts with row kernels of their own (one-shot and pipelined).
 #define MH_ROW16_CLASSES(X) \
     X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11) X(12) X(13) X(14) X(15) X(16)
+// the one-shot kernels' class counts: up to 16, and rows of whole quads of 20-32 classes
+#define MH_ONESHOT_CLASSES(X) MH_ROW16_CLASSES(X) X(20) X(24) X(28) X(32)
+static inline bool oneshot_classes(int K) { return K <= 16 || (K <= 32 && K % 4 == 0); }
 
 // Blocks of a persistent kernel: as many as can be resident at once (queried once per
 // kernel), so no block waits for another to finish.
@@ -1397,7 +1434,9 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
             return MH_OK;
         }
     } else {
-        if (K <= 16 && al) {  // one-shot blocks of 64 rows
+        // one-shot blocks of 64 rows (whole quads of 20-32 classes too: streamed over 8M
+        // elements 15.7-16.8 us against 16.3-19.6 us in the multi-lane engine)
+        if (oneshot_classes(K) && al) {
             const int64_t nb = (rows + kORows - 1) / kORows;
             *nblocks_out = nb;
             for (int64_t b0 = 0; b0 < nb; b0 += kOMaxBlocks) {
@@ -1408,7 +1447,7 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
                 switch (K) {
 #define MH_K(KK) \
     case KK: hipLaunchKernelGGL((k_rowo_fwd<V, KK>), g, b, 0, st, x + off, tg + off, nr, part + b0); break;
-                    MH_ROW16_CLASSES(MH_K)
+                    MH_ONESHOT_CLASSES(MH_K)
 #undef MH_K
                     default: return fail(MH_ERR_INVALID, "row kernel: %d classes", K);
                 }
@@ -1486,7 +1525,7 @@ template <int V>
 static int launch_bwd(float* gx, const float* x, const float* up, const float* ug, int64_t rows, int K, float c) {
     hipStream_t st = ctx().stream;
     const bool al = al16s(x) && al16s(up) && al16s(gx);
-    if (K <= 16 && al) {  // one-shot blocks of 64 rows, several launches past one dispatch
+    if (oneshot_classes(K) && al) {  // one-shot blocks of 64 rows, several launches past one dispatch
         const int64_t nb = (rows + kORows - 1) / kORows;
         for (int64_t b0 = 0; b0 < nb; b0 += kOMaxBlocks) {
             const int64_t cnt = nb - b0 < kOMaxBlocks ? nb - b0 : kOMaxBlocks;
@@ -1496,17 +1535,18 @@ static int launch_bwd(float* gx, const float* x, const float* up, const float* u
             switch (K) {
 #define MH_K(KK) \
     case KK: hipLaunchKernelGGL((k_rowo_bwd<V, KK>), g, b, 0, st, gx + off, x + off, up + off, ug, nr, c); break;
-                MH_ROW16_CLASSES(MH_K)
+                MH_ONESHOT_CLASSES(MH_K)
 #undef MH_K
                 default: return fail(MH_ERR_INVALID, "row kernel: %d classes", K);
             }
         }
         return MH_OK;
     }
-    // multi-lane engine, aligned operands: rows of whole quads and other rows of more than 24
-    // classes. Streamed over 8M elements, rows of 17-23 classes that are not whole quads run
-    // 41-56 us in the thread engine against 47-63 us here (about equal at 21), so they stay
-    // there.
+    // multi-lane engine, aligned operands: rows of whole quads of more than 32 classes and other
+    // rows of more than 24 (whole quads of 20-32 classes take the one-shot kernels above:
+    // streamed over 8M elements, backwards 24-28 us there against 30-34 us here). Rows of 17-23
+    // classes that are not whole quads run 41-56 us in the thread engine against 47-63 us here
+    // (about equal at 21), so they stay there.
     if (K > 16 && K <= 4 * kMNE && al && (K % 4 == 0 || K > 24)) {
         const int P = (K + kMNE - 1) / kMNE;
         const int64_t rpb = (int64_t)(kSThreads / 64) * (64 / P);

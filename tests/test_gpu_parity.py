@@ -1362,15 +1362,16 @@ def test_fused_loss_sums_over_many_block_partials(gpu, rows, classes):
     assert_bitexact(tg.to_numpy(), gr["x"], "cross-entropy backward")
 
 
-ORACLE_ROW_CASES = [(513, 17), (300, 24), (1000, 31), (40, 33), (777, 47), (1200, 64), (500, 32)]
+ORACLE_ROW_CASES = [(513, 17), (300, 24), (1000, 31), (40, 33), (777, 47), (1200, 64), (500, 32), (280, 20), (150, 28),
+                    (333, 36)]
 _rng_oracle_rows = np.random.default_rng(20261202)
 ORACLE_ROW_CASES += [(int(_rng_oracle_rows.integers(1, 1500)), int(_rng_oracle_rows.integers(17, 65))) for _ in range(6)]
 
 
 @pytest.mark.parametrize("rows,classes", ORACLE_ROW_CASES, ids=[f"{r}x{c}" for r, c in ORACLE_ROW_CASES])
 def test_fused_rows_17_to_64_classes_against_the_oracle(gpu, rows, classes):
-    """The thread and multi-lane row engines (17-64 classes) through mh_softmax_*,
-    mh_logsoftmax_* and mh_cross_entropy_* against the oracle's op-by-op graphs
+    """The thread, multi-lane and (whole quads of 20-32 classes) one-shot row engines through
+    mh_softmax_*, mh_logsoftmax_* and mh_cross_entropy_* against the oracle's op-by-op graphs
     (activations.mojo:74-108, loss.mojo:45-61), ties injected, backward accumulated into a
     non-zero grad_x:
     - bit-exact against the oracle with nelts = 1, whose row sums run in element order, the
