@@ -443,8 +443,7 @@ int mh_plan_unbroadcast(const mh_shape* sgrad, const mh_shape* srg, mh_reduce_pl
  * and longer tensors take several launches; the unaligned fill and k_adam loop over their grid
  * (k_adam_al, which does not, only takes tensors its grid covers). MH_LAUNCH_ROWS16 counts rows,
  * not elements: the row-fused losses' forward and every row-fused backward over rows of at most
- * 16 classes (or whole quads of 20-32) run 64-row workgroups, several launches past one dispatch
- * (none for zero rows). */
+ * 32 classes run 64-row workgroups, several launches past one dispatch (none for zero rows). */
 enum {
     MH_LAUNCH_FILL = 0,            /* mh_fill / mh_zero, 16-byte-aligned tensor */
     MH_LAUNCH_FILL_UNALIGNED = 1,  /* mh_fill / mh_zero, other tensors */
@@ -452,8 +451,7 @@ enum {
     MH_LAUNCH_SAME_SHAPE = 3,      /* same-shape elementwise forward / backward, aligned */
     MH_LAUNCH_ADAM = 4,            /* mh_adam_step, all four tensors 16-byte aligned */
     MH_LAUNCH_ADAM_UNALIGNED = 5,  /* mh_adam_step, other tensors */
-    MH_LAUNCH_ROWS16 = 6           /* row-fused one-shot kernels over n rows (<= 16 classes, or whole
-                                      quads of 20-32), aligned */
+    MH_LAUNCH_ROWS16 = 6           /* row-fused one-shot kernels over n rows of <= 32 classes, aligned */
 };
 typedef struct {
     int32_t kernel;

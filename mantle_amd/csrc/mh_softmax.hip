@@ -1367,9 +1367,11 @@ static inline bool al16s(const void* p) { return (reinterpret_cast<uintptr_t>(p)
 // The class counts with row kernels of their own (one-shot and pipelined).
 #define MH_ROW16_CLASSES(X) \
     X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11) X(12) X(13) X(14) X(15) X(16)
-// the one-shot kernels' class counts: up to 16, and rows of whole quads of 20-32 classes
-#define MH_ONESHOT_CLASSES(X) MH_ROW16_CLASSES(X) X(20) X(24) X(28) X(32)
-static inline bool oneshot_classes(int K) { return K <= 16 || (K <= 32 && K % 4 == 0); }
+// the one-shot kernels' class counts: up to 32
+#define MH_ONESHOT_CLASSES(X) \
+    MH_ROW16_CLASSES(X)       \
+    X(17) X(18) X(19) X(20) X(21) X(22) X(23) X(24) X(25) X(26) X(27) X(28) X(29) X(30) X(31) X(32)
+static inline bool oneshot_classes(int K) { return K <= 32; }
 
 // Blocks of a persistent kernel: as many as can be resident at once (queried once per
 // kernel), so no block waits for another to finish.
@@ -1434,8 +1436,9 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
             return MH_OK;
         }
     } else {
-        // one-shot blocks of 64 rows (whole quads of 20-32 classes too: streamed over 8M
-        // elements 15.7-16.8 us against 16.3-19.6 us in the multi-lane engine)
+        // one-shot blocks of 64 rows, up to 32 classes (streamed over 8M elements, the
+        // CrossEntropy forward of 17-32 classes 15.1-16.8 us against 16.3-27.6 us in the
+        // multi-lane and thread engines)
         if (oneshot_classes(K) && al) {
             const int64_t nb = (rows + kORows - 1) / kORows;
             *nblocks_out = nb;
@@ -1455,8 +1458,9 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
             return MH_OK;
         }
     }
-    // multi-lane engine, aligned operands: loss rows of whole 16-byte quads or of more than 24
-    // classes, and Softmax / LogSoftmax rows of whole quads of 40, 48 or more than 52 classes.
+    // multi-lane engine, aligned operands: loss rows of 33-64 classes (up to 32 the one-shot
+    // kernels take them), and Softmax / LogSoftmax rows of whole quads of 40, 48 or more than
+    // 52 classes.
     // Streamed over 8M elements, Softmax quad rows run 14.1-19 us in the thread engine at 20-36,
     // 44 and 52 classes (32 with its rows padded in LDS: 14.5 against 36 us unpadded) against
     // 19.6-20.7 us here; at 40-64 classes the thread engine's LDS tiles (and, above 32, its
@@ -1465,7 +1469,7 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
     // 15-19 us there (32 us at 63 classes) against 30-31 us here; losses of 17-23 classes
     // 22-28 us there against 23-28 us here.
     const bool rowm_map = K % 4 == 0 && K > 32 && (K % 8 == 0 || K > 52);
-    if (K > 16 && K <= 4 * kMNE && al && (LOSS ? (K % 4 == 0 || K > 24) : rowm_map)) {
+    if (K > 16 && K <= 4 * kMNE && al && (LOSS || rowm_map)) {
         const int P = (K + kMNE - 1) / kMNE;
         const int64_t rpb = (int64_t)(kSThreads / 64) * (64 / P);
         const int64_t nb = (rows + rpb - 1) / rpb;
@@ -1542,12 +1546,10 @@ static int launch_bwd(float* gx, const float* x, const float* up, const float* u
         }
         return MH_OK;
     }
-    // multi-lane engine, aligned operands: rows of whole quads of more than 32 classes and other
-    // rows of more than 24 (whole quads of 20-32 classes take the one-shot kernels above:
-    // streamed over 8M elements, backwards 24-28 us there against 30-34 us here). Rows of 17-23
-    // classes that are not whole quads run 41-56 us in the thread engine against 47-63 us here
-    // (about equal at 21), so they stay there.
-    if (K > 16 && K <= 4 * kMNE && al && (K % 4 == 0 || K > 24)) {
+    // multi-lane engine, aligned operands, rows of 33-64 classes (up to 32 the one-shot kernels
+    // above take them: streamed over 8M elements, backwards of 17-32 classes 24-28 us there
+    // against 30-56 us in this and the thread engine)
+    if (K > 16 && K <= 4 * kMNE && al) {
         const int P = (K + kMNE - 1) / kMNE;
         const int64_t rpb = (int64_t)(kSThreads / 64) * (64 / P);
         const int64_t nb = (rows + rpb - 1) / rpb;
