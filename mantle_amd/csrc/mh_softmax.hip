@@ -1403,9 +1403,10 @@ static int check_rows(const char* what, int64_t rows, int64_t classes) {
 }
 
 // Loss graphs leave one partial per block in `part` (the caller sums them); Softmax and
-// LogSoftmax write `out`. Over rows of up to 16 classes with aligned operands, Softmax and
-// LogSoftmax run the pipelined engine and the loss graphs the one-shot engine, in several
-// launches (each over its own rows and partials) past one dispatch.
+// LogSoftmax write `out`. With aligned operands, Softmax and LogSoftmax over rows of up to 16
+// classes run the pipelined engine, and the loss graphs over rows of up to 32 classes the
+// one-shot engine, in several launches (each over its own rows and partials) past one
+// dispatch.
 template <int V>
 static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows, int K, float* part,
                       int64_t* nblocks_out) {
@@ -1466,8 +1467,7 @@ static int launch_fwd(const float* x, const float* tg, float* out, int64_t rows,
     // 19.6-20.7 us here; at 40-64 classes the thread engine's LDS tiles (and, above 32, its
     // 64-element registers) hold a CU to two or three blocks, and how its blocks fall into
     // rounds decides (18-31 us against 20.6-21.0 us here). Rows that are not whole quads run
-    // 15-19 us there (32 us at 63 classes) against 30-31 us here; losses of 17-23 classes
-    // 22-28 us there against 23-28 us here.
+    // 15-19 us there (32 us at 63 classes) against 30-31 us here.
     const bool rowm_map = K % 4 == 0 && K > 32 && (K % 8 == 0 || K > 52);
     if (K > 16 && K <= 4 * kMNE && al && (LOSS || rowm_map)) {
         const int P = (K + kMNE - 1) / kMNE;
