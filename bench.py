@@ -1131,7 +1131,7 @@ C2_KERNEL = {"ADD.bwd": "void mh::k_bwd2_same4<0, false>", "SUB.bwd": "void mh::
              "TANH.fwd": "void mh::k_same4<mh::FUn<15>,", "EXP.bwd": "void mh::k_same4<mh::FUnBwd<4>,",
              "LOG.bwd": "void mh::k_same4<mh::FUnBwd<5>,", "SIGMOID.bwd": "void mh::k_same4<mh::FUnBwd<13>,",
              "RELU.bwd": "void mh::k_same4<mh::FUnBwd<14>,", "TANH.bwd": "void mh::k_same4<mh::FUnBwd<15>,",
-             "POW.fwd": "void mh::k_same4<mh::FPowi,", "POW.bwd": "mh::k_pow_grad_quads("}
+             "POW.fwd": "void mh::k_same4<mh::FPowi,", "POW.bwd": "void mh::k_pow_grad_quads<true>("}
 
 
 # workload kernels for the traffic table: (op, kernel-name prefix, launch grid in threads,
@@ -1279,7 +1279,7 @@ def traffic_summary_md(commands):
 VALU_KERNELS = [  # (label, kernel-name prefix, elements per dispatch)
     ("c5 fused head forward [2^20, 10]", "void mh::k_rowo_fwd<0, 10>", _N5),
     ("c5 fused head backward [2^20, 10]", "void mh::k_rowo_bwd<0, 10>", _N5),
-    ("c2 POW backward, x and exponent gradients (2^28)", "mh::k_pow_grad_quads(", 1 << 28),
+    ("c2 POW backward, x and exponent gradients (2^28)", "void mh::k_pow_grad_quads<true>(", 1 << 28),
     ("c2 TANH backward (2^28)", "void mh::k_same4<mh::FUnBwd<15>, 2, true>", 1 << 28),
     ("c2 MUL backward, both operands (2^28)", "void mh::k_bwd2_same4<2, false>", 1 << 28),
     ("c2 ADD forward (2^28)", "void mh::k_same4<mh::FBin<0>, 2, false>", 1 << 28),

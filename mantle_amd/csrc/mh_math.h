@@ -50,17 +50,17 @@ __device__ __forceinline__ float mexp(float x) {
 
 // log of a positive normal finite x (Cephes logf): frexp, fold below sqrt(1/2), degree-8
 // polynomial, exponent added in two parts of ln 2. eadj corrects the exponent of a
-// pre-scaled subnormal.
+// pre-scaled subnormal. Three steps are written as fmas that give the method's bits: the
+// fold's m + m - 1 and m - 1 are exact (Sterbenz), as is fma(m, 2 or 1, -1); -0.5 z is
+// exact (z = m^2 is 0 or at least 2^-48), so y + (-0.5 z) is fma(-0.5, z, y); and
+// 0.693359375 fe is exact (a 9-bit constant times an integer below 2^8).
 __device__ __forceinline__ float mlog_core(float x, int eadj) {
-    uint32_t u = __float_as_uint(x);
-    int e = (int)((u >> 23) & 0xffu) - 126 + eadj;
+    const uint32_t u = __float_as_uint(x);
     float m = __uint_as_float((u & 0x807fffffu) | 0x3f000000u);
-    if (m < 0.707106781186547524f) {
-        e -= 1;
-        m = m + m - 1.0f;
-    } else {
-        m = m - 1.0f;
-    }
+    const bool fold = m < 0.707106781186547524f;
+    // frexp's exponent of a normal x: its biased exponent - 126
+    const int e = __builtin_amdgcn_frexp_expf(x) + eadj - (int)fold;
+    m = __builtin_fmaf(m, fold ? 2.0f : 1.0f, -1.0f);
     float z = m * m;
     float y = 7.0376836292e-2f;
     y = y * m - 1.1514610310e-1f;
@@ -72,12 +72,11 @@ __device__ __forceinline__ float mlog_core(float x, int eadj) {
     y = y * m - 2.4999993993e-1f;
     y = y * m + 3.3333331174e-1f;
     y = y * m * z;
-    float fe = (float)e;
+    const float fe = (float)e;
     y = y + -2.12194440e-4f * fe;
-    y = y + -0.5f * z;
-    float r = m + y;
-    r = r + 0.693359375f * fe;
-    return r;
+    y = __builtin_fmaf(-0.5f, z, y);
+    const float r = m + y;
+    return __builtin_fmaf(0.693359375f, fe, r);
 }
 
 // NaN, negative, zero, subnormal and infinite arguments, off the hot path.

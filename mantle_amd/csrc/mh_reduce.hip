@@ -237,6 +237,19 @@ struct LdPowGrad {
             return (mpowf_lg(xv, a, lx) * lg) * u;
         }
     }
+    // elem<true, GX>'s first branch without branches: ok says whether x is a positive normal
+    // value below 2e38 (mlog's straight-line case) and the powers took that branch; where it
+    // holds, g and the term are elem's, and the caller recomputes any other lane with elem.
+    template <bool GX>
+    __device__ __forceinline__ float elem_frac_fast(float xv, float u, float& g, bool& ok) const {
+        const float lx = mlog_core(xv, 0);
+        const bool same = xv + 1e-12f == xv;
+        const float p = mexp_core(am1 * lx);
+        const float t = p * xv;
+        ok = in_band(xv) && same && in_band(p) && in_band(t);
+        if constexpr (GX) g = g + (a * p) * u;
+        return (t * lx) * u;
+    }
     template <bool FRAC, bool GX>
     __device__ float get_t(int64_t i) const {
         const float xv = ld_nt(x + i), u = ld_nt(ug + i);
@@ -2159,25 +2172,30 @@ int unbroadcast_binrg(int op, int id, bool divs, float* grad, const mh_shape& sg
 }
 
 // The POW backward over whole aligned quads (LdPowGrad's terms, and with gx the x gradient) in
-// one-shot one-wavefront blocks of kPowQuads quads per thread, every load issued before the
-// first quad's log and exp work, one partial per wave. Over 2^28 elements (the x gradient
-// too, 16 B/elem) that ran at 0.69 ms against 0.71 for 256-thread blocks of four quads per
-// thread, 0.73-0.75 for 256-thread blocks taking loads and work one quad at a time, 0.80-0.94
-// with a one-quad prefetch loop and 0.91-0.93 as a grid-stride loop. Element j of every quad
-// of a thread adds into its sum j; the sums and then the wave add in a fixed order.
+// one-shot one-wavefront blocks, every load issued before the first quad's log and exp work.
+// Each run of 64 quads (a quad per lane) adds into one partial the same way whatever the
+// launch shape: a lane adds its quad's four terms as ((0 + t0) + (0 + t1)) + ((0 + t2) + (0 + t3)),
+// the wave adds its lanes in a fixed order, so the exponent gradient has the same bits with and
+// without the x gradient. Blocks take two such runs per thread for the exponent gradient alone
+// (over 2^28 elements 374-388 us against 467-473 us at one) and one with the x gradient too
+// (three streams; 671-678 us against 715-727 us at two, 0.69-0.71 ms for 256-thread blocks of
+// four quads per thread, 0.73-0.75 ms for 256-thread blocks taking loads and work one quad at
+// a time).
 constexpr int kPowThreads = 64;
-constexpr int kPowQuads = 2;
 constexpr int64_t kPowStreamMinQuads = 1 << 16;
+template <bool GX>
+constexpr int pow_runs() { return GX ? 1 : 2; }
+template <int NQ>
 struct PowQuads {
-    float4 xs[kPowQuads], us[kPowQuads], gs[kPowQuads];
+    float4 xs[NQ], us[NQ], gs[NQ];
 };
 
 // every quad's loads (a quad past the end reloads the last quad, unused)
-template <bool GX>
-__device__ __forceinline__ void pow_load_quads(const LdPowGrad& ld, int64_t nq, PowQuads& t) {
-    const int64_t base = (int64_t)blockIdx.x * (kPowThreads * kPowQuads) + threadIdx.x;
+template <bool GX, int NQ>
+__device__ __forceinline__ void pow_load_quads(const LdPowGrad& ld, int64_t nq, PowQuads<NQ>& t) {
+    const int64_t base = (int64_t)blockIdx.x * (kPowThreads * NQ) + threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < kPowQuads; ++k) {
+    for (int k = 0; k < NQ; ++k) {
         const int64_t q = base + k * kPowThreads;
         const int64_t qc = q < nq ? q : nq - 1;
         t.xs[k] = ld_nt4(ld.x, qc);
@@ -2186,42 +2204,67 @@ __device__ __forceinline__ void pow_load_quads(const LdPowGrad& ld, int64_t nq, 
     }
 }
 
-template <bool FRAC, bool GX>
-__device__ __forceinline__ void pow_block_quads(const LdPowGrad& ld, int64_t nq, PowQuads& t, float (&acc)[4]) {
-    const int64_t base = (int64_t)blockIdx.x * (kPowThreads * kPowQuads) + threadIdx.x;
+__device__ __forceinline__ float pow_quad_sum(float t0, float t1, float t2, float t3) {
+    return ((0.0f + t0) + (0.0f + t1)) + ((0.0f + t2) + (0.0f + t3));
+}
+
+// s[k]: the lane's sum over its quad of run k (0 past the end)
+template <bool FRAC, bool GX, int NQ>
+__device__ __forceinline__ void pow_block_quads(const LdPowGrad& ld, int64_t nq, PowQuads<NQ>& t, float (&s)[NQ]) {
+    const int64_t base = (int64_t)blockIdx.x * (kPowThreads * NQ) + threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < kPowQuads; ++k) {
+    for (int k = 0; k < NQ; ++k) {
         const int64_t q = base + k * kPowThreads;
+        s[k] = 0.0f;
         if (q < nq) {
-            acc[0] = acc[0] + ld.elem<FRAC, GX>(t.xs[k].x, t.us[k].x, t.gs[k].x);
-            acc[1] = acc[1] + ld.elem<FRAC, GX>(t.xs[k].y, t.us[k].y, t.gs[k].y);
-            acc[2] = acc[2] + ld.elem<FRAC, GX>(t.xs[k].z, t.us[k].z, t.gs[k].z);
-            acc[3] = acc[3] + ld.elem<FRAC, GX>(t.xs[k].w, t.us[k].w, t.gs[k].w);
-            if constexpr (GX) st_nt4(ld.gx, q, t.gs[k]);
+            const float4 &xq = t.xs[k], &uq = t.us[k], &g0 = t.gs[k];
+            float4 g = g0;
+            float r0, r1, r2, r3;
+            if constexpr (FRAC) {
+                // the quad's common case straight through, one wave-wide test, then elem for
+                // the lanes' elements that left it
+                bool o0, o1, o2, o3;
+                r0 = ld.elem_frac_fast<GX>(xq.x, uq.x, g.x, o0);
+                r1 = ld.elem_frac_fast<GX>(xq.y, uq.y, g.y, o1);
+                r2 = ld.elem_frac_fast<GX>(xq.z, uq.z, g.z, o2);
+                r3 = ld.elem_frac_fast<GX>(xq.w, uq.w, g.w, o3);
+                if (__builtin_expect(!(o0 && o1 && o2 && o3), 0)) {
+                    if (!o0) { g.x = g0.x; r0 = ld.elem<true, GX>(xq.x, uq.x, g.x); }
+                    if (!o1) { g.y = g0.y; r1 = ld.elem<true, GX>(xq.y, uq.y, g.y); }
+                    if (!o2) { g.z = g0.z; r2 = ld.elem<true, GX>(xq.z, uq.z, g.z); }
+                    if (!o3) { g.w = g0.w; r3 = ld.elem<true, GX>(xq.w, uq.w, g.w); }
+                }
+            } else {
+                r0 = ld.elem<false, GX>(xq.x, uq.x, g.x);
+                r1 = ld.elem<false, GX>(xq.y, uq.y, g.y);
+                r2 = ld.elem<false, GX>(xq.z, uq.z, g.z);
+                r3 = ld.elem<false, GX>(xq.w, uq.w, g.w);
+            }
+            s[k] = pow_quad_sum(r0, r1, r2, r3);
+            if constexpr (GX) st_nt4(ld.gx, q, g);
         }
     }
 }
 
 // The quads' loads go out before the exponent is read (setup): read first, every wave waited
-// for that scalar load before its quads' loads issued.
-__global__ void __launch_bounds__(kPowThreads) k_pow_grad_quads(LdPowGrad ld, int64_t nq, float* part) {
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    PowQuads t;
-    if (ld.gx) {
-        pow_load_quads<true>(ld, nq, t);
-        __builtin_amdgcn_sched_barrier(0);
-        ld.setup();
-        if (ld.frac) pow_block_quads<true, true>(ld, nq, t, acc);
-        else pow_block_quads<false, true>(ld, nq, t, acc);
-    } else {
-        pow_load_quads<false>(ld, nq, t);
-        __builtin_amdgcn_sched_barrier(0);
-        ld.setup();
-        if (ld.frac) pow_block_quads<true, false>(ld, nq, t, acc);
-        else pow_block_quads<false, false>(ld, nq, t, acc);
+// for that scalar load before its quads' loads issued. part[r] is run r's sum, r < nruns.
+template <bool GX>
+__global__ void __launch_bounds__(kPowThreads) k_pow_grad_quads(LdPowGrad ld, int64_t nq, int64_t nruns,
+                                                                float* part) {
+    constexpr int NQ = pow_runs<GX>();
+    PowQuads<NQ> t;
+    pow_load_quads<GX, NQ>(ld, nq, t);
+    __builtin_amdgcn_sched_barrier(0);
+    ld.setup();
+    float s[NQ];
+    if (ld.frac) pow_block_quads<true, GX, NQ>(ld, nq, t, s);
+    else pow_block_quads<false, GX, NQ>(ld, nq, t, s);
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const float a = wave_reduce<RSum>(s[k]);
+        const int64_t r = (int64_t)blockIdx.x * NQ + k;
+        if (threadIdx.x == 0 && r < nruns) part[r] = a;
     }
-    const float a = wave_reduce<RSum>((acc[0] + acc[1]) + (acc[2] + acc[3]));
-    if (threadIdx.x == 0) part[blockIdx.x] = a;
 }
 
 int pow_exponent_grad(float* grad, const float* x, const float* exponent, const float* ug, int64_t n,
@@ -2229,13 +2272,21 @@ int pow_exponent_grad(float* grad, const float* x, const float* exponent, const 
     LdPowGrad ld{x, ug, exponent, 0.0f, grad_x, 0.0f, false};
     const bool vec = al16(x) && al16(ug) && (!grad_x || al16(grad_x));
     float* tmp = nullptr;
-    if (vec && n % 4 == 0 && n / 4 >= kPowStreamMinQuads && n / 4 / (kPowThreads * kPowQuads) < 0x7fffffff) {
-        // block partials, then a row reduction of them into grad
+    if (vec && n % 4 == 0 && n / 4 >= kPowStreamMinQuads && n / 4 / kPowThreads < 0x7fffffff) {
+        // run partials, then a row reduction of them into grad
         const int64_t nq = n / 4;
-        const int64_t G = (nq + kPowThreads * kPowQuads - 1) / (kPowThreads * kPowQuads);
+        const int64_t G = (nq + kPowThreads - 1) / kPowThreads;  // runs of 64 quads
         const size_t t = pad64((size_t)G) + tmp_floats_t<RSum>(1, G, 1, true);
         MH_TRY(scratch((t + 64) * sizeof(float), reinterpret_cast<void**>(&tmp)));
-        hipLaunchKernelGGL(k_pow_grad_quads, dim3((unsigned)G), dim3(kPowThreads), 0, ctx().stream, ld, nq, tmp);
+        if (grad_x) {
+            constexpr int NQ = pow_runs<true>();
+            hipLaunchKernelGGL(k_pow_grad_quads<true>, dim3((unsigned)((G + NQ - 1) / NQ)), dim3(kPowThreads), 0,
+                               ctx().stream, ld, nq, G, tmp);
+        } else {
+            constexpr int NQ = pow_runs<false>();
+            hipLaunchKernelGGL(k_pow_grad_quads<false>, dim3((unsigned)((G + NQ - 1) / NQ)), dim3(kPowThreads), 0,
+                               ctx().stream, ld, nq, G, tmp);
+        }
         return reduce_t<RSum, LdPlain<RSum>>(LdPlain<RSum>{tmp}, true, EPI_ACCUM, 1, G, 1, grad, nullptr, 0.0f,
                                              tmp + pad64((size_t)G), false, true);
     }
