@@ -399,8 +399,8 @@ def test_pow_bwd_both_operands_fused(gpu, n):
     mh_pow_bwd_accum calls bit for bit: the x gradient element by element, the exponent gradient
     through the same reduction kernels in the same order (every reduction shape the length
     selects: LDS rows, one wavefront, block chunks with a combine, and for aligned lengths of
-    2^16 whole quads or more the grid-stride kernel, one and several quads per thread with a
-    ragged last pass). Bases include values where
+    2^16 whole quads or more the one-shot quad kernel, a 64-quad run per block with the x
+    gradient and two without, with a ragged last run). Bases include values where
     x + 1e-12 is not x (0, 1e-13, a subnormal), a negative base, NaN and inf; exponents integral
     and fractional; x, ug and the gradients also as unaligned views. The x gradient also matches
     the oracle bit for bit and the exponent gradient the oracle's in the sum class."""
